@@ -1,0 +1,100 @@
+/* librfill -- MI355X (gfx950) kernels for the RidgeFill late-layer fill.
+ *
+ * A flat C ABI: plain device pointers, element counts and strides, and the HIP stream every call is
+ * ordered on. Nothing here allocates device memory or keeps state between calls except the
+ * thread-local error text. Every call returns RF_OK or a negative status and leaves a message for
+ * rf_last_error(). Tensors are row-major; "bf16" buffers hold IEEE bfloat16 bit patterns (uint16_t).
+ *
+ * Each entry point names the reference code it replaces (paths in the reference repository,
+ * Approximate-Science/ridgefill-data).
+ */
+#ifndef RFILL_H
+#define RFILL_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define RF_OK 0
+#define RF_EINVAL_SHAPE (-1)   /* a size, stride or alignment the kernels do not take */
+#define RF_EINVAL_ARG (-2)     /* a null pointer or an out-of-range scalar argument */
+#define RF_EUNSUPPORTED (-3)   /* a model feature these kernels do not implement (never approximated) */
+#define RF_EHIP (-4)           /* the HIP runtime reported an error (launch or device) */
+
+/* Columns per row sum-of-squares partial: RMSNorm statistics travel as fp32 [rows, H / 256]. */
+#define RF_SSQ_COLS 256
+
+const char* rf_last_error(void);
+int rf_version(void);
+
+/* Ridge-map apply, x = b W^T + c in bf16 (one rounding after the fp32 sum and the bias), for P rows.
+ * Replaces Projector.__call__ (code/kva/kva.py:150-156, F.linear in bf16).
+ * b [P, h_in] (row stride ldb), w [h_out, h_in] (F.linear layout), c [h_out] or NULL,
+ * x [P, h_out] (row stride ldx). Also writes ssq [P, h_out / 256]: each row's sum of squares of the
+ * rounded x over consecutive 256-column groups (the next layer's RMSNorm statistics).
+ * Needs h_in % 64 == 0, h_out % 256 == 0, ldb / ldx multiples of 8, 16-byte aligned pointers. */
+int rf_map_apply(const uint16_t* b, int64_t ldb, const uint16_t* w, const uint16_t* c,
+                 uint16_t* x, int64_t ldx, float* ssq, int64_t P, int64_t h_in, int64_t h_out,
+                 hipStream_t stream);
+
+/* Row sum-of-squares partials of given layer inputs x [P, H] -> ssq [P, H / 256], the statistics the
+ * fused input RMSNorm of rf_norm_kv_write reads (the mean of x^2 in code/kva/ops.py:14-25).
+ * Bitwise the partials rf_map_apply writes for the same x. */
+int rf_row_ssq(const uint16_t* x, int64_t ldx, float* ssq, int64_t P, int64_t H, hipStream_t stream);
+
+/* Exact-row scatter x[rows[j]] = hr[j] for j < nrows, bit-exact, and those rows' ssq partials.
+ * Replaces x.index_copy(0, rows, hr) (code/kva/kva.py:428-431). rows: int64 on the device; the caller
+ * checks they are sorted, unique and < P (as kva.py:357-362 does); a row outside [0, P) is skipped. */
+int rf_row_scatter(uint16_t* x, int64_t ldx, float* ssq, int64_t P, int64_t H, const int64_t* rows,
+                   int64_t nrows, const uint16_t* hr, int64_t ldhr, hipStream_t stream);
+
+/* Fold an RMSNorm gain into projection weights: w_out[n, k] = bf16(w[n, k] * g(k)), with
+ * g = gain (Llama / Qwen3 rms_norm, kind 0) or 1 + gain (Qwen3.5 rms_norm_zc, kind 1).
+ * Run once per layer when weights are packed; feeds rf_norm_kv_write. w, w_out [N, K]; gain [K]. */
+int rf_fold_norm(const uint16_t* w, const uint16_t* gain, int kind, uint16_t* w_out, int64_t N,
+                 int64_t K, hipStream_t stream);
+
+/* RoPE table for P rows: cs [P, rot] bf16 with cs[j, 0 : rot/2] = bf16(cos(float(pos[j]) * inv_freq))
+ * and cs[j, rot/2 : rot] = bf16(sin(...)), fp32 angles (code/kva/ops.py:59-63; the reference's cos /
+ * sin tables repeat the half table twice, so the half table is all that is kept). One table serves
+ * every late layer of a prompt: the positions and frequencies do not change between layers. */
+int rf_rope_table(const int64_t* pos, int64_t P, const float* inv_freq, int rot, uint16_t* cs,
+                  hipStream_t stream);
+
+/* Fused attention-layer fill from layer inputs: input RMSNorm, K / V projections, optional per-head
+ * k_norm, RoPE on K and the write of P rows into the K / V cache.
+ * Replaces Model.fill (code/kva/model.py:278-280) = in_norm (ops.py:14-25) + Llama._kv /
+ * Qwen3._kv / Qwen35._attn_kv (model.py:234-239, 340-345, 415-421) + _append_kv (model.py:139-159).
+ *   x [P, H] layer inputs (row stride ldx), ssq [P, H / 256] their partials, eps the norm epsilon;
+ *   wkv [2 hkv d, H]: rows [0, hkv d) the K projection, then the V projection, both with the input
+ *       norm gain folded in (rf_fold_norm);
+ *   knorm [d] bf16 or NULL, knorm_kind 0 = Llama rms_norm, 1 = Qwen3.5 rms_norm_zc (ignored if NULL);
+ *   cs [P, rot] the RoPE table of the rows' positions (rf_rope_table), rot the rotated dims (partial
+ *       RoPE when rot < d, half-split rotation as ops.py:66-77);
+ *   kbuf / vbuf: cache [hkv, cap, d] with element strides head_stride / row_stride; row j goes to
+ *       slot slot_begin + j.
+ * Needs H % 64 == 0, 2 hkv d % 256 == 0, 256 % d == 0, d % 8 == 0, rot even, rot <= d, rot / 2 a
+ * multiple of 8 or equal to 4, slot_begin + P <= cap. */
+int rf_norm_kv_write(const uint16_t* x, int64_t ldx, const float* ssq, int64_t P, int64_t H, float eps,
+                     const uint16_t* wkv, int hkv, int d, const uint16_t* knorm, int knorm_kind,
+                     const uint16_t* cs, int rot,
+                     uint16_t* kbuf, uint16_t* vbuf, int64_t head_stride, int64_t row_stride,
+                     int64_t slot_begin, int64_t cap, hipStream_t stream);
+
+/* RoPE on given pre-RoPE K and the K / V cache write of m rows.
+ * Replaces Model.fill_kv (code/kva/model.py:161-165): ops.apply_rope (ops.py:66-77) + _append_kv.
+ * k / v: [m, hkv, d] with token strides ld_k / ld_v (a head's d values contiguous, heads d apart);
+ * cs, rot and the cache arguments as rf_norm_kv_write. */
+int rf_rope_kv_write(const uint16_t* k, int64_t ld_k, const uint16_t* v, int64_t ld_v, int64_t m, int hkv,
+                     int d, const uint16_t* cs, int rot,
+                     uint16_t* kbuf, uint16_t* vbuf, int64_t head_stride, int64_t row_stride,
+                     int64_t slot_begin, int64_t cap, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* RFILL_H */

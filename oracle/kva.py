@@ -1,0 +1,139 @@
+"""Oracle fill driver (test infrastructure; see oracle/__init__.py).
+
+Restates the parts of code/kva/kva.py on the fill path: Arm and its prefix length (:79-118), the
+Projector map type and its safetensors format (:121-193), rounded_tail (:270-273), run_lower
+(:282-300) and finish()'s late-layer loop for the fills 'proj', 'identity', 'oracle' and 'none',
+exact rows and the GDN terminal-state correction st (:319-460).
+"""
+import json
+from dataclasses import dataclass, field
+
+import torch
+import torch.nn.functional as F
+
+MAX_ABS_WEIGHT = 1e4
+
+
+@dataclass
+class Arm:
+    name: str
+    split: int | None = None
+    tail: int = 0
+    fill: str = "exact"
+    projector: object = None
+    st: dict | None = None
+    meta: dict = field(default_factory=dict)
+
+    def prefix_len(self, n):
+        """P = n - tail (0 for the exact arm), code/kva/kva.py:101-106."""
+        return 0 if self.fill == "exact" else max(0, n - self.tail)
+
+
+def rounded_tail(n, base, block):
+    """Tail length when the prefix boundary is rounded down to a block multiple (code/kva/kva.py:270-273)."""
+    start = max(0, (n - base) // block * block)
+    return n - start
+
+
+def check_weights(tensors, where):
+    """Refuse stored maps with a non-finite entry or |w| > 1e4 (code/kva/kva.py:121-134)."""
+    for name, t in tensors.items():
+        tf = t.float()
+        bad = ~torch.isfinite(tf) | (tf.abs() > MAX_ABS_WEIGHT)
+        if bool(bad.any()):
+            r, c = bad.nonzero()[0].tolist()
+            raise ValueError(f"{where}: {name} has {int(bad.sum())} non-finite or |w| > {MAX_ABS_WEIGHT:g} "
+                             f"weights (first at row {r}, col {c}); refusing")
+
+
+class Projector:
+    """x_i = b W_i^T + c_i per late layer (code/kva/kva.py:137-156). File format (:161-193):
+    safetensors, tensor 'layer.{i}' = [d_out, d_in + 1] bf16 with the bias as the last column, string
+    metadata including 'split'."""
+
+    def __init__(self, split, weights, biases, meta=None):
+        self.split, self.W, self.b, self.meta = split, weights, biases, meta or {}
+
+    def __call__(self, i, b):
+        return F.linear(b, self.W[i].to(b.dtype), self.b[i].to(b.dtype))
+
+    def save(self, path, meta):
+        from safetensors.torch import save_file
+        out = {f"layer.{i}": torch.cat((self.W[i], self.b[i][:, None]), 1).to(torch.bfloat16).contiguous()
+               for i in sorted(self.W)}
+        check_weights(out, f"Projector.save {path}")
+        save_file(out, str(path), metadata={k: str(v) for k, v in dict(meta, split=self.split).items()})
+
+    @classmethod
+    def load(cls, path, dtype=torch.bfloat16):
+        from safetensors.torch import load_file
+        with open(path, "rb") as f:
+            hdr = f.read(8)
+            meta = json.loads(f.read(int.from_bytes(hdr, "little"))).get("__metadata__") or {}
+        W, B = {}, {}
+        for name, t in load_file(str(path)).items():
+            check_weights({name: t}, f"Projector.load {path}")
+            i = int(name.split(".")[1])
+            W[i], B[i] = t[:, :-1].to(dtype).contiguous(), t[:, -1].to(dtype).contiguous()
+        return cls(int(meta["split"]), W, B, meta)
+
+
+def run_lower(model, ids, splits):
+    """Exact forward of layers < max(splits); returns ({split: h_split}, cache) (code/kva/kva.py:282-300)."""
+    pos = torch.arange(ids.shape[0])
+    cache = model.new_cache()
+    h = model.embed(ids)
+    hs = {}
+    for i in range(max(splits)):
+        if i in splits:
+            hs[i] = h
+        h = model.layer(i, h, pos, cache)
+    hs[max(splits)] = h
+    return hs, cache
+
+
+def finish(model, ids, h_split, lower_cache, arm, keep, oracle=None, exact_rows=None, fill_store=None):
+    """Late layers of one arm (code/kva/kva.py:319-460, the fill subset). Prefix rows [0, P) fill each
+    late layer from x (projector / identity / true inputs) with the exact rows R scattered in
+    (index_copy) and run through layer_rows; then +st; then the tail rows run the exact layer.
+    Returns (logits of the last `keep` rows, cache, P)."""
+    n = ids.shape[0]
+    split = arm.split
+    P = arm.prefix_len(n)
+    pos = torch.arange(n)
+    cache = [dict(c) for c in lower_cache[:split]] + [dict() for _ in range(model.n_layers - split)]
+    if keep > n - P:
+        raise ValueError(f"keep {keep} rows > exact tail {n - P}")
+    b, h = h_split[:P], h_split[P:]
+    rows = None
+    if exact_rows is not None and len(exact_rows) > 0:
+        rows = torch.as_tensor(exact_rows, dtype=torch.long)
+        if int(rows[-1]) >= P or bool((rows.diff() <= 0).any()):
+            raise ValueError("exact rows: sorted unique rows < P")
+        hr = h_split[rows]
+    for i in range(split, model.n_layers):
+        if P > 0:
+            if arm.fill == "none":
+                if rows is not None:
+                    hr = model.layer(i, hr, pos[rows], cache)
+            else:
+                if arm.fill == "proj":
+                    x = arm.projector(i, b)
+                elif arm.fill == "identity":
+                    x = b
+                elif arm.fill == "oracle":
+                    x = oracle[i][:P]
+                else:
+                    raise ValueError(arm.fill)
+                if rows is not None:
+                    x = x.index_copy(0, rows, hr.to(x.dtype))
+                    hr = model.layer_rows(i, x, pos[:P], rows, cache)
+                else:
+                    model.fill(i, x, pos[:P], cache)
+            if fill_store is not None:
+                fill_store[i] = dict(cache[i])
+            st = arm.st.get(i) if arm.st else None
+            if st is not None:
+                cache[i]["rec"] = cache[i]["rec"] + st.to(cache[i]["rec"])
+        h = model.layer(i, h, pos[P:], cache)
+    return model.logits(h[h.shape[0] - keep:]), cache, P

@@ -1,0 +1,346 @@
+// bf16 MFMA GEMM core for gfx950 and the two fill GEMMs built on it:
+//   rf_map_apply      x = b W^T + c, rounded to bf16, plus the rows' sum-of-squares partials;
+//   rf_norm_kv_write  [K | V] = rms_norm(x) W_kv^T with the norm gain folded into W_kv, per-head
+//                     k_norm, RoPE on K, written straight into the [hkv, cap, d] cache slots.
+//
+// Tiling. A workgroup of 4 wave64s computes a 256 x 256 output tile over K in 64-wide steps. Both
+// operands are K-contiguous (row-major activations, F.linear-layout weights), so each 64-wide K slice
+// of a 256-row operand tile is 256 rows x 128 bytes: 8 threads load one row with 128-bit loads.
+// The slices sit in LDS with the 16-byte chunk index XOR-ed by the row's low 3 bits, so the MFMA
+// fragment reads (32 rows, one chunk) and the loader's writes (one row, 8 chunks) both spread over
+// all banks. Two LDS stages (2 x 64 KiB): the next slice is fetched into registers while the current
+// one feeds the MFMAs, then stored to the other stage; one barrier per step.
+//
+// Each wave owns a 128 x 128 quarter and issues v_mfma_f32_32x32x16_bf16 on 4 x 4 sub-tiles. The
+// weight tile is the MFMA's A operand and the activation tile its B operand, so the accumulator of a
+// lane holds, for one activation row (lane % 32), four runs of 4 consecutive output columns: the
+// epilogue rounds them to bf16 and writes 8-byte runs into a row-major LDS image of the 256 x 256
+// tile, which a row pass then reads as 16-byte chunks (32 threads per 256-column row) to compute
+// row statistics, apply k_norm / RoPE and issue coalesced 128-bit stores.
+#include "rf_common.h"
+
+namespace rf {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int BM = 256, BN = 256, BK = 64, NTHR = 256;
+constexpr int STAGE_U4 = (BM + BN) * BK / 8;   // 16-byte chunks per LDS stage (activations, then weights)
+constexpr int LDS_U4 = 2 * STAGE_U4;           // 128 KiB; reused by the epilogue as the 256 x 256 bf16 tile
+
+__device__ __forceinline__ bf16x8 as_frag(const uint4& u) { return __builtin_bit_cast(bf16x8, u); }
+
+// Logical tile of a hardware block. Blocks are dealt round-robin over the 8 XCDs (block b runs on
+// XCD b % 8); this gives every XCD a contiguous run of logical tiles, and tiles are numbered
+// column-fastest, so the tiles sharing one 256-row activation block mostly share one XCD's L2.
+__device__ __forceinline__ int xcd_tile(int bid, int nb) {
+  const int q = nb >> 3, r = nb & 7, x = bid & 7, i = bid >> 3;
+  return (x < r) ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
+}
+
+// acc[nt][mt] += W[n0 + wn*128 + nt*32 .. +32, :] . X[m0 + wm*128 + mt*32 .. +32, :]^T over all of K.
+// Rows of X at or past M read as zeros. Ends with a barrier: LDS is free for the epilogue.
+__device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t ldx,
+                                         const uint16_t* __restrict__ W, int64_t ldw, int M, int K,
+                                         int m0, int n0, uint4* lds, f32x16 (&acc)[4][4]) {
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int wm = w >> 1, wn = w & 1;
+  const int lrow = t >> 3, lch = t & 7;           // loader: rows lrow + 32 i, 16-byte chunk lch
+  const int lpos = lrow * 8 + (lch ^ (lrow & 7)); // swizzled slot of (lrow, lch); + 256 per 32 rows
+  const uint16_t* gx = X + static_cast<int64_t>(m0 + lrow) * ldx + lch * 8;
+  const uint16_t* gw = W + static_cast<int64_t>(n0 + lrow) * ldw + lch * 8;
+  const int rows_left = M - m0 - lrow;            // X rows i with 32 i < rows_left are in range
+
+  uint4 rx[8], rw[8];
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      rx[i] = (32 * i < rows_left) ? *reinterpret_cast<const uint4*>(gx + 32 * i * ldx + k0)
+                                   : make_uint4(0u, 0u, 0u, 0u);
+      rw[i] = *reinterpret_cast<const uint4*>(gw + 32 * i * ldw + k0);
+    }
+  };
+  auto stash = [&](int s) {
+    uint4* sx = lds + s * STAGE_U4;
+    uint4* sw = sx + BM * 8;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      sx[lpos + 256 * i] = rx[i];
+      sw[lpos + 256 * i] = rw[i];
+    }
+  };
+
+#pragma unroll
+  for (int a = 0; a < 4; ++a)
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  const int nk = K / BK;
+  const int lr = lane & 31, lk = lane >> 5, sw7 = lane & 7;
+  for (int kt = 0; kt < nk; ++kt) {
+    const int s = kt & 1;
+    if (kt + 1 < nk) fetch((kt + 1) * BK);
+    const uint4* sx = lds + s * STAGE_U4;
+    const uint4* sw = sx + BM * 8;
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      const int slot = (ks * 2 + lk) ^ sw7;
+      bf16x8 fx[4], fw[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        fx[i] = as_frag(sx[(wm * 128 + i * 32 + lr) * 8 + slot]);
+        fw[i] = as_frag(sw[(wn * 128 + i * 32 + lr) * 8 + slot]);
+      }
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt)
+          acc[nt][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[nt], fx[mt], acc[nt][mt], 0, 0, 0);
+    }
+    if (kt + 1 < nk) stash(s ^ 1);
+    __syncthreads();
+  }
+}
+
+// Epilogue stage 1: value(mt, nt, g, e, acc) rounded to bf16 into the row-major LDS image of the tile.
+// Lane (lr, lk) holds, for tile row wm*128 + mt*32 + lr, columns wn*128 + nt*32 + 8g + 4lk + e.
+// Image layout: row r's 16-byte chunk c lives at slot r * 32 + (c ^ (r & 31)).
+template <class F>
+__device__ __forceinline__ void stage_tile(uint4* lds, const f32x16 (&acc)[4][4], F value) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w >> 1, wn = w & 1, lr = lane & 31, lk = lane >> 5;
+  char* base = reinterpret_cast<char*>(lds);
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int row = wm * 128 + mt * 32 + lr;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int c0 = wn * 128 + nt * 32 + 8 * g + 4 * lk;
+        uint16_t h[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) h[e] = f2bf(value(mt, nt, g, e, acc[nt][mt][4 * g + e]));
+        const int off = row * 512 + (((c0 >> 3) ^ (row & 31)) << 4) + ((c0 & 7) << 1);
+        *reinterpret_cast<uint2*>(base + off) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
+      }
+  }
+}
+
+__device__ __forceinline__ uint4 image_chunk(const uint4* lds, int row, int c) {
+  return lds[row * 32 + (c ^ (row & 31))];
+}
+
+__global__ __launch_bounds__(NTHR) void k_map_apply(const uint16_t* __restrict__ B, int64_t ldb,
+                                                    const uint16_t* __restrict__ W,
+                                                    const uint16_t* __restrict__ bias,
+                                                    uint16_t* __restrict__ X, int64_t ldx,
+                                                    float* __restrict__ ssq, int M, int N, int K) {
+  __shared__ uint4 lds[LDS_U4];
+  const int tiles_n = N / BN;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int tn = tile % tiles_n, m0 = (tile / tiles_n) * BM, n0 = tn * BN;
+  f32x16 acc[4][4];
+  mainloop(B, ldb, W, K, M, K, m0, n0, lds, acc);
+
+  const int lane = threadIdx.x & 63, wn = (threadIdx.x >> 6) & 1, lk = lane >> 5;
+  float bv[4][4][4];
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c = n0 + wn * 128 + nt * 32 + 8 * g + 4 * lk;
+      uint2 u = bias ? *reinterpret_cast<const uint2*>(bias + c) : make_uint2(0u, 0u);
+      bv[nt][g][0] = bf2f(u.x & 0xffffu);
+      bv[nt][g][1] = bf2f(u.x >> 16);
+      bv[nt][g][2] = bf2f(u.y & 0xffffu);
+      bv[nt][g][3] = bf2f(u.y >> 16);
+    }
+  stage_tile(lds, acc, [&](int, int nt, int g, int e, float a) { return a + bv[nt][g][e]; });
+  __syncthreads();
+
+  const int t = threadIdx.x, ch = t & 31;
+  const int nparts = N / SSQ_COLS;
+  for (int it = 0; it < BM / 8; ++it) {
+    const int row = it * 8 + (t >> 5);
+    const uint4 v = image_chunk(lds, row, ch);
+    const float s = halfwave_sum(chunk_ssq(v));
+    const int gm = m0 + row;
+    if (gm < M) {
+      *reinterpret_cast<uint4*>(X + static_cast<int64_t>(gm) * ldx + n0 + ch * 8) = v;
+      if (ch == 0) ssq[static_cast<int64_t>(gm) * nparts + tn] = s;
+    }
+  }
+}
+
+struct KvArgs {
+  const float* ssq;
+  int nparts;
+  float h;            // norm width (the GEMM's K)
+  float eps;
+  int hkv, d;
+  const uint16_t* knorm;
+  int knorm_kind;
+  const uint16_t* cs;
+  int rot;
+  uint16_t* kbuf;
+  uint16_t* vbuf;
+  int64_t head_stride, row_stride, slot0;
+};
+
+// k_norm of one chunk's 8 values given the head's inverse RMS (code/kva/ops.py:14-25 per head).
+__device__ __forceinline__ void knorm_chunk(float (&f)[8], float rinv, const uint16_t* kw, int kind, int j0) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float w = bf2f(kw[j0 + e]);
+    f[e] = kind == 0 ? bf2f(f2bf(w * bf2f(f2bf(f[e] * rinv)))) : bf2f(f2bf(f[e] * rinv * (1.0f + w)));
+  }
+}
+
+__global__ __launch_bounds__(NTHR) void k_norm_kv(const uint16_t* __restrict__ Xin, int64_t ldx,
+                                                  const uint16_t* __restrict__ W, int M, int N, int K,
+                                                  KvArgs a) {
+  __shared__ uint4 lds[LDS_U4];
+  const int tiles_n = N / BN;
+  const int tile = xcd_tile(blockIdx.x, gridDim.x);
+  const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+  f32x16 acc[4][4];
+  mainloop(Xin, ldx, W, K, M, K, m0, n0, lds, acc);
+
+  // Input RMSNorm: the gain is folded into W, so each row is scaled by 1 / sqrt(mean(x^2) + eps).
+  const int lane = threadIdx.x & 63, wm = threadIdx.x >> 7;
+  float rs[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int gm = m0 + wm * 128 + mt * 32 + (lane & 31);
+    float s = 0.f;
+    if (gm < M) {
+      const float* p = a.ssq + static_cast<int64_t>(gm) * a.nparts;
+      for (int q = 0; q < a.nparts; ++q) s += p[q];
+    }
+    rs[mt] = 1.0f / sqrtf(s / a.h + a.eps);
+  }
+  stage_tile(lds, acc, [&](int mt, int, int, int, float v) { return v * rs[mt]; });
+  __syncthreads();
+
+  const int t = threadIdx.x, ch = t & 31;
+  const int d = a.d, kw = a.hkv * a.d, rot = a.rot, half = a.rot >> 1;
+  const int group = d >> 3;                       // chunks per head: a power of two <= 32
+  for (int it = 0; it < BM / 8; ++it) {
+    const int row = it * 8 + (t >> 5);
+    const int gm = m0 + row;
+    const int col = n0 + ch * 8;
+    const bool is_k = col < kw;
+    const int cc = is_k ? col : col - kw;
+    const int head = cc / d, j0 = cc - head * d;
+    const uint4 v = image_chunk(lds, row, ch);
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = bf2f(lane_of(v, e));
+    // Per-head sum of squares for k_norm: every lane joins the shuffles (head groups never straddle
+    // the K / V boundary, so V lanes only ever combine with V lanes).
+    float ss = chunk_ssq(v);
+    for (int o = 1; o < group; o <<= 1) ss += __shfl_xor(ss, o, 64);
+    if (gm >= M) continue;
+    const int64_t slot = a.slot0 + gm;
+    if (!is_k) {
+      *reinterpret_cast<uint4*>(a.vbuf + head * a.head_stride + slot * a.row_stride + j0) = v;
+      continue;
+    }
+    const float rinv = 1.0f / sqrtf(ss / static_cast<float>(d) + a.eps);
+    if (a.knorm) knorm_chunk(f, rinv, a.knorm, a.knorm_kind, j0);
+    uint16_t out[8];
+    if (j0 >= rot) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) out[e] = f2bf(f[e]);
+    } else {
+      float pf[8];                                // rotate_half partner values of this chunk
+      if (half >= 8) {
+        const int pj0 = j0 < half ? j0 + half : j0 - half;
+        const uint4 pv = image_chunk(lds, row, ch + (pj0 - j0) / 8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pf[e] = bf2f(lane_of(pv, e));
+        if (a.knorm) knorm_chunk(pf, rinv, a.knorm, a.knorm_kind, pj0);
+      } else {                                    // half == 4: the partner is in the same chunk
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pf[e] = f[e ^ 4];
+      }
+      const uint16_t* cs = a.cs + static_cast<int64_t>(gm) * rot;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int j = j0 + e;
+        const int fi = j < half ? j : j - half;
+        const float c = bf2f(cs[fi]), s = bf2f(cs[half + fi]);
+        const float rh = j < half ? -pf[e] : pf[e];
+        out[e] = f2bf(bf2f(f2bf(f[e] * c)) + bf2f(f2bf(rh * s)));
+      }
+    }
+    *reinterpret_cast<uint4*>(a.kbuf + head * a.head_stride + slot * a.row_stride + j0) =
+        make_uint4(pack2(out[0], out[1]), pack2(out[2], out[3]), pack2(out[4], out[5]), pack2(out[6], out[7]));
+  }
+}
+
+int grid_of(int64_t M, int64_t N) { return static_cast<int>(((M + BM - 1) / BM) * (N / BN)); }
+
+}  // namespace
+}  // namespace rf
+
+using namespace rf;
+
+extern "C" int rf_map_apply(const uint16_t* b, int64_t ldb, const uint16_t* w, const uint16_t* c, uint16_t* x,
+                            int64_t ldx, float* ssq, int64_t P, int64_t h_in, int64_t h_out,
+                            hipStream_t stream) {
+  if (!b || !w || !x || !ssq) return fail(RF_EINVAL_ARG, "rf_map_apply: null pointer");
+  if (P < 0 || P > (1ll << 30)) return fail(RF_EINVAL_SHAPE, "rf_map_apply: P = %lld out of range", (long long)P);
+  if (h_in <= 0 || h_in % BK || h_out <= 0 || h_out % BN)
+    return fail(RF_EINVAL_SHAPE, "rf_map_apply: h_in %lld must be a multiple of 64 and h_out %lld of 256",
+                (long long)h_in, (long long)h_out);
+  if (ldb < h_in || ldx < h_out || ldb % 8 || ldx % 8)
+    return fail(RF_EINVAL_SHAPE, "rf_map_apply: row strides ldb %lld / ldx %lld", (long long)ldb, (long long)ldx);
+  if (!aligned16(b) || !aligned16(w) || !aligned16(x) || (c && (reinterpret_cast<uintptr_t>(c) & 7u)))
+    return fail(RF_EINVAL_SHAPE, "rf_map_apply: pointers must be 16-byte aligned (bias 8-byte)");
+  if (P == 0) return RF_OK;
+  hipLaunchKernelGGL(k_map_apply, dim3(grid_of(P, h_out)), dim3(NTHR), 0, stream, b, ldb, w, c, x, ldx, ssq,
+                     static_cast<int>(P), static_cast<int>(h_out), static_cast<int>(h_in));
+  return check_launch("rf_map_apply");
+}
+
+extern "C" int rf_norm_kv_write(const uint16_t* x, int64_t ldx, const float* ssq, int64_t P, int64_t H, float eps,
+                                const uint16_t* wkv, int hkv, int d, const uint16_t* knorm, int knorm_kind,
+                                const uint16_t* cs, int rot, uint16_t* kbuf, uint16_t* vbuf,
+                                int64_t head_stride, int64_t row_stride, int64_t slot_begin, int64_t cap,
+                                hipStream_t stream) {
+  if (!x || !ssq || !wkv || !cs || !kbuf || !vbuf) return fail(RF_EINVAL_ARG, "rf_norm_kv_write: null pointer");
+  if (P < 0 || P > (1ll << 30)) return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write: P = %lld out of range", (long long)P);
+  if (H <= 0 || H % BK || H % SSQ_COLS)
+    return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write: H = %lld must be a multiple of 256", (long long)H);
+  if (d <= 0 || d % 8 || 256 % d || hkv <= 0 || (2ll * hkv * d) % BN)
+    return fail(RF_EUNSUPPORTED, "rf_norm_kv_write: head_dim %d / kv heads %d (need 256 %% d == 0, d %% 8 == 0, "
+                "2 hkv d %% 256 == 0)", d, hkv);
+  if (rot <= 0 || rot > d || rot % 2 || ((rot / 2) % 8 && rot / 2 != 4))
+    return fail(RF_EUNSUPPORTED, "rf_norm_kv_write: rotary dims %d of head_dim %d", rot, d);
+  if (knorm && knorm_kind != 0 && knorm_kind != 1)
+    return fail(RF_EINVAL_ARG, "rf_norm_kv_write: knorm_kind %d", knorm_kind);
+  if (ldx < H || ldx % 8 || head_stride % 8 || row_stride % 8 || row_stride < d)
+    return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write: strides (ldx %lld, head %lld, row %lld)", (long long)ldx,
+                (long long)head_stride, (long long)row_stride);
+  if (slot_begin < 0 || slot_begin + P > cap)
+    return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write: rows [%lld, %lld) exceed cache capacity %lld",
+                (long long)slot_begin, (long long)(slot_begin + P), (long long)cap);
+  if (!aligned16(x) || !aligned16(wkv) || !aligned16(kbuf) || !aligned16(vbuf))
+    return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write: pointers must be 16-byte aligned");
+  if (!(eps >= 0.f)) return fail(RF_EINVAL_ARG, "rf_norm_kv_write: eps %g", static_cast<double>(eps));
+  if (P == 0) return RF_OK;
+  KvArgs a{ssq, static_cast<int>(H / SSQ_COLS), static_cast<float>(H), eps, hkv, d, knorm, knorm_kind, cs, rot,
+           kbuf, vbuf, head_stride, row_stride, slot_begin};
+  const int64_t N = 2ll * hkv * d;
+  hipLaunchKernelGGL(k_norm_kv, dim3(grid_of(P, N)), dim3(NTHR), 0, stream, x, ldx, wkv, static_cast<int>(P),
+                     static_cast<int>(N), static_cast<int>(H), a);
+  return check_launch("rf_norm_kv_write");
+}

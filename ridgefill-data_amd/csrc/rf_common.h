@@ -1,0 +1,59 @@
+// Shared helpers of librfill: status codes, the thread-local error text, bf16 conversions and the
+// per-row sum-of-squares partial used by the fused RMSNorm.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/rfill.h"
+
+namespace rf {
+
+// Error text of the last failing call on this host thread (rf_last_error()).
+int fail(int code, const char* fmt, ...);
+int check_launch(const char* what);
+
+// Columns covered by one row sum-of-squares partial (the RMSNorm statistics are kept as
+// [rows, H / SSQ_COLS] fp32 partials so that producers write them without atomics).
+constexpr int SSQ_COLS = 256;
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+__device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
+
+// fp32 -> bf16, round to nearest even (the rounding torch's .to(torch.bfloat16) performs).
+__device__ __forceinline__ uint16_t f2bf(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<uint16_t>(u >> 16);
+}
+
+__device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
+  return static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
+}
+
+__device__ __forceinline__ uint16_t lane_of(const uint4& v, int e) {
+  const uint32_t w = (e < 2) ? v.x : (e < 4) ? v.y : (e < 6) ? v.z : v.w;
+  return static_cast<uint16_t>((e & 1) ? (w >> 16) : (w & 0xffffu));
+}
+
+// Sum of squares of the 8 bf16 values of one 16-byte chunk, in element order.
+__device__ __forceinline__ float chunk_ssq(const uint4& v) {
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float f = bf2f(lane_of(v, e));
+    s = fmaf(f, f, s);
+  }
+  return s;
+}
+
+// Butterfly sum over the 32 lanes of each half-wave (lane bits 0..4): a fixed order, so every
+// producer of a row partial (GEMM epilogue, row_ssq, row_scatter) gives the same bits.
+__device__ __forceinline__ float halfwave_sum(float s) {
+#pragma unroll
+  for (int o = 16; o >= 1; o >>= 1) s += __shfl_xor(s, o, 64);
+  return s;
+}
+
+}  // namespace rf

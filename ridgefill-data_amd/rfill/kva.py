@@ -1,0 +1,157 @@
+"""Fill driver over the device fill model: the reference's Arm, Projector map type and the late-layer
+fill loop of finish() (code/kva/kva.py:79-193, 392-454), with every fill step on librfill kernels.
+
+fill_late() runs the hot path of finish() for one arm: for each late layer i >= split, the prefix rows
+[0, P) get x_i = W_i b + c_i (fill 'proj', one rf_map_apply that also yields x's RMSNorm statistics)
+or x_i = b (fill 'identity'), the exact rows R are scattered in bit-exactly (rf_row_scatter, the
+index_copy of kva.py:428-431), and the layer's cache is filled (rf_norm_kv_write). One x buffer, one
+statistics buffer and one RoPE table serve all late layers.
+"""
+import json
+from dataclasses import dataclass, field
+
+import torch
+
+from . import ops
+
+MAX_ABS_WEIGHT = 1e4
+
+
+@dataclass
+class Arm:
+    """An arm's fill parameters (code/kva/kva.py:79-118): split, tail, fill kind, projector, st."""
+    name: str
+    split: int | None = None
+    tail: int = 0
+    fill: str = "exact"
+    projector: object = None
+    st: dict | None = None
+    meta: dict = field(default_factory=dict)
+
+    def prefix_len(self, n):
+        if self.fill == "exact":
+            return 0
+        if self.fill == "swiftkv_native":
+            return n
+        return max(0, n - self.tail)
+
+
+def rounded_tail(n, base, block):
+    """Tail length when the prefix boundary is rounded down to a block multiple (code/kva/kva.py:270-273)."""
+    return n - max(0, (n - base) // block * block)
+
+
+def check_weights(tensors, where):
+    """Refuse maps with a non-finite entry or |w| > 1e4, naming the first bad entry (code/kva/kva.py:121-134)."""
+    for name, t in tensors.items():
+        tf = t.float()
+        bad = ~torch.isfinite(tf) | (tf.abs() > MAX_ABS_WEIGHT)
+        if bool(bad.any()):
+            r, c = bad.nonzero()[0].tolist()
+            raise ValueError(f"{where}: {name} has {int(bad.sum())} non-finite or |w| > {MAX_ABS_WEIGHT:g} weights "
+                             f"(first at row {r}, col {c}: {tf[r, c].item():.4g}); refusing")
+
+
+class Projector:
+    """Per late layer x_i = b W_i^T + c_i in bf16 (code/kva/kva.py:137-159). Maps may live anywhere;
+    the first call on a GPU keeps one bf16 device copy (release() drops it). File format
+    (code/kva/kva.py:161-193): safetensors, 'layer.{i}' = [d_out, d_in + 1] bf16, bias last column,
+    string metadata with 'split'."""
+
+    def __init__(self, split, weights, biases, meta=None):
+        self.split, self.W, self.b, self.meta = split, weights, biases, meta or {}
+        self._dev = None
+
+    def _maps(self, device):
+        if self._dev is None or self._dev[0] != device:
+            self._dev = (device,
+                         {i: w.to(device, torch.bfloat16).contiguous() for i, w in self.W.items()},
+                         {i: c.to(device, torch.bfloat16).contiguous() for i, c in self.b.items()})
+        return self._dev[1], self._dev[2]
+
+    def apply(self, i, b, out=None, ssq=None):
+        """(x_i [P, d_out] bf16, its row sum-of-squares partials) for rows b [P, d_in] bf16."""
+        W, B = self._maps(b.device)
+        return ops.map_apply(b, W[i], B[i], out, ssq)
+
+    def __call__(self, i, b):
+        return self.apply(i, b)[0]
+
+    def release(self):
+        self._dev = None
+
+    def save(self, path, meta):
+        from safetensors.torch import save_file
+        out = {f"layer.{i}": torch.cat((self.W[i].float(), self.b[i].float()[:, None]), 1).to(torch.bfloat16).cpu()
+               .contiguous() for i in sorted(self.W)}
+        check_weights(out, f"Projector.save {path}")
+        save_file(out, str(path), metadata={k: str(v) for k, v in dict(meta, split=self.split).items()})
+
+    @staticmethod
+    def meta_of(path):
+        with open(path, "rb") as f:
+            n = int.from_bytes(f.read(8), "little")
+            return json.loads(f.read(n)).get("__metadata__") or {}
+
+    @classmethod
+    def load(cls, path, device="cpu", dtype=torch.bfloat16):
+        from safetensors.torch import load_file
+        W, B = {}, {}
+        for name, t in load_file(str(path)).items():
+            check_weights({name: t}, f"Projector.load {path}")
+            i = int(name.split(".")[1])
+            W[i] = t[:, :-1].to(device, dtype).contiguous()
+            B[i] = t[:, -1].to(device, dtype).contiguous()
+        meta = cls.meta_of(path)
+        return cls(int(meta["split"]), W, B, meta)
+
+
+def check_rows(exact_rows, P):
+    """Sorted unique int64 rows < P, else ValueError (code/kva/kva.py:357-362)."""
+    rows = torch.as_tensor(exact_rows, dtype=torch.long)
+    if rows.dim() != 1 or rows.numel() == 0:
+        raise ValueError("exact rows: a non-empty 1-d row list")
+    rc = rows.cpu()
+    if int(rc[-1]) >= P or int(rc[0]) < 0 or bool((rc.diff() <= 0).any()):
+        raise ValueError("exact rows: sorted unique rows < P")
+    return rows
+
+
+def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None):
+    """The late-layer fill of finish() for one arm: every late layer's cache filled from the prefix rows
+    [0, P) of h_split [N, H] (bf16, on the GPU). exact_rows: sorted prefix rows whose layer inputs are
+    given by hr (one [|R|, H] tensor for every layer, or {layer: tensor}) instead of the fill's x.
+    Returns (cache, P)."""
+    n = h_split.shape[0]
+    P = arm.prefix_len(n)
+    cache = model.new_cache() if cache is None else cache
+    if arm.fill not in ("proj", "identity"):
+        raise ValueError(f"fill {arm.fill!r}: fill_late runs 'proj' and 'identity'")
+    if P == 0:
+        return cache, P
+    dev = h_split.device
+    b = h_split[:P]
+    pos = torch.arange(P, device=dev)
+    cs = model.rope_table(pos)
+    rows = None
+    if exact_rows is not None and len(exact_rows) > 0:
+        rows = check_rows(exact_rows, P).to(dev)
+    H = h_split.shape[1]
+    xbuf = torch.empty(P, H, dtype=torch.bfloat16, device=dev)
+    sbuf = torch.empty(P, ops.ssq_parts(H), dtype=torch.float32, device=dev)
+    base_ssq = None
+    for i in range(arm.split, model.n_layers):
+        if arm.fill == "proj":
+            x, ssq = arm.projector.apply(i, b, xbuf, sbuf)
+        else:
+            if rows is None:
+                base_ssq = ops.row_ssq(b) if base_ssq is None else base_ssq
+                x, ssq = b, base_ssq
+            else:
+                x = xbuf.copy_(b)
+                ssq = ops.row_ssq(x, sbuf)
+        if rows is not None:
+            hri = hr[i] if isinstance(hr, dict) else hr
+            ops.row_scatter(x, ssq, rows, hri.to(dev, torch.bfloat16))
+        model.fill(i, x, pos, cache, ssq=ssq, cs=cs)
+    return cache, P

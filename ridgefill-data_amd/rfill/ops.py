@@ -1,0 +1,183 @@
+"""Torch-tensor front end of the librfill kernels (device memory and streams are PyTorch's; the
+arithmetic is the HIP kernels'). Every function checks devices, dtypes and layouts before it hands
+raw pointers to the C ABI, and launches on the current stream of the tensors' device."""
+import math
+
+import torch
+
+from . import _lib
+from ._lib import SSQ_COLS
+
+
+def _stream(t):
+    return ctypes_ptr(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def ctypes_ptr(v):
+    return v if v else None
+
+
+def _ptr(t):
+    return t.data_ptr() if t is not None else None
+
+
+def _need(t, name, dtype, dims=None):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name}: expected a tensor")
+    if t.device.type != "cuda":
+        raise ValueError(f"{name}: must be on a GPU (got {t.device}); the fill has no CPU path")
+    if t.dtype != dtype:
+        raise ValueError(f"{name}: dtype {t.dtype}, expected {dtype}")
+    if dims is not None and t.dim() != dims:
+        raise ValueError(f"{name}: {t.dim()}-d, expected {dims}-d")
+    if t.dim() and t.stride(-1) != 1:
+        raise ValueError(f"{name}: last dim must be contiguous")
+
+
+def ssq_parts(h):
+    """Partials per row for width h."""
+    if h % SSQ_COLS:
+        raise ValueError(f"hidden size {h} is not a multiple of {SSQ_COLS}")
+    return h // SSQ_COLS
+
+
+def map_apply(b, w, c, out=None, ssq=None):
+    """x = b W^T + c in bf16 (Projector.__call__) and x's row sum-of-squares partials.
+    b [P, h_in], w [h_out, h_in], c [h_out] or None. Returns (x [P, h_out], ssq [P, h_out / 256])."""
+    _need(b, "b", torch.bfloat16, 2)
+    _need(w, "w", torch.bfloat16, 2)
+    if not w.is_contiguous():
+        raise ValueError("w must be contiguous")
+    if c is not None:
+        _need(c, "c", torch.bfloat16, 1)
+    P, h_in = b.shape
+    h_out = w.shape[0]
+    if w.shape[1] != h_in or (c is not None and c.shape[0] != h_out):
+        raise ValueError(f"map shapes: b {tuple(b.shape)}, w {tuple(w.shape)}, c {None if c is None else tuple(c.shape)}")
+    out = torch.empty(P, h_out, dtype=torch.bfloat16, device=b.device) if out is None else out
+    ssq = torch.empty(P, ssq_parts(h_out), dtype=torch.float32, device=b.device) if ssq is None else ssq
+    _need(out, "out", torch.bfloat16, 2)
+    _need(ssq, "ssq", torch.float32, 2)
+    if tuple(out.shape) != (P, h_out) or tuple(ssq.shape) != (P, h_out // SSQ_COLS) or not ssq.is_contiguous():
+        raise ValueError("map_apply: output shapes")
+    _lib.call("rf_map_apply", _ptr(b), b.stride(0), _ptr(w), _ptr(c), _ptr(out), out.stride(0), _ptr(ssq),
+              P, h_in, h_out, _stream(b))
+    return out, ssq
+
+
+def row_ssq(x, ssq=None):
+    """Row sum-of-squares partials [P, H / 256] of layer inputs x [P, H]."""
+    _need(x, "x", torch.bfloat16, 2)
+    P, H = x.shape
+    ssq = torch.empty(P, ssq_parts(H), dtype=torch.float32, device=x.device) if ssq is None else ssq
+    _need(ssq, "ssq", torch.float32, 2)
+    if tuple(ssq.shape) != (P, H // SSQ_COLS) or not ssq.is_contiguous():
+        raise ValueError("row_ssq: ssq shape")
+    _lib.call("rf_row_ssq", _ptr(x), x.stride(0), _ptr(ssq), P, H, _stream(x))
+    return ssq
+
+
+def row_scatter(x, ssq, rows, hr):
+    """In place: x[rows] = hr (bit-exact) and those rows' ssq partials (x.index_copy(0, rows, hr))."""
+    _need(x, "x", torch.bfloat16, 2)
+    _need(ssq, "ssq", torch.float32, 2)
+    _need(rows, "rows", torch.int64, 1)
+    _need(hr, "hr", torch.bfloat16, 2)
+    P, H = x.shape
+    if hr.shape[1] != H or hr.shape[0] != rows.shape[0] or tuple(ssq.shape) != (P, ssq_parts(H)):
+        raise ValueError("row_scatter: shapes")
+    _lib.call("rf_row_scatter", _ptr(x), x.stride(0), _ptr(ssq), P, H, _ptr(rows), rows.shape[0], _ptr(hr),
+              hr.stride(0), _stream(x))
+    return x
+
+
+def fold_norm(w, gain, kind):
+    """bf16(w * gain) (kind 0, rms_norm) or bf16(w * (1 + gain)) (kind 1, rms_norm_zc), per column."""
+    _need(w, "w", torch.bfloat16, 2)
+    _need(gain, "gain", torch.bfloat16, 1)
+    w = w.contiguous()
+    gain = gain.contiguous()
+    if gain.shape[0] != w.shape[1]:
+        raise ValueError("fold_norm: gain width")
+    out = torch.empty_like(w)
+    _lib.call("rf_fold_norm", _ptr(w), _ptr(gain), int(kind), _ptr(out), w.shape[0], w.shape[1], _stream(w))
+    return out
+
+
+def rope_table(pos, inv_freq):
+    """RoPE table [P, rot]: bf16 cos of the rot / 2 angles, then their bf16 sin (rope_cos_sin's half table)."""
+    _need(pos, "pos", torch.int64, 1)
+    _need(inv_freq, "inv_freq", torch.float32, 1)
+    rot = 2 * inv_freq.shape[0]
+    cs = torch.empty(pos.shape[0], rot, dtype=torch.bfloat16, device=pos.device)
+    _lib.call("rf_rope_table", _ptr(pos.contiguous()), pos.shape[0], _ptr(inv_freq.contiguous()), rot, _ptr(cs),
+              _stream(pos))
+    return cs
+
+
+def _cache_args(kbuf, vbuf, hkv, d, slot_begin, m):
+    for name, t in (("kbuf", kbuf), ("vbuf", vbuf)):
+        _need(t, name, torch.bfloat16, 3)
+        if t.shape[0] != hkv or t.shape[2] != d:
+            raise ValueError(f"{name}: shape {tuple(t.shape)}, expected [{hkv}, cap, {d}]")
+    if kbuf.stride() != vbuf.stride() or kbuf.shape != vbuf.shape:
+        raise ValueError("kbuf / vbuf must share shape and strides")
+    return kbuf.stride(0), kbuf.stride(1), kbuf.shape[1]
+
+
+def norm_kv_write(x, ssq, eps, wkv, hkv, d, knorm, knorm_kind, cs, kbuf, vbuf, slot_begin):
+    """Fused fill of one attention layer: RMSNorm (gain folded into wkv), K / V projections, k_norm,
+    RoPE, write of rows [slot_begin, slot_begin + P) into kbuf / vbuf [hkv, cap, d]."""
+    _need(x, "x", torch.bfloat16, 2)
+    _need(ssq, "ssq", torch.float32, 2)
+    _need(wkv, "wkv", torch.bfloat16, 2)
+    _need(cs, "cs", torch.bfloat16, 2)
+    P, H = x.shape
+    if tuple(ssq.shape) != (P, ssq_parts(H)) or not ssq.is_contiguous():
+        raise ValueError("norm_kv_write: ssq shape")
+    if tuple(wkv.shape) != (2 * hkv * d, H) or not wkv.is_contiguous():
+        raise ValueError(f"norm_kv_write: wkv {tuple(wkv.shape)}, expected ({2 * hkv * d}, {H})")
+    if cs.shape[0] != P or not cs.is_contiguous():
+        raise ValueError("norm_kv_write: cs rows")
+    if knorm is not None:
+        _need(knorm, "knorm", torch.bfloat16, 1)
+        if knorm.shape[0] != d:
+            raise ValueError("norm_kv_write: knorm width")
+    hs, rs, cap = _cache_args(kbuf, vbuf, hkv, d, slot_begin, P)
+    _lib.call("rf_norm_kv_write", _ptr(x), x.stride(0), _ptr(ssq), P, H, float(eps), _ptr(wkv), hkv, d,
+              _ptr(knorm), int(knorm_kind), _ptr(cs), cs.shape[1], _ptr(kbuf), _ptr(vbuf), hs, rs,
+              int(slot_begin), cap, _stream(x))
+
+
+def rope_kv_write(k, v, cs, kbuf, vbuf, slot_begin):
+    """fill_kv: RoPE on pre-RoPE k and the write of k / v [m, hkv, d] into rows [slot_begin, +m)."""
+    for name, t in (("k", k), ("v", v)):
+        _need(t, name, torch.bfloat16, 3)
+        if t.stride(1) != t.shape[2]:
+            raise ValueError(f"{name}: heads of one token must be contiguous")
+    _need(cs, "cs", torch.bfloat16, 2)
+    m, hkv, d = k.shape
+    if tuple(v.shape) != (m, hkv, d) or cs.shape[0] != m or not cs.is_contiguous():
+        raise ValueError("rope_kv_write: shapes")
+    hs, rs, cap = _cache_args(kbuf, vbuf, hkv, d, slot_begin, m)
+    _lib.call("rf_rope_kv_write", _ptr(k), k.stride(0), _ptr(v), v.stride(0), m, hkv, d, _ptr(cs), cs.shape[1],
+              _ptr(kbuf), _ptr(vbuf), hs, rs, int(slot_begin), cap, _stream(k))
+
+
+# ------------------------------------------------------------------------ host-side RoPE frequencies
+
+def inv_freq_default(theta, rot_dim):
+    """theta^(-2j/rot), fp32 on the host, as the reference computes it (code/kva/ops.py:42-43)."""
+    return 1.0 / (theta ** (torch.arange(0, rot_dim, 2, dtype=torch.float32) / rot_dim))
+
+
+def inv_freq_llama3(theta, dim, factor, low_freq_factor, high_freq_factor, original_max):
+    """Llama-3.1 rescale of the default frequencies (code/kva/ops.py:46-56)."""
+    inv = inv_freq_default(theta, dim)
+    wavelen = 2 * math.pi / inv
+    lo_wl, hi_wl = original_max / low_freq_factor, original_max / high_freq_factor
+    scaled = torch.where(wavelen > lo_wl, inv / factor, inv)
+    smooth = (original_max / wavelen - low_freq_factor) / (high_freq_factor - low_freq_factor)
+    mixed = (1 - smooth) * scaled / factor + smooth * scaled
+    mid = (wavelen >= hi_wl) & (wavelen <= lo_wl)
+    return torch.where(mid, mixed, scaled)

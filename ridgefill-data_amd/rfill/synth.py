@@ -1,0 +1,71 @@
+"""Seeded synthetic workloads for the fill (no checkpoints or datasets are used).
+
+  dense_fill(...)  Llama-3.1-8B / Qwen3-8B shaped late-layer fill: split-layer hidden states h_split
+                   [N, H] bf16 = N(0, 1) rows x a per-channel log-normal(0, 0.5) gain, 4 outlier
+                   channels x 20; per late layer l a ridge map W_l = I + 0.02 N(0, 1/H) (variance 1/H)
+                   with bias N(0, 1e-3) (std), an input RMSNorm gain 1 + N(0, 0.05), K / V projections
+                   N(0, 0.02) and, for Qwen3, a k_norm gain 1 + N(0, 0.05).
+Seeds: 10 (rows), 11 (channel gains and outliers), 12 + l (layer l's weights), 13 (exact-row
+positions), 14 (exact-row inputs). Normal(mu, s) parameters are standard deviations except the
+explicit variance 1/H of the map noise.
+"""
+import torch
+
+LLAMA_8B = dict(model_type="llama", num_hidden_layers=32, hidden_size=4096, num_attention_heads=32,
+                num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-5, rope_theta=500000.0)
+QWEN3_8B = dict(model_type="qwen3", num_hidden_layers=36, hidden_size=4096, num_attention_heads=32,
+                num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-6,
+                rope_parameters=dict(rope_type="default", rope_theta=1000000.0))
+
+
+def _gen(seed, device):
+    return torch.Generator(device=device).manual_seed(seed)
+
+
+def hidden_states(n, h, device="cpu", seed_rows=10, seed_gain=11, outliers=4, outlier_scale=20.0):
+    """[n, h] bf16 split-layer rows: N(0, 1) x log-normal(0, 0.5) channel gain, `outliers` channels x 20."""
+    g = _gen(seed_gain, "cpu")
+    gain = torch.exp(0.5 * torch.randn(h, generator=g))
+    pick = torch.randperm(h, generator=g)[:outliers]
+    gain[pick] *= outlier_scale
+    rows = torch.randn(n, h, generator=_gen(seed_rows, device), device=device)
+    return (rows * gain.to(device)).to(torch.bfloat16)
+
+
+def layer_weights(cfg, layer, device="cpu", map_noise=0.02, with_map=True):
+    """HF-named weights of one late attention layer plus its ridge map (W, c), seed 12 + layer."""
+    h, hkv, d = cfg["hidden_size"], cfg["num_key_value_heads"], cfg["head_dim"]
+    g = _gen(12 + layer, device)
+    p = f"model.layers.{layer}."
+    t = {
+        p + "input_layernorm.weight": 1 + 0.05 * torch.randn(h, generator=g, device=device),
+        p + "self_attn.k_proj.weight": 0.02 * torch.randn(hkv * d, h, generator=g, device=device),
+        p + "self_attn.v_proj.weight": 0.02 * torch.randn(hkv * d, h, generator=g, device=device),
+    }
+    if cfg["model_type"] != "llama":
+        t[p + "self_attn.k_norm.weight"] = 1 + 0.05 * torch.randn(d, generator=g, device=device)
+    t = {k: v.to(torch.bfloat16) for k, v in t.items()}
+    if not with_map:
+        return t, None, None
+    w = torch.eye(h, device=device) + map_noise * torch.randn(h, h, generator=g, device=device) / h ** 0.5
+    c = 1e-3 * torch.randn(h, generator=g, device=device)
+    return t, w.to(torch.bfloat16), c.to(torch.bfloat16)
+
+
+def dense_fill(cfg, split, n_rows, tail, device="cpu", exact_frac=0.0, with_maps=True):
+    """A late-layer fill workload: dict(cfg, split, layers, h_split [n, H], P, tensors (HF names),
+    maps {l: W}, biases {l: c}, rows (sorted exact-row positions < P), hr [|rows|, H])."""
+    L, h = cfg["num_hidden_layers"], cfg["hidden_size"]
+    layers = list(range(split, L))
+    tensors, maps, biases = {}, {}, {}
+    for l in layers:
+        t, w, c = layer_weights(cfg, l, device, with_map=with_maps)
+        tensors.update(t)
+        if with_maps:
+            maps[l], biases[l] = w, c
+    P = n_rows - tail
+    n_exact = int(round(exact_frac * P))
+    rows = torch.randperm(P, generator=_gen(13, "cpu"))[:n_exact].sort().values
+    hr = hidden_states(n_exact, h, device=device, seed_rows=14) if n_exact else None
+    return dict(cfg=cfg, split=split, layers=layers, h_split=hidden_states(n_rows, h, device=device), P=P,
+                tensors=tensors, maps=maps, biases=biases, rows=rows.to(device), hr=hr)
