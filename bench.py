@@ -1,0 +1,245 @@
+#!/usr/bin/env python3
+"""Benchmark: the RidgeFill late-layer fill of a Llama-3.1-8B-shaped 32K prompt on one MI355X.
+
+Workload (synthetic, seeded; rfill.synth): hidden 4096, 32 query / 8 KV heads, head_dim 128, RoPE
+theta 5e5, split at layer 16, 16 late layers each with a ridge map W_l = I + 0.02 N(0, 1/4096) and bias
+N(0, 1e-3); prompt 32768 rows, exact tail 4096, so P = 28672 filled rows. One step = the fill of all
+16 late layers from h_split already resident in HBM: per layer rf_map_apply (x = b W^T + c, with the
+rows' RMSNorm statistics) then rf_norm_kv_write (RMSNorm, K / V projections, RoPE, cache write).
+
+Reported: filled tokens/s = P * steps / elapsed; the dominant kernel's roofline (rf_map_apply, MFMA
+bound, 2 P H^2 flop per launch over its mean HIP-event duration on the launch stream); the second
+fill kernel and the standalone RoPE + KV-write kernel (HBM bound) beside it; library ceilings (a plain
+hipBLASLt GEMM of the same shape and a device copy); and the CPU baseline: the oracle's fill (the
+reference op sequence in torch on the host cores) timed on a bounded row sample.
+"""
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for p in (ROOT, ROOT / "ridgefill-data_amd"):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+import torch  # noqa: E402
+
+METRIC = "filled tokens/s (16-layer fill, 8B, 32K); MFMA % bf16 peak; HBM GB/s"
+PEAK_BF16 = 2.5e15        # MI355X dense bf16 MFMA, FLOP/s
+PEAK_HBM = 8.0e12         # MI355X HBM3E, B/s
+N_ROWS, TAIL, SPLIT = 32768, 4096, 16
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+class KernelTimer:
+    """Start / end HIP events around launches on the current stream; mean duration per name."""
+
+    def __init__(self):
+        self.ev = {}
+
+    def run(self, name, fn):
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        out = fn()
+        e.record()
+        self.ev.setdefault(name, []).append((s, e))
+        return out
+
+    def mean_s(self, name):
+        pairs = self.ev.get(name, [])
+        return sum(s.elapsed_time(e) for s, e in pairs) / max(1, len(pairs)) / 1e3
+
+
+def build_workload(dev):
+    from rfill import synth
+    from rfill.kva import Arm, Projector
+    from rfill.model import FillModel
+    cfg = synth.LLAMA_8B
+    log("generating the synthetic workload on the GPU")
+    w = synth.dense_fill(cfg, SPLIT, N_ROWS, TAIL, device=dev)
+    model = FillModel(cfg, w["tensors"], dev, layers=w["layers"])
+    arm = Arm("ridgefill", split=SPLIT, tail=TAIL, fill="proj", projector=Projector(SPLIT, w["maps"], w["biases"]))
+    return cfg, w, model, arm
+
+
+def fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches, timer=None):
+    """One step: the 16-layer fill (the hot path of finish() for the ridgefill arm, no exact rows)."""
+    from rfill import ops
+    W, B = arm.projector._maps(b.device)
+    for i in range(arm.split, model.n_layers):
+        w, c = model.W[i], caches[i]
+        m1 = lambda: ops.map_apply(b, W[i], B[i], xbuf, sbuf)                         # noqa: E731
+        m2 = lambda: ops.norm_kv_write(xbuf, sbuf, model.eps, w["wkv"], model.n_kv, model.head_dim,  # noqa: E731
+                                       w.get("k_norm"), model.knorm_kind, cs, c["kbuf"], c["vbuf"], 0)
+        if timer is None:
+            m1()
+            m2()
+        else:
+            timer.run("rf_map_apply", m1)
+            timer.run("rf_norm_kv_write", m2)
+
+
+def ceilings(dev, P, H):
+    """Library GEMM (hipBLASLt via torch) of the map's shape and a device-to-device copy."""
+    a = torch.randn(P, H, device=dev, dtype=torch.bfloat16)
+    w = torch.randn(H, H, device=dev, dtype=torch.bfloat16)
+    out = torch.empty(P, H, device=dev, dtype=torch.bfloat16)
+    for _ in range(3):
+        torch.matmul(a, w.t(), out=out)
+    torch.cuda.synchronize()
+    t = KernelTimer()
+    for _ in range(10):
+        t.run("gemm", lambda: torch.matmul(a, w.t(), out=out))
+    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    for _ in range(10):
+        t.run("copy", lambda: dst.copy_(src))
+    torch.cuda.synchronize()
+    return {"hipblaslt_gemm_tflops": round(2 * P * H * H / t.mean_s("gemm") / 1e12, 1),
+            "copy_gbs": round(2 * src.numel() / t.mean_s("copy") / 1e9, 1),
+            "gemm_shape": [P, H, H]}
+
+
+def kv_write_bench(model, dev, P, layer):
+    """The standalone RoPE + K / V cache write (fill_kv) at the workload's shape: HBM bound,
+    algorithmic bytes 4 Hkv d 2 per row (read pre-RoPE K, V; write post-RoPE K, V)."""
+    from rfill import ops
+    hkv, d = model.n_kv, model.head_dim
+    k = torch.randn(P, hkv, d, device=dev).to(torch.bfloat16)
+    v = torch.randn(P, hkv, d, device=dev).to(torch.bfloat16)
+    cs = model.rope_table(torch.arange(P, device=dev))
+    kb = torch.empty(hkv, P + 64, d, dtype=torch.bfloat16, device=dev)
+    vb = torch.empty_like(kb)
+    for _ in range(3):
+        ops.rope_kv_write(k, v, cs, kb, vb, 0)
+    torch.cuda.synchronize()
+    t = KernelTimer()
+    for _ in range(20):
+        t.run("kv", lambda: ops.rope_kv_write(k, v, cs, kb, vb, 0))
+    torch.cuda.synchronize()
+    sec = t.mean_s("kv")
+    byts = 4 * hkv * d * 2 * P
+    return {"kernel": "rf_rope_kv_write", "bound": "hbm", "achieved": round(byts / sec / 1e9, 1),
+            "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": round(byts / sec / PEAK_HBM, 4),
+            "bytes_per_launch": byts, "mean_us": round(sec * 1e6, 2)}
+
+
+def cpu_baseline(cfg, w, layer, budget_s=12.0, rows=1024):
+    """The oracle's fill (reference op sequence: F.linear map in bf16, rms_norm, K / V F.linear, RoPE,
+    cache append) on the host, for `rows`-row blocks of one late layer until `budget_s` has passed;
+    scaled to filled tokens/s of the 16-layer fill."""
+    from oracle import model as OM
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    b = w["h_split"][:rows].cpu()
+    W, c = w["maps"][layer].cpu(), w["biases"][layer].cpu()
+    t = {k: v.cpu() for k, v in w["tensors"].items() if f"layers.{layer}." in k}
+    om = OM.OracleModel(cfg, t, dtype=torch.bfloat16, layers=[layer])
+    pos = torch.arange(rows)
+    done, t0 = 0, time.perf_counter()
+    while True:
+        cache = om.new_cache()
+        x = torch.nn.functional.linear(b, W, c)
+        om.fill(layer, x, pos, cache)
+        done += rows
+        el = time.perf_counter() - t0
+        if el >= budget_s:
+            break
+    rate = done / el / (cfg["num_hidden_layers"] - SPLIT)
+    return {"value": round(rate, 2), "unit": "filled tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle fill of one late layer, {rows}-row blocks x {done // rows} in {el:.1f} s, bf16, "
+                      f"scaled by 1/16 layers; torch {torch.__version__}"}
+
+
+def traffic_from_profiles(kernel):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE scaled
+    by a copy kernel of known size), or None if it has not been measured."""
+    f = ROOT / "profiles" / "traffic.json"
+    if not f.exists():
+        return None
+    try:
+        return json.loads(f.read_text()).get(kernel, {}).get("traffic_bytes")
+    except (ValueError, OSError):
+        return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-extras", action="store_true", help="skip ceilings and the standalone KV-write leg")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py: this build measures one GPU only (one MI355X per box); --gpus must be 1", file=sys.stderr)
+        sys.exit(2)
+    dev = torch.device("cuda")
+    torch.cuda.set_device(0)
+    cfg, w, model, arm = build_workload(dev)
+    P = w["P"]
+    H = cfg["hidden_size"]
+    b = w["h_split"][:P]
+    pos = torch.arange(P, device=dev)
+    cs = model.rope_table(pos)
+    xbuf = torch.empty(P, H, dtype=torch.bfloat16, device=dev)
+    sbuf = torch.empty(P, H // 256, dtype=torch.float32, device=dev)
+    caches = model.new_cache()
+    for i in w["layers"]:
+        caches[i] = dict(kbuf=torch.empty(model.n_kv, P + 64, model.head_dim, dtype=torch.bfloat16, device=dev),
+                         vbuf=torch.empty(model.n_kv, P + 64, model.head_dim, dtype=torch.bfloat16, device=dev), n=0)
+    log(f"warmup {args.warmup} steps")
+    for _ in range(args.warmup):
+        fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches)
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    timer = KernelTimer()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches, timer)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    L = len(w["layers"])
+    map_s, kv_s = timer.mean_s("rf_map_apply"), timer.mean_s("rf_norm_kv_write")
+    map_flop = 2 * P * H * H
+    kv_flop = 2 * P * H * 2 * model.n_kv * model.head_dim
+    step_flop = L * (map_flop + kv_flop)
+    ms_step = elapsed / args.steps * 1e3
+    out = {
+        "metric": METRIC, "value": round(P * args.steps / elapsed, 1), "unit": "filled tokens/s", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms_step, 3), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "llama-3.1-8b-shaped 32K fill: 16 late layers (split 16), 28672 filled rows, tail 4096",
+                   "hidden": H, "kv_heads": model.n_kv, "head_dim": model.head_dim, "late_layers": L,
+                   "seq_len": N_ROWS, "filled_rows": P, "parallelism": "none (1 GPU)"},
+        "roofline": {"kernel": "rf_map_apply", "bound": "mfma",
+                     "achieved": round(map_flop / map_s / 1e12, 1), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
+                     "frac": round(map_flop / map_s / PEAK_BF16, 4), "traffic": traffic_from_profiles("rf_map_apply"),
+                     "flop_per_launch": map_flop, "mean_us": round(map_s * 1e6, 1)},
+        "fill_mfma_frac": round(step_flop / (elapsed / args.steps) / PEAK_BF16, 4),
+        "kernels": {"rf_norm_kv_write": {"bound": "mfma", "mean_us": round(kv_s * 1e6, 1),
+                                         "achieved_tflops": round(kv_flop / kv_s / 1e12, 1),
+                                         "frac": round(kv_flop / kv_s / PEAK_BF16, 4), "flop_per_launch": kv_flop,
+                                         "traffic": traffic_from_profiles("rf_norm_kv_write")}},
+    }
+    if not args.no_extras:
+        log("standalone RoPE + KV write and library ceilings")
+        out["kernels"]["rf_rope_kv_write"] = kv_write_bench(model, dev, P, SPLIT)
+        out["ceilings"] = ceilings(dev, P, H)
+    if not args.no_cpu:
+        log("CPU baseline (oracle fill on the host cores)")
+        out["cpu_baseline"] = cpu_baseline(cfg, w, SPLIT)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
