@@ -5,11 +5,11 @@
 //
 // Tiling. A workgroup of 4 wave64s computes a 256 x 256 output tile over K in 64-wide steps. Both
 // operands are K-contiguous (row-major activations, F.linear-layout weights), so each 64-wide K slice
-// of a 256-row operand tile is 256 rows x 128 bytes: 8 threads load one row with 128-bit loads.
-// The slices sit in LDS with the 16-byte chunk index XOR-ed by the row's low 3 bits, so the MFMA
-// fragment reads (32 rows, one chunk) and the loader's writes (one row, 8 chunks) both spread over
-// all banks. Two LDS stages (2 x 64 KiB): the next slice is fetched into registers while the current
-// one feeds the MFMAs, then stored to the other stage; one barrier per step.
+// of a 256-row operand tile is 256 rows x 128 bytes. The slices go from memory straight into LDS
+// (buffer_load_dwordx4 ... lds, no staging registers; the buffer's range check turns rows past M into
+// zeros) with the 16-byte chunk index XOR-ed by the row's low 3 bits, so the MFMA fragment reads
+// (32 rows, one chunk per lane) hit all banks. Two LDS stages (2 x 64 KiB): the loads of step k+1 are
+// in flight while step k feeds the MFMAs; one wait and one barrier per step.
 //
 // Each wave owns a 128 x 128 quarter and issues v_mfma_f32_32x32x16_bf16 on 4 x 4 sub-tiles. The
 // weight tile is the MFMA's A operand and the activation tile its B operand, so the accumulator of a
@@ -39,6 +39,28 @@ __device__ __forceinline__ int xcd_tile(int bid, int nb) {
   return (x < r) ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
 }
 
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+// Raw buffer resource over [base, base + bytes): loads past the end return zeros (rows >= M).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+// One K step's operand tiles straight from memory into an LDS stage (buffer_load_dwordx4 ... lds):
+// each instruction fills 64 consecutive 16-byte slots, lane L writing slot base + L. Slot s of a
+// 256-row tile holds row s / 8, chunk (s % 8) ^ (row & 7); for wave w's instruction j that is row
+// w*64 + j*8 + L/8 and chunk (L % 8) ^ (L / 8), so the lane picks its global address to match.
+__device__ __forceinline__ void issue_tiles(__amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rw, const uint32_t (&vx)[8],
+                                            const uint32_t (&vw)[8], int k0, char* stage, int w) {
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int slot0 = w * 512 + j * 64;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(stage + slot0 * 16), 16, vx[j], k0 * 2, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(stage + BM * 128 + slot0 * 16), 16, vw[j], k0 * 2, 0, 0);
+  }
+}
+
 // acc[nt][mt] += W[n0 + wn*128 + nt*32 .. +32, :] . X[m0 + wm*128 + mt*32 .. +32, :]^T over all of K.
 // Rows of X at or past M read as zeros. Ends with a barrier: LDS is free for the epilogue.
 __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t ldx,
@@ -46,30 +68,18 @@ __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t
                                          int m0, int n0, uint4* lds, f32x16 (&acc)[4][4]) {
   const int t = threadIdx.x, lane = t & 63, w = t >> 6;
   const int wm = w >> 1, wn = w & 1;
-  const int lrow = t >> 3, lch = t & 7;           // loader: rows lrow + 32 i, 16-byte chunk lch
-  const int lpos = lrow * 8 + (lch ^ (lrow & 7)); // swizzled slot of (lrow, lch); + 256 per 32 rows
-  const uint16_t* gx = X + static_cast<int64_t>(m0 + lrow) * ldx + lch * 8;
-  const uint16_t* gw = W + static_cast<int64_t>(n0 + lrow) * ldw + lch * 8;
-  const int rows_left = M - m0 - lrow;            // X rows i with 32 i < rows_left are in range
-
-  uint4 rx[8], rw[8];
-  auto fetch = [&](int k0) {
+  const int rows_x = min(M - m0, BM);
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(X + static_cast<int64_t>(m0) * ldx,
+                                                static_cast<uint32_t>(rows_x * ldx * 2));
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(W + static_cast<int64_t>(n0) * ldw, static_cast<uint32_t>(BN * ldw * 2));
+  const int lr8 = lane >> 3, lch = (lane & 7) ^ lr8;
+  uint32_t vx[8], vw[8];
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      rx[i] = (32 * i < rows_left) ? *reinterpret_cast<const uint4*>(gx + 32 * i * ldx + k0)
-                                   : make_uint4(0u, 0u, 0u, 0u);
-      rw[i] = *reinterpret_cast<const uint4*>(gw + 32 * i * ldw + k0);
-    }
-  };
-  auto stash = [&](int s) {
-    uint4* sx = lds + s * STAGE_U4;
-    uint4* sw = sx + BM * 8;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      sx[lpos + 256 * i] = rx[i];
-      sw[lpos + 256 * i] = rw[i];
-    }
-  };
+  for (int j = 0; j < 8; ++j) {
+    const int row = w * 64 + j * 8 + lr8;
+    vx[j] = static_cast<uint32_t>((row * ldx + lch * 8) * 2);
+    vw[j] = static_cast<uint32_t>((row * ldw + lch * 8) * 2);
+  }
 
 #pragma unroll
   for (int a = 0; a < 4; ++a)
@@ -78,32 +88,41 @@ __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
-  fetch(0);
-  stash(0);
+  char* base = reinterpret_cast<char*>(lds);
+  issue_tiles(rx, rw, vx, vw, 0, base, w);
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
   const int nk = K / BK;
   const int lr = lane & 31, lk = lane >> 5, sw7 = lane & 7;
   for (int kt = 0; kt < nk; ++kt) {
     const int s = kt & 1;
-    if (kt + 1 < nk) fetch((kt + 1) * BK);
+    if (kt + 1 < nk) issue_tiles(rx, rw, vx, vw, (kt + 1) * BK, base + (s ^ 1) * STAGE_U4 * 16, w);
     const uint4* sx = lds + s * STAGE_U4;
     const uint4* sw = sx + BM * 8;
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
+    // Fragments of K slice ks + 1 are read while slice ks's 16 MFMAs run (two fragment sets).
+    bf16x8 fx[2][4], fw[2][4];
+    auto read_frags = [&](int ks, bf16x8 (&ax)[4], bf16x8 (&aw)[4]) {
       const int slot = (ks * 2 + lk) ^ sw7;
-      bf16x8 fx[4], fw[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        fx[i] = as_frag(sx[(wm * 128 + i * 32 + lr) * 8 + slot]);
-        fw[i] = as_frag(sw[(wn * 128 + i * 32 + lr) * 8 + slot]);
+        aw[i] = as_frag(sw[(wn * 128 + i * 32 + lr) * 8 + slot]);
+        ax[i] = as_frag(sx[(wm * 128 + i * 32 + lr) * 8 + slot]);
       }
+    };
+    read_frags(0, fx[0], fw[0]);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      const int cur = ks & 1;
+      if (ks + 1 < BK / 16) read_frags(ks + 1, fx[cur ^ 1], fw[cur ^ 1]);
+      __builtin_amdgcn_sched_barrier(0);          // keep the reads ahead of this slice's MFMAs
 #pragma unroll
       for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
         for (int mt = 0; mt < 4; ++mt)
-          acc[nt][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[nt], fx[mt], acc[nt][mt], 0, 0, 0);
+          acc[nt][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[cur][nt], fx[cur][mt], acc[nt][mt], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    if (kt + 1 < nk) stash(s ^ 1);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
   }
 }
@@ -301,7 +320,7 @@ extern "C" int rf_map_apply(const uint16_t* b, int64_t ldb, const uint16_t* w, c
   if (h_in <= 0 || h_in % BK || h_out <= 0 || h_out % BN)
     return fail(RF_EINVAL_SHAPE, "rf_map_apply: h_in %lld must be a multiple of 64 and h_out %lld of 256",
                 (long long)h_in, (long long)h_out);
-  if (ldb < h_in || ldx < h_out || ldb % 8 || ldx % 8)
+  if (ldb < h_in || ldx < h_out || ldb % 8 || ldx % 8 || ldb > (1 << 21) || h_in > (1 << 21))
     return fail(RF_EINVAL_SHAPE, "rf_map_apply: row strides ldb %lld / ldx %lld", (long long)ldb, (long long)ldx);
   if (!aligned16(b) || !aligned16(w) || !aligned16(x) || (c && (reinterpret_cast<uintptr_t>(c) & 7u)))
     return fail(RF_EINVAL_SHAPE, "rf_map_apply: pointers must be 16-byte aligned (bias 8-byte)");
@@ -327,7 +346,7 @@ extern "C" int rf_norm_kv_write(const uint16_t* x, int64_t ldx, const float* ssq
     return fail(RF_EUNSUPPORTED, "rf_norm_kv_write: rotary dims %d of head_dim %d", rot, d);
   if (knorm && knorm_kind != 0 && knorm_kind != 1)
     return fail(RF_EINVAL_ARG, "rf_norm_kv_write: knorm_kind %d", knorm_kind);
-  if (ldx < H || ldx % 8 || head_stride % 8 || row_stride % 8 || row_stride < d)
+  if (ldx < H || ldx % 8 || ldx > (1 << 21) || head_stride % 8 || row_stride % 8 || row_stride < d)
     return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write: strides (ldx %lld, head %lld, row %lld)", (long long)ldx,
                 (long long)head_stride, (long long)row_stride);
   if (slot_begin < 0 || slot_begin + P > cap)
