@@ -17,6 +17,8 @@
 // epilogue rounds them to bf16 and writes 8-byte runs into a row-major LDS image of the 256 x 256
 // tile, which a row pass then reads as 16-byte chunks (32 threads per 256-column row) to compute
 // row statistics, apply k_norm / RoPE and issue coalesced 128-bit stores.
+#include <type_traits>
+
 #include "rf_common.h"
 
 namespace rf {
@@ -25,19 +27,40 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 256, BN = 256, BK = 64, NTHR = 256;
-constexpr int STAGE_U4 = (BM + BN) * BK / 8;   // 16-byte chunks per LDS stage (activations, then weights)
-constexpr int LDS_U4 = 2 * STAGE_U4;           // 128 KiB; reused by the epilogue as the 256 x 256 bf16 tile
+constexpr int BM = 256, BN = 256, BK = 32, NTHR = 256;
+constexpr int STAGES = 4;                      // LDS stages: loads run STAGES - 1 K steps ahead
+constexpr int CPR = BK / 8;                    // 16-byte chunks per operand row in a stage
+constexpr int STAGE_U4 = (BM + BN) * CPR;      // 16-byte chunks per LDS stage (activations, then weights)
+constexpr int LDS_U4 = STAGES * STAGE_U4;      // 128 KiB; reused by the epilogue as the 256 x 256 bf16 tile
+constexpr int LOADS_PER_STEP = (BM + BN) * CPR / 64 / 4;   // direct-load instructions per wave per K step
+static_assert(LDS_U4 >= 256 * 32, "the epilogue's 256 x 256 bf16 image must fit in the stages");
+static_assert(STAGES >= 3 && LOADS_PER_STEP == 8, "the load schedule assumes 8 loads per step, >= 3 stages");
 
 __device__ __forceinline__ bf16x8 as_frag(const uint4& u) { return __builtin_bit_cast(bf16x8, u); }
 
 // Logical tile of a hardware block. Blocks are dealt round-robin over the 8 XCDs (block b runs on
-// XCD b % 8); this gives every XCD a contiguous run of logical tiles, and tiles are numbered
-// column-fastest, so the tiles sharing one 256-row activation block mostly share one XCD's L2.
+// XCD b % 8); this gives every XCD a contiguous run of logical tiles.
 __device__ __forceinline__ int xcd_tile(int bid, int nb) {
   const int q = nb >> 3, r = nb & 7, x = bid & 7, i = bid >> 3;
   return (x < r) ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
 }
+
+// Logical tile -> (tile row, tile column). Tiles go in groups of GROUP_M tile rows walked column by
+// column, so the ~32 tiles one XCD runs at a time form a GROUP_M x 8 block: per K step its L2 sees
+// GROUP_M activation slices and 8 weight slices instead of 2 and 16.
+constexpr int GROUP_M = 4;
+__device__ __forceinline__ void tile_coords(int tile, int tiles_m, int tiles_n, int& tm, int& tn) {
+  const int per_group = GROUP_M * tiles_n;
+  const int g = tile / per_group, in = tile - g * per_group;
+  const int rows = min(GROUP_M, tiles_m - g * GROUP_M);
+  tm = g * GROUP_M + in % rows;
+  tn = in / rows;
+}
+
+// LDS slot of (row, 16-byte chunk) in a 32-wide K slice: 4 chunks (64 bytes) per row, the chunk
+// XOR-ed with (row >> 2) & 3. A fragment read takes one chunk of 32 consecutive rows; the LDS serves
+// 16 lanes of 16 bytes per cycle, and any 16 consecutive rows then fall on distinct banks.
+__device__ __forceinline__ int row_swz(int row) { return (row >> 2) & 3; }
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
@@ -47,22 +70,38 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
                                            0x00020000);
 }
 
-// One K step's operand tiles straight from memory into an LDS stage (buffer_load_dwordx4 ... lds):
-// each instruction fills 64 consecutive 16-byte slots, lane L writing slot base + L. Slot s of a
-// 256-row tile holds row s / 8, chunk (s % 8) ^ (row & 7); for wave w's instruction j that is row
-// w*64 + j*8 + L/8 and chunk (L % 8) ^ (L / 8), so the lane picks its global address to match.
-__device__ __forceinline__ void issue_tiles(__amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rw, const uint32_t (&vx)[8],
-                                            const uint32_t (&vw)[8], int k0, char* stage, int w) {
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int slot0 = w * 512 + j * 64;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(stage + slot0 * 16), 16, vx[j], k0 * 2, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(stage + BM * 128 + slot0 * 16), 16, vw[j], k0 * 2, 0, 0);
-  }
+// s_waitcnt with vmcnt <= n and lgkmcnt = 0 (expcnt not waited), gfx9 encoding.
+template <int n>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (0 << 8) | ((n >> 4) << 14));
+}
+
+// Load j (0..7) of one K step's operand tiles, straight from memory into an LDS stage
+// (buffer_load_dwordx4 ... lds): even j fill activation rows, odd j weight rows. Each instruction fills
+// 64 consecutive 16-byte slots, lane L writing slot base + L, i.e. 16 rows x 4 chunks. Slot s of a
+// 256-row tile holds row s / 4, chunk (s % 4) ^ row_swz(row); for wave w's load j that is row
+// w*64 + (j/2)*16 + L/4 and chunk (L % 4) ^ ((L / 16) % 4), so each lane fetches the global address
+// that belongs in its slot.
+__device__ __forceinline__ void issue_one(__amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rw, const uint32_t (&vx)[4],
+                                          const uint32_t (&vw)[4], int j, int k0, char* stage, int w) {
+  const int jj = j >> 1, slot0 = w * 256 + jj * 64;
+  if (j & 1)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(stage + BM * CPR * 16 + slot0 * 16), 16, vw[jj], k0 * 2, 0, 0);
+  else
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(stage + slot0 * 16), 16, vx[jj], k0 * 2, 0, 0);
 }
 
 // acc[nt][mt] += W[n0 + wn*128 + nt*32 .. +32, :] . X[m0 + wm*128 + mt*32 .. +32, :]^T over all of K.
 // Rows of X at or past M read as zeros. Ends with a barrier: LDS is free for the epilogue.
+//
+// Pipeline: step k's tiles land in stage k % STAGES, loaded STAGES - 1 steps ahead. A step is two
+// 16-wide K slices of 16 MFMAs each. The wave's instruction stream is in order, so anything issued
+// in a burst stalls the MFMA pipe; instead one LDS fragment read for the next slice follows each of a
+// slice's first 8 MFMAs, and one global->LDS load follows every second of its last 8 (8 loads per
+// step). Between the slices the wave waits for step k + 1's loads (vmcnt) and its own LDS reads
+// (lgkmcnt 0) and meets the other waves at a barrier; after it, stage k % STAGES is free for the loads
+// issued in step k + 1, and the second slice reads step k + 1's first fragments.
 __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t ldx,
                                          const uint16_t* __restrict__ W, int64_t ldw, int M, int K,
                                          int m0, int n0, uint4* lds, f32x16 (&acc)[4][4]) {
@@ -72,13 +111,13 @@ __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t
   const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(X + static_cast<int64_t>(m0) * ldx,
                                                 static_cast<uint32_t>(rows_x * ldx * 2));
   const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(W + static_cast<int64_t>(n0) * ldw, static_cast<uint32_t>(BN * ldw * 2));
-  const int lr8 = lane >> 3, lch = (lane & 7) ^ lr8;
-  uint32_t vx[8], vw[8];
+  uint32_t vx[4], vw[4];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int row = w * 64 + j * 8 + lr8;
-    vx[j] = static_cast<uint32_t>((row * ldx + lch * 8) * 2);
-    vw[j] = static_cast<uint32_t>((row * ldw + lch * 8) * 2);
+  for (int j = 0; j < 4; ++j) {
+    const int row = w * 64 + j * 16 + (lane >> 2);
+    const int ch = (lane & 3) ^ row_swz(row);
+    vx[j] = static_cast<uint32_t>((row * ldx + ch * 8) * 2);
+    vw[j] = static_cast<uint32_t>((row * ldw + ch * 8) * 2);
   }
 
 #pragma unroll
@@ -89,42 +128,59 @@ __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t
       for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
 
   char* base = reinterpret_cast<char*>(lds);
-  issue_tiles(rx, rw, vx, vw, 0, base, w);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
   const int nk = K / BK;
-  const int lr = lane & 31, lk = lane >> 5, sw7 = lane & 7;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int s = kt & 1;
-    if (kt + 1 < nk) issue_tiles(rx, rw, vx, vw, (kt + 1) * BK, base + (s ^ 1) * STAGE_U4 * 16, w);
-    const uint4* sx = lds + s * STAGE_U4;
-    const uint4* sw = sx + BM * 8;
-    // Fragments of K slice ks + 1 are read while slice ks's 16 MFMAs run (two fragment sets).
-    bf16x8 fx[2][4], fw[2][4];
-    auto read_frags = [&](int ks, bf16x8 (&ax)[4], bf16x8 (&aw)[4]) {
-      const int slot = (ks * 2 + lk) ^ sw7;
+  const int lr = lane & 31, lk = lane >> 5, swz = row_swz(lr);
+  bf16x8 fx[2][4], fw[2][4];
+  // fragment r (0..7) of slice ks from stage st: r < 4 -> weight block r, else activation block r - 4
+  auto read_one = [&](int st, int ks, int r, bf16x8 (&ax)[4], bf16x8 (&aw)[4]) {
+    const uint4* sx = lds + st * STAGE_U4;
+    const uint4* sw = sx + BM * CPR;
+    const int slot = (ks * 2 + lk) ^ swz;
+    if (r < 4) aw[r] = as_frag(sw[(wn * 128 + r * 32 + lr) * CPR + slot]);
+    else ax[r - 4] = as_frag(sx[(wm * 128 + (r - 4) * 32 + lr) * CPR + slot]);
+  };
+  auto slice = [&](const bf16x8 (&ax)[4], const bf16x8 (&aw)[4], bool do_read, int rst, int rks, bf16x8 (&nx)[4],
+                   bf16x8 (&nw)[4], bool do_load, int half, int kload, char* lstage) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        aw[i] = as_frag(sw[(wn * 128 + i * 32 + lr) * 8 + slot]);
-        ax[i] = as_frag(sx[(wm * 128 + i * 32 + lr) * 8 + slot]);
+    for (int q = 0; q < 16; ++q) {
+      acc[q >> 2][q & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aw[q >> 2], ax[q & 3], acc[q >> 2][q & 3], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (q < 8) {
+        if (do_read) read_one(rst, rks, q, nx, nw);
+      } else if (do_load && (q & 1)) {
+        issue_one(rx, rw, vx, vw, half * 4 + ((q - 9) >> 1), kload, lstage, w);
       }
-    };
-    read_frags(0, fx[0], fw[0]);
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      const int cur = ks & 1;
-      if (ks + 1 < BK / 16) read_frags(ks + 1, fx[cur ^ 1], fw[cur ^ 1]);
-      __builtin_amdgcn_sched_barrier(0);          // keep the reads ahead of this slice's MFMAs
-#pragma unroll
-      for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-        for (int mt = 0; mt < 4; ++mt)
-          acc[nt][mt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fw[cur][nt], fx[cur][mt], acc[nt][mt], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-  }
+  };
+  // `steady` (a compile-time tag) marks the steps that still issue loads; the steady loop has no
+  // branches, so the compiler's own wait counting stays exact.
+  auto step = [&](int kt, auto steady) {
+    const int s = kt % STAGES;
+    const int kload = (kt + STAGES - 1) * BK;
+    char* lstage = base + ((kt + STAGES - 1) % STAGES) * STAGE_U4 * 16;
+    slice(fx[0], fw[0], true, s, 1, fx[1], fw[1], steady, 0, kload, lstage);
+    // outstanding after step k + 1's loads: step k + 2's (all) and step k + 3's first half
+    if (steady) wait_vm_lgkm0<LOADS_PER_STEP * (STAGES - 3) + LOADS_PER_STEP / 2>();
+    else wait_vm_lgkm0<0>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    slice(fx[1], fw[1], steady || kt + 1 < nk, (kt + 1) % STAGES, 0, fx[0], fw[0], steady, 1, kload, lstage);
+  };
+
+#pragma unroll
+  for (int st = 0; st < STAGES - 1; ++st)
+    if (st < nk)
+      for (int j = 0; j < LOADS_PER_STEP; ++j) issue_one(rx, rw, vx, vw, j, st * BK, base + st * STAGE_U4 * 16, w);
+  if (nk >= STAGES - 1) wait_vm_lgkm0<LOADS_PER_STEP * (STAGES - 2)>();
+  else wait_vm_lgkm0<0>();
+  __builtin_amdgcn_s_barrier();
+  for (int r = 0; r < 8; ++r) read_one(0, 0, r, fx[0], fw[0]);
+  int kt = 0;
+  for (; kt + STAGES - 1 < nk; ++kt) step(kt, std::true_type{});
+  for (; kt < nk; ++kt) step(kt, std::false_type{});
+  wait_vm_lgkm0<0>();
+  __syncthreads();
 }
 
 // Epilogue stage 1: value(mt, nt, g, e, acc) rounded to bf16 into the row-major LDS image of the tile.
@@ -163,8 +219,9 @@ __global__ __launch_bounds__(NTHR) void k_map_apply(const uint16_t* __restrict__
                                                     float* __restrict__ ssq, int M, int N, int K) {
   __shared__ uint4 lds[LDS_U4];
   const int tiles_n = N / BN;
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
-  const int tn = tile % tiles_n, m0 = (tile / tiles_n) * BM, n0 = tn * BN;
+  int tm, tn;
+  tile_coords(xcd_tile(blockIdx.x, gridDim.x), (M + BM - 1) / BM, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
   f32x16 acc[4][4];
   mainloop(B, ldb, W, K, M, K, m0, n0, lds, acc);
 
@@ -227,8 +284,9 @@ __global__ __launch_bounds__(NTHR) void k_norm_kv(const uint16_t* __restrict__ X
                                                   KvArgs a) {
   __shared__ uint4 lds[LDS_U4];
   const int tiles_n = N / BN;
-  const int tile = xcd_tile(blockIdx.x, gridDim.x);
-  const int m0 = (tile / tiles_n) * BM, n0 = (tile % tiles_n) * BN;
+  int tm, tn;
+  tile_coords(xcd_tile(blockIdx.x, gridDim.x), (M + BM - 1) / BM, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
   f32x16 acc[4][4];
   mainloop(Xin, ldx, W, K, M, K, m0, n0, lds, acc);
 
