@@ -69,20 +69,25 @@ def build_workload(dev):
 
 
 def fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches, timer=None):
-    """One step: the 16-layer fill (the hot path of finish() for the ridgefill arm, no exact rows)."""
+    """One step: the 16-layer fill (the hot path of finish() for the ridgefill arm, no exact rows),
+    scheduled as fill_late schedules it by default: each layer's map apply, then its fused K / V cache
+    write, on the current stream (rfill.kva.serial)."""
     from rfill import ops
+    from rfill.kva import serial
     W, B = arm.projector._maps(b.device)
-    for i in range(arm.split, model.n_layers):
+
+    def produce(i, slot):
+        f = lambda: ops.map_apply(b, W[i], B[i], xbuf[slot], sbuf[slot])          # noqa: E731
+        f() if timer is None else timer.run("rf_map_apply", f)
+
+    def consume(i, slot):
         w, c = model.W[i], caches[i]
-        m1 = lambda: ops.map_apply(b, W[i], B[i], xbuf, sbuf)                         # noqa: E731
-        m2 = lambda: ops.norm_kv_write(xbuf, sbuf, model.eps, w["wkv"], model.n_kv, model.head_dim,  # noqa: E731
-                                       w.get("k_norm"), model.knorm_kind, cs, c["kbuf"], c["vbuf"], 0)
-        if timer is None:
-            m1()
-            m2()
-        else:
-            timer.run("rf_map_apply", m1)
-            timer.run("rf_norm_kv_write", m2)
+        f = lambda: ops.norm_kv_write(xbuf[slot], sbuf[slot], model.eps, w["wkv"], model.n_kv,  # noqa: E731
+                                      model.head_dim, w.get("k_norm"), model.knorm_kind, cs, c["kbuf"],
+                                      c["vbuf"], 0)
+        f() if timer is None else timer.run("rf_norm_kv_write", f)
+
+    serial(range(arm.split, model.n_layers), produce, consume, b.device)
 
 
 def ceilings(dev, P, H):
@@ -190,8 +195,8 @@ def main():
     b = w["h_split"][:P]
     pos = torch.arange(P, device=dev)
     cs = model.rope_table(pos)
-    xbuf = torch.empty(P, H, dtype=torch.bfloat16, device=dev)
-    sbuf = torch.empty(P, H // 256, dtype=torch.float32, device=dev)
+    xbuf = [torch.empty(P, H, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+    sbuf = [torch.empty(P, H // 256, dtype=torch.float32, device=dev) for _ in range(2)]
     caches = model.new_cache()
     for i in w["layers"]:
         caches[i] = dict(kbuf=torch.empty(model.n_kv, P + 64, model.head_dim, dtype=torch.bfloat16, device=dev),

@@ -4,8 +4,9 @@ fill loop of finish() (code/kva/kva.py:79-193, 392-454), with every fill step on
 fill_late() runs the hot path of finish() for one arm: for each late layer i >= split, the prefix rows
 [0, P) get x_i = W_i b + c_i (fill 'proj', one rf_map_apply that also yields x's RMSNorm statistics)
 or x_i = b (fill 'identity'), the exact rows R are scattered in bit-exactly (rf_row_scatter, the
-index_copy of kva.py:428-431), and the layer's cache is filled (rf_norm_kv_write). One x buffer, one
-statistics buffer and one RoPE table serve all late layers.
+index_copy of kva.py:428-431), and the layer's cache is filled (rf_norm_kv_write). Two x / statistics
+buffers and one RoPE table serve all late layers; optionally layer i's cache write runs on a second
+stream beside layer i + 1's map apply (two_stream).
 """
 import json
 from dataclasses import dataclass, field
@@ -117,11 +118,43 @@ def check_rows(exact_rows, P):
     return rows
 
 
-def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None):
+def two_stream(layers, produce, consume, device):
+    """Run produce(i, slot) for each layer on the current stream and consume(i, slot) on a second
+    stream (default priority), slot = position % 2 naming one of two buffer sets: consume(i) waits for
+    produce(i), and produce(i + 2) waits for consume(i) before reusing its slot. The second stream's
+    K / V GEMM of layer i thus overlaps the map GEMM of layer i + 1 (their tile counts do not fill the
+    GPU's last wave alike). Returns after the current stream has been ordered after all of it."""
+    main = torch.cuda.current_stream(device)
+    side = torch.cuda.Stream(device=device)
+    side.wait_stream(main)
+    ready = [torch.cuda.Event(), torch.cuda.Event()]
+    free = [torch.cuda.Event(), torch.cuda.Event()]
+    for n, i in enumerate(layers):
+        slot = n % 2
+        if n >= 2:
+            main.wait_event(free[slot])
+        produce(i, slot)
+        ready[slot].record(main)
+        side.wait_event(ready[slot])
+        with torch.cuda.stream(side):
+            consume(i, slot)
+        free[slot].record(side)
+    main.wait_stream(side)
+
+
+def serial(layers, produce, consume, device):
+    """produce(i, slot) then consume(i, slot) for each layer, all on the current stream."""
+    for n, i in enumerate(layers):
+        produce(i, n % 2)
+        consume(i, n % 2)
+
+
+def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap=False):
     """The late-layer fill of finish() for one arm: every late layer's cache filled from the prefix rows
     [0, P) of h_split [N, H] (bf16, on the GPU). exact_rows: sorted prefix rows whose layer inputs are
     given by hr (one [|R|, H] tensor for every layer, or {layer: tensor}) instead of the fill's x.
-    Returns (cache, P)."""
+    overlap: run each layer's cache write on a second stream beside the next layer's map apply
+    (two_stream; about 1% faster at the Llama-8B 32K shape). Returns (cache, P)."""
     n = h_split.shape[0]
     P = arm.prefix_len(n)
     cache = model.new_cache() if cache is None else cache
@@ -137,21 +170,31 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None):
     if exact_rows is not None and len(exact_rows) > 0:
         rows = check_rows(exact_rows, P).to(dev)
     H = h_split.shape[1]
-    xbuf = torch.empty(P, H, dtype=torch.bfloat16, device=dev)
-    sbuf = torch.empty(P, ops.ssq_parts(H), dtype=torch.float32, device=dev)
-    base_ssq = None
-    for i in range(arm.split, model.n_layers):
+    layers = list(range(arm.split, model.n_layers))
+    for i in layers:                                    # allocate / grow every cache before any launch
+        if model.layer_types[i] == "attn":
+            model.reserve(cache[i], P, model.n_kv, model.head_dim, dev)
+    xbuf = [torch.empty(P, H, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+    sbuf = [torch.empty(P, ops.ssq_parts(H), dtype=torch.float32, device=dev) for _ in range(2)]
+    base_ssq = ops.row_ssq(b) if arm.fill == "identity" and rows is None else None
+    inputs = {}
+
+    def produce(i, slot):
         if arm.fill == "proj":
-            x, ssq = arm.projector.apply(i, b, xbuf, sbuf)
+            x, ssq = arm.projector.apply(i, b, xbuf[slot], sbuf[slot])
+        elif rows is None:
+            x, ssq = b, base_ssq
         else:
-            if rows is None:
-                base_ssq = ops.row_ssq(b) if base_ssq is None else base_ssq
-                x, ssq = b, base_ssq
-            else:
-                x = xbuf.copy_(b)
-                ssq = ops.row_ssq(x, sbuf)
+            x = xbuf[slot].copy_(b)
+            ssq = ops.row_ssq(x, sbuf[slot])
         if rows is not None:
             hri = hr[i] if isinstance(hr, dict) else hr
             ops.row_scatter(x, ssq, rows, hri.to(dev, torch.bfloat16))
+        inputs[slot] = (x, ssq)
+
+    def consume(i, slot):
+        x, ssq = inputs[slot]
         model.fill(i, x, pos, cache, ssq=ssq, cs=cs)
+
+    (two_stream if overlap else serial)(layers, produce, consume, dev)
     return cache, P
