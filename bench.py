@@ -164,6 +164,38 @@ def cpu_baseline(cfg, w, layer, budget_s=12.0, rows=1024):
                       f"scaled by 1/16 layers; torch {torch.__version__}"}
 
 
+def fit_bench(dev, chunks=2, rows=65536, d=4096, targets=16, lams=(1e-4, 1e-3, 1e-2)):
+    """The closed-form fit at the 8B-width shape (d 4096, 16 targets, 64K-row chunks of Student-t rows):
+    `chunks` of the 32 chunks of 2,097,152 rows are generated (untimed) and accumulated (timed: transposes,
+    column sums and the MFMA Gram / cross accumulation into fp64), then the fp64 solve of every target
+    for 3 lambdas (timed). Work per chunk: 2 rows d^2 (1 + targets) flop."""
+    from rfill import ridge, synth
+    maps = synth.fit_maps(d, targets, device=dev)
+    stats = ridge.RidgeStats(0, list(range(targets)), d, device=dev)
+    t_acc = 0.0
+    for c in range(chunks):
+        x, ys = synth.fit_chunk(c, rows, d, maps, device=dev)
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        stats.add(x, dict(enumerate(ys)), block=rows)
+        e.record()
+        torch.cuda.synchronize()
+        t_acc += s.elapsed_time(e) / 1e3
+        del x, ys
+    flop = 2.0 * chunks * rows * d * d * (1 + targets)
+    t0 = time.perf_counter()
+    fit = ridge.RidgeFit(stats.state(device=dev), device=dev)
+    for i in range(targets):
+        fit.layer(i, lams)
+    torch.cuda.synchronize()
+    t_solve = time.perf_counter() - t0
+    return {"workload": f"ridge fit: d {d}, {targets} targets, {chunks} x {rows}-row chunks of 32 (timed sample)",
+            "accumulate_s": round(t_acc, 4), "gram_tflops": round(flop / t_acc / 1e12, 1),
+            "gram_frac_bf16_peak": round(flop / t_acc / PEAK_BF16, 4), "solve_s": round(t_solve, 3),
+            "projected_full_fit_s": round(t_acc * 32 / chunks + t_solve, 2)}
+
+
 def traffic_from_profiles(kernel):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE scaled
     by a copy kernel of known size), or None if it has not been measured."""
@@ -183,6 +215,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extras", action="store_true", help="skip ceilings and the standalone KV-write leg")
+    ap.add_argument("--no-fit", action="store_true", help="skip the closed-form fit leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (one MI355X per box); --gpus must be 1", file=sys.stderr)
@@ -240,6 +273,11 @@ def main():
         log("standalone RoPE + KV write and library ceilings")
         out["kernels"]["rf_rope_kv_write"] = kv_write_bench(model, dev, P, SPLIT)
         out["ceilings"] = ceilings(dev, P, H)
+    if not args.no_fit:
+        log("closed-form fit leg")
+        del caches, xbuf, sbuf
+        torch.cuda.empty_cache()
+        out["fit"] = fit_bench(dev)
     if not args.no_cpu:
         log("CPU baseline (oracle fill on the host cores)")
         out["cpu_baseline"] = cpu_baseline(cfg, w, SPLIT)

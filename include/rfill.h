@@ -93,6 +93,26 @@ int rf_rope_kv_write(const uint16_t* k, int64_t ld_k, const uint16_t* v, int64_t
                      uint16_t* kbuf, uint16_t* vbuf, int64_t head_stride, int64_t row_stride,
                      int64_t slot_begin, int64_t cap, hipStream_t stream);
 
+/* ---- closed-form fit (code/kva/ridge.py:19-105, code/scripts/fit_sweep.py:87-144) ---- */
+
+/* Transpose row-major samples src [rows, cols] into dst [cols, >= round_up(rows, 64)] (row stride
+ * ld_dst), zero-filling the columns past `rows`: the K-contiguous operand of rf_gram_accumulate. If
+ * partial is not NULL it receives the column sums of every 64-row tile, fp32 [round_up(rows, 64)/64, cols]
+ * (fold them with rf_colsum_fold). Needs cols % 64 == 0, 16-byte aligned pointers, strides % 8 == 0. */
+int rf_transpose(const uint16_t* src, int64_t ld_src, int64_t rows, int64_t cols, uint16_t* dst, int64_t ld_dst,
+                 float* partial, hipStream_t stream);
+
+/* sums[c] += sum_j partial[j, c] (j in order, fp64): the sum(0) of a sample block
+ * (RidgeStats' sx / sy, code/kva/ridge.py:46, :61). */
+int rf_colsum_fold(const float* partial, int64_t ntiles, int64_t cols, double* sums, hipStream_t stream);
+
+/* Gram / cross accumulation C[M, N] += A[M, K] B[N, K]^T: bf16 products summed in fp32 on MFMA over
+ * this call's K, then added into the fp64 accumulator C (row stride ldc). With A = X^T and B = X^T or
+ * Y^T of one sample block this is RidgeStats' per-block fp32 GEMM into fp64 (code/kva/ridge.py:47,
+ * :62). Needs N % 256 == 0, K % 64 == 0 (pad samples with zero rows), lda / ldb % 8 == 0, ldc even. */
+int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t M, int64_t N,
+                       int64_t K, double* c, int64_t ldc, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

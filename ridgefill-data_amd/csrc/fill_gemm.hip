@@ -363,6 +363,42 @@ __global__ __launch_bounds__(NTHR) void k_norm_kv(const uint16_t* __restrict__ X
   }
 }
 
+// C[m, n] += sum_k A[m, k] B[n, k] in fp32 for this launch, added into the fp64 accumulator C. Each
+// tile owns its 256 x 256 block of C, so the read-modify-write is race-free and the result does not
+// depend on the schedule. A lane's accumulator holds 4 consecutive columns of one row per (nt, g).
+__global__ __launch_bounds__(NTHR) void k_gram(const uint16_t* __restrict__ A, int64_t lda,
+                                               const uint16_t* __restrict__ B, int64_t ldb, int M, int N, int K,
+                                               double* __restrict__ C, int64_t ldc) {
+  __shared__ uint4 lds[LDS_U4];
+  const int tiles_n = N / BN;
+  int tm, tn;
+  tile_coords(xcd_tile(blockIdx.x, gridDim.x), (M + BM - 1) / BM, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  f32x16 acc[4][4];
+  mainloop(A, lda, B, ldb, M, K, m0, n0, lds, acc);
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int wm = w >> 1, wn = w & 1, lr = lane & 31, lk = lane >> 5;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int gm = m0 + wm * 128 + mt * 32 + lr;
+    if (gm >= M) continue;
+    double* row = C + static_cast<int64_t>(gm) * ldc + n0 + wn * 128 + 4 * lk;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        double* p = row + nt * 32 + 8 * g;
+        double2 lo = *reinterpret_cast<double2*>(p), hi = *reinterpret_cast<double2*>(p + 2);
+        lo.x += acc[nt][mt][4 * g + 0];
+        lo.y += acc[nt][mt][4 * g + 1];
+        hi.x += acc[nt][mt][4 * g + 2];
+        hi.y += acc[nt][mt][4 * g + 3];
+        *reinterpret_cast<double2*>(p) = lo;
+        *reinterpret_cast<double2*>(p + 2) = hi;
+      }
+  }
+}
+
 int grid_of(int64_t M, int64_t N) { return static_cast<int>(((M + BM - 1) / BM) * (N / BN)); }
 
 }  // namespace
@@ -420,4 +456,21 @@ extern "C" int rf_norm_kv_write(const uint16_t* x, int64_t ldx, const float* ssq
   hipLaunchKernelGGL(k_norm_kv, dim3(grid_of(P, N)), dim3(NTHR), 0, stream, x, ldx, wkv, static_cast<int>(P),
                      static_cast<int>(N), static_cast<int>(H), a);
   return check_launch("rf_norm_kv_write");
+}
+
+extern "C" int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t M,
+                                  int64_t N, int64_t K, double* c, int64_t ldc, hipStream_t stream) {
+  if (!a || !b || !c) return fail(RF_EINVAL_ARG, "rf_gram_accumulate: null pointer");
+  if (M < 0 || M > (1 << 30) || N <= 0 || N % BN || K <= 0 || K % 64)
+    return fail(RF_EINVAL_SHAPE, "rf_gram_accumulate: M %lld, N %lld (multiple of 256), K %lld (multiple of 64)",
+                (long long)M, (long long)N, (long long)K);
+  if (lda < K || ldb < K || lda % 8 || ldb % 8 || lda > (1 << 21) || ldb > (1 << 21) || ldc < N || ldc % 2)
+    return fail(RF_EINVAL_SHAPE, "rf_gram_accumulate: strides lda %lld, ldb %lld, ldc %lld", (long long)lda,
+                (long long)ldb, (long long)ldc);
+  if (!aligned16(a) || !aligned16(b) || !aligned16(c))
+    return fail(RF_EINVAL_SHAPE, "rf_gram_accumulate: pointers must be 16-byte aligned");
+  if (M == 0) return RF_OK;
+  hipLaunchKernelGGL(k_gram, dim3(grid_of(M, N)), dim3(NTHR), 0, stream, a, lda, b, ldb, static_cast<int>(M),
+                     static_cast<int>(N), static_cast<int>(K), c, ldc);
+  return check_launch("rf_gram_accumulate");
 }

@@ -1,0 +1,92 @@
+// HBM-bound helpers of the closed-form fit: the row-block transpose that turns row-major samples
+// [rows, cols] into the K-contiguous operand [cols, rows] of rf_gram_accumulate, with the columns'
+// sums per 64-row tile as a by-product, and the fixed-order fp64 fold of those sums.
+#include "rf_common.h"
+
+namespace rf {
+namespace {
+
+constexpr int TT = 64;                            // transpose tile: 64 rows x 64 columns
+
+// Block = one 64 x 64 tile, 256 threads. Load: thread t takes tile row t / 4, columns (t % 4) * 16 ..
+// + 15 (two 16-byte loads). Store: thread t writes output row (source column) t / 4, source rows
+// (t % 4) * 16 .. + 15. Rows at or past `rows` read as zeros, so padded output columns are zero.
+__global__ __launch_bounds__(256) void k_transpose(const uint16_t* __restrict__ src, int64_t ld_src, int64_t rows,
+                                                   int cols, uint16_t* __restrict__ dst, int64_t ld_dst,
+                                                   float* __restrict__ partial) {
+  __shared__ uint16_t tile[TT][TT + 2];
+  const int t = threadIdx.x;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * TT;
+  const int c0 = blockIdx.y * TT;
+  {
+    const int r = t >> 2, c = (t & 3) * 16;
+    uint4 a = make_uint4(0u, 0u, 0u, 0u), b = a;
+    if (r0 + r < rows) {
+      const uint4* p = reinterpret_cast<const uint4*>(src + (r0 + r) * ld_src + c0 + c);
+      a = p[0];
+      b = p[1];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      tile[r][c + e] = lane_of(a, e);
+      tile[r][c + 8 + e] = lane_of(b, e);
+    }
+  }
+  __syncthreads();
+  const int oc = t >> 2, rr = (t & 3) * 16;       // output row = source column c0 + oc
+  uint16_t v[16];
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    v[e] = tile[rr + e][oc];
+    s += bf2f(v[e]);
+  }
+  uint4* q = reinterpret_cast<uint4*>(dst + static_cast<int64_t>(c0 + oc) * ld_dst + r0 + rr);
+  q[0] = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+  q[1] = make_uint4(pack2(v[8], v[9]), pack2(v[10], v[11]), pack2(v[12], v[13]), pack2(v[14], v[15]));
+  if (partial) {
+    // the 4 threads of one column are adjacent lanes: fixed-order pairwise sum
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    if ((t & 3) == 0) partial[static_cast<int64_t>(blockIdx.x) * cols + c0 + oc] = s;
+  }
+}
+
+// sums[c] += sum over tiles j (in order) of partial[j, c], in fp64.
+__global__ __launch_bounds__(256) void k_colsum_fold(const float* __restrict__ partial, int64_t ntiles, int cols,
+                                                     double* __restrict__ sums) {
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  if (c >= cols) return;
+  double s = 0.0;
+  for (int64_t j = 0; j < ntiles; ++j) s += static_cast<double>(partial[j * cols + c]);
+  sums[c] += s;
+}
+
+}  // namespace
+}  // namespace rf
+
+using namespace rf;
+
+extern "C" int rf_transpose(const uint16_t* src, int64_t ld_src, int64_t rows, int64_t cols, uint16_t* dst,
+                            int64_t ld_dst, float* partial, hipStream_t stream) {
+  if (!src || !dst) return fail(RF_EINVAL_ARG, "rf_transpose: null pointer");
+  const int64_t rows_out = (rows + TT - 1) / TT * TT;
+  if (rows < 0 || cols <= 0 || cols % TT || cols > (1 << 24) || ld_src < cols || ld_src % 8 || ld_dst < rows_out ||
+      ld_dst % 8 || rows_out / TT > (1ll << 31) - 1)
+    return fail(RF_EINVAL_SHAPE, "rf_transpose: rows %lld, cols %lld (multiple of 64), ld_src %lld, ld_dst %lld "
+                "(>= rows rounded up to 64)", (long long)rows, (long long)cols, (long long)ld_src, (long long)ld_dst);
+  if (!aligned16(src) || !aligned16(dst)) return fail(RF_EINVAL_SHAPE, "rf_transpose: 16-byte alignment");
+  if (rows == 0) return RF_OK;
+  hipLaunchKernelGGL(k_transpose, dim3(static_cast<unsigned>(rows_out / TT), static_cast<unsigned>(cols / TT)),
+                     dim3(256), 0, stream, src, ld_src, rows, static_cast<int>(cols), dst, ld_dst, partial);
+  return check_launch("rf_transpose");
+}
+
+extern "C" int rf_colsum_fold(const float* partial, int64_t ntiles, int64_t cols, double* sums, hipStream_t stream) {
+  if (!partial || !sums) return fail(RF_EINVAL_ARG, "rf_colsum_fold: null pointer");
+  if (ntiles < 0 || cols <= 0 || cols > (1 << 30)) return fail(RF_EINVAL_SHAPE, "rf_colsum_fold: shape");
+  if (ntiles == 0) return RF_OK;
+  hipLaunchKernelGGL(k_colsum_fold, dim3(static_cast<unsigned>((cols + 255) / 256)), dim3(256), 0, stream, partial,
+                     ntiles, static_cast<int>(cols), sums);
+  return check_launch("rf_colsum_fold");
+}

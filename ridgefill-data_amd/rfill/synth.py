@@ -69,3 +69,34 @@ def dense_fill(cfg, split, n_rows, tail, device="cpu", exact_frac=0.0, with_maps
     hr = hidden_states(n_exact, h, device=device, seed_rows=14) if n_exact else None
     return dict(cfg=cfg, split=split, layers=layers, h_split=hidden_states(n_rows, h, device=device), P=P,
                 tensors=tensors, maps=maps, biases=biases, rows=rows.to(device), hr=hr)
+
+
+def student_t(shape, nu, generator, device):
+    """Student-t(nu) samples z / sqrt(chi2_nu / nu), chi2 from nu squared normals (nu integer)."""
+    z = torch.randn(shape, generator=generator, device=device)
+    chi2 = torch.zeros(shape, device=device)
+    for _ in range(nu):
+        chi2 += torch.randn(shape, generator=generator, device=device) ** 2
+    return z * torch.rsqrt(chi2 / nu)
+
+
+def fit_maps(d, targets, device="cpu", scale=0.05):
+    """The fit workload's true maps T_l = I + scale N(0, 1/d) (variance 1/d), seed 21 + l."""
+    return [torch.eye(d, device=device) + scale * torch.randn(d, d, generator=_gen(21 + l, device), device=device)
+            / d ** 0.5 for l in range(targets)]
+
+
+def fit_chunk(chunk, rows, d, maps, device="cpu", nu=5, outliers=4, noise=0.1):
+    """Rows [chunk * rows, (chunk + 1) * rows) of the fit workload: X = Student-t(nu) per element (seed
+    20 + 1000 chunk) with `outliers` channels x 20 (seed 20), Y_l = X T_l + N(0, noise) (seed
+    21 + l + 1000 chunk); bf16 storage, Y computed from the bf16 X in fp32."""
+    g = _gen(20, "cpu")
+    pick = torch.randperm(d, generator=g)[:outliers].to(device)
+    x = student_t((rows, d), nu, _gen(20 + 1000 * chunk, device), device)
+    x[:, pick] *= 20.0
+    x = x.to(torch.bfloat16)
+    ys = []
+    for l, t in enumerate(maps):
+        e = noise * torch.randn(rows, d, generator=_gen(21 + l + 1000 * chunk, device), device=device)
+        ys.append((x.float() @ t + e).to(torch.bfloat16))
+    return x, ys
