@@ -93,6 +93,24 @@ int rf_rope_kv_write(const uint16_t* k, int64_t ld_k, const uint16_t* v, int64_t
                      uint16_t* kbuf, uint16_t* vbuf, int64_t head_stride, int64_t row_stride,
                      int64_t slot_begin, int64_t cap, hipStream_t stream);
 
+/* Fused RMSNorm + linear: out[P, N] = bf16(r_row * (x w^T)) with r_row = 1 / sqrt(mean(x^2) + eps) from
+ * the row partials ssq [P, H / 256] and the norm gain folded into w [N, H] (rf_fold_norm). The Gated
+ * DeltaNet in-projections of a fill (code/kva/model.py:448-450 after in_norm, :513). Needs
+ * H % 256 == 0, N % 256 == 0 (pad w with zero rows), 16-byte aligned pointers. */
+int rf_norm_linear(const uint16_t* x, int64_t ldx, const float* ssq, int64_t P, int64_t H, float eps,
+                   const uint16_t* w, int64_t N, uint16_t* out, int64_t ldo, hipStream_t stream);
+
+/* Gated DeltaNet fill of one layer from its in-projection rows pre [P, ld] bf16 (columns: q [nk dk] |
+ * k [nk dk] | v [nv dv] | b [nv] | a [nv]): causal conv + SiLU (conv_w [C, 4], C = 2 nk dk + nv dv,
+ * continuing conv_in [3, C] or zeros), k l2-norm, beta = sigmoid(b), g = -exp(a_log) softplus(a +
+ * dt_bias) (a_log, dt_bias [nv] fp32), and the chunked (64-row) gated delta rule updating state
+ * [nv, dk, dv] fp32 in place. Writes conv_out [3, C] (the last 3 pre-conv rows; must not alias conv_in).
+ * Replaces Qwen35._gdn_core with need_out = False (code/kva/model.py:452-484, ops.py:173-262) inside
+ * Qwen35.fill (model.py:510-523). Needs dk = dv = 128, nv % nk == 0. */
+int rf_gdn_fill(const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int dk, int dv, const uint16_t* conv_w,
+                const uint16_t* conv_in, uint16_t* conv_out, const float* a_log, const float* dt_bias, float* state,
+                hipStream_t stream);
+
 /* ---- closed-form fit (code/kva/ridge.py:19-105, code/scripts/fit_sweep.py:87-144) ---- */
 
 /* Transpose row-major samples src [rows, cols] into dst [cols, >= round_up(rows, 64)] (row stride

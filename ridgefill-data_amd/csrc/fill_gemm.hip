@@ -363,6 +363,44 @@ __global__ __launch_bounds__(NTHR) void k_norm_kv(const uint16_t* __restrict__ X
   }
 }
 
+// out = bf16(r_row * (x W^T)) with W's columns carrying the input norm gain (rf_fold_norm) and
+// r_row = 1 / sqrt(mean(x^2) + eps) from the row partials: F.linear of the normed input, as the GDN
+// in-projections (code/kva/model.py:448-450) compute it.
+__global__ __launch_bounds__(NTHR) void k_norm_linear(const uint16_t* __restrict__ Xin, int64_t ldx,
+                                                      const uint16_t* __restrict__ W, int M, int N, int K,
+                                                      const float* __restrict__ ssq, float eps,
+                                                      uint16_t* __restrict__ out, int64_t ldo) {
+  __shared__ uint4 lds[LDS_U4];
+  const int tiles_n = N / BN;
+  int tm, tn;
+  tile_coords(xcd_tile(blockIdx.x, gridDim.x), (M + BM - 1) / BM, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+  f32x16 acc[4][4];
+  mainloop(Xin, ldx, W, K, M, K, m0, n0, lds, acc);
+  const int lane = threadIdx.x & 63, wm = threadIdx.x >> 7;
+  const int nparts = K / SSQ_COLS;
+  float rs[4];
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int gm = m0 + wm * 128 + mt * 32 + (lane & 31);
+    float s = 0.f;
+    if (gm < M) {
+      const float* p = ssq + static_cast<int64_t>(gm) * nparts;
+      for (int q = 0; q < nparts; ++q) s += p[q];
+    }
+    rs[mt] = 1.0f / sqrtf(s / static_cast<float>(K) + eps);
+  }
+  stage_tile(lds, acc, [&](int mt, int, int, int, float v) { return v * rs[mt]; });
+  __syncthreads();
+  const int t = threadIdx.x, ch = t & 31;
+  for (int it = 0; it < BM / 8; ++it) {
+    const int row = it * 8 + (t >> 5);
+    const int gm = m0 + row;
+    if (gm < M)
+      *reinterpret_cast<uint4*>(out + static_cast<int64_t>(gm) * ldo + n0 + ch * 8) = image_chunk(lds, row, ch);
+  }
+}
+
 // C[m, n] += sum_k A[m, k] B[n, k] in fp32 for this launch, added into the fp64 accumulator C. Each
 // tile owns its 256 x 256 block of C, so the read-modify-write is race-free and the result does not
 // depend on the schedule. A lane's accumulator holds 4 consecutive columns of one row per (nt, g).
@@ -473,4 +511,20 @@ extern "C" int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t
   hipLaunchKernelGGL(k_gram, dim3(grid_of(M, N)), dim3(NTHR), 0, stream, a, lda, b, ldb, static_cast<int>(M),
                      static_cast<int>(N), static_cast<int>(K), c, ldc);
   return check_launch("rf_gram_accumulate");
+}
+
+extern "C" int rf_norm_linear(const uint16_t* x, int64_t ldx, const float* ssq, int64_t P, int64_t H, float eps,
+                              const uint16_t* w, int64_t N, uint16_t* out, int64_t ldo, hipStream_t stream) {
+  if (!x || !ssq || !w || !out) return fail(RF_EINVAL_ARG, "rf_norm_linear: null pointer");
+  if (P < 0 || P > (1ll << 30) || H <= 0 || H % SSQ_COLS || N <= 0 || N % BN)
+    return fail(RF_EINVAL_SHAPE, "rf_norm_linear: P %lld, H %lld (multiple of 256), N %lld (multiple of 256)",
+                (long long)P, (long long)H, (long long)N);
+  if (ldx < H || ldx % 8 || ldx > (1 << 21) || ldo < N || ldo % 8)
+    return fail(RF_EINVAL_SHAPE, "rf_norm_linear: strides ldx %lld, ldo %lld", (long long)ldx, (long long)ldo);
+  if (!aligned16(x) || !aligned16(w) || !aligned16(out)) return fail(RF_EINVAL_SHAPE, "rf_norm_linear: alignment");
+  if (!(eps >= 0.f)) return fail(RF_EINVAL_ARG, "rf_norm_linear: eps");
+  if (P == 0) return RF_OK;
+  hipLaunchKernelGGL(k_norm_linear, dim3(grid_of(P, N)), dim3(NTHR), 0, stream, x, ldx, w, static_cast<int>(P),
+                     static_cast<int>(N), static_cast<int>(H), ssq, eps, out, ldo);
+  return check_launch("rf_norm_linear");
 }

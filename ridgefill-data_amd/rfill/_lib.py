@@ -35,6 +35,8 @@ SIGNATURES = {
     "rf_norm_kv_write": [_P, _I64, _P, _I64, _I64, _F32, _P, _I32, _I32, _P, _I32, _P, _I32,
                          _P, _P, _I64, _I64, _I64, _I64, _P],
     "rf_rope_kv_write": [_P, _I64, _P, _I64, _I64, _I32, _I32, _P, _I32, _P, _P, _I64, _I64, _I64, _I64, _P],
+    "rf_norm_linear": [_P, _I64, _P, _I64, _I64, _F32, _P, _I64, _P, _I64, _P],
+    "rf_gdn_fill": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P],
     "rf_transpose": [_P, _I64, _I64, _I64, _P, _I64, _P, _P],
     "rf_colsum_fold": [_P, _I64, _I64, _P, _P],
     "rf_gram_accumulate": [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],

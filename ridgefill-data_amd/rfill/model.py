@@ -49,6 +49,9 @@ class FillModel:
             self.rot = int(self.head_dim * frac)
             inv = ops.inv_freq_default(theta, self.rot)
             self.layer_types = ["gdn" if t == "linear_attention" else "attn" for t in c["layer_types"]]
+            self.nk, self.nv = c.get("linear_num_key_heads"), c.get("linear_num_value_heads")
+            self.dk, self.dv = c.get("linear_key_head_dim"), c.get("linear_value_head_dim")
+            self.conv_k = c.get("linear_conv_kernel_dim")
         else:
             if self.arch == "qwen3" and rp.get("rope_type", "default") != "default":
                 raise UnsupportedArchitecture(f"Qwen3 rope_type {rp.get('rope_type')!r}")
@@ -70,7 +73,7 @@ class FillModel:
     def _pack(self, i, p, tensors):
         dev = lambda k: tensors[k].to(self.device, torch.bfloat16).contiguous()   # noqa: E731
         if self.layer_types[i] != "attn":
-            return dict(kind="gdn")
+            return self._pack_gdn(p, tensors, dev)
         a = p + "self_attn."
         ln1 = dev(p + "input_layernorm.weight")
         wkv = torch.cat((dev(a + "k_proj.weight"), dev(a + "v_proj.weight")), 0)
@@ -78,6 +81,25 @@ class FillModel:
         if self.arch != "llama":
             w["k_norm"] = dev(a + "k_norm.weight")
         return w
+
+    def _pack_gdn(self, p, tensors, dev):
+        """GDN layer: in-projections [W_qkv; W_b; W_a] with the zero-centred input norm's (1 + g) folded
+        into the columns, zero rows up to a multiple of 256; conv weight [C, 4]; the gates' A_log and
+        dt_bias in fp32 as stored (code/kva/model.py:396-400)."""
+        if self.conv_k != 4 or self.dk != 128 or self.dv != 128:
+            raise UnsupportedArchitecture(f"GDN conv kernel {self.conv_k}, head dims {self.dk} / {self.dv} "
+                                          f"(kernels: 4, 128 / 128)")
+        a = p + "linear_attn."
+        ln1 = dev(p + "input_layernorm.weight")
+        w_in = torch.cat((dev(a + "in_proj_qkv.weight"), dev(a + "in_proj_b.weight"), dev(a + "in_proj_a.weight")), 0)
+        n = w_in.shape[0]
+        pad = (-n) % 256
+        if pad:
+            w_in = torch.cat((w_in, w_in.new_zeros(pad, w_in.shape[1])), 0)
+        conv = tensors[a + "conv1d.weight"].to(self.device, torch.bfloat16).reshape(-1, self.conv_k).contiguous()
+        return dict(kind="gdn", ln1=ln1, w_in=ops.fold_norm(w_in, ln1, 1), conv=conv,
+                    a_log=tensors[a + "A_log"].to(self.device, torch.float32).contiguous(),
+                    dt_bias=tensors[a + "dt_bias"].to(self.device, torch.float32).contiguous())
 
     @classmethod
     def from_hf(cls, hf_model, device="cuda", layers=None):
@@ -112,18 +134,22 @@ class FillModel:
         c["n"] = n
         c["k"], c["v"] = c["kbuf"][:, :n], c["vbuf"][:, :n]
 
-    def _layer(self, i):
+    def _layer(self, i, kind="attn"):
         w = self.W[i]
         if w is None:
             raise ValueError(f"layer {i} was not packed (FillModel(layers=...))")
-        if w["kind"] != "attn":
-            raise UnsupportedArchitecture(f"layer {i}: Gated DeltaNet fill is not built in this library version")
+        if w["kind"] != kind:
+            raise ValueError(f"layer {i} is a {w['kind']} layer")
         return w
 
-    def fill(self, i, x, pos, cache, st=None, ssq=None, cs=None):
-        """Cache-only fill of layer i from inputs x [P, H] bf16 at positions pos. ssq: x's row
-        sum-of-squares partials if already known (rf_map_apply / rf_row_scatter produce them);
-        cs: the RoPE table of pos if already built."""
+    def fill(self, i, x, pos, cache, st=None, ssq=None, cs=None, checkpoint_every=None):
+        """Cache-only fill of layer i from inputs x [P, H] bf16 at positions pos (code/kva/model.py:
+        278-280, 510-523). Attention layers: K / V into the cache. GDN layers: conv state and recurrent
+        state continued over the rows, then + st (the terminal-state correction) if given. ssq: x's row
+        sum-of-squares partials if already known (rf_map_apply / rf_row_scatter produce them); cs: the
+        RoPE table of pos if already built."""
+        if self.layer_types[i] == "gdn":
+            return self._fill_gdn(i, x, cache, st, ssq, checkpoint_every)
         w = self._layer(i)
         if st is not None:
             raise ValueError("st corrects GDN recurrent states; layer is attention")
@@ -137,6 +163,28 @@ class FillModel:
         ops.norm_kv_write(x, ssq, self.eps, w["wkv"], self.n_kv, self.head_dim, w.get("k_norm"), self.knorm_kind,
                           cs, c["kbuf"], c["vbuf"], slot)
         self.commit(c, P)
+        return {}
+
+    def _fill_gdn(self, i, x, cache, st, ssq, checkpoint_every):
+        if checkpoint_every:
+            raise UnsupportedArchitecture("GDN state checkpoints are not produced by the fill kernels")
+        w = self._layer(i, "gdn")
+        P = x.shape[0]
+        c = cache[i]
+        if P == 0:
+            return {}
+        if ssq is None:
+            ssq = ops.row_ssq(x)
+        pre = ops.norm_linear(x, ssq, self.eps, w["w_in"])
+        rec = c.get("rec")
+        rec = (torch.zeros(self.nv, self.dk, self.dv, dtype=torch.float32, device=x.device) if rec is None
+               else rec.float().contiguous().clone())
+        c["conv"] = ops.gdn_fill(pre, self.nk, self.nv, self.dk, self.dv, w["conv"], c.get("conv"), w["a_log"],
+                                 w["dt_bias"], rec)
+        c["rec"] = rec
+        c["len"] = c.get("len", 0) + P
+        if st is not None:
+            c["rec"] = c["rec"] + st.to(c["rec"])
         return {}
 
     def fill_kv(self, i, k, v, pos, cache, cs=None):

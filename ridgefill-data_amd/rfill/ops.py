@@ -164,6 +164,48 @@ def rope_kv_write(k, v, cs, kbuf, vbuf, slot_begin):
               _ptr(kbuf), _ptr(vbuf), hs, rs, int(slot_begin), cap, _stream(k))
 
 
+def norm_linear(x, ssq, eps, w, out=None):
+    """bf16(rms-normed x @ w^T) with the norm gain already folded into w [N, H] (N % 256 == 0)."""
+    _need(x, "x", torch.bfloat16, 2)
+    _need(ssq, "ssq", torch.float32, 2)
+    _need(w, "w", torch.bfloat16, 2)
+    P, H = x.shape
+    N = w.shape[0]
+    if w.shape[1] != H or not w.is_contiguous() or tuple(ssq.shape) != (P, ssq_parts(H)):
+        raise ValueError("norm_linear: shapes")
+    out = torch.empty(P, N, dtype=torch.bfloat16, device=x.device) if out is None else out
+    _need(out, "out", torch.bfloat16, 2)
+    _lib.call("rf_norm_linear", _ptr(x), x.stride(0), _ptr(ssq), P, H, float(eps), _ptr(w), N, _ptr(out), out.stride(0),
+              _stream(x))
+    return out
+
+
+def gdn_fill(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state):
+    """Gated DeltaNet fill from in-projection rows pre [P, >= C + 2 nv] (q | k | v | b | a): updates
+    state [nv, dk, dv] fp32 in place, returns the new conv state [3, C] bf16."""
+    _need(pre, "pre", torch.bfloat16, 2)
+    _need(conv_w, "conv_w", torch.bfloat16, 2)
+    _need(a_log, "a_log", torch.float32, 1)
+    _need(dt_bias, "dt_bias", torch.float32, 1)
+    _need(state, "state", torch.float32, 3)
+    C = 2 * nk * dk + nv * dv
+    if tuple(conv_w.shape) != (C, 4) or not conv_w.is_contiguous():
+        raise ValueError(f"gdn_fill: conv weight {tuple(conv_w.shape)}, expected ({C}, 4)")
+    if tuple(state.shape) != (nv, dk, dv) or not state.is_contiguous():
+        raise ValueError(f"gdn_fill: state {tuple(state.shape)}")
+    if pre.shape[1] < C + 2 * nv or a_log.numel() != nv or dt_bias.numel() != nv:
+        raise ValueError(f"gdn_fill: rows {tuple(pre.shape)} (need >= {C + 2 * nv} columns), "
+                         f"a_log {a_log.numel()}, dt_bias {dt_bias.numel()} (need {nv})")
+    if conv_in is not None:
+        _need(conv_in, "conv_in", torch.bfloat16, 2)
+        if tuple(conv_in.shape) != (3, C) or not conv_in.is_contiguous():
+            raise ValueError("gdn_fill: conv state shape")
+    conv_out = torch.empty(3, C, dtype=torch.bfloat16, device=pre.device)
+    _lib.call("rf_gdn_fill", _ptr(pre), pre.stride(0), pre.shape[0], nk, nv, dk, dv, _ptr(conv_w), _ptr(conv_in),
+              _ptr(conv_out), _ptr(a_log), _ptr(dt_bias), _ptr(state), _stream(pre))
+    return conv_out
+
+
 # ------------------------------------------------------------------------ host-side RoPE frequencies
 
 def inv_freq_default(theta, rot_dim):

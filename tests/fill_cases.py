@@ -75,3 +75,33 @@ def case(name, layers=1, seed=0):
     arch, h, hkv, d, theta, kw = CASES[name]
     cfg = attn_config(arch, h, hkv, d, theta, layers=layers, **kw)
     return cfg, random_tensors(cfg, seed)
+
+
+def gdn_config(hidden=512, nk=2, nv=4, layers=1, eps=1e-6):
+    """A Qwen3.5 text config whose layers are all Gated DeltaNet (dk = dv = 128, conv kernel 4)."""
+    return dict(model_type="qwen3_5_text", num_hidden_layers=layers, hidden_size=hidden, num_attention_heads=4,
+                num_key_value_heads=2, head_dim=128, rms_norm_eps=eps, intermediate_size=256,
+                layer_types=["linear_attention"] * layers, linear_num_key_heads=nk, linear_num_value_heads=nv,
+                linear_key_head_dim=128, linear_value_head_dim=128, linear_conv_kernel_dim=4,
+                rope_parameters=dict(rope_type="default", rope_theta=1e7, partial_rotary_factor=0.25))
+
+
+def gdn_tensors(cfg, seed=0):
+    """GDN layer weights (checkpoint names). Gates: A_log = log U(0.05, 0.2), dt_bias N(0, 0.5), W_a small,
+    so decays stay mild and the state integrates many rows."""
+    g = torch.Generator().manual_seed(seed)
+    h, nk, nv = cfg["hidden_size"], cfg["linear_num_key_heads"], cfg["linear_num_value_heads"]
+    C = 2 * nk * 128 + nv * 128
+    t = {}
+    for i in range(cfg["num_hidden_layers"]):
+        p = f"model.layers.{i}."
+        a = p + "linear_attn."
+        t.update({p + "input_layernorm.weight": 0.1 * torch.randn(h, generator=g),
+                  a + "in_proj_qkv.weight": torch.randn(C, h, generator=g) / h ** 0.5,
+                  a + "in_proj_b.weight": torch.randn(nv, h, generator=g) / h ** 0.5,
+                  a + "in_proj_a.weight": 0.3 * torch.randn(nv, h, generator=g) / h ** 0.5,
+                  a + "conv1d.weight": 0.5 * torch.randn(C, 1, 4, generator=g)})
+        t = {k: v.to(torch.bfloat16) for k, v in t.items()}
+        t[a + "A_log"] = torch.log(0.05 + 0.15 * torch.rand(nv, generator=g))
+        t[a + "dt_bias"] = 0.5 * torch.randn(nv, generator=g)
+    return t

@@ -1,0 +1,93 @@
+"""GPU parity of the Gated DeltaNet fill (rf_norm_linear + rf_gdn_fill) against the CPU oracle, whose GDN
+math is pinned to transformers' Qwen3.5 (tests/test_oracle_model.py). Bars: the conv state is a copy of
+pre-conv rows, bit-exact; with the oracle's own in-projection rows as input the recurrent state agrees
+to fp32 rounding (<= 1e-4 relative Frobenius); through the whole bf16 fill path <= 1e-2."""
+import pytest
+import torch
+
+from fill_cases import gdn_config, gdn_tensors, inputs, rel_err
+from oracle import model as OM
+
+pytestmark = pytest.mark.gpu
+STATE_TOL = 1e-2
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    return torch.device("cuda")
+
+
+def _pre_rows(om, x):
+    """The oracle's in-projection rows [P, C + 2 nv] (q | k | v | b | a), bf16, as rf_gdn_fill reads them."""
+    pre, b, a = om.gdn_inputs(0, om.in_norm(x, om.W[0]["ln1"]))
+    return torch.cat((pre, b, a), 1)
+
+
+@pytest.mark.parametrize("P", [1000, 64, 3])
+def test_recurrence_matches_oracle_given_the_same_rows(dev, P):
+    from rfill import ops
+    cfg = gdn_config()
+    t = gdn_tensors(cfg)
+    om = OM.OracleModel(cfg, t, dtype=torch.bfloat16)
+    x = inputs(P, cfg["hidden_size"], seed=21)
+    c = om.new_cache()
+    om.fill(0, x, torch.arange(P), c)
+    rows = _pre_rows(om, x).to(dev)
+    w = om.W[0]
+    state = torch.zeros(4, 128, 128, dtype=torch.float32, device=dev)
+    conv = ops.gdn_fill(rows, 2, 4, 128, 128, w["conv"].to(dev).contiguous(), None, w["A_log"].to(dev),
+                        w["dt_bias"].to(dev), state)
+    torch.cuda.synchronize()
+    err = rel_err(state, c[0]["rec"])
+    print(f"P {P}: recurrent state rel err {err:.2e}")
+    assert err < 1e-4
+    assert torch.equal(conv.cpu(), c[0]["conv"])
+
+
+def test_fill_matches_oracle_and_continues(dev):
+    """FillModel.fill (in-projection GEMM + GDN kernel) against the oracle's fill, then a second call
+    continuing both states; plus the terminal-state correction st."""
+    from rfill.model import FillModel
+    cfg = gdn_config()
+    t = gdn_tensors(cfg, seed=1)
+    om = OM.OracleModel(cfg, t, dtype=torch.bfloat16)
+    m = FillModel(cfg, t, dev)
+    x = inputs(1500, cfg["hidden_size"], seed=22)
+    oc, mc = om.new_cache(), m.new_cache()
+    for a, b in ((0, 1100), (1100, 1500)):
+        om.fill(0, x[a:b], torch.arange(a, b), oc)
+        m.fill(0, x[a:b].to(dev), torch.arange(a, b, device=dev), mc)
+        torch.cuda.synchronize()
+        err = rel_err(mc[0]["rec"], oc[0]["rec"])
+        conv = rel_err(mc[0]["conv"], oc[0]["conv"])
+        print(f"rows [{a}, {b}): state rel err {err:.2e}, conv state rel err {conv:.2e}")
+        assert err < STATE_TOL and conv < STATE_TOL and mc[0]["len"] == oc[0]["len"] == b
+    st = 0.01 * torch.randn(4, 128, 128, generator=torch.Generator().manual_seed(3))
+    before = mc[0]["rec"].clone()
+    m2 = m.new_cache()
+    m2[0] = dict(mc[0], rec=before.clone())
+    m.fill(0, x[:0].to(dev), torch.arange(0, device=dev), m2)          # zero rows: nothing changes
+    assert torch.equal(m2[0]["rec"], before)
+    one = m.new_cache()
+    m.fill(0, x[:200].to(dev), torch.arange(200, device=dev), one, st=st.to(dev))
+    ref = om.new_cache()
+    om.fill(0, x[:200], torch.arange(200), ref, st=st)
+    assert rel_err(one[0]["rec"], ref[0]["rec"]) < STATE_TOL
+
+
+def test_fill_c4_gdn_layer_shape(dev):
+    """One GDN layer at the hybrid config's widths (hidden 2048, 16 key / 32 value heads) over 2048 rows."""
+    from rfill.model import FillModel
+    cfg = gdn_config(hidden=2048, nk=16, nv=32)
+    t = gdn_tensors(cfg, seed=2)
+    om = OM.OracleModel(cfg, t, dtype=torch.bfloat16)
+    m = FillModel(cfg, t, dev)
+    x = inputs(2048, 2048, seed=23)
+    oc, mc = om.new_cache(), m.new_cache()
+    om.fill(0, x, torch.arange(2048), oc)
+    m.fill(0, x.to(dev), torch.arange(2048, device=dev), mc)
+    torch.cuda.synchronize()
+    err = rel_err(mc[0]["rec"], oc[0]["rec"])
+    print(f"C4 GDN layer: state rel err {err:.2e}")
+    assert err < STATE_TOL
