@@ -196,6 +196,77 @@ def fit_bench(dev, chunks=2, rows=65536, d=4096, targets=16, lams=(1e-4, 1e-3, 1
             "projected_full_fit_s": round(t_acc * 32 / chunks + t_solve, 2)}
 
 
+def hybrid_bench(dev, reps=3, split=24, n_rows=32768, tail=4096):
+    """The Gated-DeltaNet hybrid's late-layer fill (hidden 2048; layers 24..47 = 18 GDN + 6 attention;
+    GDN 16 key / 32 value heads of 128, attention 2 KV heads of 256; P = 28672 filled rows from zero
+    state). Per layer: rf_map_apply, then the GDN fill (rf_norm_linear in-projection + rf_gdn_fill) or
+    the attention fill (rf_norm_kv_write). Counted work per filled row (the reference's accounting):
+    GDN layer 2 H (2 nk dk + nv dv + 2 nv) + 2 H^2 + 2 K C + 6 nv dk dv flop, attention layer
+    2 H^2 + 2 H (2 Hkv d)."""
+    from rfill import ops, synth
+    from rfill.kva import Projector
+    from rfill.model import FillModel
+    cfg = synth.QWEN35_HYBRID
+    w = synth.hybrid_fill(cfg, split, n_rows, tail, device=dev)
+    model = FillModel(cfg, w["tensors"], dev, layers=w["layers"])
+    proj = Projector(split, w["maps"], w["biases"])
+    P, H = w["P"], cfg["hidden_size"]
+    b = w["h_split"][:P]
+    pos = torch.arange(P, device=dev)
+    cs = model.rope_table(pos)
+    x = torch.empty(P, H, dtype=torch.bfloat16, device=dev)
+    ssq = torch.empty(P, ops.ssq_parts(H), dtype=torch.float32, device=dev)
+    nk, nv, dk, dv = model.nk, model.nv, model.dk, model.dv
+    C = 2 * nk * dk + nv * dv
+
+    def step(timer=None):
+        caches = model.new_cache()
+        for i in w["layers"]:
+            kind = model.layer_types[i]
+            f_map = lambda: proj.apply(i, b, x, ssq)                                       # noqa: E731
+            f_fill = lambda: model.fill(i, x, pos, caches, ssq=ssq, cs=cs)                 # noqa: E731
+            for name, f in (("map", f_map), (kind, f_fill)):
+                f() if timer is None else timer.run(name, f)
+        return caches
+
+    step()
+    torch.cuda.synchronize()
+    t = KernelTimer()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        step(t)
+    torch.cuda.synchronize()
+    el = (time.perf_counter() - t0) / reps
+    # one GDN layer's two kernels apart
+    g = next(i for i in w["layers"] if model.layer_types[i] == "gdn")
+    wg = model.W[g]
+    proj.apply(g, b, x, ssq)
+    pre = ops.norm_linear(x, ssq, model.eps, wg["w_in"])
+    st = torch.zeros(nv, dk, dv, dtype=torch.float32, device=dev)
+    for _ in range(reps):
+        t.run("norm_linear", lambda: ops.norm_linear(x, ssq, model.eps, wg["w_in"], pre))
+        st.zero_()
+        t.run("gdn_fill", lambda: ops.gdn_fill(pre, nk, nv, dk, dv, wg["conv"], None, wg["a_log"], wg["dt_bias"], st))
+    torch.cuda.synchronize()
+    n_gdn = sum(model.layer_types[i] == "gdn" for i in w["layers"])
+    n_attn = len(w["layers"]) - n_gdn
+    f_gdn = 2 * H * (C + 2 * nv) + 2 * H * H + 2 * 4 * C + 6 * nv * dk * dv
+    f_attn = 2 * H * H + 2 * H * 2 * model.n_kv * model.head_dim
+    counted = P * (n_gdn * f_gdn + n_attn * f_attn)
+    nl_flop = 2 * P * H * wg["w_in"].shape[0]
+    return {"workload": f"qwen3.5-shaped hybrid fill: hidden {H}, late layers {split}..{cfg['num_hidden_layers'] - 1} "
+                        f"({n_gdn} GDN + {n_attn} attention), {P} filled rows",
+            "filled_tokens_per_s": round(P / el, 1), "ms_per_fill": round(el * 1e3, 3),
+            "counted_flop": counted, "counted_frac_bf16_peak": round(counted / el / PEAK_BF16, 4),
+            "layer_mean_us": {k: round(t.mean_s(k) * 1e6, 1) for k in ("map", "gdn", "attn")},
+            "gdn_kernels": {
+                "rf_norm_linear": {"mean_us": round(t.mean_s("norm_linear") * 1e6, 1),
+                                   "achieved_tflops": round(nl_flop / t.mean_s("norm_linear") / 1e12, 1),
+                                   "flop_per_launch": nl_flop},
+                "rf_gdn_fill": {"mean_us": round(t.mean_s("gdn_fill") * 1e6, 1),
+                                "counted_flop_per_launch": P * (2 * 4 * C + 6 * nv * dk * dv)}}}
+
+
 def traffic_from_profiles(kernel):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE scaled
     by a copy kernel of known size), or None if it has not been measured."""
@@ -216,6 +287,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--no-extras", action="store_true", help="skip ceilings and the standalone KV-write leg")
     ap.add_argument("--no-fit", action="store_true", help="skip the closed-form fit leg")
+    ap.add_argument("--no-hybrid", action="store_true", help="skip the Gated-DeltaNet hybrid fill leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (one MI355X per box); --gpus must be 1", file=sys.stderr)
@@ -273,10 +345,14 @@ def main():
         log("standalone RoPE + KV write and library ceilings")
         out["kernels"]["rf_rope_kv_write"] = kv_write_bench(model, dev, P, SPLIT)
         out["ceilings"] = ceilings(dev, P, H)
+    del caches, xbuf, sbuf
+    torch.cuda.empty_cache()
+    if not args.no_hybrid:
+        log("Gated-DeltaNet hybrid fill leg")
+        out["hybrid"] = hybrid_bench(dev)
+        torch.cuda.empty_cache()
     if not args.no_fit:
         log("closed-form fit leg")
-        del caches, xbuf, sbuf
-        torch.cuda.empty_cache()
         out["fit"] = fit_bench(dev)
     if not args.no_cpu:
         log("CPU baseline (oracle fill on the host cores)")

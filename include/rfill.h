@@ -106,10 +106,17 @@ int rf_norm_linear(const uint16_t* x, int64_t ldx, const float* ssq, int64_t P, 
  * dt_bias) (a_log, dt_bias [nv] fp32), and the chunked (64-row) gated delta rule updating state
  * [nv, dk, dv] fp32 in place. Writes conv_out [3, C] (the last 3 pre-conv rows; must not alias conv_in).
  * Replaces Qwen35._gdn_core with need_out = False (code/kva/model.py:452-484, ops.py:173-262) inside
- * Qwen35.fill (model.py:510-523). Needs dk = dv = 128, nv % nk == 0. */
+ * Qwen35.fill (model.py:510-523). Needs dk = dv = 128, nv % nk == 0, ld % 8 == 0 and 16-byte aligned
+ * pre, conv_w, conv_in and workspace. The workspace (caller-owned device memory) holds the per-chunk
+ * products between the two kernels; a workspace of rf_gdn_workspace_bytes(P, ...) does the fill in one
+ * pass, a smaller one (at least one chunk's worth) in several passes with the same result. */
 int rf_gdn_fill(const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int dk, int dv, const uint16_t* conv_w,
                 const uint16_t* conv_in, uint16_t* conv_out, const float* a_log, const float* dt_bias, float* state,
-                hipStream_t stream);
+                void* workspace, size_t ws_bytes, hipStream_t stream);
+
+/* Workspace bytes rf_gdn_fill needs to fill `rows` rows in one pass (rows = 0: the one-chunk minimum).
+ * Host-only; no device work. */
+int rf_gdn_workspace_bytes(int64_t rows, int nk, int nv, int dk, int dv, size_t* bytes);
 
 /* ---- closed-form fit (code/kva/ridge.py:19-105, code/scripts/fit_sweep.py:87-144) ---- */
 

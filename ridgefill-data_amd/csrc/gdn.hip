@@ -1,240 +1,479 @@
 // Gated DeltaNet fill for gfx950: causal conv + SiLU, k l2-norm, gates and the chunked gated delta
 // rule's state update over P rows of one layer, continuing a carried state (code/kva/model.py:452-484,
-// ops.py:173-262 with need_out = False: the fill keeps only the final state and conv state).
+// ops.py:173-262 with need_out = False: the fill keeps only the final state and the conv state).
 //
-// One workgroup (256 threads) per value head h walks the 64-row chunks in order. Thread t owns one
-// conv channel (t < 128: the k channel t of key head h / (nv / nk); else the v channel t - 128 of
-// head h) with its 3-row window in registers, and the state column c = t % 128, rows
-// (t / 128) * 64 .. + 63, in registers. Per chunk, in LDS (fp32): k (l2-normed, row stride 132 so the
-// 4 x 4-blocked K K^T reads spread over the banks), v then W, U then v_new, A then T = (I + A)^-1, the
-// exchange of the state product's half sums, and the chunk's gates. All arithmetic is fp32, in the
-// reference's order where it rounds differently (conv taps accumulated in order, no fused multiply-add
-// there; bf16 rounding of the conv output and of sigmoid(b)).
+// Per 64-row chunk (gamma = in-chunk cumsum of g, r_i = 1 / |k_i| of the conv output k_i, beta_i):
+//   A = tril_{-1}(beta_i r_i r_j (k_i . k_j) e^{gamma_i - gamma_j}),  T = (I + A)^-1
+//   X = K S,  Y = beta (V - e^gamma r X),  v_new = T Y              (= U - W S of the reference)
+//   S <- e^{gamma_last} S + K^T (r e^{gamma_last - gamma} v_new)
+// with K the raw (bf16) conv output, so K K^T, K S and K^T Z multiply exact bf16 values.
+//
+// Two kernels per pass of up to `chunks` chunks:
+//   k_gdn_prep (chunk x key head, 256 threads): conv + SiLU of the key head's k and of each of its
+//     value heads' v, row norms, gates, G = K K^T on MFMA, A and T = (I + A)^-1 by forward substitution
+//     (fp32). Writes per chunk, in the MFMA operand order the scan reads: K (A operand of K S), K^T (A
+//     operand of K^T Z), T split into hi / lo bf16, V (accumulator layout) and the per-row scalars.
+//   k_gdn_scan (value head x 16-column block, one wave): the sequential chunk recurrence with the fp32
+//     state block [128 x 16] in registers. Each product runs on v_mfma_f32_16x16x32_bf16; fp32 operands
+//     (S, Y, Z, T) are split into hi + lo bf16 so each product keeps ~2^-16 relative accuracy. The
+//     in-lane order of the contraction index is permuted so that every product's accumulator layout
+//     is the next product's B operand (no LDS exchange): lane group g = lane / 16 holds contraction
+//     indices {32s + 4g + e, 32s + 16 + 4g + e : e < 4} of k-step s. The next chunk's operands
+//     (51 KB) stream into LDS by direct buffer loads while the current chunk computes from
+//     registers.
+// k_conv_tail writes the new conv state (the last 3 pre-conv rows of [conv_in; pre]).
+#include <algorithm>
+
 #include "rf_common.h"
 
 namespace rf {
 namespace {
 
-constexpr int DK = 128, DV = 128, CH = 64, NT = 256, KST = DK + 4;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) void* lds_ptr;
 
-struct GdnArgs {
+constexpr int DK = 128, DV = 128, CH = 64, TAPS = 4;
+constexpr int KST = DK + 8;                        // bf16 row stride of the k / v tiles in LDS
+constexpr int FST = CH + 4;                        // fp32 row stride of the 64 x 64 tiles in LDS
+// workspace layout per chunk (bytes): every key head's K orders, then every value head's T, V, scalars
+constexpr uint32_t KP_BYTES = 16384, KTP_BYTES = 16384;
+constexpr uint32_t TP_BYTES = 16384, VP_BYTES = 16384, SC_BYTES = 1024;
+constexpr uint32_t KH_BYTES = KP_BYTES + KTP_BYTES;
+constexpr uint32_t VH_BYTES = TP_BYTES + VP_BYTES + SC_BYTES;
+// scalar block: beta [64], q = e^gamma r [64], z = r e^{gamma_last - gamma} [64], decay e^{gamma_last}
+constexpr int SC_BETA = 0, SC_Q = 64, SC_Z = 128, SC_DECAY = 192;
+
+__device__ __forceinline__ int kperm(int s, int g, int e) { return 32 * s + 4 * g + (e & 3) + ((e >> 2) << 4); }
+
+__device__ __forceinline__ bf16x8 as_frag(const uint4& u) { return __builtin_bit_cast(bf16x8, u); }
+
+// x = hi + lo: hi = x truncated to bf16, lo = (x - hi) rounded to bf16.
+__device__ __forceinline__ void split8(const float (&x)[8], uint4& hi, uint4& lo) {
+  uint32_t h[8], l[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t u = __float_as_uint(x[e]) & 0xffff0000u;
+    h[e] = u >> 16;
+    l[e] = f2bf(x[e] - __uint_as_float(u));
+  }
+  hi = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
+  lo = make_uint4(l[0] | (l[1] << 16), l[2] | (l[3] << 16), l[4] | (l[5] << 16), l[6] | (l[7] << 16));
+}
+
+struct PrepArgs {
   const uint16_t* pre;      // [P, ld] bf16: q | k | v channels, then b [nv], a [nv]
-  int64_t ld, P;
-  int nk, nv, C;            // C = 2 nk DK + nv DV
-  const uint16_t* conv_w;   // [C, 4] bf16
-  const uint16_t* conv_in;  // [3, C] bf16 or null (zeros)
-  uint16_t* conv_out;       // [3, C] bf16
-  const float* a_log;       // [nv]
-  const float* dt_bias;     // [nv]
-  float* state;             // [nv, DK, DV] fp32, updated in place
+  int64_t ld, P, p_begin;   // this pass's chunks start at row p_begin
+  int nk, nv, C;
+  const uint16_t* conv_w;   // [C, 4]
+  const uint16_t* conv_in;  // [3, C] or null
+  const float* a_log;
+  const float* dt_bias;
+  uint8_t* ws;
+  uint32_t chunk_bytes;
 };
 
-__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
-__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
-
-__global__ __launch_bounds__(NT) void k_gdn_fill(GdnArgs a) {
-  __shared__ float k_s[CH][KST];
-  __shared__ float vw_s[CH][DV];
-  __shared__ float u_s[CH][DV];
-  __shared__ float x_s[CH][DV];
-  __shared__ float t_s[CH][CH];
-  __shared__ float beta_s[CH], g_s[CH], gam_s[CH], ed_s[CH];
-
-  const int h = blockIdx.x, t = threadIdx.x;
-  const int rep = a.nv / a.nk, kh = h / rep;
-  const bool is_k = t < DK;
-  const int ch = is_k ? a.nk * DK + kh * DK + t : 2 * a.nk * DK + h * DV + (t - DK);
-  float w0 = bf2f(a.conv_w[ch * 4 + 0]), w1 = bf2f(a.conv_w[ch * 4 + 1]);
-  float w2 = bf2f(a.conv_w[ch * 4 + 2]), w3 = bf2f(a.conv_w[ch * 4 + 3]);
-  // window: x3 oldest .. x1 newest pre-conv input (bf16 values as fp32)
-  float x3 = 0.f, x2 = 0.f, x1 = 0.f;
-  if (a.conv_in) {
-    x3 = bf2f(a.conv_in[0 * a.C + ch]);
-    x2 = bf2f(a.conv_in[1 * a.C + ch]);
-    x1 = bf2f(a.conv_in[2 * a.C + ch]);
+// 8 channels [ch0, ch0 + 8) of input row p (relative to the call's first row); rows before 0 come from
+// the carried conv state, rows at or past P are zero.
+__device__ __forceinline__ uint4 pre_row(const PrepArgs& a, int64_t p, int ch0) {
+  if (p < 0) {
+    if (!a.conv_in) return make_uint4(0, 0, 0, 0);
+    return *reinterpret_cast<const uint4*>(a.conv_in + (3 + p) * a.C + ch0);
   }
-  const int c = t & (DV - 1), r0 = (t >> 7) * 64;
-  float S[64];
-  float* st = a.state + static_cast<int64_t>(h) * DK * DV;
-#pragma unroll
-  for (int r = 0; r < 64; ++r) S[r] = st[(r0 + r) * DV + c];
-  const float negA = -expf(a.a_log[h]), dtb = a.dt_bias[h];
-  const int boff = a.C + h, aoff = a.C + a.nv + h;
+  if (p >= a.P) return make_uint4(0, 0, 0, 0);
+  return *reinterpret_cast<const uint4*>(a.pre + p * a.ld + ch0);
+}
 
-  for (int64_t p0 = 0; p0 < a.P; p0 += CH) {
-    const int m = static_cast<int>(min(static_cast<int64_t>(CH), a.P - p0));
-    // conv + SiLU (bf16 output) of this thread's channel over the chunk's rows
-    for (int r = 0; r < CH; ++r) {
-      float y = 0.f;
-      if (r < m) {
-        const float xin = bf2f(a.pre[(p0 + r) * a.ld + ch]);
-        float acc = mul_rn(x3, w0);
-        acc = add_rn(acc, mul_rn(x2, w1));
-        acc = add_rn(acc, mul_rn(x1, w2));
-        acc = add_rn(acc, mul_rn(xin, w3));
-        y = bf2f(f2bf(acc / (1.0f + expf(-acc))));
-        x3 = x2;
-        x2 = x1;
-        x1 = xin;
-      }
-      if (is_k) k_s[r][t] = y;
-      else vw_s[r][t - DK] = y;
+// Conv + SiLU (bf16) of 8 channels over 4 output rows (thread t: channel group t % 16, rows
+// 4 (t / 16) .. + 3) into dst [64][KST]; taps accumulate oldest first, products and sums rounded
+// separately as the reference's fp32 tap loop; rows at or past m are zero.
+__device__ __forceinline__ void conv_tile(const PrepArgs& a, int64_t p0, int m, int ch_base, uint16_t* dst) {
+  const int t = threadIdx.x, cg = t & 15, r0 = (t >> 4) * 4;
+  const int ch0 = ch_base + cg * 8;
+  float w[8][TAPS];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const uint4 u0 = *reinterpret_cast<const uint4*>(a.conv_w + (ch0 + 4 * q) * TAPS);
+    const uint4 u1 = *reinterpret_cast<const uint4*>(a.conv_w + (ch0 + 4 * q) * TAPS + 8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      w[4 * q + e / 4][e % 4] = bf2f(lane_of(u0, e));
+      w[4 * q + 2 + e / 4][e % 4] = bf2f(lane_of(u1, e));
     }
+  }
+  float x[7][8];
+#pragma unroll
+  for (int j = 0; j < 7; ++j) {
+    const uint4 u = pre_row(a, p0 + r0 - 3 + j, ch0);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[j][e] = bf2f(lane_of(u, e));
+  }
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    uint16_t o[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      float acc = __fmul_rn(x[q][e], w[e][0]);
+      acc = __fadd_rn(acc, __fmul_rn(x[q + 1][e], w[e][1]));
+      acc = __fadd_rn(acc, __fmul_rn(x[q + 2][e], w[e][2]));
+      acc = __fadd_rn(acc, __fmul_rn(x[q + 3][e], w[e][3]));
+      o[e] = (r0 + q < m) ? f2bf(acc / (1.0f + expf(-acc))) : 0;
+    }
+    *reinterpret_cast<uint4*>(dst + (r0 + q) * KST + cg * 8) =
+        make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
+  }
+}
+
+__global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
+  __shared__ __align__(16) uint16_t k_s[CH * KST];
+  __shared__ __align__(16) uint16_t v_s[CH * KST];
+  __shared__ __align__(16) float g_s[CH * FST];     // K K^T
+  __shared__ __align__(16) float a_s[CH * FST];     // A, then T
+  __shared__ float r_s[CH], beta_s[CH], gate_s[CH], gam_s[CH];
+
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6, gi = lane >> 4, ln = lane & 15;
+  const int c = blockIdx.x, kh = blockIdx.y, rep = a.nv / a.nk;
+  const int64_t p0 = a.p_begin + static_cast<int64_t>(c) * CH;
+  const int m = static_cast<int>(min(static_cast<int64_t>(CH), a.P - p0));
+  uint8_t* cbase = a.ws + static_cast<size_t>(c) * a.chunk_bytes;
+
+  conv_tile(a, p0, m, a.nk * DK + kh * DK, k_s);
+  __syncthreads();
+  {  // row norms: 4 threads per row
+    const int row = t >> 2, q = (t & 3) * 32;
+    float s = 0.f;
+    for (int e = 0; e < 32; ++e) {
+      const float f = bf2f(k_s[row * KST + q + e]);
+      s = fmaf(f, f, s);
+    }
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    if ((t & 3) == 0) r_s[row] = 1.0f / sqrtf(s + 1e-6f);
+  }
+  // G = K K^T, lower 16 x 16 tiles: wave w computes tile row w
+  for (int tj = 0; tj <= wave; ++tj) {
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const uint4 ua = *reinterpret_cast<const uint4*>(k_s + (16 * wave + ln) * KST + 32 * s + 8 * gi);
+      const uint4 ub = *reinterpret_cast<const uint4*>(k_s + (16 * tj + ln) * KST + 32 * s + 8 * gi);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(ua), as_frag(ub), acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) g_s[(16 * wave + 4 * gi + r) * FST + 16 * tj + ln] = acc[r];
+  }
+  {  // K in the scan's operand orders: Kp [it][s][lane][8] = K[16 it + lane % 16][kperm(s, g, e)],
+     // Ktp [t][s][lane][8] = K[kperm(s, g, e)][16 t + lane % 16]
+    uint4* kp = reinterpret_cast<uint4*>(cbase + static_cast<size_t>(kh) * KH_BYTES);
+    uint4* ktp = reinterpret_cast<uint4*>(cbase + static_cast<size_t>(kh) * KH_BYTES + KP_BYTES);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int idx = t + 256 * k, l = idx & 63, g = l >> 4, n = l & 15;
+      {
+        const int it = idx >> 8, s = (idx >> 6) & 3;
+        const uint16_t* row = k_s + (16 * it + n) * KST + 32 * s + 4 * g;
+        const uint2 lo = *reinterpret_cast<const uint2*>(row), hi = *reinterpret_cast<const uint2*>(row + 16);
+        kp[idx] = make_uint4(lo.x, lo.y, hi.x, hi.y);
+      }
+      {
+        const int tt = idx >> 7, s = (idx >> 6) & 1;
+        uint16_t v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = k_s[kperm(s, g, e) * KST + 16 * tt + n];
+        ktp[idx] = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+      }
+    }
+  }
+  for (int hv = 0; hv < rep; ++hv) {
+    const int h = kh * rep + hv;
+    __syncthreads();                              // g_s / r_s ready; v_s and a_s free again
+    conv_tile(a, p0, m, 2 * a.nk * DK + h * DV, v_s);
     if (t < CH) {
       float beta = 0.f, g = 0.f;
       if (t < m) {
-        const float b = bf2f(a.pre[(p0 + t) * a.ld + boff]);
+        const int64_t row = (p0 + t) * a.ld;
+        const float b = bf2f(a.pre[row + a.C + h]);
         beta = bf2f(f2bf(1.0f / (1.0f + expf(-b))));
-        const float av = bf2f(a.pre[(p0 + t) * a.ld + aoff]) + dtb;
-        g = negA * (av > 20.0f ? av : log1pf(expf(av)));
+        const float av = bf2f(a.pre[row + a.C + a.nv + h]) + a.dt_bias[h];
+        g = -expf(a.a_log[h]) * (av > 20.0f ? av : log1pf(expf(av)));
       }
       beta_s[t] = beta;
-      g_s[t] = g;
+      gate_s[t] = g;
     }
     __syncthreads();
-    {  // k rows l2-normalised: 4 threads per row
-      const int row = t >> 2, q = (t & 3) * 32;
-      float s = 0.f;
-      for (int e = 0; e < 32; ++e) s = fmaf(k_s[row][q + e], k_s[row][q + e], s);
-      s += __shfl_xor(s, 1, 64);
-      s += __shfl_xor(s, 2, 64);
-      const float inv = 1.0f / sqrtf(s + 1e-6f);
-      for (int e = 0; e < 32; ++e) k_s[row][q + e] *= inv;
-    }
     if (t == 0) {
       float acc = 0.f;
       for (int i = 0; i < CH; ++i) {
-        acc += g_s[i];
+        acc += gate_s[i];
         gam_s[i] = acc;
       }
     }
     __syncthreads();
-    if (t < CH) ed_s[t] = expf(gam_s[CH - 1] - gam_s[t]);
-    {  // t_s = -A, A = tril(beta_i (k_i . k_j) exp(gam_i - gam_j), -1): 4 x 4 blocks, lower half only
-      const int bi = t >> 4, bj = t & 15;
-      float acc[4][4] = {};
-      if (bj <= bi) {
-        for (int d = 0; d < DK; d += 4) {
-          float4 ki[4], kj[4];
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            ki[q] = *reinterpret_cast<const float4*>(&k_s[bi * 4 + q][d]);
-            kj[q] = *reinterpret_cast<const float4*>(&k_s[bj * 4 + q][d]);
-          }
-#pragma unroll
-          for (int p = 0; p < 4; ++p)
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-              acc[p][q] = fmaf(ki[p].x, kj[q].x, fmaf(ki[p].y, kj[q].y, fmaf(ki[p].z, kj[q].z,
-                               fmaf(ki[p].w, kj[q].w, acc[p][q]))));
-        }
-      }
-#pragma unroll
-      for (int p = 0; p < 4; ++p)
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const int i = bi * 4 + p, j = bj * 4 + q;
-          t_s[i][j] = j < i ? -((beta_s[i] * acc[p][q]) * expf(gam_s[i] - gam_s[j])) : 0.f;
-        }
+#pragma unroll 4
+    for (int k = 0; k < 16; ++k) {
+      const int idx = t + 256 * k, i = idx >> 6, j = idx & 63;
+      a_s[i * FST + j] = j < i ? (beta_s[i] * (g_s[i * FST + j] * r_s[i] * r_s[j])) * expf(gam_s[i] - gam_s[j]) : 0.f;
     }
     __syncthreads();
-    // T = (I + A)^-1 below the diagonal, row by row: t[i][j] = t0[i][j] + sum_{j<m<i} t0[i][m] t[m][j]
-    for (int i = 2; i < CH; ++i) {
-      float v = 0.f;
-      if (t < i) {
-        v = t_s[i][t];
-        for (int mm = t + 1; mm < i; ++mm) v = fmaf(t_s[i][mm], t_s[mm][t], v);
-      }
-      __syncthreads();
-      if (t < i) t_s[i][t] = v;
-      __syncthreads();
-    }
-    // U = T (beta v), W = T (beta e^gam k): thread column c, rows (t / 128) * 32 .. + 31. T = t_s + I,
-    // t_s zero on and above the diagonal, so every row sums all 64 columns (register arrays are only
-    // ever indexed by compile-time constants) and adds its diagonal term from LDS.
-    {
-      const int i0 = (t >> 7) * 32;
-      float bv[CH];
+    uint8_t* vbase = cbase + static_cast<size_t>(a.nk) * KH_BYTES + static_cast<size_t>(h) * VH_BYTES;
+    if (wave == 0) {
+      // T = (I + A)^-1: lane j holds column j; T[i][j] = delta_ij - sum_{m < i} A[i][m] T[m][j]
+      // (A is zero on and above the diagonal and tc[m] is zero until row m is done)
+      float tc[CH];
 #pragma unroll
-      for (int j = 0; j < CH; ++j) bv[j] = beta_s[j] * vw_s[j][c];
-      for (int ii = 0; ii < 32; ++ii) {
-        const int i = i0 + ii;
-        float acc = beta_s[i] * vw_s[i][c];
+      for (int i = 0; i < CH; ++i) tc[i] = 0.f;
 #pragma unroll
-        for (int j = 0; j < CH; ++j) acc = fmaf(t_s[i][j], bv[j], acc);
-        u_s[i][c] = acc;
-      }
-#pragma unroll
-      for (int j = 0; j < CH; ++j) bv[j] = (beta_s[j] * expf(gam_s[j])) * k_s[j][c];
-      __syncthreads();                            // every v read: vw_s now takes W
-      for (int ii = 0; ii < 32; ++ii) {
-        const int i = i0 + ii;
-        float acc = (beta_s[i] * expf(gam_s[i])) * k_s[i][c];
-#pragma unroll
-        for (int j = 0; j < CH; ++j) acc = fmaf(t_s[i][j], bv[j], acc);
-        vw_s[i][c] = acc;
-      }
-    }
-    __syncthreads();
-    // v_new = U - W S. Each thread sums its 64 state rows; the lower half subtracts its sums from U
-    // in place, the upper half hands its sums over through x_s, then the lower half subtracts those.
-    for (int i = 0; i < CH; ++i) {
-      float acc = 0.f;
-#pragma unroll
-      for (int r = 0; r < 64; r += 4) {
-        const float4 wv = *reinterpret_cast<const float4*>(&vw_s[i][r0 + r]);
-        acc = fmaf(wv.x, S[r], acc);
-        acc = fmaf(wv.y, S[r + 1], acc);
-        acc = fmaf(wv.z, S[r + 2], acc);
-        acc = fmaf(wv.w, S[r + 3], acc);
-      }
-      if (r0) x_s[i][c] = acc;
-      else u_s[i][c] = u_s[i][c] - acc;
-    }
-    __syncthreads();
-    if (!r0) {
-      for (int i = 0; i < CH; ++i) u_s[i][c] = u_s[i][c] - x_s[i][c];
-    }
-    __syncthreads();
-    // S = S e^{gam_last} + (k e^{gam_last - gam})^T v_new
-    {
-      const float cd = expf(gam_s[CH - 1]);
-      float acc[64];
-#pragma unroll
-      for (int r = 0; r < 64; ++r) acc[r] = 0.f;
       for (int i = 0; i < CH; ++i) {
-        const float vn = u_s[i][c], e = ed_s[i];
+        float acc0 = (i == lane) ? 1.f : 0.f, acc1 = 0.f;
 #pragma unroll
-        for (int r = 0; r < 64; r += 4) {
-          const float4 kv = *reinterpret_cast<const float4*>(&k_s[i][r0 + r]);
-          acc[r] = fmaf(kv.x * e, vn, acc[r]);
-          acc[r + 1] = fmaf(kv.y * e, vn, acc[r + 1]);
-          acc[r + 2] = fmaf(kv.z * e, vn, acc[r + 2]);
-          acc[r + 3] = fmaf(kv.w * e, vn, acc[r + 3]);
+        for (int q = 0; q < i; q += 4) {
+          const float4 av = *reinterpret_cast<const float4*>(a_s + i * FST + q);
+          acc0 = fmaf(-av.x, tc[q], acc0);
+          acc1 = fmaf(-av.y, tc[q + 1], acc1);
+          acc0 = fmaf(-av.z, tc[q + 2], acc0);
+          acc1 = fmaf(-av.w, tc[q + 3], acc1);
         }
+        tc[i] = acc0 + acc1;
       }
 #pragma unroll
-      for (int r = 0; r < 64; ++r) S[r] = S[r] * cd + acc[r];
+      for (int i = 0; i < CH; ++i) a_s[i * FST + lane] = tc[i];
+    } else {
+      // V in the scan's accumulator order: Vp [cb][lane][4 it + r] = V[16 it + 4 g + r][16 cb + lane % 16]
+      uint4* vp = reinterpret_cast<uint4*>(vbase + TP_BYTES);
+      for (int idx = t - 64; idx < 512; idx += 192) {
+        const int cb = idx >> 6, l = idx & 63, g = l >> 4, n = l & 15;
+        uint16_t v[16];
+#pragma unroll
+        for (int it = 0; it < 4; ++it)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) v[4 * it + r] = v_s[(16 * it + 4 * g + r) * KST + 16 * cb + n];
+        vp[2 * idx] = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+        vp[2 * idx + 1] = make_uint4(pack2(v[8], v[9]), pack2(v[10], v[11]), pack2(v[12], v[13]), pack2(v[14], v[15]));
+      }
+      if (wave == 1) {
+        float* sc = reinterpret_cast<float*>(vbase + TP_BYTES + VP_BYTES);
+        const float gl = gam_s[CH - 1];
+        sc[SC_BETA + lane] = beta_s[lane];
+        sc[SC_Q + lane] = expf(gam_s[lane]) * r_s[lane];
+        sc[SC_Z + lane] = r_s[lane] * expf(gl - gam_s[lane]);
+        sc[SC_DECAY + lane] = lane == 0 ? expf(gl) : 0.f;
+      }
     }
     __syncthreads();
-  }
+    {  // T split hi / lo in the scan's A-operand order: Tp [it][s][hl][lane][8] = T[16 it + lane % 16][kperm(s, g, e)]
+      uint4* tp = reinterpret_cast<uint4*>(vbase);
 #pragma unroll
-  for (int r = 0; r < 64; ++r) st[(r0 + r) * DV + c] = S[r];
-  // conv state: the last 3 rows of [conv_in; pre] for this thread's channel, and (one head per key
-  // head) the q channels of key head kh
-  a.conv_out[0 * a.C + ch] = f2bf(x3);
-  a.conv_out[1 * a.C + ch] = f2bf(x2);
-  a.conv_out[2 * a.C + ch] = f2bf(x1);
-  if (h % rep == 0 && t < DK) {
-    const int qc = kh * DK + t;
-    for (int j = 0; j < 3; ++j) {
-      const int64_t idx = a.P - 3 + j;
-      uint16_t v = 0;
-      if (idx >= 0) v = a.pre[idx * a.ld + qc];
-      else if (a.conv_in) v = a.conv_in[(3 + idx) * a.C + qc];
-      a.conv_out[j * a.C + qc] = v;
+      for (int k = 0; k < 2; ++k) {
+        const int idx = t + 256 * k, it = idx >> 7, s = (idx >> 6) & 1, l = idx & 63, g = l >> 4, n = l & 15;
+        float x[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = a_s[(16 * it + n) * FST + kperm(s, g, e)];
+        uint4 hi, lo;
+        split8(x, hi, lo);
+        tp[((it * 2 + s) * 2 + 0) * 64 + l] = hi;
+        tp[((it * 2 + s) * 2 + 1) * 64 + l] = lo;
+      }
     }
   }
+}
+
+struct ScanArgs {
+  const uint8_t* ws;
+  uint32_t chunk_bytes, ws_bytes;
+  int chunks, nk, nv;
+  float* state;             // [nv, DK, DV] fp32, updated in place
+};
+
+// LDS image of one chunk: K, K^T and T orders (16 KB each), this block's V columns (2 KB), the scalars
+constexpr uint32_t ST_KP = 0, ST_KTP = 16384, ST_TP = 32768, ST_VP = 49152, ST_SC = 51200, ST_BYTES = 52224;
+
+// s_waitcnt vmcnt(0) (expcnt, lgkmcnt not waited) and s_waitcnt lgkmcnt(0) (vmcnt, expcnt not waited)
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8) | (0 << 14)); }
+__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
+
+__global__ __launch_bounds__(64) void k_gdn_scan(ScanArgs a) {
+  __shared__ __align__(16) uint8_t smem[ST_BYTES];
+  const int lane = threadIdx.x, gi = lane >> 4, ln = lane & 15;
+  // block b runs on XCD b % 8: XCD x takes (head, column block) pairs [x nv, (x + 1) nv), so the
+  // blocks that share a head's (and a key head's) operands share an L2
+  const int b = blockIdx.x, pair = (b & 7) * a.nv + (b >> 3);
+  const int h = pair >> 3, cb = pair & 7, kh = h / (a.nv / a.nk);
+  float* st = a.state + static_cast<size_t>(h) * DK * DV + cb * 16 + ln;
+  f32x4 S[8];
+#pragma unroll
+  for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) S[tt][r] = st[(16 * tt + 4 * gi + r) * DV];
+
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.ws), static_cast<short>(0),
+                                                                      static_cast<int>(a.ws_bytes), 0x00020000);
+  const uint32_t kh_off = static_cast<uint32_t>(kh) * KH_BYTES;
+  const uint32_t vh_off = static_cast<uint32_t>(a.nk) * KH_BYTES + static_cast<uint32_t>(h) * VH_BYTES;
+  const uint32_t lo = lane * 16;
+  // the chunk's operands, global -> LDS (1 KB per instruction: 64 lanes x 16 bytes)
+  auto issue = [&](int c) {
+    const uint32_t base = static_cast<uint32_t>(c) * a.chunk_bytes;
+#pragma unroll
+    for (int k = 0; k < 32; ++k)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(smem + ST_KP + k * 1024), 16, base + kh_off + k * 1024 + lo,
+                                               0, 0, 0);
+#pragma unroll
+    for (int k = 0; k < 16; ++k)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(smem + ST_TP + k * 1024), 16, base + vh_off + k * 1024 + lo,
+                                               0, 0, 0);
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(smem + ST_VP + k * 1024), 16,
+                                               base + vh_off + TP_BYTES + cb * 2048 + k * 1024 + lo, 0, 0, 0);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(smem + ST_SC), 16, base + vh_off + TP_BYTES + VP_BYTES + lo,
+                                             0, 0, 0);
+  };
+  auto frag = [&](uint32_t off) { return *reinterpret_cast<const uint4*>(smem + off + lo); };
+
+  issue(0);
+  for (int c = 0; c < a.chunks; ++c) {
+    // chunk c's operands: LDS -> registers, then the LDS takes chunk c + 1 while chunk c computes
+    wait_vm0();
+    __builtin_amdgcn_sched_barrier(0);
+    uint4 kp[4][4], ktp[8][2], tp[4][2][2];
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) kp[it][s] = frag(ST_KP + (it * 4 + s) * 1024);
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+      for (int s = 0; s < 2; ++s) ktp[tt][s] = frag(ST_KTP + (tt * 2 + s) * 1024);
+#pragma unroll
+    for (int it = 0; it < 4; ++it)
+#pragma unroll
+      for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int hl = 0; hl < 2; ++hl)
+          if (s == 0 || it >= 2) tp[it][s][hl] = frag(ST_TP + ((it * 2 + s) * 2 + hl) * 1024);
+    const uint4 v0 = *reinterpret_cast<const uint4*>(smem + ST_VP + lane * 32);
+    const uint4 v1 = *reinterpret_cast<const uint4*>(smem + ST_VP + lane * 32 + 16);
+    const float* sc = reinterpret_cast<const float*>(smem + ST_SC);
+    float4 be[4], qq[4], zz[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      be[it] = *reinterpret_cast<const float4*>(sc + SC_BETA + 16 * it + 4 * gi);
+      qq[it] = *reinterpret_cast<const float4*>(sc + SC_Q + 16 * it + 4 * gi);
+      zz[it] = *reinterpret_cast<const float4*>(sc + SC_Z + 16 * it + 4 * gi);
+    }
+    const float decay = sc[SC_DECAY];
+    wait_lgkm0();
+    __builtin_amdgcn_sched_barrier(0);
+    if (c + 1 < a.chunks) issue(c + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    // X = K S
+    f32x4 X[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) X[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      float x[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        x[r] = S[2 * s][r];
+        x[4 + r] = S[2 * s + 1][r];
+      }
+      uint4 bh, bl;
+      split8(x, bh, bl);
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        X[it] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(kp[it][s]), as_frag(bh), X[it], 0, 0, 0);
+        X[it] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(kp[it][s]), as_frag(bl), X[it], 0, 0, 0);
+      }
+    }
+    // Y = beta (V - q X), rows 16 it + 4 g + r
+    float Y[4][4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      const float bb[4] = {be[it].x, be[it].y, be[it].z, be[it].w}, q4[4] = {qq[it].x, qq[it].y, qq[it].z, qq[it].w};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int e = 4 * it + r;
+        const float v = bf2f(lane_of(e < 8 ? v0 : v1, e & 7));
+        Y[it][r] = bb[r] * (v - q4[r] * X[it][r]);
+      }
+    }
+    uint4 yh[2], yl[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      float x[8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        x[r] = Y[2 * s][r];
+        x[4 + r] = Y[2 * s + 1][r];
+      }
+      split8(x, yh[s], yl[s]);
+    }
+    // v_new = T Y (T lower triangular: row tiles 0 and 1 need k-step 0 only)
+    f32x4 vn[4];
+#pragma unroll
+    for (int it = 0; it < 4; ++it) {
+      vn[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        if (s == 1 && it < 2) continue;
+        const bf16x8 th = as_frag(tp[it][s][0]), tl = as_frag(tp[it][s][1]);
+        vn[it] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(th, as_frag(yh[s]), vn[it], 0, 0, 0);
+        vn[it] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(th, as_frag(yl[s]), vn[it], 0, 0, 0);
+        vn[it] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tl, as_frag(yh[s]), vn[it], 0, 0, 0);
+      }
+    }
+    // Z = z v_new; S <- decay S + K^T Z
+    uint4 zh[2], zl[2];
+#pragma unroll
+    for (int s = 0; s < 2; ++s) {
+      float x[8];
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        const int it = 2 * s + half;
+        const float z4[4] = {zz[it].x, zz[it].y, zz[it].z, zz[it].w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) x[4 * half + r] = z4[r] * vn[it][r];
+      }
+      split8(x, zh[s], zl[s]);
+    }
+#pragma unroll
+    for (int tt = 0; tt < 8; ++tt) {
+      f32x4 acc = S[tt] * decay;
+#pragma unroll
+      for (int s = 0; s < 2; ++s) {
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(ktp[tt][s]), as_frag(zh[s]), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(ktp[tt][s]), as_frag(zl[s]), acc, 0, 0, 0);
+      }
+      S[tt] = acc;
+    }
+  }
+  wait_vm0();
+#pragma unroll
+  for (int tt = 0; tt < 8; ++tt)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) st[(16 * tt + 4 * gi + r) * DV] = S[tt][r];
+}
+
+// conv_out[j][ch] = row P - 3 + j of [conv_in; pre] (conv_in rows -3..-1; zeros if conv_in is null)
+__global__ void k_conv_tail(const uint16_t* pre, int64_t ld, int64_t P, int C, const uint16_t* conv_in,
+                            uint16_t* conv_out) {
+  const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= 3 * C) return;
+  const int j = idx / C, ch = idx % C;
+  const int64_t p = P - 3 + j;
+  uint16_t v = 0;
+  if (p >= 0) v = pre[p * ld + ch];
+  else if (conv_in) v = conv_in[(3 + p) * C + ch];
+  conv_out[idx] = v;
+}
+
+inline uint32_t chunk_bytes(int nk, int nv) { return static_cast<uint32_t>(nk) * KH_BYTES + static_cast<uint32_t>(nv) * VH_BYTES; }
+
+int check_heads(const char* fn, int nk, int nv, int dk, int dv) {
+  if (dk != DK || dv != DV) return fail(RF_EUNSUPPORTED, "%s: key / value head dims %d / %d (128 / 128)", fn, dk, dv);
+  if (nk <= 0 || nv <= 0 || nv % nk || nv > 1024) return fail(RF_EINVAL_SHAPE, "%s: heads nk %d nv %d", fn, nk, nv);
+  return RF_OK;
 }
 
 }  // namespace
@@ -242,17 +481,44 @@ __global__ __launch_bounds__(NT) void k_gdn_fill(GdnArgs a) {
 
 using namespace rf;
 
+extern "C" int rf_gdn_workspace_bytes(int64_t rows, int nk, int nv, int dk, int dv, size_t* bytes) {
+  if (const int e = check_heads("rf_gdn_workspace_bytes", nk, nv, dk, dv)) return e;
+  if (rows < 0 || !bytes) return fail(RF_EINVAL_ARG, "rf_gdn_workspace_bytes: rows %lld", (long long)rows);
+  const int64_t chunks = rows > 0 ? (rows + CH - 1) / CH : 1;
+  *bytes = static_cast<size_t>(chunks) * chunk_bytes(nk, nv);
+  return RF_OK;
+}
+
 extern "C" int rf_gdn_fill(const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int dk, int dv,
                            const uint16_t* conv_w, const uint16_t* conv_in, uint16_t* conv_out, const float* a_log,
-                           const float* dt_bias, float* state, hipStream_t stream) {
-  if (!pre || !conv_w || !conv_out || !a_log || !dt_bias || !state) return fail(RF_EINVAL_ARG, "rf_gdn_fill: null pointer");
-  if (dk != DK || dv != DV) return fail(RF_EUNSUPPORTED, "rf_gdn_fill: key / value head dims %d / %d (128 / 128)", dk, dv);
-  if (nk <= 0 || nv <= 0 || nv % nk || nv > 4096) return fail(RF_EINVAL_SHAPE, "rf_gdn_fill: heads nk %d nv %d", nk, nv);
+                           const float* dt_bias, float* state, void* workspace, size_t ws_bytes, hipStream_t stream) {
+  if (!pre || !conv_w || !conv_out || !a_log || !dt_bias || !state || !workspace)
+    return fail(RF_EINVAL_ARG, "rf_gdn_fill: null pointer");
+  if (const int e = check_heads("rf_gdn_fill", nk, nv, dk, dv)) return e;
   const int64_t C = 2ll * nk * DK + static_cast<int64_t>(nv) * DV;
-  if (P < 0 || ld < C + 2 * nv) return fail(RF_EINVAL_SHAPE, "rf_gdn_fill: P %lld, ld %lld < %lld", (long long)P,
-                                            (long long)ld, (long long)(C + 2 * nv));
+  if (P < 0 || ld < C + 2 * nv || ld % 8)
+    return fail(RF_EINVAL_SHAPE, "rf_gdn_fill: P %lld, ld %lld (need >= %lld and a multiple of 8)", (long long)P,
+                (long long)ld, (long long)(C + 2 * nv));
+  if (!aligned16(pre) || !aligned16(conv_w) || (conv_in && !aligned16(conv_in)) || !aligned16(workspace))
+    return fail(RF_EINVAL_ARG, "rf_gdn_fill: pre, conv_w, conv_in and workspace must be 16-byte aligned");
   if (conv_in == conv_out) return fail(RF_EINVAL_ARG, "rf_gdn_fill: conv_out must not alias conv_in");
-  GdnArgs a{pre, ld, P, nk, nv, static_cast<int>(C), conv_w, conv_in, conv_out, a_log, dt_bias, state};
-  hipLaunchKernelGGL(k_gdn_fill, dim3(nv), dim3(NT), 0, stream, a);
-  return check_launch("rf_gdn_fill");
+  const uint32_t cbytes = chunk_bytes(nk, nv);
+  // chunks per pass: what the workspace holds, with buffer offsets below 2^31
+  const int64_t per_pass = std::min<int64_t>(static_cast<int64_t>(ws_bytes / cbytes), 0x7fffffffll / cbytes);
+  if (per_pass < 1)
+    return fail(RF_EINVAL_ARG, "rf_gdn_fill: workspace %zu bytes < one chunk (%u bytes)", ws_bytes, cbytes);
+  const int64_t chunks = (P + CH - 1) / CH;
+  for (int64_t c0 = 0; c0 < chunks; c0 += per_pass) {
+    const int nc = static_cast<int>(std::min<int64_t>(per_pass, chunks - c0));
+    PrepArgs pa{pre, ld, P, c0 * CH, nk, nv, static_cast<int>(C), conv_w, conv_in, a_log, dt_bias,
+                static_cast<uint8_t*>(workspace), cbytes};
+    hipLaunchKernelGGL(k_gdn_prep, dim3(nc, nk), dim3(256), 0, stream, pa);
+    if (const int e = check_launch("rf_gdn_fill (prep)")) return e;
+    ScanArgs sa{static_cast<const uint8_t*>(workspace), cbytes, static_cast<uint32_t>(nc) * cbytes, nc, nk, nv, state};
+    hipLaunchKernelGGL(k_gdn_scan, dim3(nv * 8), dim3(64), 0, stream, sa);
+    if (const int e = check_launch("rf_gdn_fill (scan)")) return e;
+  }
+  hipLaunchKernelGGL(k_conv_tail, dim3((3 * C + 255) / 256), dim3(256), 0, stream, pre, ld, P, static_cast<int>(C),
+                     conv_in, conv_out);
+  return check_launch("rf_gdn_fill (conv state)");
 }

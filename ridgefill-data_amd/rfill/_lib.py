@@ -24,6 +24,7 @@ class HipError(RuntimeError):
 
 
 _P, _I64, _I32, _F32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+_SZ, _PSZ = ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)
 
 # name -> argument types (every function returns int status)
 SIGNATURES = {
@@ -36,7 +37,8 @@ SIGNATURES = {
                          _P, _P, _I64, _I64, _I64, _I64, _P],
     "rf_rope_kv_write": [_P, _I64, _P, _I64, _I64, _I32, _I32, _P, _I32, _P, _P, _I64, _I64, _I64, _I64, _P],
     "rf_norm_linear": [_P, _I64, _P, _I64, _I64, _F32, _P, _I64, _P, _I64, _P],
-    "rf_gdn_fill": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P],
+    "rf_gdn_fill": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+    "rf_gdn_workspace_bytes": [_I64, _I32, _I32, _I32, _I32, _PSZ],
     "rf_transpose": [_P, _I64, _I64, _I64, _P, _I64, _P, _P],
     "rf_colsum_fold": [_P, _I64, _I64, _P, _P],
     "rf_gram_accumulate": [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],

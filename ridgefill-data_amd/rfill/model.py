@@ -21,6 +21,7 @@ from . import ops
 from ._lib import UnsupportedArchitecture
 
 KV_RESERVE = 64
+GDN_ROWS = 8192          # rows per GDN workspace pass (the reference's GDN segment, code/kva/model.py:31)
 
 
 class FillModel:
@@ -67,6 +68,7 @@ class FillModel:
         pre = "model.language_model." if "model.language_model.embed_tokens.weight" in tensors else "model."
         want = range(self.n_layers) if layers is None else layers
         self.W = [None] * self.n_layers
+        self._gdn_ws = None
         for i in want:
             self.W[i] = self._pack(i, f"{pre}layers.{i}.", tensors)
 
@@ -180,12 +182,20 @@ class FillModel:
         rec = (torch.zeros(self.nv, self.dk, self.dv, dtype=torch.float32, device=x.device) if rec is None
                else rec.float().contiguous().clone())
         c["conv"] = ops.gdn_fill(pre, self.nk, self.nv, self.dk, self.dv, w["conv"], c.get("conv"), w["a_log"],
-                                 w["dt_bias"], rec)
+                                 w["dt_bias"], rec, self._gdn_workspace(P, x.device))
         c["rec"] = rec
         c["len"] = c.get("len", 0) + P
         if st is not None:
             c["rec"] = c["rec"] + st.to(c["rec"])
         return {}
+
+    def _gdn_workspace(self, rows, device):
+        """The GDN kernels' per-chunk workspace, shared by every GDN layer (stream-ordered reuse), sized
+        for min(rows, GDN_ROWS) rows per pass."""
+        need = ops.gdn_workspace_bytes(min(rows, GDN_ROWS), self.nk, self.nv, self.dk, self.dv)
+        if self._gdn_ws is None or self._gdn_ws.numel() < need or self._gdn_ws.device != device:
+            self._gdn_ws = torch.empty(need, dtype=torch.uint8, device=device)
+        return self._gdn_ws
 
     def fill_kv(self, i, k, v, pos, cache, cs=None):
         """Cache-only fill from pre-RoPE K and V [P, Hkv, d] (the reads() layout)."""

@@ -1,6 +1,7 @@
 """Torch-tensor front end of the librfill kernels (device memory and streams are PyTorch's; the
 arithmetic is the HIP kernels'). Every function checks devices, dtypes and layouts before it hands
 raw pointers to the C ABI, and launches on the current stream of the tensors' device."""
+import ctypes
 import math
 
 import torch
@@ -180,9 +181,18 @@ def norm_linear(x, ssq, eps, w, out=None):
     return out
 
 
-def gdn_fill(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state):
+def gdn_workspace_bytes(rows, nk, nv, dk=128, dv=128):
+    """Bytes of device workspace rf_gdn_fill needs to fill `rows` rows in one pass."""
+    n = ctypes.c_size_t(0)
+    _lib.call("rf_gdn_workspace_bytes", rows, nk, nv, dk, dv, ctypes.byref(n))
+    return n.value
+
+
+def gdn_fill(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state, workspace=None):
     """Gated DeltaNet fill from in-projection rows pre [P, >= C + 2 nv] (q | k | v | b | a): updates
-    state [nv, dk, dv] fp32 in place, returns the new conv state [3, C] bf16."""
+    state [nv, dk, dv] fp32 in place, returns the new conv state [3, C] bf16. workspace: uint8 device
+    memory for the per-chunk products (None: allocated for one pass over P rows; a smaller one, of at
+    least gdn_workspace_bytes(0, ...), makes several passes)."""
     _need(pre, "pre", torch.bfloat16, 2)
     _need(conv_w, "conv_w", torch.bfloat16, 2)
     _need(a_log, "a_log", torch.float32, 1)
@@ -200,9 +210,14 @@ def gdn_fill(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state):
         _need(conv_in, "conv_in", torch.bfloat16, 2)
         if tuple(conv_in.shape) != (3, C) or not conv_in.is_contiguous():
             raise ValueError("gdn_fill: conv state shape")
+    if workspace is None:
+        workspace = torch.empty(gdn_workspace_bytes(pre.shape[0], nk, nv, dk, dv), dtype=torch.uint8,
+                                device=pre.device)
+    _need(workspace, "workspace", torch.uint8, 1)
     conv_out = torch.empty(3, C, dtype=torch.bfloat16, device=pre.device)
     _lib.call("rf_gdn_fill", _ptr(pre), pre.stride(0), pre.shape[0], nk, nv, dk, dv, _ptr(conv_w), _ptr(conv_in),
-              _ptr(conv_out), _ptr(a_log), _ptr(dt_bias), _ptr(state), _stream(pre))
+              _ptr(conv_out), _ptr(a_log), _ptr(dt_bias), _ptr(state), _ptr(workspace), workspace.numel(),
+              _stream(pre))
     return conv_out
 
 

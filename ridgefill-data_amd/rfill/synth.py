@@ -5,8 +5,15 @@
                    channels x 20; per late layer l a ridge map W_l = I + 0.02 N(0, 1/H) (variance 1/H)
                    with bias N(0, 1e-3) (std), an input RMSNorm gain 1 + N(0, 0.05), K / V projections
                    N(0, 0.02) and, for Qwen3, a k_norm gain 1 + N(0, 0.05).
-Seeds: 10 (rows), 11 (channel gains and outliers), 12 + l (layer l's weights), 13 (exact-row
-positions), 14 (exact-row inputs). Normal(mu, s) parameters are standard deviations except the
+  hybrid_fill(...) the Gated-DeltaNet hybrid (Qwen3.5-shaped, hidden 2048, layers 3 GDN : 1 attention)
+                   late-layer fill: the same h_split and ridge maps at H = 2048; zero-centred input-norm
+                   gains N(0, 0.05); GDN in-projections (q | k | v [8192, 2048], b, a [32, 2048])
+                   N(0, 0.02), depthwise conv U(-0.5, 0.5) [8192, 4], A_log = log U(0, 16) and
+                   dt_bias = 1 (the architecture's own initialisation), so the gates run through the
+                   checkpoint formula g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b);
+                   attention layers K / V N(0, 0.02) with a zero-centred k_norm gain N(0, 0.05).
+Seeds: 10 (rows), 11 (channel gains and outliers), 12 + l (layer l's weights), 100 + l (the map of
+hybrid GDN layer l), 13 (exact-row positions), 14 (exact-row inputs). Normal(mu, s) parameters are standard deviations except the
 explicit variance 1/H of the map noise.
 """
 import torch
@@ -16,6 +23,14 @@ LLAMA_8B = dict(model_type="llama", num_hidden_layers=32, hidden_size=4096, num_
 QWEN3_8B = dict(model_type="qwen3", num_hidden_layers=36, hidden_size=4096, num_attention_heads=32,
                 num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-6,
                 rope_parameters=dict(rope_type="default", rope_theta=1000000.0))
+
+
+QWEN35_HYBRID = dict(model_type="qwen3_5_text", num_hidden_layers=48, hidden_size=2048, num_attention_heads=16,
+                     num_key_value_heads=2, head_dim=256, rms_norm_eps=1e-6,
+                     layer_types=["full_attention" if i % 4 == 3 else "linear_attention" for i in range(48)],
+                     linear_num_key_heads=16, linear_num_value_heads=32, linear_key_head_dim=128,
+                     linear_value_head_dim=128, linear_conv_kernel_dim=4,
+                     rope_parameters=dict(rope_type="default", rope_theta=10000000.0, partial_rotary_factor=0.25))
 
 
 def _gen(seed, device):
@@ -100,3 +115,46 @@ def fit_chunk(chunk, rows, d, maps, device="cpu", nu=5, outliers=4, noise=0.1):
         e = noise * torch.randn(rows, d, generator=_gen(21 + l + 1000 * chunk, device), device=device)
         ys.append((x.float() @ t + e).to(torch.bfloat16))
     return x, ys
+
+
+def gdn_layer_weights(cfg, layer, device="cpu"):
+    """HF-named weights of one Gated DeltaNet layer (seed 12 + layer)."""
+    h, nk, nv = cfg["hidden_size"], cfg["linear_num_key_heads"], cfg["linear_num_value_heads"]
+    dk, dv, kc = cfg["linear_key_head_dim"], cfg["linear_value_head_dim"], cfg["linear_conv_kernel_dim"]
+    C = 2 * nk * dk + nv * dv
+    g = _gen(12 + layer, device)
+    p = f"model.layers.{layer}."
+    a = p + "linear_attn."
+    rn = lambda *s: torch.randn(*s, generator=g, device=device)                        # noqa: E731
+    t = {p + "input_layernorm.weight": 0.05 * rn(h), a + "in_proj_qkv.weight": 0.02 * rn(C, h),
+         a + "in_proj_b.weight": 0.02 * rn(nv, h), a + "in_proj_a.weight": 0.02 * rn(nv, h),
+         a + "conv1d.weight": torch.rand(C, 1, kc, generator=g, device=device) - 0.5}
+    t = {k: v.to(torch.bfloat16) for k, v in t.items()}
+    t[a + "A_log"] = torch.log(16 * torch.rand(nv, generator=g, device=device).clamp_min(1e-6))
+    t[a + "dt_bias"] = torch.ones(nv, device=device)
+    return t
+
+
+def hybrid_fill(cfg, split, n_rows, tail, device="cpu", map_noise=0.02):
+    """The hybrid late-layer fill workload (dict as dense_fill's, plus layer_types)."""
+    L, h = cfg["num_hidden_layers"], cfg["hidden_size"]
+    layers = list(range(split, L))
+    tensors, maps, biases = {}, {}, {}
+    for l in layers:
+        if cfg["layer_types"][l] == "linear_attention":
+            tensors.update(gdn_layer_weights(cfg, l, device))
+            g = _gen(100 + l, device)
+        else:
+            hkv, d = cfg["num_key_value_heads"], cfg["head_dim"]
+            g = _gen(12 + l, device)
+            p = f"model.layers.{l}."
+            t = {p + "input_layernorm.weight": 0.05 * torch.randn(h, generator=g, device=device),
+                 p + "self_attn.k_proj.weight": 0.02 * torch.randn(hkv * d, h, generator=g, device=device),
+                 p + "self_attn.v_proj.weight": 0.02 * torch.randn(hkv * d, h, generator=g, device=device),
+                 p + "self_attn.k_norm.weight": 0.05 * torch.randn(d, generator=g, device=device)}
+            tensors.update({k: v.to(torch.bfloat16) for k, v in t.items()})
+        w = torch.eye(h, device=device) + map_noise * torch.randn(h, h, generator=g, device=device) / h ** 0.5
+        maps[l] = w.to(torch.bfloat16)
+        biases[l] = (1e-3 * torch.randn(h, generator=g, device=device)).to(torch.bfloat16)
+    return dict(cfg=cfg, split=split, layers=layers, h_split=hidden_states(n_rows, h, device=device),
+                P=n_rows - tail, tensors=tensors, maps=maps, biases=biases)

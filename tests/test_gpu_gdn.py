@@ -1,7 +1,8 @@
 """GPU parity of the Gated DeltaNet fill (rf_norm_linear + rf_gdn_fill) against the CPU oracle, whose GDN
 math is pinned to transformers' Qwen3.5 (tests/test_oracle_model.py). Bars: the conv state is a copy of
 pre-conv rows, bit-exact; with the oracle's own in-projection rows as input the recurrent state agrees
-to fp32 rounding (<= 1e-4 relative Frobenius); through the whole bf16 fill path <= 1e-2."""
+to fp32 rounding (<= 1e-4 relative Frobenius; the products run on bf16 MFMA with fp32 operands split
+into hi + lo bf16 halves); through the whole bf16 fill path <= 1e-2."""
 import pytest
 import torch
 
@@ -43,6 +44,32 @@ def test_recurrence_matches_oracle_given_the_same_rows(dev, P):
     print(f"P {P}: recurrent state rel err {err:.2e}")
     assert err < 1e-4
     assert torch.equal(conv.cpu(), c[0]["conv"])
+
+
+def test_workspace_passes_are_bitwise_equal(dev):
+    """A workspace of 1 or 3 chunks (several prep / scan passes) gives the single pass's bits."""
+    from rfill import ops
+    cfg = gdn_config()
+    t = gdn_tensors(cfg, seed=4)
+    om = OM.OracleModel(cfg, t, dtype=torch.bfloat16)
+    x = inputs(700, cfg["hidden_size"], seed=24)
+    rows = _pre_rows(om, x).to(dev)
+    w = om.W[0]
+    args = (w["conv"].to(dev).contiguous(), None, w["A_log"].to(dev), w["dt_bias"].to(dev))
+    out = {}
+    for chunks in (None, 1, 3):
+        st = torch.zeros(4, 128, 128, dtype=torch.float32, device=dev)
+        ws = None
+        if chunks:
+            ws = torch.empty(chunks * ops.gdn_workspace_bytes(0, 2, 4), dtype=torch.uint8, device=dev)
+        conv = ops.gdn_fill(rows, 2, 4, 128, 128, *args, st, ws)
+        out[chunks] = (st, conv)
+    torch.cuda.synchronize()
+    for chunks in (1, 3):
+        assert torch.equal(out[chunks][0], out[None][0]) and torch.equal(out[chunks][1], out[None][1])
+    with pytest.raises(ValueError):
+        ops.gdn_fill(rows, 2, 4, 128, 128, *args, out[None][0],
+                     torch.empty(ops.gdn_workspace_bytes(0, 2, 4) - 16, dtype=torch.uint8, device=dev))
 
 
 def test_fill_matches_oracle_and_continues(dev):
