@@ -92,10 +92,12 @@ def run_lower(model, ids, splits):
     return hs, cache
 
 
-def finish(model, ids, h_split, lower_cache, arm, keep, oracle=None, exact_rows=None, fill_store=None):
+def finish(model, ids, h_split, lower_cache, arm, keep, oracle=None, exact_rows=None, fill_store=None,
+           row_inputs=None):
     """Late layers of one arm (code/kva/kva.py:319-460, the fill subset). Prefix rows [0, P) fill each
     late layer from x (projector / identity / true inputs) with the exact rows R scattered in
     (index_copy) and run through layer_rows; then +st; then the tail rows run the exact layer.
+    row_inputs (dict): receives the exact rows' input to every late layer {layer: [|R|, H]}.
     Returns (logits of the last `keep` rows, cache, P)."""
     n = ids.shape[0]
     split = arm.split
@@ -115,6 +117,8 @@ def finish(model, ids, h_split, lower_cache, arm, keep, oracle=None, exact_rows=
         if P > 0:
             if arm.fill == "none":
                 if rows is not None:
+                    if row_inputs is not None:
+                        row_inputs[i] = hr
                     hr = model.layer(i, hr, pos[rows], cache)
             else:
                 if arm.fill == "proj":
@@ -126,6 +130,8 @@ def finish(model, ids, h_split, lower_cache, arm, keep, oracle=None, exact_rows=
                 else:
                     raise ValueError(arm.fill)
                 if rows is not None:
+                    if row_inputs is not None:
+                        row_inputs[i] = hr
                     x = x.index_copy(0, rows, hr.to(x.dtype))
                     hr = model.layer_rows(i, x, pos[:P], rows, cache)
                 else:
