@@ -183,28 +183,45 @@ __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t
   __syncthreads();
 }
 
+// LDS beyond the stages (32 KiB): per-tile side data the epilogues read -- the bias tile, the rows'
+// norm scales, the rows' sum-of-squares halves. Filled before the main loop, read after it.
+constexpr int AUX_U4 = 2048;
+constexpr int LDS_ALL_U4 = LDS_U4 + AUX_U4;   // 160 KiB, the whole LDS of a CU
+
 // Epilogue stage 1: value(mt, nt, g, e, acc) rounded to bf16 into the row-major LDS image of the tile.
 // Lane (lr, lk) holds, for tile row wm*128 + mt*32 + lr, columns wn*128 + nt*32 + 8g + 4lk + e.
 // Image layout: row r's 16-byte chunk c lives at slot r * 32 + (c ^ (r & 31)).
-template <class F>
-__device__ __forceinline__ void stage_tile(uint4* lds, const f32x16 (&acc)[4][4], F value) {
+// With SSQ, ss[mt] receives the sum of squares of the lane's 64 rounded values of that row, a sequential
+// fma chain in (nt, g, e) order (the order rf_row_ssq reproduces).
+template <bool SSQ, class F>
+__device__ __forceinline__ void stage_tile(uint4* lds, const f32x16 (&acc)[4][4], F value, float (&ss)[4]) {
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
   const int wm = w >> 1, wn = w & 1, lr = lane & 31, lk = lane >> 5;
   char* base = reinterpret_cast<char*>(lds);
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
     const int row = wm * 128 + mt * 32 + lr;
+    float sq = 0.f;
 #pragma unroll
     for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int c0 = wn * 128 + nt * 32 + 8 * g + 4 * lk;
-        uint16_t h[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) h[e] = f2bf(value(mt, nt, g, e, acc[nt][mt][4 * g + e]));
+        const uint32_t p0 = bf16_pair(value(mt, nt, g, 0, acc[nt][mt][4 * g + 0]),
+                                      value(mt, nt, g, 1, acc[nt][mt][4 * g + 1]));
+        const uint32_t p1 = bf16_pair(value(mt, nt, g, 2, acc[nt][mt][4 * g + 2]),
+                                      value(mt, nt, g, 3, acc[nt][mt][4 * g + 3]));
+        if (SSQ) {
+          const float r0 = bf_lo(p0), r1 = bf_hi(p0), r2 = bf_lo(p1), r3 = bf_hi(p1);
+          sq = fmaf(r0, r0, sq);
+          sq = fmaf(r1, r1, sq);
+          sq = fmaf(r2, r2, sq);
+          sq = fmaf(r3, r3, sq);
+        }
         const int off = row * 512 + (((c0 >> 3) ^ (row & 31)) << 4) + ((c0 & 7) << 1);
-        *reinterpret_cast<uint2*>(base + off) = make_uint2(pack2(h[0], h[1]), pack2(h[2], h[3]));
+        *reinterpret_cast<uint2*>(base + off) = make_uint2(p0, p1);
       }
+    ss[mt] = sq;
   }
 }
 
@@ -212,46 +229,64 @@ __device__ __forceinline__ uint4 image_chunk(const uint4* lds, int row, int c) {
   return lds[row * 32 + (c ^ (row & 31))];
 }
 
+// Each of the tile's rows' input RMSNorm scale 1 / sqrt(mean(x^2) + eps) from its sum-of-squares
+// partials (summed in order), into rs[0..255]; thread t takes row m0 + t. Called before the main loop
+// (the loads overlap its first operand loads); rs is read after it.
+__device__ __forceinline__ void row_scales(const float* __restrict__ ssq, int nparts, float width, float eps, int M,
+                                           int m0, float* rs) {
+  const int t = threadIdx.x, gm = m0 + t;
+  float s = 0.f;
+  if (gm < M) {
+    const float* q = ssq + static_cast<int64_t>(gm) * nparts;
+    for (int i = 0; i < nparts; ++i) s += q[i];
+  }
+  rs[t] = 1.0f / sqrtf(s / width + eps);
+}
+
 __global__ __launch_bounds__(NTHR) void k_map_apply(const uint16_t* __restrict__ B, int64_t ldb,
                                                     const uint16_t* __restrict__ W,
                                                     const uint16_t* __restrict__ bias,
                                                     uint16_t* __restrict__ X, int64_t ldx,
                                                     float* __restrict__ ssq, int M, int N, int K) {
-  __shared__ uint4 lds[LDS_U4];
+  __shared__ uint4 lds[LDS_ALL_U4];
+  uint4* aux = lds + LDS_U4;
+  float* halves = reinterpret_cast<float*>(aux + 32);          // [2][256] row sum-of-squares halves
   const int tiles_n = N / BN;
   int tm, tn;
   tile_coords(xcd_tile(blockIdx.x, gridDim.x), (M + BM - 1) / BM, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
+  const int t = threadIdx.x;
+  if (t < 32) aux[t] = bias ? *reinterpret_cast<const uint4*>(bias + n0 + t * 8) : make_uint4(0u, 0u, 0u, 0u);
   f32x16 acc[4][4];
   mainloop(B, ldb, W, K, M, K, m0, n0, lds, acc);
 
-  const int lane = threadIdx.x & 63, wn = (threadIdx.x >> 6) & 1, lk = lane >> 5;
-  float bv[4][4][4];
+  const int lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1, lr = lane & 31, lk = lane >> 5;
+  const uint16_t* bt = reinterpret_cast<const uint16_t*>(aux);
+  uint2 bq[4][4];
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int c = n0 + wn * 128 + nt * 32 + 8 * g + 4 * lk;
-      uint2 u = bias ? *reinterpret_cast<const uint2*>(bias + c) : make_uint2(0u, 0u);
-      bv[nt][g][0] = bf2f(u.x & 0xffffu);
-      bv[nt][g][1] = bf2f(u.x >> 16);
-      bv[nt][g][2] = bf2f(u.y & 0xffffu);
-      bv[nt][g][3] = bf2f(u.y >> 16);
-    }
-  stage_tile(lds, acc, [&](int, int nt, int g, int e, float a) { return a + bv[nt][g][e]; });
+    for (int g = 0; g < 4; ++g) bq[nt][g] = *reinterpret_cast<const uint2*>(bt + wn * 128 + nt * 32 + 8 * g + 4 * lk);
+  float ss[4];
+  stage_tile<true>(lds, acc, [&](int, int nt, int g, int e, float a) {
+    const uint32_t u = (e < 2) ? bq[nt][g].x : bq[nt][g].y;
+    return a + bf2f(static_cast<uint16_t>((e & 1) ? (u >> 16) : (u & 0xffffu)));
+  }, ss);
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const float tot = ss[mt] + __shfl_xor(ss[mt], 32, 64);     // the row's 128 columns of this wave
+    if (lk == 0) halves[wn * 256 + wm * 128 + mt * 32 + lr] = tot;
+  }
   __syncthreads();
 
-  const int t = threadIdx.x, ch = t & 31;
   const int nparts = N / SSQ_COLS;
+  if (m0 + t < M) ssq[static_cast<int64_t>(m0 + t) * nparts + tn] = halves[t] + halves[256 + t];
+  const int ch = t & 31;
+#pragma unroll 4
   for (int it = 0; it < BM / 8; ++it) {
     const int row = it * 8 + (t >> 5);
-    const uint4 v = image_chunk(lds, row, ch);
-    const float s = halfwave_sum(chunk_ssq(v));
     const int gm = m0 + row;
-    if (gm < M) {
-      *reinterpret_cast<uint4*>(X + static_cast<int64_t>(gm) * ldx + n0 + ch * 8) = v;
-      if (ch == 0) ssq[static_cast<int64_t>(gm) * nparts + tn] = s;
-    }
+    if (gm < M) *reinterpret_cast<uint4*>(X + static_cast<int64_t>(gm) * ldx + n0 + ch * 8) = image_chunk(lds, row, ch);
   }
 }
 
@@ -270,96 +305,125 @@ struct KvArgs {
   int64_t head_stride, row_stride, slot0;
 };
 
-// k_norm of one chunk's 8 values given the head's inverse RMS (code/kva/ops.py:14-25 per head).
-__device__ __forceinline__ void knorm_chunk(float (&f)[8], float rinv, const uint16_t* kw, int kind, int j0) {
+// k_norm of one chunk's 8 values given the head's inverse RMS (code/kva/ops.py:14-25 per head), with
+// the reference's roundings: bf16(w * bf16(x r)) (rms_norm) or bf16(x r (1 + w)) (rms_norm_zc).
+__device__ __forceinline__ void knorm_chunk(float (&f)[8], float rinv, const uint4& kw, int kind) {
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float w = bf2f(kw[j0 + e]);
-    f[e] = kind == 0 ? bf2f(f2bf(w * bf2f(f2bf(f[e] * rinv)))) : bf2f(f2bf(f[e] * rinv * (1.0f + w)));
+  for (int e = 0; e < 8; e += 2) {
+    const float w0 = bf2f(lane_of(kw, e)), w1 = bf2f(lane_of(kw, e + 1));
+    uint32_t p;
+    if (kind == 0) {
+      const uint32_t n = bf16_pair(f[e] * rinv, f[e + 1] * rinv);
+      p = bf16_pair(w0 * bf_lo(n), w1 * bf_hi(n));
+    } else {
+      p = bf16_pair(f[e] * rinv * (1.0f + w0), f[e + 1] * rinv * (1.0f + w1));
+    }
+    f[e] = bf_lo(p);
+    f[e + 1] = bf_hi(p);
   }
 }
 
 __global__ __launch_bounds__(NTHR) void k_norm_kv(const uint16_t* __restrict__ Xin, int64_t ldx,
                                                   const uint16_t* __restrict__ W, int M, int N, int K,
                                                   KvArgs a) {
-  __shared__ uint4 lds[LDS_U4];
+  __shared__ uint4 lds[LDS_ALL_U4];
+  float* rsc = reinterpret_cast<float*>(lds + LDS_U4);           // [256] row norm scales
   const int tiles_n = N / BN;
   int tm, tn;
   tile_coords(xcd_tile(blockIdx.x, gridDim.x), (M + BM - 1) / BM, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
+  row_scales(a.ssq, a.nparts, a.h, a.eps, M, m0, rsc);
   f32x16 acc[4][4];
   mainloop(Xin, ldx, W, K, M, K, m0, n0, lds, acc);
 
   // Input RMSNorm: the gain is folded into W, so each row is scaled by 1 / sqrt(mean(x^2) + eps).
   const int lane = threadIdx.x & 63, wm = threadIdx.x >> 7;
-  float rs[4];
+  float rs[4], unused[4];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    const int gm = m0 + wm * 128 + mt * 32 + (lane & 31);
-    float s = 0.f;
-    if (gm < M) {
-      const float* p = a.ssq + static_cast<int64_t>(gm) * a.nparts;
-      for (int q = 0; q < a.nparts; ++q) s += p[q];
-    }
-    rs[mt] = 1.0f / sqrtf(s / a.h + a.eps);
-  }
-  stage_tile(lds, acc, [&](int mt, int, int, int, float v) { return v * rs[mt]; });
+  for (int mt = 0; mt < 4; ++mt) rs[mt] = rsc[wm * 128 + mt * 32 + (lane & 31)];
+  stage_tile<false>(lds, acc, [&](int mt, int, int, int, float v) { return v * rs[mt]; }, unused);
   __syncthreads();
 
   const int t = threadIdx.x, ch = t & 31;
   const int d = a.d, kw = a.hkv * a.d, rot = a.rot, half = a.rot >> 1;
   const int group = d >> 3;                       // chunks per head: a power of two <= 32
+  const int col = n0 + ch * 8;
+  const bool is_k = col < kw;
+  const int cc = is_k ? col : col - kw;
+  const int head = cc / d, j0 = cc - head * d;
+  uint16_t* const dst0 = (is_k ? a.kbuf : a.vbuf) + head * a.head_stride + j0;
+  // this lane's k_norm gains, its RoPE partner chunk and table offsets (the same for every row)
+  const bool norm = is_k && a.knorm != nullptr;
+  const bool rope = is_k && j0 < rot;
+  const int pj0 = j0 < half ? j0 + half : j0 - half;
+  const int fi0 = j0 < half ? j0 : j0 - half;       // table index of the chunk's first element
+  uint4 kn = make_uint4(0u, 0u, 0u, 0u), kn_p = kn;
+  if (norm) {
+    kn = *reinterpret_cast<const uint4*>(a.knorm + j0);
+    if (rope && half >= 8) kn_p = *reinterpret_cast<const uint4*>(a.knorm + pj0);
+  }
   for (int it = 0; it < BM / 8; ++it) {
     const int row = it * 8 + (t >> 5);
     const int gm = m0 + row;
-    const int col = n0 + ch * 8;
-    const bool is_k = col < kw;
-    const int cc = is_k ? col : col - kw;
-    const int head = cc / d, j0 = cc - head * d;
     const uint4 v = image_chunk(lds, row, ch);
+    float ss = 0.f;
+    if (a.knorm) {                                   // per-head sum of squares; uniform branch
+      ss = chunk_ssq(v);
+      for (int o = 1; o < group; o <<= 1) ss += __shfl_xor(ss, o, 64);
+    }
+    if (gm >= M) continue;
+    uint16_t* dst = dst0 + (a.slot0 + gm) * a.row_stride;
+    if (!is_k || (!norm && !rope)) {
+      *reinterpret_cast<uint4*>(dst) = v;
+      continue;
+    }
     float f[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) f[e] = bf2f(lane_of(v, e));
-    // Per-head sum of squares for k_norm: every lane joins the shuffles (head groups never straddle
-    // the K / V boundary, so V lanes only ever combine with V lanes).
-    float ss = chunk_ssq(v);
-    for (int o = 1; o < group; o <<= 1) ss += __shfl_xor(ss, o, 64);
-    if (gm >= M) continue;
-    const int64_t slot = a.slot0 + gm;
-    if (!is_k) {
-      *reinterpret_cast<uint4*>(a.vbuf + head * a.head_stride + slot * a.row_stride + j0) = v;
-      continue;
-    }
     const float rinv = 1.0f / sqrtf(ss / static_cast<float>(d) + a.eps);
-    if (a.knorm) knorm_chunk(f, rinv, a.knorm, a.knorm_kind, j0);
-    uint16_t out[8];
-    if (j0 >= rot) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) out[e] = f2bf(f[e]);
+    if (norm) knorm_chunk(f, rinv, kn, a.knorm_kind);
+    uint4 o;
+    if (!rope) {
+      o = make_uint4(bf16_pair(f[0], f[1]), bf16_pair(f[2], f[3]), bf16_pair(f[4], f[5]), bf16_pair(f[6], f[7]));
     } else {
       float pf[8];                                // rotate_half partner values of this chunk
       if (half >= 8) {
-        const int pj0 = j0 < half ? j0 + half : j0 - half;
         const uint4 pv = image_chunk(lds, row, ch + (pj0 - j0) / 8);
 #pragma unroll
         for (int e = 0; e < 8; ++e) pf[e] = bf2f(lane_of(pv, e));
-        if (a.knorm) knorm_chunk(pf, rinv, a.knorm, a.knorm_kind, pj0);
+        if (norm) knorm_chunk(pf, rinv, kn_p, a.knorm_kind);
       } else {                                    // half == 4: the partner is in the same chunk
 #pragma unroll
         for (int e = 0; e < 8; ++e) pf[e] = f[e ^ 4];
       }
       const uint16_t* cs = a.cs + static_cast<int64_t>(gm) * rot;
+      float c[8], sn[8];
+      if (half >= 8) {                            // 8 consecutive table entries of each half
+        const uint4 cv = *reinterpret_cast<const uint4*>(cs + fi0);
+        const uint4 sv = *reinterpret_cast<const uint4*>(cs + half + fi0);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          c[e] = bf2f(lane_of(cv, e));
+          sn[e] = bf2f(lane_of(sv, e));
+        }
+      } else {                                    // rot == 8: entries 0..3 serve both halves of the chunk
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          c[e] = bf2f(cs[e & 3]);
+          sn[e] = bf2f(cs[4 + (e & 3)]);
+        }
+      }
+      // x cos + rotate_half(x) sin with each product rounded to bf16, then the sum (ops.py:66-77)
+      float y[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int j = j0 + e;
-        const int fi = j < half ? j : j - half;
-        const float c = bf2f(cs[fi]), s = bf2f(cs[half + fi]);
-        const float rh = j < half ? -pf[e] : pf[e];
-        out[e] = f2bf(bf2f(f2bf(f[e] * c)) + bf2f(f2bf(rh * s)));
+        const float rh = j0 + e < half ? -pf[e] : pf[e];
+        const uint32_t pr = bf16_pair(f[e] * c[e], rh * sn[e]);
+        y[e] = bf_lo(pr) + bf_hi(pr);
       }
+      o = make_uint4(bf16_pair(y[0], y[1]), bf16_pair(y[2], y[3]), bf16_pair(y[4], y[5]), bf16_pair(y[6], y[7]));
     }
-    *reinterpret_cast<uint4*>(a.kbuf + head * a.head_stride + slot * a.row_stride + j0) =
-        make_uint4(pack2(out[0], out[1]), pack2(out[2], out[3]), pack2(out[4], out[5]), pack2(out[6], out[7]));
+    *reinterpret_cast<uint4*>(dst) = o;
   }
 }
 
@@ -370,29 +434,23 @@ __global__ __launch_bounds__(NTHR) void k_norm_linear(const uint16_t* __restrict
                                                       const uint16_t* __restrict__ W, int M, int N, int K,
                                                       const float* __restrict__ ssq, float eps,
                                                       uint16_t* __restrict__ out, int64_t ldo) {
-  __shared__ uint4 lds[LDS_U4];
+  __shared__ uint4 lds[LDS_ALL_U4];
+  float* rsc = reinterpret_cast<float*>(lds + LDS_U4);
   const int tiles_n = N / BN;
   int tm, tn;
   tile_coords(xcd_tile(blockIdx.x, gridDim.x), (M + BM - 1) / BM, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
+  row_scales(ssq, K / SSQ_COLS, static_cast<float>(K), eps, M, m0, rsc);
   f32x16 acc[4][4];
   mainloop(Xin, ldx, W, K, M, K, m0, n0, lds, acc);
   const int lane = threadIdx.x & 63, wm = threadIdx.x >> 7;
-  const int nparts = K / SSQ_COLS;
-  float rs[4];
+  float rs[4], unused[4];
 #pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    const int gm = m0 + wm * 128 + mt * 32 + (lane & 31);
-    float s = 0.f;
-    if (gm < M) {
-      const float* p = ssq + static_cast<int64_t>(gm) * nparts;
-      for (int q = 0; q < nparts; ++q) s += p[q];
-    }
-    rs[mt] = 1.0f / sqrtf(s / static_cast<float>(K) + eps);
-  }
-  stage_tile(lds, acc, [&](int mt, int, int, int, float v) { return v * rs[mt]; });
+  for (int mt = 0; mt < 4; ++mt) rs[mt] = rsc[wm * 128 + mt * 32 + (lane & 31)];
+  stage_tile<false>(lds, acc, [&](int mt, int, int, int, float v) { return v * rs[mt]; }, unused);
   __syncthreads();
   const int t = threadIdx.x, ch = t & 31;
+#pragma unroll 4
   for (int it = 0; it < BM / 8; ++it) {
     const int row = it * 8 + (t >> 5);
     const int gm = m0 + row;
@@ -454,8 +512,8 @@ extern "C" int rf_map_apply(const uint16_t* b, int64_t ldb, const uint16_t* w, c
                 (long long)h_in, (long long)h_out);
   if (ldb < h_in || ldx < h_out || ldb % 8 || ldx % 8 || ldb > (1 << 21) || h_in > (1 << 21))
     return fail(RF_EINVAL_SHAPE, "rf_map_apply: row strides ldb %lld / ldx %lld", (long long)ldb, (long long)ldx);
-  if (!aligned16(b) || !aligned16(w) || !aligned16(x) || (c && (reinterpret_cast<uintptr_t>(c) & 7u)))
-    return fail(RF_EINVAL_SHAPE, "rf_map_apply: pointers must be 16-byte aligned (bias 8-byte)");
+  if (!aligned16(b) || !aligned16(w) || !aligned16(x) || (c && !aligned16(c)))
+    return fail(RF_EINVAL_SHAPE, "rf_map_apply: pointers must be 16-byte aligned");
   if (P == 0) return RF_OK;
   hipLaunchKernelGGL(k_map_apply, dim3(grid_of(P, h_out)), dim3(NTHR), 0, stream, b, ldb, w, c, x, ldx, ssq,
                      static_cast<int>(P), static_cast<int>(h_out), static_cast<int>(h_in));

@@ -27,19 +27,38 @@ int check_launch(const char* what) {
 
 namespace {
 
-// One wave per row: lanes 0-31 take group 2q, lanes 32-63 group 2q + 1 of the row's 256-column groups.
+// One wave per row. The sum of squares of each 256-column group is formed in the order the GEMM
+// epilogue forms it, so every producer of a row partial gives the same bits: four partials, one per
+// (w, h) in {0, 1}^2, each a sequential fma chain over the 64 columns w*128 + n*32 + 8g + 4h + e
+// (n, g, e = 0..3 in that order); then the two h partials of each w are added, then the two w sums.
+// Lane L takes group L / 4 (16 groups per pass) and partial q = L % 4 (w = q / 2, h = q % 2); with
+// dst it also copies its 64 columns (row_scatter).
 __device__ __forceinline__ void row_partials(const uint16_t* src, uint16_t* dst, float* ssq_row, int nparts,
                                              int lane) {
-  for (int q = 0; q < nparts; q += 2) {
-    const int part = q + (lane >> 5);
+  const int q = lane & 3, off_q = (q >> 1) * 128 + (q & 1) * 4;
+  for (int p0 = 0; p0 < nparts; p0 += 16) {
+    const int part = p0 + (lane >> 2);
     const bool ok = part < nparts;
-    const int64_t off = static_cast<int64_t>(part) * SSQ_COLS + (lane & 31) * 8;
-    const uint4 v = ok ? *reinterpret_cast<const uint4*>(src + off) : make_uint4(0u, 0u, 0u, 0u);
-    const float s = halfwave_sum(chunk_ssq(v));
+    float s = 0.f;
     if (ok) {
-      if (dst) *reinterpret_cast<uint4*>(dst + off) = v;
-      if ((lane & 31) == 0) ssq_row[part] = s;
+      const int64_t base = static_cast<int64_t>(part) * SSQ_COLS + off_q;
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int64_t o = base + n * 32 + 8 * g;
+          const uint2 v = *reinterpret_cast<const uint2*>(src + o);
+          if (dst) *reinterpret_cast<uint2*>(dst + o) = v;
+          const float f0 = bf2f(v.x & 0xffffu), f1 = bf2f(v.x >> 16), f2 = bf2f(v.y & 0xffffu), f3 = bf2f(v.y >> 16);
+          s = fmaf(f0, f0, s);
+          s = fmaf(f1, f1, s);
+          s = fmaf(f2, f2, s);
+          s = fmaf(f3, f3, s);
+        }
     }
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    if (ok && q == 0) ssq_row[part] = s;
   }
 }
 

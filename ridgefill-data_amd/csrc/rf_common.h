@@ -28,6 +28,20 @@ __device__ __forceinline__ uint16_t f2bf(float f) {
   return static_cast<uint16_t>(u >> 16);
 }
 
+typedef float rf_f32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 rf_bf16x2 __attribute__((ext_vector_type(2)));
+
+// Two floats rounded to bf16 (nearest even, as f2bf for every finite value) in one hardware conversion
+// (v_cvt_pk_bf16_f32), lo in bits 0-15, hi in bits 16-31. Both halves must carry values: with a half
+// the caller discards, the compiler feeds that operand an undefined register and then drops the masking
+// of the unused half, so single values go through f2bf.
+__device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(rf_f32x2{lo, hi}, rf_bf16x2));
+}
+
+__device__ __forceinline__ float bf_lo(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf_hi(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
+
 __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
   return static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
 }
