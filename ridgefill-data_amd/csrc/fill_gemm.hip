@@ -374,7 +374,7 @@ __global__ __launch_bounds__(NTHR) void k_norm_kv(const uint16_t* __restrict__ X
     if (gm >= M) continue;
     uint16_t* dst = dst0 + (a.slot0 + gm) * a.row_stride;
     if (!is_k || (!norm && !rope)) {
-      *reinterpret_cast<uint4*>(dst) = v;
+      st_stream16(dst, v);
       continue;
     }
     float f[8];
@@ -423,7 +423,7 @@ __global__ __launch_bounds__(NTHR) void k_norm_kv(const uint16_t* __restrict__ X
       }
       o = make_uint4(bf16_pair(y[0], y[1]), bf16_pair(y[2], y[3]), bf16_pair(y[4], y[5]), bf16_pair(y[6], y[7]));
     }
-    *reinterpret_cast<uint4*>(dst) = o;
+    st_stream16(dst, o);
   }
 }
 
@@ -542,7 +542,8 @@ extern "C" int rf_norm_kv_write(const uint16_t* x, int64_t ldx, const float* ssq
   if (slot_begin < 0 || slot_begin + P > cap)
     return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write: rows [%lld, %lld) exceed cache capacity %lld",
                 (long long)slot_begin, (long long)(slot_begin + P), (long long)cap);
-  if (!aligned16(x) || !aligned16(wkv) || !aligned16(kbuf) || !aligned16(vbuf))
+  if (!aligned16(x) || !aligned16(wkv) || !aligned16(kbuf) || !aligned16(vbuf) || !aligned16(cs) ||
+      (knorm && !aligned16(knorm)))
     return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write: pointers must be 16-byte aligned");
   if (!(eps >= 0.f)) return fail(RF_EINVAL_ARG, "rf_norm_kv_write: eps %g", static_cast<double>(eps));
   if (P == 0) return RF_OK;

@@ -5,6 +5,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <algorithm>
+
 #include "rf_common.h"
 
 namespace rf {
@@ -108,14 +110,14 @@ __global__ __launch_bounds__(256) void k_rope_table(const int64_t* __restrict__ 
   cs[row * 2 * half + half + f] = f2bf(sinf(ang));
 }
 
-// One thread per 16-byte chunk: chunks [0, m hkv d/8) are K, the next as many are V.
-__global__ __launch_bounds__(256) void k_rope_kv(const uint16_t* __restrict__ k, int64_t ld_k,
-                                                 const uint16_t* __restrict__ v, int64_t ld_v, int64_t m, int hkv,
-                                                 int d, const uint16_t* __restrict__ cs, int rot,
-                                                 uint16_t* __restrict__ kbuf, uint16_t* __restrict__ vbuf,
-                                                 int64_t head_stride, int64_t row_stride, int64_t slot0) {
-  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
-  const int cpr = hkv * (d >> 3);                 // chunks per token row
+// One 16-byte chunk per iteration: chunks [0, m hkv d/8) are K, the next as many are V; the cache writes
+// are streaming (nontemporal) stores.
+__device__ __forceinline__ void one_chunk(int64_t i, const uint16_t* __restrict__ k, int64_t ld_k,
+                                          const uint16_t* __restrict__ v, int64_t ld_v, int64_t m, int hkv, int d,
+                                          const uint16_t* __restrict__ cs, int rot, uint16_t* __restrict__ kbuf,
+                                          uint16_t* __restrict__ vbuf, int64_t head_stride, int64_t row_stride,
+                                          int64_t slot0) {
+  const int cpr = hkv * (d >> 3);
   const int64_t per = m * cpr;
   if (i >= 2 * per) return;
   const bool is_k = i < per;
@@ -126,37 +128,61 @@ __global__ __launch_bounds__(256) void k_rope_kv(const uint16_t* __restrict__ k,
   const int j0 = (rem - head * (d >> 3)) * 8;
   uint16_t* dst = (is_k ? kbuf : vbuf) + head * head_stride + (slot0 + tok) * row_stride + j0;
   if (!is_k) {
-    *reinterpret_cast<uint4*>(dst) = *reinterpret_cast<const uint4*>(v + tok * ld_v + head * d + j0);
+    st_stream16(dst, *reinterpret_cast<const uint4*>(v + tok * ld_v + head * d + j0));
     return;
   }
   const uint16_t* src = k + tok * ld_k + head * d;
   const uint4 x = *reinterpret_cast<const uint4*>(src + j0);
   if (j0 >= rot) {
-    *reinterpret_cast<uint4*>(dst) = x;
+    st_stream16(dst, x);
     return;
   }
   const int half = rot >> 1;
-  float f[8], pf[8];
+  float f[8], pf[8], co[8], sn[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) f[e] = bf2f(lane_of(x, e));
-  if (half >= 8) {
-    const uint4 p = *reinterpret_cast<const uint4*>(src + (j0 < half ? j0 + half : j0 - half));
-#pragma unroll
-    for (int e = 0; e < 8; ++e) pf[e] = bf2f(lane_of(p, e));
-  } else {
-#pragma unroll
-    for (int e = 0; e < 8; ++e) pf[e] = f[e ^ 4];
-  }
   const uint16_t* t = cs + tok * rot;
-  uint16_t o[8];
+  if (half >= 8) {
+    const bool lo = j0 < half;
+    const uint4 p = *reinterpret_cast<const uint4*>(src + (lo ? j0 + half : j0 - half));
+    const int fi0 = lo ? j0 : j0 - half;            // 8 consecutive entries of each half of the table
+    const uint4 cv = *reinterpret_cast<const uint4*>(t + fi0);
+    const uint4 sv = *reinterpret_cast<const uint4*>(t + half + fi0);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      pf[e] = bf2f(lane_of(p, e));
+      co[e] = bf2f(lane_of(cv, e));
+      sn[e] = bf2f(lane_of(sv, e));
+    }
+  } else {                                          // rot == 8: one chunk holds both halves
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      pf[e] = f[e ^ 4];
+      co[e] = bf2f(t[e & 3]);
+      sn[e] = bf2f(t[4 + (e & 3)]);
+    }
+  }
+  // x cos + rotate_half(x) sin with each product rounded to bf16, then the sum (code/kva/ops.py:66-77)
+  float y[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const int j = j0 + e;
-    const int fi = j < half ? j : j - half;
-    const float rh = j < half ? -pf[e] : pf[e];
-    o[e] = f2bf(bf2f(f2bf(f[e] * bf2f(t[fi]))) + bf2f(f2bf(rh * bf2f(t[half + fi]))));
+    const float rh = j0 + e < half ? -pf[e] : pf[e];
+    const uint32_t pr = bf16_pair(f[e] * co[e], rh * sn[e]);
+    y[e] = bf_lo(pr) + bf_hi(pr);
   }
-  *reinterpret_cast<uint4*>(dst) = make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
+  st_stream16(dst, make_uint4(bf16_pair(y[0], y[1]), bf16_pair(y[2], y[3]), bf16_pair(y[4], y[5]), bf16_pair(y[6], y[7])));
+}
+
+// Grid-stride over the chunks (at most 8192 blocks of 256 threads).
+__global__ __launch_bounds__(256) void k_rope_kv(const uint16_t* __restrict__ k, int64_t ld_k,
+                                                 const uint16_t* __restrict__ v, int64_t ld_v, int64_t m, int hkv,
+                                                 int d, const uint16_t* __restrict__ cs, int rot,
+                                                 uint16_t* __restrict__ kbuf, uint16_t* __restrict__ vbuf,
+                                                 int64_t head_stride, int64_t row_stride, int64_t slot0) {
+  const int64_t n = 2 * m * hkv * (d >> 3);
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * 256;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x; i < n; i += stride)
+    one_chunk(i, k, ld_k, v, ld_v, m, hkv, d, cs, rot, kbuf, vbuf, head_stride, row_stride, slot0);
 }
 
 int blocks(int64_t n, int per) { return static_cast<int>((n + per - 1) / per); }
@@ -229,11 +255,11 @@ extern "C" int rf_rope_kv_write(const uint16_t* k, int64_t ld_k, const uint16_t*
   if (slot_begin < 0 || slot_begin + m > cap)
     return fail(RF_EINVAL_SHAPE, "rf_rope_kv_write: rows [%lld, %lld) exceed cache capacity %lld",
                 (long long)slot_begin, (long long)(slot_begin + m), (long long)cap);
-  if (!aligned16(k) || !aligned16(v) || !aligned16(kbuf) || !aligned16(vbuf))
+  if (!aligned16(k) || !aligned16(v) || !aligned16(kbuf) || !aligned16(vbuf) || !aligned16(cs))
     return fail(RF_EINVAL_SHAPE, "rf_rope_kv_write: pointers must be 16-byte aligned");
   if (m == 0) return RF_OK;
   const int64_t threads = 2 * m * hkv * (d / 8);
-  hipLaunchKernelGGL(k_rope_kv, dim3(blocks(threads, 256)), dim3(256), 0, stream, k, ld_k, v, ld_v, m, hkv, d, cs,
+  hipLaunchKernelGGL(k_rope_kv, dim3(std::min(blocks(threads, 256), 8192)), dim3(256), 0, stream, k, ld_k, v, ld_v, m, hkv, d, cs,
                      rot, kbuf, vbuf, head_stride, row_stride, slot_begin);
   return check_launch("rf_rope_kv_write");
 }

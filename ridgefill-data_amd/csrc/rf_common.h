@@ -42,6 +42,13 @@ __device__ __forceinline__ uint32_t bf16_pair(float lo, float hi) {
 __device__ __forceinline__ float bf_lo(uint32_t p) { return __uint_as_float(p << 16); }
 __device__ __forceinline__ float bf_hi(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
 
+typedef uint32_t rf_u32x4 __attribute__((ext_vector_type(4)));
+
+// A 16-byte streaming store (nontemporal: data written once and not re-read by this kernel).
+__device__ __forceinline__ void st_stream16(void* p, const uint4& v) {
+  __builtin_nontemporal_store(rf_u32x4{v.x, v.y, v.z, v.w}, reinterpret_cast<rf_u32x4*>(p));
+}
+
 __device__ __forceinline__ uint32_t pack2(uint16_t lo, uint16_t hi) {
   return static_cast<uint32_t>(lo) | (static_cast<uint32_t>(hi) << 16);
 }
