@@ -189,8 +189,7 @@ def fit_bench(dev, chunks=2, rows=65536, d=4096, targets=16, lams=(1e-4, 1e-3, 1
     flop = 2.0 * chunks * rows * d * d * (1 + targets)
     t0 = time.perf_counter()
     fit = ridge.RidgeFit(stats.state(device=dev), device=dev)
-    for i in range(targets):
-        fit.layer(i, lams)
+    fit.layers(range(targets), lams)
     torch.cuda.synchronize()
     t_solve = time.perf_counter() - t0
     return {"workload": f"ridge fit: d {d}, {targets} targets, {chunks} x {rows}-row chunks of 32 (timed sample)",

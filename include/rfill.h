@@ -127,8 +127,8 @@ int rf_gdn_workspace_bytes(int64_t rows, int nk, int nv, int dk, int dv, size_t*
 int rf_transpose(const uint16_t* src, int64_t ld_src, int64_t rows, int64_t cols, uint16_t* dst, int64_t ld_dst,
                  float* partial, hipStream_t stream);
 
-/* sums[c] += sum_j partial[j, c] (j in order, fp64): the sum(0) of a sample block
- * (RidgeStats' sx / sy, code/kva/ridge.py:46, :61). */
+/* sums[c] += sum_j partial[j, c] in fp64 and a fixed order (16 interleaved runs over j, then a pairwise
+ * fold; the same bits every run): the sum(0) of a sample block (RidgeStats' sx / sy, code/kva/ridge.py:46, :61). */
 int rf_colsum_fold(const float* partial, int64_t ntiles, int64_t cols, double* sums, hipStream_t stream);
 
 /* Gram / cross accumulation C[M, N] += A[M, K] B[N, K]^T: bf16 products summed in fp32 on MFMA over

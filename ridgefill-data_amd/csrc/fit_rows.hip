@@ -52,14 +52,24 @@ __global__ __launch_bounds__(256) void k_transpose(const uint16_t* __restrict__ 
   }
 }
 
-// sums[c] += sum over tiles j (in order) of partial[j, c], in fp64.
+// sums[c] += sum over tiles j of partial[j, c], in fp64, in a fixed order: 16 threads per column, thread i
+// sums tiles i, i + 16, i + 32, ... in order, then the 16 partial sums are added pairwise (i with i + 8,
+// then + 4, + 2, + 1). A block of 256 threads covers 16 consecutive columns.
 __global__ __launch_bounds__(256) void k_colsum_fold(const float* __restrict__ partial, int64_t ntiles, int cols,
                                                      double* __restrict__ sums) {
-  const int c = blockIdx.x * 256 + threadIdx.x;
-  if (c >= cols) return;
+  __shared__ double red[16][17];
+  const int t = threadIdx.x, cl = t & 15, i = t >> 4;
+  const int c = blockIdx.x * 16 + cl;
   double s = 0.0;
-  for (int64_t j = 0; j < ntiles; ++j) s += static_cast<double>(partial[j * cols + c]);
-  sums[c] += s;
+  if (c < cols)
+    for (int64_t j = i; j < ntiles; j += 16) s += static_cast<double>(partial[j * cols + c]);
+  red[i][cl] = s;
+  __syncthreads();
+  for (int h = 8; h >= 1; h >>= 1) {
+    if (i < h) red[i][cl] += red[i + h][cl];
+    __syncthreads();
+  }
+  if (i == 0 && c < cols) sums[c] += red[0][cl];
 }
 
 }  // namespace
@@ -86,7 +96,7 @@ extern "C" int rf_colsum_fold(const float* partial, int64_t ntiles, int64_t cols
   if (!partial || !sums) return fail(RF_EINVAL_ARG, "rf_colsum_fold: null pointer");
   if (ntiles < 0 || cols <= 0 || cols > (1 << 30)) return fail(RF_EINVAL_SHAPE, "rf_colsum_fold: shape");
   if (ntiles == 0) return RF_OK;
-  hipLaunchKernelGGL(k_colsum_fold, dim3(static_cast<unsigned>((cols + 255) / 256)), dim3(256), 0, stream, partial,
+  hipLaunchKernelGGL(k_colsum_fold, dim3(static_cast<unsigned>((cols + 15) / 16)), dim3(256), 0, stream, partial,
                      ntiles, static_cast<int>(cols), sums);
   return check_launch("rf_colsum_fold");
 }

@@ -141,11 +141,22 @@ class RidgeFit:
 
     def layer(self, i, lams):
         """{lam: (weight [d_out, d_in] fp32, bias [d_out] fp32)} for layer i (F.linear layout)."""
-        cxy, mean_y = self.cross(i)
-        out = {}
+        return self.layers([i], lams)[i]
+
+    def layers(self, ids, lams):
+        """{i: {lam: (weight, bias)}} for every layer i in ids: the targets' cross statistics side by side,
+        so each lambda costs one factorisation and one pair of triangular solves for all of them."""
+        ids = list(ids)
+        cross = [self.cross(i) for i in ids]
+        cxy = torch.cat([c for c, _ in cross], 1)
+        out = {i: {} for i in ids}
         for lam in lams:
-            w = self.solve(cxy, lam)
-            out[lam] = (w.T.float().contiguous(), (mean_y - self.mean_x @ w).float())
+            w_all = self.solve(cxy, lam)
+            col = 0
+            for i, (c, mean_y) in zip(ids, cross):
+                w = w_all[:, col:col + c.shape[1]]
+                col += c.shape[1]
+                out[i][lam] = (w.T.float().contiguous(), (mean_y - self.mean_x @ w).float())
         return out
 
 
