@@ -93,6 +93,43 @@ int rf_rope_kv_write(const uint16_t* k, int64_t ld_k, const uint16_t* v, int64_t
                      uint16_t* kbuf, uint16_t* vbuf, int64_t head_stride, int64_t row_stride,
                      int64_t slot_begin, int64_t cap, hipStream_t stream);
 
+/* ---- the exact rows' full layer (Model.layer_rows, code/kva/model.py:259-276) ---- */
+
+/* out[j] = x[rows[j]] for j < nrows, bit-exact, and out's row sum-of-squares partials ssq [nrows, H / 256]
+ * (the rows' input RMSNorm statistics). The gather of h[rows] in layer_rows (code/kva/model.py:270); a row
+ * outside [0, P) gives a zero row. rows: int64 on the device. */
+int rf_row_gather(const uint16_t* x, int64_t ldx, int64_t P, int64_t H, const int64_t* rows, int64_t nrows,
+                  uint16_t* out, int64_t ldo, float* ssq, hipStream_t stream);
+
+/* Query projection of rows x [rows, H] at positions pos [rows] (int64, device): input RMSNorm (gain folded
+ * into wq, rf_fold_norm; row statistics ssq), q = xn wq^T [hq d], optional per-head q_norm (qnorm [d],
+ * kind 0 rms_norm, 1 rms_norm_zc), RoPE with table row pos[j] of cs (rf_rope_table of positions 0..).
+ * Writes q [rows, hq d] (row stride ldq). Replaces Llama.queries / Qwen3 q_norm (code/kva/model.py:241-245,
+ * :347-352) on the normed rows. Needs H % 256 == 0, hq d % 256 == 0, and the rotary limits of
+ * rf_norm_kv_write. */
+int rf_norm_q(const uint16_t* x, int64_t ldx, const float* ssq, int64_t rows, int64_t H, float eps,
+              const uint16_t* wq, int hq, int d, const uint16_t* qnorm, int qnorm_kind, const uint16_t* cs, int rot,
+              const int64_t* pos, uint16_t* q, int64_t ldq, hipStream_t stream);
+
+/* Causal attention of nq query rows q [nq, hq d] at sorted positions qpos [nq] (int64, device; each
+ * < cache_rows) over the cache kbuf / vbuf [hkv, cap, d] (element strides head_stride / row_stride): query
+ * j sees keys 0 .. qpos[j]; scores in fp32 scaled by `scale`, softmax in fp32, probabilities as bf16 into
+ * the second product. Writes out [nq, hq d] (row stride ldo). Replaces ops.attend_at / attend_rows
+ * (code/kva/ops.py:131-170) in layer_rows. Needs d == 128 and hq / hkv dividing 64. */
+int rf_attend_rows(const uint16_t* q, int64_t ldq, const int64_t* qpos, int64_t nq, int hq, int d,
+                   const uint16_t* kbuf, const uint16_t* vbuf, int hkv, int64_t head_stride, int64_t row_stride,
+                   int64_t cache_rows, float scale, uint16_t* out, int64_t ldo, hipStream_t stream);
+
+/* out = bf16(x + y) row by row (rows x H) and out's row sum-of-squares partials ssq [rows, H / 256]: the
+ * residual adds of layer_rows (code/kva/model.py:274, Model.mlp :114). out may alias x. */
+int rf_residual_add(const uint16_t* x, int64_t ldx, const uint16_t* y, int64_t ldy, uint16_t* out, int64_t ldo,
+                    float* ssq, int64_t rows, int64_t H, hipStream_t stream);
+
+/* SwiGLU: act[j, c] = bf16(bf16(silu(gu[j, c])) * gu[j, I + c]) for c < I (gate columns then up columns of
+ * one in-projection). Model.mlp's F.silu(gate) * up (code/kva/model.py:112-119). */
+int rf_silu_mul(const uint16_t* gu, int64_t ldg, int64_t rows, int64_t I, uint16_t* act, int64_t lda,
+                hipStream_t stream);
+
 /* Fused RMSNorm + linear: out[P, N] = bf16(r_row * (x w^T)) with r_row = 1 / sqrt(mean(x^2) + eps) from
  * the row partials ssq [P, H / 256] and the norm gain folded into w [N, H] (rf_fold_norm). The Gated
  * DeltaNet in-projections of a fill (code/kva/model.py:448-450 after in_norm, :513). Needs

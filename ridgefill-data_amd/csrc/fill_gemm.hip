@@ -303,6 +303,7 @@ struct KvArgs {
   uint16_t* kbuf;
   uint16_t* vbuf;
   int64_t head_stride, row_stride, slot0;
+  const int64_t* pos;   // RoPE table row of input row j: pos[j] (null: j)
 };
 
 // k_norm of one chunk's 8 values given the head's inverse RMS (code/kva/ops.py:14-25 per head), with
@@ -396,7 +397,7 @@ __global__ __launch_bounds__(NTHR) void k_norm_kv(const uint16_t* __restrict__ X
 #pragma unroll
         for (int e = 0; e < 8; ++e) pf[e] = f[e ^ 4];
       }
-      const uint16_t* cs = a.cs + static_cast<int64_t>(gm) * rot;
+      const uint16_t* cs = a.cs + (a.pos ? a.pos[gm] : static_cast<int64_t>(gm)) * rot;
       float c[8], sn[8];
       if (half >= 8) {                            // 8 consecutive table entries of each half
         const uint4 cv = *reinterpret_cast<const uint4*>(cs + fi0);
@@ -548,11 +549,39 @@ extern "C" int rf_norm_kv_write(const uint16_t* x, int64_t ldx, const float* ssq
   if (!(eps >= 0.f)) return fail(RF_EINVAL_ARG, "rf_norm_kv_write: eps %g", static_cast<double>(eps));
   if (P == 0) return RF_OK;
   KvArgs a{ssq, static_cast<int>(H / SSQ_COLS), static_cast<float>(H), eps, hkv, d, knorm, knorm_kind, cs, rot,
-           kbuf, vbuf, head_stride, row_stride, slot_begin};
+           kbuf, vbuf, head_stride, row_stride, slot_begin, nullptr};
   const int64_t N = 2ll * hkv * d;
   hipLaunchKernelGGL(k_norm_kv, dim3(grid_of(P, N)), dim3(NTHR), 0, stream, x, ldx, wkv, static_cast<int>(P),
                      static_cast<int>(N), static_cast<int>(H), a);
   return check_launch("rf_norm_kv_write");
+}
+
+extern "C" int rf_norm_q(const uint16_t* x, int64_t ldx, const float* ssq, int64_t rows, int64_t H, float eps,
+                         const uint16_t* wq, int hq, int d, const uint16_t* qnorm, int qnorm_kind, const uint16_t* cs,
+                         int rot, const int64_t* pos, uint16_t* q, int64_t ldq, hipStream_t stream) {
+  if (!x || !ssq || !wq || !cs || !pos || !q) return fail(RF_EINVAL_ARG, "rf_norm_q: null pointer");
+  if (rows < 0 || rows > (1ll << 30)) return fail(RF_EINVAL_SHAPE, "rf_norm_q: rows = %lld out of range", (long long)rows);
+  if (H <= 0 || H % BK || H % SSQ_COLS) return fail(RF_EINVAL_SHAPE, "rf_norm_q: H = %lld must be a multiple of 256",
+                                                   (long long)H);
+  if (d <= 0 || d % 8 || 256 % d || hq <= 0 || (static_cast<int64_t>(hq) * d) % BN)
+    return fail(RF_EUNSUPPORTED, "rf_norm_q: head_dim %d / heads %d (need 256 %% d == 0, d %% 8 == 0, hq d %% 256 == 0)",
+                d, hq);
+  if (rot <= 0 || rot > d || rot % 2 || ((rot / 2) % 8 && rot / 2 != 4))
+    return fail(RF_EUNSUPPORTED, "rf_norm_q: rotary dims %d of head_dim %d", rot, d);
+  if (qnorm && qnorm_kind != 0 && qnorm_kind != 1) return fail(RF_EINVAL_ARG, "rf_norm_q: qnorm_kind %d", qnorm_kind);
+  if (ldx < H || ldx % 8 || ldx > (1 << 21) || ldq < static_cast<int64_t>(hq) * d || ldq % 8)
+    return fail(RF_EINVAL_SHAPE, "rf_norm_q: strides (ldx %lld, ldq %lld)", (long long)ldx, (long long)ldq);
+  if (!aligned16(x) || !aligned16(wq) || !aligned16(q) || !aligned16(cs) || (qnorm && !aligned16(qnorm)))
+    return fail(RF_EINVAL_SHAPE, "rf_norm_q: pointers must be 16-byte aligned");
+  if (!(eps >= 0.f)) return fail(RF_EINVAL_ARG, "rf_norm_q: eps %g", static_cast<double>(eps));
+  if (rows == 0) return RF_OK;
+  // every output column is a "K" column: hkv = hq heads, row j at q + j ldq, head h at + h d
+  KvArgs a{ssq, static_cast<int>(H / SSQ_COLS), static_cast<float>(H), eps, hq, d, qnorm, qnorm_kind, cs, rot,
+           q, q, static_cast<int64_t>(d), ldq, 0, pos};
+  const int64_t N = static_cast<int64_t>(hq) * d;
+  hipLaunchKernelGGL(k_norm_kv, dim3(grid_of(rows, N)), dim3(NTHR), 0, stream, x, ldx, wq, static_cast<int>(rows),
+                     static_cast<int>(N), static_cast<int>(H), a);
+  return check_launch("rf_norm_q");
 }
 
 extern "C" int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t M,

@@ -29,46 +29,13 @@ int check_launch(const char* what) {
 
 namespace {
 
-// One wave per row. The sum of squares of each 256-column group is formed in the order the GEMM
-// epilogue forms it, so every producer of a row partial gives the same bits: four partials, one per
-// (w, h) in {0, 1}^2, each a sequential fma chain over the 64 columns w*128 + n*32 + 8g + 4h + e
-// (n, g, e = 0..3 in that order); then the two h partials of each w are added, then the two w sums.
-// Lane L takes group L / 4 (16 groups per pass) and partial q = L % 4 (w = q / 2, h = q % 2); with
-// dst it also copies its 64 columns (row_scatter).
-__device__ __forceinline__ void row_partials(const uint16_t* src, uint16_t* dst, float* ssq_row, int nparts,
-                                             int lane) {
-  const int q = lane & 3, off_q = (q >> 1) * 128 + (q & 1) * 4;
-  for (int p0 = 0; p0 < nparts; p0 += 16) {
-    const int part = p0 + (lane >> 2);
-    const bool ok = part < nparts;
-    float s = 0.f;
-    if (ok) {
-      const int64_t base = static_cast<int64_t>(part) * SSQ_COLS + off_q;
-#pragma unroll
-      for (int n = 0; n < 4; ++n)
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int64_t o = base + n * 32 + 8 * g;
-          const uint2 v = *reinterpret_cast<const uint2*>(src + o);
-          if (dst) *reinterpret_cast<uint2*>(dst + o) = v;
-          const float f0 = bf2f(v.x & 0xffffu), f1 = bf2f(v.x >> 16), f2 = bf2f(v.y & 0xffffu), f3 = bf2f(v.y >> 16);
-          s = fmaf(f0, f0, s);
-          s = fmaf(f1, f1, s);
-          s = fmaf(f2, f2, s);
-          s = fmaf(f3, f3, s);
-        }
-    }
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    if (ok && q == 0) ssq_row[part] = s;
-  }
-}
-
 __global__ __launch_bounds__(256) void k_row_ssq(const uint16_t* __restrict__ x, int64_t ldx, float* __restrict__ ssq,
                                                  int64_t P, int nparts) {
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= P) return;
-  row_partials(x + row * ldx, nullptr, ssq + row * nparts, nparts, threadIdx.x & 63);
+  const uint16_t* xr = x + row * ldx;
+  row_partials([&](int64_t o) { return *reinterpret_cast<const uint2*>(xr + o); }, ssq + row * nparts, nparts,
+               threadIdx.x & 63);
 }
 
 __global__ __launch_bounds__(256) void k_row_scatter(uint16_t* __restrict__ x, int64_t ldx, float* __restrict__ ssq,
@@ -78,7 +45,30 @@ __global__ __launch_bounds__(256) void k_row_scatter(uint16_t* __restrict__ x, i
   if (j >= nrows) return;
   const int64_t row = rows[j];
   if (row < 0 || row >= P) return;
-  row_partials(hr + j * ldhr, x + row * ldx, ssq + row * nparts, nparts, threadIdx.x & 63);
+  const uint16_t* src = hr + j * ldhr;
+  uint16_t* dst = x + row * ldx;
+  row_partials([&](int64_t o) {
+    const uint2 v = *reinterpret_cast<const uint2*>(src + o);
+    *reinterpret_cast<uint2*>(dst + o) = v;
+    return v;
+  }, ssq + row * nparts, nparts, threadIdx.x & 63);
+}
+
+// out[j] = x[rows[j]] for j < nrows (bit-exact) and out's row partials; a row outside [0, P) gives zeros.
+__global__ __launch_bounds__(256) void k_row_gather(const uint16_t* __restrict__ x, int64_t ldx, int64_t P,
+                                                    int nparts, const int64_t* __restrict__ rows, int64_t nrows,
+                                                    uint16_t* __restrict__ out, int64_t ldo, float* __restrict__ ssq) {
+  const int64_t j = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (j >= nrows) return;
+  const int64_t row = rows[j];
+  const bool ok = row >= 0 && row < P;
+  const uint16_t* src = x + (ok ? row : 0) * ldx;
+  uint16_t* dst = out + j * ldo;
+  row_partials([&](int64_t o) {
+    const uint2 v = ok ? *reinterpret_cast<const uint2*>(src + o) : make_uint2(0u, 0u);
+    *reinterpret_cast<uint2*>(dst + o) = v;
+    return v;
+  }, ssq + j * nparts, nparts, threadIdx.x & 63);
 }
 
 __global__ __launch_bounds__(256) void k_fold_norm(const uint16_t* __restrict__ w, const uint16_t* __restrict__ gain,
@@ -218,6 +208,19 @@ extern "C" int rf_row_scatter(uint16_t* x, int64_t ldx, float* ssq, int64_t P, i
   hipLaunchKernelGGL(k_row_scatter, dim3(blocks(nrows, 4)), dim3(256), 0, stream, x, ldx, ssq, P,
                      static_cast<int>(H / SSQ_COLS), rows, nrows, hr, ldhr);
   return check_launch("rf_row_scatter");
+}
+
+extern "C" int rf_row_gather(const uint16_t* x, int64_t ldx, int64_t P, int64_t H, const int64_t* rows, int64_t nrows,
+                             uint16_t* out, int64_t ldo, float* ssq, hipStream_t stream) {
+  if (!x || !rows || !out || !ssq) return fail(RF_EINVAL_ARG, "rf_row_gather: null pointer");
+  if (P < 0 || nrows < 0 || H <= 0 || H % SSQ_COLS || ldx < H || ldo < H || ldx % 4 || ldo % 4)
+    return fail(RF_EINVAL_SHAPE, "rf_row_gather: P %lld, H %lld (multiple of 256), strides", (long long)P, (long long)H);
+  if ((reinterpret_cast<uintptr_t>(x) & 7u) || (reinterpret_cast<uintptr_t>(out) & 7u))
+    return fail(RF_EINVAL_SHAPE, "rf_row_gather: 8-byte alignment");
+  if (nrows == 0) return RF_OK;
+  hipLaunchKernelGGL(k_row_gather, dim3(blocks(nrows, 4)), dim3(256), 0, stream, x, ldx, P, static_cast<int>(H / SSQ_COLS),
+                     rows, nrows, out, ldo, ssq);
+  return check_launch("rf_row_gather");
 }
 
 extern "C" int rf_fold_norm(const uint16_t* w, const uint16_t* gain, int kind, uint16_t* w_out, int64_t N, int64_t K,

@@ -77,4 +77,38 @@ __device__ __forceinline__ float halfwave_sum(float s) {
   return s;
 }
 
+// One wave per row. The sum of squares of each 256-column group is formed in the order the GEMM
+// epilogue forms it, so every producer of a row partial gives the same bits: four partials, one per
+// (w, h) in {0, 1}^2, each a sequential fma chain over the 64 columns w*128 + n*32 + 8g + 4h + e
+// (n, g, e = 0..3 in that order); then the two h partials of each w are added, then the two w sums.
+// Lane L takes group L / 4 (16 groups per pass) and partial q = L % 4 (w = q / 2, h = q % 2).
+// piece(o) returns the row's 4 bf16 values at column offset o (8 bytes); it may also store them
+// (the scatter's copy, the residual add's sum).
+template <class F>
+__device__ __forceinline__ void row_partials(F piece, float* ssq_row, int nparts, int lane) {
+  const int q = lane & 3, off_q = (q >> 1) * 128 + (q & 1) * 4;
+  for (int p0 = 0; p0 < nparts; p0 += 16) {
+    const int part = p0 + (lane >> 2);
+    const bool ok = part < nparts;
+    float s = 0.f;
+    if (ok) {
+      const int64_t base = static_cast<int64_t>(part) * SSQ_COLS + off_q;
+#pragma unroll
+      for (int n = 0; n < 4; ++n)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const uint2 v = piece(base + n * 32 + 8 * g);
+          const float f0 = bf2f(v.x & 0xffffu), f1 = bf2f(v.x >> 16), f2 = bf2f(v.y & 0xffffu), f3 = bf2f(v.y >> 16);
+          s = fmaf(f0, f0, s);
+          s = fmaf(f1, f1, s);
+          s = fmaf(f2, f2, s);
+          s = fmaf(f3, f3, s);
+        }
+    }
+    s += __shfl_xor(s, 1, 64);
+    s += __shfl_xor(s, 2, 64);
+    if (ok && q == 0) ssq_row[part] = s;
+  }
+}
+
 }  // namespace rf

@@ -4,9 +4,10 @@ fill loop of finish() (code/kva/kva.py:79-193, 392-454), with every fill step on
 fill_late() runs the hot path of finish() for one arm: for each late layer i >= split, the prefix rows
 [0, P) get x_i = W_i b + c_i (fill 'proj', one rf_map_apply that also yields x's RMSNorm statistics)
 or x_i = b (fill 'identity'), the exact rows R are scattered in bit-exactly (rf_row_scatter, the
-index_copy of kva.py:428-431), and the layer's cache is filled (rf_norm_kv_write). Two x / statistics
-buffers and one RoPE table serve all late layers; optionally layer i's cache write runs on a second
-stream beside layer i + 1's map apply (two_stream).
+index_copy of kva.py:428-431), the layer's cache is filled (rf_norm_kv_write) and, for exact rows, the
+layer's full computation runs on them (FillModel.layer_rows, kva.py:436-437) to give their next input.
+Two x / statistics buffers and one RoPE table serve all late layers; optionally layer i's cache work
+runs on a second stream beside layer i + 1's map apply (two_stream).
 """
 import json
 from dataclasses import dataclass, field
@@ -149,12 +150,17 @@ def serial(layers, produce, consume, device):
         consume(i, n % 2)
 
 
-def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap=False):
+def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap=False, row_inputs=None):
     """The late-layer fill of finish() for one arm: every late layer's cache filled from the prefix rows
-    [0, P) of h_split [N, H] (bf16, on the GPU). exact_rows: sorted prefix rows whose layer inputs are
-    given by hr (one [|R|, H] tensor for every layer, or {layer: tensor}) instead of the fill's x.
-    overlap: run each layer's cache write on a second stream beside the next layer's map apply
-    (two_stream; about 1% faster at the Llama-8B 32K shape). Returns (cache, P)."""
+    [0, P) of h_split [N, H] (bf16, on the GPU), with exact rows R (sorted prefix rows) whose inputs replace
+    the fill's x (code/kva/kva.py:392-454).
+
+    hr None (the reference's path): the rows enter the first late layer with their split-layer state
+    h_split[R]; each late layer fills its cache with them scattered in and runs its full layer on them
+    (layer_rows), whose output is their input to the next layer. hr given (one [|R|, H] tensor for every
+    layer, or {layer: tensor}): those inputs are scattered in and no full layer runs.
+    row_inputs (dict): receives the rows' input to every late layer. overlap: run each layer's cache work
+    on a second stream beside the next layer's map apply (two_stream). Returns (cache, P)."""
     n = h_split.shape[0]
     P = arm.prefix_len(n)
     cache = model.new_cache() if cache is None else cache
@@ -177,6 +183,8 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
     xbuf = [torch.empty(P, H, dtype=torch.bfloat16, device=dev) for _ in range(2)]
     sbuf = [torch.empty(P, ops.ssq_parts(H), dtype=torch.float32, device=dev) for _ in range(2)]
     base_ssq = ops.row_ssq(b) if arm.fill == "identity" and rows is None else None
+    computed = rows is not None and hr is None
+    state = {"hr": ops.row_gather(b, rows)[0] if computed else None}
     inputs = {}
 
     def produce(i, slot):
@@ -187,14 +195,22 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
         else:
             x = xbuf[slot].copy_(b)
             ssq = ops.row_ssq(x, sbuf[slot])
-        if rows is not None:
-            hri = hr[i] if isinstance(hr, dict) else hr
-            ops.row_scatter(x, ssq, rows, hri.to(dev, torch.bfloat16))
+        if rows is not None and not computed:
+            hri = (hr[i] if isinstance(hr, dict) else hr).to(dev, torch.bfloat16)
+            if row_inputs is not None:
+                row_inputs[i] = hri
+            ops.row_scatter(x, ssq, rows, hri)
         inputs[slot] = (x, ssq)
 
     def consume(i, slot):
         x, ssq = inputs[slot]
-        model.fill(i, x, pos, cache, ssq=ssq, cs=cs)
+        if computed:
+            if row_inputs is not None:
+                row_inputs[i] = state["hr"]
+            ops.row_scatter(x, ssq, rows, state["hr"])
+            state["hr"] = model.layer_rows(i, x, pos, rows, cache, ssq=ssq, cs=cs)
+        else:
+            model.fill(i, x, pos, cache, ssq=ssq, cs=cs)
 
     (two_stream if overlap else serial)(layers, produce, consume, dev)
     return cache, P

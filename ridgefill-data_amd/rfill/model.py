@@ -66,6 +66,8 @@ class FillModel:
         self.inv_freq = inv.to(self.device)
         self.knorm_kind = 1 if self.arch == "qwen3_5" else 0
         pre = "model.language_model." if "model.language_model.embed_tokens.weight" in tensors else "model."
+        self._src, self._pre = tensors, pre                # the full-layer weights are packed on first use
+        self.scale = self.head_dim ** -0.5
         want = range(self.n_layers) if layers is None else layers
         self.W = [None] * self.n_layers
         self._gdn_ws = None
@@ -196,6 +198,69 @@ class FillModel:
         if self._gdn_ws is None or self._gdn_ws.numel() < need or self._gdn_ws.device != device:
             self._gdn_ws = torch.empty(need, dtype=torch.uint8, device=device)
         return self._gdn_ws
+
+    def _pack_rows(self, i):
+        """Layer i's weights for the exact rows' full layer, packed on first use: the query projection with
+        the input norm gain folded in, q_norm, o_proj, [gate; up] with the post-attention norm gain folded in
+        (zero rows to a multiple of 256), down (zero columns to a multiple of 64)."""
+        w = self._layer(i)
+        if "wq" in w:
+            return w
+        if self.arch == "qwen3_5":
+            raise UnsupportedArchitecture("exact rows through Qwen3.5 layers (gated attention, GDN) are not "
+                                          "implemented by the kernels")
+        dev = lambda k: self._src[k].to(self.device, torch.bfloat16).contiguous()   # noqa: E731
+        p = f"{self._pre}layers.{i}."
+        a = p + "self_attn."
+        w["wq"] = ops.fold_norm(dev(a + "q_proj.weight"), w["ln1"], self.knorm_kind)
+        if self.arch == "qwen3":
+            w["q_norm"] = dev(a + "q_norm.weight")
+        w["wo"] = dev(a + "o_proj.weight")
+        gate, up = dev(p + "mlp.gate_proj.weight"), dev(p + "mlp.up_proj.weight")
+        inter = gate.shape[0]
+        gu = torch.cat((gate, up), 0)
+        pad = (-gu.shape[0]) % 256
+        if pad:
+            gu = torch.cat((gu, gu.new_zeros(pad, gu.shape[1])), 0)
+        w["wgu"] = ops.fold_norm(gu, dev(p + "post_attention_layernorm.weight"), 0)
+        down = dev(p + "mlp.down_proj.weight")
+        pad = (-inter) % 64
+        if pad:
+            down = torch.cat((down, down.new_zeros(down.shape[0], pad)), 1).contiguous()
+        w["wd"], w["inter"] = down, inter
+        return w
+
+    def layer_rows(self, i, x, pos, rows, cache, ssq=None, cs=None):
+        """Fill cache[i] from the inputs x [P, H] of rows at positions pos (an empty cache, as fill()) and
+        return the exact layer output of the rows x[rows] over that cache, [len(rows), H] bf16
+        (code/kva/model.py:259-276): the rows' queries attend over the filled keys up to their own
+        position, then o_proj, the residual, and the MLP with its residual. rows: sorted prefix rows."""
+        if self.layer_types[i] != "attn":
+            raise UnsupportedArchitecture("exact rows through GDN layers are not implemented by the kernels")
+        w = self._pack_rows(i)
+        c = cache[i]
+        if c.get("n", 0):
+            raise ValueError("layer_rows fills an empty cache (cache slot = position)")
+        if ssq is None:
+            ssq = ops.row_ssq(x)
+        if cs is None:
+            cs = self.rope_table(pos)
+        self.fill(i, x, pos, cache, ssq=ssq, cs=cs)
+        rows = torch.as_tensor(rows, dtype=torch.int64).to(x.device)
+        xr, sr = ops.row_gather(x, rows)
+        q = ops.norm_q(xr, sr, self.eps, w["wq"], self.n_heads, self.head_dim, w.get("q_norm"), self.knorm_kind, cs,
+                       rows)
+        o = ops.attend_rows(q, pos.to(x.device, torch.int64)[rows], c["kbuf"], c["vbuf"], c["n"], self.n_heads,
+                            self.scale)
+        a, _ = ops.map_apply(o, w["wo"], None)
+        h1, s1 = ops.residual_add(xr, a)
+        gu = ops.norm_linear(h1, s1, self.eps, w["wgu"])
+        inter = w["inter"]
+        act = torch.zeros(xr.shape[0], w["wd"].shape[1], dtype=torch.bfloat16, device=x.device)
+        ops.silu_mul(gu[:, :2 * inter], act[:, :inter])
+        dn, _ = ops.map_apply(act, w["wd"], None)
+        h2, _ = ops.residual_add(h1, dn)
+        return h2
 
     def fill_kv(self, i, k, v, pos, cache, cs=None):
         """Cache-only fill from pre-RoPE K and V [P, Hkv, d] (the reads() layout)."""

@@ -181,6 +181,92 @@ def norm_linear(x, ssq, eps, w, out=None):
     return out
 
 
+def row_gather(x, rows, out=None, ssq=None):
+    """out = x[rows] (bit-exact) and its row sum-of-squares partials; rows int64 on the device."""
+    _need(x, "x", torch.bfloat16, 2)
+    _need(rows, "rows", torch.int64, 1)
+    P, H = x.shape
+    n = rows.shape[0]
+    out = torch.empty(n, H, dtype=torch.bfloat16, device=x.device) if out is None else out
+    ssq = torch.empty(n, ssq_parts(H), dtype=torch.float32, device=x.device) if ssq is None else ssq
+    _need(out, "out", torch.bfloat16, 2)
+    _need(ssq, "ssq", torch.float32, 2)
+    if tuple(out.shape) != (n, H) or tuple(ssq.shape) != (n, H // SSQ_COLS) or not ssq.is_contiguous():
+        raise ValueError("row_gather: output shapes")
+    _lib.call("rf_row_gather", _ptr(x), x.stride(0), P, H, _ptr(rows.contiguous()), n, _ptr(out), out.stride(0),
+              _ptr(ssq), _stream(x))
+    return out, ssq
+
+
+def norm_q(x, ssq, eps, wq, hq, d, qnorm, qnorm_kind, cs, pos, out=None):
+    """Queries of rows x at positions pos: RMSNorm (gain folded into wq), x wq^T, per-head q_norm, RoPE with
+    table rows cs[pos]. Returns q [rows, hq d] bf16."""
+    _need(x, "x", torch.bfloat16, 2)
+    _need(ssq, "ssq", torch.float32, 2)
+    _need(wq, "wq", torch.bfloat16, 2)
+    _need(cs, "cs", torch.bfloat16, 2)
+    _need(pos, "pos", torch.int64, 1)
+    rows, H = x.shape
+    if tuple(wq.shape) != (hq * d, H) or not wq.is_contiguous() or tuple(ssq.shape) != (rows, ssq_parts(H)):
+        raise ValueError(f"norm_q: wq {tuple(wq.shape)}, expected ({hq * d}, {H}); ssq {tuple(ssq.shape)}")
+    if pos.shape[0] != rows or not cs.is_contiguous():
+        raise ValueError("norm_q: pos / cs")
+    if qnorm is not None:
+        _need(qnorm, "qnorm", torch.bfloat16, 1)
+    out = torch.empty(rows, hq * d, dtype=torch.bfloat16, device=x.device) if out is None else out
+    _need(out, "out", torch.bfloat16, 2)
+    _lib.call("rf_norm_q", _ptr(x), x.stride(0), _ptr(ssq), rows, H, float(eps), _ptr(wq), hq, d, _ptr(qnorm),
+              int(qnorm_kind), _ptr(cs), cs.shape[1], _ptr(pos.contiguous()), _ptr(out), out.stride(0), _stream(x))
+    return out
+
+
+def attend_rows(q, qpos, kbuf, vbuf, n, hq, scale, out=None):
+    """Causal attention of query rows q [nq, hq d] at sorted positions qpos over the first n cache rows of
+    kbuf / vbuf [hkv, cap, d]. Returns [nq, hq d] bf16."""
+    _need(q, "q", torch.bfloat16, 2)
+    _need(qpos, "qpos", torch.int64, 1)
+    for name, t in (("kbuf", kbuf), ("vbuf", vbuf)):
+        _need(t, name, torch.bfloat16, 3)
+    if kbuf.stride() != vbuf.stride() or kbuf.shape != vbuf.shape:
+        raise ValueError("kbuf / vbuf must share shape and strides")
+    hkv, cap, d = kbuf.shape
+    nq = q.shape[0]
+    if q.shape[1] < hq * d or qpos.shape[0] != nq or n > cap:
+        raise ValueError("attend_rows: shapes")
+    out = torch.empty(nq, hq * d, dtype=torch.bfloat16, device=q.device) if out is None else out
+    _need(out, "out", torch.bfloat16, 2)
+    _lib.call("rf_attend_rows", _ptr(q), q.stride(0), _ptr(qpos.contiguous()), nq, hq, d, _ptr(kbuf), _ptr(vbuf), hkv,
+              kbuf.stride(0), kbuf.stride(1), n, float(scale), _ptr(out), out.stride(0), _stream(q))
+    return out
+
+
+def residual_add(x, y, out=None, ssq=None):
+    """out = bf16(x + y) and its row sum-of-squares partials."""
+    _need(x, "x", torch.bfloat16, 2)
+    _need(y, "y", torch.bfloat16, 2)
+    rows, H = x.shape
+    if tuple(y.shape) != (rows, H):
+        raise ValueError("residual_add: shapes")
+    out = torch.empty_like(x) if out is None else out
+    ssq = torch.empty(rows, ssq_parts(H), dtype=torch.float32, device=x.device) if ssq is None else ssq
+    _need(out, "out", torch.bfloat16, 2)
+    _need(ssq, "ssq", torch.float32, 2)
+    _lib.call("rf_residual_add", _ptr(x), x.stride(0), _ptr(y), y.stride(0), _ptr(out), out.stride(0), _ptr(ssq), rows,
+              H, _stream(x))
+    return out, ssq
+
+
+def silu_mul(gu, out=None):
+    """SwiGLU of gu = [gate | up] [rows, 2 I]: bf16(bf16(silu(gate)) * up) [rows, I]."""
+    _need(gu, "gu", torch.bfloat16, 2)
+    rows, two_i = gu.shape
+    I = two_i // 2
+    out = torch.empty(rows, I, dtype=torch.bfloat16, device=gu.device) if out is None else out
+    _need(out, "out", torch.bfloat16, 2)
+    _lib.call("rf_silu_mul", _ptr(gu), gu.stride(0), rows, I, _ptr(out), out.stride(0), _stream(gu))
+    return out
+
+
 def gdn_workspace_bytes(rows, nk, nv, dk=128, dv=128):
     """Bytes of device workspace rf_gdn_fill needs to fill `rows` rows in one pass."""
     n = ctypes.c_size_t(0)

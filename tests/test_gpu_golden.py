@@ -44,7 +44,7 @@ def run():
     return oracle_run()
 
 
-@pytest.mark.parametrize("name", ["proj", "identity", "exact"])
+@pytest.mark.parametrize("name", ["proj", "identity", "exact", "exact_computed"])
 def test_fill_late_matches_reference(dev, gold, run, name):
     from rfill.kva import Arm, Projector, fill_late
     from rfill.model import FillModel
@@ -57,25 +57,34 @@ def test_fill_late_matches_reference(dev, gold, run, name):
     arm = Arm(name, split=S, tail=c1.TAIL, fill=fill, projector=Projector(S, W, B) if fill == "proj" else None)
     h_split = run["hs"][S].to(dev, torch.bfloat16)
     rows = hr = None
-    if name == "exact":
+    row_inputs = {}
+    if name == "exact":              # the rows' inputs given (the reference's row_inputs)
         rows = c1.exact_rows()
         hr = {i: torch.from_numpy(gold[f"exact_hr_{i}"]).to(dev, torch.bfloat16) for i in late}
-    cache, P = fill_late(model, h_split, arm, exact_rows=rows, hr=hr)
+    elif name == "exact_computed":   # the rows run through every late layer on the device (layer_rows)
+        rows = c1.exact_rows()
+    cache, P = fill_late(model, h_split, arm, exact_rows=rows, hr=hr, row_inputs=row_inputs)
     torch.cuda.synchronize()
-    assert P == int(gold[f"{name}_P"])
+    gname = "exact" if name == "exact_computed" else name
+    assert P == int(gold[f"{gname}_P"])
+    if name == "exact_computed":
+        for i in late:
+            err = rel(row_inputs[i].double().cpu().numpy(), gold[f"exact_hr_{i}"])
+            print(f"exact rows' input to layer {i}: rel err vs the reference {err:.2e}")
+            assert err < TOL, (i, err)
     u = c1.probes(102, 64)
     worst = 0.0
     for i in late:
         assert cache[i]["n"] == P
         for part in ("k", "v"):
             got = (cache[i][part].double().cpu() @ u).numpy()          # [Hkv, P]
-            want = gold[f"{name}_{part}_u_{i}"][:, :P]
+            want = gold[f"{gname}_{part}_u_{i}"][:, :P]
             err = rel(got, want)
             worst = max(worst, err)
             assert err < TOL, (i, part, err)
             # the rows the fixture keeps in full: slots 0, 1, P - 1
             full = cache[i][part][:, [0, 1, P - 1]].double().cpu().numpy()
-            assert rel(full, gold[f"{name}_{part}_rows_{i}"][:, :3]) < TOL
+            assert rel(full, gold[f"{gname}_{part}_rows_{i}"][:, :3]) < TOL
     print(f"{name}: worst K/V rel err vs the reference {worst:.2e}")
 
 

@@ -1,0 +1,158 @@
+"""GPU parity of the exact rows' full layer (FillModel.layer_rows: rf_row_gather, rf_norm_q, rf_attend_rows,
+rf_residual_add, rf_silu_mul over rf_map_apply / rf_norm_linear) against the CPU oracle's layer_rows
+(code/kva/model.py:259-276) and of the attention kernel against the oracle's attend_at
+(code/kva/ops.py:131-155) on identical seeded inputs.
+
+Bars: outputs within relative Frobenius error 1e-2 (bf16 path); the filled cache as in the fill tests;
+causality: keys after a query's position never change its output (bitwise), keys before it do."""
+import pytest
+import torch
+
+from fill_cases import case, inputs, rel_err
+from oracle import model as OM
+from oracle import ops as oops
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-2
+
+
+@pytest.fixture(scope="module")
+def dev():
+    assert torch.cuda.is_available(), "GPU tests need a GPU"
+    from rfill import _lib
+    _lib.load()
+    return torch.device("cuda")
+
+
+def _qkv(nq, hq, hkv, d, n, seed):
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(nq, hq * d, generator=g).to(torch.bfloat16)
+    k = torch.randn(hkv, n, d, generator=g).to(torch.bfloat16)
+    v = torch.randn(hkv, n, d, generator=g).to(torch.bfloat16)
+    return q, k, v
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(32, 8, 128), (4, 2, 64), (8, 8, 128), (16, 2, 64)])
+def test_attend_rows_matches_oracle(dev, hq, hkv, d):
+    from rfill import ops
+    n, nq = 1500, 70
+    q, k, v = _qkv(nq, hq, hkv, d, n, seed=hq + d)
+    g = torch.Generator().manual_seed(5)
+    qpos = torch.randperm(n, generator=g)[:nq].sort().values
+    qpos[0], qpos[-1] = 0, n - 1                      # a query that sees one key, one that sees them all
+    qpos = qpos.sort().values
+    kb = torch.zeros(hkv, n + 64, d, dtype=torch.bfloat16)
+    vb = torch.zeros_like(kb)
+    kb[:, :n], vb[:, :n] = k, v
+    scale = d ** -0.5
+    got = ops.attend_rows(q.to(dev), qpos.to(dev), kb.to(dev), vb.to(dev), n, hq, scale)
+    torch.cuda.synchronize()
+    want = oops.attend_at(q.view(nq, hq, d).transpose(0, 1), k, v, scale, qpos)
+    err = rel_err(got, want)
+    print(f"hq {hq} hkv {hkv} d {d}: attention rel err {err:.2e}")
+    assert err < TOL
+    # the query at position 0 sees only key 0: its output is V[0] of its K / V head exactly (p = 1)
+    rep = hq // hkv
+    first = got[0].view(hq, d).cpu()
+    for h in range(hq):
+        assert torch.equal(first[h], v[h // rep, 0])
+
+
+def test_attend_rows_is_causal(dev):
+    """Keys after every query's position leave the outputs bitwise unchanged; a key before changes them."""
+    from rfill import ops
+    hq, hkv, d, n, nq = 32, 8, 128, 900, 20
+    q, k, v = _qkv(nq, hq, hkv, d, n, seed=3)
+    qpos = torch.arange(nq) * 20 + 5                  # max position 385 < n
+    kb = torch.zeros(hkv, n + 64, d, dtype=torch.bfloat16, device=dev)
+    vb = torch.zeros_like(kb)
+    kb[:, :n], vb[:, :n] = k.to(dev), v.to(dev)
+    base = ops.attend_rows(q.to(dev), qpos.to(dev), kb, vb, n, hq, d ** -0.5)
+    kb2, vb2 = kb.clone(), vb.clone()
+    kb2[:, 400:n] = 7.0
+    vb2[:, 400:n] = -3.0
+    later = ops.attend_rows(q.to(dev), qpos.to(dev), kb2, vb2, n, hq, d ** -0.5)
+    assert torch.equal(base, later)
+    vb2[:, 0] += 1.0
+    earlier = ops.attend_rows(q.to(dev), qpos.to(dev), kb2, vb2, n, hq, d ** -0.5)
+    assert not torch.equal(base, earlier)
+
+
+@pytest.mark.parametrize("name", ["llama_c1", "llama3_scaled", "qwen3_knorm"])
+def test_layer_rows_matches_oracle(dev, name):
+    from rfill.model import FillModel
+    cfg, t = case(name)
+    P, H = 1200, cfg["hidden_size"]
+    x = inputs(P, H, seed=21)
+    g = torch.Generator().manual_seed(22)
+    rows = torch.randperm(P, generator=g)[:37].sort().values
+    rows[0] = 0
+    rows = rows.sort().values.unique()
+    pos = torch.arange(P)
+    om = OM.OracleModel(cfg, t, dtype=torch.bfloat16)
+    oc = om.new_cache()
+    want = om.layer_rows(0, x, pos, rows, oc)
+    m = FillModel(cfg, t, dev)
+    c = m.new_cache()
+    got = m.layer_rows(0, x.to(dev), pos.to(dev), rows.to(dev), c)
+    torch.cuda.synchronize()
+    err = rel_err(got, want)
+    ek, ev = rel_err(c[0]["k"], oc[0]["k"]), rel_err(c[0]["v"], oc[0]["v"])
+    # the layer's own contribution (output minus input), the part an error would hide in
+    ed = rel_err(got.cpu().float() - x[rows].float(), want.float() - x[rows].float())
+    print(f"{name}: layer_rows out rel err {err:.2e}, update {ed:.2e}, K {ek:.2e}, V {ev:.2e}")
+    assert err < TOL and ed < TOL and ek < TOL and ev < TOL
+    assert c[0]["n"] == P
+
+
+def test_layer_rows_refuses_a_filled_cache_and_gdn(dev):
+    from rfill._lib import UnsupportedArchitecture
+    from rfill.model import FillModel
+    from fill_cases import gdn_config, gdn_tensors
+    cfg, t = case("llama_c1")
+    m = FillModel(cfg, t, dev)
+    x = inputs(300, cfg["hidden_size"], seed=2).to(dev)
+    pos = torch.arange(300, device=dev)
+    c = m.new_cache()
+    m.fill(0, x, pos, c)
+    with pytest.raises(ValueError):
+        m.layer_rows(0, x, pos, torch.tensor([3, 9], device=dev), c)
+    gcfg = gdn_config()
+    gm = FillModel(gcfg, gdn_tensors(gcfg), dev)
+    with pytest.raises(UnsupportedArchitecture):
+        gm.layer_rows(0, inputs(64, gcfg["hidden_size"]).to(dev), torch.arange(64, device=dev),
+                      torch.tensor([1], device=dev), gm.new_cache())
+
+
+def test_fill_late_runs_the_exact_rows_through_every_layer(dev):
+    """finish()'s late loop with exact rows and no given inputs: the rows start from h_split and each late
+    layer's layer_rows gives their next input; caches and row inputs against the oracle's finish loop."""
+    from rfill.kva import Arm, Projector, fill_late
+    from rfill.model import FillModel
+    cfg, t = case("llama_c1", layers=8)
+    N, tail, split = 2048, 256, 5
+    P, H = N - tail, cfg["hidden_size"]
+    h = inputs(N, H, seed=12)
+    g = torch.Generator().manual_seed(13)
+    W = {i: (torch.eye(H) + 0.05 * torch.randn(H, H, generator=g) / H ** 0.5).to(torch.bfloat16)
+         for i in range(split, 8)}
+    B = {i: (1e-2 * torch.randn(H, generator=g)).to(torch.bfloat16) for i in range(split, 8)}
+    rows = torch.randperm(P, generator=g)[:18].sort().values
+    arm = Arm("ridgefill", split=split, tail=tail, fill="proj", projector=Projector(split, W, B))
+    m = FillModel(cfg, t, dev)
+    got_inputs = {}
+    cache, P_got = fill_late(m, h.to(dev), arm, exact_rows=rows, row_inputs=got_inputs)
+    torch.cuda.synchronize()
+    assert P_got == P
+    om = OM.OracleModel(cfg, t, dtype=torch.bfloat16)
+    oc = om.new_cache()
+    pos = torch.arange(P)
+    hr = h[rows]
+    for i in range(split, 8):
+        eh = rel_err(got_inputs[i], hr)
+        x = torch.nn.functional.linear(h[:P], W[i], B[i]).index_copy(0, rows, hr)
+        hr = om.layer_rows(i, x, pos, rows, oc)
+        ek, ev = rel_err(cache[i]["k"], oc[i]["k"]), rel_err(cache[i]["v"], oc[i]["v"])
+        er = rel_err(cache[i]["k"][:, rows.to(dev)], oc[i]["k"][:, rows])
+        print(f"layer {i}: row inputs {eh:.2e}, K {ek:.2e} V {ev:.2e} exact-row K {er:.2e}")
+        assert eh < TOL and ek < TOL and ev < TOL and er < TOL
