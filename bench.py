@@ -269,6 +269,42 @@ def hybrid_bench(dev, reps=3, split=24, n_rows=32768, tail=4096):
                                 "counted_flop_per_launch": P * (2 * 4 * C + 6 * nv * dk * dv)}}}
 
 
+def exact_rows_bench(dev, reps=3, split=18, n_rows=32768, tail=4096, frac=0.01):
+    """The Qwen3-8B-shaped fill (hidden 4096, 32 / 8 heads, k_norm, layers 18..35, 32K prompt, P = 28672)
+    with 1% of the filled rows exact (287 rows at seeded positions) run as finish() runs them: every late
+    layer's cache is filled with the rows' inputs scattered in, and each exact row goes through the layer
+    (layer_rows: query projection, attention over the filled keys, o_proj, SwiGLU MLP), its output being
+    its input to the next layer. Reported beside the same fill without exact rows."""
+    from rfill import synth
+    from rfill.kva import Arm, Projector, fill_late
+    from rfill.model import FillModel
+    cfg = synth.QWEN3_8B
+    w = synth.dense_fill(cfg, split, n_rows, tail, device=dev, exact_frac=frac, full=True)
+    model = FillModel(cfg, w["tensors"], dev, layers=w["layers"])
+    arm = Arm("ridgefill", split=split, tail=tail, fill="proj", projector=Projector(split, w["maps"], w["biases"]))
+    P, rows = w["P"], w["rows"]
+
+    def run(exact):
+        caches = model.new_cache()
+        fill_late(model, w["h_split"], arm, exact_rows=rows if exact else None, cache=caches)
+        return caches
+
+    out = {}
+    for name, exact in (("plain", False), ("exact", True)):
+        run(exact)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(reps):
+            run(exact)
+        torch.cuda.synchronize()
+        out[name] = (time.perf_counter() - t0) / reps
+    return {"workload": f"qwen3-8b-shaped 32K fill: layers {split}..{cfg['num_hidden_layers'] - 1}, {P} filled rows, "
+                        f"{len(rows)} exact rows (1%) through their full layers",
+            "filled_tokens_per_s": round(P / out["exact"], 1), "ms_per_fill": round(out["exact"] * 1e3, 3),
+            "ms_per_fill_without_exact_rows": round(out["plain"] * 1e3, 3),
+            "exact_rows_ms": round((out["exact"] - out["plain"]) * 1e3, 3), "exact_rows": len(rows)}
+
+
 def traffic_from_profiles(kernel):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE scaled
     by a copy kernel of known size), or None if it has not been measured."""
@@ -290,6 +326,7 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="skip ceilings and the standalone KV-write leg")
     ap.add_argument("--no-fit", action="store_true", help="skip the closed-form fit leg")
     ap.add_argument("--no-hybrid", action="store_true", help="skip the Gated-DeltaNet hybrid fill leg")
+    ap.add_argument("--no-exact", action="store_true", help="skip the Qwen3-8B exact-rows fill leg")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (one MI355X per box); --gpus must be 1", file=sys.stderr)
@@ -349,6 +386,10 @@ def main():
         out["ceilings"] = ceilings(dev, P, H)
     del caches, xbuf, sbuf
     torch.cuda.empty_cache()
+    if not args.no_exact:
+        log("Qwen3-8B fill with 1% exact rows")
+        out["exact_rows"] = exact_rows_bench(dev)
+        torch.cuda.empty_cache()
     if not args.no_hybrid:
         log("Gated-DeltaNet hybrid fill leg")
         out["hybrid"] = hybrid_bench(dev)

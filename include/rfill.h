@@ -115,10 +115,17 @@ int rf_norm_q(const uint16_t* x, int64_t ldx, const float* ssq, int64_t rows, in
  * < cache_rows) over the cache kbuf / vbuf [hkv, cap, d] (element strides head_stride / row_stride): query
  * j sees keys 0 .. qpos[j]; scores in fp32 scaled by `scale`, softmax in fp32, probabilities as bf16 into
  * the second product. Writes out [nq, hq d] (row stride ldo). Replaces ops.attend_at / attend_rows
- * (code/kva/ops.py:131-170) in layer_rows. Needs d == 128 and hq / hkv dividing 64. */
+ * (code/kva/ops.py:131-170) in layer_rows. Needs d 64 or 128 and hq / hkv dividing 64. With a workspace
+ * (caller-owned device memory, 16-byte aligned) the key range is split over more blocks and the splits are
+ * merged in a fixed order (rf_attend_rows_workspace_bytes gives the size for the full split; a smaller one
+ * gives fewer splits, NULL none). */
 int rf_attend_rows(const uint16_t* q, int64_t ldq, const int64_t* qpos, int64_t nq, int hq, int d,
                    const uint16_t* kbuf, const uint16_t* vbuf, int hkv, int64_t head_stride, int64_t row_stride,
-                   int64_t cache_rows, float scale, uint16_t* out, int64_t ldo, hipStream_t stream);
+                   int64_t cache_rows, float scale, uint16_t* out, int64_t ldo, void* workspace, size_t ws_bytes,
+                   hipStream_t stream);
+
+/* Workspace bytes rf_attend_rows uses to split the key range fully for these sizes (0: no split). Host only. */
+int rf_attend_rows_workspace_bytes(int64_t nq, int hq, int hkv, int d, int64_t cache_rows, size_t* bytes);
 
 /* out = bf16(x + y) row by row (rows x H) and out's row sum-of-squares partials ssq [rows, H / 256]: the
  * residual adds of layer_rows (code/kva/model.py:274, Model.mlp :114). out may alias x. */

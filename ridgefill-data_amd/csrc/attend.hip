@@ -13,9 +13,15 @@
 //       already have: the contraction order over a 32-key step is permuted to keys {4g .. 4g + 3,
 //       16 + 4g .. 16 + 4g + 3} for lane group g, and the V operand is read in that order from a
 //       transposed V tile (V^T in LDS).
-// The next tile's K / V rows load into registers while the current tile computes. Scores are fp32
+// The next tile's K / V rows load into registers while the current tile computes. The key range of a
+// block can be split over several blocks (blockIdx.z): each writes its unnormalised O with its row maxima
+// and sums to a workspace, and k_attend_combine merges them in split order. Scores are fp32
 // products of the bf16 q and k values, as the reference's fp32 matmul; the probabilities enter the
 // second product as bf16, as the reference's cast (here before normalisation, within rounding).
+#include <stdint.h>
+
+#include <algorithm>
+
 #include "rf_common.h"
 
 namespace rf {
@@ -41,7 +47,13 @@ struct AttnArgs {
   float scale;
   uint16_t* out;           // [nq, >= hq * d]
   int64_t ldo;
+  float* part;             // nsplit > 1: per (query block, head, split) O [64][d], max [64], sum [64]
 };
+
+template <int AD>
+__device__ __forceinline__ float* part_block(const AttnArgs& a, int qblock, int hk, int split) {
+  return a.part + ((static_cast<int64_t>(qblock) * a.hkv + hk) * gridDim.z + split) * (64 * AD + 128);
+}
 
 // AD = head_dim (64 or 128); K tile rows are AD + 8 bf16 apart in LDS (conflict-free fragment reads).
 template <int AD>
@@ -102,14 +114,18 @@ __global__ __launch_bounds__(256) void k_attend_rows(AttnArgs a) {
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) o[nb] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m = -INFINITY, lpart = 0.f;
+  // this block's share of the key tiles
   const int ntiles = static_cast<int>(kmax / KT) + 1;
-  load(0);
-  for (int it = 0; it < ntiles; ++it) {
+  const int ns = gridDim.z, sp = blockIdx.z;
+  const int it0 = static_cast<int>(static_cast<int64_t>(ntiles) * sp / ns);
+  const int it1 = static_cast<int>(static_cast<int64_t>(ntiles) * (sp + 1) / ns);
+  if (it0 < it1) load(static_cast<int64_t>(it0) * KT);
+  for (int it = it0; it < it1; ++it) {
     const int64_t k0 = static_cast<int64_t>(it) * KT;
     __syncthreads();                                          // the previous tile's reads are done
     store();
     __syncthreads();
-    if (it + 1 < ntiles) load(k0 + KT);
+    if (it + 1 < it1) load(k0 + KT);
 
     // scores of the wave's 16 query rows against the tile's 64 keys
     f32x4 sc[4];
@@ -177,6 +193,20 @@ __global__ __launch_bounds__(256) void k_attend_rows(AttnArgs a) {
   float lsum = lpart;
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
+  if (ns > 1) {                                               // unnormalised partials for the combine
+    float* pb = part_block<AD>(a, blockIdx.x, hk, sp);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rr = 16 * w + 4 * g + i;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) pb[rr * AD + 16 * nb + ln] = o[nb][i];
+    }
+    if (g == 0) {
+      pb[64 * AD + r] = m;
+      pb[64 * AD + 64 + r] = lsum;
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const float li = __shfl(lsum, 4 * g + i, 64);
@@ -192,6 +222,39 @@ __global__ __launch_bounds__(256) void k_attend_rows(AttnArgs a) {
       dst[16 * (nb + 1)] = static_cast<uint16_t>(pr >> 16);
     }
   }
+}
+
+// Merges the key-range splits of one (query block, K / V head): M = max_s m_s, L = sum_s l_s e^{m_s - M},
+// O = sum_s O_s e^{m_s - M} / L, in split order; thread t takes query row t / 4 and a quarter of d.
+template <int AD>
+__global__ __launch_bounds__(256) void k_attend_combine(AttnArgs a, int ns) {
+  const int t = threadIdx.x, r = t >> 2, q4 = t & 3;
+  const int rep = a.hq / a.hkv, qb = 64 / rep;
+  const int hk = blockIdx.y, jo = blockIdx.x * qb + r % qb;
+  if (jo >= a.nq) return;
+  const int64_t stride = 64 * AD + 128;
+  const float* base = a.part + (static_cast<int64_t>(blockIdx.x) * a.hkv + hk) * ns * stride;
+  float mx = -INFINITY;
+  for (int sp = 0; sp < ns; ++sp) mx = fmaxf(mx, base[sp * stride + 64 * AD + r]);
+  float l = 0.f;
+  float acc[AD / 4];
+#pragma unroll
+  for (int e = 0; e < AD / 4; ++e) acc[e] = 0.f;
+  for (int sp = 0; sp < ns; ++sp) {
+    const float* pb = base + sp * stride;
+    const float ms = pb[64 * AD + r];
+    const float f = ms == -INFINITY ? 0.f : expf(ms - mx);
+    l += pb[64 * AD + 64 + r] * f;
+#pragma unroll
+    for (int e = 0; e < AD / 4; ++e) acc[e] += pb[r * AD + q4 * (AD / 4) + e] * f;
+  }
+  const float inv = 1.0f / l;
+  uint16_t* dst = a.out + static_cast<int64_t>(jo) * a.ldo + (hk * rep + r / qb) * AD + q4 * (AD / 4);
+#pragma unroll
+  for (int e = 0; e < AD / 4; e += 8)
+    *reinterpret_cast<uint4*>(dst + e) =
+        make_uint4(bf16_pair(acc[e] * inv, acc[e + 1] * inv), bf16_pair(acc[e + 2] * inv, acc[e + 3] * inv),
+                   bf16_pair(acc[e + 4] * inv, acc[e + 5] * inv), bf16_pair(acc[e + 6] * inv, acc[e + 7] * inv));
 }
 
 // out[j, :] = bf16(x[j, :] + y[j, :]) for `rows` rows of width H, and out's row sum-of-squares partials
@@ -241,10 +304,35 @@ __global__ __launch_bounds__(256) void k_silu_mul(const uint16_t* __restrict__ g
 
 using namespace rf;
 
+namespace rf {
+namespace {
+// Key-range splits for nq queries: enough blocks for about three per CU, at most one split per key tile,
+// at most 32, and what the workspace holds.
+int attend_splits(int64_t nq, int hq, int hkv, int d, int64_t cache_rows, size_t ws_bytes) {
+  const int64_t qb = 64 / (hq / hkv);
+  const int64_t blocks = (nq + qb - 1) / qb * hkv;
+  int64_t ns = (768 + blocks - 1) / blocks;
+  ns = std::min<int64_t>(ns, std::min<int64_t>(32, (cache_rows + KT - 1) / KT));
+  const int64_t per = blocks * (64 * static_cast<int64_t>(d) + 128) * 4;
+  ns = std::min<int64_t>(ns, static_cast<int64_t>(ws_bytes / static_cast<size_t>(per)));
+  return static_cast<int>(std::max<int64_t>(ns, 1));
+}
+}  // namespace
+}  // namespace rf
+
+extern "C" int rf_attend_rows_workspace_bytes(int64_t nq, int hq, int hkv, int d, int64_t cache_rows, size_t* bytes) {
+  if (!bytes || nq < 0 || hq <= 0 || hkv <= 0 || hq % hkv || 64 % (hq / hkv) || (d != 64 && d != 128))
+    return fail(RF_EINVAL_ARG, "rf_attend_rows_workspace_bytes: arguments");
+  const int ns = attend_splits(nq, hq, hkv, d, cache_rows, SIZE_MAX);
+  const int64_t qb = 64 / (hq / hkv);
+  *bytes = ns > 1 ? static_cast<size_t>((nq + qb - 1) / qb * hkv * ns * (64 * static_cast<int64_t>(d) + 128) * 4) : 0;
+  return RF_OK;
+}
+
 extern "C" int rf_attend_rows(const uint16_t* q, int64_t ldq, const int64_t* qpos, int64_t nq, int hq, int d,
                               const uint16_t* kbuf, const uint16_t* vbuf, int hkv, int64_t head_stride,
                               int64_t row_stride, int64_t cache_rows, float scale, uint16_t* out, int64_t ldo,
-                              hipStream_t stream) {
+                              void* workspace, size_t ws_bytes, hipStream_t stream) {
   if (!q || !qpos || !kbuf || !vbuf || !out) return fail(RF_EINVAL_ARG, "rf_attend_rows: null pointer");
   if (d != 64 && d != 128) return fail(RF_EUNSUPPORTED, "rf_attend_rows: head_dim %d (the kernel takes 64, 128)", d);
   if (hq <= 0 || hkv <= 0 || hq % hkv || 64 % (hq / hkv))
@@ -256,11 +344,22 @@ extern "C" int rf_attend_rows(const uint16_t* q, int64_t ldq, const int64_t* qpo
                 (long long)ldq, (long long)ldo);
   if (!aligned16(q) || !aligned16(kbuf) || !aligned16(vbuf)) return fail(RF_EINVAL_SHAPE, "rf_attend_rows: alignment");
   if (nq == 0) return RF_OK;
-  AttnArgs a{q, ldq, qpos, static_cast<int>(nq), kbuf, vbuf, head_stride, row_stride, hq, hkv, scale, out, ldo};
+  if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 15u))
+    return fail(RF_EINVAL_SHAPE, "rf_attend_rows: workspace alignment");
+  const int ns = workspace ? attend_splits(nq, hq, hkv, d, cache_rows, ws_bytes) : 1;
+  AttnArgs a{q, ldq, qpos, static_cast<int>(nq), kbuf, vbuf, head_stride, row_stride, hq, hkv, scale, out, ldo,
+             static_cast<float*>(workspace)};
   const int qb = 64 / (hq / hkv);
-  const dim3 grid(static_cast<unsigned>((nq + qb - 1) / qb), static_cast<unsigned>(hkv));
+  const dim3 grid(static_cast<unsigned>((nq + qb - 1) / qb), static_cast<unsigned>(hkv), static_cast<unsigned>(ns));
   if (d == 128) hipLaunchKernelGGL(k_attend_rows<128>, grid, dim3(256), 0, stream, a);
   else hipLaunchKernelGGL(k_attend_rows<64>, grid, dim3(256), 0, stream, a);
+  if (ns > 1) {
+    const int st = check_launch("rf_attend_rows");
+    if (st != RF_OK) return st;
+    const dim3 g2(grid.x, grid.y);
+    if (d == 128) hipLaunchKernelGGL(k_attend_combine<128>, g2, dim3(256), 0, stream, a, ns);
+    else hipLaunchKernelGGL(k_attend_combine<64>, g2, dim3(256), 0, stream, a, ns);
+  }
   return check_launch("rf_attend_rows");
 }
 

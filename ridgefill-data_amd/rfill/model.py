@@ -191,6 +191,16 @@ class FillModel:
             c["rec"] = c["rec"] + st.to(c["rec"])
         return {}
 
+    def _attn_workspace(self, nq, n, device):
+        """The exact-row attention's key-split workspace, shared by every layer (stream-ordered reuse)."""
+        need = ops.attend_rows_workspace_bytes(nq, self.n_heads, self.n_kv, self.head_dim, n)
+        if need == 0:
+            return None
+        ws = getattr(self, "_attn_ws", None)
+        if ws is None or ws.numel() < need or ws.device != device:
+            self._attn_ws = ws = torch.empty(need, dtype=torch.uint8, device=device)
+        return ws
+
     def _gdn_workspace(self, rows, device):
         """The GDN kernels' per-chunk workspace, shared by every GDN layer (stream-ordered reuse), sized
         for min(rows, GDN_ROWS) rows per pass."""
@@ -251,7 +261,7 @@ class FillModel:
         q = ops.norm_q(xr, sr, self.eps, w["wq"], self.n_heads, self.head_dim, w.get("q_norm"), self.knorm_kind, cs,
                        rows)
         o = ops.attend_rows(q, pos.to(x.device, torch.int64)[rows], c["kbuf"], c["vbuf"], c["n"], self.n_heads,
-                            self.scale)
+                            self.scale, workspace=self._attn_workspace(len(rows), c["n"], x.device))
         a, _ = ops.map_apply(o, w["wo"], None)
         h1, s1 = ops.residual_add(xr, a)
         gu = ops.norm_linear(h1, s1, self.eps, w["wgu"])

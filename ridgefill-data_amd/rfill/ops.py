@@ -220,9 +220,17 @@ def norm_q(x, ssq, eps, wq, hq, d, qnorm, qnorm_kind, cs, pos, out=None):
     return out
 
 
-def attend_rows(q, qpos, kbuf, vbuf, n, hq, scale, out=None):
+def attend_rows_workspace_bytes(nq, hq, hkv, d, n):
+    """Device bytes attend_rows uses to split the key range over more blocks (0: no split)."""
+    b = ctypes.c_size_t(0)
+    _lib.call("rf_attend_rows_workspace_bytes", nq, hq, hkv, d, n, ctypes.byref(b))
+    return b.value
+
+
+def attend_rows(q, qpos, kbuf, vbuf, n, hq, scale, out=None, workspace="auto"):
     """Causal attention of query rows q [nq, hq d] at sorted positions qpos over the first n cache rows of
-    kbuf / vbuf [hkv, cap, d]. Returns [nq, hq d] bf16."""
+    kbuf / vbuf [hkv, cap, d]. Returns [nq, hq d] bf16. workspace: uint8 device memory for the key-range
+    splits ("auto": allocated here at the full size; None: no split)."""
     _need(q, "q", torch.bfloat16, 2)
     _need(qpos, "qpos", torch.int64, 1)
     for name, t in (("kbuf", kbuf), ("vbuf", vbuf)):
@@ -235,8 +243,14 @@ def attend_rows(q, qpos, kbuf, vbuf, n, hq, scale, out=None):
         raise ValueError("attend_rows: shapes")
     out = torch.empty(nq, hq * d, dtype=torch.bfloat16, device=q.device) if out is None else out
     _need(out, "out", torch.bfloat16, 2)
+    if isinstance(workspace, str):
+        need = attend_rows_workspace_bytes(nq, hq, hkv, d, n)
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device) if need else None
+    if workspace is not None:
+        _need(workspace, "workspace", torch.uint8, 1)
     _lib.call("rf_attend_rows", _ptr(q), q.stride(0), _ptr(qpos.contiguous()), nq, hq, d, _ptr(kbuf), _ptr(vbuf), hkv,
-              kbuf.stride(0), kbuf.stride(1), n, float(scale), _ptr(out), out.stride(0), _stream(q))
+              kbuf.stride(0), kbuf.stride(1), n, float(scale), _ptr(out), out.stride(0), _ptr(workspace),
+              0 if workspace is None else workspace.numel(), _stream(q))
     return out
 
 

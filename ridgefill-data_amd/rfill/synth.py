@@ -19,9 +19,9 @@ explicit variance 1/H of the map noise.
 import torch
 
 LLAMA_8B = dict(model_type="llama", num_hidden_layers=32, hidden_size=4096, num_attention_heads=32,
-                num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-5, rope_theta=500000.0)
+                num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-5, rope_theta=500000.0, intermediate_size=14336)
 QWEN3_8B = dict(model_type="qwen3", num_hidden_layers=36, hidden_size=4096, num_attention_heads=32,
-                num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-6,
+                num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-6, intermediate_size=12288,
                 rope_parameters=dict(rope_type="default", rope_theta=1000000.0))
 
 
@@ -47,34 +47,48 @@ def hidden_states(n, h, device="cpu", seed_rows=10, seed_gain=11, outliers=4, ou
     return (rows * gain.to(device)).to(torch.bfloat16)
 
 
-def layer_weights(cfg, layer, device="cpu", map_noise=0.02, with_map=True):
-    """HF-named weights of one late attention layer plus its ridge map (W, c), seed 12 + layer."""
+def layer_weights(cfg, layer, device="cpu", map_noise=0.02, with_map=True, full=False):
+    """HF-named weights of one late attention layer plus its ridge map (W, c), seed 12 + layer. full: also
+    the rest of the layer the exact rows run through (q / o projections, q_norm, the post-attention norm,
+    the SwiGLU MLP; matrices N(0, 0.02), norm gains 1 + N(0, 0.05)), drawn after the fill's weights."""
     h, hkv, d = cfg["hidden_size"], cfg["num_key_value_heads"], cfg["head_dim"]
     g = _gen(12 + layer, device)
     p = f"model.layers.{layer}."
+    rn = lambda *s: torch.randn(*s, generator=g, device=device)                        # noqa: E731
     t = {
-        p + "input_layernorm.weight": 1 + 0.05 * torch.randn(h, generator=g, device=device),
-        p + "self_attn.k_proj.weight": 0.02 * torch.randn(hkv * d, h, generator=g, device=device),
-        p + "self_attn.v_proj.weight": 0.02 * torch.randn(hkv * d, h, generator=g, device=device),
+        p + "input_layernorm.weight": 1 + 0.05 * rn(h),
+        p + "self_attn.k_proj.weight": 0.02 * rn(hkv * d, h),
+        p + "self_attn.v_proj.weight": 0.02 * rn(hkv * d, h),
     }
     if cfg["model_type"] != "llama":
-        t[p + "self_attn.k_norm.weight"] = 1 + 0.05 * torch.randn(d, generator=g, device=device)
+        t[p + "self_attn.k_norm.weight"] = 1 + 0.05 * rn(d)
+    w = c = None
+    if with_map:
+        w = (torch.eye(h, device=device) + map_noise * rn(h, h) / h ** 0.5).to(torch.bfloat16)
+        c = (1e-3 * rn(h)).to(torch.bfloat16)
+    if full:
+        hq, inter = cfg["num_attention_heads"], cfg["intermediate_size"]
+        t[p + "self_attn.q_proj.weight"] = 0.02 * rn(hq * d, h)
+        t[p + "self_attn.o_proj.weight"] = 0.02 * rn(h, hq * d)
+        if cfg["model_type"] != "llama":
+            t[p + "self_attn.q_norm.weight"] = 1 + 0.05 * rn(d)
+        t[p + "post_attention_layernorm.weight"] = 1 + 0.05 * rn(h)
+        t[p + "mlp.gate_proj.weight"] = 0.02 * rn(inter, h)
+        t[p + "mlp.up_proj.weight"] = 0.02 * rn(inter, h)
+        t[p + "mlp.down_proj.weight"] = 0.02 * rn(h, inter)
     t = {k: v.to(torch.bfloat16) for k, v in t.items()}
-    if not with_map:
-        return t, None, None
-    w = torch.eye(h, device=device) + map_noise * torch.randn(h, h, generator=g, device=device) / h ** 0.5
-    c = 1e-3 * torch.randn(h, generator=g, device=device)
-    return t, w.to(torch.bfloat16), c.to(torch.bfloat16)
+    return t, w, c
 
 
-def dense_fill(cfg, split, n_rows, tail, device="cpu", exact_frac=0.0, with_maps=True):
+def dense_fill(cfg, split, n_rows, tail, device="cpu", exact_frac=0.0, with_maps=True, full=False):
     """A late-layer fill workload: dict(cfg, split, layers, h_split [n, H], P, tensors (HF names),
-    maps {l: W}, biases {l: c}, rows (sorted exact-row positions < P), hr [|rows|, H])."""
+    maps {l: W}, biases {l: c}, rows (sorted exact-row positions < P), hr [|rows|, H]). full: the late
+    layers' whole weights (for exact rows run through their layers)."""
     L, h = cfg["num_hidden_layers"], cfg["hidden_size"]
     layers = list(range(split, L))
     tensors, maps, biases = {}, {}, {}
     for l in layers:
-        t, w, c = layer_weights(cfg, l, device, with_map=with_maps)
+        t, w, c = layer_weights(cfg, l, device, with_map=with_maps, full=full)
         tensors.update(t)
         if with_maps:
             maps[l], biases[l] = w, c

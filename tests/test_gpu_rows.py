@@ -45,17 +45,20 @@ def test_attend_rows_matches_oracle(dev, hq, hkv, d):
     vb = torch.zeros_like(kb)
     kb[:, :n], vb[:, :n] = k, v
     scale = d ** -0.5
-    got = ops.attend_rows(q.to(dev), qpos.to(dev), kb.to(dev), vb.to(dev), n, hq, scale)
+    got = ops.attend_rows(q.to(dev), qpos.to(dev), kb.to(dev), vb.to(dev), n, hq, scale)          # key splits
+    one = ops.attend_rows(q.to(dev), qpos.to(dev), kb.to(dev), vb.to(dev), n, hq, scale, workspace=None)
     torch.cuda.synchronize()
     want = oops.attend_at(q.view(nq, hq, d).transpose(0, 1), k, v, scale, qpos)
-    err = rel_err(got, want)
-    print(f"hq {hq} hkv {hkv} d {d}: attention rel err {err:.2e}")
-    assert err < TOL
+    err, err1 = rel_err(got, want), rel_err(one, want)
+    print(f"hq {hq} hkv {hkv} d {d}: attention rel err {err:.2e} (split keys), {err1:.2e} (one pass)")
+    assert err < TOL and err1 < TOL
+    assert ops.attend_rows_workspace_bytes(nq, hq, hkv, d, n) > 0
     # the query at position 0 sees only key 0: its output is V[0] of its K / V head exactly (p = 1)
     rep = hq // hkv
-    first = got[0].view(hq, d).cpu()
-    for h in range(hq):
-        assert torch.equal(first[h], v[h // rep, 0])
+    for res in (got, one):
+        first = res[0].view(hq, d).cpu()
+        for h in range(hq):
+            assert torch.equal(first[h], v[h // rep, 0])
 
 
 def test_attend_rows_is_causal(dev):
@@ -67,15 +70,18 @@ def test_attend_rows_is_causal(dev):
     kb = torch.zeros(hkv, n + 64, d, dtype=torch.bfloat16, device=dev)
     vb = torch.zeros_like(kb)
     kb[:, :n], vb[:, :n] = k.to(dev), v.to(dev)
-    base = ops.attend_rows(q.to(dev), qpos.to(dev), kb, vb, n, hq, d ** -0.5)
-    kb2, vb2 = kb.clone(), vb.clone()
-    kb2[:, 400:n] = 7.0
-    vb2[:, 400:n] = -3.0
-    later = ops.attend_rows(q.to(dev), qpos.to(dev), kb2, vb2, n, hq, d ** -0.5)
-    assert torch.equal(base, later)
-    vb2[:, 0] += 1.0
-    earlier = ops.attend_rows(q.to(dev), qpos.to(dev), kb2, vb2, n, hq, d ** -0.5)
-    assert not torch.equal(base, earlier)
+    for ws in ("auto", None):
+        base = ops.attend_rows(q.to(dev), qpos.to(dev), kb, vb, n, hq, d ** -0.5, workspace=ws)
+        again = ops.attend_rows(q.to(dev), qpos.to(dev), kb, vb, n, hq, d ** -0.5, workspace=ws)
+        assert torch.equal(base, again)                   # run to run, the same bits
+        kb2, vb2 = kb.clone(), vb.clone()
+        kb2[:, 400:n] = 7.0
+        vb2[:, 400:n] = -3.0
+        later = ops.attend_rows(q.to(dev), qpos.to(dev), kb2, vb2, n, hq, d ** -0.5, workspace=ws)
+        assert torch.equal(base, later)
+        vb2[:, 0] += 1.0
+        earlier = ops.attend_rows(q.to(dev), qpos.to(dev), kb2, vb2, n, hq, d ** -0.5, workspace=ws)
+        assert not torch.equal(base, earlier)
 
 
 @pytest.mark.parametrize("name", ["llama_c1", "llama3_scaled", "qwen3_knorm"])
