@@ -3,13 +3,13 @@
 //   rf_norm_kv_write  [K | V] = rms_norm(x) W_kv^T with the norm gain folded into W_kv, per-head
 //                     k_norm, RoPE on K, written straight into the [hkv, cap, d] cache slots.
 //
-// Tiling. A workgroup of 4 wave64s computes a 256 x 256 output tile over K in 64-wide steps. Both
-// operands are K-contiguous (row-major activations, F.linear-layout weights), so each 64-wide K slice
-// of a 256-row operand tile is 256 rows x 128 bytes. The slices go from memory straight into LDS
+// Tiling. A workgroup of 4 wave64s computes a 256 x 256 output tile over K in 32-wide steps. Both
+// operands are K-contiguous (row-major activations, F.linear-layout weights), so each 32-wide K slice
+// of a 256-row operand tile is 256 rows x 64 bytes. The slices go from memory straight into LDS
 // (buffer_load_dwordx4 ... lds, no staging registers; the buffer's range check turns rows past M into
-// zeros) with the 16-byte chunk index XOR-ed by the row's low 3 bits, so the MFMA fragment reads
-// (32 rows, one chunk per lane) hit all banks. Two LDS stages (2 x 64 KiB): the loads of step k+1 are
-// in flight while step k feeds the MFMAs; one wait and one barrier per step.
+// zeros) with the 16-byte chunk index XOR-ed by (row >> 2) & 3, so the MFMA fragment reads (32 rows,
+// one chunk per lane) hit all banks. Four LDS stages (4 x 32 KiB): loads run three steps ahead of the
+// MFMAs; one wait and one barrier per step.
 //
 // Each wave owns a 128 x 128 quarter and issues v_mfma_f32_32x32x16_bf16 on 4 x 4 sub-tiles. The
 // weight tile is the MFMA's A operand and the activation tile its B operand, so the accumulator of a

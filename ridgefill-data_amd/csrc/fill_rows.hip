@@ -1,7 +1,7 @@
-// Row-wise HBM-bound kernels of the fill: RMSNorm statistics of given inputs, the exact-row scatter,
-// the norm-gain fold, the RoPE table and the standalone RoPE + K / V cache write (fill_kv).
-// All of them move 16-byte chunks (8 bf16) per thread; 32 consecutive lanes cover one 256-column
-// group of a row, which is also the unit of the sum-of-squares partials.
+// Row-wise HBM-bound kernels of the fill: RMSNorm statistics of given inputs, the exact-row scatter and
+// gather, the norm-gain fold, the RoPE table and the standalone RoPE + K / V cache write (fill_kv).
+// The row-statistics kernels run one wave per row and form each 256-column group's sum of squares with
+// row_partials (rf_common.h), in the order the GEMM epilogue uses; the others move 16-byte chunks.
 #include <stdarg.h>
 #include <stdio.h>
 
