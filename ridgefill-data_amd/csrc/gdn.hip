@@ -13,14 +13,14 @@
 //     value heads' v, row norms, gates, G = K K^T on MFMA, A and T = (I + A)^-1 by forward substitution
 //     (fp32). Writes per chunk, in the MFMA operand order the scan reads: K (A operand of K S), K^T (A
 //     operand of K^T Z), T split into hi / lo bf16, V (accumulator layout) and the per-row scalars.
-//   k_gdn_scan (value head x 16-column block, one wave): the sequential chunk recurrence with the fp32
-//     state block [128 x 16] in registers. Each product runs on v_mfma_f32_16x16x32_bf16; fp32 operands
-//     (S, Y, Z, T) are split into hi + lo bf16 so each product keeps ~2^-16 relative accuracy. The
-//     in-lane order of the contraction index is permuted so that every product's accumulator layout
-//     is the next product's B operand (no LDS exchange): lane group g = lane / 16 holds contraction
-//     indices {32s + 4g + e, 32s + 16 + 4g + e : e < 4} of k-step s. The next chunk's operands
-//     (51 KB) stream into LDS by direct buffer loads while the current chunk computes from
-//     registers.
+//   k_gdn_scan (value head x 16-column block, 4 waves): the sequential chunk recurrence with the fp32
+//     state block [128 x 16] in registers, 32 rows per wave. Each product runs on
+//     v_mfma_f32_16x16x32_bf16; fp32 operands (S, Y, Z, T) are split into hi + lo bf16 so each product
+//     keeps ~2^-16 relative accuracy. The in-lane order of the contraction index is permuted so that an
+//     accumulator tile is a B-operand half as it stands: lane group g = lane / 16 holds contraction
+//     indices {32s + 4g + e, 32s + 16 + 4g + e : e < 4} of k-step s. The waves split each chunk's
+//     products four ways and meet three times per chunk in LDS (X partials, Y, Z); the next chunk's
+//     operands load into registers meanwhile.
 // k_conv_tail writes the new conv state (the last 3 pre-conv rows of [conv_in; pre]).
 #include <algorithm>
 
@@ -31,7 +31,6 @@ namespace {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef __attribute__((address_space(3))) void* lds_ptr;
 
 constexpr int DK = 128, DV = 128, CH = 64, TAPS = 4;
 constexpr int KST = DK + 8;                        // bf16 row stride of the k / v tiles in LDS
@@ -279,180 +278,174 @@ __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
 
 struct ScanArgs {
   const uint8_t* ws;
-  uint32_t chunk_bytes, ws_bytes;
+  uint32_t chunk_bytes;
   int chunks, nk, nv;
   float* state;             // [nv, DK, DV] fp32, updated in place
 };
 
-// LDS image of one chunk: K, K^T and T orders (16 KB each), this block's V columns (2 KB), the scalars
-constexpr uint32_t ST_KP = 0, ST_KTP = 16384, ST_TP = 32768, ST_VP = 49152, ST_SC = 51200, ST_BYTES = 52224;
+// One chunk's operands for wave w of a scan block, straight from the workspace into registers.
+struct ScanOps {
+  uint4 kp[4];              // K frags (row tile it, k-step w): A operand of X_w = K[:, 32w..] S_w
+  uint4 kt[2][2];           // K^T frags (row tile 2w + j, k-step s): A operand of the S update
+  uint4 tp[2][2];           // T frags (row tile w, k-step s, hi / lo); k-step 1 only for w >= 2
+  uint2 v;                  // V[16w + 4g + r][16 cb + n], r < 4
+  float4 be, qq, zz;        // beta, q, z of rows 16w + 4g + r
+  float decay;
+};
 
-// s_waitcnt vmcnt(0) (expcnt, lgkmcnt not waited) and s_waitcnt lgkmcnt(0) (vmcnt, expcnt not waited)
-__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt((0 & 15) | (7 << 4) | (15 << 8) | (0 << 14)); }
-__device__ __forceinline__ void wait_lgkm0() { __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14)); }
+__device__ __forceinline__ void load_ops(ScanOps& o, const uint8_t* chunk, uint32_t kh_off, uint32_t vh_off, int cb,
+                                         int w, int lane) {
+  const uint8_t* kb = chunk + kh_off + lane * 16;
+  const uint8_t* vb = chunk + vh_off;
+#pragma unroll
+  for (int it = 0; it < 4; ++it) o.kp[it] = *reinterpret_cast<const uint4*>(kb + (it * 4 + w) * 1024);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int s = 0; s < 2; ++s) o.kt[j][s] = *reinterpret_cast<const uint4*>(kb + KP_BYTES + ((2 * w + j) * 2 + s) * 1024);
+#pragma unroll
+  for (int s = 0; s < 2; ++s)
+#pragma unroll
+    for (int hl = 0; hl < 2; ++hl)
+      o.tp[s][hl] = (s == 0 || w >= 2) ? *reinterpret_cast<const uint4*>(vb + ((w * 2 + s) * 2 + hl) * 1024 + lane * 16)
+                                       : make_uint4(0u, 0u, 0u, 0u);
+  o.v = *reinterpret_cast<const uint2*>(vb + TP_BYTES + cb * 2048 + lane * 32 + w * 8);
+  const float* sc = reinterpret_cast<const float*>(vb + TP_BYTES + VP_BYTES);
+  const int r0 = 16 * w + 4 * (lane >> 4);
+  o.be = *reinterpret_cast<const float4*>(sc + SC_BETA + r0);
+  o.qq = *reinterpret_cast<const float4*>(sc + SC_Q + r0);
+  o.zz = *reinterpret_cast<const float4*>(sc + SC_Z + r0);
+  o.decay = sc[SC_DECAY];
+}
 
-__global__ __launch_bounds__(64) void k_gdn_scan(ScanArgs a) {
-  __shared__ __align__(16) uint8_t smem[ST_BYTES];
-  const int lane = threadIdx.x, gi = lane >> 4, ln = lane & 15;
+// 4 values -> hi (truncated to bf16) and lo (the rest rounded to bf16), as split8.
+__device__ __forceinline__ void split4(const float (&x)[4], uint2& hi, uint2& lo) {
+  uint32_t h[4], l[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t u = __float_as_uint(x[e]) & 0xffff0000u;
+    h[e] = u >> 16;
+    l[e] = f2bf(x[e] - __uint_as_float(u));
+  }
+  hi = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
+  lo = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+}
+
+// Block = (value head, 16-column block), 4 waves, one per SIMD. Wave w keeps state rows 32w .. 32w + 31
+// (row tiles 2w, 2w + 1, accumulator layout) and per chunk:
+//   X_w = K[:, 32w .. 32w + 31] S_w (its k-step of X = K S), then the four X_w meet in LDS and X = the
+//   sum over w in order; wave w forms row tile w of Y = beta (V - q X) and of v_new = T Y (T lower
+//   triangular: tiles 0 and 1 need k-step 0 only), and row tile w of Z = z v_new; Y and Z are shared as
+//   hi / lo bf16 B-operand frags through LDS; S_w <- decay S_w + K^T[32w .., :] Z.
+// Three barriers per chunk; the next chunk's operands load into registers while this one computes.
+__global__ __launch_bounds__(256) void k_gdn_scan(ScanArgs a) {
+  __shared__ __align__(16) f32x4 xp[4][4][64];        // X_w partials [wave][row tile][lane]
+  __shared__ __align__(16) uint4 yf[2][2][64];        // Y frags [k-step][hi / lo][lane]
+  __shared__ __align__(16) uint4 zf[2][2][64];        // Z frags
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, gi = lane >> 4, ln = lane & 15;
   // block b runs on XCD b % 8: XCD x takes (head, column block) pairs [x nv, (x + 1) nv), so the
   // blocks that share a head's (and a key head's) operands share an L2
   const int b = blockIdx.x, pair = (b & 7) * a.nv + (b >> 3);
   const int h = pair >> 3, cb = pair & 7, kh = h / (a.nv / a.nk);
   float* st = a.state + static_cast<size_t>(h) * DK * DV + cb * 16 + ln;
-  f32x4 S[8];
+  f32x4 S[2];
 #pragma unroll
-  for (int tt = 0; tt < 8; ++tt)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) S[tt][r] = st[(16 * tt + 4 * gi + r) * DV];
+    for (int r = 0; r < 4; ++r) S[j][r] = st[(16 * (2 * w + j) + 4 * gi + r) * DV];
 
-  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(a.ws), static_cast<short>(0),
-                                                                      static_cast<int>(a.ws_bytes), 0x00020000);
   const uint32_t kh_off = static_cast<uint32_t>(kh) * KH_BYTES;
   const uint32_t vh_off = static_cast<uint32_t>(a.nk) * KH_BYTES + static_cast<uint32_t>(h) * VH_BYTES;
-  const uint32_t lo = lane * 16;
-  // the chunk's operands, global -> LDS (1 KB per instruction: 64 lanes x 16 bytes)
-  auto issue = [&](int c) {
-    const uint32_t base = static_cast<uint32_t>(c) * a.chunk_bytes;
-#pragma unroll
-    for (int k = 0; k < 32; ++k)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(smem + ST_KP + k * 1024), 16, base + kh_off + k * 1024 + lo,
-                                               0, 0, 0);
-#pragma unroll
-    for (int k = 0; k < 16; ++k)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(smem + ST_TP + k * 1024), 16, base + vh_off + k * 1024 + lo,
-                                               0, 0, 0);
-#pragma unroll
-    for (int k = 0; k < 2; ++k)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(smem + ST_VP + k * 1024), 16,
-                                               base + vh_off + TP_BYTES + cb * 2048 + k * 1024 + lo, 0, 0, 0);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(smem + ST_SC), 16, base + vh_off + TP_BYTES + VP_BYTES + lo,
-                                             0, 0, 0);
-  };
-  auto frag = [&](uint32_t off) { return *reinterpret_cast<const uint4*>(smem + off + lo); };
-
-  issue(0);
+  ScanOps cur, nxt;
+  load_ops(cur, a.ws, kh_off, vh_off, cb, w, lane);
   for (int c = 0; c < a.chunks; ++c) {
-    // chunk c's operands: LDS -> registers, then the LDS takes chunk c + 1 while chunk c computes
-    wait_vm0();
-    __builtin_amdgcn_sched_barrier(0);
-    uint4 kp[4][4], ktp[8][2], tp[4][2][2];
-#pragma unroll
-    for (int it = 0; it < 4; ++it)
-#pragma unroll
-      for (int s = 0; s < 4; ++s) kp[it][s] = frag(ST_KP + (it * 4 + s) * 1024);
-#pragma unroll
-    for (int tt = 0; tt < 8; ++tt)
-#pragma unroll
-      for (int s = 0; s < 2; ++s) ktp[tt][s] = frag(ST_KTP + (tt * 2 + s) * 1024);
-#pragma unroll
-    for (int it = 0; it < 4; ++it)
-#pragma unroll
-      for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int hl = 0; hl < 2; ++hl)
-          if (s == 0 || it >= 2) tp[it][s][hl] = frag(ST_TP + ((it * 2 + s) * 2 + hl) * 1024);
-    const uint4 v0 = *reinterpret_cast<const uint4*>(smem + ST_VP + lane * 32);
-    const uint4 v1 = *reinterpret_cast<const uint4*>(smem + ST_VP + lane * 32 + 16);
-    const float* sc = reinterpret_cast<const float*>(smem + ST_SC);
-    float4 be[4], qq[4], zz[4];
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      be[it] = *reinterpret_cast<const float4*>(sc + SC_BETA + 16 * it + 4 * gi);
-      qq[it] = *reinterpret_cast<const float4*>(sc + SC_Q + 16 * it + 4 * gi);
-      zz[it] = *reinterpret_cast<const float4*>(sc + SC_Z + 16 * it + 4 * gi);
-    }
-    const float decay = sc[SC_DECAY];
-    wait_lgkm0();
-    __builtin_amdgcn_sched_barrier(0);
-    if (c + 1 < a.chunks) issue(c + 1);
-    __builtin_amdgcn_sched_barrier(0);
-    // X = K S
-    f32x4 X[4];
-#pragma unroll
-    for (int it = 0; it < 4; ++it) X[it] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
+    // the next chunk's operands (the last chunk reloads itself; the copy is not used)
+    load_ops(nxt, a.ws + static_cast<size_t>(min(c + 1, a.chunks - 1)) * a.chunk_bytes, kh_off, vh_off, cb, w, lane);
+    // X_w = K[:, 32w ..] S_w: S_w's rows in k-step order are (tile 2w, r) then (tile 2w + 1, r)
+    {
       float x[8];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        x[r] = S[2 * s][r];
-        x[4 + r] = S[2 * s + 1][r];
+        x[r] = S[0][r];
+        x[4 + r] = S[1][r];
       }
       uint4 bh, bl;
       split8(x, bh, bl);
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
-        X[it] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(kp[it][s]), as_frag(bh), X[it], 0, 0, 0);
-        X[it] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(kp[it][s]), as_frag(bl), X[it], 0, 0, 0);
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(cur.kp[it]), as_frag(bh), acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(cur.kp[it]), as_frag(bl), acc, 0, 0, 0);
+        xp[w][it][lane] = acc;
       }
     }
-    // Y = beta (V - q X), rows 16 it + 4 g + r
-    float Y[4][4];
+    __syncthreads();
+    // row tile w: X, Y = beta (V - q X), its hi / lo halves into k-step w / 2, slots 4 (w % 2) ..
+    {
+      f32x4 X = xp[0][w][lane];
 #pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const float bb[4] = {be[it].x, be[it].y, be[it].z, be[it].w}, q4[4] = {qq[it].x, qq[it].y, qq[it].z, qq[it].w};
+      for (int q = 1; q < 4; ++q) X += xp[q][w][lane];
+      const float bb[4] = {cur.be.x, cur.be.y, cur.be.z, cur.be.w}, q4[4] = {cur.qq.x, cur.qq.y, cur.qq.z, cur.qq.w};
+      const uint32_t vv[2] = {cur.v.x, cur.v.y};
+      float y[4];
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int e = 4 * it + r;
-        const float v = bf2f(lane_of(e < 8 ? v0 : v1, e & 7));
-        Y[it][r] = bb[r] * (v - q4[r] * X[it][r]);
+        const float v = bf2f((vv[r >> 1] >> (16 * (r & 1))) & 0xffffu);
+        y[r] = bb[r] * (v - q4[r] * X[r]);
       }
+      uint2 hi, lo;
+      split4(y, hi, lo);
+      reinterpret_cast<uint2*>(&yf[w >> 1][0][lane])[w & 1] = hi;
+      reinterpret_cast<uint2*>(&yf[w >> 1][1][lane])[w & 1] = lo;
     }
-    uint4 yh[2], yl[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      float x[8];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        x[r] = Y[2 * s][r];
-        x[4 + r] = Y[2 * s + 1][r];
-      }
-      split8(x, yh[s], yl[s]);
-    }
-    // v_new = T Y (T lower triangular: row tiles 0 and 1 need k-step 0 only)
-    f32x4 vn[4];
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      vn[it] = f32x4{0.f, 0.f, 0.f, 0.f};
+    __syncthreads();
+    // v_new row tile w = sum over k-steps of T Y; Z = z v_new into the Z frags
+    {
+      f32x4 vn = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        if (s == 1 && it < 2) continue;
-        const bf16x8 th = as_frag(tp[it][s][0]), tl = as_frag(tp[it][s][1]);
-        vn[it] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(th, as_frag(yh[s]), vn[it], 0, 0, 0);
-        vn[it] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(th, as_frag(yl[s]), vn[it], 0, 0, 0);
-        vn[it] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tl, as_frag(yh[s]), vn[it], 0, 0, 0);
+        if (s == 1 && w < 2) continue;
+        const bf16x8 th = as_frag(cur.tp[s][0]), tl = as_frag(cur.tp[s][1]);
+        const bf16x8 yh = as_frag(yf[s][0][lane]), yl = as_frag(yf[s][1][lane]);
+        vn = __builtin_amdgcn_mfma_f32_16x16x32_bf16(th, yh, vn, 0, 0, 0);
+        vn = __builtin_amdgcn_mfma_f32_16x16x32_bf16(th, yl, vn, 0, 0, 0);
+        vn = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tl, yh, vn, 0, 0, 0);
       }
+      const float z4[4] = {cur.zz.x, cur.zz.y, cur.zz.z, cur.zz.w};
+      float z[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) z[r] = z4[r] * vn[r];
+      uint2 hi, lo;
+      split4(z, hi, lo);
+      reinterpret_cast<uint2*>(&zf[w >> 1][0][lane])[w & 1] = hi;
+      reinterpret_cast<uint2*>(&zf[w >> 1][1][lane])[w & 1] = lo;
     }
-    // Z = z v_new; S <- decay S + K^T Z
-    uint4 zh[2], zl[2];
-#pragma unroll
-    for (int s = 0; s < 2; ++s) {
-      float x[8];
-#pragma unroll
-      for (int half = 0; half < 2; ++half) {
-        const int it = 2 * s + half;
-        const float z4[4] = {zz[it].x, zz[it].y, zz[it].z, zz[it].w};
-#pragma unroll
-        for (int r = 0; r < 4; ++r) x[4 * half + r] = z4[r] * vn[it][r];
-      }
-      split8(x, zh[s], zl[s]);
-    }
-#pragma unroll
-    for (int tt = 0; tt < 8; ++tt) {
-      f32x4 acc = S[tt] * decay;
+    __syncthreads();
+    // S_w <- decay S_w + K^T Z
+    {
+      bf16x8 zh[2], zl[2];
 #pragma unroll
       for (int s = 0; s < 2; ++s) {
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(ktp[tt][s]), as_frag(zh[s]), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(ktp[tt][s]), as_frag(zl[s]), acc, 0, 0, 0);
+        zh[s] = as_frag(zf[s][0][lane]);
+        zl[s] = as_frag(zf[s][1][lane]);
       }
-      S[tt] = acc;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        f32x4 acc = S[j] * cur.decay;
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(cur.kt[j][s]), zh[s], acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(cur.kt[j][s]), zl[s], acc, 0, 0, 0);
+        }
+        S[j] = acc;
+      }
     }
+    cur = nxt;
   }
-  wait_vm0();
 #pragma unroll
-  for (int tt = 0; tt < 8; ++tt)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) st[(16 * tt + 4 * gi + r) * DV] = S[tt][r];
+    for (int r = 0; r < 4; ++r) st[(16 * (2 * w + j) + 4 * gi + r) * DV] = S[j][r];
 }
 
 // conv_out[j][ch] = row P - 3 + j of [conv_in; pre] (conv_in rows -3..-1; zeros if conv_in is null)
@@ -514,8 +507,8 @@ extern "C" int rf_gdn_fill(const uint16_t* pre, int64_t ld, int64_t P, int nk, i
                 static_cast<uint8_t*>(workspace), cbytes};
     hipLaunchKernelGGL(k_gdn_prep, dim3(nc, nk), dim3(256), 0, stream, pa);
     if (const int e = check_launch("rf_gdn_fill (prep)")) return e;
-    ScanArgs sa{static_cast<const uint8_t*>(workspace), cbytes, static_cast<uint32_t>(nc) * cbytes, nc, nk, nv, state};
-    hipLaunchKernelGGL(k_gdn_scan, dim3(nv * 8), dim3(64), 0, stream, sa);
+    ScanArgs sa{static_cast<const uint8_t*>(workspace), cbytes, nc, nk, nv, state};
+    hipLaunchKernelGGL(k_gdn_scan, dim3(nv * 8), dim3(256), 0, stream, sa);
     if (const int e = check_launch("rf_gdn_fill (scan)")) return e;
   }
   hipLaunchKernelGGL(k_conv_tail, dim3((3 * C + 255) / 256), dim3(256), 0, stream, pre, ld, P, static_cast<int>(C),
