@@ -9,8 +9,8 @@
 // with K the raw (bf16) conv output, so K K^T, K S and K^T Z multiply exact bf16 values.
 //
 // Two kernels per pass of up to `chunks` chunks:
-//   k_gdn_prep (chunk x key head, 256 threads): conv + SiLU of the key head's k and of each of its
-//     value heads' v, row norms, gates, G = K K^T on MFMA, A and T = (I + A)^-1 by forward substitution
+//   k_gdn_prep (chunk x value head, 256 threads): conv + SiLU of the key head's k and of the value
+//     head's v, row norms, gates, G = K K^T on MFMA, A and T = (I + A)^-1 by forward substitution
 //     (fp32). Writes per chunk, in the MFMA operand order the scan reads: K (A operand of K S), K^T (A
 //     operand of K^T Z), T split into hi / lo bf16, V (accumulator layout) and the per-row scalars.
 //   k_gdn_scan (value head x 16-column block, 4 waves): the sequential chunk recurrence with the fp32
@@ -123,20 +123,39 @@ __device__ __forceinline__ void conv_tile(const PrepArgs& a, int64_t p0, int m, 
   }
 }
 
+// Block = (chunk, value head h). The K-side work (conv of the key head's k, norms, G = K K^T) is
+// recomputed by each of the key head's value heads; the first of them writes K's operand orders.
 __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
   __shared__ __align__(16) uint16_t k_s[CH * KST];
   __shared__ __align__(16) uint16_t v_s[CH * KST];
-  __shared__ __align__(16) float g_s[CH * FST];     // K K^T
   __shared__ __align__(16) float a_s[CH * FST];     // A, then T
   __shared__ float r_s[CH], beta_s[CH], gate_s[CH], gam_s[CH];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, gi = lane >> 4, ln = lane & 15;
-  const int c = blockIdx.x, kh = blockIdx.y, rep = a.nv / a.nk;
+  const int c = blockIdx.x, h = blockIdx.y, rep = a.nv / a.nk, kh = h / rep;
   const int64_t p0 = a.p_begin + static_cast<int64_t>(c) * CH;
   const int m = static_cast<int>(min(static_cast<int64_t>(CH), a.P - p0));
   uint8_t* cbase = a.ws + static_cast<size_t>(c) * a.chunk_bytes;
 
+  // row t's gate inputs first, so their latency overlaps the conv loads
+  float braw = 0.f, araw = 0.f;
+  if (t < m) {
+    const int64_t row = (p0 + t) * a.ld;
+    braw = bf2f(a.pre[row + a.C + h]);
+    araw = bf2f(a.pre[row + a.C + a.nv + h]);
+  }
   conv_tile(a, p0, m, a.nk * DK + kh * DK, k_s);
+  conv_tile(a, p0, m, 2 * a.nk * DK + h * DV, v_s);
+  if (t < CH) {
+    float beta = 0.f, g = 0.f;
+    if (t < m) {
+      beta = bf2f(f2bf(1.0f / (1.0f + expf(-braw))));
+      const float av = araw + a.dt_bias[h];
+      g = -expf(a.a_log[h]) * (av > 20.0f ? av : log1pf(expf(av)));
+    }
+    beta_s[t] = beta;
+    gate_s[t] = g;
+  }
   __syncthreads();
   {  // row norms: 4 threads per row
     const int row = t >> 2, q = (t & 3) * 32;
@@ -149,20 +168,26 @@ __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
     s += __shfl_xor(s, 2, 64);
     if ((t & 3) == 0) r_s[row] = 1.0f / sqrtf(s + 1e-6f);
   }
-  // G = K K^T, lower 16 x 16 tiles: wave w computes tile row w
-  for (int tj = 0; tj <= wave; ++tj) {
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+  if (t < CH) {  // gamma_t = gate_0 + ... + gate_t, added in row order (the serial cumsum's bits)
+    float acc = 0.f;
+    for (int i = 0; i <= t; ++i) acc += gate_s[i];
+    gam_s[t] = acc;
+  }
+  // G = K K^T, lower 16 x 16 tiles of tile row `wave`, kept in registers
+  f32x4 G[4];
+#pragma unroll
+  for (int tj = 0; tj < 4; ++tj) {
+    G[tj] = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (tj > wave) continue;
 #pragma unroll
     for (int s = 0; s < 4; ++s) {
       const uint4 ua = *reinterpret_cast<const uint4*>(k_s + (16 * wave + ln) * KST + 32 * s + 8 * gi);
       const uint4 ub = *reinterpret_cast<const uint4*>(k_s + (16 * tj + ln) * KST + 32 * s + 8 * gi);
-      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(ua), as_frag(ub), acc, 0, 0, 0);
+      G[tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(ua), as_frag(ub), G[tj], 0, 0, 0);
     }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) g_s[(16 * wave + 4 * gi + r) * FST + 16 * tj + ln] = acc[r];
   }
-  {  // K in the scan's operand orders: Kp [it][s][lane][8] = K[16 it + lane % 16][kperm(s, g, e)],
-     // Ktp [t][s][lane][8] = K[kperm(s, g, e)][16 t + lane % 16]
+  if (h % rep == 0) {  // K in the scan's operand orders: Kp [it][s][lane][8] = K[16 it + lane % 16][kperm(s, g, e)],
+                       // Ktp [t][s][lane][8] = K[kperm(s, g, e)][16 t + lane % 16]
     uint4* kp = reinterpret_cast<uint4*>(cbase + static_cast<size_t>(kh) * KH_BYTES);
     uint4* ktp = reinterpret_cast<uint4*>(cbase + static_cast<size_t>(kh) * KH_BYTES + KP_BYTES);
 #pragma unroll
@@ -183,95 +208,75 @@ __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
       }
     }
   }
-  for (int hv = 0; hv < rep; ++hv) {
-    const int h = kh * rep + hv;
-    __syncthreads();                              // g_s / r_s ready; v_s and a_s free again
-    conv_tile(a, p0, m, 2 * a.nk * DK + h * DV, v_s);
-    if (t < CH) {
-      float beta = 0.f, g = 0.f;
-      if (t < m) {
-        const int64_t row = (p0 + t) * a.ld;
-        const float b = bf2f(a.pre[row + a.C + h]);
-        beta = bf2f(f2bf(1.0f / (1.0f + expf(-b))));
-        const float av = bf2f(a.pre[row + a.C + a.nv + h]) + a.dt_bias[h];
-        g = -expf(a.a_log[h]) * (av > 20.0f ? av : log1pf(expf(av)));
-      }
-      beta_s[t] = beta;
-      gate_s[t] = g;
+  __syncthreads();                                  // r_s, gam_s ready
+  // A = tril_{-1}(beta_i (G_ij r_i r_j) e^{gamma_i - gamma_j}); lane (gi, ln) holds G[16 wave + 4 gi + r][16 tj + ln]
+#pragma unroll
+  for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int i = 16 * wave + 4 * gi + r, j = 16 * tj + ln;
+      a_s[i * FST + j] = (tj <= wave && j < i)
+                             ? (beta_s[i] * (G[tj][r] * r_s[i] * r_s[j])) * expf(gam_s[i] - gam_s[j])
+                             : 0.f;
     }
-    __syncthreads();
-    if (t == 0) {
-      float acc = 0.f;
-      for (int i = 0; i < CH; ++i) {
-        acc += gate_s[i];
-        gam_s[i] = acc;
+  __syncthreads();
+  uint8_t* vbase = cbase + static_cast<size_t>(a.nk) * KH_BYTES + static_cast<size_t>(h) * VH_BYTES;
+  if (wave == 0) {
+    // T = (I + A)^-1: lane j holds column j; T[i][j] = delta_ij - sum_{m < i} A[i][m] T[m][j]
+    // (A is zero on and above the diagonal and tc[m] is zero until row m is done)
+    float tc[CH];
+#pragma unroll
+    for (int i = 0; i < CH; ++i) tc[i] = 0.f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      float acc0 = (i == lane) ? 1.f : 0.f, acc1 = 0.f;
+#pragma unroll
+      for (int q = 0; q < i; q += 4) {
+        const float4 av = *reinterpret_cast<const float4*>(a_s + i * FST + q);
+        acc0 = fmaf(-av.x, tc[q], acc0);
+        acc1 = fmaf(-av.y, tc[q + 1], acc1);
+        acc0 = fmaf(-av.z, tc[q + 2], acc0);
+        acc1 = fmaf(-av.w, tc[q + 3], acc1);
       }
+      tc[i] = acc0 + acc1;
     }
-    __syncthreads();
-#pragma unroll 4
-    for (int k = 0; k < 16; ++k) {
-      const int idx = t + 256 * k, i = idx >> 6, j = idx & 63;
-      a_s[i * FST + j] = j < i ? (beta_s[i] * (g_s[i * FST + j] * r_s[i] * r_s[j])) * expf(gam_s[i] - gam_s[j]) : 0.f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) a_s[i * FST + lane] = tc[i];
+  } else {
+    // V in the scan's accumulator order: Vp [cb][lane][4 it + r] = V[16 it + 4 g + r][16 cb + lane % 16]
+    uint4* vp = reinterpret_cast<uint4*>(vbase + TP_BYTES);
+    for (int idx = t - 64; idx < 512; idx += 192) {
+      const int cb = idx >> 6, l = idx & 63, g = l >> 4, n = l & 15;
+      uint16_t v[16];
+#pragma unroll
+      for (int it = 0; it < 4; ++it)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) v[4 * it + r] = v_s[(16 * it + 4 * g + r) * KST + 16 * cb + n];
+      vp[2 * idx] = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+      vp[2 * idx + 1] = make_uint4(pack2(v[8], v[9]), pack2(v[10], v[11]), pack2(v[12], v[13]), pack2(v[14], v[15]));
     }
-    __syncthreads();
-    uint8_t* vbase = cbase + static_cast<size_t>(a.nk) * KH_BYTES + static_cast<size_t>(h) * VH_BYTES;
-    if (wave == 0) {
-      // T = (I + A)^-1: lane j holds column j; T[i][j] = delta_ij - sum_{m < i} A[i][m] T[m][j]
-      // (A is zero on and above the diagonal and tc[m] is zero until row m is done)
-      float tc[CH];
-#pragma unroll
-      for (int i = 0; i < CH; ++i) tc[i] = 0.f;
-#pragma unroll
-      for (int i = 0; i < CH; ++i) {
-        float acc0 = (i == lane) ? 1.f : 0.f, acc1 = 0.f;
-#pragma unroll
-        for (int q = 0; q < i; q += 4) {
-          const float4 av = *reinterpret_cast<const float4*>(a_s + i * FST + q);
-          acc0 = fmaf(-av.x, tc[q], acc0);
-          acc1 = fmaf(-av.y, tc[q + 1], acc1);
-          acc0 = fmaf(-av.z, tc[q + 2], acc0);
-          acc1 = fmaf(-av.w, tc[q + 3], acc1);
-        }
-        tc[i] = acc0 + acc1;
-      }
-#pragma unroll
-      for (int i = 0; i < CH; ++i) a_s[i * FST + lane] = tc[i];
-    } else {
-      // V in the scan's accumulator order: Vp [cb][lane][4 it + r] = V[16 it + 4 g + r][16 cb + lane % 16]
-      uint4* vp = reinterpret_cast<uint4*>(vbase + TP_BYTES);
-      for (int idx = t - 64; idx < 512; idx += 192) {
-        const int cb = idx >> 6, l = idx & 63, g = l >> 4, n = l & 15;
-        uint16_t v[16];
-#pragma unroll
-        for (int it = 0; it < 4; ++it)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) v[4 * it + r] = v_s[(16 * it + 4 * g + r) * KST + 16 * cb + n];
-        vp[2 * idx] = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
-        vp[2 * idx + 1] = make_uint4(pack2(v[8], v[9]), pack2(v[10], v[11]), pack2(v[12], v[13]), pack2(v[14], v[15]));
-      }
-      if (wave == 1) {
-        float* sc = reinterpret_cast<float*>(vbase + TP_BYTES + VP_BYTES);
-        const float gl = gam_s[CH - 1];
-        sc[SC_BETA + lane] = beta_s[lane];
-        sc[SC_Q + lane] = expf(gam_s[lane]) * r_s[lane];
-        sc[SC_Z + lane] = r_s[lane] * expf(gl - gam_s[lane]);
-        sc[SC_DECAY + lane] = lane == 0 ? expf(gl) : 0.f;
-      }
+    if (wave == 1) {
+      float* sc = reinterpret_cast<float*>(vbase + TP_BYTES + VP_BYTES);
+      const float gl = gam_s[CH - 1];
+      sc[SC_BETA + lane] = beta_s[lane];
+      sc[SC_Q + lane] = expf(gam_s[lane]) * r_s[lane];
+      sc[SC_Z + lane] = r_s[lane] * expf(gl - gam_s[lane]);
+      sc[SC_DECAY + lane] = lane == 0 ? expf(gl) : 0.f;
     }
-    __syncthreads();
-    {  // T split hi / lo in the scan's A-operand order: Tp [it][s][hl][lane][8] = T[16 it + lane % 16][kperm(s, g, e)]
-      uint4* tp = reinterpret_cast<uint4*>(vbase);
+  }
+  __syncthreads();
+  {  // T split hi / lo in the scan's A-operand order: Tp [it][s][hl][lane][8] = T[16 it + lane % 16][kperm(s, g, e)]
+    uint4* tp = reinterpret_cast<uint4*>(vbase);
 #pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int idx = t + 256 * k, it = idx >> 7, s = (idx >> 6) & 1, l = idx & 63, g = l >> 4, n = l & 15;
-        float x[8];
+    for (int k = 0; k < 2; ++k) {
+      const int idx = t + 256 * k, it = idx >> 7, s = (idx >> 6) & 1, l = idx & 63, g = l >> 4, n = l & 15;
+      float x[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = a_s[(16 * it + n) * FST + kperm(s, g, e)];
-        uint4 hi, lo;
-        split8(x, hi, lo);
-        tp[((it * 2 + s) * 2 + 0) * 64 + l] = hi;
-        tp[((it * 2 + s) * 2 + 1) * 64 + l] = lo;
-      }
+      for (int e = 0; e < 8; ++e) x[e] = a_s[(16 * it + n) * FST + kperm(s, g, e)];
+      uint4 hi, lo;
+      split8(x, hi, lo);
+      tp[((it * 2 + s) * 2 + 0) * 64 + l] = hi;
+      tp[((it * 2 + s) * 2 + 1) * 64 + l] = lo;
     }
   }
 }
@@ -505,7 +510,7 @@ extern "C" int rf_gdn_fill(const uint16_t* pre, int64_t ld, int64_t P, int nk, i
     const int nc = static_cast<int>(std::min<int64_t>(per_pass, chunks - c0));
     PrepArgs pa{pre, ld, P, c0 * CH, nk, nv, static_cast<int>(C), conv_w, conv_in, a_log, dt_bias,
                 static_cast<uint8_t*>(workspace), cbytes};
-    hipLaunchKernelGGL(k_gdn_prep, dim3(nc, nk), dim3(256), 0, stream, pa);
+    hipLaunchKernelGGL(k_gdn_prep, dim3(nc, nv), dim3(256), 0, stream, pa);
     if (const int e = check_launch("rf_gdn_fill (prep)")) return e;
     ScanArgs sa{static_cast<const uint8_t*>(workspace), cbytes, nc, nk, nv, state};
     hipLaunchKernelGGL(k_gdn_scan, dim3(nv * 8), dim3(256), 0, stream, sa);
