@@ -47,17 +47,18 @@ __device__ __forceinline__ int kperm(int s, int g, int e) { return 32 * s + 4 * 
 
 __device__ __forceinline__ bf16x8 as_frag(const uint4& u) { return __builtin_bit_cast(bf16x8, u); }
 
-// x = hi + lo: hi = x truncated to bf16, lo = (x - hi) rounded to bf16.
+// x = hi + lo: hi = x truncated to bf16, lo = (x - hi) rounded to bf16 (pairs in one v_cvt_pk_bf16_f32).
 __device__ __forceinline__ void split8(const float (&x)[8], uint4& hi, uint4& lo) {
-  uint32_t h[8], l[8];
+  uint32_t h[8];
+  float r[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const uint32_t u = __float_as_uint(x[e]) & 0xffff0000u;
     h[e] = u >> 16;
-    l[e] = f2bf(x[e] - __uint_as_float(u));
+    r[e] = x[e] - __uint_as_float(u);
   }
   hi = make_uint4(h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16));
-  lo = make_uint4(l[0] | (l[1] << 16), l[2] | (l[3] << 16), l[4] | (l[5] << 16), l[6] | (l[7] << 16));
+  lo = make_uint4(bf16_pair(r[0], r[1]), bf16_pair(r[2], r[3]), bf16_pair(r[4], r[5]), bf16_pair(r[6], r[7]));
 }
 
 struct PrepArgs {
@@ -292,7 +293,7 @@ struct ScanArgs {
 struct ScanOps {
   uint4 kp[4];              // K frags (row tile it, k-step w): A operand of X_w = K[:, 32w..] S_w
   uint4 kt[2][2];           // K^T frags (row tile 2w + j, k-step s): A operand of the S update
-  uint4 tp[2][2];           // T frags (row tile w, k-step s, hi / lo); k-step 1 only for w >= 2
+  uint4 tp[2][2];           // T frags (row tile w, k-step s, hi / lo); k-step 1 used only for w >= 2
   uint2 v;                  // V[16w + 4g + r][16 cb + n], r < 4
   float4 be, qq, zz;        // beta, q, z of rows 16w + 4g + r
   float decay;
@@ -308,12 +309,11 @@ __device__ __forceinline__ void load_ops(ScanOps& o, const uint8_t* chunk, uint3
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int s = 0; s < 2; ++s) o.kt[j][s] = *reinterpret_cast<const uint4*>(kb + KP_BYTES + ((2 * w + j) * 2 + s) * 1024);
+  // every wave issues the same loads (uniform wait counts); waves 0 and 1 fetch a k-step 1 frag they skip
 #pragma unroll
   for (int s = 0; s < 2; ++s)
 #pragma unroll
-    for (int hl = 0; hl < 2; ++hl)
-      o.tp[s][hl] = (s == 0 || w >= 2) ? *reinterpret_cast<const uint4*>(vb + ((w * 2 + s) * 2 + hl) * 1024 + lane * 16)
-                                       : make_uint4(0u, 0u, 0u, 0u);
+    for (int hl = 0; hl < 2; ++hl) o.tp[s][hl] = *reinterpret_cast<const uint4*>(vb + ((w * 2 + s) * 2 + hl) * 1024 + lane * 16);
   o.v = *reinterpret_cast<const uint2*>(vb + TP_BYTES + cb * 2048 + lane * 32 + w * 8);
   const float* sc = reinterpret_cast<const float*>(vb + TP_BYTES + VP_BYTES);
   const int r0 = 16 * w + 4 * (lane >> 4);
@@ -325,15 +325,16 @@ __device__ __forceinline__ void load_ops(ScanOps& o, const uint8_t* chunk, uint3
 
 // 4 values -> hi (truncated to bf16) and lo (the rest rounded to bf16), as split8.
 __device__ __forceinline__ void split4(const float (&x)[4], uint2& hi, uint2& lo) {
-  uint32_t h[4], l[4];
+  uint32_t h[4];
+  float r[4];
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const uint32_t u = __float_as_uint(x[e]) & 0xffff0000u;
     h[e] = u >> 16;
-    l[e] = f2bf(x[e] - __uint_as_float(u));
+    r[e] = x[e] - __uint_as_float(u);
   }
   hi = make_uint2(h[0] | (h[1] << 16), h[2] | (h[3] << 16));
-  lo = make_uint2(l[0] | (l[1] << 16), l[2] | (l[3] << 16));
+  lo = make_uint2(bf16_pair(r[0], r[1]), bf16_pair(r[2], r[3]));
 }
 
 // Block = (value head, 16-column block), 4 waves, one per SIMD. Wave w keeps state rows 32w .. 32w + 31

@@ -22,10 +22,10 @@ __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(stati
 
 // fp32 -> bf16, round to nearest even (the rounding torch's .to(torch.bfloat16) performs).
 __device__ __forceinline__ uint16_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<uint16_t>((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<uint16_t>(u >> 16);
+  const uint32_t u = __float_as_uint(f);
+  const uint32_t rounded = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  const uint32_t quiet_nan = (u >> 16) | 0x40u;
+  return static_cast<uint16_t>((u & 0x7fffffffu) > 0x7f800000u ? quiet_nan : rounded);   // a select, no branch
 }
 
 typedef float rf_f32x2 __attribute__((ext_vector_type(2)));
