@@ -86,28 +86,35 @@ __device__ __forceinline__ uint4 pre_row(const PrepArgs& a, int64_t p, int ch0) 
 
 // Conv + SiLU (bf16) of 8 channels over 4 output rows (thread t: channel group t % 16, rows
 // 4 (t / 16) .. + 3) into dst [64][KST]; taps accumulate oldest first, products and sums rounded
-// separately as the reference's fp32 tap loop; rows at or past m are zero.
-__device__ __forceinline__ void conv_tile(const PrepArgs& a, int64_t p0, int m, int ch_base, uint16_t* dst) {
+// separately as the reference's fp32 tap loop; rows at or past m are zero. conv_load issues the
+// thread's loads (weights of its 8 channels, input rows r0 - 3 .. r0 + 3) so that several tiles' loads
+// can be in flight together; conv_store computes and writes.
+struct ConvIn {
+  uint4 w[4];               // channel pairs (ch0 + 2j, ch0 + 2j + 1) x 4 taps
+  uint4 x[7];
+};
+
+__device__ __forceinline__ void conv_load(const PrepArgs& a, int64_t p0, int ch_base, ConvIn& in) {
   const int t = threadIdx.x, cg = t & 15, r0 = (t >> 4) * 4;
   const int ch0 = ch_base + cg * 8;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) in.w[j] = *reinterpret_cast<const uint4*>(a.conv_w + (ch0 + 2 * j) * TAPS);
+#pragma unroll
+  for (int j = 0; j < 7; ++j) in.x[j] = pre_row(a, p0 + r0 - 3 + j, ch0);
+}
+
+__device__ __forceinline__ void conv_store(const ConvIn& in, int m, uint16_t* dst) {
+  const int t = threadIdx.x, cg = t & 15, r0 = (t >> 4) * 4;
   float w[8][TAPS];
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const uint4 u0 = *reinterpret_cast<const uint4*>(a.conv_w + (ch0 + 4 * q) * TAPS);
-    const uint4 u1 = *reinterpret_cast<const uint4*>(a.conv_w + (ch0 + 4 * q) * TAPS + 8);
+  for (int j = 0; j < 4; ++j)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      w[4 * q + e / 4][e % 4] = bf2f(lane_of(u0, e));
-      w[4 * q + 2 + e / 4][e % 4] = bf2f(lane_of(u1, e));
-    }
-  }
+    for (int e = 0; e < 8; ++e) w[2 * j + e / 4][e % 4] = bf2f(lane_of(in.w[j], e));
   float x[7][8];
 #pragma unroll
-  for (int j = 0; j < 7; ++j) {
-    const uint4 u = pre_row(a, p0 + r0 - 3 + j, ch0);
+  for (int j = 0; j < 7; ++j)
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[j][e] = bf2f(lane_of(u, e));
-  }
+    for (int e = 0; e < 8; ++e) x[j][e] = bf2f(lane_of(in.x[j], e));
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     uint16_t o[8];
@@ -117,19 +124,28 @@ __device__ __forceinline__ void conv_tile(const PrepArgs& a, int64_t p0, int m, 
       acc = __fadd_rn(acc, __fmul_rn(x[q + 1][e], w[e][1]));
       acc = __fadd_rn(acc, __fmul_rn(x[q + 2][e], w[e][2]));
       acc = __fadd_rn(acc, __fmul_rn(x[q + 3][e], w[e][3]));
-      o[e] = (r0 + q < m) ? f2bf(acc / (1.0f + expf(-acc))) : 0;
+      // SiLU with the hardware exp2 and reciprocal (about 1 ulp each, before the bf16 rounding)
+      o[e] = (r0 + q < m) ? f2bf(acc * __builtin_amdgcn_rcpf(1.0f + __expf(-acc))) : 0;
     }
     *reinterpret_cast<uint4*>(dst + (r0 + q) * KST + cg * 8) =
         make_uint4(pack2(o[0], o[1]), pack2(o[2], o[3]), pack2(o[4], o[5]), pack2(o[6], o[7]));
   }
 }
 
+// Sum of a value over the 4 lanes of each lane quad (DPP quad permutes, no LDS round trip); every lane
+// of the quad gets the same bits ((l0 + l1) + (l2 + l3) in either order of the commutative adds).
+__device__ __forceinline__ float quad_sum(float v) {
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0xb1, 0xf, 0xf, false));  // lanes ^ 1
+  v += __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x4e, 0xf, 0xf, false));  // lanes ^ 2
+  return v;
+}
+
 // Block = (chunk, value head h). The K-side work (conv of the key head's k, norms, G = K K^T) is
 // recomputed by each of the key head's value heads; the first of them writes K's operand orders.
 __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
-  __shared__ __align__(16) uint16_t k_s[CH * KST];
+  __shared__ __align__(16) uint16_t k_s[CH * KST];  // the k tile, then T (fp32)
   __shared__ __align__(16) uint16_t v_s[CH * KST];
-  __shared__ __align__(16) float a_s[CH * FST];     // A, then T
+  __shared__ __align__(16) float a_s[CH * FST];     // A
   __shared__ float r_s[CH], beta_s[CH], gate_s[CH], gam_s[CH];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, gi = lane >> 4, ln = lane & 15;
@@ -145,8 +161,13 @@ __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
     braw = bf2f(a.pre[row + a.C + h]);
     araw = bf2f(a.pre[row + a.C + a.nv + h]);
   }
-  conv_tile(a, p0, m, a.nk * DK + kh * DK, k_s);
-  conv_tile(a, p0, m, 2 * a.nk * DK + h * DV, v_s);
+  {
+    ConvIn ik, iv;
+    conv_load(a, p0, a.nk * DK + kh * DK, ik);
+    conv_load(a, p0, 2 * a.nk * DK + h * DV, iv);
+    conv_store(ik, m, k_s);
+    conv_store(iv, m, v_s);
+  }
   if (t < CH) {
     float beta = 0.f, g = 0.f;
     if (t < m) {
@@ -209,7 +230,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
       }
     }
   }
-  __syncthreads();                                  // r_s, gam_s ready
+  __syncthreads();                                  // r_s, gam_s ready; k_s free
   // A = tril_{-1}(beta_i (G_ij r_i r_j) e^{gamma_i - gamma_j}); lane (gi, ln) holds G[16 wave + 4 gi + r][16 tj + ln]
 #pragma unroll
   for (int tj = 0; tj < 4; ++tj)
@@ -220,34 +241,12 @@ __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
                              ? (beta_s[i] * (G[tj][r] * r_s[i] * r_s[j])) * expf(gam_s[i] - gam_s[j])
                              : 0.f;
     }
-  __syncthreads();
   uint8_t* vbase = cbase + static_cast<size_t>(a.nk) * KH_BYTES + static_cast<size_t>(h) * VH_BYTES;
-  if (wave == 0) {
-    // T = (I + A)^-1: lane j holds column j; T[i][j] = delta_ij - sum_{m < i} A[i][m] T[m][j]
-    // (A is zero on and above the diagonal and tc[m] is zero until row m is done)
-    float tc[CH];
-#pragma unroll
-    for (int i = 0; i < CH; ++i) tc[i] = 0.f;
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      float acc0 = (i == lane) ? 1.f : 0.f, acc1 = 0.f;
-#pragma unroll
-      for (int q = 0; q < i; q += 4) {
-        const float4 av = *reinterpret_cast<const float4*>(a_s + i * FST + q);
-        acc0 = fmaf(-av.x, tc[q], acc0);
-        acc1 = fmaf(-av.y, tc[q + 1], acc1);
-        acc0 = fmaf(-av.z, tc[q + 2], acc0);
-        acc1 = fmaf(-av.w, tc[q + 3], acc1);
-      }
-      tc[i] = acc0 + acc1;
-    }
-#pragma unroll
-    for (int i = 0; i < CH; ++i) a_s[i * FST + lane] = tc[i];
-  } else {
-    // V in the scan's accumulator order: Vp [cb][lane][4 it + r] = V[16 it + 4 g + r][16 cb + lane % 16]
+  {  // V in the scan's accumulator order: Vp [cb][lane][4 it + r] = V[16 it + 4 g + r][16 cb + lane % 16]
     uint4* vp = reinterpret_cast<uint4*>(vbase + TP_BYTES);
-    for (int idx = t - 64; idx < 512; idx += 192) {
-      const int cb = idx >> 6, l = idx & 63, g = l >> 4, n = l & 15;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int idx = t + 256 * k, cb = idx >> 6, l = idx & 63, g = l >> 4, n = l & 15;
       uint16_t v[16];
 #pragma unroll
       for (int it = 0; it < 4; ++it)
@@ -256,14 +255,41 @@ __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
       vp[2 * idx] = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
       vp[2 * idx + 1] = make_uint4(pack2(v[8], v[9]), pack2(v[10], v[11]), pack2(v[12], v[13]), pack2(v[14], v[15]));
     }
-    if (wave == 1) {
-      float* sc = reinterpret_cast<float*>(vbase + TP_BYTES + VP_BYTES);
-      const float gl = gam_s[CH - 1];
-      sc[SC_BETA + lane] = beta_s[lane];
-      sc[SC_Q + lane] = expf(gam_s[lane]) * r_s[lane];
-      sc[SC_Z + lane] = r_s[lane] * expf(gl - gam_s[lane]);
-      sc[SC_DECAY + lane] = lane == 0 ? expf(gl) : 0.f;
+  }
+  if (wave == 1) {
+    float* sc = reinterpret_cast<float*>(vbase + TP_BYTES + VP_BYTES);
+    const float gl = gam_s[CH - 1];
+    sc[SC_BETA + lane] = beta_s[lane];
+    sc[SC_Q + lane] = expf(gam_s[lane]) * r_s[lane];
+    sc[SC_Z + lane] = r_s[lane] * expf(gl - gam_s[lane]);
+    sc[SC_DECAY + lane] = lane == 0 ? expf(gl) : 0.f;
+  }
+  __syncthreads();                                  // A complete
+  float* t_s = reinterpret_cast<float*>(k_s);       // T [64][FST] fp32 in the k tile's space
+  {
+    // T = (I + A)^-1 by forward substitution, T[i][j] = delta_ij - sum_{m < i} A[i][m] T[m][j]. Wave w takes
+    // columns 16w .. 16w + 15, four lanes per column: part p sums the terms m = 4k + p (two accumulators,
+    // k even / odd) and keeps T[4k + p][j]; a quad sum combines the parts. A is zero on and above the
+    // diagonal and tk is zero until its row is done, so every term past row i vanishes.
+    const int col = 16 * wave + (lane >> 2), part = lane & 3;
+    float tk[16];
+#pragma unroll
+    for (int k = 0; k < 16; ++k) tk[k] = 0.f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      float acc0 = 0.f, acc1 = 0.f;
+#pragma unroll
+      for (int k = 0; 4 * k < i; ++k) {
+        const float av = a_s[i * FST + 4 * k + part];
+        if (k & 1) acc1 = fmaf(-av, tk[k], acc1);
+        else acc0 = fmaf(-av, tk[k], acc0);
+      }
+      const float sum = quad_sum(acc0 + acc1);
+      const float tij = (i == col ? 1.f : 0.f) + sum;
+      if (part == (i & 3)) tk[i >> 2] = tij;
     }
+#pragma unroll
+    for (int k = 0; k < 16; ++k) t_s[(4 * k + part) * FST + col] = tk[k];
   }
   __syncthreads();
   {  // T split hi / lo in the scan's A-operand order: Tp [it][s][hl][lane][8] = T[16 it + lane % 16][kperm(s, g, e)]
@@ -273,7 +299,7 @@ __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
       const int idx = t + 256 * k, it = idx >> 7, s = (idx >> 6) & 1, l = idx & 63, g = l >> 4, n = l & 15;
       float x[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) x[e] = a_s[(16 * it + n) * FST + kperm(s, g, e)];
+      for (int e = 0; e < 8; ++e) x[e] = t_s[(16 * it + n) * FST + kperm(s, g, e)];
       uint4 hi, lo;
       split8(x, hi, lo);
       tp[((it * 2 + s) * 2 + 0) * 64 + l] = hi;
@@ -299,28 +325,42 @@ struct ScanOps {
   float decay;
 };
 
-__device__ __forceinline__ void load_ops(ScanOps& o, const uint8_t* chunk, uint32_t kh_off, uint32_t vh_off, int cb,
-                                         int w, int lane) {
-  const uint8_t* kb = chunk + kh_off + lane * 16;
-  const uint8_t* vb = chunk + vh_off;
+// Loads of one chunk's operands for wave w, in four groups (the scan spreads them over a step's phases).
+struct ScanSrc {
+  const uint8_t* kb;        // this wave's lane slot in the key head's K orders
+  const uint8_t* vb;        // the value head's block
+};
+
+__device__ __forceinline__ ScanSrc scan_src(const uint8_t* chunk, uint32_t kh_off, uint32_t vh_off, int lane) {
+  return ScanSrc{chunk + kh_off + lane * 16, chunk + vh_off};
+}
+
+__device__ __forceinline__ void load_part(ScanOps& o, const ScanSrc& q, int part, int cb, int w, int lane) {
+  if (part == 0) {
 #pragma unroll
-  for (int it = 0; it < 4; ++it) o.kp[it] = *reinterpret_cast<const uint4*>(kb + (it * 4 + w) * 1024);
+    for (int it = 0; it < 4; ++it) o.kp[it] = *reinterpret_cast<const uint4*>(q.kb + (it * 4 + w) * 1024);
+  } else if (part == 1) {
 #pragma unroll
-  for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int s = 0; s < 2; ++s) o.kt[j][s] = *reinterpret_cast<const uint4*>(kb + KP_BYTES + ((2 * w + j) * 2 + s) * 1024);
-  // every wave issues the same loads (uniform wait counts); waves 0 and 1 fetch a k-step 1 frag they skip
+      for (int s = 0; s < 2; ++s)
+        o.kt[j][s] = *reinterpret_cast<const uint4*>(q.kb + KP_BYTES + ((2 * w + j) * 2 + s) * 1024);
+  } else if (part == 2) {
+    // every wave issues the same loads (uniform wait counts); waves 0 and 1 fetch a k-step 1 frag they skip
 #pragma unroll
-  for (int s = 0; s < 2; ++s)
+    for (int s = 0; s < 2; ++s)
 #pragma unroll
-    for (int hl = 0; hl < 2; ++hl) o.tp[s][hl] = *reinterpret_cast<const uint4*>(vb + ((w * 2 + s) * 2 + hl) * 1024 + lane * 16);
-  o.v = *reinterpret_cast<const uint2*>(vb + TP_BYTES + cb * 2048 + lane * 32 + w * 8);
-  const float* sc = reinterpret_cast<const float*>(vb + TP_BYTES + VP_BYTES);
-  const int r0 = 16 * w + 4 * (lane >> 4);
-  o.be = *reinterpret_cast<const float4*>(sc + SC_BETA + r0);
-  o.qq = *reinterpret_cast<const float4*>(sc + SC_Q + r0);
-  o.zz = *reinterpret_cast<const float4*>(sc + SC_Z + r0);
-  o.decay = sc[SC_DECAY];
+      for (int hl = 0; hl < 2; ++hl)
+        o.tp[s][hl] = *reinterpret_cast<const uint4*>(q.vb + ((w * 2 + s) * 2 + hl) * 1024 + lane * 16);
+  } else {
+    o.v = *reinterpret_cast<const uint2*>(q.vb + TP_BYTES + cb * 2048 + lane * 32 + w * 8);
+    const float* sc = reinterpret_cast<const float*>(q.vb + TP_BYTES + VP_BYTES);
+    const int r0 = 16 * w + 4 * (lane >> 4);
+    o.be = *reinterpret_cast<const float4*>(sc + SC_BETA + r0);
+    o.qq = *reinterpret_cast<const float4*>(sc + SC_Q + r0);
+    o.zz = *reinterpret_cast<const float4*>(sc + SC_Z + r0);
+    o.decay = sc[SC_DECAY];
+  }
 }
 
 // 4 values -> hi (truncated to bf16) and lo (the rest rounded to bf16), as split8.
@@ -343,7 +383,8 @@ __device__ __forceinline__ void split4(const float (&x)[4], uint2& hi, uint2& lo
 //   sum over w in order; wave w forms row tile w of Y = beta (V - q X) and of v_new = T Y (T lower
 //   triangular: tiles 0 and 1 need k-step 0 only), and row tile w of Z = z v_new; Y and Z are shared as
 //   hi / lo bf16 B-operand frags through LDS; S_w <- decay S_w + K^T[32w .., :] Z.
-// Three barriers per chunk; the next chunk's operands load into registers while this one computes.
+// Three barriers per chunk; the operands of the chunk two steps ahead load into registers meanwhile,
+// in four groups between the phases so the address unit streams them in the background.
 __global__ __launch_bounds__(256) void k_gdn_scan(ScanArgs a) {
   __shared__ __align__(16) f32x4 xp[4][4][64];        // X_w partials [wave][row tile][lane]
   __shared__ __align__(16) uint4 yf[2][2][64];        // Y frags [k-step][hi / lo][lane]
@@ -362,91 +403,116 @@ __global__ __launch_bounds__(256) void k_gdn_scan(ScanArgs a) {
 
   const uint32_t kh_off = static_cast<uint32_t>(kh) * KH_BYTES;
   const uint32_t vh_off = static_cast<uint32_t>(a.nk) * KH_BYTES + static_cast<uint32_t>(h) * VH_BYTES;
-  ScanOps cur, nxt;
-  load_ops(cur, a.ws, kh_off, vh_off, cb, w, lane);
-  for (int c = 0; c < a.chunks; ++c) {
-    // the next chunk's operands (the last chunk reloads itself; the copy is not used)
-    load_ops(nxt, a.ws + static_cast<size_t>(min(c + 1, a.chunks - 1)) * a.chunk_bytes, kh_off, vh_off, cb, w, lane);
-    // X_w = K[:, 32w ..] S_w: S_w's rows in k-step order are (tile 2w, r) then (tile 2w + 1, r)
-    {
-      float x[8];
+  // One chunk step from its operands o; the four load groups of the chunk two steps on go out between
+  // the phases into L (the buffer the previous step freed). Past the last chunk (active false) only the
+  // loads run, so every path issues the same loads and waits on the same counts.
+  auto step = [&](const ScanOps& o, ScanOps& L, const ScanSrc& from, bool active) {
+    if (active) {
+      // X_w = K[:, 32w ..] S_w: S_w's rows in k-step order are (tile 2w, r) then (tile 2w + 1, r)
+      {
+        float x[8];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        x[r] = S[0][r];
-        x[4 + r] = S[1][r];
-      }
-      uint4 bh, bl;
-      split8(x, bh, bl);
+        for (int r = 0; r < 4; ++r) {
+          x[r] = S[0][r];
+          x[4 + r] = S[1][r];
+        }
+        uint4 bh, bl;
+        split8(x, bh, bl);
 #pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(cur.kp[it]), as_frag(bh), acc, 0, 0, 0);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(cur.kp[it]), as_frag(bl), acc, 0, 0, 0);
-        xp[w][it][lane] = acc;
+        for (int it = 0; it < 4; ++it) {
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(o.kp[it]), as_frag(bh), acc, 0, 0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(o.kp[it]), as_frag(bl), acc, 0, 0, 0);
+          xp[w][it][lane] = acc;
+        }
       }
     }
-    __syncthreads();
-    // row tile w: X, Y = beta (V - q X), its hi / lo halves into k-step w / 2, slots 4 (w % 2) ..
-    {
-      f32x4 X = xp[0][w][lane];
+    load_part(L, from, 0, cb, w, lane);
+    if (active) {
+      __syncthreads();
+      // row tile w: X, Y = beta (V - q X), its hi / lo halves into k-step w / 2, slots 4 (w % 2) ..
+      {
+        f32x4 X = xp[0][w][lane];
 #pragma unroll
-      for (int q = 1; q < 4; ++q) X += xp[q][w][lane];
-      const float bb[4] = {cur.be.x, cur.be.y, cur.be.z, cur.be.w}, q4[4] = {cur.qq.x, cur.qq.y, cur.qq.z, cur.qq.w};
-      const uint32_t vv[2] = {cur.v.x, cur.v.y};
-      float y[4];
+        for (int q = 1; q < 4; ++q) X += xp[q][w][lane];
+        const float bb[4] = {o.be.x, o.be.y, o.be.z, o.be.w}, q4[4] = {o.qq.x, o.qq.y, o.qq.z, o.qq.w};
+        const uint32_t vv[2] = {o.v.x, o.v.y};
+        float y[4];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float v = bf2f((vv[r >> 1] >> (16 * (r & 1))) & 0xffffu);
-        y[r] = bb[r] * (v - q4[r] * X[r]);
+        for (int r = 0; r < 4; ++r) {
+          const float v = bf2f((vv[r >> 1] >> (16 * (r & 1))) & 0xffffu);
+          y[r] = bb[r] * (v - q4[r] * X[r]);
+        }
+        uint2 hi, lo;
+        split4(y, hi, lo);
+        reinterpret_cast<uint2*>(&yf[w >> 1][0][lane])[w & 1] = hi;
+        reinterpret_cast<uint2*>(&yf[w >> 1][1][lane])[w & 1] = lo;
       }
-      uint2 hi, lo;
-      split4(y, hi, lo);
-      reinterpret_cast<uint2*>(&yf[w >> 1][0][lane])[w & 1] = hi;
-      reinterpret_cast<uint2*>(&yf[w >> 1][1][lane])[w & 1] = lo;
     }
-    __syncthreads();
-    // v_new row tile w = sum over k-steps of T Y; Z = z v_new into the Z frags
-    {
-      f32x4 vn = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        if (s == 1 && w < 2) continue;
-        const bf16x8 th = as_frag(cur.tp[s][0]), tl = as_frag(cur.tp[s][1]);
-        const bf16x8 yh = as_frag(yf[s][0][lane]), yl = as_frag(yf[s][1][lane]);
-        vn = __builtin_amdgcn_mfma_f32_16x16x32_bf16(th, yh, vn, 0, 0, 0);
-        vn = __builtin_amdgcn_mfma_f32_16x16x32_bf16(th, yl, vn, 0, 0, 0);
-        vn = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tl, yh, vn, 0, 0, 0);
-      }
-      const float z4[4] = {cur.zz.x, cur.zz.y, cur.zz.z, cur.zz.w};
-      float z[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) z[r] = z4[r] * vn[r];
-      uint2 hi, lo;
-      split4(z, hi, lo);
-      reinterpret_cast<uint2*>(&zf[w >> 1][0][lane])[w & 1] = hi;
-      reinterpret_cast<uint2*>(&zf[w >> 1][1][lane])[w & 1] = lo;
-    }
-    __syncthreads();
-    // S_w <- decay S_w + K^T Z
-    {
-      bf16x8 zh[2], zl[2];
-#pragma unroll
-      for (int s = 0; s < 2; ++s) {
-        zh[s] = as_frag(zf[s][0][lane]);
-        zl[s] = as_frag(zf[s][1][lane]);
-      }
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        f32x4 acc = S[j] * cur.decay;
+    load_part(L, from, 1, cb, w, lane);
+    if (active) {
+      __syncthreads();
+      // v_new row tile w = sum over k-steps of T Y; Z = z v_new into the Z frags
+      {
+        f32x4 vn = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int s = 0; s < 2; ++s) {
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(cur.kt[j][s]), zh[s], acc, 0, 0, 0);
-          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(cur.kt[j][s]), zl[s], acc, 0, 0, 0);
+          if (s == 1 && w < 2) continue;
+          const bf16x8 th = as_frag(o.tp[s][0]), tl = as_frag(o.tp[s][1]);
+          const bf16x8 yh = as_frag(yf[s][0][lane]), yl = as_frag(yf[s][1][lane]);
+          vn = __builtin_amdgcn_mfma_f32_16x16x32_bf16(th, yh, vn, 0, 0, 0);
+          vn = __builtin_amdgcn_mfma_f32_16x16x32_bf16(th, yl, vn, 0, 0, 0);
+          vn = __builtin_amdgcn_mfma_f32_16x16x32_bf16(tl, yh, vn, 0, 0, 0);
         }
-        S[j] = acc;
+        const float z4[4] = {o.zz.x, o.zz.y, o.zz.z, o.zz.w};
+        float z[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) z[r] = z4[r] * vn[r];
+        uint2 hi, lo;
+        split4(z, hi, lo);
+        reinterpret_cast<uint2*>(&zf[w >> 1][0][lane])[w & 1] = hi;
+        reinterpret_cast<uint2*>(&zf[w >> 1][1][lane])[w & 1] = lo;
       }
     }
-    cur = nxt;
+    load_part(L, from, 2, cb, w, lane);
+    if (active) {
+      __syncthreads();
+      // S_w <- decay S_w + K^T Z
+      {
+        bf16x8 zh[2], zl[2];
+#pragma unroll
+        for (int s = 0; s < 2; ++s) {
+          zh[s] = as_frag(zf[s][0][lane]);
+          zl[s] = as_frag(zf[s][1][lane]);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          f32x4 acc = S[j] * o.decay;
+#pragma unroll
+          for (int s = 0; s < 2; ++s) {
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(o.kt[j][s]), zh[s], acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(o.kt[j][s]), zl[s], acc, 0, 0, 0);
+          }
+          S[j] = acc;
+        }
+      }
+    }
+    load_part(L, from, 3, cb, w, lane);
+  };
+  auto src = [&](int c) {
+    return scan_src(a.ws + static_cast<size_t>(min(c, a.chunks - 1)) * a.chunk_bytes, kh_off, vh_off, lane);
+  };
+  // three buffers in rotation: chunk c + 2 loads during chunk c's step (indices past the last chunk reload
+  // it; those copies are never used)
+  ScanOps b0, b1, b2;
+  for (int part = 0; part < 4; ++part) {
+    load_part(b0, src(0), part, cb, w, lane);
+    load_part(b1, src(1), part, cb, w, lane);
+  }
+  for (int c = 0; c < a.chunks; c += 3) {
+    step(b0, b2, src(c + 2), true);
+    step(b1, b0, src(c + 3), c + 1 < a.chunks);
+    step(b2, b1, src(c + 4), c + 2 < a.chunks);
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j)
