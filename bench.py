@@ -68,12 +68,13 @@ def build_workload(dev):
     return cfg, w, model, arm
 
 
-def fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches, timer=None):
+def fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches, timer=None, overlap=False):
     """One step: the 16-layer fill (the hot path of finish() for the ridgefill arm, no exact rows),
-    scheduled as fill_late schedules it by default: each layer's map apply, then its fused K / V cache
-    write, on the current stream (rfill.kva.serial)."""
+    scheduled as fill_late schedules it: each layer's map apply, then its fused K / V cache write, on the
+    current stream (rfill.kva.serial), or with overlap each layer's K / V write on a second stream beside
+    the next layer's map apply (rfill.kva.two_stream)."""
     from rfill import ops
-    from rfill.kva import serial
+    from rfill.kva import serial, two_stream
     W, B = arm.projector._maps(b.device)
 
     def produce(i, slot):
@@ -87,7 +88,7 @@ def fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches, timer=None):
                                       c["vbuf"], 0)
         f() if timer is None else timer.run("rf_norm_kv_write", f)
 
-    serial(range(arm.split, model.n_layers), produce, consume, b.device)
+    (two_stream if overlap else serial)(range(arm.split, model.n_layers), produce, consume, b.device)
 
 
 def ceilings(dev, P, H):
@@ -327,6 +328,8 @@ def main():
     ap.add_argument("--no-fit", action="store_true", help="skip the closed-form fit leg")
     ap.add_argument("--no-hybrid", action="store_true", help="skip the Gated-DeltaNet hybrid fill leg")
     ap.add_argument("--no-exact", action="store_true", help="skip the Qwen3-8B exact-rows fill leg")
+    ap.add_argument("--overlap", action="store_true",
+                    help="run each layer's K / V write on a second stream beside the next layer's map apply")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (one MI355X per box); --gpus must be 1", file=sys.stderr)
@@ -347,14 +350,14 @@ def main():
                          vbuf=torch.empty(model.n_kv, P + 64, model.head_dim, dtype=torch.bfloat16, device=dev), n=0)
     log(f"warmup {args.warmup} steps")
     for _ in range(args.warmup):
-        fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches)
+        fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches, overlap=args.overlap)
     torch.cuda.synchronize()
     log(f"timing {args.steps} steps")
     timer = KernelTimer()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches, timer)
+        fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches, timer, overlap=args.overlap)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     L = len(w["layers"])

@@ -8,8 +8,9 @@
 // of a 256-row operand tile is 256 rows x 64 bytes. The slices go from memory straight into LDS
 // (buffer_load_dwordx4 ... lds, no staging registers; the buffer's range check turns rows past M into
 // zeros) with the 16-byte chunk index XOR-ed by (row >> 2) & 3, so the MFMA fragment reads (32 rows,
-// one chunk per lane) hit all banks. Four LDS stages (4 x 32 KiB): loads run three steps ahead of the
-// MFMAs; one wait and one barrier per step.
+// one chunk per lane) hit all banks. Five LDS slots (5 x 32 KiB, the whole LDS): loads run 2 to 3.5
+// steps ahead of the MFMAs, issued as pairs that cover both halves of each 128-byte line; one wait and
+// one barrier per step.
 //
 // Each wave owns a 128 x 128 quarter and issues v_mfma_f32_32x32x16_bf16 on 4 x 4 sub-tiles. The
 // weight tile is the MFMA's A operand and the activation tile its B operand, so the accumulator of a
@@ -28,13 +29,14 @@ typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int BM = 256, BN = 256, BK = 32, NTHR = 256;
-constexpr int STAGES = 4;                      // LDS stages: loads run STAGES - 1 K steps ahead
-constexpr int CPR = BK / 8;                    // 16-byte chunks per operand row in a stage
-constexpr int STAGE_U4 = (BM + BN) * CPR;      // 16-byte chunks per LDS stage (activations, then weights)
-constexpr int LDS_U4 = STAGES * STAGE_U4;      // 128 KiB; reused by the epilogue as the 256 x 256 bf16 tile
+constexpr int STAGES = 5;                      // LDS slots, one 32-deep K step each
+constexpr int CPR = BK / 8;                    // 16-byte chunks per operand row in a slot
+constexpr int STAGE_U4 = (BM + BN) * CPR;      // 16-byte chunks per slot (activations, then weights)
+constexpr int LDS_U4 = STAGES * STAGE_U4;      // 160 KiB, the whole LDS of a CU
+constexpr int IMAGE_U4 = 256 * 32;             // the epilogue's 256 x 256 bf16 image (128 KiB)
 constexpr int LOADS_PER_STEP = (BM + BN) * CPR / 64 / 4;   // direct-load instructions per wave per K step
-static_assert(LDS_U4 >= 256 * 32, "the epilogue's 256 x 256 bf16 image must fit in the stages");
-static_assert(STAGES >= 3 && LOADS_PER_STEP == 8, "the load schedule assumes 8 loads per step, >= 3 stages");
+static_assert(LDS_U4 >= IMAGE_U4 + 2048, "the epilogue's image and its 32 KiB of side data must fit");
+static_assert(STAGES == 5 && LOADS_PER_STEP == 8, "the load schedule assumes 8 loads per step and 5 slots");
 
 __device__ __forceinline__ bf16x8 as_frag(const uint4& u) { return __builtin_bit_cast(bf16x8, u); }
 
@@ -95,13 +97,21 @@ __device__ __forceinline__ void issue_one(__amdgpu_buffer_rsrc_t rx, __amdgpu_bu
 // acc[nt][mt] += W[n0 + wn*128 + nt*32 .. +32, :] . X[m0 + wm*128 + mt*32 .. +32, :]^T over all of K.
 // Rows of X at or past M read as zeros. Ends with a barrier: LDS is free for the epilogue.
 //
-// Pipeline: step k's tiles land in stage k % STAGES, loaded STAGES - 1 steps ahead. A step is two
-// 16-wide K slices of 16 MFMAs each. The wave's instruction stream is in order, so anything issued
-// in a burst stalls the MFMA pipe; instead one LDS fragment read for the next slice follows each of a
-// slice's first 8 MFMAs, and one global->LDS load follows every second of its last 8 (8 loads per
-// step). Between the slices the wave waits for step k + 1's loads (vmcnt) and its own LDS reads
-// (lgkmcnt 0) and meets the other waves at a barrier; after it, stage k % STAGES is free for the loads
-// issued in step k + 1, and the second slice reads step k + 1's first fragments.
+// Pipeline. Step k's tiles (32 deep) land in slot k % 5. Loads go in batches of two steps (k, k + 1)
+// issued as pairs: load j of step k, then load j of step k + 1, back to back -- the two 64-byte halves
+// of the same 128-byte lines, which the memory path serves at full-line rate (a lone half-line load
+// runs at half of it). A step is two 16-wide K slices of 16 MFMAs each. The wave's instruction stream
+// is in order, so anything issued in a burst stalls the MFMA pipe; instead one LDS fragment read for
+// the next slice follows each of a slice's first 8 MFMAs, and one load pair follows every second of
+// its last 8. Between the slices the wave waits for step k + 1's loads (vmcnt) and its own LDS reads
+// (lgkmcnt 0) and meets the other waves at a barrier; after it, slot k % 5 is free.
+//
+// Schedule: even step k issues the first half of the batch for steps (k + 4, k + 5) in its second
+// slice, into slots (k - 1) % 5 and k % 5 (free since step k - 1's barrier and this step's barrier);
+// odd step k + 1 issues the batch's second half in its first slice. At step k's barrier the loads
+// still allowed in flight are the batch started at k - 2 (16) for even k, and that batch plus the last
+// load of the batch holding step k + 1 (17) for odd k. A step's loads are thus issued 2 to 3.5 steps
+// before their slot is read.
 __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t ldx,
                                          const uint16_t* __restrict__ W, int64_t ldw, int M, int K,
                                          int m0, int n0, uint4* lds, f32x16 (&acc)[4][4]) {
@@ -131,7 +141,7 @@ __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t
   const int nk = K / BK;
   const int lr = lane & 31, lk = lane >> 5, swz = row_swz(lr);
   bf16x8 fx[2][4], fw[2][4];
-  // fragment r (0..7) of slice ks from stage st: r < 4 -> weight block r, else activation block r - 4
+  // fragment r (0..7) of slice ks from slot st: r < 4 -> weight block r, else activation block r - 4
   auto read_one = [&](int st, int ks, int r, bf16x8 (&ax)[4], bf16x8 (&aw)[4]) {
     const uint4* sx = lds + st * STAGE_U4;
     const uint4* sw = sx + BM * CPR;
@@ -139,8 +149,14 @@ __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t
     if (r < 4) aw[r] = as_frag(sw[(wn * 128 + r * 32 + lr) * CPR + slot]);
     else ax[r - 4] = as_frag(sx[(wm * 128 + (r - 4) * 32 + lr) * CPR + slot]);
   };
+  // pair j of the batch for steps (kb, kb + 1); `checked` drops steps at or past the end of K
+  auto issue_pair = [&](int j, int kb, bool checked) {
+    if (!checked || kb < nk) issue_one(rx, rw, vx, vw, j, kb * BK, base + (kb % STAGES) * STAGE_U4 * 16, w);
+    if (!checked || kb + 1 < nk)
+      issue_one(rx, rw, vx, vw, j, (kb + 1) * BK, base + ((kb + 1) % STAGES) * STAGE_U4 * 16, w);
+  };
   auto slice = [&](const bf16x8 (&ax)[4], const bf16x8 (&aw)[4], bool do_read, int rst, int rks, bf16x8 (&nx)[4],
-                   bf16x8 (&nw)[4], bool do_load, int half, int kload, char* lstage) {
+                   bf16x8 (&nw)[4], bool do_load, int j0, int kb, bool checked) {
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
       acc[q >> 2][q & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aw[q >> 2], ax[q & 3], acc[q >> 2][q & 3], 0, 0, 0);
@@ -148,45 +164,47 @@ __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t
       if (q < 8) {
         if (do_read) read_one(rst, rks, q, nx, nw);
       } else if (do_load && (q & 1)) {
-        issue_one(rx, rw, vx, vw, half * 4 + ((q - 9) >> 1), kload, lstage, w);
+        issue_pair(j0 + ((q - 9) >> 1), kb, checked);
       }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  // `steady` (a compile-time tag) marks the steps that still issue loads; the steady loop has no
-  // branches, so the compiler's own wait counting stays exact.
-  auto step = [&](int kt, auto steady) {
+  // `steady` (compile-time) marks steps whose batches lie inside K: no bounds checks, exact vmcnt
+  // waits from the schedule above; `odd` (compile-time in the steady loop) is the step's parity.
+  auto step = [&](int kt, auto steady, bool odd) {
     const int s = kt % STAGES;
-    const int kload = (kt + STAGES - 1) * BK;
-    char* lstage = base + ((kt + STAGES - 1) % STAGES) * STAGE_U4 * 16;
-    slice(fx[0], fw[0], true, s, 1, fx[1], fw[1], steady, 0, kload, lstage);
-    // outstanding after step k + 1's loads: step k + 2's (all) and step k + 3's first half
-    if (steady) wait_vm_lgkm0<LOADS_PER_STEP * (STAGES - 3) + LOADS_PER_STEP / 2>();
-    else wait_vm_lgkm0<0>();
+    slice(fx[0], fw[0], true, s, 1, fx[1], fw[1], odd, 4, kt + 3, !steady);
+    if (steady) {
+      if (odd) wait_vm_lgkm0<2 * LOADS_PER_STEP + 1>();
+      else wait_vm_lgkm0<2 * LOADS_PER_STEP>();
+    } else {
+      wait_vm_lgkm0<0>();
+    }
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    slice(fx[1], fw[1], steady || kt + 1 < nk, (kt + 1) % STAGES, 0, fx[0], fw[0], steady, 1, kload, lstage);
+    slice(fx[1], fw[1], steady || kt + 1 < nk, (kt + 1) % STAGES, 0, fx[0], fw[0], !odd, 0, kt + 4, !steady);
   };
 
-#pragma unroll
-  for (int st = 0; st < STAGES - 1; ++st)
-    if (st < nk)
-      for (int j = 0; j < LOADS_PER_STEP; ++j) issue_one(rx, rw, vx, vw, j, st * BK, base + st * STAGE_U4 * 16, w);
-  if (nk >= STAGES - 1) wait_vm_lgkm0<LOADS_PER_STEP * (STAGES - 2)>();
+  // prologue: the batches for steps (0, 1) and (2, 3), then step 0's first fragments
+  for (int j = 0; j < LOADS_PER_STEP; ++j) issue_pair(j, 0, true);
+  for (int j = 0; j < LOADS_PER_STEP; ++j) issue_pair(j, 2, true);
+  if (nk >= 4) wait_vm_lgkm0<2 * LOADS_PER_STEP + 1>();
   else wait_vm_lgkm0<0>();
   __builtin_amdgcn_s_barrier();
   for (int r = 0; r < 8; ++r) read_one(0, 0, r, fx[0], fw[0]);
   int kt = 0;
-  for (; kt + STAGES - 1 < nk; ++kt) step(kt, std::true_type{});
-  for (; kt < nk; ++kt) step(kt, std::false_type{});
+  for (; kt + 5 < nk; kt += 2) {
+    step(kt, std::true_type{}, false);
+    step(kt + 1, std::true_type{}, true);
+  }
+  for (; kt < nk; ++kt) step(kt, std::false_type{}, (kt & 1) != 0);
   wait_vm_lgkm0<0>();
   __syncthreads();
 }
 
-// LDS beyond the stages (32 KiB): per-tile side data the epilogues read -- the bias tile, the rows'
-// norm scales, the rows' sum-of-squares halves. Filled before the main loop, read after it.
-constexpr int AUX_U4 = 2048;
-constexpr int LDS_ALL_U4 = LDS_U4 + AUX_U4;   // 160 KiB, the whole LDS of a CU
+// After the main loop the LDS past the image (32 KiB) holds per-tile side data the epilogues read: the
+// bias tile, the rows' norm scales, the rows' sum-of-squares halves. What is known before the loop
+// (bias, norm scales) waits in registers through it and is written there after it.
 
 // Epilogue stage 1: value(mt, nt, g, e, acc) rounded to bf16 into the row-major LDS image of the tile.
 // Lane (lr, lk) holds, for tile row wm*128 + mt*32 + lr, columns wn*128 + nt*32 + 8g + 4lk + e.
@@ -229,18 +247,18 @@ __device__ __forceinline__ uint4 image_chunk(const uint4* lds, int row, int c) {
   return lds[row * 32 + (c ^ (row & 31))];
 }
 
-// Each of the tile's rows' input RMSNorm scale 1 / sqrt(mean(x^2) + eps) from its sum-of-squares
-// partials (summed in order), into rs[0..255]; thread t takes row m0 + t. Called before the main loop
-// (the loads overlap its first operand loads); rs is read after it.
-__device__ __forceinline__ void row_scales(const float* __restrict__ ssq, int nparts, float width, float eps, int M,
-                                           int m0, float* rs) {
-  const int t = threadIdx.x, gm = m0 + t;
+// Input RMSNorm scale 1 / sqrt(mean(x^2) + eps) of tile row threadIdx.x (row m0 + threadIdx.x) from
+// its sum-of-squares partials, summed in order. Called before the main loop (its loads overlap the
+// first operand loads); the value is published to the other waves through LDS after the loop.
+__device__ __forceinline__ float row_scale(const float* __restrict__ ssq, int nparts, float width, float eps, int M,
+                                           int m0) {
+  const int gm = m0 + static_cast<int>(threadIdx.x);
   float s = 0.f;
   if (gm < M) {
     const float* q = ssq + static_cast<int64_t>(gm) * nparts;
     for (int i = 0; i < nparts; ++i) s += q[i];
   }
-  rs[t] = 1.0f / sqrtf(s / width + eps);
+  return 1.0f / sqrtf(s / width + eps);
 }
 
 __global__ __launch_bounds__(NTHR) void k_map_apply(const uint16_t* __restrict__ B, int64_t ldb,
@@ -248,17 +266,20 @@ __global__ __launch_bounds__(NTHR) void k_map_apply(const uint16_t* __restrict__
                                                     const uint16_t* __restrict__ bias,
                                                     uint16_t* __restrict__ X, int64_t ldx,
                                                     float* __restrict__ ssq, int M, int N, int K) {
-  __shared__ uint4 lds[LDS_ALL_U4];
-  uint4* aux = lds + LDS_U4;
+  __shared__ uint4 lds[LDS_U4];
+  uint4* aux = lds + IMAGE_U4;                                  // the bias tile, then:
   float* halves = reinterpret_cast<float*>(aux + 32);          // [2][256] row sum-of-squares halves
   const int tiles_n = N / BN;
   int tm, tn;
   tile_coords(xcd_tile(blockIdx.x, gridDim.x), (M + BM - 1) / BM, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int t = threadIdx.x;
-  if (t < 32) aux[t] = bias ? *reinterpret_cast<const uint4*>(bias + n0 + t * 8) : make_uint4(0u, 0u, 0u, 0u);
+  uint4 bias_chunk = make_uint4(0u, 0u, 0u, 0u);
+  if (t < 32 && bias) bias_chunk = *reinterpret_cast<const uint4*>(bias + n0 + t * 8);
   f32x16 acc[4][4];
   mainloop(B, ldb, W, K, M, K, m0, n0, lds, acc);
+  if (t < 32) aux[t] = bias_chunk;
+  __syncthreads();
 
   const int lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1, lr = lane & 31, lk = lane >> 5;
   const uint16_t* bt = reinterpret_cast<const uint16_t*>(aux);
@@ -327,15 +348,17 @@ __device__ __forceinline__ void knorm_chunk(float (&f)[8], float rinv, const uin
 __global__ __launch_bounds__(NTHR) void k_norm_kv(const uint16_t* __restrict__ Xin, int64_t ldx,
                                                   const uint16_t* __restrict__ W, int M, int N, int K,
                                                   KvArgs a) {
-  __shared__ uint4 lds[LDS_ALL_U4];
-  float* rsc = reinterpret_cast<float*>(lds + LDS_U4);           // [256] row norm scales
+  __shared__ uint4 lds[LDS_U4];
+  float* rsc = reinterpret_cast<float*>(lds + IMAGE_U4);         // [256] row norm scales
   const int tiles_n = N / BN;
   int tm, tn;
   tile_coords(xcd_tile(blockIdx.x, gridDim.x), (M + BM - 1) / BM, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  row_scales(a.ssq, a.nparts, a.h, a.eps, M, m0, rsc);
+  const float my_rs = row_scale(a.ssq, a.nparts, a.h, a.eps, M, m0);
   f32x16 acc[4][4];
   mainloop(Xin, ldx, W, K, M, K, m0, n0, lds, acc);
+  rsc[threadIdx.x] = my_rs;
+  __syncthreads();
 
   // Input RMSNorm: the gain is folded into W, so each row is scaled by 1 / sqrt(mean(x^2) + eps).
   const int lane = threadIdx.x & 63, wm = threadIdx.x >> 7;
@@ -435,15 +458,17 @@ __global__ __launch_bounds__(NTHR) void k_norm_linear(const uint16_t* __restrict
                                                       const uint16_t* __restrict__ W, int M, int N, int K,
                                                       const float* __restrict__ ssq, float eps,
                                                       uint16_t* __restrict__ out, int64_t ldo) {
-  __shared__ uint4 lds[LDS_ALL_U4];
-  float* rsc = reinterpret_cast<float*>(lds + LDS_U4);
+  __shared__ uint4 lds[LDS_U4];
+  float* rsc = reinterpret_cast<float*>(lds + IMAGE_U4);
   const int tiles_n = N / BN;
   int tm, tn;
   tile_coords(xcd_tile(blockIdx.x, gridDim.x), (M + BM - 1) / BM, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
-  row_scales(ssq, K / SSQ_COLS, static_cast<float>(K), eps, M, m0, rsc);
+  const float my_rs = row_scale(ssq, K / SSQ_COLS, static_cast<float>(K), eps, M, m0);
   f32x16 acc[4][4];
   mainloop(Xin, ldx, W, K, M, K, m0, n0, lds, acc);
+  rsc[threadIdx.x] = my_rs;
+  __syncthreads();
   const int lane = threadIdx.x & 63, wm = threadIdx.x >> 7;
   float rs[4], unused[4];
 #pragma unroll
