@@ -306,6 +306,56 @@ def exact_rows_bench(dev, reps=3, split=18, n_rows=32768, tail=4096, frac=0.01):
             "exact_rows_ms": round((out["exact"] - out["plain"]) * 1e3, 3), "exact_rows": len(rows)}
 
 
+def finish_bench(dev, reps=3, keep=TAIL):
+    """The whole late stack of one ridgefill arm at the Llama-3.1-8B shape, as finish() runs it: the
+    16-layer fill of P = 28672 rows, then the 4096-row exact tail through every late layer (K / V appended,
+    causal attention over all 32768 keys, o_proj, SwiGLU MLP 14336) and the logits of its last `keep`
+    rows (vocab 128256). Reported: prompt tokens/s through the late layers (N / time), the fill, tail and
+    logits times apart, and the tail's counted work (its GEMMs 2 T (q + kv + o + 3 MLP) per layer and the
+    attention's 4 d flop per (query head, visible key))."""
+    from rfill import synth
+    from rfill.kva import Arm, Projector, fill_late, finish
+    from rfill.model import FillModel
+    cfg = synth.LLAMA_8B
+    w = synth.dense_fill(cfg, SPLIT, N_ROWS, TAIL, device=dev, full=True, head=True)
+    model = FillModel(cfg, w["tensors"], dev, layers=w["layers"])
+    arm = Arm("ridgefill", split=SPLIT, tail=TAIL, fill="proj", projector=Projector(SPLIT, w["maps"], w["biases"]))
+    del w["tensors"]
+    h = w["h_split"]
+    finish(model, h, arm, keep)
+    torch.cuda.synchronize()
+    times = {"finish": 0.0, "fill": 0.0, "logits": 0.0}
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        finish(model, h, arm, keep)
+        torch.cuda.synchronize()
+        times["finish"] += (time.perf_counter() - t0) / reps
+        t0 = time.perf_counter()
+        cache = model.new_cache()
+        for i in w["layers"]:
+            model.reserve(cache[i], N_ROWS, model.n_kv, model.head_dim, dev)
+        fill_late(model, h, arm, cache=cache)
+        torch.cuda.synchronize()
+        times["fill"] += (time.perf_counter() - t0) / reps
+        t0 = time.perf_counter()
+        model.logits(h[N_ROWS - keep:])
+        torch.cuda.synchronize()
+        times["logits"] += (time.perf_counter() - t0) / reps
+    H, L, T, P = cfg["hidden_size"], len(w["layers"]), TAIL, w["P"]
+    hq, hkv, d, inter = cfg["num_attention_heads"], cfg["num_key_value_heads"], cfg["head_dim"], cfg["intermediate_size"]
+    tail_gemm = 2 * T * H * (hq * d + 2 * hkv * d + hq * d + 3 * inter) * L
+    keys = sum(P + j + 1 for j in range(T))
+    tail_attn = 4 * d * hq * keys * L
+    t_tail = times["finish"] - times["fill"] - times["logits"]
+    return {"workload": f"llama-3.1-8b-shaped 32K finish(): fill of layers {SPLIT}..{cfg['num_hidden_layers'] - 1} "
+                        f"({P} rows) + {T}-row exact tail through every late layer + logits of {keep} rows",
+            "prompt_tokens_per_s": round(N_ROWS / times["finish"], 1), "ms_finish": round(times["finish"] * 1e3, 2),
+            "ms_fill": round(times["fill"] * 1e3, 2), "ms_tail": round(t_tail * 1e3, 2),
+            "ms_logits": round(times["logits"] * 1e3, 2),
+            "tail_counted_flop": tail_gemm + tail_attn, "tail_attention_flop": tail_attn,
+            "tail_tflops": round((tail_gemm + tail_attn) / t_tail / 1e12, 1)}
+
+
 def traffic_from_profiles(kernel):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary (FETCH_SIZE + WRITE_SIZE scaled
     by a copy kernel of known size), or None if it has not been measured."""
@@ -328,6 +378,7 @@ def main():
     ap.add_argument("--no-fit", action="store_true", help="skip the closed-form fit leg")
     ap.add_argument("--no-hybrid", action="store_true", help="skip the Gated-DeltaNet hybrid fill leg")
     ap.add_argument("--no-exact", action="store_true", help="skip the Qwen3-8B exact-rows fill leg")
+    ap.add_argument("--no-finish", action="store_true", help="skip the whole-finish() leg (fill + exact tail)")
     ap.add_argument("--overlap", action="store_true",
                     help="run each layer's K / V write on a second stream beside the next layer's map apply")
     args = ap.parse_args()
@@ -389,6 +440,10 @@ def main():
         out["ceilings"] = ceilings(dev, P, H)
     del caches, xbuf, sbuf
     torch.cuda.empty_cache()
+    if not args.no_finish:
+        log("finish(): fill + exact tail + logits")
+        out["finish"] = finish_bench(dev)
+        torch.cuda.empty_cache()
     if not args.no_exact:
         log("Qwen3-8B fill with 1% exact rows")
         out["exact_rows"] = exact_rows_bench(dev)

@@ -214,3 +214,35 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
 
     (two_stream if overlap else serial)(layers, produce, consume, dev)
     return cache, P
+
+
+def finish(model, h_split, arm, keep, exact_rows=None, hr=None, cache=None, row_inputs=None):
+    """Layers >= arm.split for one arm, as finish() runs them (code/kva/kva.py:319-460) for the 'proj'
+    and 'identity' fills: every late layer's cache is filled from the prefix rows [0, P) of h_split
+    (fill_late, with exact rows as there), and the exact tail rows [P, N) run through each late layer
+    in order (FillModel.layer over that layer's filled cache, kva.py:457). The fill of a layer never
+    reads the tail, so filling every layer first gives the reference's results. Each attention cache
+    is sized once for P + T rows. Returns (logits of the last `keep` rows [keep, V] fp32, cache, P)."""
+    n = h_split.shape[0]
+    P = arm.prefix_len(n)
+    T = n - P
+    if keep > T:
+        raise ValueError(f"keep {keep} rows > exact tail {T}")
+    if arm.fill not in ("proj", "identity", "exact"):
+        raise ValueError(f"fill {arm.fill!r}: finish runs 'proj', 'identity' and 'exact'")
+    cache = model.new_cache() if cache is None else cache
+    dev = h_split.device
+    layers = list(range(arm.split, model.n_layers))
+    for i in layers:
+        if model.layer_types[i] == "attn":
+            model.reserve(cache[i], n, model.n_kv, model.head_dim, dev)
+    if P > 0:
+        fill_late(model, h_split, arm, exact_rows=exact_rows, hr=hr, cache=cache, row_inputs=row_inputs)
+    h = h_split[P:]
+    pos = torch.arange(P, n, device=dev)
+    cs = model.rope_table(pos)
+    ssq = ops.row_ssq(h)
+    for i in layers:
+        h, ssq = model.layer(i, h, pos, cache, ssq=ssq, cs=cs)
+    return model.logits(h[T - keep:], ssq[T - keep:]), cache, P
+

@@ -262,15 +262,65 @@ class FillModel:
                        rows)
         o = ops.attend_rows(q, pos.to(x.device, torch.int64)[rows], c["kbuf"], c["vbuf"], c["n"], self.n_heads,
                             self.scale, workspace=self._attn_workspace(len(rows), c["n"], x.device))
+        return self._out_mlp(w, xr, o)[0]
+
+    def _out_mlp(self, w, h, o):
+        """The rest of the layer after attention: h + o W_o^T, then the SwiGLU MLP with its residual
+        (code/kva/model.py:112-118, :254-257), with the reference's bf16 roundings. Returns the layer
+        output [rows, H] bf16 and its row sum-of-squares partials (the next norm's statistics)."""
         a, _ = ops.map_apply(o, w["wo"], None)
-        h1, s1 = ops.residual_add(xr, a)
+        h1, s1 = ops.residual_add(h, a)
         gu = ops.norm_linear(h1, s1, self.eps, w["wgu"])
         inter = w["inter"]
-        act = torch.zeros(xr.shape[0], w["wd"].shape[1], dtype=torch.bfloat16, device=x.device)
+        act = (torch.zeros if w["wd"].shape[1] != inter else torch.empty)(h.shape[0], w["wd"].shape[1],
+                                                                          dtype=torch.bfloat16, device=h.device)
         ops.silu_mul(gu[:, :2 * inter], act[:, :inter])
         dn, _ = ops.map_apply(act, w["wd"], None)
-        h2, _ = ops.residual_add(h1, dn)
-        return h2
+        return ops.residual_add(h1, dn)
+
+    def layer(self, i, h, pos, cache, ssq=None, cs=None):
+        """Exact layer i for new rows h [T, H] bf16 at positions pos, appended after the cache's n rows
+        (code/kva/model.py:247-257; the exact tail of finish(), code/kva/kva.py:457): K / V of the rows
+        into slots n .. n + T - 1, the rows' queries attend causally over the keys up to their own slot
+        (bottom-right aligned, as code/kva/ops.py:107-128), then o_proj, the residual and the MLP with its
+        residual. ssq / cs: h's row sum-of-squares partials and the RoPE table of pos, if already built.
+        Returns (layer output [T, H] bf16, its row sum-of-squares partials)."""
+        if self.layer_types[i] != "attn":
+            raise UnsupportedArchitecture("the exact layer of GDN layers is not implemented by the kernels")
+        w = self._pack_rows(i)
+        c = cache[i]
+        T = h.shape[0]
+        if ssq is None:
+            ssq = ops.row_ssq(h)
+        if cs is None:
+            cs = self.rope_table(pos)
+        slot = self.reserve(c, T, self.n_kv, self.head_dim, h.device)
+        ops.norm_kv_write(h, ssq, self.eps, w["wkv"], self.n_kv, self.head_dim, w.get("k_norm"), self.knorm_kind,
+                          cs, c["kbuf"], c["vbuf"], slot)
+        self.commit(c, T)
+        idx = torch.arange(T, device=h.device)
+        q = ops.norm_q(h, ssq, self.eps, w["wq"], self.n_heads, self.head_dim, w.get("q_norm"), self.knorm_kind, cs,
+                       idx)
+        o = ops.attend_rows(q, idx + slot, c["kbuf"], c["vbuf"], c["n"], self.n_heads, self.scale,
+                            workspace=self._attn_workspace(T, c["n"], h.device))
+        return self._out_mlp(w, h, o)
+
+    def logits(self, h, ssq=None):
+        """F.linear(final_norm(h), lm_head).float() (code/kva/model.py:110-111): [rows, V] fp32 from bf16
+        rows. The final norm's gain is folded into the packed lm_head (zero rows up to a multiple of 256)."""
+        if getattr(self, "_lm", None) is None:
+            src, pre = self._src, self._pre
+            dev = lambda k: src[k].to(self.device, torch.bfloat16).contiguous()   # noqa: E731
+            head = dev("lm_head.weight") if "lm_head.weight" in src else dev(pre + "embed_tokens.weight")
+            V = head.shape[0]
+            pad = (-V) % 256
+            if pad:
+                head = torch.cat((head, head.new_zeros(pad, head.shape[1])), 0)
+            self._lm = (ops.fold_norm(head, dev(pre + "norm.weight"), self.knorm_kind), V)
+        head, V = self._lm
+        if ssq is None:
+            ssq = ops.row_ssq(h)
+        return ops.norm_linear(h, ssq, self.eps, head)[:, :V].float()
 
     def fill_kv(self, i, k, v, pos, cache, cs=None):
         """Cache-only fill from pre-RoPE K and V [P, Hkv, d] (the reads() layout)."""

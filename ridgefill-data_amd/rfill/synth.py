@@ -19,9 +19,10 @@ explicit variance 1/H of the map noise.
 import torch
 
 LLAMA_8B = dict(model_type="llama", num_hidden_layers=32, hidden_size=4096, num_attention_heads=32,
-                num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-5, rope_theta=500000.0, intermediate_size=14336)
+                num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-5, rope_theta=500000.0, intermediate_size=14336,
+                vocab_size=128256)
 QWEN3_8B = dict(model_type="qwen3", num_hidden_layers=36, hidden_size=4096, num_attention_heads=32,
-                num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-6, intermediate_size=12288,
+                num_key_value_heads=8, head_dim=128, rms_norm_eps=1e-6, intermediate_size=12288, vocab_size=151936,
                 rope_parameters=dict(rope_type="default", rope_theta=1000000.0))
 
 
@@ -80,10 +81,19 @@ def layer_weights(cfg, layer, device="cpu", map_noise=0.02, with_map=True, full=
     return t, w, c
 
 
-def dense_fill(cfg, split, n_rows, tail, device="cpu", exact_frac=0.0, with_maps=True, full=False):
+def head_weights(cfg, device="cpu"):
+    """The final norm gain 1 + N(0, 0.05) and lm_head N(0, 0.02) [vocab, H] (seed 15), bf16."""
+    h, vocab = cfg["hidden_size"], cfg["vocab_size"]
+    g = _gen(15, device)
+    return {"model.norm.weight": (1 + 0.05 * torch.randn(h, generator=g, device=device)).to(torch.bfloat16),
+            "lm_head.weight": (0.02 * torch.randn(vocab, h, generator=g, device=device)).to(torch.bfloat16)}
+
+
+def dense_fill(cfg, split, n_rows, tail, device="cpu", exact_frac=0.0, with_maps=True, full=False, head=False):
     """A late-layer fill workload: dict(cfg, split, layers, h_split [n, H], P, tensors (HF names),
     maps {l: W}, biases {l: c}, rows (sorted exact-row positions < P), hr [|rows|, H]). full: the late
-    layers' whole weights (for exact rows run through their layers)."""
+    layers' whole weights (for exact rows and the exact tail run through their layers); head: the final
+    norm and lm_head (for the tail's logits)."""
     L, h = cfg["num_hidden_layers"], cfg["hidden_size"]
     layers = list(range(split, L))
     tensors, maps, biases = {}, {}, {}
@@ -92,6 +102,8 @@ def dense_fill(cfg, split, n_rows, tail, device="cpu", exact_frac=0.0, with_maps
         tensors.update(t)
         if with_maps:
             maps[l], biases[l] = w, c
+    if head:
+        tensors.update(head_weights(cfg, device))
     P = n_rows - tail
     n_exact = int(round(exact_frac * P))
     rows = torch.randperm(P, generator=_gen(13, "cpu"))[:n_exact].sort().values

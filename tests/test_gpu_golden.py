@@ -4,6 +4,8 @@
   * fill_late (bf16) for the ridgefill arm, the identity arm and the ridgefill arm with 18 exact rows
     (their late-layer inputs taken from the fixture): the filled cache rows [0, P) against the
     reference's fp32 caches, relative Frobenius error <= 1e-2 (the bf16 bar), and n / slots exact;
+  * finish() (fill, exact tail, logits) for the same three arms: the tail logits (probe projections, the
+    last row, argmax) and every cache slot including the tail's, against the reference's finish();
   * the device fit (RidgeStats + RidgeFit on the GPU) from the calibration rows in bf16 against the
     reference's fp32-row maps (1e-2: the rows are rounded to bf16 before the products).
 
@@ -107,3 +109,38 @@ def test_device_fit_matches_reference(dev, gold, run):
             worst = max(worst, err)
             assert err < TOL, (key, err)
     print(f"device fit from bf16 rows: worst map rel err vs the reference {worst:.2e}")
+
+
+@pytest.mark.parametrize("name", ["proj", "identity", "exact"])
+def test_finish_matches_reference(dev, gold, run, name):
+    """The whole late stack on the device -- the fill, the exact rows through their layers, the 256-row
+    exact tail through every late layer and the logits of the last 256 rows -- against the reference's
+    own finish() on the same model and split-layer rows."""
+    from rfill.kva import Arm, Projector, finish
+    from rfill.model import FillModel
+    S, L = c1.SPLIT, c1.CONFIG["num_hidden_layers"]
+    late = list(range(S, L))
+    model = FillModel(c1.CONFIG, c1.tensors(), dev, layers=late)
+    W = {i: w for i, (w, _) in run["maps"].items()}
+    B = {i: b for i, (_, b) in run["maps"].items()}
+    fill = "identity" if name == "identity" else "proj"
+    arm = Arm(name, split=S, tail=c1.TAIL, fill=fill, projector=Projector(S, W, B) if fill == "proj" else None)
+    rows = c1.exact_rows() if name == "exact" else None
+    logits, cache, P = finish(model, run["hs"][S].to(dev, torch.bfloat16), arm, c1.KEEP, exact_rows=rows)
+    torch.cuda.synchronize()
+    assert P == int(gold[f"{name}_P"])
+    lg = logits.double().cpu()
+    el = rel(lg.numpy() @ c1.probes(103, 1024, 4).numpy(), gold[f"{name}_logits_u"])
+    elast = rel(lg[-1].numpy(), gold[f"{name}_logits_last"])
+    agree = float((lg.argmax(-1).numpy() == gold[f"{name}_argmax"]).mean())
+    u = c1.probes(102, 64)
+    worst = 0.0
+    for i in late:
+        assert cache[i]["n"] == int(gold[f"{name}_n_{i}"]) == c1.N_PROMPT
+        for part in ("k", "v"):
+            got = (cache[i][part].double().cpu() @ u).numpy()
+            worst = max(worst, rel(got, gold[f"{name}_{part}_u_{i}"]))
+            assert rel(got[:, P:], gold[f"{name}_{part}_u_{i}"][:, P:]) < TOL      # the tail's own slots
+    print(f"{name}: tail logits rel err {el:.2e} (last row {elast:.2e}), argmax agreement {agree:.3f}, "
+          f"worst K/V {worst:.2e}")
+    assert el < TOL and elast < TOL and worst < TOL and agree > 0.9
