@@ -127,6 +127,20 @@ int rf_attend_rows(const uint16_t* q, int64_t ldq, const int64_t* qpos, int64_t 
 /* Workspace bytes rf_attend_rows uses to split the key range fully for these sizes (0: no split). Host only. */
 int rf_attend_rows_workspace_bytes(int64_t nq, int hq, int hkv, int d, int64_t cache_rows, size_t* bytes);
 
+/* Causal attention of nq consecutive queries q [nq, hq d] at cache slots slot0 .. slot0 + nq - 1 over the
+ * first n_keys rows of kbuf / vbuf [hkv, cap, d]: query j sees keys 0 .. slot0 + j (slot0 + nq <= n_keys).
+ * Scores in fp32 scaled by `scale`, softmax in fp32, probabilities as bf16 into the second product; writes
+ * out [nq, hq d] (row stride ldo, 8-byte aligned). With slot0 = n_keys - nq this is the exact tail's
+ * attention in Model.layer, ops.attend (code/kva/ops.py:107-128, code/kva/model.py:247-257). Needs d 64 or
+ * 128 and hq / hkv in {1, 2, 4, 8}. The workspace (caller-owned device memory, 16-byte aligned, at least
+ * rf_attend_causal_workspace_bytes) receives V transposed. */
+int rf_attend_causal(const uint16_t* q, int64_t ldq, int64_t nq, int64_t slot0, int hq, int d, const uint16_t* kbuf,
+                     const uint16_t* vbuf, int hkv, int64_t head_stride, int64_t row_stride, int64_t n_keys,
+                     float scale, uint16_t* out, int64_t ldo, void* workspace, size_t ws_bytes, hipStream_t stream);
+
+/* Workspace bytes rf_attend_causal needs: hkv d round_up(n_keys, 64) bf16. Host only. */
+int rf_attend_causal_workspace_bytes(int hkv, int d, int64_t n_keys, size_t* bytes);
+
 /* out = bf16(x + y) row by row (rows x H) and out's row sum-of-squares partials ssq [rows, H / 256]: the
  * residual adds of layer_rows (code/kva/model.py:274, Model.mlp :114). out may alias x. */
 int rf_residual_add(const uint16_t* x, int64_t ldx, const uint16_t* y, int64_t ldy, uint16_t* out, int64_t ldo,

@@ -1,0 +1,352 @@
+// Causal attention of many consecutive queries over one layer's K / V cache: the exact tail's
+// attention in Model.layer (code/kva/ops.py:107-128 attend, queries bottom-right aligned with the keys),
+// head_dim 64 or 128, grouped-query heads with a group of 1, 2, 4 or 8.
+//
+// V is first transposed into the workspace (k_vt: V^T [hkv, d, round_up(n, 64)], zero past the last
+// key), so both operands of both products stream from memory into LDS as full 128-byte lines with
+// direct loads (buffer_load_dwordx4 ... lds). A block takes one K / V head and 256 query rows (256 / rep
+// consecutive queries x the rep query heads sharing the K / V head); 8 waves, each owning 32 query rows
+// of one head. The keys 0 .. (the block's last query position) go through LDS in tiles of 64, three
+// tiles in flight. Per tile and wave:
+//   S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (A = the K tile, B = the wave's queries held in registers):
+//       lane l holds, for query l % 32, the scores of keys 8 (j / 4) + 4 (l / 32) + j % 4 of each
+//       32-key half (j < 16);
+//   online softmax in fp32 in the base-2 domain (scores times scale * log2 e), keys past the query's
+//       position masked; every value a lane holds belongs to its own query, so the running maximum,
+//       the rescale and the row sum need no lane exchange except the one between the lane halves;
+//   O^T += V^T P^T on the same MFMA: P (rounded to bf16) is the B operand straight from the score
+//       registers, the contraction order over each 16-key step being keys {0..3, 8..11} + 4 (l / 32)
+//       of the step, and the V^T fragment is read in that order (two 8-byte LDS reads).
+// The probabilities enter the second product as bf16 before normalisation (the reference casts after
+// it; the difference is within rounding), scores are fp32 products of the bf16 q and k values as the
+// reference's fp32 matmul, and the output is O / (row sum) rounded to bf16.
+#include <stdint.h>
+
+#include "rf_common.h"
+
+namespace rf {
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int KT = 64;                 // keys per tile
+constexpr int NW = 8;                  // waves per block
+constexpr int NTHR = 64 * NW;
+constexpr int QROWS = 32 * NW;         // query rows (query, head) per block: 32 per wave
+constexpr int NSTAGE = 3;              // tiles in flight
+
+__device__ __forceinline__ bf16x8 as_frag(const uint4& u) { return __builtin_bit_cast(bf16x8, u); }
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), static_cast<short>(0), static_cast<int>(bytes),
+                                           0x00020000);
+}
+
+// s_waitcnt with vmcnt <= n and lgkmcnt = 0 (expcnt not waited), gfx9 encoding.
+template <int n>
+__device__ __forceinline__ void wait_vm_lgkm0() {
+  static_assert(n >= 0 && n < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (0 << 8) | ((n >> 4) << 14));
+}
+
+// LDS layout of one stage: the K tile (64 keys x AD) then the V^T tile (AD rows x 64 keys), in 16-byte
+// chunks. K row r's chunk c sits at r * KCPR + (c ^ (r % KCPR)); V^T row r's chunk c at
+// r * 8 + (c ^ ((r / 2) % 8)): the fragment reads (32 rows, one chunk or half chunk per lane) then hit
+// distinct banks.
+template <int AD>
+struct Layout {
+  static constexpr int KCPR = AD / 8;
+  static constexpr int K_U4 = KT * KCPR;
+  static constexpr int V_U4 = AD * (KT / 8);
+  static constexpr int STAGE_U4 = K_U4 + V_U4;
+  static constexpr int KLOADS = K_U4 / 64 / NW;     // direct-load instructions per wave per tile
+  static constexpr int VLOADS = V_U4 / 64 / NW;
+  static constexpr int LOADS = KLOADS + VLOADS;
+  static_assert(KLOADS * 64 * NW == K_U4 && VLOADS * 64 * NW == V_U4, "tile loads must split evenly");
+  __device__ static int kslot(int row, int c) { return row * KCPR + (c ^ (row & (KCPR - 1))); }
+  __device__ static int vslot(int row, int c) { return K_U4 + row * 8 + (c ^ ((row >> 1) & 7)); }
+};
+
+struct CausalArgs {
+  const uint16_t* q;       // [nq, >= hq * d]: query j head h at q + j * ldq + h * d
+  int64_t ldq;
+  int nq;
+  int64_t slot0;           // query j sits at slot slot0 + j and sees keys 0 .. slot0 + j
+  const uint16_t* kc;      // K cache [hkv, cap, d]
+  int64_t head_stride, row_stride;
+  int64_t n_keys;
+  const uint16_t* vt;      // V^T [hkv, d, vt_ld]
+  int64_t vt_ld;
+  int hq, hkv;
+  float scale_log2;        // scale * log2(e)
+  uint16_t* out;           // [nq, >= hq * d]
+  int64_t ldo;
+};
+
+// The direct loads of one tile into stage st: instruction i of wave w fills 64 consecutive 16-byte slots
+// (lane L slot (w * n + i) * 64 + L) from the per-lane offsets koff / voff plus the tile's byte offset.
+template <int AD>
+__device__ __forceinline__ void issue_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_buffer_rsrc_t rv,
+                                           const uint32_t (&koff)[Layout<AD>::KLOADS],
+                                           const uint32_t (&voff)[Layout<AD>::VLOADS], char* st, uint32_t kbyte,
+                                           uint32_t vbyte, int w) {
+  using L = Layout<AD>;
+#pragma unroll
+  for (int i = 0; i < L::KLOADS; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rk, (lds_ptr)(st + (w * L::KLOADS + i) * 1024), 16, koff[i], kbyte, 0, 0);
+#pragma unroll
+  for (int i = 0; i < L::VLOADS; ++i)
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rv, (lds_ptr)(st + (L::K_U4 + (w * L::VLOADS + i) * 64) * 16), 16,
+                                             voff[i], vbyte, 0, 0);
+}
+
+// One 64-key tile for one wave: S^T = K Q^T, the online softmax update, O^T += V^T P^T. st is the
+// tile's LDS stage; edge: some key of the tile lies past some query of the wave (mask needed).
+// (st is __restrict__: the LDS reads then carry alias information, and the compiler does not make them
+// wait for the direct loads in flight into the other stages; the kernel's own waits order them.)
+template <int AD>
+__device__ __forceinline__ void tile(const uint4* __restrict__ st, const bf16x8 (&qf)[AD / 16], f32x16 (&o)[AD / 32],
+                                     float& m, float& lsum, int64_t k0, bool edge, int64_t mypos, int n, int hh,
+                                     float scale_log2) {
+  using L = Layout<AD>;
+  constexpr int NS = AD / 16, NB = AD / 32;
+  f32x16 sc[2];
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sc[kb][r] = 0.f;
+    const int row = 32 * kb + n;
+#pragma unroll
+    for (int s = 0; s < NS; ++s)
+      sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_frag(st[L::kslot(row, 2 * s + hh)]), qf[s], sc[kb], 0, 0, 0);
+  }
+  // scale into the base-2 domain, mask, running maximum
+  float tmax = -INFINITY;
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      float v = sc[kb][j] * scale_log2;
+      if (edge) {
+        const int64_t key = k0 + 32 * kb + 8 * (j >> 2) + 4 * hh + (j & 3);
+        v = key <= mypos ? v : -INFINITY;
+      }
+      sc[kb][j] = v;
+      tmax = fmaxf(tmax, v);
+    }
+  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
+  const float mnew = fmaxf(m, tmax);                    // finite: key 0 is visible to every query
+  const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+  m = mnew;
+  float psum = 0.f;
+  bf16x8 pf[4];                                         // P^T fragments of the four 16-key steps
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int sub = 0; sub < 2; ++sub) {
+      uint32_t pk[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p0 = __builtin_amdgcn_exp2f(sc[kb][8 * sub + 2 * e] - mnew);
+        const float p1 = __builtin_amdgcn_exp2f(sc[kb][8 * sub + 2 * e + 1] - mnew);
+        psum += p0 + p1;
+        pk[e] = bf16_pair(p0, p1);
+      }
+      pf[2 * kb + sub] = __builtin_bit_cast(bf16x8, make_uint4(pk[0], pk[1], pk[2], pk[3]));
+    }
+  lsum = lsum * alpha + psum;
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[b][r] *= alpha;
+  // O^T[d, query] += V^T[d, keys] P^T[keys, query] over the four 16-key steps
+#pragma unroll
+  for (int stp = 0; stp < 4; ++stp) {
+    const int c0 = 2 * stp;                             // the step's first key chunk: keys 16 stp .. + 7
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      const int row = 32 * b + n;
+      const char* vrow = reinterpret_cast<const char*>(st);
+      const uint2 lo = *reinterpret_cast<const uint2*>(vrow + L::vslot(row, c0) * 16 + 8 * hh);
+      const uint2 hi = *reinterpret_cast<const uint2*>(vrow + L::vslot(row, c0 + 1) * 16 + 8 * hh);
+      o[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_frag(make_uint4(lo.x, lo.y, hi.x, hi.y)), pf[stp], o[b], 0,
+                                                     0, 0);
+    }
+  }
+}
+
+template <int AD>
+__global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
+  using L = Layout<AD>;
+  constexpr int NS = AD / 16;      // 16-deep d steps of S^T
+  constexpr int NB = AD / 32;      // 32-row d blocks of O^T
+  __shared__ uint4 lds[NSTAGE * L::STAGE_U4];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, n = lane & 31, hh = lane >> 5;
+  const int rep = a.hq / a.hkv, qp = QROWS / rep;          // consecutive queries per block
+  const int hk = blockIdx.y;
+  const int j0 = blockIdx.x * qp;
+  const int jlast = min(j0 + qp, a.nq) - 1;
+  const int64_t kmax = a.slot0 + jlast;                      // the block reads keys 0 .. kmax
+  const int ntiles = static_cast<int>(kmax / KT) + 1;
+
+  // the wave's head and queries; lanes past the last query repeat it and write nothing
+  const int hg = (32 * w) / qp, po0 = (32 * w) % qp;
+  const int jw0 = j0 + po0;
+  const int jq = min(jw0 + n, jlast);
+  const bool live = jw0 + n <= jlast;
+  const int64_t mypos = a.slot0 + jq;
+  const int64_t wave_first = a.slot0 + min(jw0, jlast), wave_last = a.slot0 + min(jw0 + 31, jlast);
+  const int head = hk * rep + hg;
+  bf16x8 qf[NS];
+  {
+    const uint16_t* qrow = a.q + static_cast<int64_t>(jq) * a.ldq + head * AD + 8 * hh;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qf[s] = as_frag(*reinterpret_cast<const uint4*>(qrow + 16 * s));
+  }
+  wait_vm_lgkm0<0>();        // the queries are in registers before any tile load is in flight
+
+  // direct loads: instruction i of wave w fills 64 consecutive slots of a tile; lane L's slot
+  // determines the row and logical chunk it fetches
+  const uint16_t* kh = a.kc + hk * a.head_stride;
+  const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kh, static_cast<uint32_t>(a.n_keys * a.row_stride * 2));
+  const __amdgpu_buffer_rsrc_t rv =
+      buffer_rsrc(a.vt + static_cast<int64_t>(hk) * AD * a.vt_ld, static_cast<uint32_t>(AD * a.vt_ld * 2));
+  uint32_t koff[L::KLOADS], voff[L::VLOADS];
+#pragma unroll
+  for (int i = 0; i < L::KLOADS; ++i) {
+    const int s = (w * L::KLOADS + i) * 64 + lane;
+    const int row = s / L::KCPR, pc = s % L::KCPR, c = pc ^ (row & (L::KCPR - 1));
+    koff[i] = static_cast<uint32_t>((row * a.row_stride + c * 8) * 2);
+  }
+#pragma unroll
+  for (int i = 0; i < L::VLOADS; ++i) {
+    const int s = (w * L::VLOADS + i) * 64 + lane;
+    const int row = s / 8, pc = s % 8, c = pc ^ ((row >> 1) & 7);
+    voff[i] = static_cast<uint32_t>((row * a.vt_ld + c * 8) * 2);
+  }
+  char* base = reinterpret_cast<char*>(lds);
+  auto issue = [&](int it) {
+    issue_tile<AD>(rk, rv, koff, voff, base + (it % NSTAGE) * L::STAGE_U4 * 16,
+                   static_cast<uint32_t>(static_cast<int64_t>(it) * KT * a.row_stride * 2),
+                   static_cast<uint32_t>(it * KT * 2), w);
+  };
+
+  f32x16 o[NB];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) o[b][r] = 0.f;
+  float m = -INFINITY, lsum = 0.f;
+
+  issue(0);
+  if (ntiles > 1) issue(1);
+  for (int it = 0; it < ntiles; ++it) {
+    if (it + 1 < ntiles) wait_vm_lgkm0<L::LOADS>();       // this tile's loads done, the next one's may fly
+    else wait_vm_lgkm0<0>();
+    __builtin_amdgcn_s_barrier();                         // every wave's share of the tile has landed and
+    if (it + 2 < ntiles) issue(it + 2);                   // every wave is done with the stage reloaded here
+    const int64_t k0 = static_cast<int64_t>(it) * KT;
+    if (k0 > wave_last) continue;                         // every key of the tile is past the wave's queries
+    tile<AD>(lds + (it % NSTAGE) * L::STAGE_U4, qf, o, m, lsum, k0, k0 + KT - 1 > wave_first, mypos, n, hh,
+             a.scale_log2);
+  }
+  wait_vm_lgkm0<0>();
+
+  // normalise and write: lane holds O[query n][d = 32 b + 8 (j / 4) + 4 hh + j % 4]
+  const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+  if (!live) return;
+  const float inv = 1.0f / ltot;
+  uint16_t* dst = a.out + static_cast<int64_t>(jq) * a.ldo + head * AD + 4 * hh;
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int g = 0; g < 4; ++g)
+      *reinterpret_cast<uint2*>(dst + 32 * b + 8 * g) =
+          make_uint2(bf16_pair(o[b][4 * g] * inv, o[b][4 * g + 1] * inv),
+                     bf16_pair(o[b][4 * g + 2] * inv, o[b][4 * g + 3] * inv));
+}
+
+// V^T [hkv, AD, vt_ld] from the V cache [hkv, cap, AD]: keys 0 .. n - 1, zeros up to vt_ld. A block
+// takes 64 keys of one head through LDS; rows of the result are written as 16-byte chunks of 8 keys.
+template <int AD>
+__global__ __launch_bounds__(256) void k_vt(const uint16_t* __restrict__ v, int64_t head_stride, int64_t row_stride,
+                                            int64_t n, uint16_t* __restrict__ vt, int64_t vt_ld) {
+  constexpr int CPR = AD / 8, ROW = AD + 8;
+  __shared__ uint16_t tile[KT * ROW];
+  const int t = threadIdx.x, hk = blockIdx.y;
+  const int64_t k0 = static_cast<int64_t>(blockIdx.x) * KT;
+  const uint16_t* vh = v + hk * head_stride;
+  for (int c = t; c < KT * CPR; c += 256) {
+    const int key = c / CPR, ch = c % CPR;
+    uint4 u = make_uint4(0u, 0u, 0u, 0u);
+    if (k0 + key < n) u = *reinterpret_cast<const uint4*>(vh + (k0 + key) * row_stride + ch * 8);
+    *reinterpret_cast<uint4*>(tile + key * ROW + ch * 8) = u;
+  }
+  __syncthreads();
+  uint16_t* dh = vt + static_cast<int64_t>(hk) * AD * vt_ld + k0;
+  for (int c = t; c < AD * (KT / 8); c += 256) {
+    const int d = c / (KT / 8), kc = c % (KT / 8);
+    uint16_t e[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) e[i] = tile[(kc * 8 + i) * ROW + d];
+    *reinterpret_cast<uint4*>(dh + d * vt_ld + kc * 8) =
+        make_uint4(pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]), pack2(e[6], e[7]));
+  }
+}
+
+int64_t vt_cols(int64_t n_keys) { return (n_keys + KT - 1) / KT * KT; }
+
+}  // namespace
+}  // namespace rf
+
+using namespace rf;
+
+extern "C" int rf_attend_causal_workspace_bytes(int hkv, int d, int64_t n_keys, size_t* bytes) {
+  if (!bytes || hkv <= 0 || (d != 64 && d != 128) || n_keys < 0)
+    return fail(RF_EINVAL_ARG, "rf_attend_causal_workspace_bytes: arguments");
+  *bytes = static_cast<size_t>(hkv) * d * vt_cols(n_keys) * 2;
+  return RF_OK;
+}
+
+extern "C" int rf_attend_causal(const uint16_t* q, int64_t ldq, int64_t nq, int64_t slot0, int hq, int d,
+                                const uint16_t* kbuf, const uint16_t* vbuf, int hkv, int64_t head_stride,
+                                int64_t row_stride, int64_t n_keys, float scale, uint16_t* out, int64_t ldo,
+                                void* workspace, size_t ws_bytes, hipStream_t stream) {
+  if (!q || !kbuf || !vbuf || !out || !workspace) return fail(RF_EINVAL_ARG, "rf_attend_causal: null pointer");
+  if (d != 64 && d != 128) return fail(RF_EUNSUPPORTED, "rf_attend_causal: head_dim %d (the kernel takes 64, 128)", d);
+  if (hq <= 0 || hkv <= 0 || hq % hkv || (hq / hkv != 1 && hq / hkv != 2 && hq / hkv != 4 && hq / hkv != 8))
+    return fail(RF_EUNSUPPORTED, "rf_attend_causal: %d query heads over %d K / V heads (group of 1, 2, 4 or 8)", hq,
+                hkv);
+  if (nq < 0 || nq > (1 << 30) || slot0 < 0 || slot0 + nq > n_keys)
+    return fail(RF_EINVAL_SHAPE, "rf_attend_causal: queries at slots [%lld, %lld) past the %lld keys", (long long)slot0,
+                (long long)(slot0 + nq), (long long)n_keys);
+  if (ldq < static_cast<int64_t>(hq) * d || ldo < static_cast<int64_t>(hq) * d || ldq % 8 || ldo % 4 ||
+      row_stride < d || row_stride % 8 || head_stride % 8 || n_keys * row_stride * 2 >= (1ll << 32) ||
+      static_cast<int64_t>(d) * vt_cols(n_keys) * 2 >= (1ll << 32))
+    return fail(RF_EINVAL_SHAPE, "rf_attend_causal: strides (ldq %lld, ldo %lld, row %lld) or %lld keys",
+                (long long)ldq, (long long)ldo, (long long)row_stride, (long long)n_keys);
+  if (!aligned16(q) || !aligned16(kbuf) || !aligned16(vbuf) || !aligned16(workspace) ||
+      (reinterpret_cast<uintptr_t>(out) & 7u))
+    return fail(RF_EINVAL_SHAPE, "rf_attend_causal: alignment");
+  const int64_t vt_ld = vt_cols(n_keys);
+  if (ws_bytes < static_cast<size_t>(hkv) * d * vt_ld * 2)
+    return fail(RF_EINVAL_SHAPE, "rf_attend_causal: workspace %zu bytes < %lld", ws_bytes,
+                (long long)(static_cast<int64_t>(hkv) * d * vt_ld * 2));
+  if (nq == 0) return RF_OK;
+  uint16_t* vt = static_cast<uint16_t*>(workspace);
+  const dim3 gt(static_cast<unsigned>(vt_ld / KT), static_cast<unsigned>(hkv));
+  if (d == 128) hipLaunchKernelGGL(k_vt<128>, gt, dim3(256), 0, stream, vbuf, head_stride, row_stride, n_keys, vt, vt_ld);
+  else hipLaunchKernelGGL(k_vt<64>, gt, dim3(256), 0, stream, vbuf, head_stride, row_stride, n_keys, vt, vt_ld);
+  const int st = check_launch("rf_attend_causal (V transpose)");
+  if (st != RF_OK) return st;
+  CausalArgs a{q, ldq, static_cast<int>(nq), slot0, kbuf, head_stride, row_stride, n_keys, vt, vt_ld, hq, hkv,
+               scale * 1.4426950408889634f, out, ldo};
+  const int qp = QROWS / (hq / hkv);
+  const dim3 grid(static_cast<unsigned>((nq + qp - 1) / qp), static_cast<unsigned>(hkv));
+  if (d == 128) hipLaunchKernelGGL(k_attend_causal<128>, grid, dim3(NTHR), 0, stream, a);
+  else hipLaunchKernelGGL(k_attend_causal<64>, grid, dim3(NTHR), 0, stream, a);
+  return check_launch("rf_attend_causal");
+}

@@ -46,6 +46,9 @@ SIGNATURES = {
     "rf_norm_q": [_P, _I64, _P, _I64, _I64, _F32, _P, _I32, _I32, _P, _I32, _P, _I32, _P, _P, _I64, _P],
     "rf_attend_rows": [_P, _I64, _P, _I64, _I32, _I32, _P, _P, _I32, _I64, _I64, _I64, _F32, _P, _I64, _P, _SZ, _P],
     "rf_attend_rows_workspace_bytes": [_I64, _I32, _I32, _I32, _I64, _PSZ],
+    "rf_attend_causal": [_P, _I64, _I64, _I64, _I32, _I32, _P, _P, _I32, _I64, _I64, _I64, _F32, _P, _I64, _P, _SZ,
+                         _P],
+    "rf_attend_causal_workspace_bytes": [_I32, _I32, _I64, _PSZ],
     "rf_residual_add": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _P],
     "rf_silu_mul": [_P, _I64, _I64, _I64, _P, _I64, _P],
 }

@@ -301,9 +301,21 @@ class FillModel:
         idx = torch.arange(T, device=h.device)
         q = ops.norm_q(h, ssq, self.eps, w["wq"], self.n_heads, self.head_dim, w.get("q_norm"), self.knorm_kind, cs,
                        idx)
-        o = ops.attend_rows(q, idx + slot, c["kbuf"], c["vbuf"], c["n"], self.n_heads, self.scale,
-                            workspace=self._attn_workspace(T, c["n"], h.device))
+        if self.n_heads // self.n_kv in ops.CAUSAL_GROUPS and self.head_dim in (64, 128):
+            o = ops.attend_causal(q, slot, c["kbuf"], c["vbuf"], c["n"], self.n_heads, self.scale,
+                                  workspace=self._vt_workspace(c["n"], h.device))
+        else:
+            o = ops.attend_rows(q, idx + slot, c["kbuf"], c["vbuf"], c["n"], self.n_heads, self.scale,
+                                workspace=self._attn_workspace(T, c["n"], h.device))
         return self._out_mlp(w, h, o)
+
+    def _vt_workspace(self, n, device):
+        """The tail attention's transposed-V workspace, shared by every layer (stream-ordered reuse)."""
+        need = ops.attend_causal_workspace_bytes(self.n_kv, self.head_dim, n)
+        ws = getattr(self, "_vt_ws", None)
+        if ws is None or ws.numel() < need or ws.device != device:
+            self._vt_ws = ws = torch.empty(need, dtype=torch.uint8, device=device)
+        return ws
 
     def logits(self, h, ssq=None):
         """F.linear(final_norm(h), lm_head).float() (code/kva/model.py:110-111): [rows, V] fp32 from bf16

@@ -254,6 +254,41 @@ def attend_rows(q, qpos, kbuf, vbuf, n, hq, scale, out=None, workspace="auto"):
     return out
 
 
+CAUSAL_GROUPS = (1, 2, 4, 8)
+
+
+def attend_causal_workspace_bytes(hkv, d, n):
+    """Device bytes attend_causal needs (V transposed)."""
+    b = ctypes.c_size_t(0)
+    _lib.call("rf_attend_causal_workspace_bytes", hkv, d, n, ctypes.byref(b))
+    return b.value
+
+
+def attend_causal(q, slot0, kbuf, vbuf, n, hq, scale, out=None, workspace=None):
+    """Causal attention of nq consecutive queries q [nq, hq d] at cache slots slot0 .. slot0 + nq - 1 over
+    the first n rows of kbuf / vbuf [hkv, cap, d] (query j sees keys 0 .. slot0 + j). Returns [nq, hq d]
+    bf16. workspace: uint8 device memory of attend_causal_workspace_bytes (allocated here if None)."""
+    _need(q, "q", torch.bfloat16, 2)
+    for name, t in (("kbuf", kbuf), ("vbuf", vbuf)):
+        _need(t, name, torch.bfloat16, 3)
+    if kbuf.stride() != vbuf.stride() or kbuf.shape != vbuf.shape:
+        raise ValueError("kbuf / vbuf must share shape and strides")
+    hkv, cap, d = kbuf.shape
+    nq = q.shape[0]
+    if q.shape[1] < hq * d or n > cap:
+        raise ValueError("attend_causal: shapes")
+    out = torch.empty(nq, hq * d, dtype=torch.bfloat16, device=q.device) if out is None else out
+    _need(out, "out", torch.bfloat16, 2)
+    need = attend_causal_workspace_bytes(hkv, d, n)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    _need(workspace, "workspace", torch.uint8, 1)
+    _lib.call("rf_attend_causal", _ptr(q), q.stride(0), nq, int(slot0), hq, d, _ptr(kbuf), _ptr(vbuf), hkv,
+              kbuf.stride(0), kbuf.stride(1), n, float(scale), _ptr(out), out.stride(0), _ptr(workspace),
+              workspace.numel(), _stream(q))
+    return out
+
+
 def residual_add(x, y, out=None, ssq=None):
     """out = bf16(x + y) and its row sum-of-squares partials."""
     _need(x, "x", torch.bfloat16, 2)

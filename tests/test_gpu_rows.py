@@ -162,3 +162,74 @@ def test_fill_late_runs_the_exact_rows_through_every_layer(dev):
         er = rel_err(cache[i]["k"][:, rows.to(dev)], oc[i]["k"][:, rows])
         print(f"layer {i}: row inputs {eh:.2e}, K {ek:.2e} V {ev:.2e} exact-row K {er:.2e}")
         assert eh < TOL and ek < TOL and ev < TOL and er < TOL
+
+
+@pytest.mark.parametrize("hq,hkv,d,nq,slot0,n", [(32, 8, 128, 300, 1000, 1300),      # a tail: the last nq keys
+                                                 (8, 8, 64, 700, 0, 700),             # group 1, from slot 0
+                                                 (16, 2, 128, 333, 517, 1200),        # group 8, keys after
+                                                 (4, 2, 64, 1000, 90, 1100),          # group 2, partial block
+                                                 (32, 8, 128, 64, 5, 69)])            # fewer keys than a tile pair
+def test_attend_causal_matches_oracle(dev, hq, hkv, d, nq, slot0, n):
+    """The many-query kernel (rf_attend_causal: V transposed, 256 query rows per block) against the
+    oracle's attend_at at positions slot0 .. slot0 + nq - 1 (attend itself when they are the last keys),
+    and against rf_attend_rows on the same queries."""
+    from rfill import ops
+    q, k, v = _qkv(nq, hq, hkv, d, n, seed=nq + d)
+    cap = n + 64
+    kb = torch.zeros(hkv, cap, d, dtype=torch.bfloat16)
+    vb = torch.zeros_like(kb)
+    kb[:, :n], vb[:, :n] = k, v
+    vb[:, n:] = float("nan")                          # rows past the keys must never be read
+    scale = d ** -0.5
+    qd, kd, vd = q.to(dev), kb.to(dev), vb.to(dev)
+    got = ops.attend_causal(qd, slot0, kd, vd, n, hq, scale)
+    qpos = torch.arange(slot0, slot0 + nq)
+    rows = ops.attend_rows(qd, qpos.to(dev), kd, vd, n, hq, scale)
+    torch.cuda.synchronize()
+    qh = q.view(nq, hq, d).transpose(0, 1)
+    want = (oops.attend(qh, k, v, scale) if slot0 + nq == n
+            else oops.attend_at(qh, k, v, scale, qpos))
+    err, err_rows = rel_err(got, want), rel_err(got, rows)
+    print(f"hq {hq} hkv {hkv} d {d} nq {nq} slot0 {slot0} n {n}: rel err {err:.2e} vs oracle, "
+          f"{err_rows:.2e} vs rf_attend_rows")
+    assert torch.isfinite(got.float()).all()
+    assert err < TOL and err_rows < TOL
+    if slot0 == 0:                                    # the query at slot 0 sees key 0 only: V[0] exactly
+        first = got[0].view(hq, d).cpu()
+        for h in range(hq):
+            assert torch.equal(first[h], v[h // (hq // hkv), 0])
+
+
+def test_attend_causal_is_causal_and_deterministic(dev):
+    from rfill import ops
+    hq, hkv, d, n, nq = 32, 8, 128, 900, 300
+    q, k, v = _qkv(nq, hq, hkv, d, n, seed=7)
+    kb = torch.zeros(hkv, n + 64, d, dtype=torch.bfloat16, device=dev)
+    vb = torch.zeros_like(kb)
+    kb[:, :n], vb[:, :n] = k.to(dev), v.to(dev)
+    slot0 = 400                                       # queries at slots 400 .. 699; keys 700 .. 899 unseen
+    base = ops.attend_causal(q.to(dev), slot0, kb, vb, n, hq, d ** -0.5)
+    again = ops.attend_causal(q.to(dev), slot0, kb, vb, n, hq, d ** -0.5)
+    assert torch.equal(base, again)
+    kb2, vb2 = kb.clone(), vb.clone()
+    kb2[:, 700:n] = 7.0
+    vb2[:, 700:n] = -3.0
+    assert torch.equal(base, ops.attend_causal(q.to(dev), slot0, kb2, vb2, n, hq, d ** -0.5))
+    # a key between the first and the last query changes only the queries at or after it
+    vb2[:, 550] += 1.0
+    later = ops.attend_causal(q.to(dev), slot0, kb2, vb2, n, hq, d ** -0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(base[:150], later[:150])
+    assert not torch.equal(base[150:], later[150:])
+
+
+def test_attend_causal_refuses(dev):
+    from rfill import ops
+    kb = torch.zeros(2, 200, 128, dtype=torch.bfloat16, device=dev)
+    q = torch.zeros(10, 4 * 128, dtype=torch.bfloat16, device=dev)
+    with pytest.raises(ValueError):
+        ops.attend_causal(q, 195, kb, kb.clone(), 200, 4, 0.1)                # slots past the keys
+    q6 = torch.zeros(10, 6 * 128, dtype=torch.bfloat16, device=dev)
+    from rfill._lib import UnsupportedArchitecture
+    with pytest.raises(UnsupportedArchitecture):
+        ops.attend_causal(q6, 0, kb, kb.clone(), 200, 6, 0.1)                 # group of 3
