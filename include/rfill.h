@@ -35,10 +35,20 @@ int rf_version(void);
  * b [P, h_in] (row stride ldb), w [h_out, h_in] (F.linear layout), c [h_out] or NULL,
  * x [P, h_out] (row stride ldx). Also writes ssq [P, h_out / 256]: each row's sum of squares of the
  * rounded x over consecutive 256-column groups (the next layer's RMSNorm statistics).
- * Needs h_in % 64 == 0, h_out % 256 == 0, ldb / ldx multiples of 8, 16-byte aligned pointers. */
+ * Needs h_in % 32 == 0, h_out % 256 == 0, ldb / ldx multiples of 8, 16-byte aligned pointers.
+ * workspace / ws_bytes (optional, NULL / 0): see rf_gemm_workspace_bytes. */
 int rf_map_apply(const uint16_t* b, int64_t ldb, const uint16_t* w, const uint16_t* c,
                  uint16_t* x, int64_t ldx, float* ssq, int64_t P, int64_t h_in, int64_t h_out,
-                 hipStream_t stream);
+                 void* workspace, size_t ws_bytes, hipStream_t stream);
+
+/* Bytes of the optional workspace of the GEMM entry points (rf_map_apply, rf_norm_kv_write, rf_norm_q,
+ * rf_norm_linear) for an M x N x K product (M rows, N outputs, K inputs): nonzero when the output tiles
+ * (256 x 256) are too few to give every CU one, e.g. the exact rows' or the tail's projections. Given a
+ * workspace at least this large (caller-owned device memory, 16-byte aligned), the entry point splits K
+ * over more blocks, keeps their fp32 partial sums there and adds them in a fixed order before the
+ * epilogue (the same bits every run; the unsplit sum order differs within fp32 rounding). With a
+ * smaller or NULL workspace it runs unsplit. Host only. */
+int rf_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, size_t* bytes);
 
 /* Row sum-of-squares partials of given layer inputs x [P, H] -> ssq [P, H / 256], the statistics the
  * fused input RMSNorm of rf_norm_kv_write reads (the mean of x^2 in code/kva/ops.py:14-25).
@@ -77,12 +87,14 @@ int rf_rope_table(const int64_t* pos, int64_t P, const float* inv_freq, int rot,
  *   kbuf / vbuf: cache [hkv, cap, d] with element strides head_stride / row_stride; row j goes to
  *       slot slot_begin + j.
  * Needs H % 64 == 0, 2 hkv d % 256 == 0, 256 % d == 0, d % 8 == 0, rot even, rot <= d, rot / 2 a
- * multiple of 8 or equal to 4, slot_begin + P <= cap. */
+ * multiple of 8 or equal to 4, slot_begin + P <= cap. workspace / ws_bytes (optional, NULL / 0): see
+ * rf_gemm_workspace_bytes (M = P, N = 2 hkv d, K = H). */
 int rf_norm_kv_write(const uint16_t* x, int64_t ldx, const float* ssq, int64_t P, int64_t H, float eps,
                      const uint16_t* wkv, int hkv, int d, const uint16_t* knorm, int knorm_kind,
                      const uint16_t* cs, int rot,
                      uint16_t* kbuf, uint16_t* vbuf, int64_t head_stride, int64_t row_stride,
-                     int64_t slot_begin, int64_t cap, hipStream_t stream);
+                     int64_t slot_begin, int64_t cap, void* workspace, size_t ws_bytes,
+                     hipStream_t stream);
 
 /* RoPE on given pre-RoPE K and the K / V cache write of m rows.
  * Replaces Model.fill_kv (code/kva/model.py:161-165): ops.apply_rope (ops.py:66-77) + _append_kv.
@@ -106,10 +118,11 @@ int rf_row_gather(const uint16_t* x, int64_t ldx, int64_t P, int64_t H, const in
  * kind 0 rms_norm, 1 rms_norm_zc), RoPE with table row pos[j] of cs (rf_rope_table of positions 0..).
  * Writes q [rows, hq d] (row stride ldq). Replaces Llama.queries / Qwen3 q_norm (code/kva/model.py:241-245,
  * :347-352) on the normed rows. Needs H % 256 == 0, hq d % 256 == 0, and the rotary limits of
- * rf_norm_kv_write. */
+ * rf_norm_kv_write. workspace / ws_bytes (optional): see rf_gemm_workspace_bytes (M = rows, N = hq d). */
 int rf_norm_q(const uint16_t* x, int64_t ldx, const float* ssq, int64_t rows, int64_t H, float eps,
               const uint16_t* wq, int hq, int d, const uint16_t* qnorm, int qnorm_kind, const uint16_t* cs, int rot,
-              const int64_t* pos, uint16_t* q, int64_t ldq, hipStream_t stream);
+              const int64_t* pos, uint16_t* q, int64_t ldq, void* workspace, size_t ws_bytes,
+              hipStream_t stream);
 
 /* Causal attention of nq query rows q [nq, hq d] at sorted positions qpos [nq] (int64, device; each
  * < cache_rows) over the cache kbuf / vbuf [hkv, cap, d] (element strides head_stride / row_stride): query
@@ -127,19 +140,25 @@ int rf_attend_rows(const uint16_t* q, int64_t ldq, const int64_t* qpos, int64_t 
 /* Workspace bytes rf_attend_rows uses to split the key range fully for these sizes (0: no split). Host only. */
 int rf_attend_rows_workspace_bytes(int64_t nq, int hq, int hkv, int d, int64_t cache_rows, size_t* bytes);
 
-/* Causal attention of nq consecutive queries q [nq, hq d] at cache slots slot0 .. slot0 + nq - 1 over the
- * first n_keys rows of kbuf / vbuf [hkv, cap, d]: query j sees keys 0 .. slot0 + j (slot0 + nq <= n_keys).
- * Scores in fp32 scaled by `scale`, softmax in fp32, probabilities as bf16 into the second product; writes
- * out [nq, hq d] (row stride ldo, 8-byte aligned). With slot0 = n_keys - nq this is the exact tail's
- * attention in Model.layer, ops.attend (code/kva/ops.py:107-128, code/kva/model.py:247-257). Needs d 64 or
- * 128 and hq / hkv in {1, 2, 4, 8}. The workspace (caller-owned device memory, 16-byte aligned, at least
- * rf_attend_causal_workspace_bytes) receives V transposed. */
-int rf_attend_causal(const uint16_t* q, int64_t ldq, int64_t nq, int64_t slot0, int hq, int d, const uint16_t* kbuf,
-                     const uint16_t* vbuf, int hkv, int64_t head_stride, int64_t row_stride, int64_t n_keys,
-                     float scale, uint16_t* out, int64_t ldo, void* workspace, size_t ws_bytes, hipStream_t stream);
+/* Causal attention of nq queries q [nq, hq d] over the first n_keys rows of kbuf / vbuf [hkv, cap, d]:
+ * query j sees keys 0 .. qpos[j] (qpos: sorted int64 positions on the device), or, with qpos NULL,
+ * consecutive queries at slots slot0 .. slot0 + nq - 1 (slot0 + nq <= n_keys). Scores in fp32 scaled by
+ * `scale`, softmax in fp32, probabilities as bf16 into the second product; writes out [nq, hq d] (row
+ * stride ldo, 8-byte aligned). With slot0 = n_keys - nq this is the exact tail's attention in
+ * Model.layer, ops.attend (code/kva/ops.py:107-128, code/kva/model.py:247-257); with qpos the exact
+ * rows' attention in layer_rows, ops.attend_at / attend_rows (code/kva/ops.py:131-170). Needs d 64 or 128
+ * and hq / hkv in {1, 2, 4, 8}. The workspace (caller-owned device memory, 16-byte aligned) receives V
+ * transposed and, when the query blocks are too few for the GPU, the partial results of a key-range
+ * split, merged in a fixed order: rf_attend_causal_workspace_bytes gives the size for the full split (a
+ * smaller one, at least the transposed V, gives fewer splits). */
+int rf_attend_causal(const uint16_t* q, int64_t ldq, int64_t nq, const int64_t* qpos, int64_t slot0, int hq, int d,
+                     const uint16_t* kbuf, const uint16_t* vbuf, int hkv, int64_t head_stride, int64_t row_stride,
+                     int64_t n_keys, float scale, uint16_t* out, int64_t ldo, void* workspace, size_t ws_bytes,
+                     hipStream_t stream);
 
-/* Workspace bytes rf_attend_causal needs: hkv d round_up(n_keys, 64) bf16. Host only. */
-int rf_attend_causal_workspace_bytes(int hkv, int d, int64_t n_keys, size_t* bytes);
+/* Workspace bytes rf_attend_causal uses for nq queries over n_keys keys (V transposed + full key split). Host
+ * only. */
+int rf_attend_causal_workspace_bytes(int64_t nq, int hq, int hkv, int d, int64_t n_keys, size_t* bytes);
 
 /* out = bf16(x + y) row by row (rows x H) and out's row sum-of-squares partials ssq [rows, H / 256]: the
  * residual adds of layer_rows (code/kva/model.py:274, Model.mlp :114). out may alias x. */
@@ -154,9 +173,11 @@ int rf_silu_mul(const uint16_t* gu, int64_t ldg, int64_t rows, int64_t I, uint16
 /* Fused RMSNorm + linear: out[P, N] = bf16(r_row * (x w^T)) with r_row = 1 / sqrt(mean(x^2) + eps) from
  * the row partials ssq [P, H / 256] and the norm gain folded into w [N, H] (rf_fold_norm). The Gated
  * DeltaNet in-projections of a fill (code/kva/model.py:448-450 after in_norm, :513). Needs
- * H % 256 == 0, N % 256 == 0 (pad w with zero rows), 16-byte aligned pointers. */
+ * H % 256 == 0, N % 256 == 0 (pad w with zero rows), 16-byte aligned pointers. workspace / ws_bytes
+ * (optional): see rf_gemm_workspace_bytes (M = P, K = H). */
 int rf_norm_linear(const uint16_t* x, int64_t ldx, const float* ssq, int64_t P, int64_t H, float eps,
-                   const uint16_t* w, int64_t N, uint16_t* out, int64_t ldo, hipStream_t stream);
+                   const uint16_t* w, int64_t N, uint16_t* out, int64_t ldo, void* workspace, size_t ws_bytes,
+                   hipStream_t stream);
 
 /* Gated DeltaNet fill of one layer from its in-projection rows pre [P, ld] bf16 (columns: q [nk dk] |
  * k [nk dk] | v [nv dv] | b [nv] | a [nv]): causal conv + SiLU (conv_w [C, 4], C = 2 nk dk + nv dv,

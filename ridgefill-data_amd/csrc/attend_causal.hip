@@ -22,6 +22,8 @@
 // reference's fp32 matmul, and the output is O / (row sum) rounded to bf16.
 #include <stdint.h>
 
+#include <algorithm>
+
 #include "rf_common.h"
 
 namespace rf {
@@ -74,7 +76,8 @@ struct CausalArgs {
   const uint16_t* q;       // [nq, >= hq * d]: query j head h at q + j * ldq + h * d
   int64_t ldq;
   int nq;
-  int64_t slot0;           // query j sits at slot slot0 + j and sees keys 0 .. slot0 + j
+  const int64_t* qpos;     // sorted query positions (query j sees keys 0 .. qpos[j]), or null:
+  int64_t slot0;           // query j at slot0 + j
   const uint16_t* kc;      // K cache [hkv, cap, d]
   int64_t head_stride, row_stride;
   int64_t n_keys;
@@ -84,7 +87,15 @@ struct CausalArgs {
   float scale_log2;        // scale * log2(e)
   uint16_t* out;           // [nq, >= hq * d]
   int64_t ldo;
+  float* part;             // splits > 1: per (query block, K / V head, split) O [256][d], max [256], sum [256]
 };
+
+__device__ __forceinline__ int64_t query_pos(const CausalArgs& a, int j) { return a.qpos ? a.qpos[j] : a.slot0 + j; }
+
+template <int AD>
+__device__ __forceinline__ float* part_block(const CausalArgs& a, int qb, int hk, int sp) {
+  return a.part + ((static_cast<int64_t>(qb) * a.hkv + hk) * gridDim.z + sp) * (QROWS * (AD + 2));
+}
 
 // The direct loads of one tile into stage st: instruction i of wave w fills 64 consecutive 16-byte slots
 // (lane L slot (w * n + i) * 64 + L) from the per-lane offsets koff / voff plus the tile's byte offset.
@@ -138,8 +149,9 @@ __device__ __forceinline__ void tile(const uint4* __restrict__ st, const bf16x8 
       tmax = fmaxf(tmax, v);
     }
   tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-  const float mnew = fmaxf(m, tmax);                    // finite: key 0 is visible to every query
-  const float alpha = __builtin_amdgcn_exp2f(m - mnew);
+  const float mnew = fmaxf(m, tmax);
+  const float mref = mnew == -INFINITY ? 0.f : mnew;    // every key so far masked (a split past the query)
+  const float alpha = __builtin_amdgcn_exp2f(m - mref);
   m = mnew;
   float psum = 0.f;
   bf16x8 pf[4];                                         // P^T fragments of the four 16-key steps
@@ -150,8 +162,8 @@ __device__ __forceinline__ void tile(const uint4* __restrict__ st, const bf16x8 
       uint32_t pk[4];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float p0 = __builtin_amdgcn_exp2f(sc[kb][8 * sub + 2 * e] - mnew);
-        const float p1 = __builtin_amdgcn_exp2f(sc[kb][8 * sub + 2 * e + 1] - mnew);
+        const float p0 = __builtin_amdgcn_exp2f(sc[kb][8 * sub + 2 * e] - mref);
+        const float p1 = __builtin_amdgcn_exp2f(sc[kb][8 * sub + 2 * e + 1] - mref);
         psum += p0 + p1;
         pk[e] = bf16_pair(p0, p1);
       }
@@ -189,16 +201,20 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
   const int hk = blockIdx.y;
   const int j0 = blockIdx.x * qp;
   const int jlast = min(j0 + qp, a.nq) - 1;
-  const int64_t kmax = a.slot0 + jlast;                      // the block reads keys 0 .. kmax
+  const int64_t kmax = min(query_pos(a, jlast), a.n_keys - 1);     // the block reads keys 0 .. kmax
   const int ntiles = static_cast<int>(kmax / KT) + 1;
+  // this block's share of the key tiles (split blockIdx.z of gridDim.z)
+  const int ns = gridDim.z, sp = blockIdx.z;
+  const int it0 = static_cast<int>(static_cast<int64_t>(ntiles) * sp / ns);
+  const int it1 = static_cast<int>(static_cast<int64_t>(ntiles) * (sp + 1) / ns);
 
   // the wave's head and queries; lanes past the last query repeat it and write nothing
   const int hg = (32 * w) / qp, po0 = (32 * w) % qp;
   const int jw0 = j0 + po0;
   const int jq = min(jw0 + n, jlast);
   const bool live = jw0 + n <= jlast;
-  const int64_t mypos = a.slot0 + jq;
-  const int64_t wave_first = a.slot0 + min(jw0, jlast), wave_last = a.slot0 + min(jw0 + 31, jlast);
+  const int64_t mypos = query_pos(a, jq);
+  const int64_t wave_first = query_pos(a, min(jw0, jlast)), wave_last = query_pos(a, min(jw0 + 31, jlast));
   const int head = hk * rep + hg;
   bf16x8 qf[NS];
   {
@@ -229,7 +245,7 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
   }
   char* base = reinterpret_cast<char*>(lds);
   auto issue = [&](int it) {
-    issue_tile<AD>(rk, rv, koff, voff, base + (it % NSTAGE) * L::STAGE_U4 * 16,
+    issue_tile<AD>(rk, rv, koff, voff, base + ((it - it0) % NSTAGE) * L::STAGE_U4 * 16,
                    static_cast<uint32_t>(static_cast<int64_t>(it) * KT * a.row_stride * 2),
                    static_cast<uint32_t>(it * KT * 2), w);
   };
@@ -241,22 +257,38 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
     for (int r = 0; r < 16; ++r) o[b][r] = 0.f;
   float m = -INFINITY, lsum = 0.f;
 
-  issue(0);
-  if (ntiles > 1) issue(1);
-  for (int it = 0; it < ntiles; ++it) {
-    if (it + 1 < ntiles) wait_vm_lgkm0<L::LOADS>();       // this tile's loads done, the next one's may fly
+  if (it0 < it1) issue(it0);
+  if (it0 + 1 < it1) issue(it0 + 1);
+  for (int it = it0; it < it1; ++it) {
+    if (it + 1 < it1) wait_vm_lgkm0<L::LOADS>();          // this tile's loads done, the next one's may fly
     else wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();                         // every wave's share of the tile has landed and
-    if (it + 2 < ntiles) issue(it + 2);                   // every wave is done with the stage reloaded here
+    if (it + 2 < it1) issue(it + 2);                      // every wave is done with the stage reloaded here
     const int64_t k0 = static_cast<int64_t>(it) * KT;
     if (k0 > wave_last) continue;                         // every key of the tile is past the wave's queries
-    tile<AD>(lds + (it % NSTAGE) * L::STAGE_U4, qf, o, m, lsum, k0, k0 + KT - 1 > wave_first, mypos, n, hh,
+    tile<AD>(lds + ((it - it0) % NSTAGE) * L::STAGE_U4, qf, o, m, lsum, k0, k0 + KT - 1 > wave_first, mypos, n, hh,
              a.scale_log2);
   }
   wait_vm_lgkm0<0>();
 
-  // normalise and write: lane holds O[query n][d = 32 b + 8 (j / 4) + 4 hh + j % 4]
+  // lane holds O[query n][d = 32 b + 8 (j / 4) + 4 hh + j % 4]
   const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+  if (ns > 1) {                                           // unnormalised partials for k_causal_combine
+    float* pb = part_block<AD>(a, blockIdx.x, hk, sp);
+    const int r = 32 * w + n;
+    float* orow = pb + r * AD + 4 * hh;
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4*>(orow + 32 * b + 8 * g) = make_float4(o[b][4 * g], o[b][4 * g + 1], o[b][4 * g + 2],
+                                                                        o[b][4 * g + 3]);
+    if (hh == 0) {
+      pb[QROWS * AD + r] = m;
+      pb[QROWS * AD + QROWS + r] = ltot;
+    }
+    return;
+  }
   if (!live) return;
   const float inv = 1.0f / ltot;
   uint16_t* dst = a.out + static_cast<int64_t>(jq) * a.ldo + head * AD + 4 * hh;
@@ -267,6 +299,46 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
       *reinterpret_cast<uint2*>(dst + 32 * b + 8 * g) =
           make_uint2(bf16_pair(o[b][4 * g] * inv, o[b][4 * g + 1] * inv),
                      bf16_pair(o[b][4 * g + 2] * inv, o[b][4 * g + 3] * inv));
+}
+
+// Merges the key-range splits of one (query block, K / V head): M = max_s m_s, L = sum_s l_s 2^(m_s - M),
+// O = sum_s O_s 2^(m_s - M) / L (base-2 maxima), splits in order; thread t takes query row t of the block.
+template <int AD>
+__global__ __launch_bounds__(QROWS) void k_causal_combine(CausalArgs a, int ns) {
+  const int r = threadIdx.x, w = r / 32, n = r % 32;
+  const int rep = a.hq / a.hkv, qp = QROWS / rep;
+  const int hk = blockIdx.y, j0 = blockIdx.x * qp;
+  const int hg = (32 * w) / qp, po0 = (32 * w) % qp;
+  const int jq = j0 + po0 + n;
+  if (jq >= a.nq) return;
+  const int64_t stride = QROWS * (AD + 2);
+  const float* base = a.part + (static_cast<int64_t>(blockIdx.x) * a.hkv + hk) * ns * stride;
+  float mx = -INFINITY;
+  for (int sp = 0; sp < ns; ++sp) mx = fmaxf(mx, base[sp * stride + QROWS * AD + r]);
+  float l = 0.f, acc[AD];
+#pragma unroll
+  for (int e = 0; e < AD; ++e) acc[e] = 0.f;
+  for (int sp = 0; sp < ns; ++sp) {
+    const float* pb = base + sp * stride;
+    const float ms = pb[QROWS * AD + r];
+    const float f = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
+    l += pb[QROWS * AD + QROWS + r] * f;
+    const float4* orow = reinterpret_cast<const float4*>(pb + r * AD);
+#pragma unroll
+    for (int e = 0; e < AD / 4; ++e) {
+      const float4 v = orow[e];
+      acc[4 * e] += v.x * f;
+      acc[4 * e + 1] += v.y * f;
+      acc[4 * e + 2] += v.z * f;
+      acc[4 * e + 3] += v.w * f;
+    }
+  }
+  const float inv = 1.0f / l;
+  uint16_t* dst = a.out + static_cast<int64_t>(jq) * a.ldo + (hk * rep + hg) * AD;
+#pragma unroll
+  for (int e = 0; e < AD; e += 4)
+    *reinterpret_cast<uint2*>(dst + e) = make_uint2(bf16_pair(acc[e] * inv, acc[e + 1] * inv),
+                                                    bf16_pair(acc[e + 2] * inv, acc[e + 3] * inv));
 }
 
 // V^T [hkv, AD, vt_ld] from the V cache [hkv, cap, AD]: keys 0 .. n - 1, zeros up to vt_ld. A block
@@ -299,28 +371,57 @@ __global__ __launch_bounds__(256) void k_vt(const uint16_t* __restrict__ v, int6
 
 int64_t vt_cols(int64_t n_keys) { return (n_keys + KT - 1) / KT * KT; }
 
+// Workspace: V^T (rounded up to 256 bytes), then the splits' partials when the key range is split.
+size_t vt_bytes(int hkv, int d, int64_t n_keys) {
+  return (static_cast<size_t>(hkv) * d * vt_cols(n_keys) * 2 + 255) / 256 * 256;
+}
+
+int64_t query_blocks(int64_t nq, int hq, int hkv) {
+  const int64_t qp = QROWS / (hq / hkv);
+  return (nq + qp - 1) / qp;
+}
+
+size_t part_bytes(int64_t nq, int hq, int hkv, int d, int splits) {
+  return splits > 1 ? static_cast<size_t>(query_blocks(nq, hq, hkv)) * hkv * splits * QROWS * (d + 2) * 4 : 0;
+}
+
+// Key-range splits: about 512 blocks in all (two per CU), at most 16, at most one per key tile.
+int causal_splits(int64_t nq, int hq, int hkv, int64_t n_keys) {
+  const int64_t blocks = std::max<int64_t>(query_blocks(nq, hq, hkv) * hkv, 1);
+  int64_t s = (512 + blocks - 1) / blocks;
+  s = std::min<int64_t>(std::min<int64_t>(s, 16), vt_cols(n_keys) / KT);
+  return static_cast<int>(std::max<int64_t>(s, 1));
+}
+
+bool causal_shape_ok(int hq, int hkv, int d) {
+  return (d == 64 || d == 128) && hq > 0 && hkv > 0 && hq % hkv == 0 &&
+         (hq / hkv == 1 || hq / hkv == 2 || hq / hkv == 4 || hq / hkv == 8);
+}
+
 }  // namespace
 }  // namespace rf
 
 using namespace rf;
 
-extern "C" int rf_attend_causal_workspace_bytes(int hkv, int d, int64_t n_keys, size_t* bytes) {
-  if (!bytes || hkv <= 0 || (d != 64 && d != 128) || n_keys < 0)
-    return fail(RF_EINVAL_ARG, "rf_attend_causal_workspace_bytes: arguments");
-  *bytes = static_cast<size_t>(hkv) * d * vt_cols(n_keys) * 2;
+extern "C" int rf_attend_causal_workspace_bytes(int64_t nq, int hq, int hkv, int d, int64_t n_keys, size_t* bytes) {
+  if (!bytes || nq < 0 || n_keys < 0) return fail(RF_EINVAL_ARG, "rf_attend_causal_workspace_bytes: arguments");
+  if (!causal_shape_ok(hq, hkv, d))
+    return fail(RF_EUNSUPPORTED, "rf_attend_causal_workspace_bytes: head_dim %d, %d query heads over %d K / V heads "
+                "(d 64 or 128, a group of 1, 2, 4 or 8)", d, hq, hkv);
+  *bytes = vt_bytes(hkv, d, n_keys) + part_bytes(nq, hq, hkv, d, causal_splits(nq, hq, hkv, n_keys));
   return RF_OK;
 }
 
-extern "C" int rf_attend_causal(const uint16_t* q, int64_t ldq, int64_t nq, int64_t slot0, int hq, int d,
-                                const uint16_t* kbuf, const uint16_t* vbuf, int hkv, int64_t head_stride,
+extern "C" int rf_attend_causal(const uint16_t* q, int64_t ldq, int64_t nq, const int64_t* qpos, int64_t slot0, int hq,
+                                int d, const uint16_t* kbuf, const uint16_t* vbuf, int hkv, int64_t head_stride,
                                 int64_t row_stride, int64_t n_keys, float scale, uint16_t* out, int64_t ldo,
                                 void* workspace, size_t ws_bytes, hipStream_t stream) {
   if (!q || !kbuf || !vbuf || !out || !workspace) return fail(RF_EINVAL_ARG, "rf_attend_causal: null pointer");
   if (d != 64 && d != 128) return fail(RF_EUNSUPPORTED, "rf_attend_causal: head_dim %d (the kernel takes 64, 128)", d);
-  if (hq <= 0 || hkv <= 0 || hq % hkv || (hq / hkv != 1 && hq / hkv != 2 && hq / hkv != 4 && hq / hkv != 8))
+  if (!causal_shape_ok(hq, hkv, d))
     return fail(RF_EUNSUPPORTED, "rf_attend_causal: %d query heads over %d K / V heads (group of 1, 2, 4 or 8)", hq,
                 hkv);
-  if (nq < 0 || nq > (1 << 30) || slot0 < 0 || slot0 + nq > n_keys)
+  if (nq < 0 || nq > (1 << 30) || n_keys <= 0 || (!qpos && (slot0 < 0 || slot0 + nq > n_keys)))
     return fail(RF_EINVAL_SHAPE, "rf_attend_causal: queries at slots [%lld, %lld) past the %lld keys", (long long)slot0,
                 (long long)(slot0 + nq), (long long)n_keys);
   if (ldq < static_cast<int64_t>(hq) * d || ldo < static_cast<int64_t>(hq) * d || ldq % 8 || ldo % 4 ||
@@ -332,21 +433,31 @@ extern "C" int rf_attend_causal(const uint16_t* q, int64_t ldq, int64_t nq, int6
       (reinterpret_cast<uintptr_t>(out) & 7u))
     return fail(RF_EINVAL_SHAPE, "rf_attend_causal: alignment");
   const int64_t vt_ld = vt_cols(n_keys);
-  if (ws_bytes < static_cast<size_t>(hkv) * d * vt_ld * 2)
-    return fail(RF_EINVAL_SHAPE, "rf_attend_causal: workspace %zu bytes < %lld", ws_bytes,
-                (long long)(static_cast<int64_t>(hkv) * d * vt_ld * 2));
+  const size_t vtb = vt_bytes(hkv, d, n_keys);
+  if (ws_bytes < vtb)
+    return fail(RF_EINVAL_SHAPE, "rf_attend_causal: workspace %zu bytes < %zu (V transposed)", ws_bytes, vtb);
   if (nq == 0) return RF_OK;
+  int ns = causal_splits(nq, hq, hkv, n_keys);
+  while (ns > 1 && ws_bytes < vtb + part_bytes(nq, hq, hkv, d, ns)) --ns;     // what the workspace holds
   uint16_t* vt = static_cast<uint16_t*>(workspace);
   const dim3 gt(static_cast<unsigned>(vt_ld / KT), static_cast<unsigned>(hkv));
   if (d == 128) hipLaunchKernelGGL(k_vt<128>, gt, dim3(256), 0, stream, vbuf, head_stride, row_stride, n_keys, vt, vt_ld);
   else hipLaunchKernelGGL(k_vt<64>, gt, dim3(256), 0, stream, vbuf, head_stride, row_stride, n_keys, vt, vt_ld);
-  const int st = check_launch("rf_attend_causal (V transpose)");
+  int st = check_launch("rf_attend_causal (V transpose)");
   if (st != RF_OK) return st;
-  CausalArgs a{q, ldq, static_cast<int>(nq), slot0, kbuf, head_stride, row_stride, n_keys, vt, vt_ld, hq, hkv,
-               scale * 1.4426950408889634f, out, ldo};
-  const int qp = QROWS / (hq / hkv);
-  const dim3 grid(static_cast<unsigned>((nq + qp - 1) / qp), static_cast<unsigned>(hkv));
+  CausalArgs a{q, ldq, static_cast<int>(nq), qpos, slot0, kbuf, head_stride, row_stride, n_keys, vt, vt_ld, hq, hkv,
+               scale * 1.4426950408889634f, out, ldo,
+               reinterpret_cast<float*>(static_cast<char*>(workspace) + vtb)};
+  const dim3 grid(static_cast<unsigned>(query_blocks(nq, hq, hkv)), static_cast<unsigned>(hkv),
+                  static_cast<unsigned>(ns));
   if (d == 128) hipLaunchKernelGGL(k_attend_causal<128>, grid, dim3(NTHR), 0, stream, a);
   else hipLaunchKernelGGL(k_attend_causal<64>, grid, dim3(NTHR), 0, stream, a);
+  if (ns > 1) {
+    st = check_launch("rf_attend_causal");
+    if (st != RF_OK) return st;
+    const dim3 g2(grid.x, grid.y);
+    if (d == 128) hipLaunchKernelGGL(k_causal_combine<128>, g2, dim3(QROWS), 0, stream, a, ns);
+    else hipLaunchKernelGGL(k_causal_combine<64>, g2, dim3(QROWS), 0, stream, a, ns);
+  }
   return check_launch("rf_attend_causal");
 }

@@ -18,6 +18,7 @@
 // epilogue rounds them to bf16 and writes 8-byte runs into a row-major LDS image of the 256 x 256
 // tile, which a row pass then reads as 16-byte chunks (32 threads per 256-column row) to compute
 // row statistics, apply k_norm / RoPE and issue coalesced 128-bit stores.
+#include <algorithm>
 #include <type_traits>
 
 #include "rf_common.h"
@@ -261,6 +262,58 @@ __device__ __forceinline__ float row_scale(const float* __restrict__ ssq, int np
   return 1.0f / sqrtf(s / width + eps);
 }
 
+// Split K. With fewer output tiles than CUs, the K range of each tile is cut into `splits` ranges,
+// each one block of k_gemm_partial, which stores its fp32 sums as row-major planes
+// part[split][row][column] (rows < M only). The reduce kernels (k_*_reduce) then run the tile's
+// epilogue as a row pass over many small blocks of 8 rows x 256 columns: each thread adds the splits of
+// its 8 columns in split order (the same bits every run) and finishes them as the unsplit epilogue
+// does. Every epilogue here is row-local, so this needs no tile-wide step.
+__device__ __forceinline__ void store_partial(float* __restrict__ part, int64_t ldp, int M, int m0, int n0,
+                                              const f32x16 (&acc)[4][4]) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, wm = w >> 1, wn = w & 1, lr = lane & 31, lk = lane >> 5;
+#pragma unroll
+  for (int mt = 0; mt < 4; ++mt) {
+    const int gm = m0 + wm * 128 + mt * 32 + lr;
+    if (gm >= M) continue;
+    float* row = part + static_cast<int64_t>(gm) * ldp + n0 + wn * 128 + 4 * lk;
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4*>(row + nt * 32 + 8 * g) =
+            make_float4(acc[nt][mt][4 * g], acc[nt][mt][4 * g + 1], acc[nt][mt][4 * g + 2], acc[nt][mt][4 * g + 3]);
+  }
+}
+
+// Split sp of every tile: X[rows of the tile, kbeg .. kbeg + klen) . W[columns, same K range]^T into
+// part + sp * M * N.
+__global__ __launch_bounds__(NTHR) void k_gemm_partial(const uint16_t* __restrict__ X, int64_t ldx,
+                                                       const uint16_t* __restrict__ W, int64_t ldw, int M, int N,
+                                                       int K, int kper, float* __restrict__ part) {
+  __shared__ uint4 lds[LDS_U4];
+  const int tiles_n = N / BN, tiles = ((M + BM - 1) / BM) * tiles_n;
+  const int tile = blockIdx.x % tiles, sp = blockIdx.x / tiles;
+  const int tm = tile / tiles_n, tn = tile - tm * tiles_n;
+  const int kbeg = sp * kper, klen = min(K - kbeg, kper);
+  f32x16 acc[4][4];
+  mainloop(X + kbeg, ldx, W + kbeg, ldw, M, klen, tm * BM, tn * BN, lds, acc);
+  store_partial(part + static_cast<int64_t>(sp) * M * N, N, M, tm * BM, tn * BN, acc);
+}
+
+// The split sums of 8 consecutive columns col .. col + 7 of row gm: 8 fp32 values, splits added in order.
+__device__ __forceinline__ void split_sums(const float* __restrict__ part, int splits, int64_t plane, int64_t off,
+                                           float (&v)[8]) {
+  const float4* p = reinterpret_cast<const float4*>(part + off);
+  float4 a = p[0], b = p[1];
+  for (int sp = 1; sp < splits; ++sp) {
+    const float4* q = reinterpret_cast<const float4*>(part + sp * plane + off);
+    const float4 c = q[0], d = q[1];
+    a.x += c.x; a.y += c.y; a.z += c.z; a.w += c.w;
+    b.x += d.x; b.y += d.y; b.z += d.z; b.w += d.w;
+  }
+  v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w; v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
 __global__ __launch_bounds__(NTHR) void k_map_apply(const uint16_t* __restrict__ B, int64_t ldb,
                                                     const uint16_t* __restrict__ W,
                                                     const uint16_t* __restrict__ bias,
@@ -345,6 +398,105 @@ __device__ __forceinline__ void knorm_chunk(float (&f)[8], float rinv, const uin
   }
 }
 
+// The K / V (or query) epilogue's per-lane constants for the 16-byte chunk ch (columns n0 + 8 ch ..
+// n0 + 8 ch + 7) of a 256-column tile column: K or V, head and offset, the k_norm gains of the chunk
+// and of its RoPE partner, and the RoPE table offsets (the same for every row).
+struct KvLane {
+  bool is_k, norm, rope;
+  int j0, pj0, fi0, half, group;
+  uint16_t* dst0;
+  uint4 kn, kn_p;
+  __device__ KvLane(const KvArgs& a, int n0, int ch) {
+    const int d = a.d, kw = a.hkv * a.d;
+    half = a.rot >> 1;
+    group = d >> 3;                                 // chunks per head: a power of two <= 32
+    const int col = n0 + ch * 8;
+    is_k = col < kw;
+    const int cc = is_k ? col : col - kw;
+    const int head = cc / d;
+    j0 = cc - head * d;
+    dst0 = (is_k ? a.kbuf : a.vbuf) + head * a.head_stride + j0;
+    norm = is_k && a.knorm != nullptr;
+    rope = is_k && j0 < a.rot;
+    pj0 = j0 < half ? j0 + half : j0 - half;
+    fi0 = j0 < half ? j0 : j0 - half;                // table index of the chunk's first element
+    kn = make_uint4(0u, 0u, 0u, 0u);
+    kn_p = kn;
+    if (norm) {
+      kn = *reinterpret_cast<const uint4*>(a.knorm + j0);
+      if (rope && half >= 8) kn_p = *reinterpret_cast<const uint4*>(a.knorm + pj0);
+    }
+  }
+};
+
+// One row's chunk of the K / V epilogue: get(c) returns the row's normed bf16 chunk c (of the tile
+// column); per-head sum of squares for k_norm over the head's chunks (lanes of one 32-lane row group,
+// all of which call this, ok or not), then k_norm, RoPE at the row's table entry and a streaming store
+// into slot slot0 + gm.
+template <class Get>
+__device__ __forceinline__ void kv_chunk_row(const KvArgs& a, const KvLane& L, Get get, int ch, int64_t gm, bool ok) {
+  const uint4 v = get(ch);
+  float ss = 0.f;
+  if (a.knorm) {                                   // per-head sum of squares; uniform branch
+    ss = chunk_ssq(v);
+    for (int o = 1; o < L.group; o <<= 1) ss += __shfl_xor(ss, o, 64);
+  }
+  if (!ok) return;
+  const int j0 = L.j0, half = L.half, rot = a.rot;
+  uint16_t* dst = L.dst0 + (a.slot0 + gm) * a.row_stride;
+  if (!L.is_k || (!L.norm && !L.rope)) {
+    st_stream16(dst, v);
+    return;
+  }
+  float f[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = bf2f(lane_of(v, e));
+  const float rinv = 1.0f / sqrtf(ss / static_cast<float>(a.d) + a.eps);
+  if (L.norm) knorm_chunk(f, rinv, L.kn, a.knorm_kind);
+  uint4 o;
+  if (!L.rope) {
+    o = make_uint4(bf16_pair(f[0], f[1]), bf16_pair(f[2], f[3]), bf16_pair(f[4], f[5]), bf16_pair(f[6], f[7]));
+  } else {
+    float pf[8];                                  // rotate_half partner values of this chunk
+    if (half >= 8) {
+      const uint4 pv = get(ch + (L.pj0 - j0) / 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pf[e] = bf2f(lane_of(pv, e));
+      if (L.norm) knorm_chunk(pf, rinv, L.kn_p, a.knorm_kind);
+    } else {                                      // half == 4: the partner is in the same chunk
+#pragma unroll
+      for (int e = 0; e < 8; ++e) pf[e] = f[e ^ 4];
+    }
+    const uint16_t* cs = a.cs + (a.pos ? a.pos[gm] : gm) * rot;
+    float c[8], sn[8];
+    if (half >= 8) {                              // 8 consecutive table entries of each half
+      const uint4 cv = *reinterpret_cast<const uint4*>(cs + L.fi0);
+      const uint4 sv = *reinterpret_cast<const uint4*>(cs + half + L.fi0);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        c[e] = bf2f(lane_of(cv, e));
+        sn[e] = bf2f(lane_of(sv, e));
+      }
+    } else {                                      // rot == 8: entries 0..3 serve both halves of the chunk
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        c[e] = bf2f(cs[e & 3]);
+        sn[e] = bf2f(cs[4 + (e & 3)]);
+      }
+    }
+    // x cos + rotate_half(x) sin with each product rounded to bf16, then the sum (ops.py:66-77)
+    float y[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float rh = j0 + e < half ? -pf[e] : pf[e];
+      const uint32_t pr = bf16_pair(f[e] * c[e], rh * sn[e]);
+      y[e] = bf_lo(pr) + bf_hi(pr);
+    }
+    o = make_uint4(bf16_pair(y[0], y[1]), bf16_pair(y[2], y[3]), bf16_pair(y[4], y[5]), bf16_pair(y[6], y[7]));
+  }
+  st_stream16(dst, o);
+}
+
 __global__ __launch_bounds__(NTHR) void k_norm_kv(const uint16_t* __restrict__ Xin, int64_t ldx,
                                                   const uint16_t* __restrict__ W, int M, int N, int K,
                                                   KvArgs a) {
@@ -369,85 +521,11 @@ __global__ __launch_bounds__(NTHR) void k_norm_kv(const uint16_t* __restrict__ X
   __syncthreads();
 
   const int t = threadIdx.x, ch = t & 31;
-  const int d = a.d, kw = a.hkv * a.d, rot = a.rot, half = a.rot >> 1;
-  const int group = d >> 3;                       // chunks per head: a power of two <= 32
-  const int col = n0 + ch * 8;
-  const bool is_k = col < kw;
-  const int cc = is_k ? col : col - kw;
-  const int head = cc / d, j0 = cc - head * d;
-  uint16_t* const dst0 = (is_k ? a.kbuf : a.vbuf) + head * a.head_stride + j0;
-  // this lane's k_norm gains, its RoPE partner chunk and table offsets (the same for every row)
-  const bool norm = is_k && a.knorm != nullptr;
-  const bool rope = is_k && j0 < rot;
-  const int pj0 = j0 < half ? j0 + half : j0 - half;
-  const int fi0 = j0 < half ? j0 : j0 - half;       // table index of the chunk's first element
-  uint4 kn = make_uint4(0u, 0u, 0u, 0u), kn_p = kn;
-  if (norm) {
-    kn = *reinterpret_cast<const uint4*>(a.knorm + j0);
-    if (rope && half >= 8) kn_p = *reinterpret_cast<const uint4*>(a.knorm + pj0);
-  }
+  const KvLane L(a, n0, ch);
   for (int it = 0; it < BM / 8; ++it) {
     const int row = it * 8 + (t >> 5);
     const int gm = m0 + row;
-    const uint4 v = image_chunk(lds, row, ch);
-    float ss = 0.f;
-    if (a.knorm) {                                   // per-head sum of squares; uniform branch
-      ss = chunk_ssq(v);
-      for (int o = 1; o < group; o <<= 1) ss += __shfl_xor(ss, o, 64);
-    }
-    if (gm >= M) continue;
-    uint16_t* dst = dst0 + (a.slot0 + gm) * a.row_stride;
-    if (!is_k || (!norm && !rope)) {
-      st_stream16(dst, v);
-      continue;
-    }
-    float f[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) f[e] = bf2f(lane_of(v, e));
-    const float rinv = 1.0f / sqrtf(ss / static_cast<float>(d) + a.eps);
-    if (norm) knorm_chunk(f, rinv, kn, a.knorm_kind);
-    uint4 o;
-    if (!rope) {
-      o = make_uint4(bf16_pair(f[0], f[1]), bf16_pair(f[2], f[3]), bf16_pair(f[4], f[5]), bf16_pair(f[6], f[7]));
-    } else {
-      float pf[8];                                // rotate_half partner values of this chunk
-      if (half >= 8) {
-        const uint4 pv = image_chunk(lds, row, ch + (pj0 - j0) / 8);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pf[e] = bf2f(lane_of(pv, e));
-        if (norm) knorm_chunk(pf, rinv, kn_p, a.knorm_kind);
-      } else {                                    // half == 4: the partner is in the same chunk
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pf[e] = f[e ^ 4];
-      }
-      const uint16_t* cs = a.cs + (a.pos ? a.pos[gm] : static_cast<int64_t>(gm)) * rot;
-      float c[8], sn[8];
-      if (half >= 8) {                            // 8 consecutive table entries of each half
-        const uint4 cv = *reinterpret_cast<const uint4*>(cs + fi0);
-        const uint4 sv = *reinterpret_cast<const uint4*>(cs + half + fi0);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          c[e] = bf2f(lane_of(cv, e));
-          sn[e] = bf2f(lane_of(sv, e));
-        }
-      } else {                                    // rot == 8: entries 0..3 serve both halves of the chunk
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          c[e] = bf2f(cs[e & 3]);
-          sn[e] = bf2f(cs[4 + (e & 3)]);
-        }
-      }
-      // x cos + rotate_half(x) sin with each product rounded to bf16, then the sum (ops.py:66-77)
-      float y[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float rh = j0 + e < half ? -pf[e] : pf[e];
-        const uint32_t pr = bf16_pair(f[e] * c[e], rh * sn[e]);
-        y[e] = bf_lo(pr) + bf_hi(pr);
-      }
-      o = make_uint4(bf16_pair(y[0], y[1]), bf16_pair(y[2], y[3]), bf16_pair(y[4], y[5]), bf16_pair(y[6], y[7]));
-    }
-    st_stream16(dst, o);
+    kv_chunk_row(a, L, [&](int c) { return image_chunk(lds, row, c); }, ch, gm, gm < M);
   }
 }
 
@@ -483,6 +561,85 @@ __global__ __launch_bounds__(NTHR) void k_norm_linear(const uint16_t* __restrict
     if (gm < M)
       *reinterpret_cast<uint4*>(out + static_cast<int64_t>(gm) * ldo + n0 + ch * 8) = image_chunk(lds, row, ch);
   }
+}
+
+// ---- split-K epilogues: a block takes 8 rows x one 256-column tile column (grid: row groups x
+// tile columns); thread t owns row t / 32 of the group and its 16-byte chunk t % 32.
+
+constexpr int RED_ROWS = 8;
+
+// The unsplit map epilogue on split sums: x = bf16(sum + bias) and the rows' sum-of-squares partial of
+// this 256-column group, formed in the order every producer uses (one wave per row).
+__global__ __launch_bounds__(256) void k_map_apply_reduce(const float* __restrict__ part, int splits,
+                                                          const uint16_t* __restrict__ bias, uint16_t* __restrict__ X,
+                                                          int64_t ldx, float* __restrict__ ssq, int M, int N) {
+  __shared__ uint4 img[RED_ROWS * 32];
+  const int t = threadIdx.x, r = t >> 5, ch = t & 31, tn = blockIdx.y, n0 = tn * BN;
+  const int m = blockIdx.x * RED_ROWS + r;
+  uint4 o = make_uint4(0u, 0u, 0u, 0u);
+  if (m < M) {
+    float v[8];
+    split_sums(part, splits, static_cast<int64_t>(M) * N, static_cast<int64_t>(m) * N + n0 + ch * 8, v);
+    if (bias) {
+      const uint4 b = *reinterpret_cast<const uint4*>(bias + n0 + ch * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] += bf2f(lane_of(b, e));
+    }
+    o = make_uint4(bf16_pair(v[0], v[1]), bf16_pair(v[2], v[3]), bf16_pair(v[4], v[5]), bf16_pair(v[6], v[7]));
+    *reinterpret_cast<uint4*>(X + static_cast<int64_t>(m) * ldx + n0 + ch * 8) = o;
+  }
+  img[r * 32 + (ch ^ r)] = o;
+  __syncthreads();
+  const int lane = t & 63, w = t >> 6;
+  for (int rr = 2 * w; rr < 2 * w + 2; ++rr) {
+    const int mm = blockIdx.x * RED_ROWS + rr;
+    if (mm >= M) break;                             // wave-uniform
+    row_partials([&](int64_t c) {
+      const uint4 q = img[rr * 32 + ((static_cast<int>(c) >> 3) ^ rr)];
+      return (c & 4) ? make_uint2(q.z, q.w) : make_uint2(q.x, q.y);
+    }, ssq + static_cast<int64_t>(mm) * (N / SSQ_COLS) + tn, 1, lane);
+  }
+}
+
+// The unsplit norm + linear epilogue on split sums: out = bf16(sum * r_row).
+__global__ __launch_bounds__(256) void k_norm_linear_reduce(const float* __restrict__ part, int splits,
+                                                            const float* __restrict__ ssq, int K, float eps,
+                                                            uint16_t* __restrict__ out, int64_t ldo, int M, int N) {
+  const int t = threadIdx.x, r = t >> 5, ch = t & 31, n0 = blockIdx.y * BN;
+  const int m = blockIdx.x * RED_ROWS + r;
+  if (m >= M) return;
+  const int nparts = K / SSQ_COLS;
+  float s2 = 0.f;
+  for (int i = 0; i < nparts; ++i) s2 += ssq[static_cast<int64_t>(m) * nparts + i];
+  const float rs = 1.0f / sqrtf(s2 / static_cast<float>(K) + eps);
+  float v[8];
+  split_sums(part, splits, static_cast<int64_t>(M) * N, static_cast<int64_t>(m) * N + n0 + ch * 8, v);
+  *reinterpret_cast<uint4*>(out + static_cast<int64_t>(m) * ldo + n0 + ch * 8) =
+      make_uint4(bf16_pair(v[0] * rs, v[1] * rs), bf16_pair(v[2] * rs, v[3] * rs), bf16_pair(v[4] * rs, v[5] * rs),
+                 bf16_pair(v[6] * rs, v[7] * rs));
+}
+
+// The unsplit K / V (or query) epilogue on split sums: the normed chunk bf16(sum * r_row), then k_norm,
+// RoPE and the cache write of kv_chunk_row.
+__global__ __launch_bounds__(256) void k_norm_kv_reduce(const float* __restrict__ part, int splits, int M, int N,
+                                                        KvArgs a) {
+  __shared__ uint4 img[RED_ROWS * 32];
+  const int t = threadIdx.x, r = t >> 5, ch = t & 31, n0 = blockIdx.y * BN;
+  const int m = blockIdx.x * RED_ROWS + r;
+  uint4 o = make_uint4(0u, 0u, 0u, 0u);
+  if (m < M) {
+    float s2 = 0.f;
+    for (int i = 0; i < a.nparts; ++i) s2 += a.ssq[static_cast<int64_t>(m) * a.nparts + i];
+    const float rs = 1.0f / sqrtf(s2 / a.h + a.eps);
+    float v[8];
+    split_sums(part, splits, static_cast<int64_t>(M) * N, static_cast<int64_t>(m) * N + n0 + ch * 8, v);
+    o = make_uint4(bf16_pair(v[0] * rs, v[1] * rs), bf16_pair(v[2] * rs, v[3] * rs), bf16_pair(v[4] * rs, v[5] * rs),
+                   bf16_pair(v[6] * rs, v[7] * rs));
+  }
+  img[r * 32 + (ch ^ r)] = o;
+  __syncthreads();
+  const KvLane L(a, n0, ch);
+  kv_chunk_row(a, L, [&](int c) { return image_chunk(img, r, c); }, ch, m, m < M);
 }
 
 // C[m, n] += sum_k A[m, k] B[n, k] in fp32 for this launch, added into the fp64 accumulator C. Each
@@ -523,14 +680,51 @@ __global__ __launch_bounds__(NTHR) void k_gram(const uint16_t* __restrict__ A, i
 
 int grid_of(int64_t M, int64_t N) { return static_cast<int>(((M + BM - 1) / BM) * (N / BN)); }
 
+// K splits for an M x N x K product: enough blocks to give every CU one (256), at least 512 of K per
+// split, at most 16 splits; 1 when the tiles alone fill the GPU.
+int split_count(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles = std::max<int64_t>(grid_of(M, N), 1);
+  int64_t s = std::min<int64_t>(std::min<int64_t>(256 / tiles, K / 512), 16);
+  return static_cast<int>(std::max<int64_t>(s, 1));
+}
+
+size_t split_bytes(int64_t M, int64_t N, int64_t K) {
+  const int s = split_count(M, N, K);
+  return s > 1 ? static_cast<size_t>(s) * M * N * 4 : 0;
+}
+
+// Runs the split partials of an M x N x K product into ws when a split pays and ws holds them; returns
+// the split count the reduce kernel must add (1: no split, run the fused kernel).
+int launch_partials(const uint16_t* X, int64_t ldx, const uint16_t* W, int64_t ldw, int64_t M, int64_t N, int64_t K,
+                    void* ws, size_t ws_bytes, hipStream_t stream) {
+  const int s = split_count(M, N, K);
+  if (s <= 1 || !ws || ws_bytes < split_bytes(M, N, K)) return 1;
+  const int kper = static_cast<int>((K / s + BK - 1) / BK * BK);
+  hipLaunchKernelGGL(k_gemm_partial, dim3(grid_of(M, N) * s), dim3(NTHR), 0, stream, X, ldx, W, ldw,
+                     static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), kper, static_cast<float*>(ws));
+  return s;
+}
+
+dim3 reduce_grid(int64_t M, int64_t N) {
+  return dim3(static_cast<unsigned>((M + RED_ROWS - 1) / RED_ROWS), static_cast<unsigned>(N / BN));
+}
+
 }  // namespace
 }  // namespace rf
 
 using namespace rf;
 
+extern "C" int rf_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, size_t* bytes) {
+  if (!bytes || M < 0 || N <= 0 || N % BN || K <= 0 || K % BK)
+    return fail(RF_EINVAL_ARG, "rf_gemm_workspace_bytes: M %lld, N %lld (multiple of 256), K %lld (multiple of 32)",
+                (long long)M, (long long)N, (long long)K);
+  *bytes = M ? split_bytes(M, N, K) : 0;
+  return RF_OK;
+}
+
 extern "C" int rf_map_apply(const uint16_t* b, int64_t ldb, const uint16_t* w, const uint16_t* c, uint16_t* x,
-                            int64_t ldx, float* ssq, int64_t P, int64_t h_in, int64_t h_out,
-                            hipStream_t stream) {
+                            int64_t ldx, float* ssq, int64_t P, int64_t h_in, int64_t h_out, void* workspace,
+                            size_t ws_bytes, hipStream_t stream) {
   if (!b || !w || !x || !ssq) return fail(RF_EINVAL_ARG, "rf_map_apply: null pointer");
   if (P < 0 || P > (1ll << 30)) return fail(RF_EINVAL_SHAPE, "rf_map_apply: P = %lld out of range", (long long)P);
   if (h_in <= 0 || h_in % BK || h_out <= 0 || h_out % BN)
@@ -540,9 +734,16 @@ extern "C" int rf_map_apply(const uint16_t* b, int64_t ldb, const uint16_t* w, c
     return fail(RF_EINVAL_SHAPE, "rf_map_apply: row strides ldb %lld / ldx %lld", (long long)ldb, (long long)ldx);
   if (!aligned16(b) || !aligned16(w) || !aligned16(x) || (c && !aligned16(c)))
     return fail(RF_EINVAL_SHAPE, "rf_map_apply: pointers must be 16-byte aligned");
+  if (workspace && !aligned16(workspace)) return fail(RF_EINVAL_SHAPE, "rf_map_apply: workspace alignment");
   if (P == 0) return RF_OK;
-  hipLaunchKernelGGL(k_map_apply, dim3(grid_of(P, h_out)), dim3(NTHR), 0, stream, b, ldb, w, c, x, ldx, ssq,
-                     static_cast<int>(P), static_cast<int>(h_out), static_cast<int>(h_in));
+  const int sp = launch_partials(b, ldb, w, h_in, P, h_out, h_in, workspace, ws_bytes, stream);
+  if (sp > 1)
+    hipLaunchKernelGGL(k_map_apply_reduce, reduce_grid(P, h_out), dim3(256), 0, stream,
+                       static_cast<const float*>(workspace), sp, c, x, ldx, ssq, static_cast<int>(P),
+                       static_cast<int>(h_out));
+  else
+    hipLaunchKernelGGL(k_map_apply, dim3(grid_of(P, h_out)), dim3(NTHR), 0, stream, b, ldb, w, c, x, ldx, ssq,
+                       static_cast<int>(P), static_cast<int>(h_out), static_cast<int>(h_in));
   return check_launch("rf_map_apply");
 }
 
@@ -550,7 +751,7 @@ extern "C" int rf_norm_kv_write(const uint16_t* x, int64_t ldx, const float* ssq
                                 const uint16_t* wkv, int hkv, int d, const uint16_t* knorm, int knorm_kind,
                                 const uint16_t* cs, int rot, uint16_t* kbuf, uint16_t* vbuf,
                                 int64_t head_stride, int64_t row_stride, int64_t slot_begin, int64_t cap,
-                                hipStream_t stream) {
+                                void* workspace, size_t ws_bytes, hipStream_t stream) {
   if (!x || !ssq || !wkv || !cs || !kbuf || !vbuf) return fail(RF_EINVAL_ARG, "rf_norm_kv_write: null pointer");
   if (P < 0 || P > (1ll << 30)) return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write: P = %lld out of range", (long long)P);
   if (H <= 0 || H % BK || H % SSQ_COLS)
@@ -576,14 +777,21 @@ extern "C" int rf_norm_kv_write(const uint16_t* x, int64_t ldx, const float* ssq
   KvArgs a{ssq, static_cast<int>(H / SSQ_COLS), static_cast<float>(H), eps, hkv, d, knorm, knorm_kind, cs, rot,
            kbuf, vbuf, head_stride, row_stride, slot_begin, nullptr};
   const int64_t N = 2ll * hkv * d;
-  hipLaunchKernelGGL(k_norm_kv, dim3(grid_of(P, N)), dim3(NTHR), 0, stream, x, ldx, wkv, static_cast<int>(P),
-                     static_cast<int>(N), static_cast<int>(H), a);
+  if (workspace && !aligned16(workspace)) return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write: workspace alignment");
+  const int sp = launch_partials(x, ldx, wkv, H, P, N, H, workspace, ws_bytes, stream);
+  if (sp > 1)
+    hipLaunchKernelGGL(k_norm_kv_reduce, reduce_grid(P, N), dim3(256), 0, stream, static_cast<const float*>(workspace),
+                       sp, static_cast<int>(P), static_cast<int>(N), a);
+  else
+    hipLaunchKernelGGL(k_norm_kv, dim3(grid_of(P, N)), dim3(NTHR), 0, stream, x, ldx, wkv, static_cast<int>(P),
+                       static_cast<int>(N), static_cast<int>(H), a);
   return check_launch("rf_norm_kv_write");
 }
 
 extern "C" int rf_norm_q(const uint16_t* x, int64_t ldx, const float* ssq, int64_t rows, int64_t H, float eps,
                          const uint16_t* wq, int hq, int d, const uint16_t* qnorm, int qnorm_kind, const uint16_t* cs,
-                         int rot, const int64_t* pos, uint16_t* q, int64_t ldq, hipStream_t stream) {
+                         int rot, const int64_t* pos, uint16_t* q, int64_t ldq, void* workspace, size_t ws_bytes,
+                         hipStream_t stream) {
   if (!x || !ssq || !wq || !cs || !pos || !q) return fail(RF_EINVAL_ARG, "rf_norm_q: null pointer");
   if (rows < 0 || rows > (1ll << 30)) return fail(RF_EINVAL_SHAPE, "rf_norm_q: rows = %lld out of range", (long long)rows);
   if (H <= 0 || H % BK || H % SSQ_COLS) return fail(RF_EINVAL_SHAPE, "rf_norm_q: H = %lld must be a multiple of 256",
@@ -604,8 +812,14 @@ extern "C" int rf_norm_q(const uint16_t* x, int64_t ldx, const float* ssq, int64
   KvArgs a{ssq, static_cast<int>(H / SSQ_COLS), static_cast<float>(H), eps, hq, d, qnorm, qnorm_kind, cs, rot,
            q, q, static_cast<int64_t>(d), ldq, 0, pos};
   const int64_t N = static_cast<int64_t>(hq) * d;
-  hipLaunchKernelGGL(k_norm_kv, dim3(grid_of(rows, N)), dim3(NTHR), 0, stream, x, ldx, wq, static_cast<int>(rows),
-                     static_cast<int>(N), static_cast<int>(H), a);
+  if (workspace && !aligned16(workspace)) return fail(RF_EINVAL_SHAPE, "rf_norm_q: workspace alignment");
+  const int sp = launch_partials(x, ldx, wq, H, rows, N, H, workspace, ws_bytes, stream);
+  if (sp > 1)
+    hipLaunchKernelGGL(k_norm_kv_reduce, reduce_grid(rows, N), dim3(256), 0, stream,
+                       static_cast<const float*>(workspace), sp, static_cast<int>(rows), static_cast<int>(N), a);
+  else
+    hipLaunchKernelGGL(k_norm_kv, dim3(grid_of(rows, N)), dim3(NTHR), 0, stream, x, ldx, wq, static_cast<int>(rows),
+                       static_cast<int>(N), static_cast<int>(H), a);
   return check_launch("rf_norm_q");
 }
 
@@ -627,7 +841,8 @@ extern "C" int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t
 }
 
 extern "C" int rf_norm_linear(const uint16_t* x, int64_t ldx, const float* ssq, int64_t P, int64_t H, float eps,
-                              const uint16_t* w, int64_t N, uint16_t* out, int64_t ldo, hipStream_t stream) {
+                              const uint16_t* w, int64_t N, uint16_t* out, int64_t ldo, void* workspace,
+                              size_t ws_bytes, hipStream_t stream) {
   if (!x || !ssq || !w || !out) return fail(RF_EINVAL_ARG, "rf_norm_linear: null pointer");
   if (P < 0 || P > (1ll << 30) || H <= 0 || H % SSQ_COLS || N <= 0 || N % BN)
     return fail(RF_EINVAL_SHAPE, "rf_norm_linear: P %lld, H %lld (multiple of 256), N %lld (multiple of 256)",
@@ -636,8 +851,15 @@ extern "C" int rf_norm_linear(const uint16_t* x, int64_t ldx, const float* ssq, 
     return fail(RF_EINVAL_SHAPE, "rf_norm_linear: strides ldx %lld, ldo %lld", (long long)ldx, (long long)ldo);
   if (!aligned16(x) || !aligned16(w) || !aligned16(out)) return fail(RF_EINVAL_SHAPE, "rf_norm_linear: alignment");
   if (!(eps >= 0.f)) return fail(RF_EINVAL_ARG, "rf_norm_linear: eps");
+  if (workspace && !aligned16(workspace)) return fail(RF_EINVAL_SHAPE, "rf_norm_linear: workspace alignment");
   if (P == 0) return RF_OK;
-  hipLaunchKernelGGL(k_norm_linear, dim3(grid_of(P, N)), dim3(NTHR), 0, stream, x, ldx, w, static_cast<int>(P),
-                     static_cast<int>(N), static_cast<int>(H), ssq, eps, out, ldo);
+  const int sp = launch_partials(x, ldx, w, H, P, N, H, workspace, ws_bytes, stream);
+  if (sp > 1)
+    hipLaunchKernelGGL(k_norm_linear_reduce, reduce_grid(P, N), dim3(256), 0, stream,
+                       static_cast<const float*>(workspace), sp, ssq, static_cast<int>(H), eps, out, ldo,
+                       static_cast<int>(P), static_cast<int>(N));
+  else
+    hipLaunchKernelGGL(k_norm_linear, dim3(grid_of(P, N)), dim3(NTHR), 0, stream, x, ldx, w, static_cast<int>(P),
+                       static_cast<int>(N), static_cast<int>(H), ssq, eps, out, ldo);
   return check_launch("rf_norm_linear");
 }

@@ -28,27 +28,28 @@ _SZ, _PSZ = ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)
 
 # name -> argument types (every function returns int status)
 SIGNATURES = {
-    "rf_map_apply": [_P, _I64, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P],
+    "rf_map_apply": [_P, _I64, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _SZ, _P],
+    "rf_gemm_workspace_bytes": [_I64, _I64, _I64, _PSZ],
     "rf_row_ssq": [_P, _I64, _P, _I64, _I64, _P],
     "rf_row_scatter": [_P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P],
     "rf_fold_norm": [_P, _P, _I32, _P, _I64, _I64, _P],
     "rf_rope_table": [_P, _I64, _P, _I32, _P, _P],
     "rf_norm_kv_write": [_P, _I64, _P, _I64, _I64, _F32, _P, _I32, _I32, _P, _I32, _P, _I32,
-                         _P, _P, _I64, _I64, _I64, _I64, _P],
+                         _P, _P, _I64, _I64, _I64, _I64, _P, _SZ, _P],
     "rf_rope_kv_write": [_P, _I64, _P, _I64, _I64, _I32, _I32, _P, _I32, _P, _P, _I64, _I64, _I64, _I64, _P],
-    "rf_norm_linear": [_P, _I64, _P, _I64, _I64, _F32, _P, _I64, _P, _I64, _P],
+    "rf_norm_linear": [_P, _I64, _P, _I64, _I64, _F32, _P, _I64, _P, _I64, _P, _SZ, _P],
     "rf_gdn_fill": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
     "rf_gdn_workspace_bytes": [_I64, _I32, _I32, _I32, _I32, _PSZ],
     "rf_transpose": [_P, _I64, _I64, _I64, _P, _I64, _P, _P],
     "rf_colsum_fold": [_P, _I64, _I64, _P, _P],
     "rf_gram_accumulate": [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
     "rf_row_gather": [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _P],
-    "rf_norm_q": [_P, _I64, _P, _I64, _I64, _F32, _P, _I32, _I32, _P, _I32, _P, _I32, _P, _P, _I64, _P],
+    "rf_norm_q": [_P, _I64, _P, _I64, _I64, _F32, _P, _I32, _I32, _P, _I32, _P, _I32, _P, _P, _I64, _P, _SZ, _P],
     "rf_attend_rows": [_P, _I64, _P, _I64, _I32, _I32, _P, _P, _I32, _I64, _I64, _I64, _F32, _P, _I64, _P, _SZ, _P],
     "rf_attend_rows_workspace_bytes": [_I64, _I32, _I32, _I32, _I64, _PSZ],
-    "rf_attend_causal": [_P, _I64, _I64, _I64, _I32, _I32, _P, _P, _I32, _I64, _I64, _I64, _F32, _P, _I64, _P, _SZ,
-                         _P],
-    "rf_attend_causal_workspace_bytes": [_I32, _I32, _I64, _PSZ],
+    "rf_attend_causal": [_P, _I64, _I64, _P, _I64, _I32, _I32, _P, _P, _I32, _I64, _I64, _I64, _F32, _P, _I64, _P,
+                         _SZ, _P],
+    "rf_attend_causal_workspace_bytes": [_I64, _I32, _I32, _I32, _I64, _PSZ],
     "rf_residual_add": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _P],
     "rf_silu_mul": [_P, _I64, _I64, _I64, _P, _I64, _P],
 }

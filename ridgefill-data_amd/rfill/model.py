@@ -201,6 +201,17 @@ class FillModel:
             self._attn_ws = ws = torch.empty(need, dtype=torch.uint8, device=device)
         return ws
 
+    def _gemm_workspace(self, M, N, K, device):
+        """The split-K workspace of an M x N x K product (None when the tiles fill the GPU unsplit), shared
+        by every GEMM of the exact rows' and the tail's layers (stream-ordered reuse)."""
+        need = ops.gemm_workspace_bytes(M, N, K)
+        if need == 0:
+            return None
+        ws = getattr(self, "_gemm_ws", None)
+        if ws is None or ws.numel() < need or ws.device != device:
+            self._gemm_ws = ws = torch.empty(need, dtype=torch.uint8, device=device)
+        return ws
+
     def _gdn_workspace(self, rows, device):
         """The GDN kernels' per-chunk workspace, shared by every GDN layer (stream-ordered reuse), sized
         for min(rows, GDN_ROWS) rows per pass."""
@@ -258,24 +269,32 @@ class FillModel:
         self.fill(i, x, pos, cache, ssq=ssq, cs=cs)
         rows = torch.as_tensor(rows, dtype=torch.int64).to(x.device)
         xr, sr = ops.row_gather(x, rows)
+        H, R = xr.shape[1], xr.shape[0]
         q = ops.norm_q(xr, sr, self.eps, w["wq"], self.n_heads, self.head_dim, w.get("q_norm"), self.knorm_kind, cs,
-                       rows)
-        o = ops.attend_rows(q, pos.to(x.device, torch.int64)[rows], c["kbuf"], c["vbuf"], c["n"], self.n_heads,
-                            self.scale, workspace=self._attn_workspace(len(rows), c["n"], x.device))
+                       rows, workspace=self._gemm_workspace(R, w["wq"].shape[0], H, x.device))
+        qpos = pos.to(x.device, torch.int64)[rows]
+        if self._causal_ok():
+            o = ops.attend_causal(q, 0, c["kbuf"], c["vbuf"], c["n"], self.n_heads, self.scale, qpos=qpos,
+                                  workspace=self._causal_workspace(R, c["n"], x.device))
+        else:
+            o = ops.attend_rows(q, qpos, c["kbuf"], c["vbuf"], c["n"], self.n_heads, self.scale,
+                                workspace=self._attn_workspace(R, c["n"], x.device))
         return self._out_mlp(w, xr, o)[0]
 
     def _out_mlp(self, w, h, o):
         """The rest of the layer after attention: h + o W_o^T, then the SwiGLU MLP with its residual
         (code/kva/model.py:112-118, :254-257), with the reference's bf16 roundings. Returns the layer
         output [rows, H] bf16 and its row sum-of-squares partials (the next norm's statistics)."""
-        a, _ = ops.map_apply(o, w["wo"], None)
+        R, dev = h.shape[0], h.device
+        gws = self._gemm_workspace
+        a, _ = ops.map_apply(o, w["wo"], None, workspace=gws(R, w["wo"].shape[0], w["wo"].shape[1], dev))
         h1, s1 = ops.residual_add(h, a)
-        gu = ops.norm_linear(h1, s1, self.eps, w["wgu"])
+        gu = ops.norm_linear(h1, s1, self.eps, w["wgu"], workspace=gws(R, w["wgu"].shape[0], w["wgu"].shape[1], dev))
         inter = w["inter"]
-        act = (torch.zeros if w["wd"].shape[1] != inter else torch.empty)(h.shape[0], w["wd"].shape[1],
-                                                                          dtype=torch.bfloat16, device=h.device)
+        act = (torch.zeros if w["wd"].shape[1] != inter else torch.empty)(R, w["wd"].shape[1],
+                                                                          dtype=torch.bfloat16, device=dev)
         ops.silu_mul(gu[:, :2 * inter], act[:, :inter])
-        dn, _ = ops.map_apply(act, w["wd"], None)
+        dn, _ = ops.map_apply(act, w["wd"], None, workspace=gws(R, w["wd"].shape[0], w["wd"].shape[1], dev))
         return ops.residual_add(h1, dn)
 
     def layer(self, i, h, pos, cache, ssq=None, cs=None):
@@ -295,27 +314,33 @@ class FillModel:
         if cs is None:
             cs = self.rope_table(pos)
         slot = self.reserve(c, T, self.n_kv, self.head_dim, h.device)
+        H = h.shape[1]
         ops.norm_kv_write(h, ssq, self.eps, w["wkv"], self.n_kv, self.head_dim, w.get("k_norm"), self.knorm_kind,
-                          cs, c["kbuf"], c["vbuf"], slot)
+                          cs, c["kbuf"], c["vbuf"], slot,
+                          workspace=self._gemm_workspace(T, w["wkv"].shape[0], H, h.device))
         self.commit(c, T)
         idx = torch.arange(T, device=h.device)
         q = ops.norm_q(h, ssq, self.eps, w["wq"], self.n_heads, self.head_dim, w.get("q_norm"), self.knorm_kind, cs,
-                       idx)
-        if self.n_heads // self.n_kv in ops.CAUSAL_GROUPS and self.head_dim in (64, 128):
+                       idx, workspace=self._gemm_workspace(T, w["wq"].shape[0], H, h.device))
+        if self._causal_ok():
             o = ops.attend_causal(q, slot, c["kbuf"], c["vbuf"], c["n"], self.n_heads, self.scale,
-                                  workspace=self._vt_workspace(c["n"], h.device))
+                                  workspace=self._causal_workspace(T, c["n"], h.device))
         else:
             o = ops.attend_rows(q, idx + slot, c["kbuf"], c["vbuf"], c["n"], self.n_heads, self.scale,
                                 workspace=self._attn_workspace(T, c["n"], h.device))
         return self._out_mlp(w, h, o)
 
-    def _vt_workspace(self, n, device):
-        """The tail attention's transposed-V workspace, shared by every layer (stream-ordered reuse)."""
-        need = ops.attend_causal_workspace_bytes(self.n_kv, self.head_dim, n)
-        ws = getattr(self, "_vt_ws", None)
+    def _causal_workspace(self, nq, n, device):
+        """rf_attend_causal's workspace (V transposed, key-range splits), shared by every layer
+        (stream-ordered reuse)."""
+        need = ops.attend_causal_workspace_bytes(nq, self.n_heads, self.n_kv, self.head_dim, n)
+        ws = getattr(self, "_causal_ws", None)
         if ws is None or ws.numel() < need or ws.device != device:
-            self._vt_ws = ws = torch.empty(need, dtype=torch.uint8, device=device)
+            self._causal_ws = ws = torch.empty(need, dtype=torch.uint8, device=device)
         return ws
+
+    def _causal_ok(self):
+        return self.n_heads // self.n_kv in ops.CAUSAL_GROUPS and self.head_dim in (64, 128)
 
     def logits(self, h, ssq=None):
         """F.linear(final_norm(h), lm_head).float() (code/kva/model.py:110-111): [rows, V] fp32 from bf16
@@ -332,7 +357,8 @@ class FillModel:
         head, V = self._lm
         if ssq is None:
             ssq = ops.row_ssq(h)
-        return ops.norm_linear(h, ssq, self.eps, head)[:, :V].float()
+        return ops.norm_linear(h, ssq, self.eps, head,
+                               workspace=self._gemm_workspace(h.shape[0], head.shape[0], h.shape[1], h.device))[:, :V].float()
 
     def fill_kv(self, i, k, v, pos, cache, cs=None):
         """Cache-only fill from pre-RoPE K and V [P, Hkv, d] (the reads() layout)."""

@@ -42,9 +42,31 @@ def ssq_parts(h):
     return h // SSQ_COLS
 
 
-def map_apply(b, w, c, out=None, ssq=None):
+def gemm_workspace_bytes(M, N, K):
+    """Bytes of the split-K workspace the GEMM entry points use for an M x N x K product (0: no split)."""
+    b = ctypes.c_size_t(0)
+    _lib.call("rf_gemm_workspace_bytes", M, N, K, ctypes.byref(b))
+    return b.value
+
+
+def _ws(workspace, M, N, K, device):
+    """(pointer, bytes) of a GEMM's split-K workspace: None -> no split; "auto" -> allocated here when a
+    split pays; a uint8 device tensor -> used if large enough."""
+    if workspace is None:
+        return None, 0
+    if isinstance(workspace, str):
+        need = gemm_workspace_bytes(M, N, K)
+        if not need:
+            return None, 0
+        workspace = torch.empty(need, dtype=torch.uint8, device=device)
+    _need(workspace, "workspace", torch.uint8, 1)
+    return workspace, workspace.numel()
+
+
+def map_apply(b, w, c, out=None, ssq=None, workspace=None):
     """x = b W^T + c in bf16 (Projector.__call__) and x's row sum-of-squares partials.
-    b [P, h_in], w [h_out, h_in], c [h_out] or None. Returns (x [P, h_out], ssq [P, h_out / 256])."""
+    b [P, h_in], w [h_out, h_in], c [h_out] or None. Returns (x [P, h_out], ssq [P, h_out / 256]).
+    workspace: the split-K workspace (see _ws)."""
     _need(b, "b", torch.bfloat16, 2)
     _need(w, "w", torch.bfloat16, 2)
     if not w.is_contiguous():
@@ -61,8 +83,9 @@ def map_apply(b, w, c, out=None, ssq=None):
     _need(ssq, "ssq", torch.float32, 2)
     if tuple(out.shape) != (P, h_out) or tuple(ssq.shape) != (P, h_out // SSQ_COLS) or not ssq.is_contiguous():
         raise ValueError("map_apply: output shapes")
+    ws, nb = _ws(workspace, P, h_out, h_in, b.device)
     _lib.call("rf_map_apply", _ptr(b), b.stride(0), _ptr(w), _ptr(c), _ptr(out), out.stride(0), _ptr(ssq),
-              P, h_in, h_out, _stream(b))
+              P, h_in, h_out, _ptr(ws), nb, _stream(b))
     return out, ssq
 
 
@@ -126,7 +149,7 @@ def _cache_args(kbuf, vbuf, hkv, d, slot_begin, m):
     return kbuf.stride(0), kbuf.stride(1), kbuf.shape[1]
 
 
-def norm_kv_write(x, ssq, eps, wkv, hkv, d, knorm, knorm_kind, cs, kbuf, vbuf, slot_begin):
+def norm_kv_write(x, ssq, eps, wkv, hkv, d, knorm, knorm_kind, cs, kbuf, vbuf, slot_begin, workspace=None):
     """Fused fill of one attention layer: RMSNorm (gain folded into wkv), K / V projections, k_norm,
     RoPE, write of rows [slot_begin, slot_begin + P) into kbuf / vbuf [hkv, cap, d]."""
     _need(x, "x", torch.bfloat16, 2)
@@ -145,9 +168,10 @@ def norm_kv_write(x, ssq, eps, wkv, hkv, d, knorm, knorm_kind, cs, kbuf, vbuf, s
         if knorm.shape[0] != d:
             raise ValueError("norm_kv_write: knorm width")
     hs, rs, cap = _cache_args(kbuf, vbuf, hkv, d, slot_begin, P)
+    ws, nb = _ws(workspace, P, 2 * hkv * d, H, x.device)
     _lib.call("rf_norm_kv_write", _ptr(x), x.stride(0), _ptr(ssq), P, H, float(eps), _ptr(wkv), hkv, d,
               _ptr(knorm), int(knorm_kind), _ptr(cs), cs.shape[1], _ptr(kbuf), _ptr(vbuf), hs, rs,
-              int(slot_begin), cap, _stream(x))
+              int(slot_begin), cap, _ptr(ws), nb, _stream(x))
 
 
 def rope_kv_write(k, v, cs, kbuf, vbuf, slot_begin):
@@ -165,7 +189,7 @@ def rope_kv_write(k, v, cs, kbuf, vbuf, slot_begin):
               _ptr(kbuf), _ptr(vbuf), hs, rs, int(slot_begin), cap, _stream(k))
 
 
-def norm_linear(x, ssq, eps, w, out=None):
+def norm_linear(x, ssq, eps, w, out=None, workspace=None):
     """bf16(rms-normed x @ w^T) with the norm gain already folded into w [N, H] (N % 256 == 0)."""
     _need(x, "x", torch.bfloat16, 2)
     _need(ssq, "ssq", torch.float32, 2)
@@ -176,8 +200,9 @@ def norm_linear(x, ssq, eps, w, out=None):
         raise ValueError("norm_linear: shapes")
     out = torch.empty(P, N, dtype=torch.bfloat16, device=x.device) if out is None else out
     _need(out, "out", torch.bfloat16, 2)
+    ws, nb = _ws(workspace, P, N, H, x.device)
     _lib.call("rf_norm_linear", _ptr(x), x.stride(0), _ptr(ssq), P, H, float(eps), _ptr(w), N, _ptr(out), out.stride(0),
-              _stream(x))
+              _ptr(ws), nb, _stream(x))
     return out
 
 
@@ -198,7 +223,7 @@ def row_gather(x, rows, out=None, ssq=None):
     return out, ssq
 
 
-def norm_q(x, ssq, eps, wq, hq, d, qnorm, qnorm_kind, cs, pos, out=None):
+def norm_q(x, ssq, eps, wq, hq, d, qnorm, qnorm_kind, cs, pos, out=None, workspace=None):
     """Queries of rows x at positions pos: RMSNorm (gain folded into wq), x wq^T, per-head q_norm, RoPE with
     table rows cs[pos]. Returns q [rows, hq d] bf16."""
     _need(x, "x", torch.bfloat16, 2)
@@ -215,8 +240,10 @@ def norm_q(x, ssq, eps, wq, hq, d, qnorm, qnorm_kind, cs, pos, out=None):
         _need(qnorm, "qnorm", torch.bfloat16, 1)
     out = torch.empty(rows, hq * d, dtype=torch.bfloat16, device=x.device) if out is None else out
     _need(out, "out", torch.bfloat16, 2)
+    ws, nb = _ws(workspace, rows, hq * d, H, x.device)
     _lib.call("rf_norm_q", _ptr(x), x.stride(0), _ptr(ssq), rows, H, float(eps), _ptr(wq), hq, d, _ptr(qnorm),
-              int(qnorm_kind), _ptr(cs), cs.shape[1], _ptr(pos.contiguous()), _ptr(out), out.stride(0), _stream(x))
+              int(qnorm_kind), _ptr(cs), cs.shape[1], _ptr(pos.contiguous()), _ptr(out), out.stride(0), _ptr(ws), nb,
+              _stream(x))
     return out
 
 
@@ -257,17 +284,18 @@ def attend_rows(q, qpos, kbuf, vbuf, n, hq, scale, out=None, workspace="auto"):
 CAUSAL_GROUPS = (1, 2, 4, 8)
 
 
-def attend_causal_workspace_bytes(hkv, d, n):
-    """Device bytes attend_causal needs (V transposed)."""
+def attend_causal_workspace_bytes(nq, hq, hkv, d, n):
+    """Device bytes attend_causal uses for nq queries over n keys (V transposed, key-range splits)."""
     b = ctypes.c_size_t(0)
-    _lib.call("rf_attend_causal_workspace_bytes", hkv, d, n, ctypes.byref(b))
+    _lib.call("rf_attend_causal_workspace_bytes", nq, hq, hkv, d, n, ctypes.byref(b))
     return b.value
 
 
-def attend_causal(q, slot0, kbuf, vbuf, n, hq, scale, out=None, workspace=None):
-    """Causal attention of nq consecutive queries q [nq, hq d] at cache slots slot0 .. slot0 + nq - 1 over
-    the first n rows of kbuf / vbuf [hkv, cap, d] (query j sees keys 0 .. slot0 + j). Returns [nq, hq d]
-    bf16. workspace: uint8 device memory of attend_causal_workspace_bytes (allocated here if None)."""
+def attend_causal(q, slot0, kbuf, vbuf, n, hq, scale, out=None, workspace=None, qpos=None):
+    """Causal attention of queries q [nq, hq d] over the first n rows of kbuf / vbuf [hkv, cap, d]: query j
+    sees keys 0 .. qpos[j] (qpos: sorted int64 positions on the device), or with qpos None the consecutive
+    slots slot0 .. slot0 + nq - 1. Returns [nq, hq d] bf16. workspace: uint8 device memory of
+    attend_causal_workspace_bytes (allocated here if None)."""
     _need(q, "q", torch.bfloat16, 2)
     for name, t in (("kbuf", kbuf), ("vbuf", vbuf)):
         _need(t, name, torch.bfloat16, 3)
@@ -277,14 +305,18 @@ def attend_causal(q, slot0, kbuf, vbuf, n, hq, scale, out=None, workspace=None):
     nq = q.shape[0]
     if q.shape[1] < hq * d or n > cap:
         raise ValueError("attend_causal: shapes")
+    if qpos is not None:
+        _need(qpos, "qpos", torch.int64, 1)
+        if qpos.shape[0] != nq:
+            raise ValueError("attend_causal: one position per query")
+        qpos = qpos.contiguous()
     out = torch.empty(nq, hq * d, dtype=torch.bfloat16, device=q.device) if out is None else out
     _need(out, "out", torch.bfloat16, 2)
-    need = attend_causal_workspace_bytes(hkv, d, n)
     if workspace is None:
-        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+        workspace = torch.empty(attend_causal_workspace_bytes(nq, hq, hkv, d, n), dtype=torch.uint8, device=q.device)
     _need(workspace, "workspace", torch.uint8, 1)
-    _lib.call("rf_attend_causal", _ptr(q), q.stride(0), nq, int(slot0), hq, d, _ptr(kbuf), _ptr(vbuf), hkv,
-              kbuf.stride(0), kbuf.stride(1), n, float(scale), _ptr(out), out.stride(0), _ptr(workspace),
+    _lib.call("rf_attend_causal", _ptr(q), q.stride(0), nq, _ptr(qpos), int(slot0), hq, d, _ptr(kbuf), _ptr(vbuf),
+              hkv, kbuf.stride(0), kbuf.stride(1), n, float(scale), _ptr(out), out.stride(0), _ptr(workspace),
               workspace.numel(), _stream(q))
     return out
 

@@ -1,6 +1,8 @@
 """The C ABI: librfill.so loads without a GPU and exports every entry point include/rfill.h declares,
 and the Python binding declares exactly those (no compute calls here)."""
 import ctypes
+
+import pytest
 import re
 from pathlib import Path
 
@@ -39,3 +41,18 @@ def test_status_codes_match_the_header():
         value = int(re.search(rf"#define {name} \(?(-?\d+)\)?", text).group(1))
         assert getattr(_lib, name) == value
     assert _lib.SSQ_COLS == int(re.search(r"#define RF_SSQ_COLS (\d+)", text).group(1))
+
+
+def test_gemm_workspace_sizes():
+    """Host-only size rule of the GEMM entry points' split-K workspace: splits x M x N fp32 when the
+    256 x 256 tiles are too few for the GPU (splits = min(256 / tiles, K / 512, 16)), else none."""
+    from rfill import ops
+    assert ops.gemm_workspace_bytes(28672, 4096, 4096) == 0          # the fill: 1792 tiles, unsplit
+    assert ops.gemm_workspace_bytes(287, 4096, 4096) == 8 * 287 * 4096 * 4       # 32 tiles: 8 splits
+    assert ops.gemm_workspace_bytes(287, 24576, 4096) == 0           # 192 tiles
+    assert ops.gemm_workspace_bytes(4096, 2048, 4096) == 2 * 4096 * 2048 * 4     # the tail's K / V: 128 tiles
+    assert ops.gemm_workspace_bytes(40, 512, 2048) == 4 * 40 * 512 * 4           # K / 512 = 4 caps the splits
+    assert ops.gemm_workspace_bytes(287, 4096, 256) == 0             # too little K to split
+    assert ops.gemm_workspace_bytes(0, 4096, 4096) == 0
+    with pytest.raises(ValueError):
+        ops.gemm_workspace_bytes(10, 100, 4096)                     # N not a multiple of 256

@@ -233,3 +233,45 @@ def test_attend_causal_refuses(dev):
     from rfill._lib import UnsupportedArchitecture
     with pytest.raises(UnsupportedArchitecture):
         ops.attend_causal(q6, 0, kb, kb.clone(), 200, 6, 0.1)                 # group of 3
+
+
+@pytest.mark.parametrize("hq,hkv,d,nq,n", [(32, 8, 128, 150, 6000), (16, 2, 128, 37, 3000), (4, 2, 64, 300, 2500),
+                                           (8, 8, 64, 5, 900)])
+def test_attend_causal_at_positions(dev, hq, hkv, d, nq, n):
+    """rf_attend_causal with sorted query positions (the exact rows' attention): with the key range split
+    over blocks (full workspace) and unsplit (a workspace holding only V transposed), against the oracle's
+    attend_at and rf_attend_rows; split results the same bits run to run."""
+    from rfill import ops
+    q, k, v = _qkv(nq, hq, hkv, d, n, seed=nq + n)
+    g = torch.Generator().manual_seed(nq)
+    qpos = torch.randperm(n, generator=g)[:nq].sort().values
+    qpos[0] = 0                                        # a query that sees only key 0
+    qpos = qpos.sort().values.unique()
+    q = q[:qpos.shape[0]]
+    nq = q.shape[0]
+    kb = torch.zeros(hkv, n + 64, d, dtype=torch.bfloat16)
+    vb = torch.zeros_like(kb)
+    kb[:, :n], vb[:, :n] = k, v
+    vb[:, n:] = float("nan")
+    scale = d ** -0.5
+    qd, kd, vd, pd = q.to(dev), kb.to(dev), vb.to(dev), qpos.to(dev)
+    full = ops.attend_causal_workspace_bytes(nq, hq, hkv, d, n)
+    vt_only = hkv * d * ((n + 63) // 64 * 64) * 2
+    vt_only = (vt_only + 255) // 256 * 256
+    assert full > vt_only                              # these sizes split the key range
+    split = ops.attend_causal(qd, 0, kd, vd, n, hq, scale, qpos=pd)
+    again = ops.attend_causal(qd, 0, kd, vd, n, hq, scale, qpos=pd)
+    one = ops.attend_causal(qd, 0, kd, vd, n, hq, scale, qpos=pd,
+                            workspace=torch.empty(vt_only, dtype=torch.uint8, device=dev))
+    rows = ops.attend_rows(qd, pd, kd, vd, n, hq, scale)
+    torch.cuda.synchronize()
+    want = oops.attend_at(q.view(nq, hq, d).transpose(0, 1), k, v, scale, qpos)
+    e_s, e_1, e_r = rel_err(split, want), rel_err(one, want), rel_err(split, rows)
+    print(f"hq {hq} hkv {hkv} d {d} nq {nq} n {n}: split {e_s:.2e}, one pass {e_1:.2e} vs oracle; "
+          f"{e_r:.2e} vs rf_attend_rows")
+    assert torch.isfinite(split.float()).all() and torch.isfinite(one.float()).all()
+    assert e_s < TOL and e_1 < TOL and e_r < TOL
+    assert torch.equal(split, again)
+    first = split[0].view(hq, d).cpu()
+    for h in range(hq):
+        assert torch.equal(first[h], v[h // (hq // hkv), 0])
