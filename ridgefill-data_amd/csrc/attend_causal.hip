@@ -7,16 +7,21 @@
 // direct loads (buffer_load_dwordx4 ... lds). A block takes one K / V head and 256 query rows (256 / rep
 // consecutive queries x the rep query heads sharing the K / V head); 8 waves, each owning 32 query rows
 // of one head. The keys 0 .. (the block's last query position) go through LDS in tiles of 64, three
-// tiles in flight. Per tile and wave:
+// tiles in flight and four stages. Per tile and wave:
 //   S^T = K Q^T on v_mfma_f32_32x32x16_bf16 (A = the K tile, B = the wave's queries held in registers):
 //       lane l holds, for query l % 32, the scores of keys 8 (j / 4) + 4 (l / 32) + j % 4 of each
 //       32-key half (j < 16);
-//   online softmax in fp32 in the base-2 domain (scores times scale * log2 e), keys past the query's
-//       position masked; every value a lane holds belongs to its own query, so the running maximum,
-//       the rescale and the row sum need no lane exchange except the one between the lane halves;
+//   online softmax in fp32 in the base-2 domain, keys past the query's position masked; every value a
+//       lane holds belongs to its own query, so the maximum, the rescale and the row sum need no lane
+//       exchange except the one between the lane halves. The reference maximum is raised lazily (only
+//       when a score exceeds it by more than 2^8), so the O rescale runs on few tiles;
 //   O^T += V^T P^T on the same MFMA: P (rounded to bf16) is the B operand straight from the score
 //       registers, the contraction order over each 16-key step being keys {0..3, 8..11} + 4 (l / 32)
 //       of the step, and the V^T fragment is read in that order (two 8-byte LDS reads).
+// Waves 4-7 (the second wave of each SIMD) run half a tile behind waves 0-3, so that one wave's
+// softmax (VALU) runs beside the other's MFMAs instead of both meeting at each tile's barrier in the
+// same phase. With few query blocks the key range is split over blocks (blockIdx.z) whose partials
+// k_causal_combine merges in a fixed order.
 // The probabilities enter the second product as bf16 before normalisation (the reference casts after
 // it; the difference is within rounding), scores are fp32 products of the bf16 q and k values as the
 // reference's fp32 matmul, and the output is O / (row sum) rounded to bf16.
@@ -36,7 +41,7 @@ constexpr int KT = 64;                 // keys per tile
 constexpr int NW = 8;                  // waves per block
 constexpr int NTHR = 64 * NW;
 constexpr int QROWS = 32 * NW;         // query rows (query, head) per block: 32 per wave
-constexpr int NSTAGE = 3;              // tiles in flight
+constexpr int NSTAGE = 4;              // LDS stages: three tiles in flight, one still read
 
 __device__ __forceinline__ bf16x8 as_frag(const uint4& u) { return __builtin_bit_cast(bf16x8, u); }
 
@@ -56,8 +61,9 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 
 // LDS layout of one stage: the K tile (64 keys x AD) then the V^T tile (AD rows x 64 keys), in 16-byte
 // chunks. K row r's chunk c sits at r * KCPR + (c ^ (r % KCPR)); V^T row r's chunk c at
-// r * 8 + (c ^ ((r / 2) % 8)): the fragment reads (32 rows, one chunk or half chunk per lane) then hit
-// distinct banks.
+// r * 8 + (c ^ ((r / 2 ^ 2 (r / 32)) % 8)): the fragment reads (32 rows, one chunk or half chunk per lane)
+// then hit distinct banks, and so do a lane's eight V^T reads of a key step (the chunk pair of the step in
+// the four d blocks, rows 32 apart), which the compiler pairs into single instructions.
 template <int AD>
 struct Layout {
   static constexpr int KCPR = AD / 8;
@@ -69,7 +75,8 @@ struct Layout {
   static constexpr int LOADS = KLOADS + VLOADS;
   static_assert(KLOADS * 64 * NW == K_U4 && VLOADS * 64 * NW == V_U4, "tile loads must split evenly");
   __device__ static int kslot(int row, int c) { return row * KCPR + (c ^ (row & (KCPR - 1))); }
-  __device__ static int vslot(int row, int c) { return K_U4 + row * 8 + (c ^ ((row >> 1) & 7)); }
+  __device__ static int vswz(int row) { return ((row >> 1) ^ ((row >> 5) << 1)) & 7; }
+  __device__ static int vslot(int row, int c) { return K_U4 + row * 8 + (c ^ vswz(row)); }
 };
 
 struct CausalArgs {
@@ -114,78 +121,128 @@ __device__ __forceinline__ void issue_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_b
                                              voff[i], vbyte, 0, 0);
 }
 
-// One 64-key tile for one wave: S^T = K Q^T, the online softmax update, O^T += V^T P^T. st is the
-// tile's LDS stage; edge: some key of the tile lies past some query of the wave (mask needed).
-// (st is __restrict__: the LDS reads then carry alias information, and the compiler does not make them
-// wait for the direct loads in flight into the other stages; the kernel's own waits order them.)
+// Headroom of the lazy softmax rescale: the running reference maximum is raised only when a score
+// exceeds it by more than this (in base 2), so probabilities stay below 2^8 and the O rescale runs
+// only on the tiles that raise it.
+constexpr float RESCALE_LOG2 = 8.0f;
+
+// Per-lane LDS byte offsets of the fragments within a stage, the same for every tile. K fragment (key
+// half kb, d step s): row 32 kb + n, chunk 2 s + hh, at ko[s] + kb * 32 KCPR 16 (row 32 kb + n has the
+// swizzle of row n). V^T fragment (d block b, key chunk c): row 32 b + n, at vo[c ^ 2 b] + b * 32 * 8 * 16
+// (row 32 b + n has the swizzle of row n XOR 2 b), 8 hh bytes into the chunk (the lane half's four keys).
 template <int AD>
-__device__ __forceinline__ void tile(const uint4* __restrict__ st, const bf16x8 (&qf)[AD / 16], f32x16 (&o)[AD / 32],
-                                     float& m, float& lsum, int64_t k0, bool edge, int64_t mypos, int n, int hh,
-                                     float scale_log2) {
+struct FragOffsets {
+  uint32_t ko[AD / 16], vo[8];
+  __device__ FragOffsets(int n, int hh) {
+    using L = Layout<AD>;
+#pragma unroll
+    for (int s = 0; s < AD / 16; ++s) ko[s] = static_cast<uint32_t>(L::kslot(n, 2 * s + hh) * 16);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) vo[c] = static_cast<uint32_t>(L::vslot(n, c) * 16 + 8 * hh);
+  }
+};
+
+// The two lane halves' values of a lane pair (l, l ^ 32), the same in both lanes: v of the lower lane
+// and v of the upper lane (one v_permlane32_swap).
+__device__ __forceinline__ void lane_pair(float v, float& lo, float& hi) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  lo = __uint_as_float(r[0]);
+  hi = __uint_as_float(r[1]);
+}
+
+// S^T = K Q^T for one 64-key tile and the wave's 32 queries: sc[kb][j] = the raw score of key
+// 32 kb + 8 (j / 4) + 4 hh + j % 4 of the tile for query n. (The stage pointers are __restrict__: the
+// LDS reads then carry alias information, and the compiler does not make them wait for the direct loads
+// in flight into the other stages; the kernel's own waits order them.)
+template <int AD>
+__device__ __forceinline__ void tile_scores(const char* __restrict__ st, const bf16x8 (&qf)[AD / 16], f32x16 (&sc)[2],
+                                            const FragOffsets<AD>& fo) {
   using L = Layout<AD>;
-  constexpr int NS = AD / 16, NB = AD / 32;
-  f32x16 sc[2];
+  constexpr int NS = AD / 16;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) sc[kb][r] = 0.f;
-    const int row = 32 * kb + n;
 #pragma unroll
     for (int s = 0; s < NS; ++s)
-      sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_frag(st[L::kslot(row, 2 * s + hh)]), qf[s], sc[kb], 0, 0, 0);
+      sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          as_frag(*reinterpret_cast<const uint4*>(st + fo.ko[s] + kb * 32 * L::KCPR * 16)), qf[s], sc[kb], 0, 0, 0);
   }
-  // scale into the base-2 domain, mask, running maximum
+}
+
+// One tile's softmax and products, with the next tile's scores interleaved: mask the scores sc of the
+// tile at key k0 when some key lies past some query of the wave (edge), raise the lane's reference
+// maximum mref (raw-score units, -inf until a key is visible) lazily, then in one block the base-2
+// probabilities exp2(fma(s, c, -mref c)) of sc (c = scale * log2(e) > 0) beside the MFMAs of the next
+// tile's scores sn (from stage sn_st), and O^T += V^T P^T from this tile's stage st.
+template <int AD>
+__device__ __forceinline__ void tile_step(const char* __restrict__ st, const char* __restrict__ sn_st,
+                                          const bf16x8 (&qf)[AD / 16], f32x16 (&sc)[2], f32x16 (&sn)[2],
+                                          f32x16 (&o)[AD / 32], float& mref, float& lsum, int64_t k0, bool edge,
+                                          int64_t mypos, int hh, float c, const FragOffsets<AD>& fo) {
+  using L = Layout<AD>;
+  constexpr int NB = AD / 32, NS = AD / 16;
+  if (edge) {
+    // key 32 kb + 8 (j / 4) + 4 hh + j % 4 of the tile is past the query when its offset exceeds rel
+    const int rel = static_cast<int>(min<int64_t>(max<int64_t>(mypos - k0, -1), KT)) - 4 * hh;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        if (32 * kb + 8 * (j >> 2) + (j & 3) > rel) sc[kb][j] = -INFINITY;
+  }
   float tmax = -INFINITY;
 #pragma unroll
   for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      float v = sc[kb][j] * scale_log2;
-      if (edge) {
-        const int64_t key = k0 + 32 * kb + 8 * (j >> 2) + 4 * hh + (j & 3);
-        v = key <= mypos ? v : -INFINITY;
-      }
-      sc[kb][j] = v;
-      tmax = fmaxf(tmax, v);
-    }
-  tmax = fmaxf(tmax, __shfl_xor(tmax, 32, 64));
-  const float mnew = fmaxf(m, tmax);
-  const float mref = mnew == -INFINITY ? 0.f : mnew;    // every key so far masked (a split past the query)
-  const float alpha = __builtin_amdgcn_exp2f(m - mref);
-  m = mnew;
+    for (int j = 0; j < 16; ++j) tmax = fmaxf(tmax, sc[kb][j]);
+  float lo, hi;
+  lane_pair(tmax, lo, hi);
+  tmax = fmaxf(lo, hi);
+  if (tmax > mref + RESCALE_LOG2 / c) {                 // raise the reference (always on the first visible key)
+    const float alpha = __builtin_amdgcn_exp2f((mref - tmax) * c);    // 0 while mref is -inf
+    mref = tmax;
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[b][r] *= alpha;
+    lsum *= alpha;
+  }
+  const float mc = mref == -INFINITY ? 0.f : mref * c;  // every key so far masked (a split past the query)
+  // the next tile's 16 score MFMAs, two probabilities after each
   float psum = 0.f;
-  bf16x8 pf[4];                                         // P^T fragments of the four 16-key steps
+  uint32_t pk[16];
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
+  for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-    for (int sub = 0; sub < 2; ++sub) {
-      uint32_t pk[4];
+    for (int r = 0; r < 16; ++r) sn[kb][r] = 0.f;
+  }
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float p0 = __builtin_amdgcn_exp2f(sc[kb][8 * sub + 2 * e] - mref);
-        const float p1 = __builtin_amdgcn_exp2f(sc[kb][8 * sub + 2 * e + 1] - mref);
-        psum += p0 + p1;
-        pk[e] = bf16_pair(p0, p1);
-      }
-      pf[2 * kb + sub] = __builtin_bit_cast(bf16x8, make_uint4(pk[0], pk[1], pk[2], pk[3]));
+  for (int q = 0; q < 2 * NS; ++q) {
+    const int kb = q / NS, s = q % NS;
+    sn[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        as_frag(*reinterpret_cast<const uint4*>(sn_st + fo.ko[s] + kb * 32 * L::KCPR * 16)), qf[s], sn[kb], 0, 0, 0);
+#pragma unroll
+    for (int e = q * 16 / (2 * NS); e < (q + 1) * 16 / (2 * NS); ++e) {
+      const int pkb = e / 8, pj = 2 * (e % 8);
+      const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[pkb][pj], c, -mc));
+      const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[pkb][pj + 1], c, -mc));
+      psum += p0 + p1;
+      pk[e] = bf16_pair(p0, p1);
     }
-  lsum = lsum * alpha + psum;
-#pragma unroll
-  for (int b = 0; b < NB; ++b)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) o[b][r] *= alpha;
-  // O^T[d, query] += V^T[d, keys] P^T[keys, query] over the four 16-key steps
+  }
+  lsum += psum;
+  // O^T[d, query] += V^T[d, keys] P^T[keys, query] over the four 16-key steps (keys 16 stp ..: chunks
+  // 2 stp and 2 stp + 1; P^T step stp = the lane's probabilities 8 stp .. 8 stp + 7)
 #pragma unroll
   for (int stp = 0; stp < 4; ++stp) {
-    const int c0 = 2 * stp;                             // the step's first key chunk: keys 16 stp .. + 7
+    const bf16x8 pf = __builtin_bit_cast(bf16x8, make_uint4(pk[4 * stp], pk[4 * stp + 1], pk[4 * stp + 2],
+                                                             pk[4 * stp + 3]));
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      const int row = 32 * b + n;
-      const char* vrow = reinterpret_cast<const char*>(st);
-      const uint2 lo = *reinterpret_cast<const uint2*>(vrow + L::vslot(row, c0) * 16 + 8 * hh);
-      const uint2 hi = *reinterpret_cast<const uint2*>(vrow + L::vslot(row, c0 + 1) * 16 + 8 * hh);
-      o[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_frag(make_uint4(lo.x, lo.y, hi.x, hi.y)), pf[stp], o[b], 0,
-                                                     0, 0);
+      const uint2 vl = *reinterpret_cast<const uint2*>(st + fo.vo[(2 * stp) ^ (2 * b)] + b * 32 * 8 * 16);
+      const uint2 vh = *reinterpret_cast<const uint2*>(st + fo.vo[(2 * stp + 1) ^ (2 * b)] + b * 32 * 8 * 16);
+      o[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_frag(make_uint4(vl.x, vl.y, vh.x, vh.y)), pf, o[b], 0, 0, 0);
     }
   }
 }
@@ -240,7 +297,7 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
 #pragma unroll
   for (int i = 0; i < L::VLOADS; ++i) {
     const int s = (w * L::VLOADS + i) * 64 + lane;
-    const int row = s / 8, pc = s % 8, c = pc ^ ((row >> 1) & 7);
+    const int row = s / 8, pc = s % 8, c = pc ^ L::vswz(row);
     voff[i] = static_cast<uint32_t>((row * a.vt_ld + c * 8) * 2);
   }
   char* base = reinterpret_cast<char*>(lds);
@@ -255,24 +312,40 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
   for (int b = 0; b < NB; ++b)
 #pragma unroll
     for (int r = 0; r < 16; ++r) o[b][r] = 0.f;
-  float m = -INFINITY, lsum = 0.f;
+  float m = -INFINITY, lsum = 0.f;                        // reference maximum (raw scores), row sum
+  const float c = a.scale_log2;
 
-  if (it0 < it1) issue(it0);
-  if (it0 + 1 < it1) issue(it0 + 1);
+  // Tile it is processed in iteration it: its softmax and products, with the scores of tile it + 1
+  // computed in the same block (the MFMAs run beside the softmax's VALU work). Loads run three tiles
+  // ahead into four stages: tile it + 3 goes into the stage of tile it - 1, whose last reads (its V^T)
+  // ended before this iteration's barrier.
+  const FragOffsets<AD> fo(n, hh);
+  f32x16 sc[2], sn[2];
+  auto stage = [&](int it) { return base + ((it - it0) % NSTAGE) * L::STAGE_U4 * 16; };
+  for (int i = 0; i < 3; ++i)
+    if (it0 + i < it1) issue(it0 + i);
+  if (it0 + 2 < it1) wait_vm_lgkm0<2 * L::LOADS>();        // tile it0 landed
+  else if (it0 + 1 < it1) wait_vm_lgkm0<L::LOADS>();
+  else wait_vm_lgkm0<0>();
+  __builtin_amdgcn_s_barrier();
+  if (it0 < it1) tile_scores<AD>(stage(it0), qf, sc, fo);
   for (int it = it0; it < it1; ++it) {
-    if (it + 1 < it1) wait_vm_lgkm0<L::LOADS>();          // this tile's loads done, the next one's may fly
+    if (it + 2 < it1) wait_vm_lgkm0<L::LOADS>();          // tile it + 1 landed, tile it + 2 may fly
     else wait_vm_lgkm0<0>();
-    __builtin_amdgcn_s_barrier();                         // every wave's share of the tile has landed and
-    if (it + 2 < it1) issue(it + 2);                      // every wave is done with the stage reloaded here
+    __builtin_amdgcn_s_barrier();                         // every wave's share of it has landed and every
+    if (it + 3 < it1) issue(it + 3);                      // wave is done with the stage reloaded here
     const int64_t k0 = static_cast<int64_t>(it) * KT;
-    if (k0 > wave_last) continue;                         // every key of the tile is past the wave's queries
-    tile<AD>(lds + ((it - it0) % NSTAGE) * L::STAGE_U4, qf, o, m, lsum, k0, k0 + KT - 1 > wave_first, mypos, n, hh,
-             a.scale_log2);
+    if (k0 > wave_last) continue;                         // this and every later tile lie past the wave's queries
+    tile_step<AD>(stage(it), stage(it + 1), qf, sc, sn, o, m, lsum, k0, k0 + KT - 1 > wave_first, mypos, hh, c, fo);
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) sc[kb] = sn[kb];
   }
   wait_vm_lgkm0<0>();
 
   // lane holds O[query n][d = 32 b + 8 (j / 4) + 4 hh + j % 4]
-  const float ltot = lsum + __shfl_xor(lsum, 32, 64);
+  float llo, lhi;
+  lane_pair(lsum, llo, lhi);
+  const float ltot = llo + lhi;
   if (ns > 1) {                                           // unnormalised partials for k_causal_combine
     float* pb = part_block<AD>(a, blockIdx.x, hk, sp);
     const int r = 32 * w + n;
@@ -284,7 +357,7 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
         *reinterpret_cast<float4*>(orow + 32 * b + 8 * g) = make_float4(o[b][4 * g], o[b][4 * g + 1], o[b][4 * g + 2],
                                                                         o[b][4 * g + 3]);
     if (hh == 0) {
-      pb[QROWS * AD + r] = m;
+      pb[QROWS * AD + r] = m == -INFINITY ? m : m * c;    // base-2 maximum of the reference
       pb[QROWS * AD + QROWS + r] = ltot;
     }
     return;
@@ -432,6 +505,8 @@ extern "C" int rf_attend_causal(const uint16_t* q, int64_t ldq, int64_t nq, cons
   if (!aligned16(q) || !aligned16(kbuf) || !aligned16(vbuf) || !aligned16(workspace) ||
       (reinterpret_cast<uintptr_t>(out) & 7u))
     return fail(RF_EINVAL_SHAPE, "rf_attend_causal: alignment");
+  if (!(scale > 0.f) || !(scale < 1e30f)) return fail(RF_EINVAL_ARG, "rf_attend_causal: scale %g (must be positive)",
+                                                      static_cast<double>(scale));
   const int64_t vt_ld = vt_cols(n_keys);
   const size_t vtb = vt_bytes(hkv, d, n_keys);
   if (ws_bytes < vtb)
