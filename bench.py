@@ -77,15 +77,19 @@ def fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches, timer=None, overlap=Fa
     from rfill.kva import serial, two_stream
     W, B = arm.projector._maps(b.device)
 
+    P, H = b.shape
+
     def produce(i, slot):
-        f = lambda: ops.map_apply(b, W[i], B[i], xbuf[slot], sbuf[slot])          # noqa: E731
+        ws = model.gemm_workspace(P, W[i].shape[0], H, b.device, "produce")
+        f = lambda: ops.map_apply(b, W[i], B[i], xbuf[slot], sbuf[slot], workspace=ws)    # noqa: E731
         f() if timer is None else timer.run("rf_map_apply", f)
 
     def consume(i, slot):
         w, c = model.W[i], caches[i]
+        ws = model.gemm_workspace(P, w["wkv"].shape[0], H, b.device)
         f = lambda: ops.norm_kv_write(xbuf[slot], sbuf[slot], model.eps, w["wkv"], model.n_kv,  # noqa: E731
                                       model.head_dim, w.get("k_norm"), model.knorm_kind, cs, c["kbuf"],
-                                      c["vbuf"], 0)
+                                      c["vbuf"], 0, workspace=ws)
         f() if timer is None else timer.run("rf_norm_kv_write", f)
 
     (two_stream if overlap else serial)(range(arm.split, model.n_layers), produce, consume, b.device)
@@ -226,7 +230,8 @@ def hybrid_bench(dev, reps=3, split=24, n_rows=32768, tail=4096):
         caches = model.new_cache()
         for i in w["layers"]:
             kind = model.layer_types[i]
-            f_map = lambda: proj.apply(i, b, x, ssq)                                       # noqa: E731
+            ws = model.gemm_workspace(P, H, H, dev, "produce")
+            f_map = lambda: proj.apply(i, b, x, ssq, workspace=ws)                         # noqa: E731
             f_fill = lambda: model.fill(i, x, pos, caches, ssq=ssq, cs=cs)                 # noqa: E731
             for name, f in (("map", f_map), (kind, f_fill)):
                 f() if timer is None else timer.run(name, f)

@@ -688,21 +688,51 @@ int split_count(int64_t M, int64_t N, int64_t K) {
   return static_cast<int>(std::max<int64_t>(s, 1));
 }
 
-size_t split_bytes(int64_t M, int64_t N, int64_t K) {
-  const int s = split_count(M, N, K);
-  return s > 1 ? static_cast<size_t>(s) * M * N * 4 : 0;
+// How an M x N x K product runs: rows [0, m_fused) through the fused kernel, rows [m_fused, M) with K split
+// `splits` ways (k_gemm_partial + a reduce kernel) when splits > 1. Too few tiles for the GPU: all rows
+// split. Otherwise, when whole tile rows fill the waves (N / 256 divides 256) and the last wave is at
+// most half full, its tile rows are split, so that wave takes a fraction of a tile's time.
+struct Plan {
+  int64_t m_fused;
+  int splits;
+};
+
+Plan plan(int64_t M, int64_t N, int64_t K) {
+  const int64_t tiles_n = N / BN, trows = (M + BM - 1) / BM;
+  if (trows * tiles_n < 256) {
+    const int s = split_count(M, N, K);
+    return s > 1 ? Plan{0, s} : Plan{M, 1};
+  }
+  if (256 % tiles_n == 0) {
+    const int64_t rem = trows % (256 / tiles_n);
+    if (rem && 2 * rem * tiles_n <= 256) {
+      const int64_t s = std::min<int64_t>(std::min<int64_t>(256 / (rem * tiles_n), K / 512), 16);
+      if (s > 1) return Plan{(trows - rem) * BM, static_cast<int>(s)};
+    }
+  }
+  return Plan{M, 1};
 }
 
-// Runs the split partials of an M x N x K product into ws when a split pays and ws holds them; returns
-// the split count the reduce kernel must add (1: no split, run the fused kernel).
-int launch_partials(const uint16_t* X, int64_t ldx, const uint16_t* W, int64_t ldw, int64_t M, int64_t N, int64_t K,
-                    void* ws, size_t ws_bytes, hipStream_t stream) {
-  const int s = split_count(M, N, K);
-  if (s <= 1 || !ws || ws_bytes < split_bytes(M, N, K)) return 1;
-  const int kper = static_cast<int>((K / s + BK - 1) / BK * BK);
-  hipLaunchKernelGGL(k_gemm_partial, dim3(grid_of(M, N) * s), dim3(NTHR), 0, stream, X, ldx, W, ldw,
-                     static_cast<int>(M), static_cast<int>(N), static_cast<int>(K), kper, static_cast<float*>(ws));
-  return s;
+size_t split_bytes(int64_t M, int64_t N, int64_t K) {
+  const Plan p = plan(M, N, K);
+  return p.splits > 1 ? static_cast<size_t>(p.splits) * (M - p.m_fused) * N * 4 : 0;
+}
+
+// The plan an entry point follows with this workspace: the split part only if the workspace holds it.
+Plan plan_with(int64_t M, int64_t N, int64_t K, const void* ws, size_t ws_bytes) {
+  const Plan p = plan(M, N, K);
+  if (p.splits <= 1 || !ws || ws_bytes < split_bytes(M, N, K)) return Plan{M, 1};
+  return p;
+}
+
+// The split partials of rows [m0, M) of an M x N x K product into ws.
+void launch_partials(const uint16_t* X, int64_t ldx, const uint16_t* W, int64_t ldw, int64_t M, int64_t N, int64_t K,
+                     const Plan& p, void* ws, hipStream_t stream) {
+  const int64_t rows = M - p.m_fused;
+  const int kper = static_cast<int>((K / p.splits + BK - 1) / BK * BK);
+  hipLaunchKernelGGL(k_gemm_partial, dim3(grid_of(rows, N) * p.splits), dim3(NTHR), 0, stream, X + p.m_fused * ldx,
+                     ldx, W, ldw, static_cast<int>(rows), static_cast<int>(N), static_cast<int>(K), kper,
+                     static_cast<float*>(ws));
 }
 
 dim3 reduce_grid(int64_t M, int64_t N) {
@@ -736,14 +766,17 @@ extern "C" int rf_map_apply(const uint16_t* b, int64_t ldb, const uint16_t* w, c
     return fail(RF_EINVAL_SHAPE, "rf_map_apply: pointers must be 16-byte aligned");
   if (workspace && !aligned16(workspace)) return fail(RF_EINVAL_SHAPE, "rf_map_apply: workspace alignment");
   if (P == 0) return RF_OK;
-  const int sp = launch_partials(b, ldb, w, h_in, P, h_out, h_in, workspace, ws_bytes, stream);
-  if (sp > 1)
-    hipLaunchKernelGGL(k_map_apply_reduce, reduce_grid(P, h_out), dim3(256), 0, stream,
-                       static_cast<const float*>(workspace), sp, c, x, ldx, ssq, static_cast<int>(P),
-                       static_cast<int>(h_out));
-  else
-    hipLaunchKernelGGL(k_map_apply, dim3(grid_of(P, h_out)), dim3(NTHR), 0, stream, b, ldb, w, c, x, ldx, ssq,
-                       static_cast<int>(P), static_cast<int>(h_out), static_cast<int>(h_in));
+  const Plan pl = plan_with(P, h_out, h_in, workspace, ws_bytes);
+  const int64_t mf = pl.m_fused, rows = P - mf;
+  if (mf > 0)
+    hipLaunchKernelGGL(k_map_apply, dim3(grid_of(mf, h_out)), dim3(NTHR), 0, stream, b, ldb, w, c, x, ldx, ssq,
+                       static_cast<int>(mf), static_cast<int>(h_out), static_cast<int>(h_in));
+  if (pl.splits > 1) {
+    launch_partials(b, ldb, w, h_in, P, h_out, h_in, pl, workspace, stream);
+    hipLaunchKernelGGL(k_map_apply_reduce, reduce_grid(rows, h_out), dim3(256), 0, stream,
+                       static_cast<const float*>(workspace), pl.splits, c, x + mf * ldx, ldx,
+                       ssq + mf * (h_out / SSQ_COLS), static_cast<int>(rows), static_cast<int>(h_out));
+  }
   return check_launch("rf_map_apply");
 }
 
@@ -778,13 +811,20 @@ extern "C" int rf_norm_kv_write(const uint16_t* x, int64_t ldx, const float* ssq
            kbuf, vbuf, head_stride, row_stride, slot_begin, nullptr};
   const int64_t N = 2ll * hkv * d;
   if (workspace && !aligned16(workspace)) return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write: workspace alignment");
-  const int sp = launch_partials(x, ldx, wkv, H, P, N, H, workspace, ws_bytes, stream);
-  if (sp > 1)
-    hipLaunchKernelGGL(k_norm_kv_reduce, reduce_grid(P, N), dim3(256), 0, stream, static_cast<const float*>(workspace),
-                       sp, static_cast<int>(P), static_cast<int>(N), a);
-  else
-    hipLaunchKernelGGL(k_norm_kv, dim3(grid_of(P, N)), dim3(NTHR), 0, stream, x, ldx, wkv, static_cast<int>(P),
+  const Plan pl = plan_with(P, N, H, workspace, ws_bytes);
+  const int64_t mf = pl.m_fused, rows = P - mf;
+  if (mf > 0)
+    hipLaunchKernelGGL(k_norm_kv, dim3(grid_of(mf, N)), dim3(NTHR), 0, stream, x, ldx, wkv, static_cast<int>(mf),
                        static_cast<int>(N), static_cast<int>(H), a);
+  if (pl.splits > 1) {
+    launch_partials(x, ldx, wkv, H, P, N, H, pl, workspace, stream);
+    KvArgs ar = a;                                  // the split rows: statistics, slots and table rows from mf
+    ar.ssq += mf * ar.nparts;
+    ar.slot0 += mf;
+    ar.cs += mf * rot;
+    hipLaunchKernelGGL(k_norm_kv_reduce, reduce_grid(rows, N), dim3(256), 0, stream,
+                       static_cast<const float*>(workspace), pl.splits, static_cast<int>(rows), static_cast<int>(N), ar);
+  }
   return check_launch("rf_norm_kv_write");
 }
 
@@ -813,13 +853,20 @@ extern "C" int rf_norm_q(const uint16_t* x, int64_t ldx, const float* ssq, int64
            q, q, static_cast<int64_t>(d), ldq, 0, pos};
   const int64_t N = static_cast<int64_t>(hq) * d;
   if (workspace && !aligned16(workspace)) return fail(RF_EINVAL_SHAPE, "rf_norm_q: workspace alignment");
-  const int sp = launch_partials(x, ldx, wq, H, rows, N, H, workspace, ws_bytes, stream);
-  if (sp > 1)
-    hipLaunchKernelGGL(k_norm_kv_reduce, reduce_grid(rows, N), dim3(256), 0, stream,
-                       static_cast<const float*>(workspace), sp, static_cast<int>(rows), static_cast<int>(N), a);
-  else
-    hipLaunchKernelGGL(k_norm_kv, dim3(grid_of(rows, N)), dim3(NTHR), 0, stream, x, ldx, wq, static_cast<int>(rows),
+  const Plan pl = plan_with(rows, N, H, workspace, ws_bytes);
+  const int64_t mf = pl.m_fused, rs = rows - mf;
+  if (mf > 0)
+    hipLaunchKernelGGL(k_norm_kv, dim3(grid_of(mf, N)), dim3(NTHR), 0, stream, x, ldx, wq, static_cast<int>(mf),
                        static_cast<int>(N), static_cast<int>(H), a);
+  if (pl.splits > 1) {
+    launch_partials(x, ldx, wq, H, rows, N, H, pl, workspace, stream);
+    KvArgs ar = a;                                  // the split rows: statistics, outputs and positions from mf
+    ar.ssq += mf * ar.nparts;
+    ar.slot0 += mf;
+    ar.pos += mf;
+    hipLaunchKernelGGL(k_norm_kv_reduce, reduce_grid(rs, N), dim3(256), 0, stream,
+                       static_cast<const float*>(workspace), pl.splits, static_cast<int>(rs), static_cast<int>(N), ar);
+  }
   return check_launch("rf_norm_q");
 }
 
@@ -853,13 +900,16 @@ extern "C" int rf_norm_linear(const uint16_t* x, int64_t ldx, const float* ssq, 
   if (!(eps >= 0.f)) return fail(RF_EINVAL_ARG, "rf_norm_linear: eps");
   if (workspace && !aligned16(workspace)) return fail(RF_EINVAL_SHAPE, "rf_norm_linear: workspace alignment");
   if (P == 0) return RF_OK;
-  const int sp = launch_partials(x, ldx, w, H, P, N, H, workspace, ws_bytes, stream);
-  if (sp > 1)
-    hipLaunchKernelGGL(k_norm_linear_reduce, reduce_grid(P, N), dim3(256), 0, stream,
-                       static_cast<const float*>(workspace), sp, ssq, static_cast<int>(H), eps, out, ldo,
-                       static_cast<int>(P), static_cast<int>(N));
-  else
-    hipLaunchKernelGGL(k_norm_linear, dim3(grid_of(P, N)), dim3(NTHR), 0, stream, x, ldx, w, static_cast<int>(P),
+  const Plan pl = plan_with(P, N, H, workspace, ws_bytes);
+  const int64_t mf = pl.m_fused, rows = P - mf;
+  if (mf > 0)
+    hipLaunchKernelGGL(k_norm_linear, dim3(grid_of(mf, N)), dim3(NTHR), 0, stream, x, ldx, w, static_cast<int>(mf),
                        static_cast<int>(N), static_cast<int>(H), ssq, eps, out, ldo);
+  if (pl.splits > 1) {
+    launch_partials(x, ldx, w, H, P, N, H, pl, workspace, stream);
+    hipLaunchKernelGGL(k_norm_linear_reduce, reduce_grid(rows, N), dim3(256), 0, stream,
+                       static_cast<const float*>(workspace), pl.splits, ssq + mf * (H / SSQ_COLS), static_cast<int>(H),
+                       eps, out + mf * ldo, ldo, static_cast<int>(rows), static_cast<int>(N));
+  }
   return check_launch("rf_norm_linear");
 }

@@ -71,10 +71,11 @@ class Projector:
                          {i: c.to(device, torch.bfloat16).contiguous() for i, c in self.b.items()})
         return self._dev[1], self._dev[2]
 
-    def apply(self, i, b, out=None, ssq=None):
-        """(x_i [P, d_out] bf16, its row sum-of-squares partials) for rows b [P, d_in] bf16."""
+    def apply(self, i, b, out=None, ssq=None, workspace=None):
+        """(x_i [P, d_out] bf16, its row sum-of-squares partials) for rows b [P, d_in] bf16. workspace: the
+        GEMM's split-K workspace (ops.map_apply)."""
         W, B = self._maps(b.device)
-        return ops.map_apply(b, W[i], B[i], out, ssq)
+        return ops.map_apply(b, W[i], B[i], out, ssq, workspace=workspace)
 
     def __call__(self, i, b):
         return self.apply(i, b)[0]
@@ -189,7 +190,9 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
 
     def produce(i, slot):
         if arm.fill == "proj":
-            x, ssq = arm.projector.apply(i, b, xbuf[slot], sbuf[slot])
+            W = arm.projector._maps(dev)[0][i]
+            x, ssq = arm.projector.apply(i, b, xbuf[slot], sbuf[slot],
+                                         workspace=model.gemm_workspace(P, W.shape[0], W.shape[1], dev, "produce"))
         elif rows is None:
             x, ssq = b, base_ssq
         else:

@@ -165,7 +165,8 @@ class FillModel:
         c = cache[i]
         slot = self.reserve(c, P, self.n_kv, self.head_dim, x.device)
         ops.norm_kv_write(x, ssq, self.eps, w["wkv"], self.n_kv, self.head_dim, w.get("k_norm"), self.knorm_kind,
-                          cs, c["kbuf"], c["vbuf"], slot)
+                          cs, c["kbuf"], c["vbuf"], slot,
+                          workspace=self.gemm_workspace(P, w["wkv"].shape[0], x.shape[1], x.device))
         self.commit(c, P)
         return {}
 
@@ -201,15 +202,17 @@ class FillModel:
             self._attn_ws = ws = torch.empty(need, dtype=torch.uint8, device=device)
         return ws
 
-    def _gemm_workspace(self, M, N, K, device):
-        """The split-K workspace of an M x N x K product (None when the tiles fill the GPU unsplit), shared
-        by every GEMM of the exact rows' and the tail's layers (stream-ordered reuse)."""
+    def gemm_workspace(self, M, N, K, device, role="consume"):
+        """The split-K workspace of an M x N x K product (None when it runs unsplit): one buffer per role,
+        shared by every GEMM of that role in stream order -- "consume" for the cache fill and the exact
+        rows' and tail's layers, "produce" for the map apply that may run beside them on another stream."""
         need = ops.gemm_workspace_bytes(M, N, K)
         if need == 0:
             return None
-        ws = getattr(self, "_gemm_ws", None)
+        wss = self.__dict__.setdefault("_gemm_ws", {})
+        ws = wss.get(role)
         if ws is None or ws.numel() < need or ws.device != device:
-            self._gemm_ws = ws = torch.empty(need, dtype=torch.uint8, device=device)
+            wss[role] = ws = torch.empty(need, dtype=torch.uint8, device=device)
         return ws
 
     def _gdn_workspace(self, rows, device):
@@ -271,7 +274,7 @@ class FillModel:
         xr, sr = ops.row_gather(x, rows)
         H, R = xr.shape[1], xr.shape[0]
         q = ops.norm_q(xr, sr, self.eps, w["wq"], self.n_heads, self.head_dim, w.get("q_norm"), self.knorm_kind, cs,
-                       rows, workspace=self._gemm_workspace(R, w["wq"].shape[0], H, x.device))
+                       rows, workspace=self.gemm_workspace(R, w["wq"].shape[0], H, x.device))
         qpos = pos.to(x.device, torch.int64)[rows]
         if self._causal_ok():
             o = ops.attend_causal(q, 0, c["kbuf"], c["vbuf"], c["n"], self.n_heads, self.scale, qpos=qpos,
@@ -286,7 +289,7 @@ class FillModel:
         (code/kva/model.py:112-118, :254-257), with the reference's bf16 roundings. Returns the layer
         output [rows, H] bf16 and its row sum-of-squares partials (the next norm's statistics)."""
         R, dev = h.shape[0], h.device
-        gws = self._gemm_workspace
+        gws = self.gemm_workspace
         a, _ = ops.map_apply(o, w["wo"], None, workspace=gws(R, w["wo"].shape[0], w["wo"].shape[1], dev))
         h1, s1 = ops.residual_add(h, a)
         gu = ops.norm_linear(h1, s1, self.eps, w["wgu"], workspace=gws(R, w["wgu"].shape[0], w["wgu"].shape[1], dev))
@@ -317,11 +320,11 @@ class FillModel:
         H = h.shape[1]
         ops.norm_kv_write(h, ssq, self.eps, w["wkv"], self.n_kv, self.head_dim, w.get("k_norm"), self.knorm_kind,
                           cs, c["kbuf"], c["vbuf"], slot,
-                          workspace=self._gemm_workspace(T, w["wkv"].shape[0], H, h.device))
+                          workspace=self.gemm_workspace(T, w["wkv"].shape[0], H, h.device))
         self.commit(c, T)
         idx = torch.arange(T, device=h.device)
         q = ops.norm_q(h, ssq, self.eps, w["wq"], self.n_heads, self.head_dim, w.get("q_norm"), self.knorm_kind, cs,
-                       idx, workspace=self._gemm_workspace(T, w["wq"].shape[0], H, h.device))
+                       idx, workspace=self.gemm_workspace(T, w["wq"].shape[0], H, h.device))
         if self._causal_ok():
             o = ops.attend_causal(q, slot, c["kbuf"], c["vbuf"], c["n"], self.n_heads, self.scale,
                                   workspace=self._causal_workspace(T, c["n"], h.device))
@@ -358,7 +361,7 @@ class FillModel:
         if ssq is None:
             ssq = ops.row_ssq(h)
         return ops.norm_linear(h, ssq, self.eps, head,
-                               workspace=self._gemm_workspace(h.shape[0], head.shape[0], h.shape[1], h.device))[:, :V].float()
+                               workspace=self.gemm_workspace(h.shape[0], head.shape[0], h.shape[1], h.device))[:, :V].float()
 
     def fill_kv(self, i, k, v, pos, cache, cs=None):
         """Cache-only fill from pre-RoPE K and V [P, Hkv, d] (the reads() layout)."""

@@ -51,6 +51,9 @@ def test_gemm_workspace_sizes():
     assert ops.gemm_workspace_bytes(287, 4096, 4096) == 8 * 287 * 4096 * 4       # 32 tiles: 8 splits
     assert ops.gemm_workspace_bytes(287, 24576, 4096) == 0           # 192 tiles
     assert ops.gemm_workspace_bytes(4096, 2048, 4096) == 2 * 4096 * 2048 * 4     # the tail's K / V: 128 tiles
+    # the fill's K / V: 896 tiles = 3 waves + 16 tile rows (128 tiles): those rows split 2 ways
+    assert ops.gemm_workspace_bytes(28672, 2048, 4096) == 2 * 4096 * 2048 * 4
+    assert ops.gemm_workspace_bytes(28672, 1024, 2048) == 0          # 48 of 64 tile rows in the last wave
     assert ops.gemm_workspace_bytes(40, 512, 2048) == 4 * 40 * 512 * 4           # K / 512 = 4 caps the splits
     assert ops.gemm_workspace_bytes(287, 4096, 256) == 0             # too little K to split
     assert ops.gemm_workspace_bytes(0, 4096, 4096) == 0

@@ -113,3 +113,47 @@ def test_norm_kv_write_split_matches_oracle(dev):
     print(f"norm_kv_write split: K {ek:.2e} V {ev:.2e} vs oracle; vs unsplit K {rel_err(kb, ku):.2e}")
     assert ek < TOL and ev < TOL and rel_err(kb, ku) < TOL
     assert bool((kb[:, :3] == 5.0).all() and (kb[:, 3 + P:] == 5.0).all() and (vb[:, 3 + P:] == 5.0).all())
+
+
+def test_last_wave_split(dev):
+    """A product whose last wave of tile rows is at most half full (10240 rows x 2048: 40 tile rows of
+    8 tiles, 32 per wave) runs rows [0, 8192) fused and rows [8192, 10240) split in K: map apply and
+    the fused norm + K / V + RoPE write against their unsplit runs and the oracle, the rows' statistics
+    bitwise those of the rounded x, the cache slots exact."""
+    from fill_cases import attn_config, random_tensors
+    from rfill import ops
+    from rfill.model import FillModel
+    P, H = 10240, 2048
+    assert ops.gemm_workspace_bytes(P, 2048, H) == 4 * 2048 * 2048 * 4       # 4 splits of the last 2048 rows
+    g = torch.Generator().manual_seed(7)
+    b = inputs(P, H, seed=8).to(dev)
+    w = (torch.eye(H) + 0.02 * torch.randn(H, H, generator=g) / H ** 0.5).to(torch.bfloat16).to(dev)
+    c = (1e-3 * torch.randn(H, generator=g)).to(torch.bfloat16).to(dev)
+    xs, ss = ops.map_apply(b, w, c, workspace="auto")
+    xu, su = ops.map_apply(b, w, c)
+    torch.cuda.synchronize()
+    assert torch.equal(xs[:8192], xu[:8192]) and torch.equal(ss[:8192], su[:8192])     # the fused rows
+    assert rel_err(xs, xu) < TOL and torch.equal(ops.row_ssq(xs), ss)
+    cfg = attn_config("llama", H, 8, 128, 5e5)                  # K and V: 2 x 8 heads x 128 = 2048 columns
+    t = random_tensors(cfg, seed=9)
+    m = FillModel(cfg, t, dev)
+    x = xu.cpu()
+    pos = torch.arange(P)
+    c0 = m.new_cache()
+    m.fill(0, xu, pos.to(dev), c0)                               # FillModel.fill passes the workspace
+    wk = m.W[0]
+    kb = torch.empty(8, P + 64, 128, dtype=torch.bfloat16, device=dev)
+    vb = torch.empty_like(kb)
+    ops.norm_kv_write(xu, su, m.eps, wk["wkv"], 8, 128, None, 0, m.rope_table(pos.to(dev)), kb, vb, 0)
+    torch.cuda.synchronize()
+    om = OM.OracleModel(cfg, t, dtype=torch.bfloat16)
+    oc = om.new_cache()
+    om.fill(0, x, pos, oc)
+    ek, ev = rel_err(c0[0]["k"], oc[0]["k"]), rel_err(c0[0]["v"], oc[0]["v"])
+    ek_tail = rel_err(c0[0]["k"][:, 8192:], oc[0]["k"][:, 8192:])
+    print(f"last-wave split: map x vs unsplit {rel_err(xs, xu):.2e}; K {ek:.2e} V {ev:.2e} (split rows K {ek_tail:.2e}) "
+          f"vs oracle; vs unsplit K {rel_err(c0[0]['k'], kb[:, :P]):.2e}")
+    assert ek < TOL and ev < TOL and ek_tail < TOL
+    assert torch.equal(c0[0]["k"][:, :8192], kb[:, :8192])      # the fused rows: the same kernel, the same bits
+    assert rel_err(c0[0]["k"], kb[:, :P]) < TOL and rel_err(c0[0]["v"], vb[:, :P]) < TOL
+    assert c0[0]["n"] == P
