@@ -35,7 +35,7 @@ int rf_version(void);
  * b [P, h_in] (row stride ldb), w [h_out, h_in] (F.linear layout), c [h_out] or NULL,
  * x [P, h_out] (row stride ldx). Also writes ssq [P, h_out / 256]: each row's sum of squares of the
  * rounded x over consecutive 256-column groups (the next layer's RMSNorm statistics).
- * Needs h_in % 32 == 0, h_out % 256 == 0, ldb / ldx multiples of 8, 16-byte aligned pointers.
+ * Needs h_in % 64 == 0, h_out % 256 == 0, ldb / ldx multiples of 8, 16-byte aligned pointers.
  * workspace / ws_bytes (optional, NULL / 0): see rf_gemm_workspace_bytes. */
 int rf_map_apply(const uint16_t* b, int64_t ldb, const uint16_t* w, const uint16_t* c,
                  uint16_t* x, int64_t ldx, float* ssq, int64_t P, int64_t h_in, int64_t h_out,
@@ -43,7 +43,9 @@ int rf_map_apply(const uint16_t* b, int64_t ldb, const uint16_t* w, const uint16
 
 /* Bytes of the optional workspace of the GEMM entry points (rf_map_apply, rf_norm_kv_write, rf_norm_q,
  * rf_norm_linear) for an M x N x K product (M rows, N outputs, K inputs): nonzero when the output tiles
- * (256 x 256) are too few to give every CU one, e.g. the exact rows' or the tail's projections. Given a
+ * (256 x 256) are too few to give every CU one, e.g. the exact rows' or the tail's projections, or when
+ * the last wave of whole tile rows is at most half full (then only those rows split; the rest run as
+ * usual), e.g. the 32K-row K/V product of an 8B model (896 tiles: 768 + 128 split two ways). Given a
  * workspace at least this large (caller-owned device memory, 16-byte aligned), the entry point splits K
  * over more blocks, keeps their fp32 partial sums there and adds them in a fixed order before the
  * epilogue (the same bits every run; the unsplit sum order differs within fp32 rounding). With a

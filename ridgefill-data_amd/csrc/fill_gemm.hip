@@ -3,14 +3,13 @@
 //   rf_norm_kv_write  [K | V] = rms_norm(x) W_kv^T with the norm gain folded into W_kv, per-head
 //                     k_norm, RoPE on K, written straight into the [hkv, cap, d] cache slots.
 //
-// Tiling. A workgroup of 4 wave64s computes a 256 x 256 output tile over K in 32-wide steps. Both
-// operands are K-contiguous (row-major activations, F.linear-layout weights), so each 32-wide K slice
-// of a 256-row operand tile is 256 rows x 64 bytes. The slices go from memory straight into LDS
-// (buffer_load_dwordx4 ... lds, no staging registers; the buffer's range check turns rows past M into
-// zeros) with the 16-byte chunk index XOR-ed by (row >> 2) & 3, so the MFMA fragment reads (32 rows,
-// one chunk per lane) hit all banks. Five LDS slots (5 x 32 KiB, the whole LDS): loads run 2 to 3.5
-// steps ahead of the MFMAs, issued as pairs that cover both halves of each 128-byte line; one wait and
-// one barrier per step.
+// Tiling. A workgroup of 4 wave64s computes a 256 x 256 output tile over K in 64-deep steps. Both
+// operands are K-contiguous (row-major activations, F.linear-layout weights), so each 64-deep K slice
+// of a 128-row operand half is 128 rows of one full 128-byte cache line each. The slices go from memory
+// straight into LDS (buffer_load_dwordx4 ... lds, no staging registers; the buffer's range check turns
+// rows past M into zeros), one instruction per 8 full lines, with the 16-byte chunk index XOR-ed by
+// (row >> 1) & 7 so the MFMA fragment reads hit all banks. A ring of ten 16 KiB slots (the whole LDS)
+// holds 2.5 steps; one wait and one barrier per step.
 //
 // Each wave owns a 128 x 128 quarter and issues v_mfma_f32_32x32x16_bf16 on 4 x 4 sub-tiles. The
 // weight tile is the MFMA's A operand and the activation tile its B operand, so the accumulator of a
@@ -29,15 +28,14 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int BM = 256, BN = 256, BK = 32, NTHR = 256;
-constexpr int STAGES = 5;                      // LDS slots, one 32-deep K step each
-constexpr int CPR = BK / 8;                    // 16-byte chunks per operand row in a slot
-constexpr int STAGE_U4 = (BM + BN) * CPR;      // 16-byte chunks per slot (activations, then weights)
-constexpr int LDS_U4 = STAGES * STAGE_U4;      // 160 KiB, the whole LDS of a CU
+constexpr int BM = 256, BN = 256, BK = 64, NTHR = 256;
+constexpr int CPR = BK / 8;                    // 16-byte chunks per 128-byte operand row of a slot
+constexpr int SLOT_ROWS = 128;                 // a slot: 128 rows of one operand over one 64-deep K step
+constexpr int SLOT_U4 = SLOT_ROWS * CPR;       // 16 KiB
+constexpr int NSLOT = 10;                      // slots in the ring: 2.5 K steps
+constexpr int LDS_U4 = NSLOT * SLOT_U4;        // 160 KiB, the whole LDS of a CU
 constexpr int IMAGE_U4 = 256 * 32;             // the epilogue's 256 x 256 bf16 image (128 KiB)
-constexpr int LOADS_PER_STEP = (BM + BN) * CPR / 64 / 4;   // direct-load instructions per wave per K step
 static_assert(LDS_U4 >= IMAGE_U4 + 2048, "the epilogue's image and its 32 KiB of side data must fit");
-static_assert(STAGES == 5 && LOADS_PER_STEP == 8, "the load schedule assumes 8 loads per step and 5 slots");
 
 __device__ __forceinline__ bf16x8 as_frag(const uint4& u) { return __builtin_bit_cast(bf16x8, u); }
 
@@ -60,10 +58,11 @@ __device__ __forceinline__ void tile_coords(int tile, int tiles_m, int tiles_n, 
   tn = in / rows;
 }
 
-// LDS slot of (row, 16-byte chunk) in a 32-wide K slice: 4 chunks (64 bytes) per row, the chunk
-// XOR-ed with (row >> 2) & 3. A fragment read takes one chunk of 32 consecutive rows; the LDS serves
-// 16 lanes of 16 bytes per cycle, and any 16 consecutive rows then fall on distinct banks.
-__device__ __forceinline__ int row_swz(int row) { return (row >> 2) & 3; }
+// Chunk swizzle of a slot: row r's 16-byte chunk c (of 8) lives at r * 8 + (c ^ slot_swz(r)). A fragment
+// read takes one chunk of 32 consecutive rows; the LDS serves 16 lanes of 16 bytes per cycle, and rows
+// r .. r + 15 then cover all 16 bank groups (row parity picks the half of the 256-byte bank line, the
+// swizzle the chunk within it).
+__device__ __forceinline__ int slot_swz(int row) { return (row >> 1) & 7; }
 
 typedef __attribute__((address_space(3))) void* lds_ptr;
 
@@ -80,56 +79,55 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (0 << 8) | ((n >> 4) << 14));
 }
 
-// Load j (0..7) of one K step's operand tiles, straight from memory into an LDS stage
-// (buffer_load_dwordx4 ... lds): even j fill activation rows, odd j weight rows. Each instruction fills
-// 64 consecutive 16-byte slots, lane L writing slot base + L, i.e. 16 rows x 4 chunks. Slot s of a
-// 256-row tile holds row s / 4, chunk (s % 4) ^ row_swz(row); for wave w's load j that is row
-// w*64 + (j/2)*16 + L/4 and chunk (L % 4) ^ ((L / 16) % 4), so each lane fetches the global address
-// that belongs in its slot.
-__device__ __forceinline__ void issue_one(__amdgpu_buffer_rsrc_t rx, __amdgpu_buffer_rsrc_t rw, const uint32_t (&vx)[4],
-                                          const uint32_t (&vw)[4], int j, int k0, char* stage, int w) {
-  const int jj = j >> 1, slot0 = w * 256 + jj * 64;
-  if (j & 1)
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, (lds_ptr)(stage + BM * CPR * 16 + slot0 * 16), 16, vw[jj], k0 * 2, 0, 0);
-  else
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(stage + slot0 * 16), 16, vx[jj], k0 * 2, 0, 0);
+// Slot of quarter q of K step kt: quarters 0, 1 are activation rows 0-127 / 128-255, quarters 2, 3
+// weight rows 0-127 / 128-255.
+__device__ __forceinline__ int slot_of(int kt, int q) { return (4 * kt + q) % NSLOT; }
+
+// Load i (0..3) of this wave for quarter q of step kt, straight from memory into its slot
+// (buffer_load_dwordx4 ... lds): 8 rows x 128 bytes, full cache lines. Lane L writes slot chunk
+// (32w + 8i) * 8 + L, i.e. row 32w + 8i + L / 8, physical chunk L % 8, and so fetches logical chunk
+// (L % 8) ^ slot_swz(row) of that row; `voff` holds the lane's byte offset of that (row, chunk), the
+// step's K offset goes in the scalar offset.
+__device__ __forceinline__ void issue_load(__amdgpu_buffer_rsrc_t rs, uint32_t voff, int kt, int q, int i, char* lds,
+                                           int w) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(
+      rs, (lds_ptr)(lds + slot_of(kt, q) * (SLOT_U4 * 16) + (32 * w + 8 * i) * (CPR * 16)), 16, voff, kt * BK * 2, 0, 0);
 }
 
-// acc[nt][mt] += W[n0 + wn*128 + nt*32 .. +32, :] . X[m0 + wm*128 + mt*32 .. +32, :]^T over all of K.
-// Rows of X at or past M read as zeros. Ends with a barrier: LDS is free for the epilogue.
+// acc[nt][mt] += W[n0 + wn*128 + nt*32 .. +32, :] . X[m0 + wm*128 + mt*32 .. +32, :]^T over all of K
+// (K % 64 == 0). Rows of X at or past M read as zeros. Ends with a barrier: LDS is free for the epilogue.
 //
-// Pipeline. Step k's tiles (32 deep) land in slot k % 5. Loads go in batches of two steps (k, k + 1)
-// issued as pairs: load j of step k, then load j of step k + 1, back to back -- the two 64-byte halves
-// of the same 128-byte lines, which the memory path serves at full-line rate (a lone half-line load
-// runs at half of it). A step is two 16-wide K slices of 16 MFMAs each. The wave's instruction stream
-// is in order, so anything issued in a burst stalls the MFMA pipe; instead one LDS fragment read for
-// the next slice follows each of a slice's first 8 MFMAs, and one load pair follows every second of
-// its last 8. Between the slices the wave waits for step k + 1's loads (vmcnt) and its own LDS reads
-// (lgkmcnt 0) and meets the other waves at a barrier; after it, slot k % 5 is free.
-//
-// Schedule: even step k issues the first half of the batch for steps (k + 4, k + 5) in its second
-// slice, into slots (k - 1) % 5 and k % 5 (free since step k - 1's barrier and this step's barrier);
-// odd step k + 1 issues the batch's second half in its first slice. At step k's barrier the loads
-// still allowed in flight are the batch started at k - 2 (16) for even k, and that batch plus the last
-// load of the batch holding step k + 1 (17) for odd k. A step's loads are thus issued 2 to 3.5 steps
-// before their slot is read.
+// Pipeline. K goes in 64-deep steps. A step's operands are four 16 KiB quarters (activation rows 0-127 and
+// 128-255, weight rows 0-127 and 128-255), each 128 rows of full 128-byte lines; the ring holds ten
+// quarters (2.5 steps, the whole LDS). Wave (wm, wn) reads activation quarter wm and weight quarter wn. A
+// step is four 16-deep slices of 16 MFMAs; the fragments of slice j + 1 are read during slice j, one LDS
+// read after each of its first 8 MFMAs. One wait and one barrier per step, between slices 2 and 3: by
+// then every wave has read all of the step's fragments (its quarters are free) and step kt + 1 has
+// landed. Loads for step kt + 2: its activation quarters during slices 0 and 1 of step kt (into the
+// slots step kt - 1's weights left), its weight quarters during slice 3 (into the slots step kt's
+// activations just left). So each barrier waits with 8 loads per wave still in flight, and the last
+// loads of a step are issued four slices (64 MFMAs) before the barrier that needs them.
 __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t ldx,
                                          const uint16_t* __restrict__ W, int64_t ldw, int M, int K,
                                          int m0, int n0, uint4* lds, f32x16 (&acc)[4][4]) {
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);      // wave-uniform: slot arithmetic stays scalar
   const int wm = w >> 1, wn = w & 1;
   const int rows_x = min(M - m0, BM);
   const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(X + static_cast<int64_t>(m0) * ldx,
                                                 static_cast<uint32_t>(rows_x * ldx * 2));
   const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(W + static_cast<int64_t>(n0) * ldw, static_cast<uint32_t>(BN * ldw * 2));
-  uint32_t vx[4], vw[4];
+  // per-lane byte offsets of load i of half h: row h*128 + 32w + 8i + lane/8, chunk (lane%8) ^ slot_swz(row)
+  uint32_t vx[2][4], vw[2][4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int row = w * 64 + j * 16 + (lane >> 2);
-    const int ch = (lane & 3) ^ row_swz(row);
-    vx[j] = static_cast<uint32_t>((row * ldx + ch * 8) * 2);
-    vw[j] = static_cast<uint32_t>((row * ldw + ch * 8) * 2);
-  }
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 32 * w + 8 * i + (lane >> 3);
+      const int ch = (lane & 7) ^ slot_swz(r);
+      vx[h][i] = static_cast<uint32_t>(((h * 128 + r) * ldx + ch * 8) * 2);
+      vw[h][i] = static_cast<uint32_t>(((h * 128 + r) * ldw + ch * 8) * 2);
+    }
 
 #pragma unroll
   for (int a = 0; a < 4; ++a)
@@ -140,65 +138,65 @@ __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t
 
   char* base = reinterpret_cast<char*>(lds);
   const int nk = K / BK;
-  const int lr = lane & 31, lk = lane >> 5, swz = row_swz(lr);
+  const int lr = lane & 31, lk = lane >> 5, swz = slot_swz(lr);
   bf16x8 fx[2][4], fw[2][4];
-  // fragment r (0..7) of slice ks from slot st: r < 4 -> weight block r, else activation block r - 4
-  auto read_one = [&](int st, int ks, int r, bf16x8 (&ax)[4], bf16x8 (&aw)[4]) {
-    const uint4* sx = lds + st * STAGE_U4;
-    const uint4* sw = sx + BM * CPR;
-    const int slot = (ks * 2 + lk) ^ swz;
-    if (r < 4) aw[r] = as_frag(sw[(wn * 128 + r * 32 + lr) * CPR + slot]);
-    else ax[r - 4] = as_frag(sx[(wm * 128 + (r - 4) * 32 + lr) * CPR + slot]);
+  // fragment r (0..7) of slice ks of step kt: r < 4 -> weight block r, else activation block r - 4
+  auto read_one = [&](int kt, int ks, int r, bf16x8 (&ax)[4], bf16x8 (&aw)[4]) {
+    const int ch = (ks * 2 + lk) ^ swz;
+    if (r < 4) aw[r] = as_frag(lds[slot_of(kt, 2 + wn) * SLOT_U4 + (r * 32 + lr) * CPR + ch]);
+    else ax[r - 4] = as_frag(lds[slot_of(kt, wm) * SLOT_U4 + ((r - 4) * 32 + lr) * CPR + ch]);
   };
-  // pair j of the batch for steps (kb, kb + 1); `checked` drops steps at or past the end of K
-  auto issue_pair = [&](int j, int kb, bool checked) {
-    if (!checked || kb < nk) issue_one(rx, rw, vx, vw, j, kb * BK, base + (kb % STAGES) * STAGE_U4 * 16, w);
-    if (!checked || kb + 1 < nk)
-      issue_one(rx, rw, vx, vw, j, (kb + 1) * BK, base + ((kb + 1) % STAGES) * STAGE_U4 * 16, w);
+  // load j (0..7) of step kt's activation (wt = false) or weight (wt = true) quarters
+  auto load = [&](int kt, bool wt, int j) {
+    const int h = j >> 2, i = j & 3;
+    if (wt) issue_load(rw, vw[h][i], kt, 2 + h, i, base, w);
+    else issue_load(rx, vx[h][i], kt, h, i, base, w);
   };
-  auto slice = [&](const bf16x8 (&ax)[4], const bf16x8 (&aw)[4], bool do_read, int rst, int rks, bf16x8 (&nx)[4],
-                   bf16x8 (&nw)[4], bool do_load, int j0, int kb, bool checked) {
+  // one slice: 16 MFMAs on (ax, aw); reads of the next slice's fragments after the first 8 (`rd`);
+  // `ld` 0: no loads, 1: activation loads (lo .. lo + 3) of step lk_step after MFMAs 9, 11, 13, 15,
+  // 2: all 8 weight loads of step lk_step, one after each of the first 8 MFMAs
+  auto slice = [&](const bf16x8 (&ax)[4], const bf16x8 (&aw)[4], bool rd, int rkt, int rks, bf16x8 (&nx)[4],
+                   bf16x8 (&nw)[4], int ld, int lkt, int lo) {
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
       acc[q >> 2][q & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aw[q >> 2], ax[q & 3], acc[q >> 2][q & 3], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
       if (q < 8) {
-        if (do_read) read_one(rst, rks, q, nx, nw);
-      } else if (do_load && (q & 1)) {
-        issue_pair(j0 + ((q - 9) >> 1), kb, checked);
+        if (rd) read_one(rkt, rks, q, nx, nw);
+        if (ld == 2) load(lkt, true, q);
+      } else if (ld == 1 && (q & 1)) {
+        load(lkt, false, lo + ((q - 9) >> 1));
       }
       __builtin_amdgcn_sched_barrier(0);
     }
   };
-  // `steady` (compile-time) marks steps whose batches lie inside K: no bounds checks, exact vmcnt
-  // waits from the schedule above; `odd` (compile-time in the steady loop) is the step's parity.
-  auto step = [&](int kt, auto steady, bool odd) {
-    const int s = kt % STAGES;
-    slice(fx[0], fw[0], true, s, 1, fx[1], fw[1], odd, 4, kt + 3, !steady);
-    if (steady) {
-      if (odd) wait_vm_lgkm0<2 * LOADS_PER_STEP + 1>();
-      else wait_vm_lgkm0<2 * LOADS_PER_STEP>();
-    } else {
-      wait_vm_lgkm0<0>();
-    }
+  // `steady` (compile-time): step kt + 2 exists, so its loads are issued and the wait is exact
+  auto step = [&](int kt, auto steady) {
+    slice(fx[0], fw[0], true, kt, 1, fx[1], fw[1], steady ? 1 : 0, kt + 2, 0);
+    slice(fx[1], fw[1], true, kt, 2, fx[0], fw[0], steady ? 1 : 0, kt + 2, 4);
+    slice(fx[0], fw[0], true, kt, 3, fx[1], fw[1], 0, 0, 0);
+    if (steady) wait_vm_lgkm0<8>();
+    else wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    slice(fx[1], fw[1], steady || kt + 1 < nk, (kt + 1) % STAGES, 0, fx[0], fw[0], !odd, 0, kt + 4, !steady);
+    slice(fx[1], fw[1], steady || kt + 1 < nk, kt + 1, 0, fx[0], fw[0], steady ? 2 : 0, kt + 2, 0);
   };
 
-  // prologue: the batches for steps (0, 1) and (2, 3), then step 0's first fragments
-  for (int j = 0; j < LOADS_PER_STEP; ++j) issue_pair(j, 0, true);
-  for (int j = 0; j < LOADS_PER_STEP; ++j) issue_pair(j, 2, true);
-  if (nk >= 4) wait_vm_lgkm0<2 * LOADS_PER_STEP + 1>();
-  else wait_vm_lgkm0<0>();
+  // prologue: steps 0 and 1, then step 0's first fragments
+  for (int j = 0; j < 8; ++j) load(0, false, j);
+  for (int j = 0; j < 8; ++j) load(0, true, j);
+  if (nk > 1) {
+    for (int j = 0; j < 8; ++j) load(1, false, j);
+    for (int j = 0; j < 8; ++j) load(1, true, j);
+    wait_vm_lgkm0<16>();
+  } else {
+    wait_vm_lgkm0<0>();
+  }
   __builtin_amdgcn_s_barrier();
   for (int r = 0; r < 8; ++r) read_one(0, 0, r, fx[0], fw[0]);
   int kt = 0;
-  for (; kt + 5 < nk; kt += 2) {
-    step(kt, std::true_type{}, false);
-    step(kt + 1, std::true_type{}, true);
-  }
-  for (; kt < nk; ++kt) step(kt, std::false_type{}, (kt & 1) != 0);
+  for (; kt + 2 < nk; ++kt) step(kt, std::true_type{});
+  for (; kt < nk; ++kt) step(kt, std::false_type{});
   wait_vm_lgkm0<0>();
   __syncthreads();
 }
@@ -746,7 +744,7 @@ using namespace rf;
 
 extern "C" int rf_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, size_t* bytes) {
   if (!bytes || M < 0 || N <= 0 || N % BN || K <= 0 || K % BK)
-    return fail(RF_EINVAL_ARG, "rf_gemm_workspace_bytes: M %lld, N %lld (multiple of 256), K %lld (multiple of 32)",
+    return fail(RF_EINVAL_ARG, "rf_gemm_workspace_bytes: M %lld, N %lld (multiple of 256), K %lld (multiple of 64)",
                 (long long)M, (long long)N, (long long)K);
   *bytes = M ? split_bytes(M, N, K) : 0;
   return RF_OK;
