@@ -153,20 +153,18 @@ __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t
     else issue_load(rx, vx[h][i], kt, h, i, base, w);
   };
   // one slice: 16 MFMAs on (ax, aw); reads of the next slice's fragments after the first 8 (`rd`);
-  // `ld` 0: no loads, 1: activation loads (lo .. lo + 3) of step lk_step after MFMAs 9, 11, 13, 15,
-  // 2: all 8 weight loads of step lk_step, one after each of the first 8 MFMAs
+  // `ld` 0: no loads, 1: activation loads lo .. lo + 3 of step lkt after MFMAs 1, 5, 9, 13,
+  // 2: all 8 weight loads of step lkt, one after every even MFMA. Spreading the loads keeps the
+  // texture units' queues from filling, which would stall the wave's in-order issue of MFMAs.
   auto slice = [&](const bf16x8 (&ax)[4], const bf16x8 (&aw)[4], bool rd, int rkt, int rks, bf16x8 (&nx)[4],
                    bf16x8 (&nw)[4], int ld, int lkt, int lo) {
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
       acc[q >> 2][q & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aw[q >> 2], ax[q & 3], acc[q >> 2][q & 3], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
-      if (q < 8) {
-        if (rd) read_one(rkt, rks, q, nx, nw);
-        if (ld == 2) load(lkt, true, q);
-      } else if (ld == 1 && (q & 1)) {
-        load(lkt, false, lo + ((q - 9) >> 1));
-      }
+      if (q < 8 && rd) read_one(rkt, rks, q, nx, nw);
+      if (ld == 2 && !(q & 1)) load(lkt, true, q >> 1);
+      if (ld == 1 && (q & 3) == 1) load(lkt, false, lo + (q >> 2));
       __builtin_amdgcn_sched_barrier(0);
     }
   };
