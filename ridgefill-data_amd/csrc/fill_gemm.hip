@@ -425,12 +425,50 @@ struct KvLane {
   }
 };
 
+// The RoPE table entries one K chunk of row gm needs: 8 cos and 8 sin values (rot / 2 >= 8), or the
+// row's whole 8-entry table (rot == 8). Zeros for chunks without RoPE.
+struct RopeEnt {
+  uint4 c, s;
+};
+__device__ __forceinline__ RopeEnt rope_fetch(const KvArgs& a, const KvLane& L, int64_t gm, bool ok) {
+  RopeEnt r{make_uint4(0u, 0u, 0u, 0u), make_uint4(0u, 0u, 0u, 0u)};
+  if (ok && L.rope) {
+    const uint16_t* cs = a.cs + (a.pos ? a.pos[gm] : gm) * a.rot;
+    if (L.half >= 8) {
+      r.c = *reinterpret_cast<const uint4*>(cs + L.fi0);
+      r.s = *reinterpret_cast<const uint4*>(cs + L.half + L.fi0);
+    } else {
+      r.c = *reinterpret_cast<const uint4*>(cs);
+    }
+  }
+  return r;
+}
+
+// The same for rows indexed by slot (no position array), without branches: every lane loads, rows past
+// M read row M - 1, chunks without RoPE read entry 0 (their values are not used). Straight-line loads
+// keep the compiler's wait counts exact, so loads issued rows ahead overlap the rows before them.
+__device__ __forceinline__ RopeEnt rope_fetch_ahead(const KvArgs& a, const KvLane& L, int64_t gm, int M) {
+  const int64_t g = gm < M ? gm : M - 1;
+  const uint16_t* cs = a.cs + g * a.rot;
+  const int fi = L.rope ? L.fi0 : 0;
+  RopeEnt r;
+  if (L.half >= 8) {                              // uniform (a kernel argument)
+    r.c = *reinterpret_cast<const uint4*>(cs + fi);
+    r.s = *reinterpret_cast<const uint4*>(cs + L.half + fi);
+  } else {
+    r.c = *reinterpret_cast<const uint4*>(cs);
+    r.s = make_uint4(0u, 0u, 0u, 0u);
+  }
+  return r;
+}
+
 // One row's chunk of the K / V epilogue: get(c) returns the row's normed bf16 chunk c (of the tile
 // column); per-head sum of squares for k_norm over the head's chunks (lanes of one 32-lane row group,
-// all of which call this, ok or not), then k_norm, RoPE at the row's table entry and a streaming store
-// into slot slot0 + gm.
+// all of which call this, ok or not), then k_norm, RoPE with the row's table entries `re`
+// (rope_fetch) and a streaming store into slot slot0 + gm.
 template <class Get>
-__device__ __forceinline__ void kv_chunk_row(const KvArgs& a, const KvLane& L, Get get, int ch, int64_t gm, bool ok) {
+__device__ __forceinline__ void kv_chunk_row(const KvArgs& a, const KvLane& L, Get get, int ch, int64_t gm, bool ok,
+                                             const RopeEnt& re) {
   const uint4 v = get(ch);
   float ss = 0.f;
   if (a.knorm) {                                   // per-head sum of squares; uniform branch
@@ -463,21 +501,18 @@ __device__ __forceinline__ void kv_chunk_row(const KvArgs& a, const KvLane& L, G
 #pragma unroll
       for (int e = 0; e < 8; ++e) pf[e] = f[e ^ 4];
     }
-    const uint16_t* cs = a.cs + (a.pos ? a.pos[gm] : gm) * rot;
     float c[8], sn[8];
     if (half >= 8) {                              // 8 consecutive table entries of each half
-      const uint4 cv = *reinterpret_cast<const uint4*>(cs + L.fi0);
-      const uint4 sv = *reinterpret_cast<const uint4*>(cs + half + L.fi0);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        c[e] = bf2f(lane_of(cv, e));
-        sn[e] = bf2f(lane_of(sv, e));
+        c[e] = bf2f(lane_of(re.c, e));
+        sn[e] = bf2f(lane_of(re.s, e));
       }
     } else {                                      // rot == 8: entries 0..3 serve both halves of the chunk
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        c[e] = bf2f(cs[e & 3]);
-        sn[e] = bf2f(cs[4 + (e & 3)]);
+        c[e] = bf2f(lane_of(re.c, e & 3));
+        sn[e] = bf2f(lane_of(re.c, 4 + (e & 3)));
       }
     }
     // x cos + rotate_half(x) sin with each product rounded to bf16, then the sum (ops.py:66-77)
@@ -516,12 +551,32 @@ __global__ __launch_bounds__(NTHR) void k_norm_kv(const uint16_t* __restrict__ X
   stage_tile<false>(lds, acc, [&](int mt, int, int, int, float v) { return v * rs[mt]; }, unused);
   __syncthreads();
 
+  // row pass: rows it * 8 + t / 32
   const int t = threadIdx.x, ch = t & 31;
   const KvLane L(a, n0, ch);
-  for (int it = 0; it < BM / 8; ++it) {
-    const int row = it * 8 + (t >> 5);
-    const int gm = m0 + row;
-    kv_chunk_row(a, L, [&](int c) { return image_chunk(lds, row, c); }, ch, gm, gm < M);
+  if (n0 < a.hkv * a.d && !a.pos) {
+    // K columns: the RoPE table entries are fetched AHEAD rows (of this thread) before their use; the
+    // pass is otherwise bound by the latency of these loads
+    constexpr int AHEAD = 8;
+    RopeEnt re[AHEAD];
+#pragma unroll
+    for (int u = 0; u < AHEAD; ++u) re[u] = rope_fetch_ahead(a, L, m0 + u * 8 + (t >> 5), M);
+    for (int it0 = 0; it0 < BM / 8; it0 += AHEAD) {
+#pragma unroll
+      for (int u = 0; u < AHEAD; ++u) {
+        const int row = (it0 + u) * 8 + (t >> 5);
+        const int gm = m0 + row;
+        const RopeEnt cur = re[u];
+        if (it0 + AHEAD < BM / 8) re[u] = rope_fetch_ahead(a, L, gm + AHEAD * 8, M);
+        kv_chunk_row(a, L, [&](int c) { return image_chunk(lds, row, c); }, ch, gm, gm < M, cur);
+      }
+    }
+  } else {
+    for (int it = 0; it < BM / 8; ++it) {
+      const int row = it * 8 + (t >> 5);
+      const int gm = m0 + row;
+      kv_chunk_row(a, L, [&](int c) { return image_chunk(lds, row, c); }, ch, gm, gm < M, rope_fetch(a, L, gm, gm < M));
+    }
   }
 }
 
@@ -635,7 +690,7 @@ __global__ __launch_bounds__(256) void k_norm_kv_reduce(const float* __restrict_
   img[r * 32 + (ch ^ r)] = o;
   __syncthreads();
   const KvLane L(a, n0, ch);
-  kv_chunk_row(a, L, [&](int c) { return image_chunk(img, r, c); }, ch, m, m < M);
+  kv_chunk_row(a, L, [&](int c) { return image_chunk(img, r, c); }, ch, m, m < M, rope_fetch(a, L, m, m < M));
 }
 
 // C[m, n] += sum_k A[m, k] B[n, k] in fp32 for this launch, added into the fp64 accumulator C. Each
