@@ -462,70 +462,149 @@ __device__ __forceinline__ RopeEnt rope_fetch_ahead(const KvArgs& a, const KvLan
   return r;
 }
 
+// The K epilogue's configuration: KV_ANY reads it from the arguments at run time; KV_D128 (no k_norm)
+// and KV_D128_KNORM (Llama-style k_norm) fix d = 128 and full rotary (rot = d) at compile time, so the
+// 8B-class fill's row pass has no branches on uniform values (each costs a pipeline refetch per chunk).
+enum KvMode { KV_ANY = 0, KV_D128 = 1, KV_D128_KNORM = 2 };
+
+// k_norm and RoPE of one K chunk v of a row: `ss` the head's sum of squares (for k_norm), pv the chunk
+// holding v's rotate_half partners (rot / 2 >= 8), `re` the row's table entries. Lanes without RoPE
+// (partial rotary) get the normed chunk unrotated, by select: no divergent branches, so the callers'
+// loads and stores keep exact wait counts.
+template <int MODE = KV_ANY>
+__device__ __forceinline__ uint4 k_chunk(const KvArgs& a, const KvLane& L, const uint4& v, const uint4& pv, float ss,
+                                         const RopeEnt& re) {
+  const bool knorm = MODE == KV_ANY ? a.knorm != nullptr : MODE == KV_D128_KNORM;
+  const int kind = MODE == KV_ANY ? a.knorm_kind : 0;
+  const int j0 = L.j0, half = MODE == KV_ANY ? L.half : 64;
+  const float dd = MODE == KV_ANY ? static_cast<float>(a.d) : 128.f;
+  float f[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = bf2f(lane_of(v, e));
+  float rinv = 0.f;
+  if (knorm) {
+    rinv = 1.0f / sqrtf(ss / dd + a.eps);
+    knorm_chunk(f, rinv, L.kn, kind);
+  }
+  // rotate_half partner values of this chunk, negated for the first half of the rotated dims: a chunk
+  // lies wholly in one half (rot / 2 is a multiple of 8), so the sign is the chunk's (or, for rot == 8,
+  // element e's: e < 4)
+  float pf[8];
+  if (half >= 8) {
+    const uint32_t sg = j0 < half ? 0x80008000u : 0u;   // bf16 sign bits (k_norm is odd in its input)
+    const uint4 pn = make_uint4(pv.x ^ sg, pv.y ^ sg, pv.z ^ sg, pv.w ^ sg);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pf[e] = bf2f(lane_of(pn, e));
+    if (knorm) knorm_chunk(pf, rinv, L.kn_p, kind);
+  } else {                                        // half == 4: the partner is in the same chunk
+#pragma unroll
+    for (int e = 0; e < 8; ++e) pf[e] = e < 4 ? -f[e ^ 4] : f[e ^ 4];
+  }
+  float c[8], sn[8];
+  if (half >= 8) {                                // 8 consecutive table entries of each half
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      c[e] = bf2f(lane_of(re.c, e));
+      sn[e] = bf2f(lane_of(re.s, e));
+    }
+  } else {                                        // rot == 8: entries 0..3 serve both halves of the chunk
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      c[e] = bf2f(lane_of(re.c, e & 3));
+      sn[e] = bf2f(lane_of(re.c, 4 + (e & 3)));
+    }
+  }
+  // x cos + rotate_half(x) sin with each product rounded to bf16, then the sum (ops.py:66-77)
+  float y[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const uint32_t pr = bf16_pair(f[e] * c[e], pf[e] * sn[e]);
+    y[e] = bf_lo(pr) + bf_hi(pr);
+  }
+  if (MODE == KV_ANY && a.rot < a.d) {            // partial rotary: chunks past rot unrotated
+#pragma unroll
+    for (int e = 0; e < 8; ++e) y[e] = L.rope ? y[e] : f[e];
+  }
+  return make_uint4(bf16_pair(y[0], y[1]), bf16_pair(y[2], y[3]), bf16_pair(y[4], y[5]), bf16_pair(y[6], y[7]));
+}
+
+// The head's sum of squares of a K chunk for k_norm: the chunk's own, summed over the head's chunks
+// (the lanes of one 32-lane row group, all of which must call this). 0 without k_norm.
+template <int MODE = KV_ANY>
+__device__ __forceinline__ float head_ssq(const KvArgs& a, const KvLane& L, const uint4& v) {
+  float ss = 0.f;
+  if (MODE == KV_ANY ? a.knorm != nullptr : MODE == KV_D128_KNORM) {   // uniform
+    ss = chunk_ssq(v);
+    const int group = MODE == KV_ANY ? L.group : 16;
+#pragma unroll
+    for (int o = 1; o < 32; o <<= 1)
+      if (o < group) ss += __shfl_xor(ss, o, 64);
+  }
+  return ss;
+}
+
 // One row's chunk of the K / V epilogue: get(c) returns the row's normed bf16 chunk c (of the tile
-// column); per-head sum of squares for k_norm over the head's chunks (lanes of one 32-lane row group,
-// all of which call this, ok or not), then k_norm, RoPE with the row's table entries `re`
-// (rope_fetch) and a streaming store into slot slot0 + gm.
+// column); k_norm and RoPE for K chunks (k_chunk, with the row's table entries `re`, rope_fetch), then
+// a streaming store into slot slot0 + gm. All lanes of a 32-lane row group call this, ok or not.
 template <class Get>
 __device__ __forceinline__ void kv_chunk_row(const KvArgs& a, const KvLane& L, Get get, int ch, int64_t gm, bool ok,
                                              const RopeEnt& re) {
   const uint4 v = get(ch);
-  float ss = 0.f;
-  if (a.knorm) {                                   // per-head sum of squares; uniform branch
-    ss = chunk_ssq(v);
-    for (int o = 1; o < L.group; o <<= 1) ss += __shfl_xor(ss, o, 64);
-  }
+  const float ss = head_ssq(a, L, v);
   if (!ok) return;
-  const int j0 = L.j0, half = L.half, rot = a.rot;
   uint16_t* dst = L.dst0 + (a.slot0 + gm) * a.row_stride;
   if (!L.is_k || (!L.norm && !L.rope)) {
     st_stream16(dst, v);
     return;
   }
-  float f[8];
+  const uint4 pv = L.half >= 8 ? get(ch + (L.pj0 - L.j0) / 8) : v;
+  st_stream16(dst, k_chunk(a, L, v, pv, ss, re));
+}
+
+// Row pass of a tile of K columns only (slot-indexed rows): rows it * 8 + t / 32, chunk t % 32, in
+// groups of 8 rows per thread, one loop iteration each (the loop is not unrolled: the instruction cache
+// holds one group's code, not the pass's). The RoPE table entries of the next group are fetched before
+// this group's math, and the group's 8 stores go out after it, so every wait covers only loads issued a
+// group earlier.
+template <int MODE>
+__device__ __forceinline__ void k_rows(const KvArgs& a, const KvLane& L, const uint4* lds, int m0, int M) {
+  const int t = threadIdx.x, ch = t & 31;
+  RopeEnt cur[8], nxt[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) f[e] = bf2f(lane_of(v, e));
-  const float rinv = 1.0f / sqrtf(ss / static_cast<float>(a.d) + a.eps);
-  if (L.norm) knorm_chunk(f, rinv, L.kn, a.knorm_kind);
-  uint4 o;
-  if (!L.rope) {
-    o = make_uint4(bf16_pair(f[0], f[1]), bf16_pair(f[2], f[3]), bf16_pair(f[4], f[5]), bf16_pair(f[6], f[7]));
-  } else {
-    float pf[8];                                  // rotate_half partner values of this chunk
-    if (half >= 8) {
-      const uint4 pv = get(ch + (L.pj0 - j0) / 8);
+  for (int u = 0; u < 8; ++u) cur[u] = rope_fetch_ahead(a, L, m0 + u * 8 + (t >> 5), M);
+#pragma unroll 1
+  for (int g = 0; g < BM / 64; ++g) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pf[e] = bf2f(lane_of(pv, e));
-      if (L.norm) knorm_chunk(pf, rinv, L.kn_p, a.knorm_kind);
-    } else {                                      // half == 4: the partner is in the same chunk
+    for (int u = 0; u < 8; ++u) nxt[u] = rope_fetch_ahead(a, L, m0 + (((g + 1) & 3) * 8 + u) * 8 + (t >> 5), M);
+    uint4 o[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pf[e] = f[e ^ 4];
+    for (int u = 0; u < 8; ++u) {
+      const int row = (g * 8 + u) * 8 + (t >> 5);
+      const uint4 v = image_chunk(lds, row, ch);
+      const bool half8 = MODE == KV_ANY ? L.half >= 8 : true;
+      const uint4 pv = half8 ? image_chunk(lds, row, ch + (L.pj0 - L.j0) / 8) : v;
+      const float ss = head_ssq<MODE>(a, L, v);
+      o[u] = (MODE != KV_ANY || L.norm || L.rope) ? k_chunk<MODE>(a, L, v, pv, ss, cur[u]) : v;
     }
-    float c[8], sn[8];
-    if (half >= 8) {                              // 8 consecutive table entries of each half
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        c[e] = bf2f(lane_of(re.c, e));
-        sn[e] = bf2f(lane_of(re.s, e));
-      }
-    } else {                                      // rot == 8: entries 0..3 serve both halves of the chunk
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        c[e] = bf2f(lane_of(re.c, e & 3));
-        sn[e] = bf2f(lane_of(re.c, 4 + (e & 3)));
-      }
+    for (int u = 0; u < 8; ++u) {
+      const int gm = m0 + (g * 8 + u) * 8 + (t >> 5);
+      if (gm < M) st_stream16(L.dst0 + (a.slot0 + gm) * a.row_stride, o[u]);
     }
-    // x cos + rotate_half(x) sin with each product rounded to bf16, then the sum (ops.py:66-77)
-    float y[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float rh = j0 + e < half ? -pf[e] : pf[e];
-      const uint32_t pr = bf16_pair(f[e] * c[e], rh * sn[e]);
-      y[e] = bf_lo(pr) + bf_hi(pr);
-    }
-    o = make_uint4(bf16_pair(y[0], y[1]), bf16_pair(y[2], y[3]), bf16_pair(y[4], y[5]), bf16_pair(y[6], y[7]));
+    for (int u = 0; u < 8; ++u) cur[u] = nxt[u];
   }
-  st_stream16(dst, o);
+}
+
+// Row pass of a tile of V columns only: a copy of the image into the cache slots.
+__device__ __forceinline__ void v_rows(const KvArgs& a, const KvLane& L, const uint4* lds, int m0, int M) {
+  const int t = threadIdx.x, ch = t & 31;
+#pragma unroll 8
+  for (int it = 0; it < BM / 8; ++it) {
+    const int row = it * 8 + (t >> 5);
+    const int gm = m0 + row;
+    if (gm < M) st_stream16(L.dst0 + (a.slot0 + gm) * a.row_stride, image_chunk(lds, row, ch));
+  }
 }
 
 __global__ __launch_bounds__(NTHR) void k_norm_kv(const uint16_t* __restrict__ Xin, int64_t ldx,
@@ -554,23 +633,16 @@ __global__ __launch_bounds__(NTHR) void k_norm_kv(const uint16_t* __restrict__ X
   // row pass: rows it * 8 + t / 32
   const int t = threadIdx.x, ch = t & 31;
   const KvLane L(a, n0, ch);
-  if (n0 < a.hkv * a.d && !a.pos) {
-    // K columns: the RoPE table entries are fetched AHEAD rows (of this thread) before their use; the
-    // pass is otherwise bound by the latency of these loads
-    constexpr int AHEAD = 8;
-    RopeEnt re[AHEAD];
-#pragma unroll
-    for (int u = 0; u < AHEAD; ++u) re[u] = rope_fetch_ahead(a, L, m0 + u * 8 + (t >> 5), M);
-    for (int it0 = 0; it0 < BM / 8; it0 += AHEAD) {
-#pragma unroll
-      for (int u = 0; u < AHEAD; ++u) {
-        const int row = (it0 + u) * 8 + (t >> 5);
-        const int gm = m0 + row;
-        const RopeEnt cur = re[u];
-        if (it0 + AHEAD < BM / 8) re[u] = rope_fetch_ahead(a, L, gm + AHEAD * 8, M);
-        kv_chunk_row(a, L, [&](int c) { return image_chunk(lds, row, c); }, ch, gm, gm < M, cur);
-      }
-    }
+  const int kw = a.hkv * a.d;
+  const bool d128 = a.d == 128 && a.rot == 128 && !a.pos;
+  if (n0 + BN <= kw && d128 && !a.knorm) {
+    k_rows<KV_D128>(a, L, lds, m0, M);
+  } else if (n0 + BN <= kw && d128 && a.knorm_kind == 0) {
+    k_rows<KV_D128_KNORM>(a, L, lds, m0, M);
+  } else if (n0 + BN <= kw && !a.pos) {
+    k_rows<KV_ANY>(a, L, lds, m0, M);
+  } else if (n0 >= kw) {
+    v_rows(a, L, lds, m0, M);
   } else {
     for (int it = 0; it < BM / 8; ++it) {
       const int row = it * 8 + (t >> 5);
