@@ -18,10 +18,11 @@
 //   O^T += V^T P^T on the same MFMA: P (rounded to bf16) is the B operand straight from the score
 //       registers, the contraction order over each 16-key step being keys {0..3, 8..11} + 4 (l / 32)
 //       of the step, and the V^T fragment is read in that order (two 8-byte LDS reads).
-// Waves 4-7 (the second wave of each SIMD) run half a tile behind waves 0-3, so that one wave's
-// softmax (VALU) runs beside the other's MFMAs instead of both meeting at each tile's barrier in the
-// same phase. With few query blocks the key range is split over blocks (blockIdx.z) whose partials
-// k_causal_combine merges in a fixed order.
+// Each SIMD holds two waves, so one wave's softmax (VALU) can issue beside the other's MFMAs, and the
+// next tile's score MFMAs run in the same instruction block as this tile's exponentials. (Waves of 64
+// query rows, one per SIMD, read half as much LDS per tile but measured 11 % slower: the second wave's
+// overlap matters more here than the LDS reads.) With few query blocks the key range is split over
+// blocks (blockIdx.z) whose partials k_causal_combine merges in a fixed order.
 // The probabilities enter the second product as bf16 before normalisation (the reference casts after
 // it; the difference is within rounding), scores are fp32 products of the bf16 q and k values as the
 // reference's fp32 matmul, and the output is O / (row sum) rounded to bf16.
