@@ -266,32 +266,54 @@ __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
   }
   __syncthreads();                                  // A complete
   float* t_s = reinterpret_cast<float*>(k_s);       // T [64][FST] fp32 in the k tile's space
+  float* p_s = reinterpret_cast<float*>(v_s) + wave * 256;   // per-wave 16 x 16 fp32 scratch (V is written out)
   {
-    // T = (I + A)^-1 by forward substitution, T[i][j] = delta_ij - sum_{m < i} A[i][m] T[m][j]. Wave w takes
-    // columns 16w .. 16w + 15, four lanes per column: part p sums the terms m = 4k + p (two accumulators,
-    // k even / odd) and keeps T[4k + p][j]; a quad sum combines the parts. A is zero on and above the
-    // diagonal and tk is zero until its row is done, so every term past row i vanishes.
-    const int col = 16 * wave + (lane >> 2), part = lane & 3;
-    float tk[16];
+    // T = (I + A)^-1 in 16 x 16 blocks (A strictly lower, so T is unit lower triangular). First wave w
+    // inverts diagonal block w by forward substitution, T[i][j] = delta_ij - sum_{m < i} A[i][m] T[m][j]
+    // within the block, four lanes per column (part p sums the terms m = 4k + p and keeps T[4k + p][j];
+    // a quad sum combines the parts; A is zero on and above the diagonal and tk is zero until its row is
+    // done, so every term past row i vanishes), and zeroes the blocks right of it.
+    const int col = lane >> 2, part = lane & 3, b0 = 16 * wave;
+    float tk[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int k = 0; k < 16; ++k) tk[k] = 0.f;
+    for (int i = 0; i < 16; ++i) {
+      float acc = 0.f;
 #pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      float acc0 = 0.f, acc1 = 0.f;
-#pragma unroll
-      for (int k = 0; 4 * k < i; ++k) {
-        const float av = a_s[i * FST + 4 * k + part];
-        if (k & 1) acc1 = fmaf(-av, tk[k], acc1);
-        else acc0 = fmaf(-av, tk[k], acc0);
-      }
-      const float sum = quad_sum(acc0 + acc1);
-      const float tij = (i == col ? 1.f : 0.f) + sum;
+      for (int k = 0; 4 * k < i; ++k) acc = fmaf(-a_s[(b0 + i) * FST + b0 + 4 * k + part], tk[k], acc);
+      const float tij = (i == col ? 1.f : 0.f) + quad_sum(acc);
       if (part == (i & 3)) tk[i >> 2] = tij;
     }
 #pragma unroll
-    for (int k = 0; k < 16; ++k) t_s[(4 * k + part) * FST + col] = tk[k];
+    for (int k = 0; k < 4; ++k) t_s[(b0 + 4 * k + part) * FST + b0 + col] = tk[k];
+    for (int j = wave + 1; j < 4; ++j)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) t_s[(b0 + 4 * e + (lane >> 4)) * FST + 16 * j + (lane & 15)] = 0.f;
   }
   __syncthreads();
+  // Then the blocks below the diagonal, one block diagonal at a time (wave j takes block (j + d, j)):
+  // T_ij = -T_ii (sum_{m = j .. i-1} A_im T_mj), both products on v_mfma_f32_16x16x4f32 (lane l feeds
+  // X[l % 16][l / 16] and Y[l / 16][l % 16] and holds Z[4 (l / 16) + r][l % 16]), fp32 throughout.
+  for (int d = 1; d < 4; ++d) {
+    if (wave + d < 4) {
+      const int bi = wave + d, bj = wave, lr = lane & 15, lk = lane >> 4;
+      f32x4 pz = {0.f, 0.f, 0.f, 0.f};
+      for (int mb = bj; mb < bi; ++mb)
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks)
+          pz = __builtin_amdgcn_mfma_f32_16x16x4f32(a_s[(16 * bi + lr) * FST + 16 * mb + 4 * ks + lk],
+                                                    t_s[(16 * mb + 4 * ks + lk) * FST + 16 * bj + lr], pz, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) p_s[(4 * lk + r) * 16 + lr] = pz[r];
+      f32x4 tz = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+        tz = __builtin_amdgcn_mfma_f32_16x16x4f32(t_s[(16 * bi + lr) * FST + 16 * bi + 4 * ks + lk],
+                                                  p_s[(4 * ks + lk) * 16 + lr], tz, 0, 0, 0);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) t_s[(16 * bi + 4 * lk + r) * FST + 16 * bj + lr] = -tz[r];
+    }
+    __syncthreads();
+  }
   {  // T split hi / lo in the scan's A-operand order: Tp [it][s][hl][lane][8] = T[16 it + lane % 16][kperm(s, g, e)]
     uint4* tp = reinterpret_cast<uint4*>(vbase);
 #pragma unroll
