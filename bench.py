@@ -118,6 +118,32 @@ def ceilings(dev, P, H):
             "gemm_shape": [P, H, H]}
 
 
+def dequant_bench(dev, rows=2560, width=10240, maps=24):
+    """Expansion of the release's i8_row128 maps (24 late layers of [2560, 10240] int8 codes with
+    per-128-column bf16 scales) to bf16 maps: HBM bound, algorithmic bytes per map = codes (1 B per
+    entry) + scales (2 B per 128 entries) read + the bf16 map (2 B per entry) written."""
+    from rfill import ops
+    g = torch.Generator(device=dev).manual_seed(30)
+    codes = torch.randint(-128, 128, (rows, width), generator=g, device=dev, dtype=torch.int16).to(torch.int8)
+    scale = (torch.rand(rows, width // 128, generator=g, device=dev) * 1e-3).to(torch.bfloat16)
+    out = torch.empty(rows, width, dtype=torch.bfloat16, device=dev)
+    for _ in range(3):
+        ops.dequant_i8_rows(codes, scale, 128, out=out)
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(maps):
+        ops.dequant_i8_rows(codes, scale, 128, out=out)
+    e.record()
+    torch.cuda.synchronize()
+    sec = s.elapsed_time(e) / 1e3 / maps
+    byts = rows * width * 3 + rows * (width // 128) * 2
+    return {"kernel": "rf_dequant_i8_rows", "bound": "hbm", "achieved": round(byts / sec / 1e9, 1),
+            "peak": PEAK_HBM / 1e9, "unit": "GB/s", "frac": round(byts / sec / PEAK_HBM, 4),
+            "bytes_per_launch": byts, "mean_us": round(sec * 1e6, 2), "maps": maps,
+            "ms_all_maps": round(sec * maps * 1e3, 3)}
+
+
 def kv_write_bench(model, dev, P, layer):
     """The standalone RoPE + K / V cache write (fill_kv) at the workload's shape: HBM bound,
     algorithmic bytes 4 Hkv d 2 per row (read pre-RoPE K, V; write post-RoPE K, V)."""
@@ -442,6 +468,7 @@ def main():
     if not args.no_extras:
         log("standalone RoPE + KV write and library ceilings")
         out["kernels"]["rf_rope_kv_write"] = kv_write_bench(model, dev, P, SPLIT)
+        out["kernels"]["rf_dequant_i8_rows"] = dequant_bench(dev)
         out["ceilings"] = ceilings(dev, P, H)
     del caches, xbuf, sbuf
     torch.cuda.empty_cache()

@@ -219,6 +219,17 @@ int rf_colsum_fold(const float* partial, int64_t ntiles, int64_t cols, double* s
 int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t M, int64_t N,
                        int64_t K, double* c, int64_t ldc, hipStream_t stream);
 
+/* ---- map formats ---- */
+
+/* int8 map rows with per-row group scales -> bf16 maps: out[i][j] = bf16(codes[i][j] * scale[i][j / group]),
+ * the product exact in fp32 and one round-to-nearest-even cast. The i8_row128 release layout (group 128:
+ * codes int8 [d_out, d_in], scale bf16 [d_out, d_in / 128]) expands to the Projector's bf16 maps exactly
+ * as the reference's conversion does (code/c5/convert.py:91-97 dequant, :100-109 maps; the bias column
+ * stays bf16). Needs group % 16 == 0, width % group == 0, ld_codes >= width and a multiple of 16,
+ * ld_out >= width and a multiple of 8, ld_scale >= width / group, 16-byte aligned codes and out. */
+int rf_dequant_i8_rows(const int8_t* codes, int64_t ld_codes, const uint16_t* scale, int64_t ld_scale,
+                       int64_t rows, int64_t width, int group, uint16_t* out, int64_t ld_out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

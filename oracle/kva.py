@@ -3,7 +3,8 @@
 Restates the parts of code/kva/kva.py on the fill path: Arm and its prefix length (:79-118), the
 Projector map type and its safetensors format (:121-193), rounded_tail (:270-273), run_lower
 (:282-300) and finish()'s late-layer loop for the fills 'proj', 'identity', 'oracle' and 'none',
-exact rows and the GDN terminal-state correction st (:319-460).
+exact rows and the GDN terminal-state correction st (:319-460); and the release's int8 map layout
+i8_row128 expanded to bf16 maps (code/c5/convert.py:91-109).
 """
 import json
 from dataclasses import dataclass, field
@@ -27,6 +28,31 @@ class Arm:
     def prefix_len(self, n):
         """P = n - tail (0 for the exact arm), code/kva/kva.py:101-106."""
         return 0 if self.fill == "exact" else max(0, n - self.tail)
+
+
+I8_GROUP = 128
+
+
+def dequant_i8_row128(codes, scale, bias):
+    """[rows, width + 1] fp32: codes times their row group's scale, then the bias column
+    (code/c5/convert.py:91-97)."""
+    rows, width = codes.shape
+    if codes.dtype != torch.int8 or width % I8_GROUP or tuple(scale.shape) != (rows, width // I8_GROUP) \
+            or tuple(bias.shape) != (rows,):
+        raise ValueError(f"i8_row128 shapes {tuple(codes.shape)} {tuple(scale.shape)} {tuple(bias.shape)}")
+    w = codes.to(torch.float32).view(rows, width // I8_GROUP, I8_GROUP) * scale.to(torch.float32)[:, :, None]
+    return torch.cat([w.view(rows, width), bias.to(torch.float32)[:, None]], 1)
+
+
+def projector_i8_row128(tensors, split):
+    """The Projector of the i8_row128 tensors proj.L.{codes, scale, bias}: each layer's [d_out, d_in + 1]
+    map cast to bf16 once (code/c5/convert.py:100-109), weight and bias columns split as Projector.load."""
+    W, B = {}, {}
+    for L in sorted({int(k.split(".")[1]) for k in tensors if k.endswith(".codes")}):
+        m = dequant_i8_row128(tensors[f"proj.{L}.codes"], tensors[f"proj.{L}.scale"],
+                              tensors[f"proj.{L}.bias"]).to(torch.bfloat16)
+        W[L], B[L] = m[:, :-1].contiguous(), m[:, -1].contiguous()
+    return Projector(split, W, B, {"layout": "i8_row128"})
 
 
 def rounded_tail(n, base, block):

@@ -109,6 +109,55 @@ class Projector:
         return cls(int(meta["split"]), W, B, meta)
 
 
+I8_GROUP = 128
+
+
+def load_i8_row128(tensors, split, device="cuda"):
+    """Projector from the i8_row128 maps of the public release (code/c5/convert.py:4-23): for each late
+    layer L, proj.L.codes int8 [d_out, d_in], proj.L.scale bf16 [d_out, d_in / 128] (row i's 128-column
+    group g is codes[i, 128 g : 128 g + 128] * scale[i, g]) and proj.L.bias bf16 [d_out]. tensors: a dict
+    of those tensors (e.g. safetensors.torch.load_file of the release's proj8 files) or a list of file
+    paths. The maps are expanded on the device by rf_dequant_i8_rows: codes * scale in fp32 (exact), one
+    cast to bf16, as convert.py's dequant + .to(bfloat16) (:91-109); the bias stays the release's bf16."""
+    if not isinstance(tensors, dict):
+        from safetensors.torch import load_file
+        merged = {}
+        for path in tensors:
+            merged.update(load_file(str(path)))
+        tensors = merged
+    layers = sorted({int(k.split(".")[1]) for k in tensors if k.startswith("proj.") and k.endswith(".codes")})
+    if not layers:
+        raise ValueError("load_i8_row128: no proj.<L>.codes tensors")
+    device = torch.device(device)
+    W, B = {}, {}
+    for L in layers:
+        try:
+            codes, scale, bias = (tensors[f"proj.{L}.{k}"] for k in ("codes", "scale", "bias"))
+        except KeyError as e:
+            raise ValueError(f"load_i8_row128: layer {L} lacks {e.args[0]}") from None
+        rows, width = codes.shape
+        if (codes.dtype != torch.int8 or scale.dtype != torch.bfloat16 or bias.dtype != torch.bfloat16
+                or width % I8_GROUP or tuple(scale.shape) != (rows, width // I8_GROUP) or tuple(bias.shape) != (rows,)):
+            raise ValueError(f"load_i8_row128: layer {L} shapes codes {tuple(codes.shape)} {codes.dtype}, scale "
+                             f"{tuple(scale.shape)} {scale.dtype}, bias {tuple(bias.shape)} {bias.dtype}")
+        W[L] = ops.dequant_i8_rows(codes.to(device).contiguous(), scale.to(device).contiguous(), I8_GROUP)
+        B[L] = bias.to(device).contiguous()
+        check_weights({f"layer.{L}": W[L]}, "load_i8_row128")
+    return Projector(split, W, B, {"layout": "i8_row128"})
+
+
+def st_from_engine(st):
+    """GDN terminal-state corrections in the engines' layout [heads, V, K] (code/c5/convert.py:7-8) to
+    the fill's recurrent-state layout [heads, dk, dv] (code/kva/ops.py:4-6, Qwen35.fill's rec += st):
+    {L: [h, V, K]} -> {L: [h, K, V]} fp32."""
+    out = {}
+    for L, t in st.items():
+        if t.dim() != 3:
+            raise ValueError(f"st_from_engine: layer {L} shape {tuple(t.shape)} (expected [heads, V, K])")
+        out[int(L)] = t.transpose(1, 2).to(torch.float32).contiguous()
+    return out
+
+
 def check_rows(exact_rows, P):
     """Sorted unique int64 rows < P, else ValueError (code/kva/kva.py:357-362)."""
     rows = torch.as_tensor(exact_rows, dtype=torch.long)

@@ -388,6 +388,27 @@ def gdn_fill(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state, worksp
     return conv_out
 
 
+# ------------------------------------------------------------------------ map formats
+
+def dequant_i8_rows(codes, scale, group=128, out=None):
+    """bf16 maps from int8 codes [rows, width] and their per-row group scales scale [rows, width / group]
+    (bf16): out[i, j] = bf16(codes[i, j] * scale[i, j // group]), exact product, one rounding
+    (the i8_row128 layout, code/c5/convert.py:91-97)."""
+    _need(codes, "codes", torch.int8, 2)
+    _need(scale, "scale", torch.bfloat16, 2)
+    rows, width = codes.shape
+    if group <= 0 or width % group or tuple(scale.shape) != (rows, width // group):
+        raise ValueError(f"dequant_i8_rows: codes {tuple(codes.shape)}, scale {tuple(scale.shape)}, group {group}")
+    if out is None:
+        out = torch.empty(rows, width, dtype=torch.bfloat16, device=codes.device)
+    _need(out, "out", torch.bfloat16, 2)
+    if tuple(out.shape) != (rows, width):
+        raise ValueError(f"dequant_i8_rows: out {tuple(out.shape)}")
+    _lib.call("rf_dequant_i8_rows", _ptr(codes), codes.stride(0), _ptr(scale), scale.stride(0), rows, width, group,
+              _ptr(out), out.stride(0), _stream(codes))
+    return out
+
+
 # ------------------------------------------------------------------------ host-side RoPE frequencies
 
 def inv_freq_default(theta, rot_dim):
