@@ -144,6 +144,34 @@ def dequant_bench(dev, rows=2560, width=10240, maps=24):
             "ms_all_maps": round(sec * maps * 1e3, 3)}
 
 
+def window_mass_bench(dev, n=32768, w=64, hq=32, hkv=8, d=128, layers=4):
+    """The qattn selector's mass (rf_window_mass) at the 8B 32K prompt: 64 window rows x 32 query heads over
+    32768 cached keys, for each of the 4 exact lower layers. Algorithmic work per layer: the scores
+    2 w hq n d FLOP; the kernel forms them twice (row statistics, then column sums)."""
+    from rfill import ops
+    g = torch.Generator(device=dev).manual_seed(31)
+    q = (0.5 * torch.randn(w, hq * d, generator=g, device=dev)).to(torch.bfloat16)
+    kb = (0.5 * torch.randn(hkv, n + 64, d, generator=g, device=dev)).to(torch.bfloat16)
+    mass = torch.zeros(n, dtype=torch.float64, device=dev)
+    ws = torch.empty(ops.window_mass_workspace_bytes(w, hq, hkv, d, n), dtype=torch.uint8, device=dev)
+    for _ in range(3):
+        ops.window_mass(q, n - w, kb, hq, d ** -0.5, mass, workspace=ws)
+    torch.cuda.synchronize()
+    reps = 20
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    s.record()
+    for _ in range(reps):
+        ops.window_mass(q, n - w, kb, hq, d ** -0.5, mass, workspace=ws)
+    e.record()
+    torch.cuda.synchronize()
+    sec = s.elapsed_time(e) / 1e3 / reps
+    flop = 2 * w * hq * n * d
+    return {"kernel": "rf_window_mass", "workload": f"qattn mass: {w} window rows x {hq} heads over {n} keys, d {d}",
+            "bound": "mfma", "mean_us": round(sec * 1e6, 1), "achieved_tflops": round(flop / sec / 1e12, 1),
+            "frac": round(flop / sec / PEAK_BF16, 4), "flop_per_launch": flop,
+            "ms_per_prompt": round(sec * layers * 1e3, 3), "layers": layers}
+
+
 def kv_write_bench(model, dev, P, layer):
     """The standalone RoPE + K / V cache write (fill_kv) at the workload's shape: HBM bound,
     algorithmic bytes 4 Hkv d 2 per row (read pre-RoPE K, V; write post-RoPE K, V)."""
@@ -469,6 +497,7 @@ def main():
         log("standalone RoPE + KV write and library ceilings")
         out["kernels"]["rf_rope_kv_write"] = kv_write_bench(model, dev, P, SPLIT)
         out["kernels"]["rf_dequant_i8_rows"] = dequant_bench(dev)
+        out["kernels"]["rf_window_mass"] = window_mass_bench(dev)
         out["ceilings"] = ceilings(dev, P, H)
     del caches, xbuf, sbuf
     torch.cuda.empty_cache()

@@ -219,6 +219,24 @@ int rf_colsum_fold(const float* partial, int64_t ntiles, int64_t cols, double* s
 int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t M, int64_t N,
                        int64_t K, double* c, int64_t ldc, hipStream_t stream);
 
+/* ---- exact-row selection (the qattn selector) ---- */
+
+/* Bytes of rf_window_mass's workspace: w window rows, hq query / hkv K-V heads of head_dim d, keys
+ * 0 .. n_end - 1 (n_end = the window's end). */
+int rf_window_mass_workspace_bytes(int w, int hq, int hkv, int d, int64_t n_end, size_t* bytes);
+
+/* Window attention mass of one exact lower attention layer (code/kva/select.py:223-245 window_mass):
+ * mass[j] += sum over the w window query rows (positions pos0 .. pos0 + w - 1) and all hq query heads of
+ * softmax_j(scale q . k_j), keys j <= the query's position (dense causal softmax over every key), for
+ * j < pos0 + w; later keys get nothing. q [w, >= hq d] post-RoPE queries of the window rows (rf_norm_q),
+ * kbuf the layer's post-RoPE K cache [hkv, cap, d] (head_stride, row_stride); mass fp64 [>= pos0 + w], the
+ * caller's accumulator over layers (zero it per prompt). Each K / V head group's sum is fp32 (rows, then
+ * heads, in a fixed order), added into mass as fp64 in group order. d 64 or 128; (hq / hkv) * w a
+ * multiple of 32, at most 1024. */
+int rf_window_mass(const uint16_t* q, int64_t ldq, int w, int64_t pos0, int hq, int d, const uint16_t* kbuf,
+                   int hkv, int64_t head_stride, int64_t row_stride, float scale, double* mass, void* workspace,
+                   size_t ws_bytes, hipStream_t stream);
+
 /* ---- map formats ---- */
 
 /* int8 map rows with per-row group scales -> bf16 maps: out[i][j] = bf16(codes[i][j] * scale[i][j / group]),

@@ -53,6 +53,8 @@ SIGNATURES = {
     "rf_residual_add": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _P],
     "rf_silu_mul": [_P, _I64, _I64, _I64, _P, _I64, _P],
     "rf_dequant_i8_rows": [_P, _I64, _P, _I64, _I64, _I64, _I32, _P, _I64, _P],
+    "rf_window_mass_workspace_bytes": [_I32, _I32, _I32, _I32, _I64, _PSZ],
+    "rf_window_mass": [_P, _I64, _I32, _I64, _I32, _I32, _P, _I32, _I64, _I64, _F32, _P, _P, _SZ, _P],
 }
 
 _lib = None

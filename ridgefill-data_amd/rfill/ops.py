@@ -388,6 +388,34 @@ def gdn_fill(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state, worksp
     return conv_out
 
 
+# ------------------------------------------------------------------------ exact-row selection
+
+def window_mass_workspace_bytes(w, hq, hkv, d, n_end):
+    n = ctypes.c_size_t(0)
+    _lib.call("rf_window_mass_workspace_bytes", w, hq, hkv, d, n_end, ctypes.byref(n))
+    return n.value
+
+
+def window_mass(q, pos0, kbuf, hq, scale, mass, workspace=None):
+    """mass [>= pos0 + w] fp64 += the attention probability each key receives from the w window query
+    rows q [w, >= hq d] (post-RoPE, at positions pos0 .. pos0 + w - 1) over the K cache kbuf [hkv, cap, d],
+    summed over rows and query heads (code/kva/select.py:223-245, one layer)."""
+    _need(q, "q", torch.bfloat16, 2)
+    _need(kbuf, "kbuf", torch.bfloat16, 3)
+    _need(mass, "mass", torch.float64, 1)
+    hkv, cap, d = kbuf.shape
+    w = q.shape[0]
+    if q.shape[1] < hq * d or pos0 < 0 or pos0 + w > cap or mass.numel() < pos0 + w:
+        raise ValueError(f"window_mass: q {tuple(q.shape)}, pos0 {pos0}, cache {tuple(kbuf.shape)}, "
+                         f"mass {mass.numel()}")
+    need = window_mass_workspace_bytes(w, hq, hkv, d, pos0 + w)
+    if workspace is None:
+        workspace = torch.empty(need, dtype=torch.uint8, device=q.device)
+    _lib.call("rf_window_mass", _ptr(q), q.stride(0), w, pos0, hq, d, _ptr(kbuf), hkv, kbuf.stride(0),
+              kbuf.stride(1), float(scale), _ptr(mass), _ptr(workspace), workspace.numel(), _stream(q))
+    return mass
+
+
 # ------------------------------------------------------------------------ map formats
 
 def dequant_i8_rows(codes, scale, group=128, out=None):
