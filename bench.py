@@ -257,6 +257,53 @@ def fit_bench(dev, chunks=2, rows=65536, d=4096, targets=16, lams=(1e-4, 1e-3, 1
             "projected_full_fit_s": round(t_acc * 32 / chunks + t_solve, 2)}
 
 
+def capture_bench(dev, split=SPLIT, n=8192, lams=9):
+    """The fit's capture and lambda selection at the Llama-3.1-8B shape (32 layers, random weights): one
+    n-token calibration document through the exact forward (layers 0 .. 30) with every input of layers
+    16 .. 31 transposed into the Gram block, then the block's one MFMA Gram launch for split 16
+    (X^T [H, n] times [H_16 .. H_31]^T: 2 n H (16 H) flop into fp64); and one n-token held-out document
+    scored for `lams` maps + the identity on all 16 late layers (per layer and candidate: the map, the
+    K | V reads GEMM and rf_read_cosine)."""
+    from rfill import fit, synth
+    from rfill.model import FillModel
+    cfg = synth.LLAMA_8B
+    model = FillModel(cfg, synth.full_model(cfg, device=dev), dev)
+    L, H = cfg["num_hidden_layers"], cfg["hidden_size"]
+    g = torch.Generator().manual_seed(17)
+    doc = torch.randint(0, cfg["vocab_size"], (n,), generator=g)
+    cap = fit.Capture(model, [split])
+    cap.add_document(doc)                 # warm-up: packs the layers, allocates the block
+    cap.flush()
+    torch.cuda.synchronize()
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+    ev[0].record()
+    cap.add_document(doc)
+    ev[1].record()
+    cap.flush()
+    ev[2].record()
+    torch.cuda.synchronize()
+    t_fwd, t_gram = ev[0].elapsed_time(ev[1]) / 1e3, ev[1].elapsed_time(ev[2]) / 1e3
+    gram_flop = 2.0 * n * H * (L - split) * H
+    del cap
+    gm = torch.Generator(device=dev).manual_seed(18)
+    maps = {lam: {i: ((torch.eye(H, device=dev) + 0.02 * torch.randn(H, H, generator=gm, device=dev) / H ** 0.5)
+                      .to(torch.bfloat16), torch.zeros(H, dtype=torch.bfloat16, device=dev))
+                  for i in range(split, L)} for lam in fit.LAMBDAS[:lams]}
+    fit.read_scores(model, [doc[: n // 4]], split, maps)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    fit.read_scores(model, [doc], split, maps)
+    torch.cuda.synchronize()
+    t_sel = time.perf_counter() - t0
+    return {"workload": f"llama-3.1-8b-shaped capture: {n}-token document, exact forward of layers 0..{L - 2}, "
+                        f"Gram of split {split} over layers {split}..{L - 1}; selection of {lams} maps + identity "
+                        f"on one {n}-token held-out document",
+            "capture_tokens_per_s": round(n / (t_fwd + t_gram), 1), "ms_forward_and_transpose": round(t_fwd * 1e3, 2),
+            "ms_gram": round(t_gram * 1e3, 2), "gram_tflops": round(gram_flop / t_gram / 1e12, 1),
+            "gram_frac_bf16_peak": round(gram_flop / t_gram / PEAK_BF16, 4),
+            "ms_select_per_doc": round(t_sel * 1e3, 1)}
+
+
 def hybrid_bench(dev, reps=3, split=24, n_rows=32768, tail=4096):
     """The Gated-DeltaNet hybrid's late-layer fill (hidden 2048; layers 24..47 = 18 GDN + 6 attention;
     GDN 16 key / 32 value heads of 128, attention 2 KV heads of 256; P = 28672 filled rows from zero
@@ -516,6 +563,10 @@ def main():
     if not args.no_fit:
         log("closed-form fit leg")
         out["fit"] = fit_bench(dev)
+        torch.cuda.empty_cache()
+        log("capture and lambda-selection leg")
+        out["capture"] = capture_bench(dev)
+        torch.cuda.empty_cache()
     if not args.no_cpu:
         log("CPU baseline (oracle fill on the host cores)")
         out["cpu_baseline"] = cpu_baseline(cfg, w, SPLIT)

@@ -219,6 +219,19 @@ int rf_colsum_fold(const float* partial, int64_t ntiles, int64_t cols, double* s
 int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t M, int64_t N,
                        int64_t K, double* c, int64_t ldc, hipStream_t stream);
 
+/* Held-out read cosine of one late layer for one document (code/scripts/fit_sweep.py:307-313): pred and
+ * truth are [rows, 2 hkv d] bf16 reads, K heads in columns 0 .. hkv d - 1 and V heads after them (the
+ * pre-RoPE K / V of code/kva/model.py:282-287, one norm_linear of the [W_k; W_v] projection). Per row
+ * and head, cos = a . b / (max(|a|, 1e-8) max(|b|, 1e-8)) in fp32 (F.cosine_similarity over head_dim);
+ * K heads are first scaled elementwise by the k_norm gain kgain [d] bf16 (gain_kind 1: 1 + gain; NULL:
+ * no k norm), which is the cosine of the k-normed reads (code/kva/model.py:353-359) since the per-head
+ * RMS factor cancels. out[0] += weight * (sum of K cosines), out[1] += weight * (sum of V cosines), in
+ * fp64 and a fixed order (weight = 1 / (rows hkv) gives the document's means). workspace: at least
+ * 8 * ceil(rows / 16) bytes. d = 64, 128 or 256; ld_pred / ld_true multiples of 8. */
+int rf_read_cosine(const uint16_t* pred, int64_t ld_pred, const uint16_t* truth, int64_t ld_true, int64_t rows,
+                   int hkv, int d, const uint16_t* kgain, int gain_kind, double weight, double* out,
+                   void* workspace, size_t ws_bytes, hipStream_t stream);
+
 /* ---- exact-row selection (the qattn selector) ---- */
 
 /* Bytes of rf_window_mass's workspace: w window rows, hq query / hkv K-V heads of head_dim d, keys

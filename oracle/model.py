@@ -161,6 +161,19 @@ class OracleModel:
             q = self.head_norm(q, w["q_norm"])
         return ops.apply_rope(q.transpose(0, 1), cos, sin), None
 
+    def reads(self, i, x):
+        """Pre-RoPE K and V per KV head, {'k', 'v'}: [tokens, Hkv, d] of layer i's inputs x, K head-normed
+        for Qwen3 / Qwen3.5 (code/kva/model.py:282-287, :353-359, :558-565 attention layers)."""
+        if self.layer_types[i] != "attn":
+            raise UnsupportedArchitecture("reads of GDN layers")
+        w = self.W[i]
+        xn = self.in_norm(x, w["ln1"])
+        n = x.shape[0]
+        k = F.linear(xn, w["k"]).view(n, self.n_kv, self.head_dim)
+        if self.arch != "llama":
+            k = self.head_norm(k, w["k_norm"])
+        return dict(k=k, v=F.linear(xn, w["v"]).view(n, self.n_kv, self.head_dim))
+
     def fill_kv(self, i, k, v, pos, cache):
         """Cache-only fill from given pre-RoPE K / V [tokens, Hkv, d] (code/kva/model.py:161-165)."""
         cos, sin = ops.rope_cos_sin(self.inv_freq, pos, k.dtype)

@@ -72,6 +72,95 @@ __global__ __launch_bounds__(256) void k_colsum_fold(const float* __restrict__ p
   if (i == 0 && c < cols) sums[c] += red[0][cl];
 }
 
+// Read cosines of one late layer for one held-out document (code/scripts/fit_sweep.py:307-313). A work
+// item is one head vector of one row: items 0 .. hkv - 1 of a row are its K heads, hkv .. 2 hkv - 1 its V
+// heads (the [K | V] column layout of the reads GEMM). d / 8 lanes take one item, one 16-byte chunk each,
+// and reduce dot and norms with xor butterflies (every lane ends with the same sums). A block covers
+// COS_ROWS rows; each lane group walks its items in a fixed order, and the block's per-thread sums are
+// folded by a fixed tree into partial[block] = (sum of K cosines, sum of V cosines).
+constexpr int COS_ROWS = 16;
+
+__global__ __launch_bounds__(256) void k_read_cosine(const uint16_t* __restrict__ pred, int64_t ldp,
+                                                     const uint16_t* __restrict__ tru, int64_t ldt, int64_t rows,
+                                                     int hkv, int d, const uint16_t* __restrict__ kgain,
+                                                     int gain_kind, float2* __restrict__ partial) {
+  __shared__ float red[2][256];
+  const int t = threadIdx.x;
+  const int g = d >> 3, sub = t & (g - 1), grp = t / g, ngrp = 256 / g;
+  const int per_row = 2 * hkv, nitems = COS_ROWS * per_row;
+  const int64_t r0 = static_cast<int64_t>(blockIdx.x) * COS_ROWS;
+  float gn[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) gn[e] = kgain ? bf2f(kgain[sub * 8 + e]) + (gain_kind ? 1.0f : 0.0f) : 1.0f;
+  float ak = 0.0f, av = 0.0f;
+  for (int it = grp; it < nitems; it += ngrp) {
+    const int64_t r = r0 + it / per_row;
+    const int hv = it % per_row;
+    if (r >= rows) break;                            // items run row-major: the rest of the walk is past `rows`
+    const int64_t col = static_cast<int64_t>(hv) * d + sub * 8;
+    const uint4 pv = *reinterpret_cast<const uint4*>(pred + r * ldp + col);
+    const uint4 tv = *reinterpret_cast<const uint4*>(tru + r * ldt + col);
+    const bool is_k = hv < hkv;
+    float dot = 0.0f, n1 = 0.0f, n2 = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float s = is_k ? gn[e] : 1.0f;
+      const float a = bf2f(lane_of(pv, e)) * s, b = bf2f(lane_of(tv, e)) * s;
+      dot += a * b;
+      n1 += a * a;
+      n2 += b * b;
+    }
+    for (int m = g >> 1; m >= 1; m >>= 1) {
+      dot += __shfl_xor(dot, m);
+      n1 += __shfl_xor(n1, m);
+      n2 += __shfl_xor(n2, m);
+    }
+    const float c = dot / (fmaxf(sqrtf(n1), 1e-8f) * fmaxf(sqrtf(n2), 1e-8f));
+    if (sub == 0) {
+      if (is_k) ak += c;
+      else av += c;
+    }
+  }
+  red[0][t] = ak;
+  red[1][t] = av;
+  __syncthreads();
+  for (int h = 128; h >= 1; h >>= 1) {
+    if (t < h) {
+      red[0][t] += red[0][t + h];
+      red[1][t] += red[1][t + h];
+    }
+    __syncthreads();
+  }
+  if (t == 0) partial[blockIdx.x] = make_float2(red[0][0], red[1][0]);
+}
+
+// out[0] += weight * sum_j partial[j].x, out[1] += weight * sum_j partial[j].y, in fp64 and a fixed order
+// (thread i sums blocks i, i + 256, ... in order, then a fixed tree over the 256 threads).
+__global__ __launch_bounds__(256) void k_cosine_fold(const float2* __restrict__ partial, int64_t nblk, double weight,
+                                                     double* __restrict__ out) {
+  __shared__ double red[2][256];
+  const int t = threadIdx.x;
+  double sk = 0.0, sv = 0.0;
+  for (int64_t j = t; j < nblk; j += 256) {
+    sk += static_cast<double>(partial[j].x);
+    sv += static_cast<double>(partial[j].y);
+  }
+  red[0][t] = sk;
+  red[1][t] = sv;
+  __syncthreads();
+  for (int h = 128; h >= 1; h >>= 1) {
+    if (t < h) {
+      red[0][t] += red[0][t + h];
+      red[1][t] += red[1][t + h];
+    }
+    __syncthreads();
+  }
+  if (t == 0) {
+    out[0] += weight * red[0][0];
+    out[1] += weight * red[1][0];
+  }
+}
+
 }  // namespace
 }  // namespace rf
 
@@ -99,4 +188,28 @@ extern "C" int rf_colsum_fold(const float* partial, int64_t ntiles, int64_t cols
   hipLaunchKernelGGL(k_colsum_fold, dim3(static_cast<unsigned>((cols + 15) / 16)), dim3(256), 0, stream, partial,
                      ntiles, static_cast<int>(cols), sums);
   return check_launch("rf_colsum_fold");
+}
+
+extern "C" int rf_read_cosine(const uint16_t* pred, int64_t ld_pred, const uint16_t* truth, int64_t ld_true,
+                              int64_t rows, int hkv, int d, const uint16_t* kgain, int gain_kind, double weight,
+                              double* out, void* workspace, size_t ws_bytes, hipStream_t stream) {
+  if (!pred || !truth || !out) return fail(RF_EINVAL_ARG, "rf_read_cosine: null pointer");
+  if (rows < 0 || hkv <= 0 || (d != 64 && d != 128 && d != 256) || ld_pred < 2ll * hkv * d ||
+      ld_true < 2ll * hkv * d || ld_pred % 8 || ld_true % 8 || (gain_kind != 0 && gain_kind != 1))
+    return fail(RF_EINVAL_SHAPE, "rf_read_cosine: rows %lld, hkv %d, d %d (64, 128 or 256), ld_pred %lld, "
+                "ld_true %lld (>= 2 hkv d, multiples of 8), gain_kind %d", (long long)rows, hkv, d,
+                (long long)ld_pred, (long long)ld_true, gain_kind);
+  if (!aligned16(pred) || !aligned16(truth)) return fail(RF_EINVAL_SHAPE, "rf_read_cosine: 16-byte alignment");
+  const int64_t nblk = (rows + COS_ROWS - 1) / COS_ROWS;
+  if (nblk > (1ll << 31) - 1) return fail(RF_EINVAL_SHAPE, "rf_read_cosine: rows %lld", (long long)rows);
+  if (rows == 0) return RF_OK;
+  if (!workspace || ws_bytes < static_cast<size_t>(nblk) * sizeof(float2))
+    return fail(RF_EINVAL_ARG, "rf_read_cosine: workspace %zu bytes, needs %lld", ws_bytes,
+                (long long)(nblk * static_cast<int64_t>(sizeof(float2))));
+  float2* part = static_cast<float2*>(workspace);
+  hipLaunchKernelGGL(k_read_cosine, dim3(static_cast<unsigned>(nblk)), dim3(256), 0, stream, pred, ld_pred, truth,
+                     ld_true, rows, hkv, d, kgain, gain_kind, part);
+  if (int rc = check_launch("rf_read_cosine")) return rc;
+  hipLaunchKernelGGL(k_cosine_fold, dim3(1), dim3(256), 0, stream, part, nblk, weight, out);
+  return check_launch("rf_read_cosine");
 }

@@ -23,7 +23,7 @@ class HipError(RuntimeError):
     """The HIP runtime reported an error for a kernel launch."""
 
 
-_P, _I64, _I32, _F32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
+_P, _I64, _I32, _F32, _F64 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_double
 _SZ, _PSZ = ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)
 
 # name -> argument types (every function returns int status)
@@ -53,6 +53,7 @@ SIGNATURES = {
     "rf_residual_add": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _P],
     "rf_silu_mul": [_P, _I64, _I64, _I64, _P, _I64, _P],
     "rf_dequant_i8_rows": [_P, _I64, _P, _I64, _I64, _I64, _I32, _P, _I64, _P],
+    "rf_read_cosine": [_P, _I64, _P, _I64, _I64, _I32, _I32, _P, _I32, _F64, _P, _P, _SZ, _P],
     "rf_window_mass_workspace_bytes": [_I32, _I32, _I32, _I32, _I64, _PSZ],
     "rf_window_mass": [_P, _I64, _I32, _I64, _I32, _I32, _P, _I32, _I64, _I64, _F32, _P, _P, _SZ, _P],
 }

@@ -1,0 +1,212 @@
+"""The fit driver on the GPU: the capture pass, the per-split ridge fit and the held-out lambda selection
+of code/scripts/fit_sweep.py, over FillModel's exact forward and librfill's kernels.
+
+Capture (fit_sweep.py:62-166, :236-248). One exact forward per calibration document
+(FillModel.forward_exact, stopped before the last layer, whose output no split needs). The inputs h_i of
+every layer i >= the smallest split S0 are transposed (rf_transpose) into one K-contiguous block
+T [(L - S0) H, B] bf16: layer i owns rows (i - S0) H .. + H, documents sit side by side at 64-row
+offsets, and the padding columns are zero, so they add nothing to any sum. When the block is full (or a
+state is asked for), one rf_gram_accumulate per split S adds T_S [H, K] times T_{S..L-1}^T into that
+split's fp64 accumulator [H, (L - S) H]: its first H columns are X_S^T X_S and its column block i - S is
+X_S^T H_i -- every (S, i) pair of the reference in one MFMA launch per split, over up to B rows at a time.
+The column sums of each layer come from the transpose (rf_colsum_fold) and serve every split.
+
+The device keeps raw sums; state(S) re-centres them in fp64 on the reference's shifts -- the first
+document's means of h_S and of h_i (fit_sweep.py:98-99, :104-105) -- so the state dict has
+split_state()'s layout and meaning (fit_sweep.py:147-166). The shift is the first document's fp64 column
+sum over its row count, rounded to fp32 as the reference's h.float().mean(0) is. Products are bf16 x bf16
+(exact) summed in fp32 over a block on MFMA and added into fp64, as the reference's per-document fp32
+GEMM is added into fp64; what differs is only the fp32 rounding inside a block, which grows with
+|mean| / spread of a channel, since the reference subtracts the shift before its GEMM.
+
+Selection (fit_sweep.py:298-318). For each held-out document: one exact forward (stopped after the last
+layer's input); per late layer i the true reads norm(h_i) [W_k; W_v]^T (one norm_linear GEMM, the
+pre-RoPE K | V of code/kva/model.py:282-287); per candidate (each lambda's map, then the identity) the
+predicted input x = h_S W^T + b (rf_map_apply) and its reads; rf_read_cosine adds the document's mean
+K and V cosines (k_norm gain applied for Qwen3) into an fp64 score per candidate and layer.
+"""
+import torch
+
+from . import ops, ridge
+from ._lib import UnsupportedArchitecture
+from .kva import Projector
+
+LAMBDAS = (1e-4, 3e-4, 1e-3, 3e-3, 0.01, 0.03, 0.1, 0.3, 1.0)      # fit_sweep.py:44
+BLOCK = 8192
+
+
+class Capture:
+    """fit_sweep's capture sums for every split in splits over the documents added (add_document)."""
+
+    def __init__(self, model, splits, block=BLOCK):
+        self.model, self.splits = model, sorted(set(int(s) for s in splits))
+        self.L, H = model.n_layers, model.hidden
+        if not self.splits or self.splits[0] < 1 or self.splits[-1] >= self.L:
+            raise ValueError(f"splits {splits}: each split S needs 1 <= S < {self.L} (late layers S .. L - 1)")
+        if any(t != "attn" for t in model.layer_types):
+            raise UnsupportedArchitecture("the capture runs the exact forward, which the kernels implement for "
+                                          "attention layers only")
+        if H % 256:
+            raise ValueError(f"hidden size {H}: the Gram accumulation needs a multiple of 256")
+        if block <= 0 or block % 64:
+            raise ValueError("block must be a positive multiple of 64")
+        self.S0, self.H, self.block = self.splits[0], H, block
+        dev = model.device
+        f64 = dict(dtype=torch.float64, device=dev)
+        nl = self.L - self.S0
+        self.n, self.docs = 0, 0
+        self.s1 = torch.zeros(nl, H, **f64)               # raw column sums of h_i, i >= S0
+        self.first = torch.zeros(nl, H, **f64)            # the first document's column sums
+        self.n_first = 0
+        self.acc = {S: torch.zeros(H, (self.L - S) * H, **f64) for S in self.splits}
+        self.T = None
+        self.part = None
+        self.off = 0
+
+    def _room(self, kp):
+        cap = self.T.shape[1] if self.T is not None else 0
+        if kp > cap:
+            self.flush()
+            cap = max(self.block, kp)
+            dev = self.model.device
+            self.T = torch.empty((self.L - self.S0) * self.H, cap, dtype=torch.bfloat16, device=dev)
+            self.part = torch.empty(cap // 64, self.H, dtype=torch.float32, device=dev)
+        elif self.off + kp > cap:
+            self.flush()
+
+    def _hook(self, i, h):
+        if i == "final" or i < self.S0:
+            return
+        rows = h.shape[0]
+        kp = (rows + 63) // 64 * 64
+        r = (i - self.S0) * self.H
+        part = self.part[:kp // 64]
+        ridge._transpose(h, self.T[r:r + self.H, self.off:self.off + kp], part)
+        ridge._colsum_fold(part, self.s1[i - self.S0])
+        if self.docs == 0:
+            ridge._colsum_fold(part, self.first[i - self.S0])
+
+    @torch.no_grad()
+    def add_document(self, ids):
+        """One calibration document's token ids: its exact forward, every layer input >= S0 into the sums."""
+        n = int(torch.as_tensor(ids).numel())
+        if n == 0:
+            raise ValueError("empty document")
+        kp = (n + 63) // 64 * 64
+        self._room(kp)
+        self.model.forward_exact(ids, hook=self._hook, stop=self.L - 1)
+        self.off += kp
+        if self.docs == 0:
+            self.n_first = n
+        self.docs += 1
+        self.n += n
+
+    def flush(self):
+        """Add the buffered rows' products into every split's accumulator."""
+        if not self.off:
+            return
+        K, H = self.off, self.H
+        for S in self.splits:
+            r = (S - self.S0) * H
+            ridge.gram_accumulate(self.T[r:r + H, :K], self.T[r:, :K], self.acc[S])
+        self.off = 0
+
+    def state(self, S, device="cpu"):
+        """split_state(acc, S, L, H) (fit_sweep.py:147-166): fp64 sums about the first document's means."""
+        if S not in self.acc:
+            raise KeyError(f"split {S} was not captured (splits {self.splits})")
+        if not self.n:
+            raise ValueError("no documents captured")
+        self.flush()
+        H, n = self.H, float(self.n)
+        mean = (self.first / self.n_first).float().double()          # fp32 shifts, as h.float().mean(0)
+        j = S - self.S0
+        cx, s1x = mean[j], self.s1[j]
+        raw = self.acc[S]
+        late = list(range(S, self.L))
+        cy, sy, sxy = {}, {}, {}
+        for i in late:
+            c, s1y = mean[i - self.S0], self.s1[i - self.S0]
+            blk = raw[:, (i - S) * H:(i - S + 1) * H]
+            cy[i] = c.to(device)
+            sy[i] = (s1y - n * c).to(device)
+            sxy[i] = (blk - torch.outer(cx, s1y) - torch.outer(s1x, c) + n * torch.outer(cx, c)).to(device)
+        sxx = raw[:, :H] - torch.outer(cx, s1x) - torch.outer(s1x, cx) + n * torch.outer(cx, cx)
+        return dict(split=S, layers=late, dim=H, n=self.n, cx=cx.to(device), cy=cy, sx=(s1x - n * cx).to(device),
+                    sxx=sxx.to(device), sy=sy, sxy=sxy)
+
+
+def fit_maps(state, lambdas=LAMBDAS, device="cuda"):
+    """{lam: {layer: (W [d_out, d_in] bf16, b [d_out] bf16)}} on the device: RidgeFit of every late layer
+    for every lambda, rounded to bf16 as the saved maps are (fit_sweep.py:286-293)."""
+    fit = ridge.RidgeFit(state, device=device)
+    per = fit.layers(state["layers"], lambdas)
+    return {lam: {i: (per[i][lam][0].to(torch.bfloat16), per[i][lam][1].to(torch.bfloat16))
+                  for i in state["layers"]} for lam in lambdas}
+
+
+def _inputs(model, ids, first):
+    got = {}
+    model.forward_exact(ids, hook=lambda i, h: got.__setitem__(i, h) if i != "final" and i >= first else None,
+                        stop=model.n_layers - 1)
+    return got
+
+
+@torch.no_grad()
+def read_scores(model, held, split, maps):
+    """{candidate: {layer: mean read cosine}} over the held-out documents (fit_sweep.py:298-314);
+    candidates: the lambdas of maps, then "identity"."""
+    late = list(range(split, model.n_layers))
+    cand = list(maps) + ["identity"]
+    dev = model.device
+    score = torch.zeros(len(cand), len(late), 2, dtype=torch.float64, device=dev)
+    H, hkv, d = model.hidden, model.n_kv, model.head_dim
+    for ids in held:
+        got = _inputs(model, ids, split)
+        hs = got[split]
+        n = hs.shape[0]
+        ws = torch.empty(8 * ((n + 15) // 16) + 8, dtype=torch.uint8, device=dev)
+        ssq_s = ops.row_ssq(hs)
+        for j, i in enumerate(late):
+            w = model._layer(i)
+            wkv = w["wkv"]
+            gws = model.gemm_workspace(n, wkv.shape[0], H, dev)
+            true = ops.norm_linear(got[i], ops.row_ssq(got[i]), model.eps, wkv, workspace=gws)
+            pred = torch.empty_like(true)
+            for c, lam in enumerate(cand):
+                if lam == "identity":
+                    x, sx = hs, ssq_s
+                else:
+                    W, b = maps[lam][i]
+                    x, sx = ops.map_apply(hs, W, b, workspace=model.gemm_workspace(n, W.shape[0], H, dev))
+                ops.norm_linear(x, sx, model.eps, wkv, out=pred, workspace=gws)
+                ops.read_cosine(pred, true, hkv, d, w.get("k_norm"), model.knorm_kind, 1.0 / (n * hkv),
+                                score[c, j], workspace=ws)
+    s = (score.sum(2) / (2 * len(held))).cpu()
+    return {lam: {i: float(s[c, j]) for j, i in enumerate(late)} for c, lam in enumerate(cand)}
+
+
+def best_lambda(scores, lambdas=LAMBDAS):
+    """The lambda with the highest mean score over layers, the first in lambdas order on ties
+    (fit_sweep.py:315-318)."""
+    mean = {c: sum(v.values()) / len(v) for c, v in scores.items()}
+    return max(lambdas, key=lambda lam: mean[lam])
+
+
+def fit_sweep(model, docs, held, splits, lambdas=LAMBDAS, block=BLOCK):
+    """Capture over docs, then per split: fit every lambda, pick one by the held-out read cosine, and
+    return {S: dict(projector=Projector(S, W, b) of the chosen lambda (bf16, on the device), lam, scores,
+    rows)} (fit_sweep.py:236-337 without the files)."""
+    cap = Capture(model, splits, block)
+    for ids in docs:
+        cap.add_document(ids)
+    out = {}
+    for S in sorted(cap.splits, reverse=True):
+        maps = fit_maps(cap.state(S, device=model.device), lambdas, device=model.device)
+        scores = read_scores(model, held, S, maps)
+        lam = best_lambda(scores, lambdas)
+        W = {i: w for i, (w, _) in maps[lam].items()}
+        B = {i: b for i, (_, b) in maps[lam].items()}
+        out[S] = dict(projector=Projector(S, W, B, dict(lam=lam, rows=cap.n, taps=S, sweep=True, docs=cap.docs)),
+                      lam=lam, scores=scores, rows=cap.n)
+    return out

@@ -5,6 +5,8 @@ arithmetic in librfill's HIP kernels.
                                 (code/kva/model.py:278-280, 510-523)
   fill_kv(i, k, v, pos, cache)  cache-only fill from given pre-RoPE K / V [P, Hkv, d]
                                 (code/kva/model.py:161-165)
+  forward_exact(ids, hook)      exact forward of one document, hook(i, h) on every layer input
+                                (code/kva/model.py:167-181; attention models)
   new_cache()                   one dict per layer (code/kva/model.py:105-106)
 
 Cache layout (code/kva/model.py:139-159): attention layers hold kbuf / vbuf [Hkv, cap, d] bf16 with
@@ -332,6 +334,40 @@ class FillModel:
             o = ops.attend_rows(q, idx + slot, c["kbuf"], c["vbuf"], c["n"], self.n_heads, self.scale,
                                 workspace=self._attn_workspace(T, c["n"], h.device))
         return self._out_mlp(w, h, o)
+
+    def embed(self, ids):
+        """Embedding rows of token ids [T] (code/kva/model.py:108-109): a bit-exact row gather from the bf16
+        table (kept on the device after the first call). Returns (h [T, H] bf16, its row sum-of-squares
+        partials)."""
+        if getattr(self, "_embed", None) is None:
+            self._embed = self._src[self._pre + "embed_tokens.weight"].to(self.device, torch.bfloat16).contiguous()
+        ids = torch.as_tensor(ids, dtype=torch.int64).to(self.device)
+        if ids.dim() != 1:
+            raise ValueError(f"ids: expected a 1-d tensor of token ids, got shape {tuple(ids.shape)}")
+        if ids.numel() and (int(ids.min()) < 0 or int(ids.max()) >= self._embed.shape[0]):
+            raise ValueError(f"ids: token ids must lie in [0, {self._embed.shape[0]})")
+        return ops.row_gather(self._embed, ids)
+
+    def forward_exact(self, ids, hook=None, cache=None, keep=None, stop=None):
+        """Exact forward over all rows of one document (code/kva/model.py:167-181): hook(i, h) sees each
+        layer's input h [T, H] bf16 and hook("final", h) the final-norm input; keep: row indices whose
+        logits to return. stop: return after hook(stop, h), before layer `stop` runs (a capture that needs
+        no later layer). Returns (logits of keep or None, cache)."""
+        cache = self.new_cache() if cache is None else cache
+        if any(c.get("n", 0) for c in cache):
+            raise ValueError("forward_exact starts from an empty cache (cache slot = position)")
+        h, ssq = self.embed(ids)
+        pos = torch.arange(h.shape[0], device=self.device)
+        cs = self.rope_table(pos)
+        for i in range(self.n_layers):
+            if hook is not None:
+                hook(i, h)
+            if i == stop:
+                return None, cache
+            h, ssq = self.layer(i, h, pos, cache, ssq=ssq, cs=cs)
+        if hook is not None:
+            hook("final", h)
+        return (self.logits(h[torch.as_tensor(keep, device=self.device)]) if keep is not None else None), cache
 
     def _causal_workspace(self, nq, n, device):
         """rf_attend_causal's workspace (V transposed, key-range splits), shared by every layer

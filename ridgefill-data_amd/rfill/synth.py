@@ -12,8 +12,10 @@
                    dt_bias = 1 (the architecture's own initialisation), so the gates run through the
                    checkpoint formula g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b);
                    attention layers K / V N(0, 0.02) with a zero-centred k_norm gain N(0, 0.05).
+  full_model(...)  every layer's whole weights, the head and an N(0, 1) embedding table (the exact forward
+                   of the capture and the lambda selection).
 Seeds: 10 (rows), 11 (channel gains and outliers), 12 + l (layer l's weights), 100 + l (the map of
-hybrid GDN layer l), 13 (exact-row positions), 14 (exact-row inputs). Normal(mu, s) parameters are standard deviations except the
+hybrid GDN layer l), 13 (exact-row positions), 14 (exact-row inputs), 16 (embedding table). Normal(mu, s) parameters are standard deviations except the
 explicit variance 1/H of the map noise.
 """
 import torch
@@ -87,6 +89,19 @@ def head_weights(cfg, device="cpu"):
     g = _gen(15, device)
     return {"model.norm.weight": (1 + 0.05 * torch.randn(h, generator=g, device=device)).to(torch.bfloat16),
             "lm_head.weight": (0.02 * torch.randn(vocab, h, generator=g, device=device)).to(torch.bfloat16)}
+
+
+def full_model(cfg, device="cpu"):
+    """HF-named weights of every layer (layer_weights(full=True), seed 12 + l), the head (seed 15) and
+    an embedding table N(0, 1) [vocab, H] (seed 16), bf16: the whole model an exact forward runs."""
+    t = {}
+    for l in range(cfg["num_hidden_layers"]):
+        t.update(layer_weights(cfg, l, device, with_map=False, full=True)[0])
+    t.update(head_weights(cfg, device))
+    g = _gen(16, device)
+    t["model.embed_tokens.weight"] = torch.randn(cfg["vocab_size"], cfg["hidden_size"], generator=g,
+                                                 device=device).to(torch.bfloat16)
+    return t
 
 
 def dense_fill(cfg, split, n_rows, tail, device="cpu", exact_frac=0.0, with_maps=True, full=False, head=False):
