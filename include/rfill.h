@@ -261,6 +261,16 @@ int rf_window_mass(const uint16_t* q, int64_t ldq, int w, int64_t pos0, int hq, 
 int rf_dequant_i8_rows(const int8_t* codes, int64_t ld_codes, const uint16_t* scale, int64_t ld_scale,
                        int64_t rows, int64_t width, int group, uint16_t* out, int64_t ld_out, hipStream_t stream);
 
+/* llama.cpp GGUF map tensors as bf16 maps (the adapter's blk.L.ridgefill.weight / .bias tensors the
+ * reference writes and checks, code/qwen38-27b-kit/identity_projector.py:26-43, :64-80): src holds `rows`
+ * rows of `width` values of ggml type ggml_type, row stride ld_src BYTES -- F32 (0), F16 (1), Q8_0 (8:
+ * blocks of 32 values, an fp16 scale d and 32 int8 codes q, value d * q) or BF16 (30). out[i, j] =
+ * bf16(value) (round to nearest even; the values are exact in fp32). Q8_0: width % 32 == 0, src and
+ * ld_src 2-byte aligned; the others: width % 8 == 0, src and ld_src 16-byte aligned. ld_out % 8 == 0.
+ * Other ggml types: RF_EUNSUPPORTED. */
+int rf_dequant_gguf_rows(int ggml_type, const void* src, int64_t ld_src, int64_t rows, int64_t width, uint16_t* out,
+                         int64_t ld_out, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

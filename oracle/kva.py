@@ -9,6 +9,7 @@ i8_row128 expanded to bf16 maps (code/c5/convert.py:91-109).
 import json
 from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 import torch.nn.functional as F
 
@@ -42,6 +43,28 @@ def dequant_i8_row128(codes, scale, bias):
         raise ValueError(f"i8_row128 shapes {tuple(codes.shape)} {tuple(scale.shape)} {tuple(bias.shape)}")
     w = codes.to(torch.float32).view(rows, width // I8_GROUP, I8_GROUP) * scale.to(torch.float32)[:, :, None]
     return torch.cat([w.view(rows, width), bias.to(torch.float32)[:, None]], 1)
+
+
+def dequant_gguf(raw, ggml_type, width):
+    """fp32 values [rows, width] of a GGUF tensor's raw bytes raw [rows, row_bytes] (numpy uint8), as
+    ggml dequantises them: F32 as stored, F16 widened, Q8_0 blocks of 32 (an fp16 scale d, then 32 int8
+    codes q) as float(d) * q, BF16 widened (the map tensors of code/qwen38-27b-kit/identity_projector.py:
+    26-43, :64-80)."""
+    rows = raw.shape[0]
+    if ggml_type == 0:
+        v = raw.view(np.float32)
+    elif ggml_type == 1:
+        v = raw.view(np.float16).astype(np.float32)
+    elif ggml_type == 30:
+        v = (raw.view(np.uint16).astype(np.uint32) << 16).view(np.float32)
+    elif ggml_type == 8:
+        blk = raw[:, :width // 32 * 34].reshape(rows, width // 32, 34)
+        d = blk[:, :, :2].copy().view(np.float16).astype(np.float32)
+        q = blk[:, :, 2:].copy().view(np.int8).astype(np.float32)
+        v = (d * q).reshape(rows, width)
+    else:
+        raise ValueError(f"ggml type {ggml_type}")
+    return torch.from_numpy(np.ascontiguousarray(v[:, :width]))
 
 
 def projector_i8_row128(tensors, split):

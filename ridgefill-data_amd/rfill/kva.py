@@ -12,6 +12,7 @@ runs on a second stream beside layer i + 1's map apply (two_stream).
 import json
 from dataclasses import dataclass, field
 
+import numpy as np
 import torch
 
 from . import ops
@@ -144,6 +145,52 @@ def load_i8_row128(tensors, split, device="cuda"):
         B[L] = bias.to(device).contiguous()
         check_weights({f"layer.{L}": W[L]}, "load_i8_row128")
     return Projector(split, W, B, {"layout": "i8_row128"})
+
+
+def load_gguf(path, device="cuda"):
+    """The Projector of a llama.cpp adapter file (the GGUF maps of code/qwen38-27b-kit/identity_projector.py:
+    15-80): metadata adapter.ridgefill.split, .n_embd and .model_layer_types; for each late attention
+    layer L, blk.L.ridgefill.weight (F16, Q8_0, F32 or BF16, ne = [n_in, n_out]) expanded to bf16 on the
+    device (rf_dequant_gguf_rows) and blk.L.ridgefill.bias (F32) cast to bf16. Linear-attention layers
+    carry no map (the engine feeds them h_S itself); they are listed in meta["native_layers"] and their
+    blk.L.ridgefill.st corrections, read in the engines' [heads, V, K] order, are returned by
+    st_from_engine in meta["st"]. The metadata entries are kept in meta as strings."""
+    from . import gguf
+    fields, tensors = gguf.read(path)
+    for k in ("adapter.ridgefill.split", "adapter.ridgefill.n_embd", "adapter.ridgefill.model_layer_types"):
+        if k not in fields:
+            raise ValueError(f"{path}: metadata {k!r} missing (not a RidgeFill adapter)")
+    split, n = int(fields["adapter.ridgefill.split"]), int(fields["adapter.ridgefill.n_embd"])
+    kinds = str(fields["adapter.ridgefill.model_layer_types"]).split()
+    W, B, native, st = {}, {}, [], {}
+    dev = torch.device(device)
+
+    def expand(t, rows, width):
+        raw = torch.from_numpy(np.array(t.data)).to(dev)
+        return ops.dequant_gguf_rows(raw, t.ggml_type, width).view(rows, width)
+
+    for L in range(split, len(kinds)):
+        base = f"blk.{L}.ridgefill."
+        if kinds[L] == "linear_attention":
+            native.append(L)
+            if base + "st" in tensors:
+                t = tensors[base + "st"]
+                if t.ggml_type != gguf.GGML_F32 or len(t.ne) != 3:
+                    raise ValueError(f"{path}: {base}st must be F32 [heads, V, K]")
+                st[L] = torch.from_numpy(np.array(t.data).view(np.float32).reshape(t.shape))
+            continue
+        w, b = tensors.get(base + "weight"), tensors.get(base + "bias")
+        if w is None or b is None:
+            raise ValueError(f"{path}: layer {L} ({kinds[L]}) has no {base}weight / {base}bias")
+        if len(w.ne) != 2 or w.ne[0] != n or b.ne != (w.ne[1],) or b.ggml_type != gguf.GGML_F32:
+            raise ValueError(f"{path}: layer {L}: weight dims {w.ne} (expected [{n}, n_out]), bias dims {b.ne} "
+                             f"type {b.ggml_type} (expected F32 [n_out])")
+        W[L] = expand(w, w.ne[1], w.ne[0])
+        B[L] = expand(b, 1, b.ne[0]).view(-1)
+    check_weights({f"layer.{L}": torch.cat((W[L].float(), B[L].float()[:, None]), 1) for L in W}, str(path))
+    meta = {k: str(v) for k, v in fields.items() if k.startswith("adapter.") or k == "general.architecture"}
+    meta.update(split=str(split), native_layers=native, st=st_from_engine(st) if st else {})
+    return Projector(split, W, B, meta)
 
 
 def st_from_engine(st):

@@ -459,6 +459,25 @@ def dequant_i8_rows(codes, scale, group=128, out=None):
     return out
 
 
+GGML_F32, GGML_F16, GGML_Q8_0, GGML_BF16 = 0, 1, 8, 30
+
+
+def dequant_gguf_rows(raw, ggml_type, width, out=None):
+    """bf16 rows [rows, width] from the raw bytes raw [rows, >= row bytes] (uint8, on the device) of a
+    GGUF tensor of ggml type F32, F16, Q8_0 (32-value blocks: fp16 scale, 32 int8 codes) or BF16; values
+    exact in fp32, one round-to-nearest-even cast to bf16."""
+    _need(raw, "raw", torch.uint8, 2)
+    rows = raw.shape[0]
+    if out is None:
+        out = torch.empty(rows, width, dtype=torch.bfloat16, device=raw.device)
+    _need(out, "out", torch.bfloat16, 2)
+    if tuple(out.shape) != (rows, width):
+        raise ValueError(f"dequant_gguf_rows: out {tuple(out.shape)}, expected {(rows, width)}")
+    _lib.call("rf_dequant_gguf_rows", int(ggml_type), _ptr(raw), raw.stride(0), rows, width, _ptr(out), out.stride(0),
+              _stream(raw))
+    return out
+
+
 # ------------------------------------------------------------------------ host-side RoPE frequencies
 
 def inv_freq_default(theta, rot_dim):
