@@ -130,7 +130,7 @@ int rf_norm_q(const uint16_t* x, int64_t ldx, const float* ssq, int64_t rows, in
  * < cache_rows) over the cache kbuf / vbuf [hkv, cap, d] (element strides head_stride / row_stride): query
  * j sees keys 0 .. qpos[j]; scores in fp32 scaled by `scale`, softmax in fp32, probabilities as bf16 into
  * the second product. Writes out [nq, hq d] (row stride ldo). Replaces ops.attend_at / attend_rows
- * (code/kva/ops.py:131-170) in layer_rows. Needs d 64 or 128 and hq / hkv dividing 64. With a workspace
+ * (code/kva/ops.py:131-170) in layer_rows. Needs d 64, 128 or 256 and hq / hkv dividing 64. With a workspace
  * (caller-owned device memory, 16-byte aligned) the key range is split over more blocks and the splits are
  * merged in a fixed order (rf_attend_rows_workspace_bytes gives the size for the full split; a smaller one
  * gives fewer splits, NULL none). */
@@ -198,6 +198,31 @@ int rf_gdn_fill(const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int 
 /* Workspace bytes rf_gdn_fill needs to fill `rows` rows in one pass (rows = 0: the one-chunk minimum).
  * Host-only; no device work. */
 int rf_gdn_workspace_bytes(int64_t rows, int nk, int nv, int dk, int dv, size_t* bytes);
+
+/* The exact GDN layer's mixing (Qwen35._gdn_core with need_out = True, code/kva/model.py:452-484 and
+ * ops.py:199-262): as rf_gdn_fill (state and conv state continued over the P rows), and also the
+ * delta-rule outputs out [P, nv dv] bf16 (row stride ldo): per chunk o = Qd S + P v_new, Qd = q_n e^gamma,
+ * P = tril(q_n k_n^T e^{gamma_i - gamma_j}), q_n = l2norm(conv q) dk^-1/2, with S the state before the chunk
+ * (stored by the scan) -- fp32 throughout, rounded once to bf16. Workspace: rf_gdn_forward_workspace_bytes
+ * (a smaller one of at least one chunk's worth gives several passes with the same result). */
+int rf_gdn_forward(const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int dk, int dv,
+                   const uint16_t* conv_w, const uint16_t* conv_in, uint16_t* conv_out, const float* a_log,
+                   const float* dt_bias, float* state, uint16_t* out, int64_t ldo, void* workspace, size_t ws_bytes,
+                   hipStream_t stream);
+
+/* Workspace bytes rf_gdn_forward needs for `rows` rows in one pass (rows = 0: one chunk). Host-only. */
+int rf_gdn_forward_workspace_bytes(int64_t rows, int nk, int nv, int dk, int dv, size_t* bytes);
+
+/* Qwen3.5's attention output gate (code/kva/model.py:444-445, o * torch.sigmoid(gate) in bf16):
+ * out = bf16(o * bf16(sigmoid(g))) over rows x n values (n % 8 == 0; strides % 8 == 0; out may alias o). */
+int rf_sigmoid_mul(const uint16_t* o, int64_t ldo, const uint16_t* g, int64_t ldg, int64_t rows, int64_t n,
+                   uint16_t* out, int64_t ld_out, hipStream_t stream);
+
+/* The GDN output norm (ops.rms_norm_gated, code/kva/ops.py:28-33; code/kva/model.py:494-499) over rows x
+ * heads vectors of dv values: y = bf16(bf16(weight * bf16(x / sqrt(mean(x^2) + eps))) * silu(z)), silu in
+ * fp32. weight [dv] bf16; dv 64, 128 or 256; strides % 8 == 0. */
+int rf_gated_rms_norm(const uint16_t* x, int64_t ldx, const uint16_t* z, int64_t ldz, const uint16_t* weight,
+                      int64_t rows, int heads, int dv, float eps, uint16_t* y, int64_t ldy, hipStream_t stream);
 
 /* ---- closed-form fit (code/kva/ridge.py:19-105, code/scripts/fit_sweep.py:87-144) ---- */
 

@@ -1,6 +1,6 @@
 // Exact-row attention for gfx950: causal attention of a few query rows at arbitrary sorted positions
 // over the filled K / V cache of one layer (the attention of Model.layer_rows, code/kva/ops.py:131-155
-// attend_at / :158-170 attend_rows), head_dim 64 or 128, grouped-query heads.
+// attend_at / :158-170 attend_rows), head_dim 64, 128 or 256, grouped-query heads.
 //
 // A block takes one K / V head and 64 query rows: 64 / rep queries x the rep query heads that share the
 // K / V head (rep = hq / hkv). Wave w owns query rows 16w .. 16w + 15. The keys 0 .. (last query's
@@ -55,7 +55,7 @@ __device__ __forceinline__ float* part_block(const AttnArgs& a, int qblock, int 
   return a.part + ((static_cast<int64_t>(qblock) * a.hkv + hk) * gridDim.z + split) * (64 * AD + 128);
 }
 
-// AD = head_dim (64 or 128); K tile rows are AD + 8 bf16 apart in LDS (conflict-free fragment reads).
+// AD = head_dim (64, 128 or 256); K tile rows are AD + 8 bf16 apart in LDS (conflict-free fragment reads).
 template <int AD>
 __global__ __launch_bounds__(256) void k_attend_rows(AttnArgs a) {
   constexpr int KROW = AD + 8, NS = AD / 32, NB = AD / 16, CPR = AD / 8;   // d steps, d blocks, chunks per row
@@ -308,6 +308,61 @@ namespace rf {
 namespace {
 // Key-range splits for nq queries: enough blocks for about three per CU, at most one split per key tile,
 // at most 32, and what the workspace holds.
+// Qwen3.5's attention output gate (code/kva/model.py:444-445, o * torch.sigmoid(gate) in bf16): out =
+// bf16(o * bf16(sigmoid(g))), 8 values per thread.
+__global__ __launch_bounds__(256) void k_sigmoid_mul(const uint16_t* __restrict__ o, int64_t ldo,
+                                                     const uint16_t* __restrict__ g, int64_t ldg, int64_t rows, int n,
+                                                     uint16_t* __restrict__ out, int64_t ld_out) {
+  const int64_t cpr = n / 8, idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= rows * cpr) return;
+  const int64_t r = idx / cpr, c = (idx - r * cpr) * 8;
+  const uint4 ov = *reinterpret_cast<const uint4*>(o + r * ldo + c);
+  const uint4 gv = *reinterpret_cast<const uint4*>(g + r * ldg + c);
+  uint16_t res[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float sg = bf2f(f2bf(1.0f / (1.0f + expf(-bf2f(lane_of(gv, e))))));
+    res[e] = f2bf(bf2f(lane_of(ov, e)) * sg);
+  }
+  *reinterpret_cast<uint4*>(out + r * ld_out + c) =
+      make_uint4(pack2(res[0], res[1]), pack2(res[2], res[3]), pack2(res[4], res[5]), pack2(res[6], res[7]));
+}
+
+// The GDN output norm (ops.rms_norm_gated, code/kva/ops.py:28-33) per (row, head) of dv values:
+// y = bf16(w * bf16(x / sqrt(mean(x^2) + eps))), out = bf16(y * silu(z)) with silu(z) = z / (1 + e^-z) in
+// fp32. dv / 8 lanes per (row, head), 8 values each; every lane of a group reaches the shuffles.
+__global__ __launch_bounds__(256) void k_gated_norm(const uint16_t* __restrict__ x, int64_t ldx,
+                                                    const uint16_t* __restrict__ z, int64_t ldz,
+                                                    const uint16_t* __restrict__ wt, int64_t rows, int heads, int dv,
+                                                    float eps, uint16_t* __restrict__ y, int64_t ldy) {
+  const int g = dv / 8, t = threadIdx.x, sub = t % g;
+  const int64_t item = static_cast<int64_t>(blockIdx.x) * (256 / g) + t / g;
+  const bool ok = item < rows * heads;
+  const int64_t r = ok ? item / heads : 0;
+  const int64_t col = (ok ? item % heads : 0) * dv + sub * 8;
+  const uint4 xv = *reinterpret_cast<const uint4*>(x + r * ldx + col);
+  float xf[8], s = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    xf[e] = bf2f(lane_of(xv, e));
+    s = fmaf(xf[e], xf[e], s);
+  }
+  for (int m = g >> 1; m >= 1; m >>= 1) s += __shfl_xor(s, m);
+  if (!ok) return;
+  const float inv = 1.0f / sqrtf(s / static_cast<float>(dv) + eps);
+  const uint4 zv = *reinterpret_cast<const uint4*>(z + r * ldz + col);
+  const uint4 wv = *reinterpret_cast<const uint4*>(wt + sub * 8);
+  uint16_t res[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float yv = bf2f(f2bf(bf2f(lane_of(wv, e)) * bf2f(f2bf(xf[e] * inv))));
+    const float zf = bf2f(lane_of(zv, e));
+    res[e] = f2bf(yv * (zf / (1.0f + expf(-zf))));
+  }
+  *reinterpret_cast<uint4*>(y + r * ldy + col) =
+      make_uint4(pack2(res[0], res[1]), pack2(res[2], res[3]), pack2(res[4], res[5]), pack2(res[6], res[7]));
+}
+
 int attend_splits(int64_t nq, int hq, int hkv, int d, int64_t cache_rows, size_t ws_bytes) {
   const int64_t qb = 64 / (hq / hkv);
   const int64_t blocks = (nq + qb - 1) / qb * hkv;
@@ -321,7 +376,7 @@ int attend_splits(int64_t nq, int hq, int hkv, int d, int64_t cache_rows, size_t
 }  // namespace rf
 
 extern "C" int rf_attend_rows_workspace_bytes(int64_t nq, int hq, int hkv, int d, int64_t cache_rows, size_t* bytes) {
-  if (!bytes || nq < 0 || hq <= 0 || hkv <= 0 || hq % hkv || 64 % (hq / hkv) || (d != 64 && d != 128))
+  if (!bytes || nq < 0 || hq <= 0 || hkv <= 0 || hq % hkv || 64 % (hq / hkv) || (d != 64 && d != 128 && d != 256))
     return fail(RF_EINVAL_ARG, "rf_attend_rows_workspace_bytes: arguments");
   const int ns = attend_splits(nq, hq, hkv, d, cache_rows, SIZE_MAX);
   const int64_t qb = 64 / (hq / hkv);
@@ -334,7 +389,8 @@ extern "C" int rf_attend_rows(const uint16_t* q, int64_t ldq, const int64_t* qpo
                               int64_t row_stride, int64_t cache_rows, float scale, uint16_t* out, int64_t ldo,
                               void* workspace, size_t ws_bytes, hipStream_t stream) {
   if (!q || !qpos || !kbuf || !vbuf || !out) return fail(RF_EINVAL_ARG, "rf_attend_rows: null pointer");
-  if (d != 64 && d != 128) return fail(RF_EUNSUPPORTED, "rf_attend_rows: head_dim %d (the kernel takes 64, 128)", d);
+  if (d != 64 && d != 128 && d != 256)
+    return fail(RF_EUNSUPPORTED, "rf_attend_rows: head_dim %d (the kernel takes 64, 128, 256)", d);
   if (hq <= 0 || hkv <= 0 || hq % hkv || 64 % (hq / hkv))
     return fail(RF_EUNSUPPORTED, "rf_attend_rows: %d query heads over %d K / V heads (need a group of at most 64 "
                 "dividing 64)", hq, hkv);
@@ -351,13 +407,15 @@ extern "C" int rf_attend_rows(const uint16_t* q, int64_t ldq, const int64_t* qpo
              static_cast<float*>(workspace)};
   const int qb = 64 / (hq / hkv);
   const dim3 grid(static_cast<unsigned>((nq + qb - 1) / qb), static_cast<unsigned>(hkv), static_cast<unsigned>(ns));
-  if (d == 128) hipLaunchKernelGGL(k_attend_rows<128>, grid, dim3(256), 0, stream, a);
+  if (d == 256) hipLaunchKernelGGL(k_attend_rows<256>, grid, dim3(256), 0, stream, a);
+  else if (d == 128) hipLaunchKernelGGL(k_attend_rows<128>, grid, dim3(256), 0, stream, a);
   else hipLaunchKernelGGL(k_attend_rows<64>, grid, dim3(256), 0, stream, a);
   if (ns > 1) {
     const int st = check_launch("rf_attend_rows");
     if (st != RF_OK) return st;
     const dim3 g2(grid.x, grid.y);
-    if (d == 128) hipLaunchKernelGGL(k_attend_combine<128>, g2, dim3(256), 0, stream, a, ns);
+    if (d == 256) hipLaunchKernelGGL(k_attend_combine<256>, g2, dim3(256), 0, stream, a, ns);
+    else if (d == 128) hipLaunchKernelGGL(k_attend_combine<128>, g2, dim3(256), 0, stream, a, ns);
     else hipLaunchKernelGGL(k_attend_combine<64>, g2, dim3(256), 0, stream, a, ns);
   }
   return check_launch("rf_attend_rows");
@@ -387,4 +445,37 @@ extern "C" int rf_silu_mul(const uint16_t* gu, int64_t ldg, int64_t rows, int64_
   hipLaunchKernelGGL(k_silu_mul, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, stream, gu, ldg, rows,
                      static_cast<int>(I), act, lda);
   return check_launch("rf_silu_mul");
+}
+
+extern "C" int rf_sigmoid_mul(const uint16_t* o, int64_t ldo, const uint16_t* g, int64_t ldg, int64_t rows, int64_t n,
+                              uint16_t* out, int64_t ld_out, hipStream_t stream) {
+  if (!o || !g || !out) return fail(RF_EINVAL_ARG, "rf_sigmoid_mul: null pointer");
+  if (rows < 0 || n <= 0 || n % 8 || n > (1 << 30) || ldo < n || ldg < n || ld_out < n || ldo % 8 || ldg % 8 ||
+      ld_out % 8)
+    return fail(RF_EINVAL_SHAPE, "rf_sigmoid_mul: rows %lld, n %lld (multiple of 8), strides", (long long)rows,
+                (long long)n);
+  if (!aligned16(o) || !aligned16(g) || !aligned16(out)) return fail(RF_EINVAL_SHAPE, "rf_sigmoid_mul: alignment");
+  if (rows == 0) return RF_OK;
+  const int64_t total = rows * (n / 8);
+  hipLaunchKernelGGL(k_sigmoid_mul, dim3(static_cast<unsigned>((total + 255) / 256)), dim3(256), 0, stream, o, ldo, g,
+                     ldg, rows, static_cast<int>(n), out, ld_out);
+  return check_launch("rf_sigmoid_mul");
+}
+
+extern "C" int rf_gated_rms_norm(const uint16_t* x, int64_t ldx, const uint16_t* z, int64_t ldz, const uint16_t* weight,
+                                 int64_t rows, int heads, int dv, float eps, uint16_t* y, int64_t ldy,
+                                 hipStream_t stream) {
+  if (!x || !z || !weight || !y) return fail(RF_EINVAL_ARG, "rf_gated_rms_norm: null pointer");
+  if (rows < 0 || heads <= 0 || (dv != 64 && dv != 128 && dv != 256) || ldx < static_cast<int64_t>(heads) * dv ||
+      ldz < static_cast<int64_t>(heads) * dv || ldy < static_cast<int64_t>(heads) * dv || ldx % 8 || ldz % 8 ||
+      ldy % 8)
+    return fail(RF_EINVAL_SHAPE, "rf_gated_rms_norm: rows %lld, heads %d, dv %d (64, 128 or 256), strides",
+                (long long)rows, heads, dv);
+  if (!aligned16(x) || !aligned16(z) || !aligned16(weight) || !aligned16(y))
+    return fail(RF_EINVAL_SHAPE, "rf_gated_rms_norm: alignment");
+  if (rows == 0) return RF_OK;
+  const int64_t items = rows * heads, per = 256 / (dv / 8);
+  hipLaunchKernelGGL(k_gated_norm, dim3(static_cast<unsigned>((items + per - 1) / per)), dim3(256), 0, stream, x, ldx,
+                     z, ldz, weight, rows, heads, dv, eps, y, ldy);
+  return check_launch("rf_gated_rms_norm");
 }

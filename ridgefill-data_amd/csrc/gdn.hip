@@ -22,6 +22,12 @@
 //     products four ways and meet three times per chunk in LDS (X partials, Y, Z); the next chunk's
 //     operands load into registers meanwhile.
 // k_conv_tail writes the new conv state (the last 3 pre-conv rows of [conv_in; pre]).
+//
+// With outputs (rf_gdn_forward: the exact layer, ops.py:199-262 with need_out = True), per chunk and value
+// head o = Qd S_prev + P v_new with Qd = q_n e^gamma, P = tril(q_n k_n^T e^{gamma_i - gamma_j}) (q_n, k_n
+// the l2-normed conv outputs, q_n scaled by dk^-1/2) and v_new = T Y of the state before the chunk. The
+// prep also writes Qd, P, T, K and V in plain layouts, the scan stores the state before each chunk, and
+// k_gdn_out (chunk x value head) forms the outputs for all chunks in parallel on fp32 MFMA.
 #include <algorithm>
 
 #include "rf_common.h"
@@ -42,6 +48,10 @@ constexpr uint32_t KH_BYTES = KP_BYTES + KTP_BYTES;
 constexpr uint32_t VH_BYTES = TP_BYTES + VP_BYTES + SC_BYTES;
 // scalar block: beta [64], q = e^gamma r [64], z = r e^{gamma_last - gamma} [64], decay e^{gamma_last}
 constexpr int SC_BETA = 0, SC_Q = 64, SC_Z = 128, SC_DECAY = 192;
+// output region per (chunk, value head), after the chunk's scan operands: the state before the chunk
+// S [DK][DV] fp32, Qd [CH][DK] fp32, P [CH][CH] fp32, T [CH][CH] fp32, K [CH][DK] bf16, V [CH][DV] bf16
+constexpr uint32_t OS_S = 0, OS_QD = 65536, OS_P = 98304, OS_T = 114688, OS_K = 131072, OS_V = 147456;
+constexpr uint32_t OUT_HEAD_BYTES = 163840;
 
 __device__ __forceinline__ int kperm(int s, int g, int e) { return 32 * s + 4 * g + (e & 3) + ((e >> 2) << 4); }
 
@@ -71,6 +81,7 @@ struct PrepArgs {
   const float* dt_bias;
   uint8_t* ws;
   uint32_t chunk_bytes;
+  uint32_t out_off;         // the output region's offset in a chunk (prep with outputs)
 };
 
 // 8 channels [ch0, ch0 + 8) of input row p (relative to the call's first row); rows before 0 come from
@@ -142,11 +153,14 @@ __device__ __forceinline__ float quad_sum(float v) {
 
 // Block = (chunk, value head h). The K-side work (conv of the key head's k, norms, G = K K^T) is
 // recomputed by each of the key head's value heads; the first of them writes K's operand orders.
+template <bool OUT>
 __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
   __shared__ __align__(16) uint16_t k_s[CH * KST];  // the k tile, then T (fp32)
   __shared__ __align__(16) uint16_t v_s[CH * KST];
   __shared__ __align__(16) float a_s[CH * FST];     // A
   __shared__ float r_s[CH], beta_s[CH], gate_s[CH], gam_s[CH];
+  __shared__ __align__(16) uint16_t q_s[OUT ? CH * KST : 8];   // the q tile (outputs only)
+  __shared__ float rq_s[OUT ? CH : 1];
 
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6, gi = lane >> 4, ln = lane & 15;
   const int c = blockIdx.x, h = blockIdx.y, rep = a.nv / a.nk, kh = h / rep;
@@ -168,6 +182,12 @@ __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
     conv_store(ik, m, k_s);
     conv_store(iv, m, v_s);
   }
+  if constexpr (OUT) {
+    ConvIn iq;
+    conv_load(a, p0, kh * DK, iq);
+    conv_store(iq, m, q_s);
+  }
+  uint8_t* obase = cbase + a.out_off + static_cast<size_t>(h) * OUT_HEAD_BYTES;
   if (t < CH) {
     float beta = 0.f, g = 0.f;
     if (t < m) {
@@ -189,6 +209,16 @@ __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
     s += __shfl_xor(s, 1, 64);
     s += __shfl_xor(s, 2, 64);
     if ((t & 3) == 0) r_s[row] = 1.0f / sqrtf(s + 1e-6f);
+    if constexpr (OUT) {
+      float sq = 0.f;
+      for (int e = 0; e < 32; ++e) {
+        const float f = bf2f(q_s[row * KST + q + e]);
+        sq = fmaf(f, f, sq);
+      }
+      sq += __shfl_xor(sq, 1, 64);
+      sq += __shfl_xor(sq, 2, 64);
+      if ((t & 3) == 0) rq_s[row] = 1.0f / sqrtf(sq + 1e-6f);
+    }
   }
   if (t < CH) {  // gamma_t = gate_0 + ... + gate_t, added in row order (the serial cumsum's bits)
     float acc = 0.f;
@@ -206,6 +236,28 @@ __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
       const uint4 ua = *reinterpret_cast<const uint4*>(k_s + (16 * wave + ln) * KST + 32 * s + 8 * gi);
       const uint4 ub = *reinterpret_cast<const uint4*>(k_s + (16 * tj + ln) * KST + 32 * s + 8 * gi);
       G[tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(ua), as_frag(ub), G[tj], 0, 0, 0);
+    }
+  }
+  // outputs: QK = Q K^T (raw conv outputs, exact bf16 products), lower tiles of tile row `wave`, and the
+  // plain K tile
+  f32x4 QK[4];
+  if constexpr (OUT) {
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj) {
+      QK[tj] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (tj > wave) continue;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const uint4 ua = *reinterpret_cast<const uint4*>(q_s + (16 * wave + ln) * KST + 32 * s + 8 * gi);
+        const uint4 ub = *reinterpret_cast<const uint4*>(k_s + (16 * tj + ln) * KST + 32 * s + 8 * gi);
+        QK[tj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_frag(ua), as_frag(ub), QK[tj], 0, 0, 0);
+      }
+    }
+    uint4* ko = reinterpret_cast<uint4*>(obase + OS_K);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int idx = t + 256 * k, row = idx >> 4, cc = idx & 15;
+      ko[idx] = *reinterpret_cast<const uint4*>(k_s + row * KST + cc * 8);
     }
   }
   if (h % rep == 0) {  // K in the scan's operand orders: Kp [it][s][lane][8] = K[16 it + lane % 16][kperm(s, g, e)],
@@ -231,6 +283,25 @@ __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
     }
   }
   __syncthreads();                                  // r_s, gam_s ready; k_s free
+  if constexpr (OUT) {
+    // Qd[i][e] = q_i[e] rq_i dk^-1/2 e^{gamma_i}; P[i][j] = QK_ij rq_i dk^-1/2 r_j e^{gamma_i - gamma_j}, j <= i
+    const float qscale = 0.08838834764831845f;      // 128^-1/2
+    float* qd = reinterpret_cast<float*>(obase + OS_QD);
+    for (int idx = t; idx < CH * DK; idx += 256) {
+      const int i = idx >> 7, e = idx & 127;
+      qd[idx] = bf2f(q_s[i * KST + e]) * rq_s[i] * qscale * expf(gam_s[i]);
+    }
+    float* pm = reinterpret_cast<float*>(obase + OS_P);
+#pragma unroll
+    for (int tj = 0; tj < 4; ++tj)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int i = 16 * wave + 4 * gi + r, j = 16 * tj + ln;
+        pm[i * CH + j] = (tj <= wave && j <= i)
+                             ? ((QK[tj][r] * rq_s[i] * qscale) * r_s[j]) * expf(gam_s[i] - gam_s[j])
+                             : 0.f;
+      }
+  }
   // A = tril_{-1}(beta_i (G_ij r_i r_j) e^{gamma_i - gamma_j}); lane (gi, ln) holds G[16 wave + 4 gi + r][16 tj + ln]
 #pragma unroll
   for (int tj = 0; tj < 4; ++tj)
@@ -254,6 +325,14 @@ __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
         for (int r = 0; r < 4; ++r) v[4 * it + r] = v_s[(16 * it + 4 * g + r) * KST + 16 * cb + n];
       vp[2 * idx] = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
       vp[2 * idx + 1] = make_uint4(pack2(v[8], v[9]), pack2(v[10], v[11]), pack2(v[12], v[13]), pack2(v[14], v[15]));
+    }
+  }
+  if constexpr (OUT) {
+    uint4* vo = reinterpret_cast<uint4*>(obase + OS_V);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int idx = t + 256 * k, row = idx >> 4, cc = idx & 15;
+      vo[idx] = *reinterpret_cast<const uint4*>(v_s + row * KST + cc * 8);
     }
   }
   if (wave == 1) {
@@ -314,6 +393,10 @@ __global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
     }
     __syncthreads();
   }
+  if constexpr (OUT) {
+    float* to = reinterpret_cast<float*>(obase + OS_T);
+    for (int idx = t; idx < CH * CH; idx += 256) to[idx] = t_s[(idx >> 6) * FST + (idx & 63)];
+  }
   {  // T split hi / lo in the scan's A-operand order: Tp [it][s][hl][lane][8] = T[16 it + lane % 16][kperm(s, g, e)]
     uint4* tp = reinterpret_cast<uint4*>(vbase);
 #pragma unroll
@@ -335,6 +418,8 @@ struct ScanArgs {
   uint32_t chunk_bytes;
   int chunks, nk, nv;
   float* state;             // [nv, DK, DV] fp32, updated in place
+  uint8_t* out_ws;          // outputs: the workspace again (written: the state before each chunk)
+  uint32_t out_off;
 };
 
 // One chunk's operands for wave w of a scan block, straight from the workspace into registers.
@@ -407,6 +492,7 @@ __device__ __forceinline__ void split4(const float (&x)[4], uint2& hi, uint2& lo
 //   hi / lo bf16 B-operand frags through LDS; S_w <- decay S_w + K^T[32w .., :] Z.
 // Three barriers per chunk; the operands of the chunk two steps ahead load into registers meanwhile,
 // in four groups between the phases so the address unit streams them in the background.
+template <bool OUT>
 __global__ __launch_bounds__(256) void k_gdn_scan(ScanArgs a) {
   __shared__ __align__(16) f32x4 xp[4][4][64];        // X_w partials [wave][row tile][lane]
   __shared__ __align__(16) uint4 yf[2][2][64];        // Y frags [k-step][hi / lo][lane]
@@ -428,7 +514,17 @@ __global__ __launch_bounds__(256) void k_gdn_scan(ScanArgs a) {
   // One chunk step from its operands o; the four load groups of the chunk two steps on go out between
   // the phases into L (the buffer the previous step freed). Past the last chunk (active false) only the
   // loads run, so every path issues the same loads and waits on the same counts.
-  auto step = [&](const ScanOps& o, ScanOps& L, const ScanSrc& from, bool active) {
+  auto step = [&](const ScanOps& o, ScanOps& L, const ScanSrc& from, bool active, int cidx) {
+    if constexpr (OUT) {
+      if (active) {                                 // the state before chunk cidx, for the outputs
+        float* sp = reinterpret_cast<float*>(a.out_ws + static_cast<size_t>(cidx) * a.chunk_bytes + a.out_off +
+                                             static_cast<size_t>(h) * OUT_HEAD_BYTES + OS_S) + cb * 16 + ln;
+#pragma unroll
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sp[(16 * (2 * w + j) + 4 * gi + r) * DV] = S[j][r];
+      }
+    }
     if (active) {
       // X_w = K[:, 32w ..] S_w: S_w's rows in k-step order are (tile 2w, r) then (tile 2w + 1, r)
       {
@@ -532,14 +628,111 @@ __global__ __launch_bounds__(256) void k_gdn_scan(ScanArgs a) {
     load_part(b1, src(1), part, cb, w, lane);
   }
   for (int c = 0; c < a.chunks; c += 3) {
-    step(b0, b2, src(c + 2), true);
-    step(b1, b0, src(c + 3), c + 1 < a.chunks);
-    step(b2, b1, src(c + 4), c + 2 < a.chunks);
+    step(b0, b2, src(c + 2), true, c);
+    step(b1, b0, src(c + 3), c + 1 < a.chunks, c + 1);
+    step(b2, b1, src(c + 4), c + 2 < a.chunks, c + 2);
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int r = 0; r < 4; ++r) st[(16 * (2 * w + j) + 4 * gi + r) * DV] = S[j][r];
+}
+
+struct OutArgs {
+  const uint8_t* ws;
+  uint32_t chunk_bytes, out_off;
+  int nk;
+  int64_t P, p_begin;
+  uint16_t* out;            // [P, >= nv DV] bf16
+  int64_t ldo;
+};
+
+constexpr int SST = DV + 4;                        // fp32 row stride of S and Y in LDS
+
+// Block = (chunk, value head h); wave w forms output rows 16w .. 16w + 15 of the chunk. On
+// v_mfma_f32_16x16x4f32 (lane l feeds A[l % 16][l / 16] and B[l / 16][l % 16], holds D[4 (l / 16) + r][l % 16]):
+//   X = K S, Y = beta (V - q X) (q = e^gamma r), v_new = T Y, O = Qd S + P v_new
+// with S the state before the chunk (LDS), Y then v_new shared through LDS; fp32 throughout, bf16 out.
+// T and P are lower triangular, but their products run over all 16 k-steps: a trip count taken from the
+// wave index (uniform per wave, which the compiler cannot see) gave wrong products here.
+__global__ __launch_bounds__(256) void k_gdn_out(OutArgs a) {
+  __shared__ __align__(16) float s_l[DK * SST];
+  __shared__ __align__(16) float y_l[CH * SST];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6, lr = lane & 15, lk = lane >> 4;
+  const int c = blockIdx.x, h = blockIdx.y;
+  const uint8_t* chunk = a.ws + static_cast<size_t>(c) * a.chunk_bytes;
+  const uint8_t* ob = chunk + a.out_off + static_cast<size_t>(h) * OUT_HEAD_BYTES;
+  const float* S = reinterpret_cast<const float*>(ob + OS_S);
+  const float* Qd = reinterpret_cast<const float*>(ob + OS_QD);
+  const float* Pm = reinterpret_cast<const float*>(ob + OS_P);
+  const float* T = reinterpret_cast<const float*>(ob + OS_T);
+  const uint16_t* K = reinterpret_cast<const uint16_t*>(ob + OS_K);
+  const uint16_t* V = reinterpret_cast<const uint16_t*>(ob + OS_V);
+  const float* sc = reinterpret_cast<const float*>(chunk + static_cast<size_t>(a.nk) * KH_BYTES +
+                                                   static_cast<size_t>(h) * VH_BYTES + TP_BYTES + VP_BYTES);
+  for (int i = t; i < DK * DV / 4; i += 256) {
+    const int row = i / (DV / 4), c4 = i % (DV / 4);
+    *reinterpret_cast<float4*>(s_l + row * SST + 4 * c4) = reinterpret_cast<const float4*>(S)[i];
+  }
+  __syncthreads();
+  const int r0 = 16 * w;
+  f32x4 acc[8];
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int ks = 0; ks < DK / 4; ++ks) {             // X = K S
+    const float av = bf2f(K[(r0 + lr) * DK + 4 * ks + lk]);
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, s_l[(4 * ks + lk) * SST + 16 * nt + lr], acc[nt], 0, 0, 0);
+  }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {                     // Y = beta (V - q X)
+    const int i = r0 + 4 * lk + r;
+    const float be = sc[SC_BETA + i], qs = sc[SC_Q + i];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const int col = 16 * nt + lr;
+      y_l[i * SST + col] = be * (bf2f(V[i * DV + col]) - qs * acc[nt][r]);
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int ks = 0; ks < CH / 4; ++ks) {             // v_new = T Y
+    const float av = T[(r0 + lr) * CH + 4 * ks + lk];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, y_l[(4 * ks + lk) * SST + 16 * nt + lr], acc[nt], 0, 0, 0);
+  }
+  __syncthreads();                                  // every wave has read Y
+#pragma unroll
+  for (int r = 0; r < 4; ++r)
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) y_l[(r0 + 4 * lk + r) * SST + 16 * nt + lr] = acc[nt][r];
+  __syncthreads();
+#pragma unroll
+  for (int nt = 0; nt < 8; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int ks = 0; ks < DK / 4; ++ks) {             // O = Qd S ...
+    const float av = Qd[(r0 + lr) * DK + 4 * ks + lk];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, s_l[(4 * ks + lk) * SST + 16 * nt + lr], acc[nt], 0, 0, 0);
+  }
+  for (int ks = 0; ks < CH / 4; ++ks) {             // ... + P v_new
+    const float av = Pm[(r0 + lr) * CH + 4 * ks + lk];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt)
+      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, y_l[(4 * ks + lk) * SST + 16 * nt + lr], acc[nt], 0, 0, 0);
+  }
+  const int64_t p0 = a.p_begin + static_cast<int64_t>(c) * CH;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int64_t p = p0 + r0 + 4 * lk + r;
+    if (p >= a.P) continue;
+    uint16_t* dst = a.out + p * a.ldo + static_cast<int64_t>(h) * DV + lr;
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) dst[16 * nt] = f2bf(acc[nt][r]);
+  }
 }
 
 // conv_out[j][ch] = row P - 3 + j of [conv_in; pre] (conv_in rows -3..-1; zeros if conv_in is null)
@@ -576,36 +769,79 @@ extern "C" int rf_gdn_workspace_bytes(int64_t rows, int nk, int nv, int dk, int 
   return RF_OK;
 }
 
-extern "C" int rf_gdn_fill(const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int dk, int dv,
-                           const uint16_t* conv_w, const uint16_t* conv_in, uint16_t* conv_out, const float* a_log,
-                           const float* dt_bias, float* state, void* workspace, size_t ws_bytes, hipStream_t stream) {
+extern "C" int rf_gdn_forward_workspace_bytes(int64_t rows, int nk, int nv, int dk, int dv, size_t* bytes) {
+  if (const int e = check_heads("rf_gdn_forward_workspace_bytes", nk, nv, dk, dv)) return e;
+  if (rows < 0 || !bytes) return fail(RF_EINVAL_ARG, "rf_gdn_forward_workspace_bytes: rows %lld", (long long)rows);
+  const int64_t chunks = rows > 0 ? (rows + CH - 1) / CH : 1;
+  *bytes = static_cast<size_t>(chunks) * (chunk_bytes(nk, nv) + static_cast<size_t>(nv) * OUT_HEAD_BYTES);
+  return RF_OK;
+}
+
+namespace {
+
+int gdn_run(const char* fn, const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int dk, int dv,
+            const uint16_t* conv_w, const uint16_t* conv_in, uint16_t* conv_out, const float* a_log,
+            const float* dt_bias, float* state, uint16_t* out, int64_t ldo, void* workspace, size_t ws_bytes,
+            hipStream_t stream) {
   if (!pre || !conv_w || !conv_out || !a_log || !dt_bias || !state || !workspace)
-    return fail(RF_EINVAL_ARG, "rf_gdn_fill: null pointer");
-  if (const int e = check_heads("rf_gdn_fill", nk, nv, dk, dv)) return e;
+    return fail(RF_EINVAL_ARG, "%s: null pointer", fn);
+  if (const int e = check_heads(fn, nk, nv, dk, dv)) return e;
   const int64_t C = 2ll * nk * DK + static_cast<int64_t>(nv) * DV;
   if (P < 0 || ld < C + 2 * nv || ld % 8)
-    return fail(RF_EINVAL_SHAPE, "rf_gdn_fill: P %lld, ld %lld (need >= %lld and a multiple of 8)", (long long)P,
+    return fail(RF_EINVAL_SHAPE, "%s: P %lld, ld %lld (need >= %lld and a multiple of 8)", fn, (long long)P,
                 (long long)ld, (long long)(C + 2 * nv));
+  if (out && (ldo < static_cast<int64_t>(nv) * DV || ldo % 8))
+    return fail(RF_EINVAL_SHAPE, "%s: ldo %lld (>= nv dv = %d, a multiple of 8)", fn, (long long)ldo, nv * DV);
   if (!aligned16(pre) || !aligned16(conv_w) || (conv_in && !aligned16(conv_in)) || !aligned16(workspace))
-    return fail(RF_EINVAL_ARG, "rf_gdn_fill: pre, conv_w, conv_in and workspace must be 16-byte aligned");
-  if (conv_in == conv_out) return fail(RF_EINVAL_ARG, "rf_gdn_fill: conv_out must not alias conv_in");
-  const uint32_t cbytes = chunk_bytes(nk, nv);
+    return fail(RF_EINVAL_ARG, "%s: pre, conv_w, conv_in and workspace must be 16-byte aligned", fn);
+  if (conv_in == conv_out) return fail(RF_EINVAL_ARG, "%s: conv_out must not alias conv_in", fn);
+  const uint32_t sbytes = chunk_bytes(nk, nv);
+  const uint64_t cb64 = sbytes + (out ? static_cast<uint64_t>(nv) * OUT_HEAD_BYTES : 0);
+  if (cb64 > 0x7fffffffull) return fail(RF_EINVAL_SHAPE, "%s: %d value heads", fn, nv);
+  const uint32_t cbytes = static_cast<uint32_t>(cb64);
   // chunks per pass: what the workspace holds, with buffer offsets below 2^31
   const int64_t per_pass = std::min<int64_t>(static_cast<int64_t>(ws_bytes / cbytes), 0x7fffffffll / cbytes);
-  if (per_pass < 1)
-    return fail(RF_EINVAL_ARG, "rf_gdn_fill: workspace %zu bytes < one chunk (%u bytes)", ws_bytes, cbytes);
+  if (per_pass < 1) return fail(RF_EINVAL_ARG, "%s: workspace %zu bytes < one chunk (%u bytes)", fn, ws_bytes, cbytes);
   const int64_t chunks = (P + CH - 1) / CH;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
   for (int64_t c0 = 0; c0 < chunks; c0 += per_pass) {
     const int nc = static_cast<int>(std::min<int64_t>(per_pass, chunks - c0));
-    PrepArgs pa{pre, ld, P, c0 * CH, nk, nv, static_cast<int>(C), conv_w, conv_in, a_log, dt_bias,
-                static_cast<uint8_t*>(workspace), cbytes};
-    hipLaunchKernelGGL(k_gdn_prep, dim3(nc, nv), dim3(256), 0, stream, pa);
-    if (const int e = check_launch("rf_gdn_fill (prep)")) return e;
-    ScanArgs sa{static_cast<const uint8_t*>(workspace), cbytes, nc, nk, nv, state};
-    hipLaunchKernelGGL(k_gdn_scan, dim3(nv * 8), dim3(256), 0, stream, sa);
-    if (const int e = check_launch("rf_gdn_fill (scan)")) return e;
+    PrepArgs pa{pre, ld, P, c0 * CH, nk, nv, static_cast<int>(C), conv_w, conv_in, a_log, dt_bias, ws, cbytes, sbytes};
+    ScanArgs sa{ws, cbytes, nc, nk, nv, state, ws, sbytes};
+    if (out) {
+      hipLaunchKernelGGL(k_gdn_prep<true>, dim3(nc, nv), dim3(256), 0, stream, pa);
+      if (const int e = check_launch(fn)) return e;
+      hipLaunchKernelGGL(k_gdn_scan<true>, dim3(nv * 8), dim3(256), 0, stream, sa);
+      if (const int e = check_launch(fn)) return e;
+      OutArgs oa{ws, cbytes, sbytes, nk, P, c0 * CH, out, ldo};
+      hipLaunchKernelGGL(k_gdn_out, dim3(nc, nv), dim3(256), 0, stream, oa);
+      if (const int e = check_launch(fn)) return e;
+    } else {
+      hipLaunchKernelGGL(k_gdn_prep<false>, dim3(nc, nv), dim3(256), 0, stream, pa);
+      if (const int e = check_launch(fn)) return e;
+      hipLaunchKernelGGL(k_gdn_scan<false>, dim3(nv * 8), dim3(256), 0, stream, sa);
+      if (const int e = check_launch(fn)) return e;
+    }
   }
   hipLaunchKernelGGL(k_conv_tail, dim3((3 * C + 255) / 256), dim3(256), 0, stream, pre, ld, P, static_cast<int>(C),
                      conv_in, conv_out);
-  return check_launch("rf_gdn_fill (conv state)");
+  return check_launch(fn);
+}
+
+}  // namespace
+
+extern "C" int rf_gdn_fill(const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int dk, int dv,
+                           const uint16_t* conv_w, const uint16_t* conv_in, uint16_t* conv_out, const float* a_log,
+                           const float* dt_bias, float* state, void* workspace, size_t ws_bytes, hipStream_t stream) {
+  return gdn_run("rf_gdn_fill", pre, ld, P, nk, nv, dk, dv, conv_w, conv_in, conv_out, a_log, dt_bias, state, nullptr,
+                 0, workspace, ws_bytes, stream);
+}
+
+extern "C" int rf_gdn_forward(const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int dk, int dv,
+                              const uint16_t* conv_w, const uint16_t* conv_in, uint16_t* conv_out, const float* a_log,
+                              const float* dt_bias, float* state, uint16_t* out, int64_t ldo, void* workspace,
+                              size_t ws_bytes, hipStream_t stream) {
+  if (!out) return fail(RF_EINVAL_ARG, "rf_gdn_forward: null out");
+  return gdn_run("rf_gdn_forward", pre, ld, P, nk, nv, dk, dv, conv_w, conv_in, conv_out, a_log, dt_bias, state, out,
+                 ldo, workspace, ws_bytes, stream);
 }

@@ -52,6 +52,10 @@ SIGNATURES = {
     "rf_attend_causal_workspace_bytes": [_I64, _I32, _I32, _I32, _I64, _PSZ],
     "rf_residual_add": [_P, _I64, _P, _I64, _P, _I64, _P, _I64, _I64, _P],
     "rf_silu_mul": [_P, _I64, _I64, _I64, _P, _I64, _P],
+    "rf_gdn_forward_workspace_bytes": [_I64, _I32, _I32, _I32, _I32, _PSZ],
+    "rf_gdn_forward": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _I64, _P, _SZ, _P],
+    "rf_sigmoid_mul": [_P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P],
+    "rf_gated_rms_norm": [_P, _I64, _P, _I64, _P, _I64, _I32, _I32, _F32, _P, _I64, _P],
     "rf_dequant_gguf_rows": [_I32, _P, _I64, _I64, _I64, _P, _I64, _P],
     "rf_dequant_i8_rows": [_P, _I64, _P, _I64, _I64, _I64, _I32, _P, _I64, _P],
     "rf_read_cosine": [_P, _I64, _P, _I64, _I64, _I32, _I32, _P, _I32, _F64, _P, _P, _SZ, _P],

@@ -28,7 +28,6 @@ K and V cosines (k_norm gain applied for Qwen3) into an fp64 score per candidate
 import torch
 
 from . import ops, ridge
-from ._lib import UnsupportedArchitecture
 from .kva import Projector
 
 LAMBDAS = (1e-4, 3e-4, 1e-3, 3e-3, 0.01, 0.03, 0.1, 0.3, 1.0)      # fit_sweep.py:44
@@ -43,9 +42,6 @@ class Capture:
         self.L, H = model.n_layers, model.hidden
         if not self.splits or self.splits[0] < 1 or self.splits[-1] >= self.L:
             raise ValueError(f"splits {splits}: each split S needs 1 <= S < {self.L} (late layers S .. L - 1)")
-        if any(t != "attn" for t in model.layer_types):
-            raise UnsupportedArchitecture("the capture runs the exact forward, which the kernels implement for "
-                                          "attention layers only")
         if H % 256:
             raise ValueError(f"hidden size {H}: the Gram accumulation needs a multiple of 256")
         if block <= 0 or block % 64:

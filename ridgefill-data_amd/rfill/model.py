@@ -6,7 +6,7 @@ arithmetic in librfill's HIP kernels.
   fill_kv(i, k, v, pos, cache)  cache-only fill from given pre-RoPE K / V [P, Hkv, d]
                                 (code/kva/model.py:161-165)
   forward_exact(ids, hook)      exact forward of one document, hook(i, h) on every layer input
-                                (code/kva/model.py:167-181; attention models)
+                                (code/kva/model.py:167-181)
   new_cache()                   one dict per layer (code/kva/model.py:105-106)
 
 Cache layout (code/kva/model.py:139-159): attention layers hold kbuf / vbuf [Hkv, cap, d] bf16 with
@@ -226,29 +226,42 @@ class FillModel:
         return self._gdn_ws
 
     def _pack_rows(self, i):
-        """Layer i's weights for the exact rows' full layer, packed on first use: the query projection with
-        the input norm gain folded in, q_norm, o_proj, [gate; up] with the post-attention norm gain folded in
-        (zero rows to a multiple of 256), down (zero columns to a multiple of 64)."""
-        w = self._layer(i)
-        if "wq" in w:
+        """Layer i's weights for its full layer (exact rows, the exact tail), packed on first use, with the
+        input norm gain folded into the projections (rf_fold_norm; the zero-centred 1 + g for Qwen3.5):
+        attention -- the query projection (Qwen3.5: its query and output-gate halves apart), q_norm, o_proj;
+        GDN -- the z projection, the gated output norm's weight, out_proj; every layer -- [gate; up] with
+        the post-attention norm gain folded in (zero rows to a multiple of 256), down (zero columns to a
+        multiple of 64)."""
+        w = self._layer(i, self.layer_types[i])
+        if "wo" in w:
             return w
-        if self.arch == "qwen3_5":
-            raise UnsupportedArchitecture("exact rows through Qwen3.5 layers (gated attention, GDN) are not "
-                                          "implemented by the kernels")
         dev = lambda k: self._src[k].to(self.device, torch.bfloat16).contiguous()   # noqa: E731
         p = f"{self._pre}layers.{i}."
-        a = p + "self_attn."
-        w["wq"] = ops.fold_norm(dev(a + "q_proj.weight"), w["ln1"], self.knorm_kind)
-        if self.arch == "qwen3":
-            w["q_norm"] = dev(a + "q_norm.weight")
-        w["wo"] = dev(a + "o_proj.weight")
+        kind = self.knorm_kind
+        if w["kind"] == "attn":
+            a = p + "self_attn."
+            wq = dev(a + "q_proj.weight")
+            if self.arch == "qwen3_5":                  # per head [q | gate] rows (code/kva/model.py:427-432)
+                qg = wq.view(self.n_heads, 2, self.head_dim, wq.shape[1])
+                w["wq"] = ops.fold_norm(qg[:, 0].reshape(-1, wq.shape[1]).contiguous(), w["ln1"], kind)
+                w["wgate"] = ops.fold_norm(qg[:, 1].reshape(-1, wq.shape[1]).contiguous(), w["ln1"], kind)
+            else:
+                w["wq"] = ops.fold_norm(wq, w["ln1"], kind)
+            if self.arch != "llama":
+                w["q_norm"] = dev(a + "q_norm.weight")
+            w["wo"] = dev(a + "o_proj.weight")
+        else:
+            a = p + "linear_attn."
+            w["wz"] = ops.fold_norm(dev(a + "in_proj_z.weight"), w["ln1"], 1)
+            w["gnorm"] = dev(a + "norm.weight")
+            w["wo"] = dev(a + "out_proj.weight")
         gate, up = dev(p + "mlp.gate_proj.weight"), dev(p + "mlp.up_proj.weight")
         inter = gate.shape[0]
         gu = torch.cat((gate, up), 0)
         pad = (-gu.shape[0]) % 256
         if pad:
             gu = torch.cat((gu, gu.new_zeros(pad, gu.shape[1])), 0)
-        w["wgu"] = ops.fold_norm(gu, dev(p + "post_attention_layernorm.weight"), 0)
+        w["wgu"] = ops.fold_norm(gu, dev(p + "post_attention_layernorm.weight"), kind)
         down = dev(p + "mlp.down_proj.weight")
         pad = (-inter) % 64
         if pad:
@@ -256,19 +269,58 @@ class FillModel:
         w["wd"], w["inter"] = down, inter
         return w
 
+    def _gdn_forward_workspace(self, rows, device):
+        need = ops.gdn_forward_workspace_bytes(rows, self.nk, self.nv, self.dk, self.dv)
+        ws = getattr(self, "_gdn_fwd_ws", None)
+        if ws is None or ws.numel() < need or ws.device != device:
+            self._gdn_fwd_ws = ws = torch.empty(need, dtype=torch.uint8, device=device)
+        return ws
+
+    def _gdn_layer(self, i, h, ssq, cache, rows=None):
+        """The exact GDN layer (code/kva/model.py:486-508; layer_rows :541-554): the in-projection, conv and
+        delta rule with outputs over every row of h, continuing cache[i]'s conv and recurrent states, then
+        for h (or its rows `rows`) the gated output norm with z, out_proj and its residual, and the MLP."""
+        w = self._pack_rows(i)
+        c = cache[i]
+        T, H = h.shape
+        pre = ops.norm_linear(h, ssq, self.eps, w["w_in"],
+                              workspace=self.gemm_workspace(T, w["w_in"].shape[0], H, h.device))
+        rec = c.get("rec")
+        rec = (torch.zeros(self.nv, self.dk, self.dv, dtype=torch.float32, device=h.device) if rec is None
+               else rec.float().contiguous().clone())
+        out, conv = ops.gdn_forward(pre, self.nk, self.nv, self.dk, self.dv, w["conv"], c.get("conv"), w["a_log"],
+                                    w["dt_bias"], rec, workspace=self._gdn_forward_workspace(T, h.device))
+        c["conv"], c["rec"], c["len"] = conv, rec, c.get("len", 0) + T
+        if rows is not None:
+            out = ops.row_gather(out, rows)[0]
+            h, ssq = ops.row_gather(h, rows)
+        R = h.shape[0]
+        z = ops.norm_linear(h, ssq, self.eps, w["wz"], workspace=self.gemm_workspace(R, w["wz"].shape[0], H, h.device))
+        y = ops.gated_rms_norm(out, z, w["gnorm"], self.nv, self.dv, self.eps)
+        return self._out_mlp(w, h, y)
+
+    def _gate(self, w, x, ssq, o):
+        """Qwen3.5's output gate: o * sigmoid(x_normed W_gate^T) in place (code/kva/model.py:444-445)."""
+        if "wgate" in w:
+            g = ops.norm_linear(x, ssq, self.eps, w["wgate"],
+                                workspace=self.gemm_workspace(x.shape[0], w["wgate"].shape[0], x.shape[1], x.device))
+            ops.sigmoid_mul(o, g, out=o)
+        return o
+
     def layer_rows(self, i, x, pos, rows, cache, ssq=None, cs=None):
         """Fill cache[i] from the inputs x [P, H] of rows at positions pos (an empty cache, as fill()) and
         return the exact layer output of the rows x[rows] over that cache, [len(rows), H] bf16
         (code/kva/model.py:259-276): the rows' queries attend over the filled keys up to their own
-        position, then o_proj, the residual, and the MLP with its residual. rows: sorted prefix rows."""
-        if self.layer_types[i] != "attn":
-            raise UnsupportedArchitecture("exact rows through GDN layers are not implemented by the kernels")
-        w = self._pack_rows(i)
+        position, then o_proj, the residual, and the MLP with its residual. rows: sorted prefix rows.
+        GDN layers (Qwen3.5): the delta rule runs with outputs over every row, the rest on the rows only."""
         c = cache[i]
-        if c.get("n", 0):
+        if c.get("n", 0) or c.get("len", 0):
             raise ValueError("layer_rows fills an empty cache (cache slot = position)")
+        w = self._pack_rows(i)
         if ssq is None:
             ssq = ops.row_ssq(x)
+        if self.layer_types[i] != "attn":
+            return self._gdn_layer(i, x, ssq, cache, torch.as_tensor(rows, dtype=torch.int64).to(x.device))[0]
         if cs is None:
             cs = self.rope_table(pos)
         self.fill(i, x, pos, cache, ssq=ssq, cs=cs)
@@ -284,7 +336,7 @@ class FillModel:
         else:
             o = ops.attend_rows(q, qpos, c["kbuf"], c["vbuf"], c["n"], self.n_heads, self.scale,
                                 workspace=self._attn_workspace(R, c["n"], x.device))
-        return self._out_mlp(w, xr, o)[0]
+        return self._out_mlp(w, xr, self._gate(w, xr, sr, o))[0]
 
     def _out_mlp(self, w, h, o):
         """The rest of the layer after attention: h + o W_o^T, then the SwiGLU MLP with its residual
@@ -308,14 +360,15 @@ class FillModel:
         into slots n .. n + T - 1, the rows' queries attend causally over the keys up to their own slot
         (bottom-right aligned, as code/kva/ops.py:107-128), then o_proj, the residual and the MLP with its
         residual. ssq / cs: h's row sum-of-squares partials and the RoPE table of pos, if already built.
-        Returns (layer output [T, H] bf16, its row sum-of-squares partials)."""
+        Returns (layer output [T, H] bf16, its row sum-of-squares partials). GDN layers (Qwen3.5): the
+        conv and delta rule continue the cache's states over the rows (code/kva/model.py:486-508)."""
+        if ssq is None:
+            ssq = ops.row_ssq(h)
         if self.layer_types[i] != "attn":
-            raise UnsupportedArchitecture("the exact layer of GDN layers is not implemented by the kernels")
+            return self._gdn_layer(i, h, ssq, cache)
         w = self._pack_rows(i)
         c = cache[i]
         T = h.shape[0]
-        if ssq is None:
-            ssq = ops.row_ssq(h)
         if cs is None:
             cs = self.rope_table(pos)
         slot = self.reserve(c, T, self.n_kv, self.head_dim, h.device)
@@ -333,7 +386,7 @@ class FillModel:
         else:
             o = ops.attend_rows(q, idx + slot, c["kbuf"], c["vbuf"], c["n"], self.n_heads, self.scale,
                                 workspace=self._attn_workspace(T, c["n"], h.device))
-        return self._out_mlp(w, h, o)
+        return self._out_mlp(w, h, self._gate(w, h, ssq, o))
 
     def embed(self, ids):
         """Embedding rows of token ids [T] (code/kva/model.py:108-109): a bit-exact row gather from the bf16
@@ -354,7 +407,7 @@ class FillModel:
         logits to return. stop: return after hook(stop, h), before layer `stop` runs (a capture that needs
         no later layer). Returns (logits of keep or None, cache)."""
         cache = self.new_cache() if cache is None else cache
-        if any(c.get("n", 0) for c in cache):
+        if any(c.get("n", 0) or c.get("len", 0) for c in cache):
             raise ValueError("forward_exact starts from an empty cache (cache slot = position)")
         h, ssq = self.embed(ids)
         pos = torch.arange(h.shape[0], device=self.device)

@@ -390,6 +390,73 @@ def gdn_fill(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state, worksp
 
 # ------------------------------------------------------------------------ exact-row selection
 
+def gdn_forward_workspace_bytes(rows, nk, nv, dk=128, dv=128):
+    """Bytes of device workspace rf_gdn_forward needs for `rows` rows in one pass."""
+    n = ctypes.c_size_t(0)
+    _lib.call("rf_gdn_forward_workspace_bytes", rows, nk, nv, dk, dv, ctypes.byref(n))
+    return n.value
+
+
+def gdn_forward(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state, out=None, workspace=None):
+    """The exact GDN layer's mixing: as gdn_fill (state updated in place, returns the new conv state) and
+    the delta-rule outputs [P, nv dv] bf16. Returns (out, conv state)."""
+    _need(pre, "pre", torch.bfloat16, 2)
+    _need(conv_w, "conv_w", torch.bfloat16, 2)
+    _need(a_log, "a_log", torch.float32, 1)
+    _need(dt_bias, "dt_bias", torch.float32, 1)
+    _need(state, "state", torch.float32, 3)
+    C = 2 * nk * dk + nv * dv
+    if tuple(conv_w.shape) != (C, 4) or not conv_w.is_contiguous() or tuple(state.shape) != (nv, dk, dv) \
+            or not state.is_contiguous() or pre.shape[1] < C + 2 * nv or a_log.numel() != nv or dt_bias.numel() != nv:
+        raise ValueError(f"gdn_forward: pre {tuple(pre.shape)}, conv {tuple(conv_w.shape)}, state {tuple(state.shape)}")
+    if conv_in is not None:
+        _need(conv_in, "conv_in", torch.bfloat16, 2)
+        if tuple(conv_in.shape) != (3, C) or not conv_in.is_contiguous():
+            raise ValueError("gdn_forward: conv state shape")
+    P = pre.shape[0]
+    out = torch.empty(P, nv * dv, dtype=torch.bfloat16, device=pre.device) if out is None else out
+    _need(out, "out", torch.bfloat16, 2)
+    if out.shape[0] != P or out.shape[1] < nv * dv:
+        raise ValueError(f"gdn_forward: out {tuple(out.shape)}")
+    if workspace is None:
+        workspace = torch.empty(gdn_forward_workspace_bytes(P, nk, nv, dk, dv), dtype=torch.uint8, device=pre.device)
+    _need(workspace, "workspace", torch.uint8, 1)
+    conv_out = torch.empty(3, C, dtype=torch.bfloat16, device=pre.device)
+    _lib.call("rf_gdn_forward", _ptr(pre), pre.stride(0), P, nk, nv, dk, dv, _ptr(conv_w), _ptr(conv_in),
+              _ptr(conv_out), _ptr(a_log), _ptr(dt_bias), _ptr(state), _ptr(out), out.stride(0), _ptr(workspace),
+              workspace.numel(), _stream(pre))
+    return out, conv_out
+
+
+def sigmoid_mul(o, g, out=None):
+    """bf16(o * bf16(sigmoid(g))) (Qwen3.5's attention output gate); out may be o."""
+    _need(o, "o", torch.bfloat16, 2)
+    _need(g, "g", torch.bfloat16, 2)
+    rows, n = o.shape
+    if tuple(g.shape) != (rows, n):
+        raise ValueError(f"sigmoid_mul: o {tuple(o.shape)}, g {tuple(g.shape)}")
+    out = torch.empty_like(o) if out is None else out
+    _need(out, "out", torch.bfloat16, 2)
+    _lib.call("rf_sigmoid_mul", _ptr(o), o.stride(0), _ptr(g), g.stride(0), rows, n, _ptr(out), out.stride(0),
+              _stream(o))
+    return out
+
+
+def gated_rms_norm(x, z, weight, heads, dv, eps, out=None):
+    """rms_norm_gated over [rows, heads dv]: bf16(bf16(weight * bf16(rms-normed x)) * silu(z))."""
+    _need(x, "x", torch.bfloat16, 2)
+    _need(z, "z", torch.bfloat16, 2)
+    _need(weight, "weight", torch.bfloat16, 1)
+    rows = x.shape[0]
+    if z.shape[0] != rows or min(x.shape[1], z.shape[1]) < heads * dv or weight.numel() != dv:
+        raise ValueError(f"gated_rms_norm: x {tuple(x.shape)}, z {tuple(z.shape)}, weight {weight.numel()}")
+    out = torch.empty(rows, heads * dv, dtype=torch.bfloat16, device=x.device) if out is None else out
+    _need(out, "out", torch.bfloat16, 2)
+    _lib.call("rf_gated_rms_norm", _ptr(x), x.stride(0), _ptr(z), z.stride(0), _ptr(weight), rows, heads, dv,
+              float(eps), _ptr(out), out.stride(0), _stream(x))
+    return out
+
+
 def window_mass_workspace_bytes(w, hq, hkv, d, n_end):
     n = ctypes.c_size_t(0)
     _lib.call("rf_window_mass_workspace_bytes", w, hq, hkv, d, n_end, ctypes.byref(n))

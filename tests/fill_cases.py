@@ -105,3 +105,47 @@ def gdn_tensors(cfg, seed=0):
         t[a + "A_log"] = torch.log(0.05 + 0.15 * torch.rand(nv, generator=g))
         t[a + "dt_bias"] = 0.5 * torch.randn(nv, generator=g)
     return t
+
+
+def hybrid_config(layer_types, hidden=512, nk=2, nv=4, hkv=2, d=128, eps=1e-6):
+    """A Qwen3.5 text config with the given layer kinds ("gdn" / "attn"): GDN heads as gdn_config, gated
+    attention with 2 hkv query heads of head_dim d, partial rotary 0.25."""
+    c = gdn_config(hidden, nk, nv, len(layer_types), eps)
+    c.update(layer_types=["linear_attention" if t == "gdn" else "full_attention" for t in layer_types],
+             num_key_value_heads=hkv, num_attention_heads=2 * hkv, head_dim=d)
+    return c
+
+
+def hybrid_tensors(cfg, seed=0, vocab=64):
+    """Every parameter of a whole Qwen3.5 model of cfg (checkpoint names): zero-centred norm gains
+    0.1 N(0, 1), the GDN output norm's weight 1 + 0.1 N(0, 1), gates as gdn_tensors, matrices N(0, 1/fan_in)."""
+    g = torch.Generator().manual_seed(seed)
+    h, hkv, d, hq, inter = (cfg["hidden_size"], cfg["num_key_value_heads"], cfg["head_dim"],
+                            cfg["num_attention_heads"], cfg["intermediate_size"])
+    nk, nv = cfg["linear_num_key_heads"], cfg["linear_num_value_heads"]
+    C = 2 * nk * 128 + nv * 128
+    rn = lambda *s: torch.randn(*s, generator=g)                                   # noqa: E731
+    t = {"model.embed_tokens.weight": rn(vocab, h), "model.norm.weight": 0.1 * rn(h),
+         "lm_head.weight": 0.05 * rn(vocab, h)}
+    raw = {}
+    for i, kind in enumerate(cfg["layer_types"]):
+        p = f"model.layers.{i}."
+        t.update({p + "input_layernorm.weight": 0.1 * rn(h), p + "post_attention_layernorm.weight": 0.1 * rn(h),
+                  p + "mlp.gate_proj.weight": rn(inter, h) / h ** 0.5, p + "mlp.up_proj.weight": rn(inter, h) / h ** 0.5,
+                  p + "mlp.down_proj.weight": rn(h, inter) / inter ** 0.5})
+        if kind == "full_attention":
+            a = p + "self_attn."
+            t.update({a + "q_proj.weight": rn(2 * hq * d, h) / h ** 0.5, a + "k_proj.weight": rn(hkv * d, h) / h ** 0.5,
+                      a + "v_proj.weight": rn(hkv * d, h) / h ** 0.5, a + "o_proj.weight": rn(h, hq * d) / (hq * d) ** 0.5,
+                      a + "q_norm.weight": 0.1 * rn(d), a + "k_norm.weight": 0.1 * rn(d)})
+        else:
+            a = p + "linear_attn."
+            t.update({a + "in_proj_qkv.weight": rn(C, h) / h ** 0.5, a + "in_proj_b.weight": rn(nv, h) / h ** 0.5,
+                      a + "in_proj_a.weight": 0.3 * rn(nv, h) / h ** 0.5, a + "conv1d.weight": 0.5 * rn(C, 1, 4),
+                      a + "in_proj_z.weight": rn(nv * 128, h) / h ** 0.5, a + "norm.weight": 1 + 0.1 * rn(128),
+                      a + "out_proj.weight": rn(h, nv * 128) / (nv * 128) ** 0.5})
+            raw[a + "A_log"] = torch.log(0.05 + 0.15 * torch.rand(nv, generator=g))
+            raw[a + "dt_bias"] = 0.5 * rn(nv)
+    out = {k: v.to(torch.bfloat16) for k, v in t.items()}
+    out.update(raw)
+    return out

@@ -166,9 +166,7 @@ def test_selection_matches_the_oracle(dev):
 
 
 def test_capture_refuses(dev):
-    from fill_cases import gdn_config, gdn_tensors
     from rfill import fit
-    from rfill._lib import UnsupportedArchitecture
     from rfill.model import FillModel
     cfg, t = case("llama_c1", layers=3)
     m = FillModel(cfg, t, dev)
@@ -184,6 +182,3 @@ def test_capture_refuses(dev):
         cap.add_document(torch.tensor([1, 64]))
     with pytest.raises(ValueError, match="no documents"):
         cap.state(1)
-    gc = gdn_config(layers=4)
-    with pytest.raises(UnsupportedArchitecture):
-        fit.Capture(FillModel(gc, gdn_tensors(gc), dev), [2])

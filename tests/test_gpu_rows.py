@@ -111,8 +111,7 @@ def test_layer_rows_matches_oracle(dev, name):
     assert c[0]["n"] == P
 
 
-def test_layer_rows_refuses_a_filled_cache_and_gdn(dev):
-    from rfill._lib import UnsupportedArchitecture
+def test_layer_rows_refuses_a_filled_cache(dev):
     from rfill.model import FillModel
     from fill_cases import gdn_config, gdn_tensors
     cfg, t = case("llama_c1")
@@ -125,9 +124,11 @@ def test_layer_rows_refuses_a_filled_cache_and_gdn(dev):
         m.layer_rows(0, x, pos, torch.tensor([3, 9], device=dev), c)
     gcfg = gdn_config()
     gm = FillModel(gcfg, gdn_tensors(gcfg), dev)
-    with pytest.raises(UnsupportedArchitecture):
-        gm.layer_rows(0, inputs(64, gcfg["hidden_size"]).to(dev), torch.arange(64, device=dev),
-                      torch.tensor([1], device=dev), gm.new_cache())
+    gx = inputs(64, gcfg["hidden_size"]).to(dev)
+    gc = gm.new_cache()
+    gm.fill(0, gx, torch.arange(64, device=dev), gc)
+    with pytest.raises(ValueError):                               # a GDN layer's filled state
+        gm.layer_rows(0, gx, torch.arange(64, device=dev), torch.tensor([1], device=dev), gc)
 
 
 def test_fill_late_runs_the_exact_rows_through_every_layer(dev):
