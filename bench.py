@@ -376,6 +376,50 @@ def hybrid_bench(dev, reps=3, split=24, n_rows=32768, tail=4096):
                                 "counted_flop_per_launch": P * (2 * 4 * C + 6 * nv * dk * dv)}}}
 
 
+def hybrid_finish_bench(dev, reps=2, split=24, n_rows=32768, tail=4096):
+    """The hybrid's whole late stack as finish() runs it, without the logits: the fill of layers 24..47
+    (P = 28672 rows), then the 4096-row exact tail through every late layer -- GDN layers continue the
+    filled conv and recurrent states (in-projection, rf_gdn_forward with outputs, gated norm, out_proj,
+    MLP), attention layers attend over all 32768 keys with the output gate (head_dim 256)."""
+    from rfill import ops, synth
+    from rfill.kva import Arm, Projector, fill_late
+    from rfill.model import FillModel
+    cfg = synth.QWEN35_HYBRID
+    w = synth.hybrid_fill(cfg, split, n_rows, tail, device=dev, full=True)
+    model = FillModel(cfg, w["tensors"], dev, layers=w["layers"])
+    arm = Arm("ridgefill", split=split, tail=tail, fill="proj", projector=Projector(split, w["maps"], w["biases"]))
+    h = w["h_split"]
+    P = w["P"]
+    pos = torch.arange(P, n_rows, device=dev)
+    cs = model.rope_table(pos)
+
+    def run():
+        cache = model.new_cache()
+        for i in w["layers"]:
+            if model.layer_types[i] == "attn":
+                model.reserve(cache[i], n_rows, model.n_kv, model.head_dim, dev)
+        t0 = time.perf_counter()
+        fill_late(model, h, arm, cache=cache)
+        torch.cuda.synchronize()
+        t1 = time.perf_counter()
+        x, ssq = h[P:], ops.row_ssq(h[P:])
+        for i in w["layers"]:
+            x, ssq = model.layer(i, x, pos, cache, ssq=ssq, cs=cs)
+        torch.cuda.synchronize()
+        return t1 - t0, time.perf_counter() - t1
+
+    run()
+    tf = tt = 0.0
+    for _ in range(reps):
+        a, b = run()
+        tf += a / reps
+        tt += b / reps
+    return {"workload": f"qwen3.5-shaped hybrid late stack: fill of layers {split}..{cfg['num_hidden_layers'] - 1} "
+                        f"({P} rows) + {tail}-row exact tail through every late layer (MLP 6144)",
+            "prompt_tokens_per_s": round(n_rows / (tf + tt), 1), "ms_fill": round(tf * 1e3, 2),
+            "ms_tail": round(tt * 1e3, 2)}
+
+
 def exact_rows_bench(dev, reps=3, split=18, n_rows=32768, tail=4096, frac=0.01):
     """The Qwen3-8B-shaped fill (hidden 4096, 32 / 8 heads, k_norm, layers 18..35, 32K prompt, P = 28672)
     with 1% of the filled rows exact (287 rows at seeded positions) run as finish() runs them: every late
@@ -559,6 +603,9 @@ def main():
     if not args.no_hybrid:
         log("Gated-DeltaNet hybrid fill leg")
         out["hybrid"] = hybrid_bench(dev)
+        torch.cuda.empty_cache()
+        log("Gated-DeltaNet hybrid fill + exact tail")
+        out["hybrid_finish"] = hybrid_finish_bench(dev)
         torch.cuda.empty_cache()
     if not args.no_fit:
         log("closed-form fit leg")

@@ -321,7 +321,8 @@ def finish(model, h_split, arm, keep, exact_rows=None, hr=None, cache=None, row_
     (fill_late, with exact rows as there), and the exact tail rows [P, N) run through each late layer
     in order (FillModel.layer over that layer's filled cache, kva.py:457). The fill of a layer never
     reads the tail, so filling every layer first gives the reference's results. Each attention cache
-    is sized once for P + T rows. Returns (logits of the last `keep` rows [keep, V] fp32, cache, P)."""
+    is sized once for P + T rows. arm.st {layer: [heads, dk, dv]} is added to each late GDN layer's filled
+    recurrent state before the tail. Returns (logits of the last `keep` rows [keep, V] fp32, cache, P)."""
     n = h_split.shape[0]
     P = arm.prefix_len(n)
     T = n - P
@@ -337,6 +338,9 @@ def finish(model, h_split, arm, keep, exact_rows=None, hr=None, cache=None, row_
             model.reserve(cache[i], n, model.n_kv, model.head_dim, dev)
     if P > 0:
         fill_late(model, h_split, arm, exact_rows=exact_rows, hr=hr, cache=cache, row_inputs=row_inputs)
+        for i, st in (arm.st or {}).items():            # GDN terminal-state corrections (kva.py:452-454)
+            if i in layers and model.layer_types[i] == "gdn":
+                cache[i]["rec"] = cache[i]["rec"] + st.to(cache[i]["rec"])
     h = h_split[P:]
     pos = torch.arange(P, n, device=dev)
     cs = model.rope_table(pos)

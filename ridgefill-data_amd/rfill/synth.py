@@ -11,7 +11,9 @@
                    N(0, 0.02), depthwise conv U(-0.5, 0.5) [8192, 4], A_log = log U(0, 16) and
                    dt_bias = 1 (the architecture's own initialisation), so the gates run through the
                    checkpoint formula g = -exp(A_log) softplus(a + dt_bias), beta = sigmoid(b);
-                   attention layers K / V N(0, 0.02) with a zero-centred k_norm gain N(0, 0.05).
+                   attention layers K / V N(0, 0.02) with a zero-centred k_norm gain N(0, 0.05). With
+                   full=True also the rest of each late layer for the exact tail (hybrid_full_weights; MLP
+                   width 6144, which the hybrid's description leaves open).
   full_model(...)  every layer's whole weights, the head and an N(0, 1) embedding table (the exact forward
                    of the capture and the lambda selection).
 Seeds: 10 (rows), 11 (channel gains and outliers), 12 + l (layer l's weights), 100 + l (the map of
@@ -33,7 +35,8 @@ QWEN35_HYBRID = dict(model_type="qwen3_5_text", num_hidden_layers=48, hidden_siz
                      layer_types=["full_attention" if i % 4 == 3 else "linear_attention" for i in range(48)],
                      linear_num_key_heads=16, linear_num_value_heads=32, linear_key_head_dim=128,
                      linear_value_head_dim=128, linear_conv_kernel_dim=4,
-                     rope_parameters=dict(rope_type="default", rope_theta=10000000.0, partial_rotary_factor=0.25))
+                     rope_parameters=dict(rope_type="default", rope_theta=10000000.0, partial_rotary_factor=0.25),
+                     intermediate_size=6144)
 
 
 def _gen(seed, device):
@@ -176,8 +179,33 @@ def gdn_layer_weights(cfg, layer, device="cpu"):
     return t
 
 
-def hybrid_fill(cfg, split, n_rows, tail, device="cpu", map_noise=0.02):
-    """The hybrid late-layer fill workload (dict as dense_fill's, plus layer_types)."""
+def hybrid_full_weights(cfg, layer, device="cpu"):
+    """The rest of a hybrid layer the exact tail runs through (seed 200 + layer): the SwiGLU MLP and its
+    zero-centred post norm; attention: the gated q projection [2 hq d, H], o_proj, q_norm; GDN: the z
+    projection, the gated output norm's weight 1 + N(0, 0.05), out_proj. Matrices N(0, 0.02), zero-centred
+    norm gains N(0, 0.05)."""
+    h, inter = cfg["hidden_size"], cfg["intermediate_size"]
+    g = _gen(200 + layer, device)
+    rn = lambda *s: torch.randn(*s, generator=g, device=device)                        # noqa: E731
+    p = f"model.layers.{layer}."
+    t = {p + "post_attention_layernorm.weight": 0.05 * rn(h), p + "mlp.gate_proj.weight": 0.02 * rn(inter, h),
+         p + "mlp.up_proj.weight": 0.02 * rn(inter, h), p + "mlp.down_proj.weight": 0.02 * rn(h, inter)}
+    if cfg["layer_types"][layer] == "linear_attention":
+        nv, dv = cfg["linear_num_value_heads"], cfg["linear_value_head_dim"]
+        a = p + "linear_attn."
+        t.update({a + "in_proj_z.weight": 0.02 * rn(nv * dv, h), a + "norm.weight": 1 + 0.05 * rn(dv),
+                  a + "out_proj.weight": 0.02 * rn(h, nv * dv)})
+    else:
+        hq, d = cfg["num_attention_heads"], cfg["head_dim"]
+        a = p + "self_attn."
+        t.update({a + "q_proj.weight": 0.02 * rn(2 * hq * d, h), a + "o_proj.weight": 0.02 * rn(h, hq * d),
+                  a + "q_norm.weight": 0.05 * rn(d)})
+    return {k: v.to(torch.bfloat16) for k, v in t.items()}
+
+
+def hybrid_fill(cfg, split, n_rows, tail, device="cpu", map_noise=0.02, full=False):
+    """The hybrid late-layer fill workload (dict as dense_fill's, plus layer_types); full: also each late
+    layer's whole weights (hybrid_full_weights) for the exact tail."""
     L, h = cfg["num_hidden_layers"], cfg["hidden_size"]
     layers = list(range(split, L))
     tensors, maps, biases = {}, {}, {}
@@ -197,5 +225,7 @@ def hybrid_fill(cfg, split, n_rows, tail, device="cpu", map_noise=0.02):
         w = torch.eye(h, device=device) + map_noise * torch.randn(h, h, generator=g, device=device) / h ** 0.5
         maps[l] = w.to(torch.bfloat16)
         biases[l] = (1e-3 * torch.randn(h, generator=g, device=device)).to(torch.bfloat16)
+        if full:
+            tensors.update(hybrid_full_weights(cfg, l, device))
     return dict(cfg=cfg, split=split, layers=layers, h_split=hidden_states(n_rows, h, device=device),
                 P=n_rows - tail, tensors=tensors, maps=maps, biases=biases)

@@ -184,3 +184,38 @@ def test_hybrid_forward_and_capture(dev, hybrid):
     e = max(rel_err(a["sxx"], b["sxx"]), *(rel_err(a["sxy"][i], b["sxy"][i]) for i in (1, 2, 3)))
     print(f"hybrid capture sums: {e:.1e}")
     assert a["n"] == 429 and e < 1e-5
+
+
+@pytest.mark.parametrize("exact", [False, True])
+def test_hybrid_finish_matches_oracle(dev, exact):
+    """finish() on an 8-layer hybrid (GDN, GDN, GDN, attention, twice), split 4: the fill of the late
+    layers (with exact rows through their GDN and attention layers, or none), the terminal-state
+    corrections st on the late GDN layers, the 192-row exact tail through every late layer, tail logits."""
+    from oracle import kva as OK
+    from rfill.kva import Arm, Projector, finish
+    from rfill.model import FillModel
+    cfg = hybrid_config(["gdn", "gdn", "gdn", "attn"] * 2)
+    t = hybrid_tensors(cfg, seed=7)
+    N, tail, split, keep = 900, 192, 4, 64
+    P, H = N - tail, cfg["hidden_size"]
+    h = inputs(N, H, seed=47)
+    g = torch.Generator().manual_seed(48)
+    W = {i: (torch.eye(H) + 0.05 * torch.randn(H, H, generator=g) / H ** 0.5).to(torch.bfloat16) for i in range(split, 8)}
+    B = {i: (1e-2 * torch.randn(H, generator=g)).to(torch.bfloat16) for i in range(split, 8)}
+    st = {i: 0.01 * torch.randn(4, 128, 128, generator=g) for i in (4, 5, 6)}
+    rows = torch.randperm(P, generator=g)[:12].sort().values if exact else None
+    m = FillModel(cfg, t, dev)
+    arm = Arm("ridgefill", split=split, tail=tail, fill="proj", projector=Projector(split, W, B),
+              st={i: s.to(dev) for i, s in st.items()})
+    logits, cache, P_got = finish(m, h.to(dev), arm, keep, exact_rows=rows)
+    torch.cuda.synchronize()
+    om = OM.OracleModel(cfg, t, dtype=torch.bfloat16)
+    oarm = OK.Arm("ridgefill", split=split, tail=tail, fill="proj", projector=OK.Projector(split, W, B), st=st)
+    want, oc, P_want = OK.finish(om, torch.zeros(N, dtype=torch.long), h, om.new_cache(), oarm, keep, exact_rows=rows)
+    assert P_got == P_want == P
+    el = rel_err(logits, want)
+    es = max(rel_err(cache[i]["rec"], oc[i]["rec"]) for i in (4, 5, 6))
+    ek = max(rel_err(cache[7][part], oc[7][part]) for part in ("k", "v"))
+    agree = float((logits.argmax(-1).cpu() == want.argmax(-1)).float().mean())
+    print(f"hybrid finish (exact rows: {exact}): logits {el:.2e}, GDN states {es:.2e}, K/V {ek:.2e}, argmax {agree:.3f}")
+    assert el < 2 * TOL and es < TOL and ek < TOL and agree > 0.9
