@@ -56,14 +56,17 @@ __device__ __forceinline__ float* part_block(const AttnArgs& a, int qblock, int 
 }
 
 // AD = head_dim (64, 128 or 256); K tile rows are AD + 8 bf16 apart in LDS (conflict-free fragment reads).
-template <int AD>
-__global__ __launch_bounds__(256) void k_attend_rows(AttnArgs a) {
+// NT = threads: 256 (64 query rows per block, key-range splits allowed) or 512 (128 rows: for many queries
+// at head_dim 256, each K / V tile serves twice the rows; no splits).
+template <int AD, int NT>
+__global__ __launch_bounds__(NT) void k_attend_rows(AttnArgs a) {
   constexpr int KROW = AD + 8, NS = AD / 32, NB = AD / 16, CPR = AD / 8;   // d steps, d blocks, chunks per row
-  constexpr int LOADS = KT * CPR / 256;                                    // 16-byte K (and V) chunks per thread
+  constexpr int LOADS = KT * CPR / NT;                                     // 16-byte K (and V) chunks per thread
+  constexpr int ROWS = NT / 4;                                             // query rows per block (16 per wave)
   __shared__ uint16_t ks[KT * KROW];
   __shared__ uint16_t vts[AD * VROW];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, ln = lane & 15, g = lane >> 4;
-  const int rep = a.hq / a.hkv, qb = 64 / rep;
+  const int rep = a.hq / a.hkv, qb = ROWS / rep;
   const int hk = blockIdx.y;
   const int j0 = blockIdx.x * qb;
   const int jlast = min(j0 + qb, a.nq) - 1;
@@ -87,24 +90,24 @@ __global__ __launch_bounds__(256) void k_attend_rows(AttnArgs a) {
 
   const uint16_t* kh = a.kc + hk * a.head_stride;
   const uint16_t* vh = a.vc + hk * a.head_stride;
-  // tile loads: K chunk c of thread t = key (t / CPR) + (256 / CPR) c, 16-byte column t % CPR;
-  //             V chunk c = key t & 63, column block (t >> 6) + 4 c
+  // tile loads: K chunk c of thread t = key (t / CPR) + (NT / CPR) c, 16-byte column t % CPR;
+  //             V chunk c = key t & 63, column block (t >> 6) + (NT / 64) c
   uint4 kr[LOADS], vr[LOADS];
   auto load = [&](int64_t k0) {
 #pragma unroll
     for (int c = 0; c < LOADS; ++c) {
-      const int64_t kk = k0 + t / CPR + (256 / CPR) * c, kv = k0 + (t & 63);
+      const int64_t kk = k0 + t / CPR + (NT / CPR) * c, kv = k0 + (t & 63);
       kr[c] = kk <= kmax ? *reinterpret_cast<const uint4*>(kh + kk * a.row_stride + (t % CPR) * 8)
                          : make_uint4(0u, 0u, 0u, 0u);
-      vr[c] = kv <= kmax ? *reinterpret_cast<const uint4*>(vh + kv * a.row_stride + ((t >> 6) + 4 * c) * 8)
+      vr[c] = kv <= kmax ? *reinterpret_cast<const uint4*>(vh + kv * a.row_stride + ((t >> 6) + (NT / 64) * c) * 8)
                          : make_uint4(0u, 0u, 0u, 0u);
     }
   };
   auto store = [&]() {
 #pragma unroll
     for (int c = 0; c < LOADS; ++c) {
-      *reinterpret_cast<uint4*>(ks + (t / CPR + (256 / CPR) * c) * KROW + (t % CPR) * 8) = kr[c];
-      const int key = t & 63, d0 = ((t >> 6) + 4 * c) * 8;
+      *reinterpret_cast<uint4*>(ks + (t / CPR + (NT / CPR) * c) * KROW + (t % CPR) * 8) = kr[c];
+      const int key = t & 63, d0 = ((t >> 6) + (NT / 64) * c) * 8;
 #pragma unroll
       for (int e = 0; e < 8; ++e) vts[(d0 + e) * VROW + key] = lane_of(vr[c], e);
     }
@@ -193,7 +196,7 @@ __global__ __launch_bounds__(256) void k_attend_rows(AttnArgs a) {
   float lsum = lpart;
   lsum += __shfl_xor(lsum, 16, 64);
   lsum += __shfl_xor(lsum, 32, 64);
-  if (ns > 1) {                                               // unnormalised partials for the combine
+  if (NT == 256 && ns > 1) {                                  // unnormalised partials for the combine
     float* pb = part_block<AD>(a, blockIdx.x, hk, sp);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -402,14 +405,17 @@ extern "C" int rf_attend_rows(const uint16_t* q, int64_t ldq, const int64_t* qpo
   if (nq == 0) return RF_OK;
   if (workspace && (reinterpret_cast<uintptr_t>(workspace) & 15u))
     return fail(RF_EINVAL_SHAPE, "rf_attend_rows: workspace alignment");
-  const int ns = workspace ? attend_splits(nq, hq, hkv, d, cache_rows, ws_bytes) : 1;
+  // many queries at head_dim 256 (an exact tail): 128-row blocks, no key-range splits
+  const bool wide = d == 256 && nq >= 2048;
+  const int ns = (workspace && !wide) ? attend_splits(nq, hq, hkv, d, cache_rows, ws_bytes) : 1;
   AttnArgs a{q, ldq, qpos, static_cast<int>(nq), kbuf, vbuf, head_stride, row_stride, hq, hkv, scale, out, ldo,
              static_cast<float*>(workspace)};
-  const int qb = 64 / (hq / hkv);
+  const int qb = (wide ? 128 : 64) / (hq / hkv);
   const dim3 grid(static_cast<unsigned>((nq + qb - 1) / qb), static_cast<unsigned>(hkv), static_cast<unsigned>(ns));
-  if (d == 256) hipLaunchKernelGGL(k_attend_rows<256>, grid, dim3(256), 0, stream, a);
-  else if (d == 128) hipLaunchKernelGGL(k_attend_rows<128>, grid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL(k_attend_rows<64>, grid, dim3(256), 0, stream, a);
+  if (wide) hipLaunchKernelGGL((k_attend_rows<256, 512>), grid, dim3(512), 0, stream, a);
+  else if (d == 256) hipLaunchKernelGGL((k_attend_rows<256, 256>), grid, dim3(256), 0, stream, a);
+  else if (d == 128) hipLaunchKernelGGL((k_attend_rows<128, 256>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((k_attend_rows<64, 256>), grid, dim3(256), 0, stream, a);
   if (ns > 1) {
     const int st = check_launch("rf_attend_rows");
     if (st != RF_OK) return st;

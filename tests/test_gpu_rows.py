@@ -276,3 +276,28 @@ def test_attend_causal_at_positions(dev, hq, hkv, d, nq, n):
     first = split[0].view(hq, d).cpu()
     for h in range(hq):
         assert torch.equal(first[h], v[h // (hq // hkv), 0])
+
+
+def test_attend_rows_head_dim_256_many_queries(dev):
+    """An exact tail at head_dim 256 (Qwen3.5's gated attention): 2600 queries take the 512-thread,
+    128-row-block variant; against the oracle's attend_at and bitwise against the 64-row variant run over
+    the same queries in pieces of fewer than 2048 (no key-range splits in either)."""
+    from oracle import ops as oops
+    from rfill import ops
+    hq, hkv, d, n, nq = 16, 2, 256, 4000, 2600
+    q, k, v = _qkv(nq, hq, hkv, d, n, seed=77)
+    qpos = torch.arange(n - nq, n)
+    kb = torch.zeros(hkv, n + 64, d, dtype=torch.bfloat16)
+    vb = torch.zeros_like(kb)
+    kb[:, :n], vb[:, :n] = k, v
+    kb, vb, qd, pd = kb.to(dev), vb.to(dev), q.to(dev), qpos.to(dev)
+    scale = d ** -0.5
+    wide = ops.attend_rows(qd, pd, kb, vb, n, hq, scale, workspace=None)
+    parts = torch.cat([ops.attend_rows(qd[a:b], pd[a:b], kb, vb, n, hq, scale, workspace=None)
+                       for a, b in ((0, 1300), (1300, 2600))])
+    torch.cuda.synchronize()
+    assert torch.equal(wide, parts)
+    want = oops.attend_at(q.view(nq, hq, d).transpose(0, 1), k, v, scale, qpos)
+    err = rel_err(wide, want)
+    print(f"head_dim 256, {nq} queries: rel err {err:.2e}")
+    assert err < TOL
