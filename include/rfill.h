@@ -269,7 +269,7 @@ int rf_window_mass_workspace_bytes(int w, int hq, int hkv, int d, int64_t n_end,
  * j < pos0 + w; later keys get nothing. q [w, >= hq d] post-RoPE queries of the window rows (rf_norm_q),
  * kbuf the layer's post-RoPE K cache [hkv, cap, d] (head_stride, row_stride); mass fp64 [>= pos0 + w], the
  * caller's accumulator over layers (zero it per prompt). Each K / V head group's sum is fp32 (rows, then
- * heads, in a fixed order), added into mass as fp64 in group order. d 64 or 128; (hq / hkv) * w a
+ * heads, in a fixed order), added into mass as fp64 in group order. d 64, 128 or 256; (hq / hkv) * w a
  * multiple of 32, at most 1024. */
 int rf_window_mass(const uint16_t* q, int64_t ldq, int w, int64_t pos0, int hq, int d, const uint16_t* kbuf,
                    int hkv, int64_t head_stride, int64_t row_stride, float scale, double* mass, void* workspace,

@@ -258,7 +258,7 @@ size_t mass_bytes(int w, int hq, int hkv, int64_t n_end) {
 }
 
 int mass_shape(const char* fn, int w, int hq, int hkv, int d) {
-  if (d != 64 && d != 128) return fail(RF_EUNSUPPORTED, "%s: head_dim %d (64 or 128)", fn, d);
+  if (d != 64 && d != 128 && d != 256) return fail(RF_EUNSUPPORTED, "%s: head_dim %d (64, 128 or 256)", fn, d);
   if (hq <= 0 || hkv <= 0 || hq % hkv || w <= 0 || (static_cast<int64_t>(hq / hkv) * w) % 32 ||
       static_cast<int64_t>(hq / hkv) * w > 1024)
     return fail(RF_EINVAL_SHAPE, "%s: %d window rows x %d query heads per K / V head must be a multiple of 32, "
@@ -303,12 +303,14 @@ extern "C" int rf_window_mass(const uint16_t* q, int64_t ldq, int w, int64_t pos
              reinterpret_cast<float2*>(ws + (part + 255) / 256 * 256),
              reinterpret_cast<float*>(ws + (part + 255) / 256 * 256 + (stats + 255) / 256 * 256)};
   const dim3 grid(static_cast<unsigned>(nkb), static_cast<unsigned>(hkv));
-  if (d == 128) hipLaunchKernelGGL(k_mass_stats<128>, grid, dim3(256), 0, stream, a);
+  if (d == 256) hipLaunchKernelGGL(k_mass_stats<256>, grid, dim3(256), 0, stream, a);
+  else if (d == 128) hipLaunchKernelGGL(k_mass_stats<128>, grid, dim3(256), 0, stream, a);
   else hipLaunchKernelGGL(k_mass_stats<64>, grid, dim3(256), 0, stream, a);
   if (const int e = check_launch("rf_window_mass (row blocks)")) return e;
   hipLaunchKernelGGL(k_mass_rows, dim3(static_cast<unsigned>((hkv * R + 3) / 4)), dim3(256), 0, stream, a);
   if (const int e = check_launch("rf_window_mass (rows)")) return e;
-  if (d == 128) hipLaunchKernelGGL(k_mass_cols<128>, grid, dim3(256), 0, stream, a);
+  if (d == 256) hipLaunchKernelGGL(k_mass_cols<256>, grid, dim3(256), 0, stream, a);
+  else if (d == 128) hipLaunchKernelGGL(k_mass_cols<128>, grid, dim3(256), 0, stream, a);
   else hipLaunchKernelGGL(k_mass_cols<64>, grid, dim3(256), 0, stream, a);
   if (const int e = check_launch("rf_window_mass (columns)")) return e;
   hipLaunchKernelGGL(k_mass_fold, dim3(static_cast<unsigned>((n_end + 255) / 256)), dim3(256), 0, stream, a.colsum,

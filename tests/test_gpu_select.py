@@ -33,7 +33,8 @@ def mass64(q, k, pos0, scale):
     return torch.softmax(s, -1).sum((0, 1))
 
 
-@pytest.mark.parametrize("n,w,end,hq,hkv,d", [(4096, 64, 4096, 32, 8, 128), (1000, 16, 700, 8, 4, 64)])
+@pytest.mark.parametrize("n,w,end,hq,hkv,d", [(4096, 64, 4096, 32, 8, 128), (1000, 16, 700, 8, 4, 64),
+                                               (3000, 64, 2900, 16, 2, 256)])
 def test_window_mass_kernel(dev, n, w, end, hq, hkv, d):
     from rfill import ops
     g = torch.Generator().manual_seed(n)
@@ -88,3 +89,28 @@ def test_window_mass_refuses(dev):
         ops.window_mass(q, 100, kb, 4, 0.125, mass)
     with pytest.raises(ValueError):
         ops.window_mass(q[:8], 195, kb, 4, 0.125, mass)      # past the cache
+
+
+def test_select_on_a_hybrid(dev):
+    """The qattn mass at the attention layer of a Qwen3.5 hybrid (gated queries, zero-centred q_norm,
+    partial RoPE, head_dim 256): layer 3 filled from the same inputs on both sides."""
+    from fill_cases import hybrid_config, hybrid_tensors
+    from rfill.model import FillModel
+    from rfill import select as RS
+    cfg = hybrid_config(["gdn", "gdn", "gdn", "attn"], hidden=512, hkv=2, d=256)
+    t = hybrid_tensors(cfg, seed=9)
+    n, w, layers = 1500, 64, [3]
+    pos = torch.arange(n)
+    x = inputs(n, cfg["hidden_size"], seed=63)
+    om = OM.OracleModel(cfg, t, dtype=torch.bfloat16)
+    oc = om.new_cache()
+    om.fill(3, x, pos, oc)
+    m = FillModel(cfg, t, dev)
+    c = m.new_cache()
+    m.fill(3, x.to(dev), pos.to(dev), c)
+    want = OS.window_mass(om, {3: x[n - w:]}, oc, layers)
+    got = RS.window_mass(m, {3: x[n - w:].to(dev)}, c, layers)
+    err = rel_err(got, want)
+    print(f"hybrid window mass vs the oracle: rel err {err:.2e}")
+    assert err < 1e-2
+    assert abs(float(got.sum()) - w * m.n_heads) < 1e-3 * w * m.n_heads
