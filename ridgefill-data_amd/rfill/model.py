@@ -173,8 +173,12 @@ class FillModel:
         return {}
 
     def _fill_gdn(self, i, x, cache, st, ssq, checkpoint_every):
-        if checkpoint_every:
-            raise UnsupportedArchitecture("GDN state checkpoints are not produced by the fill kernels")
+        """checkpoint_every (a multiple of the 64-row chunk): also return {len + t: state after t rows} for
+        every t (rows of this call) that is a multiple of it (code/kva/ops.py:206-209, :258-260). The rows
+        then go through the kernels in segments of that many rows; a segment boundary on the chunk grid
+        leaves every chunk's arithmetic, and so the final state, unchanged."""
+        if checkpoint_every and (checkpoint_every <= 0 or checkpoint_every % 64):
+            raise ValueError(f"checkpoint_every {checkpoint_every}: a positive multiple of the 64-row chunk")
         w = self._layer(i, "gdn")
         P = x.shape[0]
         c = cache[i]
@@ -186,13 +190,20 @@ class FillModel:
         rec = c.get("rec")
         rec = (torch.zeros(self.nv, self.dk, self.dv, dtype=torch.float32, device=x.device) if rec is None
                else rec.float().contiguous().clone())
-        c["conv"] = ops.gdn_fill(pre, self.nk, self.nv, self.dk, self.dv, w["conv"], c.get("conv"), w["a_log"],
-                                 w["dt_bias"], rec, self._gdn_workspace(P, x.device))
-        c["rec"] = rec
-        c["len"] = c.get("len", 0) + P
+        offset, ck = c.get("len", 0), {}
+        seg = checkpoint_every or P
+        conv = c.get("conv")
+        for r0 in range(0, P, seg):
+            r1 = min(P, r0 + seg)
+            conv = ops.gdn_fill(pre[r0:r1], self.nk, self.nv, self.dk, self.dv, w["conv"], conv, w["a_log"],
+                                w["dt_bias"], rec, self._gdn_workspace(r1 - r0, x.device))
+            if checkpoint_every and r1 % checkpoint_every == 0:
+                ck[offset + r1] = rec.clone()
+        c["conv"], c["rec"] = conv, rec
+        c["len"] = offset + P
         if st is not None:
             c["rec"] = c["rec"] + st.to(c["rec"])
-        return {}
+        return ck
 
     def _attn_workspace(self, nq, n, device):
         """The exact-row attention's key-split workspace, shared by every layer (stream-ordered reuse)."""

@@ -118,3 +118,30 @@ def test_fill_c4_gdn_layer_shape(dev):
     err = rel_err(mc[0]["rec"], oc[0]["rec"])
     print(f"C4 GDN layer: state rel err {err:.2e}")
     assert err < STATE_TOL
+
+
+def test_fill_checkpoints(dev):
+    """fill(..., checkpoint_every=256) over 1100 rows continuing 300 filled rows: the states after 256,
+    512, 768 and 1024 rows of the call, keyed by position (300 + t), against the oracle's checkpoints; the
+    final state and conv state bit-identical to a fill without checkpoints."""
+    from rfill.model import FillModel
+    cfg = gdn_config()
+    t = gdn_tensors(cfg, seed=4)
+    om = OM.OracleModel(cfg, t, dtype=torch.bfloat16)
+    m = FillModel(cfg, t, dev)
+    x = inputs(1400, cfg["hidden_size"], seed=23)
+    oc, mc, plain = om.new_cache(), m.new_cache(), m.new_cache()
+    om.fill(0, x[:300], torch.arange(300), oc)
+    for c in (mc, plain):
+        m.fill(0, x[:300].to(dev), torch.arange(300, device=dev), c)
+    want = om.fill(0, x[300:], torch.arange(300, 1400), oc, checkpoint_every=256)
+    got = m.fill(0, x[300:].to(dev), torch.arange(300, 1400, device=dev), mc, checkpoint_every=256)
+    m.fill(0, x[300:].to(dev), torch.arange(300, 1400, device=dev), plain)
+    torch.cuda.synchronize()
+    assert sorted(got) == sorted(want) == [556, 812, 1068, 1324]
+    errs = {k: rel_err(got[k], want[k]) for k in got}
+    print("checkpoint state rel errs", {k: f"{v:.2e}" for k, v in errs.items()})
+    assert all(e < STATE_TOL for e in errs.values())
+    assert torch.equal(mc[0]["rec"], plain[0]["rec"]) and torch.equal(mc[0]["conv"], plain[0]["conv"])
+    with pytest.raises(ValueError, match="multiple"):
+        m.fill(0, x[:64].to(dev), torch.arange(64, device=dev), m.new_cache(), checkpoint_every=100)
