@@ -144,6 +144,40 @@ def dequant_bench(dev, rows=2560, width=10240, maps=24):
             "ms_all_maps": round(sec * maps * 1e3, 3)}
 
 
+def gguf_bench(dev, rows=5120, width=5120, maps=48):
+    """rf_dequant_gguf_rows on the GGUF adapters' map tensors: Q8_0 (the fitted adapters) and F16 (the
+    identity one), [5120, 5120] each (the 27B kit's width), HBM-bound: Q8_0 reads 34 bytes per 32 values
+    and writes 2 bytes per value; F16 reads 2 and writes 2."""
+    from rfill import ops
+    g = torch.Generator(device=dev).manual_seed(33)
+    out = torch.empty(rows, width, dtype=torch.bfloat16, device=dev)
+    res = {}
+    for name, gt, row_bytes in (("q8_0", 8, width // 32 * 34), ("f16", 1, 2 * width)):
+        raw = torch.randint(0, 256, (rows, row_bytes), generator=g, device=dev, dtype=torch.int32).to(torch.uint8)
+        if gt == 8:                                  # finite fp16 scales in every block's first two bytes
+            blk = raw.view(rows, width // 32, 34)
+            blk[:, :, 0] = 0
+            blk[:, :, 1] = 0x20
+        else:
+            raw.view(rows, width, 2)[:, :, 1] &= 0x3F
+        for _ in range(3):
+            ops.dequant_gguf_rows(raw, gt, width, out=out)
+        torch.cuda.synchronize()
+        reps = 20
+        s0, e0 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record()
+        for _ in range(reps):
+            ops.dequant_gguf_rows(raw, gt, width, out=out)
+        e0.record()
+        torch.cuda.synchronize()
+        sec = s0.elapsed_time(e0) / 1e3 / reps
+        byts = rows * row_bytes + 2 * rows * width
+        res[name] = {"mean_us": round(sec * 1e6, 1), "achieved": round(byts / sec / 1e9, 1), "unit": "GB/s",
+                     "frac": round(byts / sec / PEAK_HBM, 4), "bytes_per_launch": byts,
+                     "ms_per_adapter": round(sec * maps * 1e3, 3)}
+    return {"kernel": "rf_dequant_gguf_rows", "bound": "hbm", "workload": f"{maps} GGUF maps [{rows}, {width}]", **res}
+
+
 def window_mass_bench(dev, n=32768, w=64, hq=32, hkv=8, d=128, layers=4):
     """The qattn selector's mass (rf_window_mass) at the 8B 32K prompt: 64 window rows x 32 query heads over
     32768 cached keys, for each of the 4 exact lower layers. Algorithmic work per layer: the scores
@@ -589,6 +623,7 @@ def main():
         out["kernels"]["rf_rope_kv_write"] = kv_write_bench(model, dev, P, SPLIT)
         out["kernels"]["rf_dequant_i8_rows"] = dequant_bench(dev)
         out["kernels"]["rf_window_mass"] = window_mass_bench(dev)
+        out["kernels"]["rf_dequant_gguf_rows"] = gguf_bench(dev)
         out["ceilings"] = ceilings(dev, P, H)
     del caches, xbuf, sbuf
     torch.cuda.empty_cache()
