@@ -24,11 +24,18 @@ class Arm:
     fill: str = "exact"
     projector: object = None
     st: dict | None = None
+    fill_by_type: dict | None = None
     meta: dict = field(default_factory=dict)
 
     def prefix_len(self, n):
         """P = n - tail (0 for the exact arm), code/kva/kva.py:101-106."""
         return 0 if self.fill == "exact" else max(0, n - self.tail)
+
+    def fill_of(self, layer_type):
+        """A late layer's fill: fill_by_type['attention' | 'gdn'] if set, else the arm's (code/kva/kva.py:108-112)."""
+        if self.fill_by_type is None:
+            return self.fill
+        return self.fill_by_type["attention" if layer_type == "attn" else layer_type]
 
 
 I8_GROUP = 128
@@ -114,17 +121,25 @@ class Projector:
         save_file(out, str(path), metadata={k: str(v) for k, v in dict(meta, split=self.split).items()})
 
     @classmethod
-    def load(cls, path, dtype=torch.bfloat16):
-        from safetensors.torch import load_file
+    def load(cls, path, dtype=torch.bfloat16, sha256=None):
+        """Maps from the file's bytes, read once; with sha256 given, bytes of another hash are refused
+        (code/kva/kva.py:161-178; the page-cache re-read of code/kva/integrity.py is the product's)."""
+        import hashlib
+        from safetensors.torch import load as from_bytes
         with open(path, "rb") as f:
-            hdr = f.read(8)
-            meta = json.loads(f.read(int.from_bytes(hdr, "little"))).get("__metadata__") or {}
+            data = f.read()
+        sha = hashlib.sha256(data).hexdigest()
+        if sha256 is not None and sha != sha256:
+            raise RuntimeError(f"{path}: sha256 {sha}, expected {sha256}")
+        meta = json.loads(data[8:8 + int.from_bytes(data[:8], "little")]).get("__metadata__") or {}
         W, B = {}, {}
-        for name, t in load_file(str(path)).items():
+        for name, t in from_bytes(data).items():
             check_weights({name: t}, f"Projector.load {path}")
             i = int(name.split(".")[1])
             W[i], B[i] = t[:, :-1].to(dtype).contiguous(), t[:, -1].to(dtype).contiguous()
-        return cls(int(meta["split"]), W, B, meta)
+        p = cls(int(meta["split"]), W, B, meta)
+        p.sha256 = sha
+        return p
 
 
 def run_lower(model, ids, splits):
@@ -142,10 +157,12 @@ def run_lower(model, ids, splits):
 
 
 def finish(model, ids, h_split, lower_cache, arm, keep, oracle=None, exact_rows=None, fill_store=None,
-           row_inputs=None):
+           row_inputs=None, fill_reuse=None, keep_cache=True, hook=None):
     """Late layers of one arm (code/kva/kva.py:319-460, the fill subset). Prefix rows [0, P) fill each
-    late layer from x (projector / identity / true inputs) with the exact rows R scattered in
-    (index_copy) and run through layer_rows; then +st; then the tail rows run the exact layer.
+    late layer from x (projector / identity / true inputs, per layer type through fill_by_type) with the
+    exact rows R scattered in (index_copy) and run through layer_rows -- or, with fill 'none', only the
+    rows R run the layer; a fill_reuse dict replaces the fill; then +st; then the tail rows run the exact
+    layer (hook(i, h) first; keep_cache=False drops the layer's cache after).
     row_inputs (dict): receives the exact rows' input to every late layer {layer: [|R|, H]}.
     Returns (logits of the last `keep` rows, cache, P)."""
     n = ids.shape[0]
@@ -162,22 +179,29 @@ def finish(model, ids, h_split, lower_cache, arm, keep, oracle=None, exact_rows=
         if int(rows[-1]) >= P or bool((rows.diff() <= 0).any()):
             raise ValueError("exact rows: sorted unique rows < P")
         hr = h_split[rows]
+    if rows is not None and fill_reuse is not None:
+        raise ValueError("exact rows: no fill reuse")
     for i in range(split, model.n_layers):
-        if P > 0:
-            if arm.fill == "none":
+        fill = arm.fill_of(model.layer_types[i])
+        if P > 0 and fill_reuse is not None:
+            if fill_reuse[i].get("n", P) != P:
+                raise ValueError(f"reused fill of layer {i} has {fill_reuse[i]['n']} rows, P = {P}")
+            cache[i] = dict(fill_reuse[i])
+        elif P > 0:
+            if fill == "none":
                 if rows is not None:
                     if row_inputs is not None:
                         row_inputs[i] = hr
                     hr = model.layer(i, hr, pos[rows], cache)
             else:
-                if arm.fill == "proj":
+                if fill == "proj":
                     x = arm.projector(i, b)
-                elif arm.fill == "identity":
+                elif fill == "identity":
                     x = b
-                elif arm.fill == "oracle":
+                elif fill == "oracle":
                     x = oracle[i][:P]
                 else:
-                    raise ValueError(arm.fill)
+                    raise ValueError(fill)
                 if rows is not None:
                     if row_inputs is not None:
                         row_inputs[i] = hr
@@ -185,10 +209,14 @@ def finish(model, ids, h_split, lower_cache, arm, keep, oracle=None, exact_rows=
                     hr = model.layer_rows(i, x, pos[:P], rows, cache)
                 else:
                     model.fill(i, x, pos[:P], cache)
-            if fill_store is not None:
-                fill_store[i] = dict(cache[i])
-            st = arm.st.get(i) if arm.st else None
-            if st is not None:
-                cache[i]["rec"] = cache[i]["rec"] + st.to(cache[i]["rec"])
+        if P > 0 and fill_store is not None:
+            fill_store[i] = dict(cache[i])
+        st = arm.st.get(i) if (arm.st and P > 0) else None
+        if st is not None:
+            cache[i]["rec"] = cache[i]["rec"] + st.to(cache[i]["rec"])
+        if hook is not None:
+            hook(i, h)
         h = model.layer(i, h, pos[P:], cache)
+        if not keep_cache:
+            cache[i] = {}
     return model.logits(h[h.shape[0] - keep:]), cache, P

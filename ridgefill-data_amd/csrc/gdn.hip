@@ -653,15 +653,18 @@ constexpr int SST = DV + 4;                        // fp32 row stride of S and Y
 // v_mfma_f32_16x16x4f32 (lane l feeds A[l % 16][l / 16] and B[l / 16][l % 16], holds D[4 (l / 16) + r][l % 16]):
 //   X = K S, Y = beta (V - q X) (q = e^gamma r), v_new = T Y, O = Qd S + P v_new
 // with S the state before the chunk (LDS), Y then v_new shared through LDS; fp32 throughout, bf16 out.
-// T and P are lower triangular, but their products run over all 16 k-steps, in loops the compiler keeps
-// as they are: two other shapes (a trip count taken from the wave index; the k-steps unrolled by 8) gave
-// wrong products. Both compile to accumulators rotated through v_accvgpr moves at the loop head, the
-// first read 6 wait states after an 8-pass MFMA; the shape used has no such moves. Its outputs are
-// checked against the oracle's chunked rule, and any change here must be rechecked on the GPU.
+// T and P are lower triangular, but their products run over all 16 k-steps: two other shapes (a trip
+// count taken from the wave index; the k-steps unrolled by 8) gave wrong products. Both compiled to
+// accumulators rotated through v_accvgpr moves at the loop head, the first read 6 wait states after an
+// 8-pass MFMA. The shape used compiles fully unrolled: 768 MFMAs, no v_accvgpr moves or writes, and at
+// least 10 wait states between an MFMA and the first read of its result. The wave index is made
+// wave-uniform (an SGPR), which changes only the address arithmetic. The outputs are checked against
+// the oracle's chunked rule at the hybrid's widths, and any change here must be rechecked on the GPU.
 __global__ __launch_bounds__(256) void k_gdn_out(OutArgs a) {
   __shared__ __align__(16) float s_l[DK * SST];
   __shared__ __align__(16) float y_l[CH * SST];
-  const int t = threadIdx.x, lane = t & 63, w = t >> 6, lr = lane & 15, lk = lane >> 4;
+  const int t = threadIdx.x, lane = t & 63, lr = lane & 15, lk = lane >> 4;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
   const int c = blockIdx.x, h = blockIdx.y;
   const uint8_t* chunk = a.ws + static_cast<size_t>(c) * a.chunk_bytes;
   const uint8_t* ob = chunk + a.out_off + static_cast<size_t>(h) * OUT_HEAD_BYTES;

@@ -1,13 +1,15 @@
-"""Fill driver over the device fill model: the reference's Arm, Projector map type and the late-layer
-fill loop of finish() (code/kva/kva.py:79-193, 392-454), with every fill step on librfill kernels.
+"""Fill driver over the device fill model: the reference's Arm, Projector map type, run_lower and finish()
+(code/kva/kva.py:79-193, 282-300, 319-460), with every fill step on librfill kernels.
 
 fill_late() runs the hot path of finish() for one arm: for each late layer i >= split, the prefix rows
-[0, P) get x_i = W_i b + c_i (fill 'proj', one rf_map_apply that also yields x's RMSNorm statistics)
-or x_i = b (fill 'identity'), the exact rows R are scattered in bit-exactly (rf_row_scatter, the
-index_copy of kva.py:428-431), the layer's cache is filled (rf_norm_kv_write) and, for exact rows, the
-layer's full computation runs on them (FillModel.layer_rows, kva.py:436-437) to give their next input.
-Two x / statistics buffers and one RoPE table serve all late layers; optionally layer i's cache work
-runs on a second stream beside layer i + 1's map apply (two_stream).
+[0, P) get the layer's fill (Arm.fill_of: the arm's fill, or per layer type through fill_by_type) --
+x_i = W_i b + c_i ('proj', one rf_map_apply that also yields x's RMSNorm statistics), x_i = b
+('identity'), the true inputs ('oracle') or nothing ('none') -- the exact rows R are scattered in
+bit-exactly (rf_row_scatter, the index_copy of kva.py:428-431), the layer's cache is filled
+(rf_norm_kv_write, or the GDN fill) and, for exact rows, the layer's full computation runs on them
+(FillModel.layer_rows, kva.py:436-437) to give their next input. Two x / statistics buffers and one RoPE
+table serve all late layers; optionally layer i's cache work runs on a second stream beside layer i + 1's
+map apply (two_stream). finish() adds fill reuse, the st corrections, the exact tail and the logits.
 """
 import json
 from dataclasses import dataclass, field
@@ -19,16 +21,47 @@ from . import ops
 
 MAX_ABS_WEIGHT = 1e4
 
+# Fills this package runs per late layer; the other fills of the reference are refused by name.
+FILLS = ("proj", "identity", "oracle", "none")
+UNSUPPORTED_FILLS = ("swiftkv", "swiftkv_native", "kvfold")
+
+
+class NonFiniteLogits(RuntimeError):
+    """Logits with a NaN or an infinity: a broken forward stops the run rather than becoming a data point
+    (code/kva/kva.py:470-473)."""
+
+
+def check_finite(logits, where):
+    """logits unchanged if every entry is finite, else NonFiniteLogits naming `where` (code/kva/kva.py:476-479)."""
+    if not bool(torch.isfinite(logits).all()):
+        raise NonFiniteLogits(f"{where}: logits hold NaN or infinite values")
+    return logits
+
 
 @dataclass
 class Arm:
-    """An arm's fill parameters (code/kva/kva.py:79-118): split, tail, fill kind, projector, st."""
+    """An arm's fill parameters (code/kva/kva.py:79-118). The fields are the reference's, so arms built for
+    it build here too. finish() runs the fills in FILLS, per layer type through fill_by_type
+    ({'attention': fill, 'gdn': fill}), with exact rows, st corrections and fill reuse; the exploratory
+    options (f1, kvfold, context, refresh, tail_bias_from, exact_part, rescale) are refused by name."""
     name: str
     split: int | None = None
     tail: int = 0
     fill: str = "exact"
     projector: object = None
     st: dict | None = None
+    f1: bool = False
+    fill_by_type: dict | None = None
+    kvfold: object = None
+    context: int = 0
+    refresh: int | None = None
+    refresh_projector: object = None
+    tail_bias_from: int | None = None
+    tail_bias_skip_last: int = 0
+    exact_part: str | None = None
+    rescale: str | None = None
+    rescale_skip_last: int = 0
+    tail_from: str | None = None
     meta: dict = field(default_factory=dict)
 
     def prefix_len(self, n):
@@ -38,32 +71,68 @@ class Arm:
             return n
         return max(0, n - self.tail)
 
+    def fill_of(self, layer_type):
+        """The fill of a late layer of type 'attn' or 'gdn' (fill_by_type names them 'attention' and 'gdn')."""
+        if self.fill_by_type is None:
+            return self.fill
+        return self.fill_by_type["attention" if layer_type == "attn" else layer_type]
+
+    def uses(self, fill):
+        return fill in (self.fill_by_type.values() if self.fill_by_type else (self.fill,))
+
+
+def _refuse_options(arm):
+    """UnsupportedArchitecture for an arm option outside the fill path built here."""
+    from ._lib import UnsupportedArchitecture
+    opts = dict(f1=arm.f1, kvfold=arm.kvfold is not None, context=arm.context, refresh=arm.refresh is not None,
+                tail_bias_from=arm.tail_bias_from is not None, exact_part=arm.exact_part is not None,
+                rescale=arm.rescale is not None)
+    on = [k for k, v in opts.items() if v]
+    if on:
+        raise UnsupportedArchitecture(f"arm {arm.name!r}: option(s) {', '.join(on)} are not implemented on the device")
+    for f in (arm.fill_by_type or {}).values() if arm.fill_by_type else (arm.fill,):
+        if f in UNSUPPORTED_FILLS:
+            raise UnsupportedArchitecture(f"arm {arm.name!r}: fill {f!r} is not implemented on the device")
+
 
 def rounded_tail(n, base, block):
-    """Tail length when the prefix boundary is rounded down to a block multiple (code/kva/kva.py:270-273)."""
+    """Exact-tail length of an n-row prompt when a block-granular scheduler rounds the prefix boundary down
+    to a multiple of `block` with at least `base` rows left exact: the boundary is the largest block multiple
+    <= n - base (0 if n < base), so base <= tail < base + block for long prompts (code/kva/kva.py:270-273)."""
     return n - max(0, (n - base) // block * block)
 
 
 def check_weights(tensors, where):
-    """Refuse maps with a non-finite entry or |w| > 1e4, naming the first bad entry (code/kva/kva.py:121-134)."""
+    """Refuse stored maps {name: [d_out, d_in + 1]} that hold a NaN, an infinity or an entry of magnitude
+    above MAX_ABS_WEIGHT -- what a failed fit, or bytes damaged after the file was written, leave behind.
+    Raises ValueError naming the tensor and its first bad entry (the refusal of code/kva/kva.py:121-134)."""
     for name, t in tensors.items():
-        tf = t.float()
-        bad = ~torch.isfinite(tf) | (tf.abs() > MAX_ABS_WEIGHT)
-        if bool(bad.any()):
-            r, c = bad.nonzero()[0].tolist()
-            raise ValueError(f"{where}: {name} has {int(bad.sum())} non-finite or |w| > {MAX_ABS_WEIGHT:g} weights "
-                             f"(first at row {r}, col {c}: {tf[r, c].item():.4g}); refusing")
+        v = t.float()
+        ok = torch.isfinite(v) & (v.abs() <= MAX_ABS_WEIGHT)
+        if bool(ok.all()):
+            continue
+        bad = (~ok).nonzero()
+        at = tuple(bad[0].tolist())
+        raise ValueError(f"{where}: refusing {name}: {bad.shape[0]} entries are NaN, infinite or above "
+                         f"{MAX_ABS_WEIGHT:g} in magnitude, the first at {list(at)} = {v[at].item():.4g}")
+
+
+def _header(data):
+    """The JSON header of safetensors bytes."""
+    n = int.from_bytes(data[:8], "little")
+    return json.loads(data[8:8 + n])
 
 
 class Projector:
     """Per late layer x_i = b W_i^T + c_i in bf16 (code/kva/kva.py:137-159). Maps may live anywhere;
     the first call on a GPU keeps one bf16 device copy (release() drops it). File format
     (code/kva/kva.py:161-193): safetensors, 'layer.{i}' = [d_out, d_in + 1] bf16, bias last column,
-    string metadata with 'split'."""
+    string metadata with 'split'; load() checks the file's sha256 and keeps it as .sha256."""
 
     def __init__(self, split, weights, biases, meta=None):
         self.split, self.W, self.b, self.meta = split, weights, biases, meta or {}
         self._dev = None
+        self.sha256 = None
 
     def _maps(self, device):
         if self._dev is None or self._dev[0] != device:
@@ -85,29 +154,41 @@ class Projector:
         self._dev = None
 
     def save(self, path, meta):
+        """Write the maps as [W | c] cast once to bf16 (the two operands promoted to one dtype first, so a
+        map saved here is the same file the reference writes for the same tensors), refusing bad maps."""
         from safetensors.torch import save_file
-        out = {f"layer.{i}": torch.cat((self.W[i].float(), self.b[i].float()[:, None]), 1).to(torch.bfloat16).cpu()
-               .contiguous() for i in sorted(self.W)}
+        out = {}
+        for i in sorted(self.W):
+            w, c = self.W[i], self.b[i].to(self.W[i].device)
+            out[f"layer.{i}"] = torch.cat((w, c[:, None]), 1).to(torch.bfloat16).cpu().contiguous()
         check_weights(out, f"Projector.save {path}")
         save_file(out, str(path), metadata={k: str(v) for k, v in dict(meta, split=self.split).items()})
 
     @staticmethod
     def meta_of(path):
+        """The file's string metadata from its header alone (no maps read)."""
         with open(path, "rb") as f:
             n = int.from_bytes(f.read(8), "little")
             return json.loads(f.read(n)).get("__metadata__") or {}
 
     @classmethod
-    def load(cls, path, device="cpu", dtype=torch.bfloat16):
-        from safetensors.torch import load_file
+    def load(cls, path, device="cpu", dtype=torch.bfloat16, sha256=None):
+        """The maps of a file written by save(): the bytes are read once and checked against sha256 (the
+        hash recorded when the file was written; None: the disk copy, read around the page cache), and
+        the maps come from those same bytes. Refuses bad maps (check_weights)."""
+        from safetensors.torch import load as from_bytes
+        from .integrity import read_verified
+        data, sha = read_verified(path, sha256)
+        meta = _header(data).get("__metadata__") or {}
         W, B = {}, {}
-        for name, t in load_file(str(path)).items():
+        for name, t in from_bytes(data).items():
             check_weights({name: t}, f"Projector.load {path}")
             i = int(name.split(".")[1])
             W[i] = t[:, :-1].to(device, dtype).contiguous()
             B[i] = t[:, -1].to(device, dtype).contiguous()
-        meta = cls.meta_of(path)
-        return cls(int(meta["split"]), W, B, meta)
+        p = cls(int(meta["split"]), W, B, meta)
+        p.sha256 = sha
+        return p
 
 
 I8_GROUP = 128
@@ -247,10 +328,23 @@ def serial(layers, produce, consume, device):
         consume(i, n % 2)
 
 
-def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap=False, row_inputs=None):
+def _layer_fill(arm, model, i):
+    """The fill of late layer i for this arm, checked against the fills this package runs."""
+    f = arm.fill_of(model.layer_types[i])
+    if f not in FILLS:
+        from ._lib import UnsupportedArchitecture
+        if f in UNSUPPORTED_FILLS:
+            raise UnsupportedArchitecture(f"fill {f!r} (layer {i}) is not implemented on the device")
+        raise ValueError(f"fill {f!r} (layer {i}): expected one of {FILLS}")
+    return f
+
+
+def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap=False, row_inputs=None, oracle=None):
     """The late-layer fill of finish() for one arm: every late layer's cache filled from the prefix rows
     [0, P) of h_split [N, H] (bf16, on the GPU), with exact rows R (sorted prefix rows) whose inputs replace
-    the fill's x (code/kva/kva.py:392-454).
+    the fill's x (code/kva/kva.py:392-454). Each late layer takes its arm's fill for its type (Arm.fill_of):
+    'proj' x = W_i b + c_i, 'identity' x = b, 'oracle' x = oracle[i][:P] (given true inputs), 'none' no
+    prefix fill (with exact rows, the rows alone run the layer: code/kva/kva.py:406-411).
 
     hr None (the reference's path): the rows enter the first late layer with their split-layer state
     h_split[R]; each late layer fills its cache with them scattered in and runs its full layer on them
@@ -261,8 +355,11 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
     n = h_split.shape[0]
     P = arm.prefix_len(n)
     cache = model.new_cache() if cache is None else cache
-    if arm.fill not in ("proj", "identity"):
-        raise ValueError(f"fill {arm.fill!r}: fill_late runs 'proj' and 'identity'")
+    if arm.fill == "exact":
+        raise ValueError("fill 'exact' has no prefix fill")
+    _refuse_options(arm)
+    layers = list(range(arm.split, model.n_layers))
+    fills = {i: _layer_fill(arm, model, i) for i in layers}
     if P == 0:
         return cache, P
     dev = h_split.device
@@ -272,27 +369,39 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
     rows = None
     if exact_rows is not None and len(exact_rows) > 0:
         rows = check_rows(exact_rows, P).to(dev)
+    computed = rows is not None and hr is None
+    if hr is not None and "none" in fills.values():
+        raise ValueError("fill 'none' runs the exact rows' layers itself; it takes no given row inputs")
+    if oracle is None and "oracle" in fills.values():
+        raise ValueError("fill 'oracle' fills from the true late-layer inputs: pass oracle={layer: [>= P, H]}")
     H = h_split.shape[1]
-    layers = list(range(arm.split, model.n_layers))
     for i in layers:                                    # allocate / grow every cache before any launch
         if model.layer_types[i] == "attn":
-            model.reserve(cache[i], P, model.n_kv, model.head_dim, dev)
+            model.reserve(cache[i], rows.shape[0] if fills[i] == "none" and rows is not None else P,
+                          model.n_kv, model.head_dim, dev)
     xbuf = [torch.empty(P, H, dtype=torch.bfloat16, device=dev) for _ in range(2)]
     sbuf = [torch.empty(P, ops.ssq_parts(H), dtype=torch.float32, device=dev) for _ in range(2)]
-    base_ssq = ops.row_ssq(b) if arm.fill == "identity" and rows is None else None
-    computed = rows is not None and hr is None
+    base_ssq = (ops.row_ssq(b) if rows is None and "identity" in fills.values() else None)
     state = {"hr": ops.row_gather(b, rows)[0] if computed else None}
+    qpos = rows if rows is not None else None
     inputs = {}
 
     def produce(i, slot):
-        if arm.fill == "proj":
+        f = fills[i]
+        if f == "none":
+            inputs[slot] = None
+            return
+        if f == "proj":
             W = arm.projector._maps(dev)[0][i]
             x, ssq = arm.projector.apply(i, b, xbuf[slot], sbuf[slot],
                                          workspace=model.gemm_workspace(P, W.shape[0], W.shape[1], dev, "produce"))
-        elif rows is None:
+        elif f == "identity" and rows is None:
             x, ssq = b, base_ssq
         else:
-            x = xbuf[slot].copy_(b)
+            src = b if f == "identity" else oracle[i][:P]
+            if src.shape != b.shape:
+                raise ValueError(f"oracle inputs of layer {i}: shape {tuple(src.shape)}, expected {tuple(b.shape)}")
+            x = xbuf[slot].copy_(src)
             ssq = ops.row_ssq(x, sbuf[slot])
         if rows is not None and not computed:
             hri = (hr[i] if isinstance(hr, dict) else hr).to(dev, torch.bfloat16)
@@ -302,6 +411,12 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
         inputs[slot] = (x, ssq)
 
     def consume(i, slot):
+        if fills[i] == "none":
+            if rows is not None:                        # only the exact rows reach this layer
+                if row_inputs is not None:
+                    row_inputs[i] = state["hr"]
+                state["hr"] = model.layer(i, state["hr"], qpos, cache)[0]
+            return
         x, ssq = inputs[slot]
         if computed:
             if row_inputs is not None:
@@ -315,37 +430,91 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
     return cache, P
 
 
-def finish(model, h_split, arm, keep, exact_rows=None, hr=None, cache=None, row_inputs=None):
-    """Layers >= arm.split for one arm, as finish() runs them (code/kva/kva.py:319-460) for the 'proj'
-    and 'identity' fills: every late layer's cache is filled from the prefix rows [0, P) of h_split
-    (fill_late, with exact rows as there), and the exact tail rows [P, N) run through each late layer
-    in order (FillModel.layer over that layer's filled cache, kva.py:457). The fill of a layer never
-    reads the tail, so filling every layer first gives the reference's results. Each attention cache
-    is sized once for P + T rows. arm.st {layer: [heads, dk, dv]} is added to each late GDN layer's filled
-    recurrent state before the tail. Returns (logits of the last `keep` rows [keep, V] fp32, cache, P)."""
-    n = h_split.shape[0]
+def run_lower(model, ids, splits):
+    """Exact forward of the layers below max(splits) over all prompt rows (code/kva/kva.py:282-300):
+    ({split: h_split [N, H] bf16}, cache with those layers filled). model needs its lower layers packed."""
+    splits = set(splits)
+    top = max(splits)
+    got = {}
+
+    def hook(i, h):
+        if i in splits:
+            got[i] = h
+
+    cache = model.new_cache()
+    if top == 0:
+        got[0] = model.embed(ids)[0]
+        return got, cache
+    _, cache = model.forward_exact(ids, hook=hook, cache=cache, stop=top)
+    return got, cache
+
+
+def finish(model, ids, h_split, lower_cache, arm, keep, oracle=None, keep_cache=True, fill_store=None,
+           fill_reuse=None, exact_rows=None, row_inputs=None, hook=None, mix=None, hr=None):
+    """Layers >= arm.split for one arm, as finish() runs them (code/kva/kva.py:319-460), with the reference's
+    call signature: ids [N] (only its length is read here), h_split [N, H] (moved to the model's device as
+    bf16), lower_cache (the caches of layers < split from run_lower, kept; None for a model packed with its
+    late layers only), keep (the last rows whose logits to return), oracle ({layer: true inputs [>= P, H]}
+    for 'oracle' fills), keep_cache=False (each late layer's cache is dropped once the tail has run it),
+    fill_store (dict: receives each late layer's cache right after its prefix fill, before + st), fill_reuse
+    (such a dict from an arm with the same fill, split and P: used instead of filling), exact_rows and
+    row_inputs (as fill_late), hook(i, h) (the tail's rows before layer i runs). mix feeds context arms,
+    which are refused. hr: given exact-row inputs (fill_late's hr), an addition to the reference's API.
+
+    Every late layer's cache is filled from the prefix rows [0, P) first (fill_late), then the exact tail
+    [P, N) runs through each late layer in order (FillModel.layer over that layer's filled cache,
+    kva.py:457). The fill of a layer never reads the tail, so this gives the reference's interleaved order's
+    results. Attention caches are sized once for all N rows. arm.st {layer: [heads, dk, dv]} is added to
+    each late GDN layer's filled recurrent state before the tail. Returns (logits of the last `keep` rows
+    [keep, V] fp32, cache, P)."""
+    n = int(ids.shape[0]) if hasattr(ids, "shape") else len(ids)
+    if h_split.shape[0] != n:
+        raise ValueError(f"h_split has {h_split.shape[0]} rows for {n} ids")
+    if arm.fill == "swiftkv_native" or mix is not None:
+        from ._lib import UnsupportedArchitecture
+        raise UnsupportedArchitecture(f"arm {arm.name!r}: SwiftKV native and context arms are not implemented")
+    _refuse_options(arm)
     P = arm.prefix_len(n)
     T = n - P
     if keep > T:
         raise ValueError(f"keep {keep} rows > exact tail {T}")
-    if arm.fill not in ("proj", "identity", "exact"):
-        raise ValueError(f"fill {arm.fill!r}: finish runs 'proj', 'identity' and 'exact'")
-    cache = model.new_cache() if cache is None else cache
-    dev = h_split.device
-    layers = list(range(arm.split, model.n_layers))
+    split = arm.split
+    dev = model.device
+    h_split = h_split.to(dev, torch.bfloat16)
+    cache = ([dict(c) for c in lower_cache[:split]] if lower_cache is not None else [dict() for _ in range(split)])
+    cache += [dict() for _ in range(model.n_layers - split)]
+    layers = list(range(split, model.n_layers))
+    has_rows = exact_rows is not None and len(exact_rows) > 0
+    if fill_reuse is not None and has_rows:
+        raise ValueError("exact rows: sorted unique rows < P, no fill reuse")
+    if P > 0 and fill_reuse is not None:
+        for i in layers:
+            got = fill_reuse[i].get("n", P)
+            if got != P:
+                raise ValueError(f"reused fill of layer {i} has {got} rows, P = {P}")
+            cache[i] = dict(fill_reuse[i])
     for i in layers:
         if model.layer_types[i] == "attn":
-            model.reserve(cache[i], n, model.n_kv, model.head_dim, dev)
+            model.reserve(cache[i], n - cache[i].get("n", 0), model.n_kv, model.head_dim, dev)
+    if P > 0 and fill_reuse is None:
+        fill_late(model, h_split, arm, exact_rows=exact_rows, hr=hr, cache=cache, row_inputs=row_inputs, oracle=oracle)
     if P > 0:
-        fill_late(model, h_split, arm, exact_rows=exact_rows, hr=hr, cache=cache, row_inputs=row_inputs)
-        for i, st in (arm.st or {}).items():            # GDN terminal-state corrections (kva.py:452-454)
-            if i in layers and model.layer_types[i] == "gdn":
+        for i in layers:
+            if fill_store is not None:
+                fill_store[i] = dict(cache[i])
+            st = arm.st.get(i) if arm.st else None   # GDN terminal-state corrections (kva.py:452-454)
+            if st is not None:
+                if model.layer_types[i] != "gdn":
+                    raise ValueError(f"st corrects GDN recurrent states; layer {i} is attention")
                 cache[i]["rec"] = cache[i]["rec"] + st.to(cache[i]["rec"])
     h = h_split[P:]
     pos = torch.arange(P, n, device=dev)
     cs = model.rope_table(pos)
     ssq = ops.row_ssq(h)
     for i in layers:
+        if hook is not None:
+            hook(i, h)
         h, ssq = model.layer(i, h, pos, cache, ssq=ssq, cs=cs)
+        if not keep_cache:
+            cache[i] = {}
     return model.logits(h[T - keep:], ssq[T - keep:]), cache, P
-

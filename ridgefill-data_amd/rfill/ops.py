@@ -200,6 +200,8 @@ def norm_linear(x, ssq, eps, w, out=None, workspace=None):
         raise ValueError("norm_linear: shapes")
     out = torch.empty(P, N, dtype=torch.bfloat16, device=x.device) if out is None else out
     _need(out, "out", torch.bfloat16, 2)
+    if tuple(out.shape) != (P, N) or not ssq.is_contiguous():
+        raise ValueError(f"norm_linear: out {tuple(out.shape)}, expected {(P, N)}; ssq must be contiguous")
     ws, nb = _ws(workspace, P, N, H, x.device)
     _lib.call("rf_norm_linear", _ptr(x), x.stride(0), _ptr(ssq), P, H, float(eps), _ptr(w), N, _ptr(out), out.stride(0),
               _ptr(ws), nb, _stream(x))
@@ -332,6 +334,8 @@ def residual_add(x, y, out=None, ssq=None):
     ssq = torch.empty(rows, ssq_parts(H), dtype=torch.float32, device=x.device) if ssq is None else ssq
     _need(out, "out", torch.bfloat16, 2)
     _need(ssq, "ssq", torch.float32, 2)
+    if tuple(out.shape) != (rows, H) or tuple(ssq.shape) != (rows, H // SSQ_COLS) or not ssq.is_contiguous():
+        raise ValueError(f"residual_add: out {tuple(out.shape)}, ssq {tuple(ssq.shape)} for rows {rows}, width {H}")
     _lib.call("rf_residual_add", _ptr(x), x.stride(0), _ptr(y), y.stride(0), _ptr(out), out.stride(0), _ptr(ssq), rows,
               H, _stream(x))
     return out, ssq
@@ -341,9 +345,13 @@ def silu_mul(gu, out=None):
     """SwiGLU of gu = [gate | up] [rows, 2 I]: bf16(bf16(silu(gate)) * up) [rows, I]."""
     _need(gu, "gu", torch.bfloat16, 2)
     rows, two_i = gu.shape
+    if two_i % 2:
+        raise ValueError(f"silu_mul: gu width {two_i} is odd (expected gate and up halves)")
     I = two_i // 2
     out = torch.empty(rows, I, dtype=torch.bfloat16, device=gu.device) if out is None else out
     _need(out, "out", torch.bfloat16, 2)
+    if tuple(out.shape) != (rows, I):
+        raise ValueError(f"silu_mul: out {tuple(out.shape)}, expected {(rows, I)}")
     _lib.call("rf_silu_mul", _ptr(gu), gu.stride(0), rows, I, _ptr(out), out.stride(0), _stream(gu))
     return out
 

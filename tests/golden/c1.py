@@ -132,3 +132,29 @@ def summarise(state, state2, maps, runs):
             if row_inputs:
                 out[f"{name}_hr_{i}"] = row_inputs[i].double().numpy()
     return out
+
+
+# ---- the map file fixture (Projector.save / load, code/kva/kva.py:161-193)
+
+PROJ_FIXTURE = Path(__file__).with_name("projector_ref.safetensors")
+PROJ_SPLIT = 3
+PROJ_META = {"fit": "golden", "lam": 0.01, "layers": "3,4", "n": 4096}
+
+
+def projector_tensors():
+    """The fixture projector's maps {layer: (W [24, 40] fp32, bias [24] fp32)} for late layers 3 and 4 of a
+    5-layer stack: seeded normals at a few scales, so the bf16 cast in save() rounds most entries, plus
+    entries that pin the cast (an exact bf16 value, a round-to-nearest-even tie, -0.0) and the |w| <= 1e4
+    limit (1e4 itself, which save() and load() accept)."""
+    g = torch.Generator().manual_seed(40)
+    out = {}
+    for L, s in ((3, 0.05), (4, 3.0)):
+        w = s * torch.randn(24, 40, generator=g, dtype=torch.float32)
+        b = 1e-3 * torch.randn(24, generator=g, dtype=torch.float32)
+        w[0, 0] = 1.5                      # exact in bf16
+        w[0, 1] = 1.0 + 2.0 ** -8          # tie between 1 and 1 + 2^-7: rounds to the even pattern, 1.0
+        w[0, 2] = 1.0 + 3 * 2.0 ** -8      # tie between 1 + 2^-7 and 1 + 2^-6: rounds to 1 + 2^-6
+        w[0, 3] = -0.0
+        w[1, 0] = 1e4
+        out[L] = (w, b)
+    return out

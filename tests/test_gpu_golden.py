@@ -126,7 +126,7 @@ def test_finish_matches_reference(dev, gold, run, name):
     fill = "identity" if name == "identity" else "proj"
     arm = Arm(name, split=S, tail=c1.TAIL, fill=fill, projector=Projector(S, W, B) if fill == "proj" else None)
     rows = c1.exact_rows() if name == "exact" else None
-    logits, cache, P = finish(model, run["hs"][S].to(dev, torch.bfloat16), arm, c1.KEEP, exact_rows=rows)
+    logits, cache, P = finish(model, c1.prompt_ids(), run["hs"][S], None, arm, c1.KEEP, exact_rows=rows)
     torch.cuda.synchronize()
     assert P == int(gold[f"{name}_P"])
     lg = logits.double().cpu()

@@ -207,7 +207,7 @@ def test_hybrid_finish_matches_oracle(dev, exact):
     m = FillModel(cfg, t, dev)
     arm = Arm("ridgefill", split=split, tail=tail, fill="proj", projector=Projector(split, W, B),
               st={i: s.to(dev) for i, s in st.items()})
-    logits, cache, P_got = finish(m, h.to(dev), arm, keep, exact_rows=rows)
+    logits, cache, P_got = finish(m, torch.zeros(N, dtype=torch.long), h.to(dev), None, arm, keep, exact_rows=rows)
     torch.cuda.synchronize()
     om = OM.OracleModel(cfg, t, dtype=torch.bfloat16)
     oarm = OK.Arm("ridgefill", split=split, tail=tail, fill="proj", projector=OK.Projector(split, W, B), st=st)

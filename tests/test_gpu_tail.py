@@ -90,7 +90,7 @@ def test_finish_matches_oracle(dev, exact):
     rows = torch.randperm(P, generator=g)[:18].sort().values if exact else None
     m = FillModel(cfg, t, dev)
     arm = Arm("ridgefill", split=split, tail=tail, fill="proj", projector=Projector(split, W, B))
-    logits, cache, P_got = finish(m, h.to(dev), arm, keep, exact_rows=rows)
+    logits, cache, P_got = finish(m, torch.zeros(N, dtype=torch.long), h.to(dev), None, arm, keep, exact_rows=rows)
     torch.cuda.synchronize()
     om = OM.OracleModel(cfg, t, dtype=torch.bfloat16)
     oarm = OK.Arm("ridgefill", split=split, tail=tail, fill="proj", projector=OK.Projector(split, W, B))
@@ -114,10 +114,11 @@ def test_finish_refuses(dev):
     cfg, t = case("llama_c1", layers=2)
     m = FillModel(cfg, t, dev)
     h = inputs(300, cfg["hidden_size"], seed=3).to(dev)
+    ids = torch.zeros(300, dtype=torch.long)
     with pytest.raises(ValueError):
-        finish(m, h, Arm("x", split=1, tail=50, fill="identity"), keep=51)      # keep > tail
+        finish(m, ids, h, None, Arm("x", split=1, tail=50, fill="identity"), keep=51)      # keep > tail
     with pytest.raises(ValueError):
-        finish(m, h, Arm("x", split=1, tail=50, fill="oracle"), keep=10)
+        finish(m, ids, h, None, Arm("x", split=1, tail=50, fill="oracle"), keep=10)
 
 
 def test_finish_exact_arm_is_the_exact_layer_stack(dev):
@@ -127,7 +128,7 @@ def test_finish_exact_arm_is_the_exact_layer_stack(dev):
     cfg, t = case("llama_c1", layers=3)
     m = FillModel(cfg, t, dev)
     h = inputs(200, cfg["hidden_size"], seed=4).to(dev)
-    logits, cache, P = finish(m, h, Arm("exact", split=1, fill="exact"), keep=20)
+    logits, cache, P = finish(m, torch.zeros(200, dtype=torch.long), h, None, Arm("exact", split=1, fill="exact"), keep=20)
     c2 = m.new_cache()
     x = h
     pos = torch.arange(200, device=dev)
