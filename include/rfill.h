@@ -233,6 +233,22 @@ int rf_gated_rms_norm(const uint16_t* x, int64_t ldx, const uint16_t* z, int64_t
 int rf_transpose(const uint16_t* src, int64_t ld_src, int64_t rows, int64_t cols, uint16_t* dst, int64_t ld_dst,
                  float* partial, hipStream_t stream);
 
+/* rf_transpose with centring, for channels whose mean dwarfs their spread: column c's values become
+ * d = x - shift[c] (fp32), written to dst as hi = bf16(d) (round to nearest even) and, when lo_row[c] >= 0,
+ * mid = bf16(d - hi) to row lo_row[c] of dst_lo and lo = bf16(d - hi - mid) to row n_centred + lo_row[c]
+ * (row stride ld_dst). hi + mid + lo == d exactly, so one rf_gram_accumulate over [dst rows; dst_lo rows]
+ * yields the products of the centred values -- the reference subtracts its shifts before its per-block
+ * fp32 GEMM (code/kva/ridge.py:44-47, :58-61; code/scripts/fit_sweep.py:100-105) -- on bf16 MFMA. Columns
+ * with shift 0 and lo_row -1 are copied as rf_transpose copies them. partial / partial_sq (each optional):
+ * fp32 column sums / sums of squares of d per 64-row tile, [round_up(rows, 64) / 64, cols] (fold with
+ * rf_colsum_fold). shift, lo_row (int32 [cols], distinct rows < n_centred for the centred columns) and
+ * dst_lo ([2 n_centred, ld_dst] at least) are all given or all NULL (then this is rf_transpose plus the
+ * squares). A shifted column needs a lo row (without one its values are rounded to bf16). Limits as
+ * rf_transpose; dst_lo 16-byte aligned. */
+int rf_transpose_centred(const uint16_t* src, int64_t ld_src, int64_t rows, int64_t cols, const float* shift,
+                         const int32_t* lo_row, int64_t n_centred, uint16_t* dst, int64_t ld_dst, uint16_t* dst_lo,
+                         float* partial, float* partial_sq, hipStream_t stream);
+
 /* sums[c] += sum_j partial[j, c] in fp64 and a fixed order (16 interleaved runs over j, then a pairwise
  * fold; the same bits every run): the sum(0) of a sample block (RidgeStats' sx / sy, code/kva/ridge.py:46, :61). */
 int rf_colsum_fold(const float* partial, int64_t ntiles, int64_t cols, double* sums, hipStream_t stream);

@@ -8,47 +8,96 @@ namespace {
 
 constexpr int TT = 64;                            // transpose tile: 64 rows x 64 columns
 
+struct TransposeArgs {
+  const uint16_t* src;
+  int64_t ld_src, rows;
+  int cols;
+  uint16_t* dst;          // [cols, ld_dst]: output row c = source column c
+  int64_t ld_dst;
+  const float* shift;     // [cols] fp32 or null (no centring)
+  const int* lo_row;      // [cols]: row of dst_lo receiving column c's middle part, or -1; null with shift null
+  uint16_t* dst_lo;       // [2 n_centred, ld_dst]: middle parts in rows [0, n_centred), low parts after them
+  int64_t lo_gap;         // n_centred: row offset of a column's low part from its middle part
+  float* partial;         // [tiles, cols] column sums per 64-row tile, or null
+  float* partial_sq;      // [tiles, cols] column sums of squares per 64-row tile, or null
+};
+
 // Block = one 64 x 64 tile, 256 threads. Load: thread t takes tile row t / 4, columns (t % 4) * 16 ..
 // + 15 (two 16-byte loads). Store: thread t writes output row (source column) t / 4, source rows
-// (t % 4) * 16 .. + 15. Rows at or past `rows` read as zeros, so padded output columns are zero.
-__global__ __launch_bounds__(256) void k_transpose(const uint16_t* __restrict__ src, int64_t ld_src, int64_t rows,
-                                                   int cols, uint16_t* __restrict__ dst, int64_t ld_dst,
-                                                   float* __restrict__ partial) {
+// (t % 4) * 16 .. + 15. Rows at or past `rows` give zeros, so padded output columns are zero.
+// Without a shift the values are copied bit for bit. With one, column c's value d = x - shift[c] (fp32)
+// is written as hi = bf16(d) and, if lo_row[c] >= 0, mid = bf16(d - hi) into row lo_row[c] of dst_lo and
+// lo = bf16(d - hi - mid) into row lo_row[c] + lo_gap: each remainder is exact in fp32 and the last one
+// has at most 8 significant bits, so hi + mid + lo == d exactly and a Gram product over [hi rows; mid and
+// lo rows] gives the products of the centred fp32 values. The sums (and squares) are of d, each 64-row
+// tile's 16 values per thread in order, then the 4 threads of a column pairwise.
+__global__ __launch_bounds__(256) void k_transpose(TransposeArgs a) {
   __shared__ uint16_t tile[TT][TT + 2];
   const int t = threadIdx.x;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * TT;
   const int c0 = blockIdx.y * TT;
   {
     const int r = t >> 2, c = (t & 3) * 16;
-    uint4 a = make_uint4(0u, 0u, 0u, 0u), b = a;
-    if (r0 + r < rows) {
-      const uint4* p = reinterpret_cast<const uint4*>(src + (r0 + r) * ld_src + c0 + c);
-      a = p[0];
-      b = p[1];
+    uint4 x0 = make_uint4(0u, 0u, 0u, 0u), x1 = x0;
+    if (r0 + r < a.rows) {
+      const uint4* p = reinterpret_cast<const uint4*>(a.src + (r0 + r) * a.ld_src + c0 + c);
+      x0 = p[0];
+      x1 = p[1];
     }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      tile[r][c + e] = lane_of(a, e);
-      tile[r][c + 8 + e] = lane_of(b, e);
+      tile[r][c + e] = lane_of(x0, e);
+      tile[r][c + 8 + e] = lane_of(x1, e);
     }
   }
   __syncthreads();
   const int oc = t >> 2, rr = (t & 3) * 16;       // output row = source column c0 + oc
-  uint16_t v[16];
-  float s = 0.f;
+  uint16_t v[16], mid[16], lo[16];
+  float s = 0.f, q = 0.f;
+  int lrow = -1;
+  if (a.shift) {
+    const float sh = a.shift[c0 + oc];
+    lrow = a.lo_row[c0 + oc];
 #pragma unroll
-  for (int e = 0; e < 16; ++e) {
-    v[e] = tile[rr + e][oc];
-    s += bf2f(v[e]);
+    for (int e = 0; e < 16; ++e) {
+      const float d = (r0 + rr + e < a.rows) ? bf2f(tile[rr + e][oc]) - sh : 0.f;
+      v[e] = f2bf(d);
+      const float r1 = d - bf2f(v[e]);
+      mid[e] = f2bf(r1);
+      lo[e] = f2bf(r1 - bf2f(mid[e]));
+      s += d;
+      q = fmaf(d, d, q);
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+      v[e] = tile[rr + e][oc];
+      const float w = bf2f(v[e]);
+      s += w;
+      q = fmaf(w, w, q);
+    }
   }
-  uint4* q = reinterpret_cast<uint4*>(dst + static_cast<int64_t>(c0 + oc) * ld_dst + r0 + rr);
-  q[0] = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
-  q[1] = make_uint4(pack2(v[8], v[9]), pack2(v[10], v[11]), pack2(v[12], v[13]), pack2(v[14], v[15]));
-  if (partial) {
-    // the 4 threads of one column are adjacent lanes: fixed-order pairwise sum
-    s += __shfl_xor(s, 1, 64);
-    s += __shfl_xor(s, 2, 64);
-    if ((t & 3) == 0) partial[static_cast<int64_t>(blockIdx.x) * cols + c0 + oc] = s;
+  uint4* o = reinterpret_cast<uint4*>(a.dst + static_cast<int64_t>(c0 + oc) * a.ld_dst + r0 + rr);
+  o[0] = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+  o[1] = make_uint4(pack2(v[8], v[9]), pack2(v[10], v[11]), pack2(v[12], v[13]), pack2(v[14], v[15]));
+  if (lrow >= 0) {
+    uint4* m = reinterpret_cast<uint4*>(a.dst_lo + static_cast<int64_t>(lrow) * a.ld_dst + r0 + rr);
+    m[0] = make_uint4(pack2(mid[0], mid[1]), pack2(mid[2], mid[3]), pack2(mid[4], mid[5]), pack2(mid[6], mid[7]));
+    m[1] = make_uint4(pack2(mid[8], mid[9]), pack2(mid[10], mid[11]), pack2(mid[12], mid[13]),
+                      pack2(mid[14], mid[15]));
+    uint4* l = reinterpret_cast<uint4*>(a.dst_lo + (static_cast<int64_t>(lrow) + a.lo_gap) * a.ld_dst + r0 + rr);
+    l[0] = make_uint4(pack2(lo[0], lo[1]), pack2(lo[2], lo[3]), pack2(lo[4], lo[5]), pack2(lo[6], lo[7]));
+    l[1] = make_uint4(pack2(lo[8], lo[9]), pack2(lo[10], lo[11]), pack2(lo[12], lo[13]), pack2(lo[14], lo[15]));
+  }
+  // the 4 threads of one column are adjacent lanes: fixed-order pairwise sums
+  s += __shfl_xor(s, 1, 64);
+  s += __shfl_xor(s, 2, 64);
+  q += __shfl_xor(q, 1, 64);
+  q += __shfl_xor(q, 2, 64);
+  if ((t & 3) == 0) {
+    const int64_t at = static_cast<int64_t>(blockIdx.x) * a.cols + c0 + oc;
+    if (a.partial) a.partial[at] = s;
+    if (a.partial_sq) a.partial_sq[at] = q;
   }
 }
 
@@ -166,19 +215,40 @@ __global__ __launch_bounds__(256) void k_cosine_fold(const float2* __restrict__ 
 
 using namespace rf;
 
-extern "C" int rf_transpose(const uint16_t* src, int64_t ld_src, int64_t rows, int64_t cols, uint16_t* dst,
-                            int64_t ld_dst, float* partial, hipStream_t stream) {
-  if (!src || !dst) return fail(RF_EINVAL_ARG, "rf_transpose: null pointer");
+static int launch_transpose(const char* fn, const TransposeArgs& a, int64_t rows, int64_t cols, int64_t ld_src,
+                            int64_t ld_dst, hipStream_t stream) {
+  if (!a.src || !a.dst) return fail(RF_EINVAL_ARG, "%s: null pointer", fn);
   const int64_t rows_out = (rows + TT - 1) / TT * TT;
   if (rows < 0 || cols <= 0 || cols % TT || cols > (1 << 24) || ld_src < cols || ld_src % 8 || ld_dst < rows_out ||
       ld_dst % 8 || rows_out / TT > (1ll << 31) - 1)
-    return fail(RF_EINVAL_SHAPE, "rf_transpose: rows %lld, cols %lld (multiple of 64), ld_src %lld, ld_dst %lld "
-                "(>= rows rounded up to 64)", (long long)rows, (long long)cols, (long long)ld_src, (long long)ld_dst);
-  if (!aligned16(src) || !aligned16(dst)) return fail(RF_EINVAL_SHAPE, "rf_transpose: 16-byte alignment");
+    return fail(RF_EINVAL_SHAPE, "%s: rows %lld, cols %lld (multiple of 64), ld_src %lld, ld_dst %lld "
+                "(>= rows rounded up to 64)", fn, (long long)rows, (long long)cols, (long long)ld_src, (long long)ld_dst);
+  if (!aligned16(a.src) || !aligned16(a.dst) || (a.dst_lo && !aligned16(a.dst_lo)))
+    return fail(RF_EINVAL_SHAPE, "%s: 16-byte alignment", fn);
   if (rows == 0) return RF_OK;
   hipLaunchKernelGGL(k_transpose, dim3(static_cast<unsigned>(rows_out / TT), static_cast<unsigned>(cols / TT)),
-                     dim3(256), 0, stream, src, ld_src, rows, static_cast<int>(cols), dst, ld_dst, partial);
-  return check_launch("rf_transpose");
+                     dim3(256), 0, stream, a);
+  return check_launch(fn);
+}
+
+extern "C" int rf_transpose(const uint16_t* src, int64_t ld_src, int64_t rows, int64_t cols, uint16_t* dst,
+                            int64_t ld_dst, float* partial, hipStream_t stream) {
+  const TransposeArgs a{src, ld_src, rows, static_cast<int>(cols), dst, ld_dst, nullptr, nullptr, nullptr, 0,
+                        partial, nullptr};
+  return launch_transpose("rf_transpose", a, rows, cols, ld_src, ld_dst, stream);
+}
+
+extern "C" int rf_transpose_centred(const uint16_t* src, int64_t ld_src, int64_t rows, int64_t cols,
+                                    const float* shift, const int32_t* lo_row, int64_t n_centred, uint16_t* dst,
+                                    int64_t ld_dst, uint16_t* dst_lo, float* partial, float* partial_sq,
+                                    hipStream_t stream) {
+  if ((shift == nullptr) != (lo_row == nullptr) || (shift && !dst_lo))
+    return fail(RF_EINVAL_ARG, "rf_transpose_centred: shift, lo_row and dst_lo go together");
+  if (n_centred < 0 || n_centred > cols)
+    return fail(RF_EINVAL_ARG, "rf_transpose_centred: n_centred %lld", (long long)n_centred);
+  const TransposeArgs a{src, ld_src, rows, static_cast<int>(cols), dst, ld_dst, shift, lo_row, dst_lo, n_centred,
+                        partial, partial_sq};
+  return launch_transpose("rf_transpose_centred", a, rows, cols, ld_src, ld_dst, stream);
 }
 
 extern "C" int rf_colsum_fold(const float* partial, int64_t ntiles, int64_t cols, double* sums, hipStream_t stream) {

@@ -41,6 +41,7 @@ SIGNATURES = {
     "rf_gdn_fill": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
     "rf_gdn_workspace_bytes": [_I64, _I32, _I32, _I32, _I32, _PSZ],
     "rf_transpose": [_P, _I64, _I64, _I64, _P, _I64, _P, _P],
+    "rf_transpose_centred": [_P, _I64, _I64, _I64, _P, _P, _I64, _P, _I64, _P, _P, _P, _P],
     "rf_colsum_fold": [_P, _I64, _I64, _P, _P],
     "rf_gram_accumulate": [_P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P],
     "rf_row_gather": [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _P],

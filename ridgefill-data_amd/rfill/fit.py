@@ -11,13 +11,15 @@ split's fp64 accumulator [H, (L - S) H]: its first H columns are X_S^T X_S and i
 X_S^T H_i -- every (S, i) pair of the reference in one MFMA launch per split, over up to B rows at a time.
 The column sums of each layer come from the transpose (rf_colsum_fold) and serve every split.
 
-The device keeps raw sums; state(S) re-centres them in fp64 on the reference's shifts -- the first
-document's means of h_S and of h_i (fit_sweep.py:98-99, :104-105) -- so the state dict has
-split_state()'s layout and meaning (fit_sweep.py:147-166). The shift is the first document's fp64 column
-sum over its row count, rounded to fp32 as the reference's h.float().mean(0) is. Products are bf16 x bf16
-(exact) summed in fp32 over a block on MFMA and added into fp64, as the reference's per-document fp32
-GEMM is added into fp64; what differs is only the fp32 rounding inside a block, which grows with
-|mean| / spread of a channel, since the reference subtracts the shift before its GEMM.
+Centring, as in rfill.ridge: the reference subtracts its shifts -- the first document's means of h_S and of
+h_i (fit_sweep.py:98-99, :104-105) -- before its per-document fp32 GEMM. Here each layer's channels whose
+first-document mean exceeds their spread (at most ridge.SHIFT_MAX) are centred in the transpose, as three
+bf16 parts whose sum is exact; every layer owns H main rows and ridge.LO_ROWS extra rows of the block, and
+the extra rows' products come out of the same Gram launch. state(S) combines them in fp64 and moves every sum onto the
+reference's shifts (the first document's fp64 column sums over its row count, rounded to fp32 as the
+reference's h.float().mean(0) is), so the state dict has split_state()'s layout and meaning
+(fit_sweep.py:147-166). Products are bf16 x bf16 (exact) summed in fp32 over a block on MFMA and added
+into fp64, as the reference's per-document fp32 GEMM is added into fp64.
 
 Selection (fit_sweep.py:298-318). For each held-out document: one exact forward (stopped after the last
 layer's input); per late layer i the true reads norm(h_i) [W_k; W_v]^T (one norm_linear GEMM, the
@@ -47,16 +49,16 @@ class Capture:
         if block <= 0 or block % 64:
             raise ValueError("block must be a positive multiple of 64")
         self.S0, self.H, self.block = self.splits[0], H, block
+        self.R = H + ridge.LO_ROWS                        # block rows per layer: H main rows, then the lo rows
         dev = model.device
         f64 = dict(dtype=torch.float64, device=dev)
         nl = self.L - self.S0
         self.n, self.docs = 0, 0
-        self.s1 = torch.zeros(nl, H, **f64)               # raw column sums of h_i, i >= S0
-        self.first = torch.zeros(nl, H, **f64)            # the first document's column sums
-        self.n_first = 0
-        self.acc = {S: torch.zeros(H, (self.L - S) * H, **f64) for S in self.splits}
+        self.s1 = torch.zeros(nl, H, **f64)               # column sums of each layer's centred values
+        self.cen = [None] * nl                            # each layer's centring (from the first document)
+        self.acc = {S: torch.zeros(self.R, (self.L - S) * self.R, **f64) for S in self.splits}
         self.T = None
-        self.part = None
+        self.part = self.part_sq = None
         self.off = 0
 
     def _room(self, kp):
@@ -65,22 +67,25 @@ class Capture:
             self.flush()
             cap = max(self.block, kp)
             dev = self.model.device
-            self.T = torch.empty((self.L - self.S0) * self.H, cap, dtype=torch.bfloat16, device=dev)
+            self.T = torch.zeros((self.L - self.S0) * self.R, cap, dtype=torch.bfloat16, device=dev)
             self.part = torch.empty(cap // 64, self.H, dtype=torch.float32, device=dev)
+            self.part_sq = torch.empty_like(self.part)
         elif self.off + kp > cap:
             self.flush()
 
     def _hook(self, i, h):
         if i == "final" or i < self.S0:
             return
-        rows = h.shape[0]
-        kp = (rows + 63) // 64 * 64
-        r = (i - self.S0) * self.H
-        part = self.part[:kp // 64]
-        ridge._transpose(h, self.T[r:r + self.H, self.off:self.off + kp], part)
-        ridge._colsum_fold(part, self.s1[i - self.S0])
-        if self.docs == 0:
-            ridge._colsum_fold(part, self.first[i - self.S0])
+        j = i - self.S0
+        kp = (h.shape[0] + 63) // 64 * 64
+        r = j * self.R
+        main, lo = self.T[r:r + self.H, self.off:self.off + kp], self.T[r + self.H:r + self.R, self.off:self.off + kp]
+        part = ridge.tiles_view(self.part, kp // 64, self.H)
+        if self.cen[j] is None:                           # the first document: its means are the shifts
+            self.cen[j] = ridge.Centring.of_rows(h, self.T[r:r + self.H, self.off:], self.part, self.part_sq)
+        c = self.cen[j]
+        ridge.transpose_centred(h, main, lo, c.shift, c.lo_row, part, n_centred=c.s)
+        ridge._colsum_fold(part, self.s1[j])
 
     @torch.no_grad()
     def add_document(self, ids):
@@ -92,8 +97,6 @@ class Capture:
         self._room(kp)
         self.model.forward_exact(ids, hook=self._hook, stop=self.L - 1)
         self.off += kp
-        if self.docs == 0:
-            self.n_first = n
         self.docs += 1
         self.n += n
 
@@ -101,10 +104,11 @@ class Capture:
         """Add the buffered rows' products into every split's accumulator."""
         if not self.off:
             return
-        K, H = self.off, self.H
+        K, H, R = self.off, self.H, self.R
         for S in self.splits:
-            r = (S - self.S0) * H
-            ridge.gram_accumulate(self.T[r:r + H, :K], self.T[r:, :K], self.acc[S])
+            r = (S - self.S0) * R
+            m = H + 2 * self.cen[S - self.S0].s
+            ridge.gram_accumulate(self.T[r:r + m, :K], self.T[r:, :K], self.acc[S][:m])
         self.off = 0
 
     def state(self, S, device="cpu"):
@@ -114,22 +118,20 @@ class Capture:
         if not self.n:
             raise ValueError("no documents captured")
         self.flush()
-        H, n = self.H, float(self.n)
-        mean = (self.first / self.n_first).float().double()          # fp32 shifts, as h.float().mean(0)
+        H, R, n = self.H, self.R, float(self.n)
         j = S - self.S0
-        cx, s1x = mean[j], self.s1[j]
-        raw = self.acc[S]
+        cx, s1x = self.cen[j], self.s1[j]
+        G = self.acc[S]
         late = list(range(S, self.L))
         cy, sy, sxy = {}, {}, {}
         for i in late:
-            c, s1y = mean[i - self.S0], self.s1[i - self.S0]
-            blk = raw[:, (i - S) * H:(i - S + 1) * H]
-            cy[i] = c.to(device)
-            sy[i] = (s1y - n * c).to(device)
-            sxy[i] = (blk - torch.outer(cx, s1y) - torch.outer(s1x, c) + n * torch.outer(cx, c)).to(device)
-        sxx = raw[:, :H] - torch.outer(cx, s1x) - torch.outer(s1x, cx) + n * torch.outer(cx, cx)
-        return dict(split=S, layers=late, dim=H, n=self.n, cx=cx.to(device), cy=cy, sx=(s1x - n * cx).to(device),
-                    sxx=sxx.to(device), sy=sy, sxy=sxy)
+            c, s1y = self.cen[i - self.S0], self.s1[i - self.S0]
+            blk = G[:, (i - S) * R:(i - S + 1) * R]
+            cy[i] = c.c.to(device)
+            sy[i] = (s1y - n * c.delta).to(device)
+            sxy[i] = ridge.recentre(ridge.centred_products(blk, H, cx, H, c), s1x, s1y, cx.delta, c.delta, n).to(device)
+        return dict(split=S, layers=late, dim=H, n=self.n, cx=cx.c.to(device), cy=cy,
+                    sx=(s1x - n * cx.delta).to(device), sxx=sxy[S].clone(), sy=sy, sxy=sxy)
 
 
 def fit_maps(state, lambdas=LAMBDAS, device="cuda"):

@@ -2,13 +2,19 @@
 statistics accumulated by librfill's MFMA Gram kernel.
 
 Per sample block (default 8192 rows, the reference's block): the block is transposed into the
-K-contiguous operands X^T, Y_i^T (rf_transpose, which also yields the column sums), then
+K-contiguous operands X^T, Y_i^T (rf_transpose_centred, which also yields the column sums), then
 rf_gram_accumulate adds X^T X and X^T Y_i -- bf16 products summed in fp32 over the block, as the
-reference's per-block fp32 GEMM (code/kva/ridge.py:47, :62) -- into fp64 accumulators. The device keeps
-raw sums (n, sum x, X^T X, sum y_i, X^T Y_i); state() re-centres them in fp64 on the reference's shifts
-(the first block's means, code/kva/ridge.py:37-38, :56-57), so the state dict has the reference's
-layout and meaning. Shifting is exact algebra; what differs from shifting each block before its GEMM is
-only the fp32 rounding inside a block, which grows with |mean| / spread of a channel.
+reference's per-block fp32 GEMM (code/kva/ridge.py:47, :62) -- into fp64 accumulators.
+
+Centring. The reference subtracts its shifts (the first block's means, code/kva/ridge.py:37-38, :56-57)
+before each block's fp32 GEMM, which keeps the fp32 sums at the size of the centred values. Here the
+channels whose first-block mean exceeds their spread (mean^2 > variance; at most SHIFT_MAX per operand,
+largest ratio first) are centred in the transpose: their fp32 values x - shift go into the operand as three
+bf16 rows whose sum is exact (hi in the main rows; mid and lo in the rows after them). One Gram product over
+[main rows; mid and lo rows] then carries every centred product. The other channels, whose
+raw sums are at most twice their centred size, are summed raw. state() combines the lo rows' products in
+fp64 and moves every sum onto the reference's shifts by exact fp64 algebra, so the state dict has the
+reference's layout and meaning.
 
 RidgeFit solves W(lam) = (C + lam mean(diag C) I)^-1 Cxy with the bias unpenalised
 (code/kva/ridge.py:80-105) in fp64 on the GPU by a Cholesky factorisation per lam (the same solution the
@@ -19,10 +25,37 @@ import torch
 from . import _lib
 from .ops import _need, _ptr, _stream
 
+SHIFT_MAX = 128      # channels per operand centred before the product (each takes a mid and a lo row)
+LO_ROWS = 256        # extra rows per operand when any channel is centred (keeps the Gram width a multiple of 256)
+
 
 def _transpose(x, dst, partial):
     rows, cols = x.shape
     _lib.call("rf_transpose", _ptr(x), x.stride(0), rows, cols, _ptr(dst), dst.stride(0), _ptr(partial), _stream(x))
+
+
+def transpose_centred(x, dst, dst_lo, shift, lo_row, partial, partial_sq=None, n_centred=0):
+    """x [rows, cols] bf16 -> dst [cols, >= round_up(rows, 64)]: values d = x - shift[c] (fp32) as bf16 hi, with
+    the centred channels' exact remainder as bf16 mid in row lo_row[c] and lo in row n_centred + lo_row[c] of
+    dst_lo (shift / lo_row / dst_lo None: a plain copy). partial / partial_sq: fp32 [tiles, cols] column sums /
+    sums of squares of d per 64-row tile."""
+    rows, cols = x.shape
+    if (shift is None) != (lo_row is None) or (shift is not None and dst_lo is None):
+        raise ValueError("transpose_centred: shift, lo_row and dst_lo go together")
+    if shift is not None:
+        _need(shift, "shift", torch.float32, 1)
+        _need(lo_row, "lo_row", torch.int32, 1)
+        if shift.numel() != cols or lo_row.numel() != cols or dst_lo.stride(0) != dst.stride(0) \
+                or dst_lo.shape[0] < 2 * n_centred:
+            raise ValueError("transpose_centred: shift / lo_row width, lo plane stride or rows")
+    _lib.call("rf_transpose_centred", _ptr(x), x.stride(0), rows, cols, _ptr(shift), _ptr(lo_row), int(n_centred),
+              _ptr(dst), dst.stride(0), _ptr(dst_lo), _ptr(partial), _ptr(partial_sq), _stream(x))
+
+
+def tiles_view(buf, tiles, cols):
+    """A dense [tiles, cols] fp32 view at the start of the flat buffer buf (the layout the transpose writes
+    its per-tile column sums in and rf_colsum_fold reads)."""
+    return buf.view(-1)[:tiles * cols].view(tiles, cols)
 
 
 def _colsum_fold(partial, sums):
@@ -43,20 +76,107 @@ def gram_accumulate(a, b, c):
     return c
 
 
-class RidgeStats:
-    """Sufficient statistics of (x, y_i) pairs over every layer i, accumulated on the GPU."""
+class Centring:
+    """One operand's centring: the reference's shift c [cols] (fp64 of an fp32 mean), the centred channels idx
+    (sorted) with their shift (fp32, 0 elsewhere) and mid rows (int32, -1 elsewhere; the lo row is s rows
+    further), and the number of extra rows the operand carries (0, or LO_ROWS when any channel is centred). Chosen from sums s1 / s2 of n rows: the
+    shift is their mean unless c is given (a resumed state's shift); a channel is centred when its shift's
+    square exceeds the rows' variance, largest ratio first, at most cap of them."""
 
-    def __init__(self, split, layers, dim, device="cuda", out_dim=None):
+    def __init__(self, s1, s2, n, c=None, cap=SHIFT_MAX):
+        mean = s1 / n
+        var = (s2 / n - mean * mean).clamp_min(0)
+        self.c = mean.float().double() if c is None else c.to(s1.device, torch.float64)
+        c2 = self.c * self.c
+        big = (c2 > var).nonzero().flatten()
+        ratio = c2[big] / var[big].clamp_min(1e-300)
+        self.idx = big[ratio.argsort(descending=True, stable=True)[:cap]].sort().values
+        cols = s1.numel()
+        self.shift = torch.zeros(cols, dtype=torch.float32, device=s1.device)
+        self.shift[self.idx] = self.c[self.idx].float()
+        self.lo_row = torch.full((cols,), -1, dtype=torch.int32, device=s1.device)
+        self.lo_row[self.idx] = torch.arange(self.idx.numel(), dtype=torch.int32, device=s1.device)
+        self.s = int(self.idx.numel())
+        self.lo_rows = LO_ROWS if self.s else 0
+        self.delta = self.c - self.shift.double()       # the stored sums' shift -> the reference's shift
+
+    @classmethod
+    def of_rows(cls, x, work, part, part_sq, c=None, cap=SHIFT_MAX):
+        """The centring chosen from rows x [n, cols] (their sums, via a plain transpose into work)."""
+        n, cols = x.shape
+        kp = (n + 63) // 64 * 64
+        s1 = torch.zeros(cols, dtype=torch.float64, device=x.device)
+        s2 = torch.zeros_like(s1)
+        p1, p2 = tiles_view(part, kp // 64, cols), tiles_view(part_sq, kp // 64, cols)
+        transpose_centred(x, work[:cols, :kp], None, None, None, p1, p2)
+        _colsum_fold(p1, s1)
+        _colsum_fold(p2, s2)
+        return cls(s1, s2, n, c, cap)
+
+
+def centred_products(G, ca, A, cb, B):
+    """[ca, cb] fp64 sums of the operands' centred values d_a d_b from an augmented Gram G [ca + 2 A.s, >= cb +
+    2 B.s]: rows (columns) ca .. ca + s - 1 are the mid parts and ca + s .. ca + 2 s - 1 the lo parts of the
+    centred channels A.idx (B.idx); each centred channel's three parts are added in a fixed order."""
+    def fold_cols(Gr):
+        Dc = Gr[:, :cb].clone()
+        if B.s:
+            Dc[:, B.idx] += Gr[:, cb:cb + B.s]
+            Dc[:, B.idx] += Gr[:, cb + B.s:cb + 2 * B.s]
+        return Dc
+    D = fold_cols(G[:ca])
+    if A.s:
+        D[A.idx] += fold_cols(G[ca:ca + A.s])
+        D[A.idx] += fold_cols(G[ca + A.s:ca + 2 * A.s])
+    return D
+
+
+def recentre(D, s1a, s1b, da, db, n):
+    """Sums about shifts moved by da / db: sum (d_a - da)(d_b - db)^T from D = sum d_a d_b^T, s1 = sum d."""
+    return D - torch.outer(da, s1b) - torch.outer(s1a, db) + n * torch.outer(da, db)
+
+
+class RidgeStats:
+    """Sufficient statistics of (x, y_i) pairs over every layer i, accumulated on the GPU. from_state()
+    continues a saved state (the reference's resumable sufficient statistics, code/scripts/fit_sweep.py:20-25,
+    :271-284)."""
+
+    def __init__(self, split, layers, dim, device="cuda", out_dim=None, centre_max=SHIFT_MAX):
+        """centre_max: at most this many channels per operand are centred before the product (0: raw sums
+        re-centred in fp64 afterwards, which loses precision on channels whose mean dwarfs their spread)."""
         self.split, self.layers, self.dim = split, list(layers), dim
+        self.centre_max = centre_max
         self.out_dim = dim if out_dim is None else out_dim
         self.device = torch.device(device)
         f64 = dict(dtype=torch.float64, device=self.device)
         self.n = 0
-        self.cx, self.cy = None, {}
+        self.cen_x, self.cen_y = None, {}
         self.s1x = torch.zeros(dim, **f64)
-        self.sxx = torch.zeros(dim, dim, **f64)
         self.s1y = {i: torch.zeros(self.out_dim, **f64) for i in self.layers}
-        self.sxy = {i: torch.zeros(dim, self.out_dim, **f64) for i in self.layers}
+        self.sxx, self.sxy = None, {}
+        self.base = None
+
+    @classmethod
+    def from_state(cls, state, device="cuda"):
+        """Statistics that continue `state` (a state() dict, e.g. saved and reloaded): new rows are summed about
+        its shifts, and state() returns the saved and the new rows' statistics together."""
+        dev = torch.device(device)
+        L = list(state["layers"])
+        out_dim = next(iter(state["sy"].values())).numel() if L else state["dim"]
+        st = cls(state["split"], L, state["dim"], dev, out_dim)
+        base = {k: state[k] for k in ("split", "layers", "dim", "n")}
+        for k in ("cx", "sx", "sxx"):
+            base[k] = state[k].to(dev, torch.float64)
+        for k in ("cy", "sy", "sxy"):
+            base[k] = {i: state[k][i].to(dev, torch.float64) for i in L}
+        st.base = base
+        return st
+
+    def _alloc(self):
+        f64 = dict(dtype=torch.float64, device=self.device)
+        d, o, cx = self.dim, self.out_dim, self.cen_x
+        self.sxx = torch.zeros(d + 2 * cx.s, d + cx.lo_rows, **f64)
+        self.sxy = {i: torch.zeros(d + 2 * cx.s, o + self.cen_y[i].lo_rows, **f64) for i in self.layers}
 
     @torch.no_grad()
     def add(self, x, ys, block=8192):
@@ -65,51 +185,80 @@ class RidgeStats:
         n, d = x.shape
         if d != self.dim or d % 256 or self.out_dim % 256:
             raise ValueError(f"x width {d} (stats dim {self.dim}); widths must be multiples of 256")
-        if block % 64:
-            raise ValueError("block must be a multiple of 64")
-        if self.cx is None:
-            self.cx = x[:block].float().mean(0)
+        if block <= 0 or block % 64:
+            raise ValueError("block must be a positive multiple of 64")
         for i in self.layers:
-            y = ys[i]
-            _need(y, f"ys[{i}]", torch.bfloat16, 2)
-            if tuple(y.shape) != (n, self.out_dim):
-                raise ValueError(f"ys[{i}] shape {tuple(y.shape)}")
-            if i not in self.cy:
-                self.cy[i] = y[:block].float().mean(0)
+            _need(ys[i], f"ys[{i}]", torch.bfloat16, 2)
+            if tuple(ys[i].shape) != (n, self.out_dim):
+                raise ValueError(f"ys[{i}] shape {tuple(ys[i].shape)}")
+        if n == 0:
+            return
         blk = min(block, (n + 63) // 64 * 64)
-        xt = torch.empty(d, blk, dtype=torch.bfloat16, device=x.device)
-        yt = torch.empty(self.out_dim, blk, dtype=torch.bfloat16, device=x.device)
-        part = torch.empty(blk // 64, max(d, self.out_dim), dtype=torch.float32, device=x.device)
+        dev = x.device
+        w = max(d, self.out_dim)
+        lo = LO_ROWS
+        xt = torch.zeros(d + lo, blk, dtype=torch.bfloat16, device=dev)
+        yt = torch.zeros(self.out_dim + lo, blk, dtype=torch.bfloat16, device=dev)
+        part = torch.empty(blk // 64 * w, dtype=torch.float32, device=dev)
+        if self.cen_x is None:                          # the first block's means are the shifts (ridge.py:37-38)
+            sq = torch.empty_like(part)
+            b = self.base
+            cap = self.centre_max
+            self.cen_x = Centring.of_rows(x[:block], xt, part, sq, None if b is None else b["cx"], cap)
+            for i in self.layers:
+                self.cen_y[i] = Centring.of_rows(ys[i][:block], yt, part, sq, None if b is None else b["cy"][i], cap)
+            self._alloc()
+        cx = self.cen_x
         for r in range(0, n, block):
             rows = min(block, n - r)
             kp = (rows + 63) // 64 * 64
-            xt_b, yt_b = xt[:, :kp], yt[:, :kp]
-            px = part[:kp // 64, :d]
-            _transpose(x[r:r + rows], xt_b, px)
+            xm, xl = xt[:d, :kp], xt[d:, :kp]
+            px = tiles_view(part, kp // 64, d)
+            transpose_centred(x[r:r + rows], xm, xl, cx.shift, cx.lo_row, px, n_centred=cx.s)
             _colsum_fold(px, self.s1x)
-            gram_accumulate(xt_b, xt_b, self.sxx)
+            a = xt[:d + 2 * cx.s, :kp]
+            gram_accumulate(a, xt[:d + cx.lo_rows, :kp], self.sxx)
             for i in self.layers:
-                py = part[:kp // 64, :self.out_dim]
-                _transpose(ys[i][r:r + rows], yt_b, py)
+                cy = self.cen_y[i]
+                o = self.out_dim
+                py = tiles_view(part, kp // 64, o)
+                transpose_centred(ys[i][r:r + rows], yt[:o, :kp], yt[o:, :kp], cy.shift, cy.lo_row, py,
+                                  n_centred=cy.s)
                 _colsum_fold(py, self.s1y[i])
-                gram_accumulate(xt_b, yt_b, self.sxy[i])
+                gram_accumulate(a, yt[:o + cy.lo_rows, :kp], self.sxy[i])
         self.n += n
 
     def state(self, device="cpu"):
         """RidgeStats.state() (code/kva/ridge.py:70-74): shifted sums about cx / cy, fp64."""
+        if self.cen_x is None:
+            if self.base is None:
+                raise ValueError("no rows added")
+            return _to(self.base, device)
         n = float(self.n)
-        cx = self.cx.double()
-        sx = self.s1x - n * cx
-        sxx = self.sxx - torch.outer(cx, self.s1x) - torch.outer(self.s1x, cx) + n * torch.outer(cx, cx)
+        d, o, cx = self.dim, self.out_dim, self.cen_x
+        dx = cx.delta
+        sxx = recentre(centred_products(self.sxx, d, cx, d, cx), self.s1x, self.s1x, dx, dx, n)
         cy, sy, sxy = {}, {}, {}
         for i in self.layers:
-            c = self.cy[i].double()
-            cy[i] = c.to(device)
-            sy[i] = (self.s1y[i] - n * c).to(device)
-            sxy[i] = (self.sxy[i] - torch.outer(cx, self.s1y[i]) - torch.outer(self.s1x, c) + n * torch.outer(cx, c)
-                      ).to(device)
-        return dict(split=self.split, layers=self.layers, dim=self.dim, n=self.n, cx=cx.to(device), cy=cy,
-                    sx=sx.to(device), sxx=sxx.to(device), sy=sy, sxy=sxy)
+            c = self.cen_y[i]
+            cy[i] = c.c
+            sy[i] = self.s1y[i] - n * c.delta
+            sxy[i] = recentre(centred_products(self.sxy[i], d, cx, o, c), self.s1x, self.s1y[i], dx, c.delta, n)
+        mine = dict(split=self.split, layers=self.layers, dim=self.dim, n=self.n, cx=cx.c, cy=cy,
+                    sx=self.s1x - n * dx, sxx=sxx, sy=sy, sxy=sxy)
+        return _to(combine(self.base, mine, 1) if self.base is not None else mine, device)
+
+
+def _to(state, device):
+    out = {}
+    for k, v in state.items():
+        if isinstance(v, torch.Tensor):
+            out[k] = v.to(device)
+        elif isinstance(v, dict):
+            out[k] = {i: t.to(device) if isinstance(t, torch.Tensor) else t for i, t in v.items()}
+        else:
+            out[k] = v
+    return out
 
 
 class RidgeFit:
