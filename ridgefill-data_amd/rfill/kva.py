@@ -274,6 +274,19 @@ def load_gguf(path, device="cuda"):
     return Projector(split, W, B, meta)
 
 
+def adapter_arm(name, projector, tail):
+    """The arm a llama.cpp adapter drives (code/qwen38-27b-kit/identity_projector.py:15-80): a Projector from
+    load_gguf fills the layers it has maps for; the layers the engine runs natively (the linear-attention,
+    i.e. GDN, layers) take h_S itself, the 'identity' fill, and their st corrections. A projector with no
+    native layers gives the plain 'proj' arm."""
+    native = projector.meta.get("native_layers") or []
+    st = projector.meta.get("st") or None
+    if not native:
+        return Arm(name, split=projector.split, tail=tail, fill="proj", projector=projector, st=st)
+    return Arm(name, split=projector.split, tail=tail, fill="by_type", projector=projector, st=st,
+               fill_by_type={"attention": "proj", "gdn": "identity"})
+
+
 def st_from_engine(st):
     """GDN terminal-state corrections in the engines' layout [heads, V, K] (code/c5/convert.py:7-8) to
     the fill's recurrent-state layout [heads, dk, dv] (code/kva/ops.py:4-6, Qwen35.fill's rec += st):
@@ -493,9 +506,10 @@ def finish(model, ids, h_split, lower_cache, arm, keep, oracle=None, keep_cache=
             if got != P:
                 raise ValueError(f"reused fill of layer {i} has {got} rows, P = {P}")
             cache[i] = dict(fill_reuse[i])
-    for i in layers:
+    for i in layers:                                 # a reused fill gets buffers of its own for its tail
         if model.layer_types[i] == "attn":
-            model.reserve(cache[i], n - cache[i].get("n", 0), model.n_kv, model.head_dim, dev)
+            model.reserve(cache[i], n - cache[i].get("n", 0), model.n_kv, model.head_dim, dev,
+                          fresh=fill_reuse is not None and P > 0)
     if P > 0 and fill_reuse is None:
         fill_late(model, h_split, arm, exact_rows=exact_rows, hr=hr, cache=cache, row_inputs=row_inputs, oracle=oracle)
     if P > 0:

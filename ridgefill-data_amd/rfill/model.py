@@ -120,11 +120,12 @@ class FillModel:
         return ops.rope_table(pos.to(self.device, torch.int64), self.inv_freq)
 
     @staticmethod
-    def reserve(c, m, hkv, d, device):
+    def reserve(c, m, hkv, d, device, fresh=False):
         """Make room for m more rows in cache dict c (code/kva/model.py:145-155: grow to n + m +
-        KV_RESERVE, copy the old rows); returns the first slot to write."""
+        KV_RESERVE, copy the old rows); returns the first slot to write. fresh: new buffers even when the
+        old ones have room (c shares its buffers with another cache dict that must not see the new rows)."""
         n = c.get("n", 0)
-        if c.get("kbuf") is None or n + m > c["kbuf"].shape[1]:
+        if c.get("kbuf") is None or n + m > c["kbuf"].shape[1] or fresh:
             cap = n + m + KV_RESERVE
             kb = torch.empty(hkv, cap, d, dtype=torch.bfloat16, device=device)
             vb = torch.empty(hkv, cap, d, dtype=torch.bfloat16, device=device)
