@@ -199,6 +199,23 @@ int rf_gdn_fill(const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int 
  * Host-only; no device work. */
 int rf_gdn_workspace_bytes(int64_t rows, int nk, int nv, int dk, int dv, size_t* bytes);
 
+/* Size in MiB of the device array rf_gdn_fill_noalloc uses as its workspace (one per GPU, for the life of
+ * the process). */
+#define RF_GDN_SCRATCH_MAX 64
+
+/* rf_gdn_fill without a workspace argument and without any allocation: the per-chunk products go to a
+ * file-scope device array of RF_GDN_SCRATCH_MAX MiB inside the library (its address on each GPU is taken
+ * once, on the first call with that GPU current), which holds as many 64-row chunks as fit per pass
+ * (41 at 16 key / 32 value heads), so any P runs, in as many passes as it needs; results are
+ * bit-identical to rf_gdn_fill's. Heads whose one chunk exceeds the array are refused (RF_EINVAL_SHAPE).
+ * No counterpart in the reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc). Every call on one GPU shares its
+ * array, so calls that overlap on one GPU (different streams or threads) race: order them. The stream must
+ * belong to the current device. */
+int rf_gdn_fill_noalloc(const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int dk, int dv,
+                        const uint16_t* conv_w, const uint16_t* conv_in, uint16_t* conv_out, const float* a_log,
+                        const float* dt_bias, float* state, hipStream_t stream);
+
 /* The exact GDN layer's mixing (Qwen35._gdn_core with need_out = True, code/kva/model.py:452-484 and
  * ops.py:199-262): as rf_gdn_fill (state and conv state continued over the P rows), and also the
  * delta-rule outputs out [P, nv dv] bf16 (row stride ldo): per chunk o = Qd S + P v_new, Qd = q_n e^gamma,

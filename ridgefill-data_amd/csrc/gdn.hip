@@ -29,6 +29,7 @@
 // prep also writes Qd, P, T, K and V in plain layouts, the scan stores the state before each chunk, and
 // k_gdn_out (chunk x value head) forms the outputs for all chunks in parallel on fp32 MFMA.
 #include <algorithm>
+#include <mutex>
 
 #include "rf_common.h"
 
@@ -841,6 +842,63 @@ extern "C" int rf_gdn_fill(const uint16_t* pre, int64_t ld, int64_t P, int nk, i
                            const float* dt_bias, float* state, void* workspace, size_t ws_bytes, hipStream_t stream) {
   return gdn_run("rf_gdn_fill", pre, ld, P, nk, nv, dk, dv, conv_w, conv_in, conv_out, a_log, dt_bias, state, nullptr,
                  0, workspace, ws_bytes, stream);
+}
+
+// ---- allocation-free GDN fill: the per-chunk workspace lives in a file-scope device array
+
+namespace {
+
+constexpr size_t GDN_SCRATCH_BYTES = static_cast<size_t>(RF_GDN_SCRATCH_MAX) << 20;
+constexpr int MAX_DEVICES = 64;
+
+// The workspace of rf_gdn_fill_noalloc: one copy per GPU (at its own address), held until the process ends.
+// Its name is a host-side stand-in: host code uses only the per-device addresses taken below.
+static __device__ __align__(256) uint8_t scratch[GDN_SCRATCH_BYTES];
+
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES] = {};
+
+// The current device's address of `scratch`, taken once per device (with that device current) and kept.
+int scratch_address(const char* fn, hipStream_t stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(RF_EHIP, "%s: hipGetDevice: %s", fn, hipGetErrorString(e));
+  if (dev < 0 || dev >= MAX_DEVICES) return fail(RF_EINVAL_ARG, "%s: device %d (at most %d)", fn, dev, MAX_DEVICES);
+  if (stream) {
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) return fail(RF_EHIP, "%s: hipStreamGetDevice: %s", fn, hipGetErrorString(e));
+    if (sdev != dev)
+      return fail(RF_EINVAL_ARG, "%s: the stream belongs to device %d, device %d is current", fn, sdev, dev);
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(RF_EHIP, "%s: hipGetSymbolAddress of the scratch array: %s", fn, hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return RF_OK;
+}
+
+}  // namespace
+
+extern "C" int rf_gdn_fill_noalloc(const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int dk, int dv,
+                                   const uint16_t* conv_w, const uint16_t* conv_in, uint16_t* conv_out,
+                                   const float* a_log, const float* dt_bias, float* state, hipStream_t stream) {
+  const char* fn = "rf_gdn_fill_noalloc";
+  if (const int e = check_heads(fn, nk, nv, dk, dv)) return e;
+  const size_t per_chunk = chunk_bytes(nk, nv);
+  if (per_chunk > GDN_SCRATCH_BYTES)
+    return fail(RF_EINVAL_SHAPE, "%s: %d key / %d value heads need %zu bytes per 64-row chunk, more than the %zu-byte "
+                "scratch array (RF_GDN_SCRATCH_MAX MiB); use rf_gdn_fill with a workspace", fn, nk, nv, per_chunk,
+                GDN_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (const int e = scratch_address(fn, stream, &ws)) return e;
+  return gdn_run(fn, pre, ld, P, nk, nv, dk, dv, conv_w, conv_in, conv_out, a_log, dt_bias, state, nullptr, 0, ws,
+                 GDN_SCRATCH_BYTES, stream);
 }
 
 extern "C" int rf_gdn_forward(const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int dk, int dv,

@@ -396,6 +396,34 @@ def gdn_fill(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state, worksp
     return conv_out
 
 
+def gdn_fill_noalloc(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state, conv_out=None):
+    """gdn_fill through rf_gdn_fill_noalloc: the per-chunk workspace is the library's own device array, so
+    the call allocates nothing beyond conv_out (pass one to allocate nothing at all). Bit-identical to
+    gdn_fill. Calls that overlap on one GPU share that array: order them on one stream."""
+    _need(pre, "pre", torch.bfloat16, 2)
+    _need(conv_w, "conv_w", torch.bfloat16, 2)
+    _need(a_log, "a_log", torch.float32, 1)
+    _need(dt_bias, "dt_bias", torch.float32, 1)
+    _need(state, "state", torch.float32, 3)
+    C = 2 * nk * dk + nv * dv
+    if tuple(conv_w.shape) != (C, 4) or not conv_w.is_contiguous() or tuple(state.shape) != (nv, dk, dv) \
+            or not state.is_contiguous() or pre.shape[1] < C + 2 * nv or a_log.numel() != nv or dt_bias.numel() != nv:
+        raise ValueError(f"gdn_fill_noalloc: pre {tuple(pre.shape)}, conv {tuple(conv_w.shape)}, "
+                         f"state {tuple(state.shape)}")
+    if conv_in is not None:
+        _need(conv_in, "conv_in", torch.bfloat16, 2)
+        if tuple(conv_in.shape) != (3, C) or not conv_in.is_contiguous():
+            raise ValueError("gdn_fill_noalloc: conv state shape")
+    if conv_out is None:
+        conv_out = torch.empty(3, C, dtype=torch.bfloat16, device=pre.device)
+    _need(conv_out, "conv_out", torch.bfloat16, 2)
+    if tuple(conv_out.shape) != (3, C) or not conv_out.is_contiguous():
+        raise ValueError("gdn_fill_noalloc: conv_out shape")
+    _lib.call("rf_gdn_fill_noalloc", _ptr(pre), pre.stride(0), pre.shape[0], nk, nv, dk, dv, _ptr(conv_w),
+              _ptr(conv_in), _ptr(conv_out), _ptr(a_log), _ptr(dt_bias), _ptr(state), _stream(pre))
+    return conv_out
+
+
 # ------------------------------------------------------------------------ exact-row selection
 
 def gdn_forward_workspace_bytes(rows, nk, nv, dk=128, dv=128):
