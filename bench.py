@@ -233,31 +233,93 @@ def kv_write_bench(model, dev, P, layer):
             "bytes_per_launch": byts, "mean_us": round(sec * 1e6, 2)}
 
 
-def cpu_baseline(cfg, w, layer, budget_s=12.0, rows=1024):
-    """The oracle's fill (reference op sequence: F.linear map in bf16, rms_norm, K / V F.linear, RoPE,
-    cache append) on the host, for `rows`-row blocks of one late layer until `budget_s` has passed;
-    scaled to filled tokens/s of the 16-layer fill."""
+def _cpu_info():
+    """(threads this process may use, the machine's CPU count, the CPU model name)."""
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS")
+    if env and env.isdigit() and int(env) > 0:
+        usable = min(usable, int(env))
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return usable, os.cpu_count(), model
+
+
+def cpu_baseline(cfg, w, layer, budget_s=8.0, rows=1024):
+    """The oracle's fill (reference op sequence: F.linear map, rms_norm, K / V F.linear, RoPE, cache append) on
+    the host, for `rows`-row blocks of one late layer until `budget_s` has passed, in bf16 (the reference's
+    model dtype) and in fp32; scaled to filled tokens/s of the 16-layer fill. Threads: every core this
+    process may use (the affinity mask, capped by OMP_NUM_THREADS)."""
     from oracle import model as OM
-    threads = min(os.cpu_count() or 1, 16)
+    threads, machine, model = _cpu_info()
     torch.set_num_threads(threads)
-    b = w["h_split"][:rows].cpu()
-    W, c = w["maps"][layer].cpu(), w["biases"][layer].cpu()
     t = {k: v.cpu() for k, v in w["tensors"].items() if f"layers.{layer}." in k}
-    om = OM.OracleModel(cfg, t, dtype=torch.bfloat16, layers=[layer])
     pos = torch.arange(rows)
-    done, t0 = 0, time.perf_counter()
-    while True:
-        cache = om.new_cache()
-        x = torch.nn.functional.linear(b, W, c)
-        om.fill(layer, x, pos, cache)
-        done += rows
-        el = time.perf_counter() - t0
-        if el >= budget_s:
-            break
-    rate = done / el / (cfg["num_hidden_layers"] - SPLIT)
+    res = {}
+    for dt in (torch.bfloat16, torch.float32):
+        b = w["h_split"][:rows].cpu().to(dt)
+        W, c = w["maps"][layer].cpu().to(dt), w["biases"][layer].cpu().to(dt)
+        om = OM.OracleModel(cfg, t, dtype=dt, layers=[layer])
+        done, t0 = 0, time.perf_counter()
+        while True:
+            cache = om.new_cache()
+            x = torch.nn.functional.linear(b, W, c)
+            om.fill(layer, x, pos, cache)
+            done += rows
+            el = time.perf_counter() - t0
+            if el >= budget_s:
+                break
+        res[str(dt).split(".")[1]] = (done / el / (cfg["num_hidden_layers"] - SPLIT), done, el)
+    rate, done, el = res["bfloat16"]
     return {"value": round(rate, 2), "unit": "filled tokens/s", "cores": threads, "kind": "port",
-            "sample": f"oracle fill of one late layer, {rows}-row blocks x {done // rows} in {el:.1f} s, bf16, "
-                      f"scaled by 1/16 layers; torch {torch.__version__}"}
+            "fp32_value": round(res["float32"][0], 2), "machine_cpus": machine, "cpu_model": model,
+            "sample": f"oracle fill of one late layer (the reference's op sequence), {rows}-row blocks: "
+                      f"bf16 {done // rows} blocks in {el:.1f} s, fp32 {res['float32'][1] // rows} blocks in "
+                      f"{res['float32'][2]:.1f} s; scaled by 1/16 layers; torch {torch.__version__}"}
+
+
+def cpu_fit_baseline(d=4096, targets=16, block=8192, lams=(1e-4, 1e-3, 1e-2)):
+    """The reference's fit on the host (code/kva/ridge.py:44-62, 80-105), bounded: one 8192-row block of
+    centred fp32 GEMMs into fp64 (X^T X and the 16 X^T Y_l) scaled to the 256 blocks of 2,097,152 rows; the
+    fp64 eigendecomposition timed in full, the solve of one target for 3 lambdas timed and scaled by 16."""
+    from rfill import synth
+    threads, _, _ = _cpu_info()
+    torch.set_num_threads(threads)
+    maps = synth.fit_maps(d, 1, device="cpu")
+    x, ys = synth.fit_chunk(0, block, d, maps, device="cpu")
+    xc = x.float() - x.float().mean(0)
+    yc = ys[0].float() - ys[0].float().mean(0)
+    sxx = torch.zeros(d, d, dtype=torch.float64)
+    sxy = torch.zeros(d, d, dtype=torch.float64)
+    t0 = time.perf_counter()
+    sxx += (xc.T @ xc).double()
+    sxy += (xc.T @ yc).double()
+    t_two = time.perf_counter() - t0
+    t_block = t_two / 2 * (1 + targets)
+    n_blocks = 2097152 // block
+    c = sxx + torch.eye(d, dtype=torch.float64) * float(sxx.diagonal().mean())
+    t0 = time.perf_counter()
+    e, v = torch.linalg.eigh(c)
+    t_eigh = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    a = v.T @ sxy
+    for lam in lams:
+        v @ (a / (e + lam * float(e.mean()))[:, None])
+    t_target = time.perf_counter() - t0
+    total = t_block * n_blocks + t_eigh + t_target * targets
+    return {"value": round(total, 1), "unit": "s per fit", "cores": threads, "kind": "port",
+            "accumulate_s": round(t_block * n_blocks, 1), "solve_s": round(t_eigh + t_target * targets, 1),
+            "sample": f"one {block}-row block of 2 of the 17 fp32 GEMMs ({t_two:.2f} s) scaled to 17 GEMMs x "
+                      f"{n_blocks} blocks; fp64 eigh of [{d}, {d}] ({t_eigh:.2f} s) + one target's solve for 3 "
+                      f"lambdas ({t_target:.2f} s) x {targets}"}
 
 
 def fit_bench(dev, chunks=3, rows=65536, d=4096, targets=16, lams=(1e-4, 1e-3, 1e-2)):
@@ -460,40 +522,48 @@ def hybrid_finish_bench(dev, reps=2, split=24, n_rows=32768, tail=4096):
             "ms_tail": round(tt * 1e3, 2)}
 
 
-def exact_rows_bench(dev, reps=3, split=18, n_rows=32768, tail=4096, frac=0.01):
-    """The Qwen3-8B-shaped fill (hidden 4096, 32 / 8 heads, k_norm, layers 18..35, 32K prompt, P = 28672)
-    with 1% of the filled rows exact (287 rows at seeded positions) run as finish() runs them: every late
-    layer's cache is filled with the rows' inputs scattered in, and each exact row goes through the layer
-    (layer_rows: query projection, attention over the filled keys, o_proj, SwiGLU MLP), its output being
-    its input to the next layer. Reported beside the same fill without exact rows."""
+def sweep_bench(dev, reps=2, split=18, tail=4096, frac=0.01, lengths=(16384, 32768, 65536, 122880)):
+    """The Qwen3-8B-shaped fill (hidden 4096, 32 / 8 heads, q_norm / k_norm, RoPE theta 1e6, layers 18..35,
+    maps I + 0.02 N(0, 1/H)) over the prompt-length sweep 16K / 32K / 64K / 120K rows with a 4096-row exact
+    tail, P = N - 4096 filled rows, with 1 % of them exact (round(0.01 P) seeded positions) run as finish()
+    runs them -- every late layer's cache filled with the rows' inputs scattered in, each exact row through
+    the layer (query projection, attention over the filled keys, o_proj, SwiGLU MLP) -- and the same fill
+    without exact rows. One model for every length; the split-layer rows are the first N of one draw."""
     from rfill import synth
     from rfill.kva import Arm, Projector, fill_late
     from rfill.model import FillModel
     cfg = synth.QWEN3_8B
-    w = synth.dense_fill(cfg, split, n_rows, tail, device=dev, exact_frac=frac, full=True)
+    n_max = max(lengths)
+    w = synth.dense_fill(cfg, split, n_max, tail, device=dev, full=True)
     model = FillModel(cfg, w["tensors"], dev, layers=w["layers"])
+    del w["tensors"]
     arm = Arm("ridgefill", split=split, tail=tail, fill="proj", projector=Projector(split, w["maps"], w["biases"]))
-    P, rows = w["P"], w["rows"]
-
-    def run(exact):
-        caches = model.new_cache()
-        fill_late(model, w["h_split"], arm, exact_rows=rows if exact else None, cache=caches)
-        return caches
-
-    out = {}
-    for name, exact in (("plain", False), ("exact", True)):
-        run(exact)
-        torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        for _ in range(reps):
-            run(exact)
-        torch.cuda.synchronize()
-        out[name] = (time.perf_counter() - t0) / reps
-    return {"workload": f"qwen3-8b-shaped 32K fill: layers {split}..{cfg['num_hidden_layers'] - 1}, {P} filled rows, "
-                        f"{len(rows)} exact rows (1%) through their full layers",
-            "filled_tokens_per_s": round(P / out["exact"], 1), "ms_per_fill": round(out["exact"] * 1e3, 3),
-            "ms_per_fill_without_exact_rows": round(out["plain"] * 1e3, 3),
-            "exact_rows_ms": round((out["exact"] - out["plain"]) * 1e3, 3), "exact_rows": len(rows)}
+    L = len(w["layers"])
+    out = {"workload": f"qwen3-8b-shaped fill: layers {split}..{cfg['num_hidden_layers'] - 1} ({L} late layers), "
+                       f"exact tail {tail}, 1% of the filled rows exact", "lengths": {}}
+    for n in lengths:
+        P = n - tail
+        rows = torch.randperm(P, generator=torch.Generator().manual_seed(13))[:int(round(frac * P))].sort().values
+        h = w["h_split"][:n]
+        res = {}
+        for name, exact in (("plain", None), ("exact", rows.to(dev))):
+            fill_late(model, h, arm, exact_rows=exact)          # warm-up (the caching allocator keeps the buffers)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                fill_late(model, h, arm, exact_rows=exact)      # a new cache per fill, as finish() starts one
+            torch.cuda.synchronize()
+            res[name] = (time.perf_counter() - t0) / reps
+        flop = 2.0 * P * L * (4096 * 4096 + 4096 * 2 * 8 * 128)
+        out["lengths"][n] = {"filled_rows": P, "exact_rows": len(rows),
+                             "filled_tokens_per_s": round(P / res["exact"], 1), "ms_per_fill": round(res["exact"] * 1e3, 2),
+                             "ms_per_fill_without_exact_rows": round(res["plain"] * 1e3, 2),
+                             "filled_tokens_per_s_without_exact_rows": round(P / res["plain"], 1),
+                             "fill_mfma_frac_without_exact_rows": round(flop / res["plain"] / PEAK_BF16, 4),
+                             "exact_rows_ms": round((res["exact"] - res["plain"]) * 1e3, 2)}
+        log(f"sweep N={n}: {out['lengths'][n]}")
+        torch.cuda.empty_cache()
+    return out
 
 
 def finish_bench(dev, reps=3, keep=TAIL):
@@ -568,7 +638,7 @@ def main():
     ap.add_argument("--no-extras", action="store_true", help="skip ceilings and the standalone KV-write leg")
     ap.add_argument("--no-fit", action="store_true", help="skip the closed-form fit leg")
     ap.add_argument("--no-hybrid", action="store_true", help="skip the Gated-DeltaNet hybrid fill leg")
-    ap.add_argument("--no-exact", action="store_true", help="skip the Qwen3-8B exact-rows fill leg")
+    ap.add_argument("--no-exact", action="store_true", help="skip the Qwen3-8B prompt-length sweep with exact rows")
     ap.add_argument("--no-finish", action="store_true", help="skip the whole-finish() leg (fill + exact tail)")
     ap.add_argument("--overlap", action="store_true",
                     help="run each layer's K / V write on a second stream beside the next layer's map apply")
@@ -639,8 +709,8 @@ def main():
         out["finish"] = finish_bench(dev)
         torch.cuda.empty_cache()
     if not args.no_exact:
-        log("Qwen3-8B fill with 1% exact rows")
-        out["exact_rows"] = exact_rows_bench(dev)
+        log("Qwen3-8B prompt-length sweep with 1% exact rows")
+        out["qwen3_sweep"] = sweep_bench(dev)
         torch.cuda.empty_cache()
     if not args.no_hybrid:
         log("Gated-DeltaNet hybrid fill leg")
@@ -659,6 +729,9 @@ def main():
     if not args.no_cpu:
         log("CPU baseline (oracle fill on the host cores)")
         out["cpu_baseline"] = cpu_baseline(cfg, w, SPLIT)
+        if not args.no_fit:
+            log("CPU baseline of the fit (bounded sample)")
+            out["cpu_fit_baseline"] = cpu_fit_baseline()
     print(json.dumps(out), flush=True)
 
 

@@ -3,7 +3,10 @@
 output gate and the gated output norm against the oracle's bf16 formulas; the gated attention layer
 (head_dim 256, partial RoPE) and the GDN layer through FillModel.layer / layer_rows against the oracle;
 a hybrid model's exact forward and the capture sums over it. Bars: 1e-2 relative Frobenius for the bf16
-paths (2e-2 for a layer output's update, as the other layer tests), 1e-5 for the capture sums."""
+paths; 2e-2 for a layer output's update (output - input: both sides round the output to bf16, 2^-9 of |out|,
+and the update is a fraction of |out|, so that rounding alone is several 1e-3 of the update) and for the
+inputs of layers past the first of the hybrid's exact forward (each carries the earlier layers' differences);
+1e-5 for the capture sums."""
 import pytest
 import torch
 import torch.nn.functional as F
@@ -218,4 +221,4 @@ def test_hybrid_finish_matches_oracle(dev, exact):
     ek = max(rel_err(cache[7][part], oc[7][part]) for part in ("k", "v"))
     agree = float((logits.argmax(-1).cpu() == want.argmax(-1)).float().mean())
     print(f"hybrid finish (exact rows: {exact}): logits {el:.2e}, GDN states {es:.2e}, K/V {ek:.2e}, argmax {agree:.3f}")
-    assert el < 2 * TOL and es < TOL and ek < TOL and agree > 0.9
+    assert el < TOL and es < TOL and ek < TOL and agree > 0.9
