@@ -95,7 +95,8 @@ __device__ __forceinline__ void issue_load(__amdgpu_buffer_rsrc_t rs, uint32_t v
 }
 
 // acc[nt][mt] += W[n0 + wn*128 + nt*32 .. +32, :] . X[m0 + wm*128 + mt*32 .. +32, :]^T over all of K
-// (K % 64 == 0). Rows of X at or past M read as zeros. Ends with a barrier: LDS is free for the epilogue.
+// (K % 64 == 0), from zero (ZERO) or from the accumulators' values on entry. Rows of X at or past M read
+// as zeros. Ends with a barrier: LDS is free for the epilogue.
 //
 // Pipeline. K goes in 64-deep steps. A step's operands are four 16 KiB quarters (activation rows 0-127 and
 // 128-255, weight rows 0-127 and 128-255), each 128 rows of full 128-byte lines; the ring holds ten
@@ -107,6 +108,7 @@ __device__ __forceinline__ void issue_load(__amdgpu_buffer_rsrc_t rs, uint32_t v
 // slots step kt - 1's weights left), its weight quarters during slice 3 (into the slots step kt's
 // activations just left). So each barrier waits with 8 loads per wave still in flight, and the last
 // loads of a step are issued four slices (64 MFMAs) before the barrier that needs them.
+template <bool ZERO = true>
 __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t ldx,
                                          const uint16_t* __restrict__ W, int64_t ldw, int M, int K,
                                          int m0, int n0, uint4* lds, f32x16 (&acc)[4][4]) {
@@ -129,12 +131,14 @@ __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t
       vw[h][i] = static_cast<uint32_t>(((h * 128 + r) * ldw + ch * 8) * 2);
     }
 
+  if (ZERO) {
 #pragma unroll
-  for (int a = 0; a < 4; ++a)
+    for (int a = 0; a < 4; ++a)
 #pragma unroll
-    for (int b = 0; b < 4; ++b)
+      for (int b = 0; b < 4; ++b)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+        for (int r = 0; r < 16; ++r) acc[a][b][r] = 0.f;
+  }
 
   char* base = reinterpret_cast<char*>(lds);
   const int nk = K / BK;
@@ -316,32 +320,33 @@ __global__ __launch_bounds__(NTHR) void k_map_apply(const uint16_t* __restrict__
                                                     uint16_t* __restrict__ X, int64_t ldx,
                                                     float* __restrict__ ssq, int M, int N, int K) {
   __shared__ uint4 lds[LDS_U4];
-  uint4* aux = lds + IMAGE_U4;                                  // the bias tile, then:
-  float* halves = reinterpret_cast<float*>(aux + 32);          // [2][256] row sum-of-squares halves
+  float* halves = reinterpret_cast<float*>(lds + IMAGE_U4);    // [2][256] row sum-of-squares halves
   const int tiles_n = N / BN;
   int tm, tn;
   tile_coords(xcd_tile(blockIdx.x, gridDim.x), (M + BM - 1) / BM, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   const int t = threadIdx.x;
-  uint4 bias_chunk = make_uint4(0u, 0u, 0u, 0u);
-  if (t < 32 && bias) bias_chunk = *reinterpret_cast<const uint4*>(bias + n0 + t * 8);
-  f32x16 acc[4][4];
-  mainloop(B, ldb, W, K, M, K, m0, n0, lds, acc);
-  if (t < 32) aux[t] = bias_chunk;
-  __syncthreads();
-
   const int lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1, lr = lane & 31, lk = lane >> 5;
-  const uint16_t* bt = reinterpret_cast<const uint16_t*>(aux);
-  uint2 bq[4][4];
+  // the accumulators start at the bias: lane (lr, lk) holds columns wn*128 + nt*32 + 8g + 4lk + e
+  f32x16 acc[4][4];
 #pragma unroll
   for (int nt = 0; nt < 4; ++nt)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) bq[nt][g] = *reinterpret_cast<const uint2*>(bt + wn * 128 + nt * 32 + 8 * g + 4 * lk);
+    for (int g = 0; g < 4; ++g) {
+      const uint2 bq = bias ? *reinterpret_cast<const uint2*>(bias + n0 + wn * 128 + nt * 32 + 8 * g + 4 * lk)
+                            : make_uint2(0u, 0u);
+      const float b0 = bf_lo(bq.x), b1 = bf_hi(bq.x), b2 = bf_lo(bq.y), b3 = bf_hi(bq.y);
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt) {
+        acc[nt][mt][4 * g + 0] = b0;
+        acc[nt][mt][4 * g + 1] = b1;
+        acc[nt][mt][4 * g + 2] = b2;
+        acc[nt][mt][4 * g + 3] = b3;
+      }
+    }
+  mainloop<false>(B, ldb, W, K, M, K, m0, n0, lds, acc);
   float ss[4];
-  stage_tile<true>(lds, acc, [&](int, int nt, int g, int e, float a) {
-    const uint32_t u = (e < 2) ? bq[nt][g].x : bq[nt][g].y;
-    return a + bf2f(static_cast<uint16_t>((e & 1) ? (u >> 16) : (u & 0xffffu)));
-  }, ss);
+  stage_tile<true>(lds, acc, [&](int, int, int, int, float a) { return a; }, ss);
 #pragma unroll
   for (int mt = 0; mt < 4; ++mt) {
     const float tot = ss[mt] + __shfl_xor(ss[mt], 32, 64);     // the row's 128 columns of this wave
