@@ -290,6 +290,25 @@ int rf_read_cosine(const uint16_t* pred, int64_t ld_pred, const uint16_t* truth,
                    int hkv, int d, const uint16_t* kgain, int gain_kind, double weight, double* out,
                    void* workspace, size_t ws_bytes, hipStream_t stream);
 
+/* The ridge solve of RidgeFit (code/kva/ridge.py:80-105) in fp64: for each of the nlam values lam (host array
+ * lams, each > 0), W_lam = (C + lam scale I)^-1 Cxy with C = cxx [d, d] (row stride ldc; symmetric positive
+ * semi-definite, the centred scatter) and Cxy = cxy [d, R] (row stride ldb; the cross statistics of every
+ * target side by side), written to w + l w_stride as [d, R] (row stride ldw); and, if bias is not NULL,
+ * bias + l bias_stride = mean_y - mean_x W_lam ([R]; mean_x [d], mean_y [R] on the device): the unpenalised
+ * bias of the centred fit. The inverse of C + lam scale I comes from a block recursion on its Schur
+ * complements over a 64 x 64 Gauss-Jordan base (the matrix padded with an identity block to a multiple of 64)
+ * and every product runs on fp64 MFMA; the reference's eigendecomposition gives the same closed form.
+ * Needs d, R, ldb, ldw even; cxy, w, mean_x and the workspace 16-byte aligned; a workspace of
+ * rf_ridge_solve_workspace_bytes(d, nlam) bytes. */
+int rf_ridge_solve(const double* cxx, int64_t ldc, int64_t d, const double* cxy, int64_t ldb, int64_t R,
+                   const double* mean_x, const double* mean_y, const double* lams, int nlam, double scale, double* w,
+                   int64_t ldw, int64_t w_stride, double* bias, int64_t bias_stride, void* workspace, size_t ws_bytes,
+                   hipStream_t stream);
+
+/* Bytes of rf_ridge_solve's workspace for dimension d and nlam lambdas (up to 8 are inverted together).
+ * Host only. */
+int rf_ridge_solve_workspace_bytes(int64_t d, int nlam, size_t* bytes);
+
 /* ---- exact-row selection (the qattn selector) ---- */
 
 /* Bytes of rf_window_mass's workspace: w window rows, hq query / hkv K-V heads of head_dim d, keys

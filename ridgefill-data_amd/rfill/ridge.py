@@ -261,20 +261,30 @@ def _to(state, device):
     return out
 
 
+def ridge_solve_workspace_bytes(d, nlam=1):
+    import ctypes
+    n = ctypes.c_size_t(0)
+    _lib.call("rf_ridge_solve_workspace_bytes", d, nlam, ctypes.byref(n))
+    return n.value
+
+
 class RidgeFit:
-    """fp64 ridge solve on the GPU for every lambda (code/kva/ridge.py:77-105)."""
+    """fp64 ridge solve on the GPU for every lambda (code/kva/ridge.py:77-105): rf_ridge_solve inverts
+    C + lam mean(diag C) I (block recursion on Schur complements, fp64 MFMA products) and multiplies the
+    cross statistics of every target at once; the bias is unpenalised (mean_y - mean_x W)."""
 
     def __init__(self, state, device="cuda"):
         dev = torch.device(device)
+        if dev.type != "cuda":
+            raise ValueError("RidgeFit solves on the GPU (rf_ridge_solve); device must be a GPU")
         self.state, self.device = state, dev
         n = state["n"]
         self.n = n
         sx = state["sx"].to(dev, torch.float64)
         self.sx = sx
         self.mean_x = state["cx"].to(dev, torch.float64) + sx / n
-        self.cxx = state["sxx"].to(dev, torch.float64) - torch.outer(sx, sx) / n
+        self.cxx = (state["sxx"].to(dev, torch.float64) - torch.outer(sx, sx) / n).contiguous()
         self.scale = self.cxx.diagonal().mean().item()
-        self._chol = {}                                   # lam -> Cholesky factor, shared by every layer
 
     def cross(self, i):
         st = self.state
@@ -282,11 +292,25 @@ class RidgeFit:
         cxy = st["sxy"][i].to(self.device, torch.float64) - torch.outer(self.sx, sy) / self.n
         return cxy, st["cy"][i].to(self.device, torch.float64) + sy / self.n
 
-    def solve(self, cxy, lam):
-        if lam not in self._chol:
-            a = self.cxx + (lam * self.scale) * torch.eye(self.cxx.shape[0], dtype=torch.float64, device=self.device)
-            self._chol[lam] = torch.linalg.cholesky(a)
-        return torch.cholesky_solve(cxy, self._chol[lam])
+    def solve(self, cxy, lams, mean_y=None):
+        """(W [nlam, d, R], bias [nlam, R] or None) fp64: (C + lam s I)^-1 cxy for each lam, and mean_y - mean_x W."""
+        lams = [float(v) for v in lams]
+        cxy = cxy.to(self.device, torch.float64).contiguous()
+        d, R = cxy.shape
+        if d % 2 or R % 2:
+            raise ValueError(f"ridge solve: d {d} and R {R} must be even")
+        f64 = dict(dtype=torch.float64, device=self.device)
+        w = torch.empty(len(lams), d, R, **f64)
+        bias = None if mean_y is None else torch.empty(len(lams), R, **f64)
+        ws = torch.empty(ridge_solve_workspace_bytes(d, len(lams)), dtype=torch.uint8, device=self.device)
+        import ctypes
+        arr = (ctypes.c_double * len(lams))(*lams)
+        mx = self.mean_x.contiguous()
+        my = None if mean_y is None else mean_y.to(self.device, torch.float64).contiguous()
+        _lib.call("rf_ridge_solve", _ptr(self.cxx), self.cxx.stride(0), d, _ptr(cxy), cxy.stride(0), R,
+                  _ptr(mx) if my is not None else None, _ptr(my), arr, len(lams), float(self.scale), _ptr(w), R, d * R,
+                  _ptr(bias), R, _ptr(ws), ws.numel(), _stream(cxy))
+        return w, bias
 
     def layer(self, i, lams):
         """{lam: (weight [d_out, d_in] fp32, bias [d_out] fp32)} for layer i (F.linear layout)."""
@@ -294,18 +318,19 @@ class RidgeFit:
 
     def layers(self, ids, lams):
         """{i: {lam: (weight, bias)}} for every layer i in ids: the targets' cross statistics side by side,
-        so each lambda costs one factorisation and one pair of triangular solves for all of them."""
-        ids = list(ids)
+        one rf_ridge_solve for every lambda and target."""
+        ids, lams = list(ids), list(lams)
         cross = [self.cross(i) for i in ids]
         cxy = torch.cat([c for c, _ in cross], 1)
+        mean_y = torch.cat([m for _, m in cross])
+        w_all, b_all = self.solve(cxy, lams, mean_y)
         out = {i: {} for i in ids}
-        for lam in lams:
-            w_all = self.solve(cxy, lam)
+        for li, lam in enumerate(lams):
             col = 0
-            for i, (c, mean_y) in zip(ids, cross):
-                w = w_all[:, col:col + c.shape[1]]
-                col += c.shape[1]
-                out[i][lam] = (w.T.float().contiguous(), (mean_y - self.mean_x @ w).float())
+            for i, (c, _) in zip(ids, cross):
+                k = c.shape[1]
+                out[i][lam] = (w_all[li, :, col:col + k].T.float().contiguous(), b_all[li, col:col + k].float())
+                col += k
         return out
 
 
