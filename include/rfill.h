@@ -270,12 +270,14 @@ int rf_transpose_centred(const uint16_t* src, int64_t ld_src, int64_t rows, int6
  * fold; the same bits every run): the sum(0) of a sample block (RidgeStats' sx / sy, code/kva/ridge.py:46, :61). */
 int rf_colsum_fold(const float* partial, int64_t ntiles, int64_t cols, double* sums, hipStream_t stream);
 
-/* Gram / cross accumulation C[M, N] += A[M, K] B[N, K]^T: bf16 products summed in fp32 on MFMA over
- * this call's K, then added into the fp64 accumulator C (row stride ldc). With A = X^T and B = X^T or
- * Y^T of one sample block this is RidgeStats' per-block fp32 GEMM into fp64 (code/kva/ridge.py:47,
- * :62). Needs N % 256 == 0, K % 64 == 0 (pad samples with zero rows), lda / ldb % 8 == 0, ldc even. */
+/* Gram / cross accumulation C[M, N] += A[M, K] B[N, K]^T: bf16 products summed in fp32 on MFMA over runs
+ * of at most fold_rows of K (0: the whole K; else a multiple of 64), each run's sums added into the fp64
+ * accumulator C (row stride ldc) as it ends. With A = X^T and B = X^T or Y^T of sample rows and fold_rows
+ * the block, this is RidgeStats' per-block fp32 GEMM into fp64 (code/kva/ridge.py:47, :62) over many
+ * blocks in one launch (runs start at K offsets 0, fold_rows, 2 fold_rows, ...). Needs N % 256 == 0,
+ * K % 64 == 0 (pad samples with zero rows), lda / ldb % 8 == 0, ldc even. */
 int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t M, int64_t N,
-                       int64_t K, double* c, int64_t ldc, hipStream_t stream);
+                       int64_t K, int64_t fold_rows, double* c, int64_t ldc, hipStream_t stream);
 
 /* Held-out read cosine of one late layer for one document (code/scripts/fit_sweep.py:307-313): pred and
  * truth are [rows, 2 hkv d] bf16 reads, K heads in columns 0 .. hkv d - 1 and V heads after them (the

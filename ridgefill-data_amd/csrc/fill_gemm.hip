@@ -770,39 +770,79 @@ __global__ __launch_bounds__(256) void k_norm_kv_reduce(const float* __restrict_
   kv_chunk_row(a, L, [&](int c) { return image_chunk(img, r, c); }, ch, m, m < M, rope_fetch(a, L, m, m < M));
 }
 
-// C[m, n] += sum_k A[m, k] B[n, k] in fp32 for this launch, added into the fp64 accumulator C. Each
-// tile owns its 256 x 256 block of C, so the read-modify-write is race-free and the result does not
-// depend on the schedule. A lane's accumulator holds 4 consecutive columns of one row per (nt, g).
+// Adds a run's fp32 sums (acc) into the fp64 accumulator C for the tile at (m0, n0), rows < M. The sums go
+// through LDS, half the tile (128 rows) at a time, as a row-major fp32 image (row r's 16-byte chunk c at
+// r * 64 + (c ^ (r & 15)): the accumulator writes and the row reads both hit 16 distinct bank groups per
+// 16 lanes), so that each wave instruction of the read-modify-write of C covers 2 KB of one row of C instead
+// of 16 bytes in each of 32 rows. Needs the LDS free on entry; leaves it free.
+__device__ __forceinline__ void fold_tile(const f32x16 (&acc)[4][4], uint4* lds, double* __restrict__ C,
+                                          int64_t ldc, int M, int m0, int n0) {
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = w >> 1, wn = w & 1, lr = lane & 31, lk = lane >> 5;
+  float4* img = reinterpret_cast<float4*>(lds);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (wm == h) {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int r = mt * 32 + lr, c = wn * 32 + nt * 8 + 2 * g + lk;
+            img[r * 64 + (c ^ (r & 15))] = make_float4(acc[nt][mt][4 * g], acc[nt][mt][4 * g + 1],
+                                                       acc[nt][mt][4 * g + 2], acc[nt][mt][4 * g + 3]);
+          }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {                 // wave w: image rows 32w .. 32w + 31, 8 per batch
+      double2 v[8][2];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int gm = m0 + h * 128 + w * 32 + b * 8 + i;
+        if (gm < M) {
+          const double* p = C + static_cast<int64_t>(gm) * ldc + n0 + 4 * lane;
+          v[i][0] = *reinterpret_cast<const double2*>(p);
+          v[i][1] = *reinterpret_cast<const double2*>(p + 2);
+        }
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        const int j = w * 32 + b * 8 + i, gm = m0 + h * 128 + j;
+        if (gm < M) {
+          const float4 a = img[j * 64 + (lane ^ (j & 15))];
+          v[i][0].x += a.x;
+          v[i][0].y += a.y;
+          v[i][1].x += a.z;
+          v[i][1].y += a.w;
+          double* p = C + static_cast<int64_t>(gm) * ldc + n0 + 4 * lane;
+          *reinterpret_cast<double2*>(p) = v[i][0];
+          *reinterpret_cast<double2*>(p + 2) = v[i][1];
+        }
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// C[m, n] += sum_k A[m, k] B[n, k]: bf16 products summed in fp32 over runs of at most `fold` of K, each run's
+// sums added into the fp64 accumulator C as it ends (fold_tile). Each tile owns its 256 x 256 block of C, so
+// the read-modify-write is race-free and the result does not depend on the schedule.
 __global__ __launch_bounds__(NTHR) void k_gram(const uint16_t* __restrict__ A, int64_t lda,
                                                const uint16_t* __restrict__ B, int64_t ldb, int M, int N, int K,
-                                               double* __restrict__ C, int64_t ldc) {
+                                               int fold, double* __restrict__ C, int64_t ldc) {
   __shared__ uint4 lds[LDS_U4];
   const int tiles_n = N / BN;
   int tm, tn;
   tile_coords(xcd_tile(blockIdx.x, gridDim.x), (M + BM - 1) / BM, tiles_n, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   f32x16 acc[4][4];
-  mainloop(A, lda, B, ldb, M, K, m0, n0, lds, acc);
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int wm = w >> 1, wn = w & 1, lr = lane & 31, lk = lane >> 5;
-#pragma unroll
-  for (int mt = 0; mt < 4; ++mt) {
-    const int gm = m0 + wm * 128 + mt * 32 + lr;
-    if (gm >= M) continue;
-    double* row = C + static_cast<int64_t>(gm) * ldc + n0 + wn * 128 + 4 * lk;
-#pragma unroll
-    for (int nt = 0; nt < 4; ++nt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        double* p = row + nt * 32 + 8 * g;
-        double2 lo = *reinterpret_cast<double2*>(p), hi = *reinterpret_cast<double2*>(p + 2);
-        lo.x += acc[nt][mt][4 * g + 0];
-        lo.y += acc[nt][mt][4 * g + 1];
-        hi.x += acc[nt][mt][4 * g + 2];
-        hi.y += acc[nt][mt][4 * g + 3];
-        *reinterpret_cast<double2*>(p) = lo;
-        *reinterpret_cast<double2*>(p + 2) = hi;
-      }
+  for (int k0 = 0; k0 < K; k0 += fold) {
+    const int k1 = min(k0 + fold, K);
+    mainloop(A + k0, lda, B + k0, ldb, M, k1 - k0, m0, n0, lds, acc);
+    fold_tile(acc, lds, C, ldc, M, m0, n0);
   }
 }
 
@@ -999,7 +1039,8 @@ extern "C" int rf_norm_q(const uint16_t* x, int64_t ldx, const float* ssq, int64
 }
 
 extern "C" int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t M,
-                                  int64_t N, int64_t K, double* c, int64_t ldc, hipStream_t stream) {
+                                  int64_t N, int64_t K, int64_t fold_rows, double* c, int64_t ldc,
+                                  hipStream_t stream) {
   if (!a || !b || !c) return fail(RF_EINVAL_ARG, "rf_gram_accumulate: null pointer");
   if (M < 0 || M > (1 << 30) || N <= 0 || N % BN || K <= 0 || K % 64)
     return fail(RF_EINVAL_SHAPE, "rf_gram_accumulate: M %lld, N %lld (multiple of 256), K %lld (multiple of 64)",
@@ -1009,9 +1050,12 @@ extern "C" int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t
                 (long long)ldb, (long long)ldc);
   if (!aligned16(a) || !aligned16(b) || !aligned16(c))
     return fail(RF_EINVAL_SHAPE, "rf_gram_accumulate: pointers must be 16-byte aligned");
+  if (fold_rows < 0 || fold_rows % 64)
+    return fail(RF_EINVAL_ARG, "rf_gram_accumulate: fold_rows %lld (0 or a multiple of 64)", (long long)fold_rows);
   if (M == 0) return RF_OK;
+  const int64_t fold = (fold_rows == 0 || fold_rows > K) ? K : fold_rows;
   hipLaunchKernelGGL(k_gram, dim3(grid_of(M, N)), dim3(NTHR), 0, stream, a, lda, b, ldb, static_cast<int>(M),
-                     static_cast<int>(N), static_cast<int>(K), c, ldc);
+                     static_cast<int>(N), static_cast<int>(K), static_cast<int>(fold), c, ldc);
   return check_launch("rf_gram_accumulate");
 }
 

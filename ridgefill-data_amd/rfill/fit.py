@@ -108,7 +108,7 @@ class Capture:
         for S in self.splits:
             r = (S - self.S0) * R
             m = H + 2 * self.cen[S - self.S0].s
-            ridge.gram_accumulate(self.T[r:r + m, :K], self.T[r:, :K], self.acc[S][:m])
+            ridge.gram_accumulate(self.T[r:r + m, :K], self.T[r:, :K], self.acc[S][:m], self.block)
         self.off = 0
 
     def state(self, S, device="cpu"):

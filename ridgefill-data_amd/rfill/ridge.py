@@ -1,10 +1,11 @@
 """Closed-form ridge maps on the GPU: RidgeStats / RidgeFit of code/kva/ridge.py with the sufficient
 statistics accumulated by librfill's MFMA Gram kernel.
 
-Per sample block (default 8192 rows, the reference's block): the block is transposed into the
-K-contiguous operands X^T, Y_i^T (rf_transpose_centred, which also yields the column sums), then
-rf_gram_accumulate adds X^T X and X^T Y_i -- bf16 products summed in fp32 over the block, as the
-reference's per-block fp32 GEMM (code/kva/ridge.py:47, :62) -- into fp64 accumulators.
+begin(x) / add_layer(i, y) (code/kva/ridge.py:34-62): up to PIECE rows at a time are transposed into the
+K-contiguous operands X^T, Y_i^T (rf_transpose_centred, which also yields the column sums), then one
+rf_gram_accumulate launch per operand pair adds X^T X or X^T Y_i: bf16 products summed in fp32 over runs of
+at most `block` rows (default 8192, the reference's block), each run added into fp64 -- as the reference's
+per-block fp32 GEMM (code/kva/ridge.py:47, :62) is. X^T is built once per piece and serves every layer.
 
 Centring. The reference subtracts its shifts (the first block's means, code/kva/ridge.py:37-38, :56-57)
 before each block's fp32 GEMM, which keeps the fp32 sums at the size of the centred values. Here the
@@ -17,8 +18,10 @@ fp64 and moves every sum onto the reference's shifts by exact fp64 algebra, so t
 reference's layout and meaning.
 
 RidgeFit solves W(lam) = (C + lam mean(diag C) I)^-1 Cxy with the bias unpenalised
-(code/kva/ridge.py:80-105) in fp64 on the GPU by a Cholesky factorisation per lam (the same solution the
-reference's eigendecomposition gives, since C + lam s I is symmetric positive definite for lam > 0).
+(code/kva/ridge.py:80-105) in fp64 on the GPU with rf_ridge_solve: the inverse of C + lam s I by a block
+recursion on its Schur complements, every product on fp64 MFMA, all lambdas and targets in each launch (the
+same closed form the reference's eigendecomposition gives, since C + lam s I is symmetric positive definite
+for lam > 0).
 """
 import torch
 
@@ -27,6 +30,7 @@ from .ops import _need, _ptr, _stream
 
 SHIFT_MAX = 128      # channels per operand centred before the product (each takes a mid and a lo row)
 LO_ROWS = 256        # extra rows per operand when any channel is centred (keeps the Gram width a multiple of 256)
+PIECE = 65536        # rows transposed and multiplied per Gram launch
 
 
 def _transpose(x, dst, partial):
@@ -62,8 +66,9 @@ def _colsum_fold(partial, sums):
     _lib.call("rf_colsum_fold", _ptr(partial), partial.shape[0], partial.shape[1], _ptr(sums), _stream(sums))
 
 
-def gram_accumulate(a, b, c):
-    """c += a b^T (a [M, K], b [N, K] bf16 K-contiguous; c [M, N] fp64): fp32 over K, added in fp64."""
+def gram_accumulate(a, b, c, fold_rows=0):
+    """c += a b^T (a [M, K], b [N, K] bf16 K-contiguous; c [M, N] fp64): fp32 over runs of at most fold_rows
+    of K (0: all of K), each run added in fp64."""
     _need(a, "a", torch.bfloat16, 2)
     _need(b, "b", torch.bfloat16, 2)
     _need(c, "c", torch.float64, 2)
@@ -71,8 +76,8 @@ def gram_accumulate(a, b, c):
     N = b.shape[0]
     if b.shape[1] != K or tuple(c.shape) != (M, N):
         raise ValueError(f"gram shapes a {tuple(a.shape)}, b {tuple(b.shape)}, c {tuple(c.shape)}")
-    _lib.call("rf_gram_accumulate", _ptr(a), a.stride(0), _ptr(b), b.stride(0), M, N, K, _ptr(c), c.stride(0),
-              _stream(a))
+    _lib.call("rf_gram_accumulate", _ptr(a), a.stride(0), _ptr(b), b.stride(0), M, N, K, int(fold_rows), _ptr(c),
+              c.stride(0), _stream(a))
     return c
 
 
@@ -155,6 +160,7 @@ class RidgeStats:
         self.s1y = {i: torch.zeros(self.out_dim, **f64) for i in self.layers}
         self.sxx, self.sxy = None, {}
         self.base = None
+        self._x, self._xt = None, None
 
     @classmethod
     def from_state(cls, state, device="cuda"):
@@ -172,61 +178,103 @@ class RidgeStats:
         st.base = base
         return st
 
-    def _alloc(self):
-        f64 = dict(dtype=torch.float64, device=self.device)
-        d, o, cx = self.dim, self.out_dim, self.cen_x
-        self.sxx = torch.zeros(d + 2 * cx.s, d + cx.lo_rows, **f64)
-        self.sxy = {i: torch.zeros(d + 2 * cx.s, o + self.cen_y[i].lo_rows, **f64) for i in self.layers}
+    def _buffers(self, kp):
+        """Transposed-operand buffers for kp rows (grown as needed, kept between calls): X^T and Y^T with their
+        extra rows, and the per-64-row column-sum partials."""
+        if self._xt is None or self._xt.shape[1] < kp:
+            d, o, lo = self.dim, self.out_dim, LO_ROWS
+            self._xt = torch.zeros(d + lo, kp, dtype=torch.bfloat16, device=self.device)
+            self._yt = torch.zeros(o + lo, kp, dtype=torch.bfloat16, device=self.device)
+            self._part = torch.empty(kp // 64 * max(d, o), dtype=torch.float32, device=self.device)
+            self._sq = torch.empty_like(self._part)
+        return self._xt, self._yt, self._part
+
+    def _x_piece(self, r, sums):
+        """Rows r .. r + PIECE of the current boundary rows, centred and transposed into X^T (the column sums
+        of their centred values added into s1x when `sums`); returns the row count."""
+        x, d, cx = self._x, self.dim, self.cen_x
+        rows = min(PIECE, x.shape[0] - r)
+        kp = (rows + 63) // 64 * 64
+        xt, _, part = self._buffers(kp)
+        px = tiles_view(part, kp // 64, d)
+        transpose_centred(x[r:r + rows], xt[:d, :kp], xt[d:, :kp], cx.shift, cx.lo_row, px, n_centred=cx.s)
+        if sums:
+            _colsum_fold(px, self.s1x)
+        self._held = r
+        return rows
 
     @torch.no_grad()
-    def add(self, x, ys, block=8192):
-        """x [n, d] and ys {layer: [n, d_out]}: bf16 rows on the GPU (the same rows, in order)."""
+    def begin(self, x, block=8192, w=None):
+        """Boundary rows x [n, d] (bf16, on the GPU) of one document: X^T X into the statistics. Follow with
+        add_layer for every layer (code/kva/ridge.py:34-47). Rows go PIECE at a time through one Gram launch
+        each, the fp32 sums running over at most `block` rows (the reference's block) before each is added
+        into fp64. w (row weights) is not supported: the weighted fit is not part of the fill path."""
+        if w is not None:
+            raise NotImplementedError("RidgeStats.begin: row weights w are not supported on the device")
         _need(x, "x", torch.bfloat16, 2)
         n, d = x.shape
         if d != self.dim or d % 256 or self.out_dim % 256:
             raise ValueError(f"x width {d} (stats dim {self.dim}); widths must be multiples of 256")
         if block <= 0 or block % 64:
             raise ValueError("block must be a positive multiple of 64")
-        for i in self.layers:
-            _need(ys[i], f"ys[{i}]", torch.bfloat16, 2)
-            if tuple(ys[i].shape) != (n, self.out_dim):
-                raise ValueError(f"ys[{i}] shape {tuple(ys[i].shape)}")
+        self._x, self._block, self._held = x, block, None
         if n == 0:
             return
-        blk = min(block, (n + 63) // 64 * 64)
-        dev = x.device
-        w = max(d, self.out_dim)
-        lo = LO_ROWS
-        xt = torch.zeros(d + lo, blk, dtype=torch.bfloat16, device=dev)
-        yt = torch.zeros(self.out_dim + lo, blk, dtype=torch.bfloat16, device=dev)
-        part = torch.empty(blk // 64 * w, dtype=torch.float32, device=dev)
         if self.cen_x is None:                          # the first block's means are the shifts (ridge.py:37-38)
-            sq = torch.empty_like(part)
+            kp = (min(block, n) + 63) // 64 * 64
+            xt, _, part = self._buffers(kp)
             b = self.base
-            cap = self.centre_max
-            self.cen_x = Centring.of_rows(x[:block], xt, part, sq, None if b is None else b["cx"], cap)
-            for i in self.layers:
-                self.cen_y[i] = Centring.of_rows(ys[i][:block], yt, part, sq, None if b is None else b["cy"][i], cap)
-            self._alloc()
+            self.cen_x = Centring.of_rows(x[:block], xt, part, self._sq, None if b is None else b["cx"],
+                                          self.centre_max)
+            self.sxx = torch.zeros(d + 2 * self.cen_x.s, d + self.cen_x.lo_rows, dtype=torch.float64,
+                                   device=self.device)
         cx = self.cen_x
-        for r in range(0, n, block):
-            rows = min(block, n - r)
-            kp = (rows + 63) // 64 * 64
-            xm, xl = xt[:d, :kp], xt[d:, :kp]
-            px = tiles_view(part, kp // 64, d)
-            transpose_centred(x[r:r + rows], xm, xl, cx.shift, cx.lo_row, px, n_centred=cx.s)
-            _colsum_fold(px, self.s1x)
-            a = xt[:d + 2 * cx.s, :kp]
-            gram_accumulate(a, xt[:d + cx.lo_rows, :kp], self.sxx)
-            for i in self.layers:
-                cy = self.cen_y[i]
-                o = self.out_dim
-                py = tiles_view(part, kp // 64, o)
-                transpose_centred(ys[i][r:r + rows], yt[:o, :kp], yt[o:, :kp], cy.shift, cy.lo_row, py,
-                                  n_centred=cy.s)
-                _colsum_fold(py, self.s1y[i])
-                gram_accumulate(a, yt[:o + cy.lo_rows, :kp], self.sxy[i])
         self.n += n
+        for r in range(0, n, PIECE):
+            rows = self._x_piece(r, True)
+            kp = (rows + 63) // 64 * 64
+            xt = self._xt
+            gram_accumulate(xt[:d + 2 * cx.s, :kp], xt[:d + cx.lo_rows, :kp], self.sxx, block)
+
+    @torch.no_grad()
+    def add_layer(self, i, y):
+        """The same rows' true inputs y [n, d_out] of layer i (code/kva/ridge.py:54-62): X^T Y_i into the statistics."""
+        if i not in self.s1y:
+            raise KeyError(f"layer {i} is not one of the statistics' layers {self.layers}")
+        x = getattr(self, "_x", None)
+        if x is None:
+            raise ValueError("add_layer before begin")
+        _need(y, f"y[{i}]", torch.bfloat16, 2)
+        n = x.shape[0]
+        if tuple(y.shape) != (n, self.out_dim):
+            raise ValueError(f"y[{i}] shape {tuple(y.shape)}; want ({n}, {self.out_dim})")
+        if n == 0:
+            return
+        d, o, block, cx = self.dim, self.out_dim, self._block, self.cen_x
+        if i not in self.cen_y:
+            kp = (min(block, n) + 63) // 64 * 64
+            _, yt, part = self._buffers(kp)
+            b = self.base
+            self.cen_y[i] = Centring.of_rows(y[:block], yt, part, self._sq, None if b is None else b["cy"][i],
+                                             self.centre_max)
+        cy = self.cen_y[i]
+        if i not in self.sxy:
+            self.sxy[i] = torch.zeros(d + 2 * cx.s, o + cy.lo_rows, dtype=torch.float64, device=self.device)
+        for r in range(0, n, PIECE):
+            rows = self._x_piece(r, False) if self._held != r else min(PIECE, n - r)
+            kp = (rows + 63) // 64 * 64
+            xt, yt, part = self._buffers(kp)
+            py = tiles_view(part, kp // 64, o)
+            transpose_centred(y[r:r + rows], yt[:o, :kp], yt[o:, :kp], cy.shift, cy.lo_row, py, n_centred=cy.s)
+            _colsum_fold(py, self.s1y[i])
+            gram_accumulate(xt[:d + 2 * cx.s, :kp], yt[:o + cy.lo_rows, :kp], self.sxy[i], block)
+
+    def add(self, x, ys, block=8192, w=None):
+        """x [n, d] and ys {layer: [n, d_out]}: bf16 rows on the GPU (the same rows, in order)
+        (code/kva/ridge.py:64-68)."""
+        self.begin(x, block, w)
+        for i in self.layers:
+            self.add_layer(i, ys[i])
 
     def state(self, device="cpu"):
         """RidgeStats.state() (code/kva/ridge.py:70-74): shifted sums about cx / cy, fp64."""
@@ -240,6 +288,10 @@ class RidgeStats:
         sxx = recentre(centred_products(self.sxx, d, cx, d, cx), self.s1x, self.s1x, dx, dx, n)
         cy, sy, sxy = {}, {}, {}
         for i in self.layers:
+            if i not in self.cen_y:                 # no rows of this layer yet: zero sums, no shift (ridge.py:73)
+                sy[i] = self.s1y[i].clone()
+                sxy[i] = torch.zeros(d, o, dtype=torch.float64, device=self.device)
+                continue
             c = self.cen_y[i]
             cy[i] = c.c
             sy[i] = self.s1y[i] - n * c.delta

@@ -46,7 +46,9 @@ def _emulate(st, x, ys, block):
         st.cen_x = _centring(x[:block], None if b is None else b["cx"], st.centre_max)
         for i in st.layers:
             st.cen_y[i] = _centring(ys[i][:block], None if b is None else b["cy"][i], st.centre_max)
-        st._alloc()
+        f64 = dict(dtype=torch.float64)
+        st.sxx = torch.zeros(d + 2 * st.cen_x.s, d + st.cen_x.lo_rows, **f64)
+        st.sxy = {i: torch.zeros(d + 2 * st.cen_x.s, o + st.cen_y[i].lo_rows, **f64) for i in st.layers}
     ax, s1 = _operand(x, st.cen_x)
     st.s1x += s1
     st.sxx += ax[:, :d + 2 * st.cen_x.s].T @ ax[:, :d + st.cen_x.lo_rows]

@@ -37,18 +37,32 @@ def test_transpose_is_bit_exact_with_column_sums(dev):
     assert rel(sums, x.double().sum(0)) < 1e-6
 
 
-def test_gram_accumulate_matches_fp64_products(dev):
+@pytest.mark.parametrize("fold_rows", [0, 128, 512])
+def test_gram_accumulate_matches_fp64_products(dev, fold_rows):
+    """fp32 runs of at most fold_rows (staggered by tile: the 6 tiles here start at 6 different offsets) added
+    into fp64, against fp64 products; fold_rows 0 sums the whole K in fp32."""
     from rfill import ridge
     g = torch.Generator().manual_seed(1)
     a = torch.randn(384, 1024, generator=g).to(torch.bfloat16)
-    b = (torch.randn(512, 1024, generator=g) * 3).to(torch.bfloat16)
-    c0 = torch.randn(384, 512, generator=g, dtype=torch.float64)
+    b = (torch.randn(768, 1024, generator=g) * 3).to(torch.bfloat16)
+    c0 = torch.randn(384, 768, generator=g, dtype=torch.float64)
     c = c0.to(dev)
-    ridge.gram_accumulate(a.to(dev), b.to(dev), c)
+    ridge.gram_accumulate(a.to(dev), b.to(dev), c, fold_rows)
     want = c0 + a.double() @ b.double().T
     err = rel(c, want)
-    print(f"gram rel err {err:.2e}")
+    print(f"gram (fold_rows {fold_rows}) rel err {err:.2e}")
     assert err < 1e-6
+    again = c0.to(dev)
+    ridge.gram_accumulate(a.to(dev), b.to(dev), again, fold_rows)
+    assert torch.equal(again, c)
+
+
+def test_gram_accumulate_refuses_bad_fold(dev):
+    from rfill import ridge
+    a = torch.zeros(256, 128, dtype=torch.bfloat16, device=dev)
+    c = torch.zeros(256, 256, dtype=torch.float64, device=dev)
+    with pytest.raises(ValueError, match="fold_rows"):
+        ridge.gram_accumulate(a, a, c, 96)
 
 
 def _student(n, d, seed):
