@@ -149,17 +149,17 @@ int rf_attend_rows_workspace_bytes(int64_t nq, int hq, int hkv, int d, int64_t c
  * stride ldo, 8-byte aligned). With slot0 = n_keys - nq this is the exact tail's attention in
  * Model.layer, ops.attend (code/kva/ops.py:107-128, code/kva/model.py:247-257); with qpos the exact
  * rows' attention in layer_rows, ops.attend_at / attend_rows (code/kva/ops.py:131-170). Needs d 64 or 128
- * and hq / hkv in {1, 2, 4, 8}. The workspace (caller-owned device memory, 16-byte aligned) receives V
- * transposed and, when the query blocks are too few for the GPU, the partial results of a key-range
- * split, merged in a fixed order: rf_attend_causal_workspace_bytes gives the size for the full split (a
- * smaller one, at least the transposed V, gives fewer splits). */
+ * and hq / hkv in {1, 2, 4, 8}. The workspace (caller-owned device memory, 16-byte aligned; may be NULL)
+ * receives, when the query blocks are too few for the GPU, the partial results of a key-range split,
+ * merged in a fixed order: rf_attend_causal_workspace_bytes gives the size for the full split (a smaller
+ * one gives fewer splits, NULL none). */
 int rf_attend_causal(const uint16_t* q, int64_t ldq, int64_t nq, const int64_t* qpos, int64_t slot0, int hq, int d,
                      const uint16_t* kbuf, const uint16_t* vbuf, int hkv, int64_t head_stride, int64_t row_stride,
                      int64_t n_keys, float scale, uint16_t* out, int64_t ldo, void* workspace, size_t ws_bytes,
                      hipStream_t stream);
 
-/* Workspace bytes rf_attend_causal uses for nq queries over n_keys keys (V transposed + full key split). Host
- * only. */
+/* Workspace bytes rf_attend_causal uses for nq queries over n_keys keys (the full key-range split; 0 when the
+ * query blocks alone fill the GPU). Host only. */
 int rf_attend_causal_workspace_bytes(int64_t nq, int hq, int hkv, int d, int64_t n_keys, size_t* bytes);
 
 /* out = bf16(x + y) row by row (rows x H) and out's row sum-of-squares partials ssq [rows, H / 256]: the
@@ -194,6 +194,29 @@ int rf_norm_linear(const uint16_t* x, int64_t ldx, const float* ssq, int64_t P, 
 int rf_gdn_fill(const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int dk, int dv, const uint16_t* conv_w,
                 const uint16_t* conv_in, uint16_t* conv_out, const float* a_log, const float* dt_bias, float* state,
                 void* workspace, size_t ws_bytes, hipStream_t stream);
+
+/* One layer's operands of rf_gdn_fill_batch: as the arguments of rf_gdn_fill of the same names. */
+typedef struct rf_gdn_layer {
+  const uint16_t* pre;
+  int64_t ld;
+  const uint16_t* conv_w;
+  const uint16_t* conv_in;
+  uint16_t* conv_out;
+  const float* a_log;
+  const float* dt_bias;
+  float* state;
+} rf_gdn_layer;
+
+#define RF_GDN_BATCH_MAX 2
+
+/* rf_gdn_fill of n_layers (1 .. RF_GDN_BATCH_MAX) independent layers over the same P rows and head shapes, in
+ * one prep and one scan launch per pass for all of them: the late GDN layers of a fill each start from
+ * their own cache (code/kva/model.py:510-523 per layer inside code/kva/kva.py:396-449), so their sequential
+ * chunk scans run side by side on the GPU. Each layer's result is bit-identical to its rf_gdn_fill. The
+ * workspace is split evenly between the layers (rf_gdn_workspace_bytes(rows, ...) each for one pass of
+ * `rows` rows); states and conv_out buffers must be distinct. */
+int rf_gdn_fill_batch(const rf_gdn_layer* layers, int n_layers, int64_t P, int nk, int nv, int dk, int dv,
+                      void* workspace, size_t ws_bytes, hipStream_t stream);
 
 /* Workspace bytes rf_gdn_fill needs to fill `rows` rows in one pass (rows = 0: the one-chunk minimum).
  * Host-only; no device work. */

@@ -2,9 +2,10 @@
 // attention in Model.layer (code/kva/ops.py:107-128 attend, queries bottom-right aligned with the keys),
 // head_dim 64 or 128, grouped-query heads with a group of 1, 2, 4 or 8.
 //
-// V is first transposed into the workspace (k_vt: V^T [hkv, d, round_up(n, 64)], zero past the last
-// key), so both operands of both products stream from memory into LDS as full 128-byte lines with
-// direct loads (buffer_load_dwordx4 ... lds). A block takes one K / V head and 256 query rows (256 / rep
+// K and V tiles stream from the caches into LDS as full 128-byte lines with direct loads
+// (buffer_load_dwordx4 ... lds), both row-major ([key, d]); the V^T operand of the second product is read
+// out of the row-major V tile with LDS transpose reads (ds_read_b64_tr_b16). A block takes one K / V head
+// and 256 query rows (256 / rep
 // consecutive queries x the rep query heads sharing the K / V head); 8 waves, each owning 32 query rows
 // of one head. The keys 0 .. (the block's last query position) go through LDS in tiles of 64, three
 // tiles in flight and four stages. Per tile and wave:
@@ -17,7 +18,8 @@
 //       when a score exceeds it by more than 2^8), so the O rescale runs on few tiles;
 //   O^T += V^T P^T on the same MFMA: P (rounded to bf16) is the B operand straight from the score
 //       registers, the contraction order over each 16-key step being keys {0..3, 8..11} + 4 (l / 32)
-//       of the step, and the V^T fragment is read in that order (two 8-byte LDS reads).
+//       of the step, and the V^T fragment is read in that order: two transpose reads, each giving a lane
+//       4 consecutive keys of its d column.
 // Each SIMD holds two waves, so one wave's softmax (VALU) can issue beside the other's MFMAs, and the
 // next tile's score MFMAs run in the same instruction block as this tile's exponentials. (Waves of 64
 // query rows, one per SIMD, read half as much LDS per tile but measured 11 % slower: the second wave's
@@ -60,24 +62,26 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (0 << 8) | ((n >> 4) << 14));
 }
 
-// LDS layout of one stage: the K tile (64 keys x AD) then the V^T tile (AD rows x 64 keys), in 16-byte
-// chunks. K row r's chunk c sits at r * KCPR + (c ^ (r % KCPR)); V^T row r's chunk c at
-// r * 8 + (c ^ ((r / 2 ^ 2 (r / 32)) % 8)): the fragment reads (32 rows, one chunk or half chunk per lane)
-// then hit distinct banks, and so do a lane's eight V^T reads of a key step (the chunk pair of the step in
-// the four d blocks, rows 32 apart), which the compiler pairs into single instructions.
+// LDS layout of one stage: the K tile then the V tile, each 64 keys x AD row-major in 16-byte chunks. K row
+// r's chunk c sits at r * KCPR + (c ^ (r % KCPR)): the score fragment reads (32 rows, one chunk per lane)
+// hit distinct banks. V row r's chunk c sits at K_U4 + r * KCPR + (c ^ (4 vsw(r))): a transpose read takes
+// 8 bytes in each of 4 consecutive rows over 4 chunks per row per 32 lanes, and the swizzle moves the four
+// rows onto four different 64-byte bank ranges.
 template <int AD>
 struct Layout {
   static constexpr int KCPR = AD / 8;
   static constexpr int K_U4 = KT * KCPR;
-  static constexpr int V_U4 = AD * (KT / 8);
+  static constexpr int V_U4 = KT * KCPR;
   static constexpr int STAGE_U4 = K_U4 + V_U4;
   static constexpr int KLOADS = K_U4 / 64 / NW;     // direct-load instructions per wave per tile
   static constexpr int VLOADS = V_U4 / 64 / NW;
   static constexpr int LOADS = KLOADS + VLOADS;
   static_assert(KLOADS * 64 * NW == K_U4 && VLOADS * 64 * NW == V_U4, "tile loads must split evenly");
   __device__ static int kslot(int row, int c) { return row * KCPR + (c ^ (row & (KCPR - 1))); }
-  __device__ static int vswz(int row) { return ((row >> 1) ^ ((row >> 5) << 1)) & 7; }
-  __device__ static int vslot(int row, int c) { return K_U4 + row * 8 + (c ^ vswz(row)); }
+  // d 128: a row is 256 bytes, rows r .. r + 3 shift by 0, 64, 128, 192 bytes; d 64: rows are 128 bytes,
+  // row parity already picks the half of a 256-byte bank line, and rows r, r + 2 shift by 0 and 64
+  __device__ static int vsw(int row) { return AD == 128 ? (row & 3) : ((row >> 1) & 1); }
+  __device__ static int vslot(int row, int c) { return K_U4 + row * KCPR + (c ^ (4 * vsw(row))); }
 };
 
 struct CausalArgs {
@@ -89,8 +93,7 @@ struct CausalArgs {
   const uint16_t* kc;      // K cache [hkv, cap, d]
   int64_t head_stride, row_stride;
   int64_t n_keys;
-  const uint16_t* vt;      // V^T [hkv, d, vt_ld]
-  int64_t vt_ld;
+  const uint16_t* vc;      // V cache, as kc
   int hq, hkv;
   float scale_log2;        // scale * log2(e)
   uint16_t* out;           // [nq, >= hq * d]
@@ -129,19 +132,33 @@ constexpr float RESCALE_LOG2 = 8.0f;
 
 // Per-lane LDS byte offsets of the fragments within a stage, the same for every tile. K fragment (key
 // half kb, d step s): row 32 kb + n, chunk 2 s + hh, at ko[s] + kb * 32 KCPR 16 (row 32 kb + n has the
-// swizzle of row n). V^T fragment (d block b, key chunk c): row 32 b + n, at vo[c ^ 2 b] + b * 32 * 8 * 16
-// (row 32 b + n has the swizzle of row n XOR 2 b), 8 hh bytes into the chunk (the lane half's four keys).
+// swizzle of row n). V^T fragment (d block b, 16-key step stp): lane l = 16 g + t takes, in each of two
+// transpose reads, row 16 stp + 8 i + 4 (g / 2) + t / 4 (i = 0, 1) at d 32 b + 16 (g % 2) + 4 (t % 4)
+// (8 bytes), and receives keys 16 stp + 8 i + 4 (g / 2) + 0 .. 3 of d 32 b + 16 (g % 2) + t: the fragment
+// order {0..3, 8..11} + 4 hh. Its byte offset is vo + vb[b] + (16 stp + 8 i) KCPR 16 (rows 16 stp + 8 i + r
+// have the swizzle of row r).
 template <int AD>
 struct FragOffsets {
-  uint32_t ko[AD / 16], vo[8];
-  __device__ FragOffsets(int n, int hh) {
+  uint32_t ko[AD / 16], vo, vb[AD / 32];
+  __device__ FragOffsets(int lane) {
     using L = Layout<AD>;
+    const int n = lane & 31, hh = lane >> 5, g = lane >> 4, t = lane & 15;
 #pragma unroll
     for (int s = 0; s < AD / 16; ++s) ko[s] = static_cast<uint32_t>(L::kslot(n, 2 * s + hh) * 16);
+    const int r0 = 4 * (g >> 1) + (t >> 2), cl = 2 * (g & 1) + ((t & 3) >> 1);
+    vo = static_cast<uint32_t>((L::K_U4 + r0 * L::KCPR + cl) * 16 + 8 * (t & 1));
 #pragma unroll
-    for (int c = 0; c < 8; ++c) vo[c] = static_cast<uint32_t>(L::vslot(n, c) * 16 + 8 * hh);
+    for (int b = 0; b < AD / 32; ++b) vb[b] = static_cast<uint32_t>(4 * (b ^ L::vsw(r0)) * 16);
   }
 };
+
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Four keys of one d column per lane out of the row-major V tile (ds_read_b64_tr_b16).
+__device__ __forceinline__ uint2 read_tr(const char* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)(p));
+  return __builtin_bit_cast(uint2, v);
+}
 
 // The two lane halves' values of a lane pair (l, l ^ 32), the same in both lanes: v of the lower lane
 // and v of the upper lane (one v_permlane32_swap).
@@ -241,8 +258,8 @@ __device__ __forceinline__ void tile_step(const char* __restrict__ st, const cha
                                                              pk[4 * stp + 3]));
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      const uint2 vl = *reinterpret_cast<const uint2*>(st + fo.vo[(2 * stp) ^ (2 * b)] + b * 32 * 8 * 16);
-      const uint2 vh = *reinterpret_cast<const uint2*>(st + fo.vo[(2 * stp + 1) ^ (2 * b)] + b * 32 * 8 * 16);
+      const char* vp = st + fo.vo + fo.vb[b] + 16 * stp * L::KCPR * 16;
+      const uint2 vl = read_tr(vp), vh = read_tr(vp + 8 * L::KCPR * 16);
       o[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_frag(make_uint4(vl.x, vl.y, vh.x, vh.y)), pf, o[b], 0, 0, 0);
     }
   }
@@ -286,8 +303,7 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
   // determines the row and logical chunk it fetches
   const uint16_t* kh = a.kc + hk * a.head_stride;
   const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kh, static_cast<uint32_t>(a.n_keys * a.row_stride * 2));
-  const __amdgpu_buffer_rsrc_t rv =
-      buffer_rsrc(a.vt + static_cast<int64_t>(hk) * AD * a.vt_ld, static_cast<uint32_t>(AD * a.vt_ld * 2));
+  const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(a.vc + hk * a.head_stride, static_cast<uint32_t>(a.n_keys * a.row_stride * 2));
   uint32_t koff[L::KLOADS], voff[L::VLOADS];
 #pragma unroll
   for (int i = 0; i < L::KLOADS; ++i) {
@@ -298,14 +314,13 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
 #pragma unroll
   for (int i = 0; i < L::VLOADS; ++i) {
     const int s = (w * L::VLOADS + i) * 64 + lane;
-    const int row = s / 8, pc = s % 8, c = pc ^ L::vswz(row);
-    voff[i] = static_cast<uint32_t>((row * a.vt_ld + c * 8) * 2);
+    const int row = s / L::KCPR, pc = s % L::KCPR, c = pc ^ (4 * L::vsw(row));
+    voff[i] = static_cast<uint32_t>((row * a.row_stride + c * 8) * 2);
   }
   char* base = reinterpret_cast<char*>(lds);
   auto issue = [&](int it) {
-    issue_tile<AD>(rk, rv, koff, voff, base + ((it - it0) % NSTAGE) * L::STAGE_U4 * 16,
-                   static_cast<uint32_t>(static_cast<int64_t>(it) * KT * a.row_stride * 2),
-                   static_cast<uint32_t>(it * KT * 2), w);
+    const uint32_t tb = static_cast<uint32_t>(static_cast<int64_t>(it) * KT * a.row_stride * 2);
+    issue_tile<AD>(rk, rv, koff, voff, base + ((it - it0) % NSTAGE) * L::STAGE_U4 * 16, tb, tb, w);
   };
 
   f32x16 o[NB];
@@ -320,7 +335,7 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
   // computed in the same block (the MFMAs run beside the softmax's VALU work). Loads run three tiles
   // ahead into four stages: tile it + 3 goes into the stage of tile it - 1, whose last reads (its V^T)
   // ended before this iteration's barrier.
-  const FragOffsets<AD> fo(n, hh);
+  const FragOffsets<AD> fo(lane);
   f32x16 sc[2], sn[2];
   auto stage = [&](int it) { return base + ((it - it0) % NSTAGE) * L::STAGE_U4 * 16; };
   for (int i = 0; i < 3; ++i)
@@ -376,10 +391,14 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
 }
 
 // Merges the key-range splits of one (query block, K / V head): M = max_s m_s, L = sum_s l_s 2^(m_s - M),
-// O = sum_s O_s 2^(m_s - M) / L (base-2 maxima), splits in order; thread t takes query row t of the block.
+// O = sum_s O_s 2^(m_s - M) / L (base-2 maxima), splits in order. A thread takes 4 consecutive d of one query
+// row (AD / 4 threads per row, blockIdx.z picks 256 of the block's QROWS * AD / 4 such pieces), so the
+// partials are read as whole rows and the outputs written as 8-byte runs.
 template <int AD>
-__global__ __launch_bounds__(QROWS) void k_causal_combine(CausalArgs a, int ns) {
-  const int r = threadIdx.x, w = r / 32, n = r % 32;
+__global__ __launch_bounds__(256) void k_causal_combine(CausalArgs a, int ns) {
+  constexpr int TPR = AD / 4;
+  const int idx = blockIdx.z * 256 + threadIdx.x;
+  const int r = idx / TPR, e = 4 * (idx % TPR), w = r / 32, n = r % 32;
   const int rep = a.hq / a.hkv, qp = QROWS / rep;
   const int hk = blockIdx.y, j0 = blockIdx.x * qp;
   const int hg = (32 * w) / qp, po0 = (32 * w) % qp;
@@ -389,66 +408,25 @@ __global__ __launch_bounds__(QROWS) void k_causal_combine(CausalArgs a, int ns) 
   const float* base = a.part + (static_cast<int64_t>(blockIdx.x) * a.hkv + hk) * ns * stride;
   float mx = -INFINITY;
   for (int sp = 0; sp < ns; ++sp) mx = fmaxf(mx, base[sp * stride + QROWS * AD + r]);
-  float l = 0.f, acc[AD];
-#pragma unroll
-  for (int e = 0; e < AD; ++e) acc[e] = 0.f;
+  float l = 0.f;
+  float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int sp = 0; sp < ns; ++sp) {
     const float* pb = base + sp * stride;
     const float ms = pb[QROWS * AD + r];
     const float f = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
     l += pb[QROWS * AD + QROWS + r] * f;
-    const float4* orow = reinterpret_cast<const float4*>(pb + r * AD);
-#pragma unroll
-    for (int e = 0; e < AD / 4; ++e) {
-      const float4 v = orow[e];
-      acc[4 * e] += v.x * f;
-      acc[4 * e + 1] += v.y * f;
-      acc[4 * e + 2] += v.z * f;
-      acc[4 * e + 3] += v.w * f;
-    }
+    const float4 v = *reinterpret_cast<const float4*>(pb + r * AD + e);
+    acc.x += v.x * f;
+    acc.y += v.y * f;
+    acc.z += v.z * f;
+    acc.w += v.w * f;
   }
   const float inv = 1.0f / l;
-  uint16_t* dst = a.out + static_cast<int64_t>(jq) * a.ldo + (hk * rep + hg) * AD;
-#pragma unroll
-  for (int e = 0; e < AD; e += 4)
-    *reinterpret_cast<uint2*>(dst + e) = make_uint2(bf16_pair(acc[e] * inv, acc[e + 1] * inv),
-                                                    bf16_pair(acc[e + 2] * inv, acc[e + 3] * inv));
+  uint16_t* dst = a.out + static_cast<int64_t>(jq) * a.ldo + (hk * rep + hg) * AD + e;
+  *reinterpret_cast<uint2*>(dst) = make_uint2(bf16_pair(acc.x * inv, acc.y * inv), bf16_pair(acc.z * inv, acc.w * inv));
 }
 
-// V^T [hkv, AD, vt_ld] from the V cache [hkv, cap, AD]: keys 0 .. n - 1, zeros up to vt_ld. A block
-// takes 64 keys of one head through LDS; rows of the result are written as 16-byte chunks of 8 keys.
-template <int AD>
-__global__ __launch_bounds__(256) void k_vt(const uint16_t* __restrict__ v, int64_t head_stride, int64_t row_stride,
-                                            int64_t n, uint16_t* __restrict__ vt, int64_t vt_ld) {
-  constexpr int CPR = AD / 8, ROW = AD + 8;
-  __shared__ uint16_t tile[KT * ROW];
-  const int t = threadIdx.x, hk = blockIdx.y;
-  const int64_t k0 = static_cast<int64_t>(blockIdx.x) * KT;
-  const uint16_t* vh = v + hk * head_stride;
-  for (int c = t; c < KT * CPR; c += 256) {
-    const int key = c / CPR, ch = c % CPR;
-    uint4 u = make_uint4(0u, 0u, 0u, 0u);
-    if (k0 + key < n) u = *reinterpret_cast<const uint4*>(vh + (k0 + key) * row_stride + ch * 8);
-    *reinterpret_cast<uint4*>(tile + key * ROW + ch * 8) = u;
-  }
-  __syncthreads();
-  uint16_t* dh = vt + static_cast<int64_t>(hk) * AD * vt_ld + k0;
-  for (int c = t; c < AD * (KT / 8); c += 256) {
-    const int d = c / (KT / 8), kc = c % (KT / 8);
-    uint16_t e[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) e[i] = tile[(kc * 8 + i) * ROW + d];
-    *reinterpret_cast<uint4*>(dh + d * vt_ld + kc * 8) =
-        make_uint4(pack2(e[0], e[1]), pack2(e[2], e[3]), pack2(e[4], e[5]), pack2(e[6], e[7]));
-  }
-}
-
-int64_t vt_cols(int64_t n_keys) { return (n_keys + KT - 1) / KT * KT; }
-
-// Workspace: V^T (rounded up to 256 bytes), then the splits' partials when the key range is split.
-size_t vt_bytes(int hkv, int d, int64_t n_keys) {
-  return (static_cast<size_t>(hkv) * d * vt_cols(n_keys) * 2 + 255) / 256 * 256;
-}
+int64_t key_tiles(int64_t n_keys) { return (n_keys + KT - 1) / KT; }
 
 int64_t query_blocks(int64_t nq, int hq, int hkv) {
   const int64_t qp = QROWS / (hq / hkv);
@@ -463,7 +441,7 @@ size_t part_bytes(int64_t nq, int hq, int hkv, int d, int splits) {
 int causal_splits(int64_t nq, int hq, int hkv, int64_t n_keys) {
   const int64_t blocks = std::max<int64_t>(query_blocks(nq, hq, hkv) * hkv, 1);
   int64_t s = (512 + blocks - 1) / blocks;
-  s = std::min<int64_t>(std::min<int64_t>(s, 16), vt_cols(n_keys) / KT);
+  s = std::min<int64_t>(std::min<int64_t>(s, 16), key_tiles(n_keys));
   return static_cast<int>(std::max<int64_t>(s, 1));
 }
 
@@ -482,7 +460,7 @@ extern "C" int rf_attend_causal_workspace_bytes(int64_t nq, int hq, int hkv, int
   if (!causal_shape_ok(hq, hkv, d))
     return fail(RF_EUNSUPPORTED, "rf_attend_causal_workspace_bytes: head_dim %d, %d query heads over %d K / V heads "
                 "(d 64 or 128, a group of 1, 2, 4 or 8)", d, hq, hkv);
-  *bytes = vt_bytes(hkv, d, n_keys) + part_bytes(nq, hq, hkv, d, causal_splits(nq, hq, hkv, n_keys));
+  *bytes = part_bytes(nq, hq, hkv, d, causal_splits(nq, hq, hkv, n_keys));
   return RF_OK;
 }
 
@@ -490,7 +468,7 @@ extern "C" int rf_attend_causal(const uint16_t* q, int64_t ldq, int64_t nq, cons
                                 int d, const uint16_t* kbuf, const uint16_t* vbuf, int hkv, int64_t head_stride,
                                 int64_t row_stride, int64_t n_keys, float scale, uint16_t* out, int64_t ldo,
                                 void* workspace, size_t ws_bytes, hipStream_t stream) {
-  if (!q || !kbuf || !vbuf || !out || !workspace) return fail(RF_EINVAL_ARG, "rf_attend_causal: null pointer");
+  if (!q || !kbuf || !vbuf || !out) return fail(RF_EINVAL_ARG, "rf_attend_causal: null pointer");
   if (d != 64 && d != 128) return fail(RF_EUNSUPPORTED, "rf_attend_causal: head_dim %d (the kernel takes 64, 128)", d);
   if (!causal_shape_ok(hq, hkv, d))
     return fail(RF_EUNSUPPORTED, "rf_attend_causal: %d query heads over %d K / V heads (group of 1, 2, 4 or 8)", hq,
@@ -499,41 +477,29 @@ extern "C" int rf_attend_causal(const uint16_t* q, int64_t ldq, int64_t nq, cons
     return fail(RF_EINVAL_SHAPE, "rf_attend_causal: queries at slots [%lld, %lld) past the %lld keys", (long long)slot0,
                 (long long)(slot0 + nq), (long long)n_keys);
   if (ldq < static_cast<int64_t>(hq) * d || ldo < static_cast<int64_t>(hq) * d || ldq % 8 || ldo % 4 ||
-      row_stride < d || row_stride % 8 || head_stride % 8 || n_keys * row_stride * 2 >= (1ll << 32) ||
-      static_cast<int64_t>(d) * vt_cols(n_keys) * 2 >= (1ll << 32))
+      row_stride < d || row_stride % 8 || head_stride % 8 || n_keys * row_stride * 2 >= (1ll << 32))
     return fail(RF_EINVAL_SHAPE, "rf_attend_causal: strides (ldq %lld, ldo %lld, row %lld) or %lld keys",
                 (long long)ldq, (long long)ldo, (long long)row_stride, (long long)n_keys);
-  if (!aligned16(q) || !aligned16(kbuf) || !aligned16(vbuf) || !aligned16(workspace) ||
+  if (!aligned16(q) || !aligned16(kbuf) || !aligned16(vbuf) || (workspace && !aligned16(workspace)) ||
       (reinterpret_cast<uintptr_t>(out) & 7u))
     return fail(RF_EINVAL_SHAPE, "rf_attend_causal: alignment");
   if (!(scale > 0.f) || !(scale < 1e30f)) return fail(RF_EINVAL_ARG, "rf_attend_causal: scale %g (must be positive)",
                                                       static_cast<double>(scale));
-  const int64_t vt_ld = vt_cols(n_keys);
-  const size_t vtb = vt_bytes(hkv, d, n_keys);
-  if (ws_bytes < vtb)
-    return fail(RF_EINVAL_SHAPE, "rf_attend_causal: workspace %zu bytes < %zu (V transposed)", ws_bytes, vtb);
   if (nq == 0) return RF_OK;
-  int ns = causal_splits(nq, hq, hkv, n_keys);
-  while (ns > 1 && ws_bytes < vtb + part_bytes(nq, hq, hkv, d, ns)) --ns;     // what the workspace holds
-  uint16_t* vt = static_cast<uint16_t*>(workspace);
-  const dim3 gt(static_cast<unsigned>(vt_ld / KT), static_cast<unsigned>(hkv));
-  if (d == 128) hipLaunchKernelGGL(k_vt<128>, gt, dim3(256), 0, stream, vbuf, head_stride, row_stride, n_keys, vt, vt_ld);
-  else hipLaunchKernelGGL(k_vt<64>, gt, dim3(256), 0, stream, vbuf, head_stride, row_stride, n_keys, vt, vt_ld);
-  int st = check_launch("rf_attend_causal (V transpose)");
-  if (st != RF_OK) return st;
-  CausalArgs a{q, ldq, static_cast<int>(nq), qpos, slot0, kbuf, head_stride, row_stride, n_keys, vt, vt_ld, hq, hkv,
-               scale * 1.4426950408889634f, out, ldo,
-               reinterpret_cast<float*>(static_cast<char*>(workspace) + vtb)};
+  int ns = workspace ? causal_splits(nq, hq, hkv, n_keys) : 1;
+  while (ns > 1 && ws_bytes < part_bytes(nq, hq, hkv, d, ns)) --ns;     // what the workspace holds
+  CausalArgs a{q, ldq, static_cast<int>(nq), qpos, slot0, kbuf, head_stride, row_stride, n_keys, vbuf, hq, hkv,
+               scale * 1.4426950408889634f, out, ldo, static_cast<float*>(workspace)};
   const dim3 grid(static_cast<unsigned>(query_blocks(nq, hq, hkv)), static_cast<unsigned>(hkv),
                   static_cast<unsigned>(ns));
   if (d == 128) hipLaunchKernelGGL(k_attend_causal<128>, grid, dim3(NTHR), 0, stream, a);
   else hipLaunchKernelGGL(k_attend_causal<64>, grid, dim3(NTHR), 0, stream, a);
   if (ns > 1) {
-    st = check_launch("rf_attend_causal");
+    const int st = check_launch("rf_attend_causal");
     if (st != RF_OK) return st;
-    const dim3 g2(grid.x, grid.y);
-    if (d == 128) hipLaunchKernelGGL(k_causal_combine<128>, g2, dim3(QROWS), 0, stream, a, ns);
-    else hipLaunchKernelGGL(k_causal_combine<64>, g2, dim3(QROWS), 0, stream, a, ns);
+    const dim3 g2(grid.x, grid.y, static_cast<unsigned>(QROWS * d / 4 / 256));
+    if (d == 128) hipLaunchKernelGGL(k_causal_combine<128>, g2, dim3(256), 0, stream, a, ns);
+    else hipLaunchKernelGGL(k_causal_combine<64>, g2, dim3(256), 0, stream, a, ns);
   }
   return check_launch("rf_attend_causal");
 }

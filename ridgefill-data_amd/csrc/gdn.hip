@@ -154,8 +154,16 @@ __device__ __forceinline__ float quad_sum(float v) {
 
 // Block = (chunk, value head h). The K-side work (conv of the key head's k, norms, G = K K^T) is
 // recomputed by each of the key head's value heads; the first of them writes K's operand orders.
+// Up to BATCH independent layers' fills per launch (the late GDN layers of a fill do not depend on each
+// other): prep blocks take their layer from blockIdx.z, scan blocks from blockIdx.x / (8 nv).
+constexpr int BATCH = 2;
+struct PrepBatch {
+  PrepArgs a[BATCH];
+};
+
 template <bool OUT>
-__global__ __launch_bounds__(256) void k_gdn_prep(PrepArgs a) {
+__global__ __launch_bounds__(256) void k_gdn_prep(PrepBatch pb) {
+  const PrepArgs a = blockIdx.z == 0 ? pb.a[0] : pb.a[1];
   __shared__ __align__(16) uint16_t k_s[CH * KST];  // the k tile, then T (fp32)
   __shared__ __align__(16) uint16_t v_s[CH * KST];
   __shared__ __align__(16) float a_s[CH * FST];     // A
@@ -493,15 +501,22 @@ __device__ __forceinline__ void split4(const float (&x)[4], uint2& hi, uint2& lo
 //   hi / lo bf16 B-operand frags through LDS; S_w <- decay S_w + K^T[32w .., :] Z.
 // Three barriers per chunk; the operands of the chunk two steps ahead load into registers meanwhile,
 // in four groups between the phases so the address unit streams them in the background.
+struct ScanBatch {
+  ScanArgs a[BATCH];
+};
+
 template <bool OUT>
-__global__ __launch_bounds__(256) void k_gdn_scan(ScanArgs a) {
+__global__ __launch_bounds__(256) void k_gdn_scan(ScanBatch sbatch) {
+  const int per_layer = sbatch.a[0].nv * 8;
+  const int layer = blockIdx.x >= per_layer ? 1 : 0;
+  const ScanArgs a = layer == 0 ? sbatch.a[0] : sbatch.a[1];
   __shared__ __align__(16) f32x4 xp[4][4][64];        // X_w partials [wave][row tile][lane]
   __shared__ __align__(16) uint4 yf[2][2][64];        // Y frags [k-step][hi / lo][lane]
   __shared__ __align__(16) uint4 zf[2][2][64];        // Z frags
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, gi = lane >> 4, ln = lane & 15;
   // block b runs on XCD b % 8: XCD x takes (head, column block) pairs [x nv, (x + 1) nv), so the
   // blocks that share a head's (and a key head's) operands share an L2
-  const int b = blockIdx.x, pair = (b & 7) * a.nv + (b >> 3);
+  const int b = blockIdx.x - layer * per_layer, pair = (b & 7) * a.nv + (b >> 3);
   const int h = pair >> 3, cb = pair & 7, kh = h / (a.nv / a.nk);
   float* st = a.state + static_cast<size_t>(h) * DK * DV + cb * 16 + ln;
   f32x4 S[2];
@@ -786,53 +801,87 @@ extern "C" int rf_gdn_forward_workspace_bytes(int64_t rows, int nk, int nv, int 
 
 namespace {
 
-int gdn_run(const char* fn, const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int dk, int dv,
-            const uint16_t* conv_w, const uint16_t* conv_in, uint16_t* conv_out, const float* a_log,
-            const float* dt_bias, float* state, uint16_t* out, int64_t ldo, void* workspace, size_t ws_bytes,
-            hipStream_t stream) {
-  if (!pre || !conv_w || !conv_out || !a_log || !dt_bias || !state || !workspace)
-    return fail(RF_EINVAL_ARG, "%s: null pointer", fn);
+// One layer's operands of a GDN fill or forward.
+struct LayerIO {
+  const uint16_t* pre;
+  int64_t ld;
+  const uint16_t* conv_w;
+  const uint16_t* conv_in;
+  uint16_t* conv_out;
+  const float* a_log;
+  const float* dt_bias;
+  float* state;
+};
+
+// The fill (out null) or the forward (one layer, out given) of n layers over the same P rows: per pass of up to
+// what each layer's share of the workspace holds, one prep and one scan launch cover every layer.
+int gdn_run(const char* fn, const LayerIO* io, int n, int64_t P, int nk, int nv, int dk, int dv, uint16_t* out,
+            int64_t ldo, void* workspace, size_t ws_bytes, hipStream_t stream) {
+  if (n < 1 || n > BATCH || (out && n != 1)) return fail(RF_EINVAL_ARG, "%s: %d layers (1 .. %d)", fn, n, BATCH);
+  if (!workspace) return fail(RF_EINVAL_ARG, "%s: null workspace", fn);
   if (const int e = check_heads(fn, nk, nv, dk, dv)) return e;
   const int64_t C = 2ll * nk * DK + static_cast<int64_t>(nv) * DV;
-  if (P < 0 || ld < C + 2 * nv || ld % 8)
-    return fail(RF_EINVAL_SHAPE, "%s: P %lld, ld %lld (need >= %lld and a multiple of 8)", fn, (long long)P,
-                (long long)ld, (long long)(C + 2 * nv));
+  for (int l = 0; l < n; ++l) {
+    const LayerIO& L = io[l];
+    if (!L.pre || !L.conv_w || !L.conv_out || !L.a_log || !L.dt_bias || !L.state)
+      return fail(RF_EINVAL_ARG, "%s: null pointer (layer %d)", fn, l);
+    if (P < 0 || L.ld < C + 2 * nv || L.ld % 8)
+      return fail(RF_EINVAL_SHAPE, "%s: P %lld, ld %lld (need >= %lld and a multiple of 8)", fn, (long long)P,
+                  (long long)L.ld, (long long)(C + 2 * nv));
+    if (!aligned16(L.pre) || !aligned16(L.conv_w) || (L.conv_in && !aligned16(L.conv_in)))
+      return fail(RF_EINVAL_ARG, "%s: pre, conv_w and conv_in must be 16-byte aligned", fn);
+    if (L.conv_in == L.conv_out) return fail(RF_EINVAL_ARG, "%s: conv_out must not alias conv_in", fn);
+    for (int m = 0; m < l; ++m)
+      if (io[m].state == L.state || io[m].conv_out == L.conv_out)
+        return fail(RF_EINVAL_ARG, "%s: layers %d and %d share a state or conv_out buffer", fn, m, l);
+  }
   if (out && (ldo < static_cast<int64_t>(nv) * DV || ldo % 8))
     return fail(RF_EINVAL_SHAPE, "%s: ldo %lld (>= nv dv = %d, a multiple of 8)", fn, (long long)ldo, nv * DV);
-  if (!aligned16(pre) || !aligned16(conv_w) || (conv_in && !aligned16(conv_in)) || !aligned16(workspace))
-    return fail(RF_EINVAL_ARG, "%s: pre, conv_w, conv_in and workspace must be 16-byte aligned", fn);
-  if (conv_in == conv_out) return fail(RF_EINVAL_ARG, "%s: conv_out must not alias conv_in", fn);
+  if (!aligned16(workspace)) return fail(RF_EINVAL_ARG, "%s: workspace must be 16-byte aligned", fn);
   const uint32_t sbytes = chunk_bytes(nk, nv);
   const uint64_t cb64 = sbytes + (out ? static_cast<uint64_t>(nv) * OUT_HEAD_BYTES : 0);
   if (cb64 > 0x7fffffffull) return fail(RF_EINVAL_SHAPE, "%s: %d value heads", fn, nv);
   const uint32_t cbytes = static_cast<uint32_t>(cb64);
-  // chunks per pass: what the workspace holds, with buffer offsets below 2^31
-  const int64_t per_pass = std::min<int64_t>(static_cast<int64_t>(ws_bytes / cbytes), 0x7fffffffll / cbytes);
-  if (per_pass < 1) return fail(RF_EINVAL_ARG, "%s: workspace %zu bytes < one chunk (%u bytes)", fn, ws_bytes, cbytes);
+  // each layer's share of the workspace (16-byte aligned); chunks per pass: what a share holds, with buffer
+  // offsets below 2^31
+  const size_t share = ws_bytes / n / 16 * 16;
+  const int64_t per_pass = std::min<int64_t>(static_cast<int64_t>(share / cbytes), 0x7fffffffll / cbytes);
+  if (per_pass < 1)
+    return fail(RF_EINVAL_ARG, "%s: workspace %zu bytes < %d chunks (%u bytes each)", fn, ws_bytes, n, cbytes);
   const int64_t chunks = (P + CH - 1) / CH;
   uint8_t* ws = static_cast<uint8_t*>(workspace);
   for (int64_t c0 = 0; c0 < chunks; c0 += per_pass) {
     const int nc = static_cast<int>(std::min<int64_t>(per_pass, chunks - c0));
-    PrepArgs pa{pre, ld, P, c0 * CH, nk, nv, static_cast<int>(C), conv_w, conv_in, a_log, dt_bias, ws, cbytes, sbytes};
-    ScanArgs sa{ws, cbytes, nc, nk, nv, state, ws, sbytes};
+    PrepBatch pb{};
+    ScanBatch sb{};
+    for (int l = 0; l < n; ++l) {
+      const LayerIO& L = io[l];
+      uint8_t* wl = ws + l * share;
+      pb.a[l] = PrepArgs{L.pre, L.ld, P, c0 * CH, nk, nv, static_cast<int>(C), L.conv_w, L.conv_in, L.a_log,
+                         L.dt_bias, wl, cbytes, sbytes};
+      sb.a[l] = ScanArgs{wl, cbytes, nc, nk, nv, L.state, wl, sbytes};
+    }
     if (out) {
-      hipLaunchKernelGGL(k_gdn_prep<true>, dim3(nc, nv), dim3(256), 0, stream, pa);
+      hipLaunchKernelGGL(k_gdn_prep<true>, dim3(nc, nv, 1), dim3(256), 0, stream, pb);
       if (const int e = check_launch(fn)) return e;
-      hipLaunchKernelGGL(k_gdn_scan<true>, dim3(nv * 8), dim3(256), 0, stream, sa);
+      hipLaunchKernelGGL(k_gdn_scan<true>, dim3(nv * 8), dim3(256), 0, stream, sb);
       if (const int e = check_launch(fn)) return e;
       OutArgs oa{ws, cbytes, sbytes, nk, P, c0 * CH, out, ldo};
       hipLaunchKernelGGL(k_gdn_out, dim3(nc, nv), dim3(256), 0, stream, oa);
       if (const int e = check_launch(fn)) return e;
     } else {
-      hipLaunchKernelGGL(k_gdn_prep<false>, dim3(nc, nv), dim3(256), 0, stream, pa);
+      hipLaunchKernelGGL(k_gdn_prep<false>, dim3(nc, nv, n), dim3(256), 0, stream, pb);
       if (const int e = check_launch(fn)) return e;
-      hipLaunchKernelGGL(k_gdn_scan<false>, dim3(nv * 8), dim3(256), 0, stream, sa);
+      hipLaunchKernelGGL(k_gdn_scan<false>, dim3(nv * 8 * n), dim3(256), 0, stream, sb);
       if (const int e = check_launch(fn)) return e;
     }
   }
-  hipLaunchKernelGGL(k_conv_tail, dim3((3 * C + 255) / 256), dim3(256), 0, stream, pre, ld, P, static_cast<int>(C),
-                     conv_in, conv_out);
-  return check_launch(fn);
+  for (int l = 0; l < n; ++l) {
+    hipLaunchKernelGGL(k_conv_tail, dim3((3 * C + 255) / 256), dim3(256), 0, stream, io[l].pre, io[l].ld, P,
+                       static_cast<int>(C), io[l].conv_in, io[l].conv_out);
+    if (const int e = check_launch(fn)) return e;
+  }
+  return RF_OK;
 }
 
 }  // namespace
@@ -840,8 +889,21 @@ int gdn_run(const char* fn, const uint16_t* pre, int64_t ld, int64_t P, int nk, 
 extern "C" int rf_gdn_fill(const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int dk, int dv,
                            const uint16_t* conv_w, const uint16_t* conv_in, uint16_t* conv_out, const float* a_log,
                            const float* dt_bias, float* state, void* workspace, size_t ws_bytes, hipStream_t stream) {
-  return gdn_run("rf_gdn_fill", pre, ld, P, nk, nv, dk, dv, conv_w, conv_in, conv_out, a_log, dt_bias, state, nullptr,
-                 0, workspace, ws_bytes, stream);
+  const LayerIO io{pre, ld, conv_w, conv_in, conv_out, a_log, dt_bias, state};
+  return gdn_run("rf_gdn_fill", &io, 1, P, nk, nv, dk, dv, nullptr, 0, workspace, ws_bytes, stream);
+}
+
+extern "C" int rf_gdn_fill_batch(const rf_gdn_layer* layers, int n_layers, int64_t P, int nk, int nv, int dk, int dv,
+                                 void* workspace, size_t ws_bytes, hipStream_t stream) {
+  if (!layers) return fail(RF_EINVAL_ARG, "rf_gdn_fill_batch: null layers");
+  if (n_layers < 1 || n_layers > RF_GDN_BATCH_MAX)
+    return fail(RF_EINVAL_ARG, "rf_gdn_fill_batch: %d layers (1 .. %d)", n_layers, RF_GDN_BATCH_MAX);
+  LayerIO io[RF_GDN_BATCH_MAX];
+  for (int l = 0; l < n_layers; ++l) {
+    const rf_gdn_layer& L = layers[l];
+    io[l] = LayerIO{L.pre, L.ld, L.conv_w, L.conv_in, L.conv_out, L.a_log, L.dt_bias, L.state};
+  }
+  return gdn_run("rf_gdn_fill_batch", io, n_layers, P, nk, nv, dk, dv, nullptr, 0, workspace, ws_bytes, stream);
 }
 
 // ---- allocation-free GDN fill: the per-chunk workspace lives in a file-scope device array
@@ -897,8 +959,8 @@ extern "C" int rf_gdn_fill_noalloc(const uint16_t* pre, int64_t ld, int64_t P, i
                 GDN_SCRATCH_BYTES);
   void* ws = nullptr;
   if (const int e = scratch_address(fn, stream, &ws)) return e;
-  return gdn_run(fn, pre, ld, P, nk, nv, dk, dv, conv_w, conv_in, conv_out, a_log, dt_bias, state, nullptr, 0, ws,
-                 GDN_SCRATCH_BYTES, stream);
+  const LayerIO io{pre, ld, conv_w, conv_in, conv_out, a_log, dt_bias, state};
+  return gdn_run(fn, &io, 1, P, nk, nv, dk, dv, nullptr, 0, ws, GDN_SCRATCH_BYTES, stream);
 }
 
 extern "C" int rf_gdn_forward(const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int dk, int dv,
@@ -906,6 +968,6 @@ extern "C" int rf_gdn_forward(const uint16_t* pre, int64_t ld, int64_t P, int nk
                               const float* dt_bias, float* state, uint16_t* out, int64_t ldo, void* workspace,
                               size_t ws_bytes, hipStream_t stream) {
   if (!out) return fail(RF_EINVAL_ARG, "rf_gdn_forward: null out");
-  return gdn_run("rf_gdn_forward", pre, ld, P, nk, nv, dk, dv, conv_w, conv_in, conv_out, a_log, dt_bias, state, out,
-                 ldo, workspace, ws_bytes, stream);
+  const LayerIO io{pre, ld, conv_w, conv_in, conv_out, a_log, dt_bias, state};
+  return gdn_run("rf_gdn_forward", &io, 1, P, nk, nv, dk, dv, out, ldo, workspace, ws_bytes, stream);
 }

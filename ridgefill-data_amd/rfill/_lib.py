@@ -39,6 +39,7 @@ SIGNATURES = {
     "rf_rope_kv_write": [_P, _I64, _P, _I64, _I64, _I32, _I32, _P, _I32, _P, _P, _I64, _I64, _I64, _I64, _P],
     "rf_norm_linear": [_P, _I64, _P, _I64, _I64, _F32, _P, _I64, _P, _I64, _P, _SZ, _P],
     "rf_gdn_fill": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
+    "rf_gdn_fill_batch": [_P, _I32, _I64, _I32, _I32, _I32, _I32, _P, _SZ, _P],
     "rf_gdn_workspace_bytes": [_I64, _I32, _I32, _I32, _I32, _PSZ],
     "rf_gdn_fill_noalloc": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P],
     "rf_transpose": [_P, _I64, _I64, _I64, _P, _I64, _P, _P],

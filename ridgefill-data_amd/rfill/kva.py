@@ -334,11 +334,23 @@ def two_stream(layers, produce, consume, device):
     main.wait_stream(side)
 
 
-def serial(layers, produce, consume, device):
-    """produce(i, slot) then consume(i, slot) for each layer, all on the current stream."""
-    for n, i in enumerate(layers):
+def serial(layers, produce, consume, device, pair=None):
+    """produce(i, slot) then consume(i, slot) for each layer, all on the current stream. pair: (can(i, j),
+    consume_pair(i, slot_i, j, slot_j)): two consecutive layers with can(i, j) are produced both, then
+    consumed together."""
+    n, k = 0, 0
+    while k < len(layers):
+        i = layers[k]
+        if pair is not None and k + 1 < len(layers) and pair[0](i, layers[k + 1]):
+            j = layers[k + 1]
+            produce(i, n % 2)
+            produce(j, (n + 1) % 2)
+            pair[1](i, n % 2, j, (n + 1) % 2)
+            n, k = n + 2, k + 2
+            continue
         produce(i, n % 2)
         consume(i, n % 2)
+        n, k = n + 1, k + 1
 
 
 def _layer_fill(arm, model, i):
@@ -439,7 +451,18 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
         else:
             model.fill(i, x, pos, cache, ssq=ssq, cs=cs)
 
-    (two_stream if overlap else serial)(layers, produce, consume, dev)
+    def can_pair(i, j):                                 # two GDN layers whose fills do not wait on exact rows
+        return (not computed and model.layer_types[i] == "gdn" and model.layer_types[j] == "gdn"
+                and fills[i] != "none" and fills[j] != "none")
+
+    def consume_pair(i, si, j, sj):
+        (xi, qi), (xj, qj) = inputs[si], inputs[sj]
+        model.fill_batch([i, j], [xi, xj], cache, ssqs=[qi, qj])
+
+    if overlap:
+        two_stream(layers, produce, consume, dev)
+    else:
+        serial(layers, produce, consume, dev, pair=(can_pair, consume_pair))
     return cache, P
 
 

@@ -187,7 +187,7 @@ class FillModel:
             return {}
         if ssq is None:
             ssq = ops.row_ssq(x)
-        pre = ops.norm_linear(x, ssq, self.eps, w["w_in"])
+        pre = self._fill_rows(w, x, ssq)
         rec = c.get("rec")
         rec = (torch.zeros(self.nv, self.dk, self.dv, dtype=torch.float32, device=x.device) if rec is None
                else rec.float().contiguous().clone())
@@ -205,6 +205,50 @@ class FillModel:
         if st is not None:
             c["rec"] = c["rec"] + st.to(c["rec"])
         return ck
+
+    def _fill_rows(self, w, x, ssq):
+        """The in-projection rows [P, q | k | v | b | a] a GDN fill reads (code/kva/model.py:452-458). The state
+        update reads k, v, b and a only, and the conv state the last 3 rows of q | k | v, so q is projected for
+        those 3 rows alone (one unsplit GEMM: the same per-element arithmetic as the full projection, so every
+        value read is the full projection's bits) and the other rows' q columns stay unwritten."""
+        W = w["w_in"]
+        P = x.shape[0]
+        nq = self.nk * self.dk
+        if nq % 256 or P <= 3:
+            return ops.norm_linear(x, ssq, self.eps, W)
+        pre = torch.empty(P, W.shape[0], dtype=torch.bfloat16, device=x.device)
+        ops.norm_linear(x, ssq, self.eps, W[nq:], out=pre[:, nq:])
+        ops.norm_linear(x[P - 3:], ssq[P - 3:], self.eps, W[:nq], out=pre[P - 3:, :nq])
+        return pre
+
+    def fill_batch(self, ids, xs, cache, ssqs=None):
+        """fill() of up to ops.GDN_BATCH_MAX GDN layers over the same rows at once: their in-projections one after
+        another, then one batched delta-rule fill (rf_gdn_fill_batch), so the layers' sequential chunk scans run
+        side by side. Every layer's conv and recurrent state is bit-identical to fill() of it alone."""
+        ids = list(ids)
+        if not 1 <= len(ids) <= ops.GDN_BATCH_MAX or any(self.layer_types[i] != "gdn" for i in ids):
+            raise ValueError(f"fill_batch: 1 .. {ops.GDN_BATCH_MAX} GDN layers, got {ids}")
+        P = xs[0].shape[0]
+        if any(x.shape[0] != P for x in xs):
+            raise ValueError("fill_batch: every layer takes the same rows")
+        if P == 0:
+            return
+        ssqs = [None] * len(ids) if ssqs is None else ssqs
+        jobs = []
+        for i, x, ssq in zip(ids, xs, ssqs):
+            w = self._layer(i, "gdn")
+            pre = self._fill_rows(w, x, ops.row_ssq(x) if ssq is None else ssq)
+            c = cache[i]
+            rec = c.get("rec")
+            rec = (torch.zeros(self.nv, self.dk, self.dv, dtype=torch.float32, device=x.device) if rec is None
+                   else rec.float().contiguous().clone())
+            jobs.append((pre, w["conv"], c.get("conv"), w["a_log"], w["dt_bias"], rec))
+        convs = ops.gdn_fill_batch(jobs, self.nk, self.nv, self.dk, self.dv,
+                                   self._gdn_workspace(P, xs[0].device, len(ids)))
+        for i, job, conv in zip(ids, jobs, convs):
+            c = cache[i]
+            c["conv"], c["rec"] = conv, job[5]
+            c["len"] = c.get("len", 0) + P
 
     def _attn_workspace(self, nq, n, device):
         """The exact-row attention's key-split workspace, shared by every layer (stream-ordered reuse)."""
@@ -229,10 +273,10 @@ class FillModel:
             wss[role] = ws = torch.empty(need, dtype=torch.uint8, device=device)
         return ws
 
-    def _gdn_workspace(self, rows, device):
+    def _gdn_workspace(self, rows, device, layers=1):
         """The GDN kernels' per-chunk workspace, shared by every GDN layer (stream-ordered reuse), sized
-        for min(rows, GDN_ROWS) rows per pass."""
-        need = ops.gdn_workspace_bytes(min(rows, GDN_ROWS), self.nk, self.nv, self.dk, self.dv)
+        for min(rows, GDN_ROWS) rows per pass of each of `layers` layers filled together."""
+        need = layers * ops.gdn_workspace_bytes(min(rows, GDN_ROWS), self.nk, self.nv, self.dk, self.dv)
         if self._gdn_ws is None or self._gdn_ws.numel() < need or self._gdn_ws.device != device:
             self._gdn_ws = torch.empty(need, dtype=torch.uint8, device=device)
         return self._gdn_ws
@@ -435,7 +479,7 @@ class FillModel:
         return (self.logits(h[torch.as_tensor(keep, device=self.device)]) if keep is not None else None), cache
 
     def _causal_workspace(self, nq, n, device):
-        """rf_attend_causal's workspace (V transposed, key-range splits), shared by every layer
+        """rf_attend_causal's workspace (the key-range splits' partials), shared by every layer
         (stream-ordered reuse)."""
         need = ops.attend_causal_workspace_bytes(nq, self.n_heads, self.n_kv, self.head_dim, n)
         ws = getattr(self, "_causal_ws", None)

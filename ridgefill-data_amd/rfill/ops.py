@@ -287,7 +287,7 @@ CAUSAL_GROUPS = (1, 2, 4, 8)
 
 
 def attend_causal_workspace_bytes(nq, hq, hkv, d, n):
-    """Device bytes attend_causal uses for nq queries over n keys (V transposed, key-range splits)."""
+    """Device bytes attend_causal uses for nq queries over n keys (the key-range splits' partials; may be 0)."""
     b = ctypes.c_size_t(0)
     _lib.call("rf_attend_causal_workspace_bytes", nq, hq, hkv, d, n, ctypes.byref(b))
     return b.value
@@ -317,9 +317,11 @@ def attend_causal(q, slot0, kbuf, vbuf, n, hq, scale, out=None, workspace=None, 
     if workspace is None:
         workspace = torch.empty(attend_causal_workspace_bytes(nq, hq, hkv, d, n), dtype=torch.uint8, device=q.device)
     _need(workspace, "workspace", torch.uint8, 1)
+    if workspace.numel() == 0:
+        workspace = None
     _lib.call("rf_attend_causal", _ptr(q), q.stride(0), nq, _ptr(qpos), int(slot0), hq, d, _ptr(kbuf), _ptr(vbuf),
               hkv, kbuf.stride(0), kbuf.stride(1), n, float(scale), _ptr(out), out.stride(0), _ptr(workspace),
-              workspace.numel(), _stream(q))
+              0 if workspace is None else workspace.numel(), _stream(q))
     return out
 
 
@@ -363,11 +365,7 @@ def gdn_workspace_bytes(rows, nk, nv, dk=128, dv=128):
     return n.value
 
 
-def gdn_fill(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state, workspace=None):
-    """Gated DeltaNet fill from in-projection rows pre [P, >= C + 2 nv] (q | k | v | b | a): updates
-    state [nv, dk, dv] fp32 in place, returns the new conv state [3, C] bf16. workspace: uint8 device
-    memory for the per-chunk products (None: allocated for one pass over P rows; a smaller one, of at
-    least gdn_workspace_bytes(0, ...), makes several passes)."""
+def _gdn_check(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state):
     _need(pre, "pre", torch.bfloat16, 2)
     _need(conv_w, "conv_w", torch.bfloat16, 2)
     _need(a_log, "a_log", torch.float32, 1)
@@ -385,6 +383,15 @@ def gdn_fill(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state, worksp
         _need(conv_in, "conv_in", torch.bfloat16, 2)
         if tuple(conv_in.shape) != (3, C) or not conv_in.is_contiguous():
             raise ValueError("gdn_fill: conv state shape")
+    return C
+
+
+def gdn_fill(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state, workspace=None):
+    """Gated DeltaNet fill from in-projection rows pre [P, >= C + 2 nv] (q | k | v | b | a): updates
+    state [nv, dk, dv] fp32 in place, returns the new conv state [3, C] bf16. workspace: uint8 device
+    memory for the per-chunk products (None: allocated for one pass over P rows; a smaller one, of at
+    least gdn_workspace_bytes(0, ...), makes several passes)."""
+    C = _gdn_check(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state)
     if workspace is None:
         workspace = torch.empty(gdn_workspace_bytes(pre.shape[0], nk, nv, dk, dv), dtype=torch.uint8,
                                 device=pre.device)
@@ -394,6 +401,42 @@ def gdn_fill(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state, worksp
               _ptr(conv_out), _ptr(a_log), _ptr(dt_bias), _ptr(state), _ptr(workspace), workspace.numel(),
               _stream(pre))
     return conv_out
+
+
+class _GdnLayer(ctypes.Structure):
+    _fields_ = [("pre", ctypes.c_void_p), ("ld", ctypes.c_int64), ("conv_w", ctypes.c_void_p),
+                ("conv_in", ctypes.c_void_p), ("conv_out", ctypes.c_void_p), ("a_log", ctypes.c_void_p),
+                ("dt_bias", ctypes.c_void_p), ("state", ctypes.c_void_p)]
+
+
+GDN_BATCH_MAX = 2
+
+
+def gdn_fill_batch(layers, nk, nv, dk, dv, workspace=None):
+    """gdn_fill of up to GDN_BATCH_MAX independent layers over the same rows in one prep and one scan launch
+    per pass: layers = [(pre, conv_w, conv_in, a_log, dt_bias, state)] (as gdn_fill's arguments; states updated
+    in place). Returns their new conv states. Each is bit-identical to gdn_fill of that layer alone.
+    workspace: split evenly between the layers (None: one pass each)."""
+    n = len(layers)
+    if not 1 <= n <= GDN_BATCH_MAX:
+        raise ValueError(f"gdn_fill_batch: {n} layers (1 .. {GDN_BATCH_MAX})")
+    P = layers[0][0].shape[0]
+    arr = (_GdnLayer * n)()
+    outs = []
+    for j, (pre, conv_w, conv_in, a_log, dt_bias, state) in enumerate(layers):
+        C = _gdn_check(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state)
+        if pre.shape[0] != P:
+            raise ValueError("gdn_fill_batch: every layer takes the same rows")
+        conv_out = torch.empty(3, C, dtype=torch.bfloat16, device=pre.device)
+        outs.append(conv_out)
+        arr[j] = _GdnLayer(_ptr(pre), pre.stride(0), _ptr(conv_w), _ptr(conv_in), _ptr(conv_out), _ptr(a_log),
+                           _ptr(dt_bias), _ptr(state))
+    pre0 = layers[0][0]
+    if workspace is None:
+        workspace = torch.empty(n * gdn_workspace_bytes(P, nk, nv, dk, dv), dtype=torch.uint8, device=pre0.device)
+    _need(workspace, "workspace", torch.uint8, 1)
+    _lib.call("rf_gdn_fill_batch", arr, n, P, nk, nv, dk, dv, _ptr(workspace), workspace.numel(), _stream(pre0))
+    return outs
 
 
 def gdn_fill_noalloc(pre, nk, nv, dk, dv, conv_w, conv_in, a_log, dt_bias, state, conv_out=None):

@@ -72,6 +72,36 @@ def test_workspace_passes_are_bitwise_equal(dev):
                      torch.empty(ops.gdn_workspace_bytes(0, 2, 4) - 16, dtype=torch.uint8, device=dev))
 
 
+@pytest.mark.parametrize("chunks", [None, 3])
+def test_batched_layers_are_bitwise_their_single_fills(dev, chunks):
+    """rf_gdn_fill_batch over two layers (different weights, rows, carried conv and recurrent states) against
+    rf_gdn_fill of each alone: every state and conv state bit for bit, in one pass and in several (a workspace
+    of 3 chunks per layer)."""
+    from rfill import ops
+    cfg = gdn_config()
+    jobs, single = [], []
+    for seed in (5, 6):
+        om = OM.OracleModel(cfg, gdn_tensors(cfg, seed=seed), dtype=torch.bfloat16)
+        rows = _pre_rows(om, inputs(900, cfg["hidden_size"], seed=30 + seed)).to(dev)
+        w = om.W[0]
+        g = torch.Generator().manual_seed(seed)
+        st0 = (0.1 * torch.randn(4, 128, 128, generator=g)).to(dev)
+        conv_in = torch.randn(3, 2 * 2 * 128 + 4 * 128, generator=g).to(torch.bfloat16).to(dev)   # [3, C]
+        args = (w["conv"].to(dev).contiguous(), conv_in, w["A_log"].to(dev), w["dt_bias"].to(dev))
+        st = st0.clone()
+        conv = ops.gdn_fill(rows, 2, 4, 128, 128, *args, st)
+        single.append((st, conv))
+        jobs.append((rows, *args, st0.clone()))
+    ws = None if chunks is None else torch.empty(2 * chunks * ops.gdn_workspace_bytes(0, 2, 4), dtype=torch.uint8,
+                                                 device=dev)
+    convs = ops.gdn_fill_batch(jobs, 2, 4, 128, 128, ws)
+    torch.cuda.synchronize()
+    for (st, conv), job, cb in zip(single, jobs, convs):
+        assert torch.equal(job[5], st) and torch.equal(cb, conv)
+    with pytest.raises(ValueError, match="share"):
+        ops.gdn_fill_batch([jobs[0], jobs[0]], 2, 4, 128, 128)
+
+
 def test_fill_matches_oracle_and_continues(dev):
     """FillModel.fill (in-projection GEMM + GDN kernel) against the oracle's fill, then a second call
     continuing both states; plus the terminal-state correction st."""
@@ -101,6 +131,34 @@ def test_fill_matches_oracle_and_continues(dev):
     ref = om.new_cache()
     om.fill(0, x[:200], torch.arange(200), ref, st=st)
     assert rel_err(one[0]["rec"], ref[0]["rec"]) < STATE_TOL
+
+
+def test_fill_matches_the_full_projection_bitwise(dev):
+    """FillModel.fill projects q for the conv state's last 3 rows only; its states are bit-identical to
+    rf_gdn_fill on the whole in-projection, and FillModel.fill_batch over two layers to fill of each."""
+    from rfill import ops
+    from rfill.model import FillModel
+    cfg = gdn_config(layers=2)
+    m = FillModel(cfg, gdn_tensors(cfg, seed=7), dev)
+    x = inputs(777, cfg["hidden_size"], seed=23).to(dev)
+    ssq = ops.row_ssq(x)
+    c = m.new_cache()
+    m.fill(0, x, None, c, ssq=ssq)
+    w = m.W[0]
+    pre = ops.norm_linear(x, ssq, m.eps, w["w_in"])
+    st = torch.zeros(m.nv, m.dk, m.dv, dtype=torch.float32, device=dev)
+    conv = ops.gdn_fill(pre, m.nk, m.nv, m.dk, m.dv, w["conv"], None, w["a_log"], w["dt_bias"], st)
+    torch.cuda.synchronize()
+    assert torch.equal(c[0]["rec"], st) and torch.equal(c[0]["conv"], conv)
+    x2 = inputs(777, cfg["hidden_size"], seed=25).to(dev)
+    one, two = m.new_cache(), m.new_cache()
+    m.fill(0, x, None, one)
+    m.fill(1, x2, None, one)
+    m.fill_batch([0, 1], [x, x2], two)
+    torch.cuda.synchronize()
+    for i in (0, 1):
+        assert torch.equal(one[i]["rec"], two[i]["rec"]) and torch.equal(one[i]["conv"], two[i]["conv"])
+        assert one[i]["len"] == two[i]["len"] == 777
 
 
 def test_fill_c4_gdn_layer_shape(dev):
