@@ -68,31 +68,25 @@ def build_workload(dev):
     return cfg, w, model, arm
 
 
-def fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches, timer=None, overlap=False):
+def fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches, timer=None):
     """One step: the 16-layer fill (the hot path of finish() for the ridgefill arm, no exact rows),
-    scheduled as fill_late schedules it: each layer's map apply, then its fused K / V cache write, on the
-    current stream (rfill.kva.serial), or with overlap each layer's K / V write on a second stream beside
-    the next layer's map apply (rfill.kva.two_stream)."""
+    scheduled as fill_late schedules it (rfill.kva.serial with ATTN_GROUP): groups of consecutive late
+    layers, each group's maps in one launch (rf_map_apply_batch), then the group's fused norm + K / V + RoPE
+    cache writes in one launch (rf_norm_kv_write_batch), all on the current stream. Rows go to slot 0 of
+    caches sized once, so every step writes the same slots."""
     from rfill import ops
-    from rfill.kva import serial, two_stream
-    W, B = arm.projector._maps(b.device)
-
-    P, H = b.shape
-
-    def produce(i, slot):
-        ws = model.gemm_workspace(P, W[i].shape[0], H, b.device, "produce")
-        f = lambda: ops.map_apply(b, W[i], B[i], xbuf[slot], sbuf[slot], workspace=ws)    # noqa: E731
-        f() if timer is None else timer.run("rf_map_apply", f)
-
-    def consume(i, slot):
-        w, c = model.W[i], caches[i]
-        ws = model.gemm_workspace(P, w["wkv"].shape[0], H, b.device)
-        f = lambda: ops.norm_kv_write(xbuf[slot], sbuf[slot], model.eps, w["wkv"], model.n_kv,  # noqa: E731
-                                      model.head_dim, w.get("k_norm"), model.knorm_kind, cs, c["kbuf"],
-                                      c["vbuf"], 0, workspace=ws)
-        f() if timer is None else timer.run("rf_norm_kv_write", f)
-
-    (two_stream if overlap else serial)(range(arm.split, model.n_layers), produce, consume, b.device)
+    from rfill.kva import ATTN_GROUP
+    layers = list(range(arm.split, model.n_layers))
+    for g0 in range(0, len(layers), ATTN_GROUP):
+        ids = layers[g0:g0 + ATTN_GROUP]
+        n = len(ids)
+        f = lambda: arm.projector.apply_batch(ids, b, xbuf[:n], sbuf[:n])    # noqa: E731
+        f() if timer is None else timer.run("rf_map_apply_batch", f)
+        g = lambda: ops.norm_kv_write_batch(  # noqa: E731
+            xbuf[:n], sbuf[:n], model.eps, [model.W[i]["wkv"] for i in ids], model.n_kv, model.head_dim,
+            [model.W[i].get("k_norm") for i in ids], model.knorm_kind, cs, [caches[i]["kbuf"] for i in ids],
+            [caches[i]["vbuf"] for i in ids], 0)
+        g() if timer is None else timer.run("rf_norm_kv_write_batch", g)
 
 
 def ceilings(dev, P, H):
@@ -643,8 +637,6 @@ def main():
     ap.add_argument("--no-hybrid", action="store_true", help="skip the Gated-DeltaNet hybrid fill leg")
     ap.add_argument("--no-exact", action="store_true", help="skip the Qwen3-8B prompt-length sweep with exact rows")
     ap.add_argument("--no-finish", action="store_true", help="skip the whole-finish() leg (fill + exact tail)")
-    ap.add_argument("--overlap", action="store_true",
-                    help="run each layer's K / V write on a second stream beside the next layer's map apply")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py: this build measures one GPU only (one MI355X per box); --gpus must be 1", file=sys.stderr)
@@ -657,29 +649,31 @@ def main():
     b = w["h_split"][:P]
     pos = torch.arange(P, device=dev)
     cs = model.rope_table(pos)
-    xbuf = [torch.empty(P, H, dtype=torch.bfloat16, device=dev) for _ in range(2)]
-    sbuf = [torch.empty(P, H // 256, dtype=torch.float32, device=dev) for _ in range(2)]
+    from rfill.kva import ATTN_GROUP
+    xbuf = [torch.empty(P, H, dtype=torch.bfloat16, device=dev) for _ in range(ATTN_GROUP)]
+    sbuf = [torch.empty(P, H // 256, dtype=torch.float32, device=dev) for _ in range(ATTN_GROUP)]
     caches = model.new_cache()
     for i in w["layers"]:
         caches[i] = dict(kbuf=torch.empty(model.n_kv, P + 64, model.head_dim, dtype=torch.bfloat16, device=dev),
                          vbuf=torch.empty(model.n_kv, P + 64, model.head_dim, dtype=torch.bfloat16, device=dev), n=0)
     log(f"warmup {args.warmup} steps")
     for _ in range(args.warmup):
-        fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches, overlap=args.overlap)
+        fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches)
     torch.cuda.synchronize()
     log(f"timing {args.steps} steps")
     timer = KernelTimer()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for _ in range(args.steps):
-        fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches, timer, overlap=args.overlap)
+        fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches, timer)
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     L = len(w["layers"])
-    map_s, kv_s = timer.mean_s("rf_map_apply"), timer.mean_s("rf_norm_kv_write")
-    map_flop = 2 * P * H * H
-    kv_flop = 2 * P * H * 2 * model.n_kv * model.head_dim
-    step_flop = L * (map_flop + kv_flop)
+    # one launch covers ATTN_GROUP layers (L is a multiple of it here)
+    map_s, kv_s = timer.mean_s("rf_map_apply_batch"), timer.mean_s("rf_norm_kv_write_batch")
+    map_flop = 2 * P * H * H * ATTN_GROUP
+    kv_flop = 2 * P * H * 2 * model.n_kv * model.head_dim * ATTN_GROUP
+    step_flop = L * (map_flop + kv_flop) // ATTN_GROUP
     ms_step = elapsed / args.steps * 1e3
     out = {
         "metric": METRIC, "value": round(P * args.steps / elapsed, 1), "unit": "filled tokens/s", "n_gpus": 1,
@@ -688,15 +682,20 @@ def main():
         "config": {"workload": "llama-3.1-8b-shaped 32K fill: 16 late layers (split 16), 28672 filled rows, tail 4096",
                    "hidden": H, "kv_heads": model.n_kv, "head_dim": model.head_dim, "late_layers": L,
                    "seq_len": N_ROWS, "filled_rows": P, "parallelism": "none (1 GPU)"},
-        "roofline": {"kernel": "rf_map_apply", "bound": "mfma",
+        "roofline": {"kernel": "rf_map_apply_batch", "bound": "mfma",
                      "achieved": round(map_flop / map_s / 1e12, 1), "peak": PEAK_BF16 / 1e12, "unit": "TFLOP/s",
-                     "frac": round(map_flop / map_s / PEAK_BF16, 4), "traffic": traffic_from_profiles("rf_map_apply"),
-                     "flop_per_launch": map_flop, "mean_us": round(map_s * 1e6, 1)},
+                     "frac": round(map_flop / map_s / PEAK_BF16, 4),
+                     "traffic": traffic_from_profiles("rf_map_apply_batch"), "flop_per_launch": map_flop,
+                     "layers_per_launch": ATTN_GROUP, "mean_us": round(map_s * 1e6, 1),
+                     "mean_us_per_layer": round(map_s * 1e6 / ATTN_GROUP, 1)},
         "fill_mfma_frac": round(step_flop / (elapsed / args.steps) / PEAK_BF16, 4),
-        "kernels": {"rf_norm_kv_write": {"bound": "mfma", "mean_us": round(kv_s * 1e6, 1),
-                                         "achieved_tflops": round(kv_flop / kv_s / 1e12, 1),
-                                         "frac": round(kv_flop / kv_s / PEAK_BF16, 4), "flop_per_launch": kv_flop,
-                                         "traffic": traffic_from_profiles("rf_norm_kv_write")}},
+        "kernels": {"rf_norm_kv_write_batch": {"bound": "mfma", "mean_us": round(kv_s * 1e6, 1),
+                                               "mean_us_per_layer": round(kv_s * 1e6 / ATTN_GROUP, 1),
+                                               "layers_per_launch": ATTN_GROUP,
+                                               "achieved_tflops": round(kv_flop / kv_s / 1e12, 1),
+                                               "frac": round(kv_flop / kv_s / PEAK_BF16, 4),
+                                               "flop_per_launch": kv_flop,
+                                               "traffic": traffic_from_profiles("rf_norm_kv_write_batch")}},
     }
     if not args.no_extras:
         log("standalone RoPE + KV write and library ceilings")

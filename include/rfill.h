@@ -98,6 +98,29 @@ int rf_norm_kv_write(const uint16_t* x, int64_t ldx, const float* ssq, int64_t P
                      int64_t slot_begin, int64_t cap, void* workspace, size_t ws_bytes,
                      hipStream_t stream);
 
+/* ---- several late layers per launch (finish()'s fill loop, code/kva/kva.py:413-452, over a group of
+ * consecutive late layers: the maps of every layer read the same rows h_split[:P]) ---- */
+
+/* rf_map_apply for nl (1 .. 32) layers in one launch: x[l] = b w[l]^T + c[l] and ssq[l], each layer
+ * bit-identical to rf_map_apply of it alone without a workspace. w, c, x, ssq: host arrays of nl device
+ * pointers (c may be NULL, or hold NULL entries: no bias); one output row stride ldx for every layer.
+ * Needs h_in >= 128 besides rf_map_apply's conditions. Replaces kva.py:413-415 for each layer. */
+int rf_map_apply_batch(int nl, const uint16_t* b, int64_t ldb, const uint16_t* const* w, const uint16_t* const* c,
+                       uint16_t* const* x, int64_t ldx, float* const* ssq, int64_t P, int64_t h_in, int64_t h_out,
+                       hipStream_t stream);
+
+/* rf_norm_kv_write for nl (1 .. 32) attention layers in one launch over the same P rows: layer l's inputs
+ * x[l] (one row stride ldx) with statistics ssq[l], its weights wkv[l], k_norm gains knorm[l] (knorm NULL:
+ * none for any layer) and caches kbuf[l] / vbuf[l] (one shape and stride for every layer); eps, heads, the
+ * RoPE table cs and the slots [slot_begin, slot_begin + P) shared. Each layer's K / V are bit-identical to
+ * rf_norm_kv_write of it alone without a workspace. Needs H <= 8192 besides rf_norm_kv_write's conditions.
+ * Replaces Model.fill (code/kva/model.py:278-280) of each layer. */
+int rf_norm_kv_write_batch(int nl, const uint16_t* const* x, int64_t ldx, const float* const* ssq, int64_t P,
+                           int64_t H, float eps, const uint16_t* const* wkv, int hkv, int d,
+                           const uint16_t* const* knorm, int knorm_kind, const uint16_t* cs, int rot,
+                           uint16_t* const* kbuf, uint16_t* const* vbuf, int64_t head_stride, int64_t row_stride,
+                           int64_t slot_begin, int64_t cap, hipStream_t stream);
+
 /* RoPE on given pre-RoPE K and the K / V cache write of m rows.
  * Replaces Model.fill_kv (code/kva/model.py:161-165): ops.apply_rope (ops.py:66-77) + _append_kv.
  * k / v: [m, hkv, d] with token strides ld_k / ld_v (a head's d values contiguous, heads d apart);

@@ -846,7 +846,547 @@ __global__ __launch_bounds__(NTHR) void k_gram(const uint16_t* __restrict__ A, i
   }
 }
 
+// ---- Persistent tiles: one block per CU runs a sequence of output tiles over one continuous ring of K
+// steps, so the next tile's first operand steps load while this tile finishes (no pipeline fill and no
+// block dispatch per tile), and a launch can hold the tiles of several layers (no tail per layer).
+//
+// The ring is the one of mainloop, indexed by a global step g that runs on across tiles (slot of quarter
+// q: (4 g + q) % 10). In a tile's last step the weight quarters of step g + 2 (the next tile's step 1) are
+// not loaded during slice 3: the epilogue of the tile runs first, in the four slots of that last step
+// (two activation slots, 32 KiB contiguous, for a 64-row image; a weight slot for per-tile side data),
+// which nothing loads into until those deferred loads, issued after the epilogue's closing barrier. They
+// still have three slices before the barrier that needs them, as in the steady loop. The MFMA k order
+// and the epilogue arithmetic are those of the per-tile kernels, so the results are bit-identical.
+
+// Buffer resources of one tile's operands: activation rows m0 .. (range-checked past the tile's rows) and
+// the tile's 256 weight rows.
+struct TileOps {
+  __amdgpu_buffer_rsrc_t rx, rw;
+};
+
+__device__ __forceinline__ void issue_load_at(__amdgpu_buffer_rsrc_t rs, uint32_t voff, int slot, int kstep, int i,
+                                              char* lds, int w) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds + slot * (SLOT_U4 * 16) + (32 * w + 8 * i) * (CPR * 16)),
+                                           16, voff, kstep * BK * 2, 0, 0);
+}
+
+// This block's tiles of T logical tiles: first + stride * i for i < cnt. With 256 blocks (T >= 256) XCD x
+// (blocks x, x + 8, ...) takes a contiguous eighth of the logical order and its 32 blocks walk it 32 tiles
+// at a time, so the tiles an XCD runs together form GROUP_M x 8 groups as in the per-tile kernels. With
+// fewer tiles than 256, one tile per block (xcd_tile order).
+struct Share {
+  int first, stride, cnt;
+};
+__device__ __forceinline__ Share block_share(int T) {
+  if (static_cast<int>(gridDim.x) < 256) return Share{xcd_tile(blockIdx.x, gridDim.x), 0, 1};
+  const int x = blockIdx.x & 7, c = blockIdx.x >> 3;
+  const int q = T >> 3, r = T & 7;
+  const int lo = x * q + min(x, r), size = q + (x < r ? 1 : 0);
+  return Share{lo + c, 32, c < size ? (size - c + 31) / 32 : 0};
+}
+
+int persistent_grid(int64_t tiles) { return static_cast<int>(std::min<int64_t>(tiles, 256)); }
+
+// Tile row of row ir (0..63) of epilogue round r's image: image rows 0..31 are tile rows r*32 .. r*32 + 31
+// (waves wm = 0), rows 32..63 tile rows 128 + r*32 .. (wm = 1).
+__device__ __forceinline__ int round_row(int ir, int r) { return (ir >> 5) * 128 + r * 32 + (ir & 31); }
+
+// threadIdx.x as a value the compiler cannot move: the epilogues derive their lane arithmetic from it, so
+// that arithmetic stays in the epilogue instead of being hoisted out of the tile loop and kept live (in
+// registers the main loop needs) across every K step.
+__device__ __forceinline__ int pinned_tid() {
+  int t = static_cast<int>(threadIdx.x);
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
+// One accumulator element read out of its AGPR where it is used (the compiler otherwise copies whole
+// accumulator vectors into VGPRs ahead of the epilogue, more registers than the tile loop has spare).
+__device__ __forceinline__ float agpr_read(float a) {
+  float v;
+  asm volatile("v_accvgpr_read_b32 %0, %1" : "=v"(v) : "a"(a));
+  return v;
+}
+
+// Epilogue round r (compile-time MT = r): the wave's rows wm*128 + r*32 + lr, rounded to bf16 by value(nt, g,
+// e, acc), into a 64-row image (row wm*32 + lr; row i's chunk c at i * 32 + (c ^ (i & 31))). With SSQ, ss
+// receives the sum of squares of the lane's 64 rounded values in (nt, g, e) order, as stage_tile forms it.
+template <int MT, bool SSQ, class F>
+__device__ __forceinline__ void stage_round(uint4* img, const f32x16 (&acc)[4][4], F value, float& ss, int t) {
+  const int lane = t & 63, w = t >> 6;
+  const int wm = w >> 1, wn = w & 1, lr = lane & 31, lk = lane >> 5;
+  char* base = reinterpret_cast<char*>(img);
+  const int row = wm * 32 + lr;
+  float sq = 0.f;
+#pragma unroll
+  for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int c0 = wn * 128 + nt * 32 + 8 * g + 4 * lk;
+      const uint32_t p0 = bf16_pair(value(nt, g, 0, agpr_read(acc[nt][MT][4 * g + 0])),
+                                    value(nt, g, 1, agpr_read(acc[nt][MT][4 * g + 1])));
+      const uint32_t p1 = bf16_pair(value(nt, g, 2, agpr_read(acc[nt][MT][4 * g + 2])),
+                                    value(nt, g, 3, agpr_read(acc[nt][MT][4 * g + 3])));
+      if (SSQ) {
+        const float r0 = bf_lo(p0), r1 = bf_hi(p0), r2 = bf_lo(p1), r3 = bf_hi(p1);
+        sq = fmaf(r0, r0, sq);
+        sq = fmaf(r1, r1, sq);
+        sq = fmaf(r2, r2, sq);
+        sq = fmaf(r3, r3, sq);
+      }
+      const int off = row * 512 + (((c0 >> 3) ^ (row & 31)) << 4) + ((c0 & 7) << 1);
+      *reinterpret_cast<uint2*>(base + off) = make_uint2(p0, p1);
+    }
+  ss = sq;
+}
+
+// Runs this block's tiles 0 .. cnt - 1 (cnt >= 1; every tile K = nk * 64 deep, nk >= 2): ops(i) gives tile
+// i's operand resources; begin(i, acc) sets its accumulators' starting values; end(i, acc, img, side) is its
+// epilogue, with img (32 KiB) and side (32 KiB) of LDS to itself. end must finish with a barrier after
+// every wave's last LDS access. pre(i, side) runs in tile i's last K step as soon as side is free (after
+// that step's barrier, one slice before the epilogue): loads it issues into side land during that slice.
+template <class Ops, class Begin, class Pre, class End>
+__device__ __forceinline__ void stream_tiles(int cnt, int nk, int64_t ldx, int64_t ldw, Ops ops, Begin begin, Pre pre,
+                                             End end, uint4* lds) {
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = w >> 1, wn = w & 1;
+  uint32_t vx[2][4], vw[2][4];
+#pragma unroll
+  for (int h = 0; h < 2; ++h)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 32 * w + 8 * i + (lane >> 3);
+      const int ch = (lane & 7) ^ slot_swz(r);
+      vx[h][i] = static_cast<uint32_t>(((h * 128 + r) * ldx + ch * 8) * 2);
+      vw[h][i] = static_cast<uint32_t>(((h * 128 + r) * ldw + ch * 8) * 2);
+    }
+  char* base = reinterpret_cast<char*>(lds);
+  const int lr = lane & 31, lk = lane >> 5, swz = slot_swz(lr);
+  bf16x8 fx[2][4], fw[2][4];
+  f32x16 acc[4][4];
+  TileOps cur = ops(0);
+  TileOps nxt = cnt > 1 ? ops(1) : cur;
+
+  // fragment r (0..7) of slice ks of global step g: r < 4 -> weight block r, else activation block r - 4
+  auto read_one = [&](int g, int ks, int r, bf16x8 (&ax)[4], bf16x8 (&aw)[4]) {
+    const int ch = (ks * 2 + lk) ^ swz;
+    if (r < 4) aw[r] = as_frag(lds[slot_of(g, 2 + wn) * SLOT_U4 + (r * 32 + lr) * CPR + ch]);
+    else ax[r - 4] = as_frag(lds[slot_of(g, wm) * SLOT_U4 + ((r - 4) * 32 + lr) * CPR + ch]);
+  };
+  // load j (0..7) of global step g's activation (wt = false) or weight quarters: tile-local step k of o
+  auto load = [&](const TileOps& o, int g, int k, bool wt, int j) {
+    const int h = j >> 2, i = j & 3;
+    if (wt) issue_load_at(o.rw, vw[h][i], slot_of(g, 2 + h), k, i, base, w);
+    else issue_load_at(o.rx, vx[h][i], slot_of(g, h), k, i, base, w);
+  };
+  // as mainloop's slice, with the loads' source o, global step lg and tile-local step lk2
+  auto slice = [&](const bf16x8 (&ax)[4], const bf16x8 (&aw)[4], bool rd, int rg, int rks, bf16x8 (&nx)[4],
+                   bf16x8 (&nw)[4], int ld, const TileOps& o, int lg, int lk2, int lo) {
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      acc[q >> 2][q & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aw[q >> 2], ax[q & 3], acc[q >> 2][q & 3], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if (q < 8 && rd) read_one(rg, rks, q, nx, nw);
+      if (ld == 2 && !(q & 1)) load(o, lg, lk2, true, q >> 1);
+      if (ld == 1 && (q & 3) == 1) load(o, lg, lk2, false, lo + (q >> 2));
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+  // global step g; the loads of step g + 2 (source o2, tile-local step k2) when `has2`; its weight
+  // quarters in slice 3 unless `defer`; `has1`: step g + 1 exists (its first fragments are read)
+  // (`defer` marks a tile's last step: its weight slots, free after the barrier, go to pre(i, ...))
+  auto step = [&](int g, const TileOps& o2, int k2, auto has2, auto defer, bool has1, int i) {
+    slice(fx[0], fw[0], true, g, 1, fx[1], fw[1], has2 ? 1 : 0, o2, g + 2, k2, 0);
+    slice(fx[1], fw[1], true, g, 2, fx[0], fw[0], has2 ? 1 : 0, o2, g + 2, k2, 4);
+    slice(fx[0], fw[0], true, g, 3, fx[1], fw[1], 0, o2, 0, 0, 0);
+    if (has2) wait_vm_lgkm0<8>();
+    else wait_vm_lgkm0<0>();
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    if (defer) {
+      pre(i, lds + slot_of(g, 2) * SLOT_U4);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    slice(fx[1], fw[1], has1, g + 1, 0, fx[0], fw[0], (has2 && !defer) ? 2 : 0, o2, g + 2, k2, 0);
+  };
+
+  // prologue: steps 0 and 1 of tile 0, then the accumulators and step 0's first fragments
+  for (int j = 0; j < 8; ++j) load(cur, 0, 0, false, j);
+  for (int j = 0; j < 8; ++j) load(cur, 0, 0, true, j);
+  for (int j = 0; j < 8; ++j) load(cur, 1, 1, false, j);
+  for (int j = 0; j < 8; ++j) load(cur, 1, 1, true, j);
+  begin(0, acc);
+  wait_vm_lgkm0<16>();
+  __builtin_amdgcn_s_barrier();
+  for (int r = 0; r < 8; ++r) read_one(0, 0, r, fx[0], fw[0]);
+  int g = 0;
+  for (int i = 0; i < cnt; ++i) {
+    const bool more = i + 1 < cnt;
+    for (int kt = 0; kt + 2 < nk; ++kt, ++g) step(g, cur, kt + 2, std::true_type{}, std::false_type{}, true, i);
+    // the tile's last two steps: step g + 2 is the next tile's step 0, then its step 1
+    step(g, nxt, 0, more, std::false_type{}, true, i);
+    ++g;
+    step(g, nxt, 1, more, std::true_type{}, false, i);
+    ++g;
+    // g is the next tile's first step (landed: the last barrier waited for it); step g - 1 left its four
+    // slots free: activation slots (img) and weight slots (side), each pair contiguous. The next tile's first fragments are read after the epilogue, so that they do not hold
+    // registers through it.
+    end(i, acc, lds + slot_of(g - 1, 0) * SLOT_U4, reinterpret_cast<float*>(lds + slot_of(g - 1, 2) * SLOT_U4));
+    if (more) {
+      for (int j = 0; j < 8; ++j) load(nxt, g + 1, 1, true, j);   // the deferred weight quarters of its step 1
+      cur = nxt;
+      if (i + 2 < cnt) nxt = ops(i + 2);
+      begin(i + 1, acc);
+      for (int r = 0; r < 8; ++r) read_one(g, 0, r, fx[0], fw[0]);
+    }
+  }
+  wait_vm_lgkm0<0>();
+}
+
+// Per-layer operands of a batched launch (one launch for the fill of several late layers: every layer
+// reads the same rows b, and has its own map, bias, output rows and statistics).
+constexpr int MAXL = 32;
+struct MapLayers {
+  const uint16_t* w[MAXL];
+  const uint16_t* c[MAXL];
+  uint16_t* x[MAXL];
+  float* ssq[MAXL];
+};
+
+// rf_map_apply on persistent tiles, for nl layers at once: x_l = b W_l^T + c_l, the accumulators starting
+// at the bias, and the rows' sum-of-squares partials; logical tile u is layer u / (tiles of a layer).
+__global__ __launch_bounds__(NTHR) void k_map_apply_p(const uint16_t* __restrict__ B, int64_t ldb, MapLayers ml, int nl,
+                                                      int64_t ldx, int M, int N, int K) {
+  __shared__ uint4 lds[LDS_U4];
+  const int tiles_n = N / BN, tiles_m = (M + BM - 1) / BM, per = tiles_m * tiles_n;
+  const Share sh = block_share(nl * per);
+  if (sh.cnt == 0) return;
+  const int t = threadIdx.x, lane = t & 63, wn = (t >> 6) & 1, lk = lane >> 5;
+  auto coords = [&](int i, int& l, int& tm, int& tn) {
+    const int u = sh.first + i * sh.stride;
+    l = u / per;
+    tile_coords(u - l * per, tiles_m, tiles_n, tm, tn);
+  };
+  auto ops = [&](int i) {
+    int l, tm, tn;
+    coords(i, l, tm, tn);
+    const int m0 = tm * BM;
+    return TileOps{buffer_rsrc(B + static_cast<int64_t>(m0) * ldb, static_cast<uint32_t>(min(M - m0, BM) * ldb * 2)),
+                   buffer_rsrc(ml.w[l] + static_cast<int64_t>(tn) * BN * K, static_cast<uint32_t>(BN * K * 2))};
+  };
+  // bias of the next tile to begin: lane (lr, lk) holds columns wn*128 + nt*32 + 8g + 4lk + e
+  uint2 bq[4][4];
+  auto load_bias = [&](int i) {
+    int l, tm, tn;
+    coords(i, l, tm, tn);
+    const uint16_t* c = ml.c[l];
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        bq[nt][g] = c ? *reinterpret_cast<const uint2*>(c + tn * BN + wn * 128 + nt * 32 + 8 * g + 4 * lk)
+                      : make_uint2(0u, 0u);
+  };
+  auto begin = [&](int, f32x16 (&acc)[4][4]) {
+#pragma unroll
+    for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float b0 = bf_lo(bq[nt][g].x), b1 = bf_hi(bq[nt][g].x), b2 = bf_lo(bq[nt][g].y), b3 = bf_hi(bq[nt][g].y);
+#pragma unroll
+        for (int mt = 0; mt < 4; ++mt) {
+          acc[nt][mt][4 * g + 0] = b0;
+          acc[nt][mt][4 * g + 1] = b1;
+          acc[nt][mt][4 * g + 2] = b2;
+          acc[nt][mt][4 * g + 3] = b3;
+        }
+      }
+  };
+  auto end = [&](int i, const f32x16 (&acc)[4][4], uint4* img, float* side) {
+    int l, tm, tn;
+    coords(i, l, tm, tn);
+    const int t = pinned_tid(), lane = t & 63, w = t >> 6, wm = w >> 1, wn = w & 1, lr = lane & 31, lk = lane >> 5;
+    const int m0 = tm * BM, n0 = tn * BN, ch = t & 31;
+    uint16_t* X = ml.x[l];
+    float* S = ml.ssq[l];
+    if (i + 1 < sh.cnt) load_bias(i + 1);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      __builtin_amdgcn_sched_barrier(0);
+      float ss = 0.f;
+      auto ident = [](int, int, int, float a) { return a; };
+      switch (r) {
+        case 0: stage_round<0, true>(img, acc, ident, ss, t); break;
+        case 1: stage_round<1, true>(img, acc, ident, ss, t); break;
+        case 2: stage_round<2, true>(img, acc, ident, ss, t); break;
+        default: stage_round<3, true>(img, acc, ident, ss, t); break;
+      }
+      const float tot = ss + __shfl_xor(ss, 32, 64);             // the row's 128 columns of this wave
+      if (lk == 0) side[wn * 64 + wm * 32 + lr] = tot;
+      __syncthreads();
+      if (t < 64) {
+        const int gm = m0 + round_row(t, r);
+        if (gm < M) S[static_cast<int64_t>(gm) * tiles_n + tn] = side[t] + side[64 + t];
+      }
+#pragma unroll 4
+      for (int it = 0; it < 8; ++it) {
+        const int ir = it * 8 + (t >> 5);
+        const int gm = m0 + round_row(ir, r);
+        if (gm < M) *reinterpret_cast<uint4*>(X + static_cast<int64_t>(gm) * ldx + n0 + ch * 8) = image_chunk(img, ir, ch);
+      }
+      __syncthreads();
+    }
+  };
+  load_bias(0);
+  stream_tiles(sh.cnt, K / BK, ldb, K, ops, begin, [](int, uint4*) {}, end, lds);
+}
+
+// Per-layer operands of a batched K / V fill.
+struct KvLayers {
+  const uint16_t* x[MAXL];
+  const float* ssq[MAXL];
+  const uint16_t* wkv[MAXL];
+  const uint16_t* knorm[MAXL];
+  uint16_t* kbuf[MAXL];
+  uint16_t* vbuf[MAXL];
+};
+
+// Input RMSNorm scale 1 / sqrt(mean(x^2) + eps) of row gm from its nparts (<= 32) partials, summed in order
+// (as row_scale). row_parts32 issues the loads (all before any use, so one wait covers them), parts_scale
+// sums them.
+__device__ __forceinline__ void row_parts32(const float* __restrict__ ssq, int nparts, int M, int gm, float (&p)[32]) {
+  const float* q = ssq + static_cast<int64_t>(gm < M ? gm : 0) * nparts;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) p[i] = q[i < nparts ? i : nparts - 1];     // unconditional loads: no branches
+#pragma unroll
+  for (int i = 0; i < 32; ++i) p[i] = i < nparts ? p[i] : 0.f;
+}
+__device__ __forceinline__ float parts_scale(const float (&p)[32], float width, float eps) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 32; ++i) s += p[i];
+  return 1.0f / sqrtf(s / width + eps);
+}
+
+// Epilogue round r of a K / V tile: fetch(r) the RoPE entries of its rows (K tiles), the image's row pass.
+// Row pass of K columns only (slot-indexed rows): image rows u*8 + t/32 (u < 8), chunk t % 32; the rows'
+// RoPE entries `re` were fetched a round earlier.
+template <int MODE>
+__device__ __forceinline__ void k_round(const KvArgs& a, const KvLane& L, const uint4* img, int r, int m0, int M,
+                                        const RopeEnt (&re)[8], int t) {
+  const int ch = t & 31;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {                   // two halves of 4 rows: fewer temporaries live at once
+    uint4 o[4];
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const int u = h * 4 + v4, ir = u * 8 + (t >> 5);
+      const uint4 v = image_chunk(img, ir, ch);
+      const bool half8 = MODE == KV_ANY ? L.half >= 8 : true;
+      const uint4 pv = half8 ? image_chunk(img, ir, ch + (L.pj0 - L.j0) / 8) : v;
+      const float ss = head_ssq<MODE>(a, L, v);
+      o[v4] = (MODE != KV_ANY || L.norm || L.rope) ? k_chunk<MODE>(a, L, v, pv, ss, re[u]) : v;
+    }
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const int gm = m0 + round_row((h * 4 + v4) * 8 + (t >> 5), r);
+      if (gm < M) st_stream16(L.dst0 + (a.slot0 + gm) * a.row_stride, o[v4]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+__device__ __forceinline__ void rope_round(const KvArgs& a, const KvLane& L, int r, int m0, int M, RopeEnt (&re)[8],
+                                           int t) {
+#pragma unroll
+  for (int u = 0; u < 8; ++u) re[u] = rope_fetch_ahead(a, L, m0 + round_row(u * 8 + (t >> 5), r), M);
+}
+
+// RoPE table rows of epilogue round r for a d 128, full-rotary K tile (256-byte rows: 64 cos, then 64 sin
+// values) from the table cs (resource rcs, slot-indexed rows < M) straight into LDS at tab (16 KiB, row ir
+// at ir * 256): 4 loads per wave, 4 rows of 16 lanes each. Rows past M read row M - 1 (never stored).
+__device__ __forceinline__ void table_round(__amdgpu_buffer_rsrc_t rcs, int r, int m0, int M, uint4* tab, int t) {
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const int ir = w * 16 + k * 4 + (lane >> 4);
+    const int gm = min(m0 + round_row(ir, r), M - 1);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rcs, (lds_ptr)(tab + (w * 16 + k * 4) * 16), 16,
+                                             static_cast<uint32_t>(gm * 256 + (lane & 15) * 16), 0, 0, 0);
+  }
+}
+
+// Row pass of epilogue round r for a d 128, full-rotary K tile with its RoPE entries in LDS (tab, as
+// table_round lays them out): image rows u*8 + t/32 (u < 8, in two halves of 4), chunk t % 32.
+template <int MODE>
+__device__ __forceinline__ void k_round_tab(const KvArgs& a, const KvLane& L, const uint4* img, const uint4* tab, int r,
+                                            int m0, int M, int t) {
+  const int ch = t & 31, fc = L.fi0 >> 3;
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    uint4 o[4];
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const int ir = (h * 4 + v4) * 8 + (t >> 5);
+      const uint4 v = image_chunk(img, ir, ch);
+      const uint4 pv = image_chunk(img, ir, ch + (L.pj0 - L.j0) / 8);
+      const float ss = head_ssq<MODE>(a, L, v);
+      const RopeEnt re{tab[ir * 16 + fc], tab[ir * 16 + 8 + fc]};
+      o[v4] = k_chunk<MODE>(a, L, v, pv, ss, re);
+    }
+#pragma unroll
+    for (int v4 = 0; v4 < 4; ++v4) {
+      const int gm = m0 + round_row((h * 4 + v4) * 8 + (t >> 5), r);
+      if (gm < M) st_stream16(L.dst0 + (a.slot0 + gm) * a.row_stride, o[v4]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// rf_norm_kv_write on persistent tiles for nl layers at once (slot-indexed rows, no position array). The
+// base arguments `a0` carry what the layers share (norm width, eps, heads, RoPE table, strides, first
+// slot); the layer's statistics, weights, k_norm gains and cache buffers come from kl. KMODE is the K
+// tiles' epilogue (one per launch: it follows from the configuration). For d 128 with full rotary
+// (KV_D128, KV_D128_KNORM) a K tile's RoPE entries go from the table into LDS, one round ahead, in the
+// two weight slots of its last K step (the first two rounds' from the tile's last step on, pre); with
+// KV_ANY they are loaded into registers as each round starts. V tiles copy; tiles holding K and V
+// columns (KV_ANY only) go chunk by chunk.
+template <int KMODE>
+__global__ __launch_bounds__(NTHR) void k_norm_kv_p(KvLayers kl, int nl, int64_t ldx, int M, int N, int K, KvArgs a0) {
+  __shared__ uint4 lds[LDS_U4];
+  const int tiles_n = N / BN, tiles_m = (M + BM - 1) / BM, per = tiles_m * tiles_n;
+  const Share sh = block_share(nl * per);
+  if (sh.cnt == 0) return;
+  const int t = threadIdx.x;
+  constexpr bool TAB = KMODE != KV_ANY;
+  auto coords = [&](int i, int& l, int& tm, int& tn) {
+    const int u = sh.first + i * sh.stride;
+    l = u / per;
+    tile_coords(u - l * per, tiles_m, tiles_n, tm, tn);
+  };
+  auto ops = [&](int i) {
+    int l, tm, tn;
+    coords(i, l, tm, tn);
+    const int m0 = tm * BM;
+    return TileOps{buffer_rsrc(kl.x[l] + static_cast<int64_t>(m0) * ldx, static_cast<uint32_t>(min(M - m0, BM) * ldx * 2)),
+                   buffer_rsrc(kl.wkv[l] + static_cast<int64_t>(tn) * BN * K, static_cast<uint32_t>(BN * K * 2))};
+  };
+  auto parts_of = [&](int i, float (&p)[32]) {
+    int l, tm, tn;
+    coords(i, l, tm, tn);
+    row_parts32(kl.ssq[l], a0.nparts, M, tm * BM + t, p);
+  };
+  float my_rs;                    // row t of the current tile
+  {
+    float p[32];
+    parts_of(0, p);
+    my_rs = parts_scale(p, a0.h, a0.eps);
+  }
+  auto begin = [&](int, f32x16 (&acc)[4][4]) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[p][q][r] = 0.f;
+  };
+  const int kw = a0.hkv * a0.d;
+  auto pre = [&](int i, uint4* side) {
+    int l, tm, tn;
+    coords(i, l, tm, tn);
+    if (TAB && tn * BN + BN <= kw) {
+      const int tp = pinned_tid();
+      const __amdgpu_buffer_rsrc_t rcs = buffer_rsrc(a0.cs, static_cast<uint32_t>(M) * 256u);
+      table_round(rcs, 0, tm * BM, M, side, tp);
+      table_round(rcs, 1, tm * BM, M, side + SLOT_U4, tp);
+    }
+  };
+  auto end = [&](int i, const f32x16 (&acc)[4][4], uint4* img, float* side_f) {
+    int l, tm, tn;
+    coords(i, l, tm, tn);
+    const int t = pinned_tid(), lane = t & 63, wm = t >> 7;
+    const int m0 = tm * BM, n0 = tn * BN, ch = t & 31;
+    const bool more = i + 1 < sh.cnt;
+    uint4* side = reinterpret_cast<uint4*>(side_f);
+    KvArgs a = a0;
+    a.ssq = kl.ssq[l];
+    a.knorm = kl.knorm[l];
+    a.kbuf = kl.kbuf[l];
+    a.vbuf = kl.vbuf[l];
+    const KvLane L(a, n0, ch);
+    // 1: K columns only; 4: V columns only; 5: both
+    const int mode = n0 + BN <= kw ? 1 : (n0 >= kw || KMODE != KV_ANY) ? 4 : 5;
+    const bool tab = TAB && mode == 1;
+    // the rows' norm scales, through the image area (free until round 0 is staged)
+    float* rsx = reinterpret_cast<float*>(img);
+    rsx[t] = my_rs;
+    __syncthreads();
+    float rs[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) rs[mt] = rsx[wm * 128 + mt * 32 + (lane & 31)];
+    __syncthreads();
+    const __amdgpu_buffer_rsrc_t rcs = buffer_rsrc(a0.cs, static_cast<uint32_t>(M) * 256u);
+    float p[32];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      __builtin_amdgcn_sched_barrier(0);
+      RopeEnt re[8];
+      if (!TAB && mode == 1) rope_round(a, L, r, m0, M, re, t);   // in flight while the round is staged
+      if (r == 3 && more) parts_of(i + 1, p);
+      float unused;
+      switch (r) {
+        case 0: stage_round<0, false>(img, acc, [&](int, int, int, float v) { return v * rs[0]; }, unused, t); break;
+        case 1: stage_round<1, false>(img, acc, [&](int, int, int, float v) { return v * rs[1]; }, unused, t); break;
+        case 2: stage_round<2, false>(img, acc, [&](int, int, int, float v) { return v * rs[2]; }, unused, t); break;
+        default: stage_round<3, false>(img, acc, [&](int, int, int, float v) { return v * rs[3]; }, unused, t); break;
+      }
+      if (tab) __builtin_amdgcn_s_waitcnt(0x0f70);      // vmcnt(0): this round's table rows are in LDS
+      __syncthreads();
+      if (mode == 1) {
+        if (TAB) k_round_tab<KMODE>(a, L, img, side + (r & 1) * SLOT_U4, r, m0, M, t);
+        else k_round<KV_ANY>(a, L, img, r, m0, M, re, t);
+      } else if (mode == 4) {
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+          const int ir = it * 8 + (t >> 5);
+          const int gm = m0 + round_row(ir, r);
+          if (gm < M) st_stream16(L.dst0 + (a.slot0 + gm) * a.row_stride, image_chunk(img, ir, ch));
+        }
+      } else if (KMODE == KV_ANY) {
+        for (int it = 0; it < 8; ++it) {
+          const int ir = it * 8 + (t >> 5);
+          const int gm = m0 + round_row(ir, r);
+          kv_chunk_row(a, L, [&](int c) { return image_chunk(img, ir, c); }, ch, gm, gm < M,
+                       rope_fetch(a, L, gm, gm < M));
+        }
+      }
+      __syncthreads();
+      if (tab && r + 2 < 4) table_round(rcs, r + 2, m0, M, side + (r & 1) * SLOT_U4, t);
+    }
+    if (more) my_rs = parts_scale(p, a0.h, a0.eps);
+  };
+  stream_tiles(sh.cnt, K / BK, ldx, K, ops, begin, pre, end, lds);
+}
+
 int grid_of(int64_t M, int64_t N) { return static_cast<int>(((M + BM - 1) / BM) * (N / BN)); }
+
+// The persistent K / V kernel for nl layers of M rows; the K epilogue's compile-time mode from the
+// configuration in a (d 128 with full rotary: without k_norm, or with Llama-style k_norm; anything else).
+void launch_norm_kv_p(const KvLayers& kl, int nl, int64_t ldx, int64_t M, int64_t N, int64_t K, const KvArgs& a,
+                      hipStream_t stream) {
+  const dim3 grid(persistent_grid(nl * static_cast<int64_t>(grid_of(M, N)))), block(NTHR);
+  const bool d128 = a.d == 128 && a.rot == 128 && M * 256 < (1ll << 32);   // table offsets fit 32 bits
+  if (d128 && !a.knorm)
+    hipLaunchKernelGGL(k_norm_kv_p<KV_D128>, grid, block, 0, stream, kl, nl, ldx, static_cast<int>(M),
+                       static_cast<int>(N), static_cast<int>(K), a);
+  else if (d128 && a.knorm_kind == 0)
+    hipLaunchKernelGGL(k_norm_kv_p<KV_D128_KNORM>, grid, block, 0, stream, kl, nl, ldx, static_cast<int>(M),
+                       static_cast<int>(N), static_cast<int>(K), a);
+  else
+    hipLaunchKernelGGL(k_norm_kv_p<KV_ANY>, grid, block, 0, stream, kl, nl, ldx, static_cast<int>(M),
+                       static_cast<int>(N), static_cast<int>(K), a);
+}
 
 // K splits for an M x N x K product: enough blocks to give every CU one (256), at least 512 of K per
 // split, at most 16 splits; 1 when the tiles alone fill the GPU.
@@ -936,9 +1476,18 @@ extern "C" int rf_map_apply(const uint16_t* b, int64_t ldb, const uint16_t* w, c
   if (P == 0) return RF_OK;
   const Plan pl = plan_with(P, h_out, h_in, workspace, ws_bytes);
   const int64_t mf = pl.m_fused, rows = P - mf;
-  if (mf > 0)
+  if (mf > 0 && h_in / BK >= 2) {
+    MapLayers ml{};
+    ml.w[0] = w;
+    ml.c[0] = c;
+    ml.x[0] = x;
+    ml.ssq[0] = ssq;
+    hipLaunchKernelGGL(k_map_apply_p, dim3(persistent_grid(grid_of(mf, h_out))), dim3(NTHR), 0, stream, b, ldb, ml, 1,
+                       ldx, static_cast<int>(mf), static_cast<int>(h_out), static_cast<int>(h_in));
+  } else if (mf > 0) {
     hipLaunchKernelGGL(k_map_apply, dim3(grid_of(mf, h_out)), dim3(NTHR), 0, stream, b, ldb, w, c, x, ldx, ssq,
                        static_cast<int>(mf), static_cast<int>(h_out), static_cast<int>(h_in));
+  }
   if (pl.splits > 1) {
     launch_partials(b, ldb, w, h_in, P, h_out, h_in, pl, workspace, stream);
     hipLaunchKernelGGL(k_map_apply_reduce, reduce_grid(rows, h_out), dim3(256), 0, stream,
@@ -981,9 +1530,19 @@ extern "C" int rf_norm_kv_write(const uint16_t* x, int64_t ldx, const float* ssq
   if (workspace && !aligned16(workspace)) return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write: workspace alignment");
   const Plan pl = plan_with(P, N, H, workspace, ws_bytes);
   const int64_t mf = pl.m_fused, rows = P - mf;
-  if (mf > 0)
+  if (mf > 0 && H / BK >= 2 && H / SSQ_COLS <= 32) {
+    KvLayers kl{};
+    kl.x[0] = x;
+    kl.ssq[0] = ssq;
+    kl.wkv[0] = wkv;
+    kl.knorm[0] = knorm;
+    kl.kbuf[0] = kbuf;
+    kl.vbuf[0] = vbuf;
+    launch_norm_kv_p(kl, 1, ldx, mf, N, H, a, stream);
+  } else if (mf > 0) {
     hipLaunchKernelGGL(k_norm_kv, dim3(grid_of(mf, N)), dim3(NTHR), 0, stream, x, ldx, wkv, static_cast<int>(mf),
                        static_cast<int>(N), static_cast<int>(H), a);
+  }
   if (pl.splits > 1) {
     launch_partials(x, ldx, wkv, H, P, N, H, pl, workspace, stream);
     KvArgs ar = a;                                  // the split rows: statistics, slots and table rows from mf
@@ -1084,4 +1643,86 @@ extern "C" int rf_norm_linear(const uint16_t* x, int64_t ldx, const float* ssq, 
                        eps, out + mf * ldo, ldo, static_cast<int>(rows), static_cast<int>(N));
   }
   return check_launch("rf_norm_linear");
+}
+
+extern "C" int rf_map_apply_batch(int nl, const uint16_t* b, int64_t ldb, const uint16_t* const* w,
+                                  const uint16_t* const* c, uint16_t* const* x, int64_t ldx, float* const* ssq, int64_t P,
+                                  int64_t h_in, int64_t h_out, hipStream_t stream) {
+  if (nl < 1 || nl > MAXL) return fail(RF_EINVAL_ARG, "rf_map_apply_batch: %d layers (1 .. %d)", nl, MAXL);
+  if (!b || !w || !x || !ssq) return fail(RF_EINVAL_ARG, "rf_map_apply_batch: null pointer");
+  if (P < 0 || P > (1ll << 30)) return fail(RF_EINVAL_SHAPE, "rf_map_apply_batch: P = %lld out of range", (long long)P);
+  if (h_in <= 0 || h_in % BK || h_in < 2 * BK || h_out <= 0 || h_out % BN)
+    return fail(RF_EINVAL_SHAPE, "rf_map_apply_batch: h_in %lld must be a multiple of 64 (>= 128) and h_out %lld of 256",
+                (long long)h_in, (long long)h_out);
+  if (ldb < h_in || ldx < h_out || ldb % 8 || ldx % 8 || ldb > (1 << 21) || h_in > (1 << 21))
+    return fail(RF_EINVAL_SHAPE, "rf_map_apply_batch: row strides ldb %lld / ldx %lld", (long long)ldb, (long long)ldx);
+  if (static_cast<int64_t>(nl) * grid_of(P, h_out) > (1ll << 30))
+    return fail(RF_EINVAL_SHAPE, "rf_map_apply_batch: too many tiles");
+  MapLayers ml{};
+  for (int l = 0; l < nl; ++l) {
+    if (!w[l] || !x[l] || !ssq[l]) return fail(RF_EINVAL_ARG, "rf_map_apply_batch: null pointer for layer %d", l);
+    if (!aligned16(w[l]) || !aligned16(x[l]) || (c && c[l] && !aligned16(c[l])))
+      return fail(RF_EINVAL_SHAPE, "rf_map_apply_batch: layer %d pointers must be 16-byte aligned", l);
+    ml.w[l] = w[l];
+    ml.c[l] = c ? c[l] : nullptr;
+    ml.x[l] = x[l];
+    ml.ssq[l] = ssq[l];
+  }
+  if (!aligned16(b)) return fail(RF_EINVAL_SHAPE, "rf_map_apply_batch: b must be 16-byte aligned");
+  if (P == 0) return RF_OK;
+  hipLaunchKernelGGL(k_map_apply_p, dim3(persistent_grid(nl * static_cast<int64_t>(grid_of(P, h_out)))), dim3(NTHR), 0,
+                     stream, b, ldb, ml, nl, ldx, static_cast<int>(P), static_cast<int>(h_out), static_cast<int>(h_in));
+  return check_launch("rf_map_apply_batch");
+}
+
+extern "C" int rf_norm_kv_write_batch(int nl, const uint16_t* const* x, int64_t ldx, const float* const* ssq, int64_t P,
+                                      int64_t H, float eps, const uint16_t* const* wkv, int hkv, int d,
+                                      const uint16_t* const* knorm, int knorm_kind, const uint16_t* cs, int rot,
+                                      uint16_t* const* kbuf, uint16_t* const* vbuf, int64_t head_stride,
+                                      int64_t row_stride, int64_t slot_begin, int64_t cap, hipStream_t stream) {
+  if (nl < 1 || nl > MAXL) return fail(RF_EINVAL_ARG, "rf_norm_kv_write_batch: %d layers (1 .. %d)", nl, MAXL);
+  if (!x || !ssq || !wkv || !cs || !kbuf || !vbuf) return fail(RF_EINVAL_ARG, "rf_norm_kv_write_batch: null pointer");
+  if (P < 0 || P > (1ll << 30))
+    return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write_batch: P = %lld out of range", (long long)P);
+  if (H <= 0 || H % SSQ_COLS || H < 2 * BK || H / SSQ_COLS > 32)
+    return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write_batch: H = %lld must be a multiple of 256 in [256, 8192]",
+                (long long)H);
+  if (d <= 0 || d % 8 || 256 % d || hkv <= 0 || (2ll * hkv * d) % BN)
+    return fail(RF_EUNSUPPORTED, "rf_norm_kv_write_batch: head_dim %d / kv heads %d (need 256 %% d == 0, d %% 8 == 0, "
+                "2 hkv d %% 256 == 0)", d, hkv);
+  if (rot <= 0 || rot > d || rot % 2 || ((rot / 2) % 8 && rot / 2 != 4))
+    return fail(RF_EUNSUPPORTED, "rf_norm_kv_write_batch: rotary dims %d of head_dim %d", rot, d);
+  if (knorm && knorm_kind != 0 && knorm_kind != 1)
+    return fail(RF_EINVAL_ARG, "rf_norm_kv_write_batch: knorm_kind %d", knorm_kind);
+  if (ldx < H || ldx % 8 || ldx > (1 << 21) || head_stride % 8 || row_stride % 8 || row_stride < d)
+    return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write_batch: strides (ldx %lld, head %lld, row %lld)", (long long)ldx,
+                (long long)head_stride, (long long)row_stride);
+  if (slot_begin < 0 || slot_begin + P > cap)
+    return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write_batch: rows [%lld, %lld) exceed cache capacity %lld",
+                (long long)slot_begin, (long long)(slot_begin + P), (long long)cap);
+  if (!aligned16(cs)) return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write_batch: cs must be 16-byte aligned");
+  if (!(eps >= 0.f)) return fail(RF_EINVAL_ARG, "rf_norm_kv_write_batch: eps %g", static_cast<double>(eps));
+  const int64_t N = 2ll * hkv * d;
+  if (static_cast<int64_t>(nl) * grid_of(P, N) > (1ll << 30))
+    return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write_batch: too many tiles");
+  KvLayers kl{};
+  for (int l = 0; l < nl; ++l) {
+    if (!x[l] || !ssq[l] || !wkv[l] || !kbuf[l] || !vbuf[l] || (knorm && !knorm[l]))
+      return fail(RF_EINVAL_ARG, "rf_norm_kv_write_batch: null pointer for layer %d", l);
+    if (!aligned16(x[l]) || !aligned16(wkv[l]) || !aligned16(kbuf[l]) || !aligned16(vbuf[l]) ||
+        (knorm && !aligned16(knorm[l])))
+      return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write_batch: layer %d pointers must be 16-byte aligned", l);
+    kl.x[l] = x[l];
+    kl.ssq[l] = ssq[l];
+    kl.wkv[l] = wkv[l];
+    kl.knorm[l] = knorm ? knorm[l] : nullptr;
+    kl.kbuf[l] = kbuf[l];
+    kl.vbuf[l] = vbuf[l];
+  }
+  if (P == 0) return RF_OK;
+  KvArgs a{nullptr, static_cast<int>(H / SSQ_COLS), static_cast<float>(H), eps, hkv, d, nullptr, knorm_kind, cs, rot,
+           nullptr, nullptr, head_stride, row_stride, slot_begin, nullptr};
+  a.knorm = knorm ? knorm[0] : nullptr;            // the K epilogue's mode follows the (shared) configuration
+  launch_norm_kv_p(kl, nl, ldx, P, N, H, a, stream);
+  return check_launch("rf_norm_kv_write_batch");
 }

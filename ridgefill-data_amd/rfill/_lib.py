@@ -25,11 +25,15 @@ class HipError(RuntimeError):
 
 _P, _I64, _I32, _F32, _F64 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_double
 _SZ, _PSZ = ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)
+_PP = ctypes.POINTER(ctypes.c_void_p)       # a host array of device pointers
 
 # name -> argument types (every function returns int status)
 SIGNATURES = {
     "rf_map_apply": [_P, _I64, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _SZ, _P],
     "rf_gemm_workspace_bytes": [_I64, _I64, _I64, _PSZ],
+    "rf_map_apply_batch": [_I32, _P, _I64, _PP, _PP, _PP, _I64, _PP, _I64, _I64, _I64, _P],
+    "rf_norm_kv_write_batch": [_I32, _PP, _I64, _PP, _I64, _I64, _F32, _PP, _I32, _I32, _PP, _I32, _P, _I32,
+                               _PP, _PP, _I64, _I64, _I64, _I64, _P],
     "rf_row_ssq": [_P, _I64, _P, _I64, _I64, _P],
     "rf_row_scatter": [_P, _I64, _P, _I64, _I64, _P, _I64, _P, _I64, _P],
     "rf_fold_norm": [_P, _P, _I32, _P, _I64, _I64, _P],

@@ -147,6 +147,12 @@ class Projector:
         W, B = self._maps(b.device)
         return ops.map_apply(b, W[i], B[i], out, ssq, workspace=workspace)
 
+    def apply_batch(self, ids, b, outs, ssqs):
+        """apply() of several layers in one launch (ops.map_apply_batch): outs[k] / ssqs[k] receive layer ids[k]'s
+        x and row statistics, bit-identical to apply() of it alone without a workspace."""
+        W, B = self._maps(b.device)
+        ops.map_apply_batch(b, [W[i] for i in ids], [B[i] for i in ids], outs, ssqs)
+
     def __call__(self, i, b):
         return self.apply(i, b)[0]
 
@@ -334,13 +340,26 @@ def two_stream(layers, produce, consume, device):
     main.wait_stream(side)
 
 
-def serial(layers, produce, consume, device, pair=None):
+# Consecutive attention layers filled together by fill_late (one map launch, then one K / V launch per group).
+ATTN_GROUP = 4
+
+
+def serial(layers, produce, consume, device, pair=None, group=None):
     """produce(i, slot) then consume(i, slot) for each layer, all on the current stream. pair: (can(i, j),
     consume_pair(i, slot_i, j, slot_j)): two consecutive layers with can(i, j) are produced both, then
-    consumed together."""
+    consumed together. group: (size, can(i), run(ids)): a run of 2 .. size consecutive layers with can(i)
+    goes to run(ids), which produces and consumes them itself."""
     n, k = 0, 0
     while k < len(layers):
         i = layers[k]
+        if group is not None and group[1](i):
+            m = 1
+            while m < group[0] and k + m < len(layers) and group[1](layers[k + m]):
+                m += 1
+            if m > 1:
+                group[2](layers[k:k + m])
+                k += m
+                continue
         if pair is not None and k + 1 < len(layers) and pair[0](i, layers[k + 1]):
             j = layers[k + 1]
             produce(i, n % 2)
@@ -459,10 +478,32 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
         (xi, qi), (xj, qj) = inputs[si], inputs[sj]
         model.fill_batch([i, j], [xi, xj], cache, ssqs=[qi, qj])
 
+    gbuf = []
+
+    def can_group(i):                                   # attention layers filled by their maps, no computed rows
+        return not computed and model.layer_types[i] == "attn" and fills[i] == "proj"
+
+    def run_group(ids):
+        """The maps of several attention layers in one launch, then their K / V fills in one launch (the GEMMs
+        fill whole waves of the GPU with no tail per layer); each layer's results are bit-identical to its
+        unsplit map apply and fill alone."""
+        while len(gbuf) < len(ids):
+            gbuf.append((torch.empty(P, H, dtype=torch.bfloat16, device=dev),
+                         torch.empty(P, ops.ssq_parts(H), dtype=torch.float32, device=dev)))
+        xs, ss = [g[0] for g in gbuf[:len(ids)]], [g[1] for g in gbuf[:len(ids)]]
+        arm.projector.apply_batch(ids, b, xs, ss)
+        if rows is not None:                            # given row inputs
+            for i, x, q in zip(ids, xs, ss):
+                hri = (hr[i] if isinstance(hr, dict) else hr).to(dev, torch.bfloat16)
+                if row_inputs is not None:
+                    row_inputs[i] = hri
+                ops.row_scatter(x, q, rows, hri)
+        model.fill_attn_batch(ids, xs, pos, cache, ssqs=ss, cs=cs)
+
     if overlap:
         two_stream(layers, produce, consume, dev)
     else:
-        serial(layers, produce, consume, dev, pair=(can_pair, consume_pair))
+        serial(layers, produce, consume, dev, pair=(can_pair, consume_pair), group=(ATTN_GROUP, can_group, run_group))
     return cache, P
 
 

@@ -173,6 +173,37 @@ class FillModel:
         self.commit(c, P)
         return {}
 
+    def fill_attn_batch(self, ids, xs, pos, cache, ssqs=None, cs=None):
+        """fill() of several attention layers over the same rows at once (ops.norm_kv_write_batch): every
+        layer's K / V bit-identical to its fill() without a split-K workspace. Layers whose caches do not take
+        the rows at one slot in one buffer layout are filled one at a time."""
+        ids = list(ids)
+        if any(self.layer_types[i] != "attn" for i in ids):
+            raise ValueError(f"fill_attn_batch: attention layers only, got {ids}")
+        P = xs[0].shape[0]
+        if P == 0:
+            return
+        ssqs = [ops.row_ssq(x) if q is None else q for x, q in zip(xs, ssqs or [None] * len(ids))]
+        if cs is None:
+            cs = self.rope_table(pos)
+        slots = [self.reserve(cache[i], P, self.n_kv, self.head_dim, xs[0].device) for i in ids]
+        c0 = cache[ids[0]]
+        same = all(s == slots[0] and cache[i]["kbuf"].shape == c0["kbuf"].shape
+                   and cache[i]["kbuf"].stride() == c0["kbuf"].stride() for i, s in zip(ids, slots))
+        if not same or len(ids) > ops.MAP_BATCH_MAX:
+            for i, x, q, s in zip(ids, xs, ssqs, slots):
+                w, c = self._layer(i), cache[i]
+                ops.norm_kv_write(x, q, self.eps, w["wkv"], self.n_kv, self.head_dim, w.get("k_norm"),
+                                  self.knorm_kind, cs, c["kbuf"], c["vbuf"], s,
+                                  workspace=self.gemm_workspace(P, w["wkv"].shape[0], x.shape[1], x.device))
+        else:
+            ws = [self._layer(i) for i in ids]
+            ops.norm_kv_write_batch(xs, ssqs, self.eps, [w["wkv"] for w in ws], self.n_kv, self.head_dim,
+                                    [w.get("k_norm") for w in ws], self.knorm_kind, cs,
+                                    [cache[i]["kbuf"] for i in ids], [cache[i]["vbuf"] for i in ids], slots[0])
+        for i in ids:
+            self.commit(cache[i], P)
+
     def _fill_gdn(self, i, x, cache, st, ssq, checkpoint_every):
         """checkpoint_every (a multiple of the 64-row chunk): also return {len + t: state after t rows} for
         every t (rows of this call) that is a multiple of it (code/kva/ops.py:206-209, :258-260). The rows

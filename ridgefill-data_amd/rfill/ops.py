@@ -89,6 +89,83 @@ def map_apply(b, w, c, out=None, ssq=None, workspace=None):
     return out, ssq
 
 
+MAP_BATCH_MAX = 32        # layers per batched map / K-V launch (the library's per-layer pointer tables)
+
+
+def _ptr_array(ts):
+    """A host array of device pointers (NULL for None) for the batched entry points."""
+    return (ctypes.c_void_p * len(ts))(*[_ptr(t) for t in ts])
+
+
+def map_apply_batch(b, ws, cs, outs, ssqs):
+    """Several late layers' maps in one launch (the fill loop of finish(), code/kva/kva.py:413-415, over
+    every layer at once): outs[l] = b ws[l]^T + cs[l] and ssqs[l] its row sum-of-squares partials, each
+    bit-identical to map_apply of that layer alone. Every layer reads the same rows b [P, h_in]; ws[l]
+    [h_out, h_in], cs[l] [h_out] or None, outs[l] [P, h_out] (one row stride for all), ssqs[l]
+    [P, h_out / 256] contiguous."""
+    nl = len(ws)
+    if not 0 < nl <= MAP_BATCH_MAX or not (len(cs) == len(outs) == len(ssqs) == nl):
+        raise ValueError("map_apply_batch: one map, bias, output and statistics per layer")
+    _need(b, "b", torch.bfloat16, 2)
+    P, h_in = b.shape
+    h_out = ws[0].shape[0]
+    for i in range(nl):
+        _need(ws[i], "w", torch.bfloat16, 2)
+        _need(outs[i], "out", torch.bfloat16, 2)
+        _need(ssqs[i], "ssq", torch.float32, 2)
+        if tuple(ws[i].shape) != (h_out, h_in) or not ws[i].is_contiguous():
+            raise ValueError(f"map_apply_batch: layer {i} map {tuple(ws[i].shape)}, expected ({h_out}, {h_in})")
+        if cs[i] is not None:
+            _need(cs[i], "c", torch.bfloat16, 1)
+            if cs[i].shape[0] != h_out:
+                raise ValueError(f"map_apply_batch: layer {i} bias width")
+        if tuple(outs[i].shape) != (P, h_out) or outs[i].stride(0) != outs[0].stride(0):
+            raise ValueError(f"map_apply_batch: layer {i} output {tuple(outs[i].shape)}, expected ({P}, {h_out})"
+                             " with the row stride of layer 0's")
+        if tuple(ssqs[i].shape) != (P, h_out // SSQ_COLS) or not ssqs[i].is_contiguous():
+            raise ValueError(f"map_apply_batch: layer {i} statistics shape")
+    _lib.call("rf_map_apply_batch", nl, _ptr(b), b.stride(0), _ptr_array(ws), _ptr_array(cs), _ptr_array(outs),
+              outs[0].stride(0), _ptr_array(ssqs), P, h_in, h_out, _stream(b))
+
+
+def norm_kv_write_batch(xs, ssqs, eps, wkvs, hkv, d, knorms, knorm_kind, cs, kbufs, vbufs, slot_begin):
+    """The fused K / V fill (norm_kv_write) of several attention layers in one launch, each layer
+    bit-identical to norm_kv_write of it alone: xs[l] [P, H] (one row stride), ssqs[l], wkvs[l]
+    [2 hkv d, H], knorms[l] [d] (all given or all None), one RoPE table cs [P, rot] for every layer, and
+    caches kbufs[l] / vbufs[l] [hkv, cap, d] of one shape and stride, rows [slot_begin, slot_begin + P)."""
+    nl = len(xs)
+    if not 0 < nl <= MAP_BATCH_MAX or not (len(ssqs) == len(wkvs) == len(knorms) == len(kbufs) == len(vbufs) == nl):
+        raise ValueError("norm_kv_write_batch: one input, statistics, weights, k_norm and cache per layer")
+    _need(cs, "cs", torch.bfloat16, 2)
+    P, H = xs[0].shape
+    hs, rs, cap = _cache_args(kbufs[0], vbufs[0], hkv, d, slot_begin, P)
+    has_kn = knorms[0] is not None
+    for i in range(nl):
+        _need(xs[i], "x", torch.bfloat16, 2)
+        _need(ssqs[i], "ssq", torch.float32, 2)
+        _need(wkvs[i], "wkv", torch.bfloat16, 2)
+        if tuple(xs[i].shape) != (P, H) or xs[i].stride(0) != xs[0].stride(0):
+            raise ValueError(f"norm_kv_write_batch: layer {i} input {tuple(xs[i].shape)}, expected ({P}, {H}) with"
+                             " layer 0's row stride")
+        if tuple(ssqs[i].shape) != (P, ssq_parts(H)) or not ssqs[i].is_contiguous():
+            raise ValueError(f"norm_kv_write_batch: layer {i} statistics shape")
+        if tuple(wkvs[i].shape) != (2 * hkv * d, H) or not wkvs[i].is_contiguous():
+            raise ValueError(f"norm_kv_write_batch: layer {i} wkv {tuple(wkvs[i].shape)}")
+        if (knorms[i] is not None) != has_kn:
+            raise ValueError("norm_kv_write_batch: k_norm gains for every layer or for none")
+        if has_kn:
+            _need(knorms[i], "knorm", torch.bfloat16, 1)
+            if knorms[i].shape[0] != d:
+                raise ValueError("norm_kv_write_batch: knorm width")
+        if _cache_args(kbufs[i], vbufs[i], hkv, d, slot_begin, P) != (hs, rs, cap):
+            raise ValueError(f"norm_kv_write_batch: layer {i} cache shape or strides differ from layer 0's")
+    if cs.shape[0] != P or not cs.is_contiguous():
+        raise ValueError("norm_kv_write_batch: cs rows")
+    _lib.call("rf_norm_kv_write_batch", nl, _ptr_array(xs), xs[0].stride(0), _ptr_array(ssqs), P, H, float(eps),
+              _ptr_array(wkvs), hkv, d, _ptr_array(knorms) if has_kn else None, int(knorm_kind), _ptr(cs),
+              cs.shape[1], _ptr_array(kbufs), _ptr_array(vbufs), hs, rs, int(slot_begin), cap, _stream(xs[0]))
+
+
 def row_ssq(x, ssq=None):
     """Row sum-of-squares partials [P, H / 256] of layer inputs x [P, H]."""
     _need(x, "x", torch.bfloat16, 2)
