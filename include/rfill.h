@@ -113,7 +113,8 @@ int rf_map_apply_batch(int nl, const uint16_t* b, int64_t ldb, const uint16_t* c
  * x[l] (one row stride ldx) with statistics ssq[l], its weights wkv[l], k_norm gains knorm[l] (knorm NULL:
  * none for any layer) and caches kbuf[l] / vbuf[l] (one shape and stride for every layer); eps, heads, the
  * RoPE table cs and the slots [slot_begin, slot_begin + P) shared. Each layer's K / V are bit-identical to
- * rf_norm_kv_write of it alone without a workspace. Needs H <= 8192 besides rf_norm_kv_write's conditions.
+ * rf_norm_kv_write of it alone without a workspace. H a multiple of 1024 up to 4096 with a power-of-two
+ * rot <= 128 runs every layer's tiles on one persistent grid; other shapes launch per layer.
  * Replaces Model.fill (code/kva/model.py:278-280) of each layer. */
 int rf_norm_kv_write_batch(int nl, const uint16_t* const* x, int64_t ldx, const float* const* ssq, int64_t P,
                            int64_t H, float eps, const uint16_t* const* wkv, int hkv, int d,

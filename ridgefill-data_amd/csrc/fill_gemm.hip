@@ -1152,92 +1152,89 @@ struct KvLayers {
   uint16_t* vbuf[MAXL];
 };
 
-// Input RMSNorm scale 1 / sqrt(mean(x^2) + eps) of row gm from its nparts (<= 32) partials, summed in order
-// (as row_scale). row_parts32 issues the loads (all before any use, so one wait covers them), parts_scale
-// sums them.
-__device__ __forceinline__ void row_parts32(const float* __restrict__ ssq, int nparts, int M, int gm, float (&p)[32]) {
-  const float* q = ssq + static_cast<int64_t>(gm < M ? gm : 0) * nparts;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) p[i] = q[i < nparts ? i : nparts - 1];     // unconditional loads: no branches
-#pragma unroll
-  for (int i = 0; i < 32; ++i) p[i] = i < nparts ? p[i] : 0.f;
-}
-__device__ __forceinline__ float parts_scale(const float (&p)[32], float width, float eps) {
-  float s = 0.f;
-#pragma unroll
-  for (int i = 0; i < 32; ++i) s += p[i];
-  return 1.0f / sqrtf(s / width + eps);
-}
-
-// Epilogue round r of a K / V tile: fetch(r) the RoPE entries of its rows (K tiles), the image's row pass.
-// Row pass of K columns only (slot-indexed rows): image rows u*8 + t/32 (u < 8), chunk t % 32; the rows'
-// RoPE entries `re` were fetched a round earlier.
-template <int MODE>
-__device__ __forceinline__ void k_round(const KvArgs& a, const KvLane& L, const uint4* img, int r, int m0, int M,
-                                        const RopeEnt (&re)[8], int t) {
-  const int ch = t & 31;
-#pragma unroll
-  for (int h = 0; h < 2; ++h) {                   // two halves of 4 rows: fewer temporaries live at once
-    uint4 o[4];
-#pragma unroll
-    for (int v4 = 0; v4 < 4; ++v4) {
-      const int u = h * 4 + v4, ir = u * 8 + (t >> 5);
-      const uint4 v = image_chunk(img, ir, ch);
-      const bool half8 = MODE == KV_ANY ? L.half >= 8 : true;
-      const uint4 pv = half8 ? image_chunk(img, ir, ch + (L.pj0 - L.j0) / 8) : v;
-      const float ss = head_ssq<MODE>(a, L, v);
-      o[v4] = (MODE != KV_ANY || L.norm || L.rope) ? k_chunk<MODE>(a, L, v, pv, ss, re[u]) : v;
-    }
-#pragma unroll
-    for (int v4 = 0; v4 < 4; ++v4) {
-      const int gm = m0 + round_row((h * 4 + v4) * 8 + (t >> 5), r);
-      if (gm < M) st_stream16(L.dst0 + (a.slot0 + gm) * a.row_stride, o[v4]);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-}
-
-__device__ __forceinline__ void rope_round(const KvArgs& a, const KvLane& L, int r, int m0, int M, RopeEnt (&re)[8],
-                                           int t) {
-#pragma unroll
-  for (int u = 0; u < 8; ++u) re[u] = rope_fetch_ahead(a, L, m0 + round_row(u * 8 + (t >> 5), r), M);
-}
-
-// RoPE table rows of epilogue round r for a d 128, full-rotary K tile (256-byte rows: 64 cos, then 64 sin
-// values) from the table cs (resource rcs, slot-indexed rows < M) straight into LDS at tab (16 KiB, row ir
-// at ir * 256): 4 loads per wave, 4 rows of 16 lanes each. Rows past M read row M - 1 (never stored).
-__device__ __forceinline__ void table_round(__amdgpu_buffer_rsrc_t rcs, int r, int m0, int M, uint4* tab, int t) {
-  const int w = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
+// Input RMSNorm scales 1 / sqrt(mean(x^2) + eps) of a tile's 256 rows from their nparts = 4 q4 partials
+// (q4 <= 4), summed in order as row_scale sums them. The tile's partials are one contiguous block, loaded
+// 16 bytes a lane: load k holds rows k * 256 / q4 + t / q4, lane t % q4 their partials 4 (t % q4) .. + 3.
+// parts_load issues the loads (all before any use); parts_sum adds each row's partials in order along its
+// q4 lanes (lane j starts from lane j - 1's running sum), leaving the scale of row k * 256 / q4 + t / q4 in
+// sc[k] of the row's last lane (t % q4 == q4 - 1). Both run without branches: all four loads issue (loads
+// k >= q4 repeat load 0) and every loaded register is read, so no load is left in flight on any path the
+// compiler's wait counting follows (a pending load there would make the next tile's K loop wait for all
+// loads at every step).
+__device__ __forceinline__ void parts_load(const float* __restrict__ ssq, int q4, int M, int m0, int t, float4 (&v)[4]) {
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
-    const int ir = w * 16 + k * 4 + (lane >> 4);
-    const int gm = min(m0 + round_row(ir, r), M - 1);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rcs, (lds_ptr)(tab + (w * 16 + k * 4) * 16), 16,
-                                             static_cast<uint32_t>(gm * 256 + (lane & 15) * 16), 0, 0, 0);
+    const int kk = k < q4 ? k : 0;
+    const int row = min(m0 + kk * (256 / q4) + t / q4, M - 1);
+    v[k] = *reinterpret_cast<const float4*>(ssq + static_cast<int64_t>(row) * (4 * q4) + 4 * (t % q4));
+  }
+}
+__device__ __forceinline__ void parts_sum(const float4 (&v)[4], int q4, float width, float eps, int t, float (&sc)[4]) {
+  const int lane = t & 63, j = t % q4;
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    float s = 0.f;
+#pragma unroll
+    for (int jj = 0; jj < 4; ++jj) {                // steps jj >= q4 change no lane (j < q4)
+      const float prev = __shfl(s, lane > 0 ? lane - 1 : 0, 64);
+      float a = jj == 0 ? 0.f : prev;
+      a += v[k].x;
+      a += v[k].y;
+      a += v[k].z;
+      a += v[k].w;
+      s = j == jj ? a : s;
+    }
+    sc[k] = 1.0f / sqrtf(s / width + eps);
   }
 }
 
-// Row pass of epilogue round r for a d 128, full-rotary K tile with its RoPE entries in LDS (tab, as
-// table_round lays them out): image rows u*8 + t/32 (u < 8, in two halves of 4), chunk t % 32.
+// RoPE table rows of epilogue round r (64 image rows) from the table cs (resource rcs, slot-indexed rows < M,
+// rb = rot * 2 bytes a row: 16 .. 256, a power of two) straight into LDS at tab (row ir at ir * rb bytes):
+// each load instruction fills 1 KiB, 1024 / rb rows of rb / 16 lanes each. Rows past M read row M - 1 (never
+// stored). The caller waits (vmcnt) before the barrier after which tab is read.
+__device__ __forceinline__ void table_round(__amdgpu_buffer_rsrc_t rcs, int rb, int r, int m0, int M, uint4* tab, int t) {
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6), lane = t & 63;
+  const int lpr = rb >> 4, rpi = 64 / lpr, nload = (64 * rb) >> 10;
+  for (int k = w; k < nload; k += 4) {               // wave-uniform
+    const int ir = k * rpi + lane / lpr;
+    const int gm = min(m0 + round_row(ir, r), M - 1);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rcs, (lds_ptr)(tab + k * 64), 16,
+                                             static_cast<uint32_t>(gm * rb + (lane % lpr) * 16), 0, 0, 0);
+  }
+}
+
+// Row pass of epilogue round r for a K tile with its RoPE entries in LDS (tab, as table_round lays them out,
+// rb bytes a row): image rows u*8 + t/32 (u < 8), chunk t % 32.
 template <int MODE>
-__device__ __forceinline__ void k_round_tab(const KvArgs& a, const KvLane& L, const uint4* img, const uint4* tab, int r,
-                                            int m0, int M, int t) {
-  const int ch = t & 31, fc = L.fi0 >> 3;
+__device__ __forceinline__ void k_round_tab(const KvArgs& a, const KvLane& L, const uint4* img, const uint4* tab, int rb,
+                                            int r, int m0, int M, int t) {
+  const int ch = t & 31, upr = MODE == KV_ANY ? rb >> 4 : 16;
+  const int half = MODE == KV_ANY ? L.half : 64;
+  const int fc = L.rope ? L.fi0 >> 3 : 0;           // chunks past rot read entry 0 (unused)
+  constexpr int G = MODE == KV_D128 ? 4 : 2;        // rows in flight (k_norm needs more registers a row)
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
-    uint4 o[4];
+  for (int h = 0; h < 8 / G; ++h) {
+    uint4 o[G];
 #pragma unroll
-    for (int v4 = 0; v4 < 4; ++v4) {
-      const int ir = (h * 4 + v4) * 8 + (t >> 5);
+    for (int v4 = 0; v4 < G; ++v4) {
+      const int ir = (h * G + v4) * 8 + (t >> 5);
       const uint4 v = image_chunk(img, ir, ch);
-      const uint4 pv = image_chunk(img, ir, ch + (L.pj0 - L.j0) / 8);
+      const bool half8 = MODE == KV_ANY ? half >= 8 : true;
+      const uint4 pv = half8 ? image_chunk(img, ir, ch + (L.pj0 - L.j0) / 8) : v;
       const float ss = head_ssq<MODE>(a, L, v);
-      const RopeEnt re{tab[ir * 16 + fc], tab[ir * 16 + 8 + fc]};
-      o[v4] = k_chunk<MODE>(a, L, v, pv, ss, re);
+      RopeEnt re;
+      if (half8) {
+        re.c = tab[ir * upr + fc];
+        re.s = tab[ir * upr + (half >> 3) + fc];
+      } else {                                        // rot == 8: the row's whole table in one chunk
+        re.c = tab[ir * upr];
+        re.s = make_uint4(0u, 0u, 0u, 0u);
+      }
+      o[v4] = (MODE != KV_ANY || L.norm || L.rope) ? k_chunk<MODE>(a, L, v, pv, ss, re) : v;
     }
 #pragma unroll
-    for (int v4 = 0; v4 < 4; ++v4) {
-      const int gm = m0 + round_row((h * 4 + v4) * 8 + (t >> 5), r);
+    for (int v4 = 0; v4 < G; ++v4) {
+      const int gm = m0 + round_row((h * G + v4) * 8 + (t >> 5), r);
       if (gm < M) st_stream16(L.dst0 + (a.slot0 + gm) * a.row_stride, o[v4]);
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -1247,11 +1244,10 @@ __device__ __forceinline__ void k_round_tab(const KvArgs& a, const KvLane& L, co
 // rf_norm_kv_write on persistent tiles for nl layers at once (slot-indexed rows, no position array). The
 // base arguments `a0` carry what the layers share (norm width, eps, heads, RoPE table, strides, first
 // slot); the layer's statistics, weights, k_norm gains and cache buffers come from kl. KMODE is the K
-// tiles' epilogue (one per launch: it follows from the configuration). For d 128 with full rotary
-// (KV_D128, KV_D128_KNORM) a K tile's RoPE entries go from the table into LDS, one round ahead, in the
-// two weight slots of its last K step (the first two rounds' from the tile's last step on, pre); with
-// KV_ANY they are loaded into registers as each round starts. V tiles copy; tiles holding K and V
-// columns (KV_ANY only) go chunk by chunk.
+// tiles' epilogue (one per launch: it follows from the configuration). A K tile's RoPE table rows go from
+// the table straight into LDS (buffer_load ... lds) one round ahead, double-buffered in the two weight
+// slots of its last K step (rounds 0 and 1 from that step on, pre). V tiles copy; tiles holding K and V
+// columns (KV_ANY only) go chunk by chunk. Takes H a multiple of 1024 up to 4096 and a power-of-two rot <= 128 (persistent_kv_ok).
 template <int KMODE>
 __global__ __launch_bounds__(NTHR) void k_norm_kv_p(KvLayers kl, int nl, int64_t ldx, int M, int N, int K, KvArgs a0) {
   __shared__ uint4 lds[LDS_U4];
@@ -1259,7 +1255,7 @@ __global__ __launch_bounds__(NTHR) void k_norm_kv_p(KvLayers kl, int nl, int64_t
   const Share sh = block_share(nl * per);
   if (sh.cnt == 0) return;
   const int t = threadIdx.x;
-  constexpr bool TAB = KMODE != KV_ANY;
+  const int rb = a0.rot * 2;                        // bytes of a RoPE table row
   auto coords = [&](int i, int& l, int& tm, int& tn) {
     const int u = sh.first + i * sh.stride;
     l = u / per;
@@ -1272,16 +1268,17 @@ __global__ __launch_bounds__(NTHR) void k_norm_kv_p(KvLayers kl, int nl, int64_t
     return TileOps{buffer_rsrc(kl.x[l] + static_cast<int64_t>(m0) * ldx, static_cast<uint32_t>(min(M - m0, BM) * ldx * 2)),
                    buffer_rsrc(kl.wkv[l] + static_cast<int64_t>(tn) * BN * K, static_cast<uint32_t>(BN * K * 2))};
   };
-  auto parts_of = [&](int i, float (&p)[32]) {
+  const int q4 = a0.nparts / 4;
+  auto parts_of = [&](int i, float4 (&v)[4], int tt) {
     int l, tm, tn;
     coords(i, l, tm, tn);
-    row_parts32(kl.ssq[l], a0.nparts, M, tm * BM + t, p);
+    parts_load(kl.ssq[l], q4, M, tm * BM, tt, v);
   };
-  float my_rs;                    // row t of the current tile
+  float sc[4];                    // the current tile's row scales (parts_sum's layout)
   {
-    float p[32];
-    parts_of(0, p);
-    my_rs = parts_scale(p, a0.h, a0.eps);
+    float4 v[4];
+    parts_of(0, v, t);
+    parts_sum(v, q4, a0.h, a0.eps, t, sc);
   }
   auto begin = [&](int, f32x16 (&acc)[4][4]) {
 #pragma unroll
@@ -1295,11 +1292,11 @@ __global__ __launch_bounds__(NTHR) void k_norm_kv_p(KvLayers kl, int nl, int64_t
   auto pre = [&](int i, uint4* side) {
     int l, tm, tn;
     coords(i, l, tm, tn);
-    if (TAB && tn * BN + BN <= kw) {
+    if (tn * BN + BN <= kw) {
       const int tp = pinned_tid();
-      const __amdgpu_buffer_rsrc_t rcs = buffer_rsrc(a0.cs, static_cast<uint32_t>(M) * 256u);
-      table_round(rcs, 0, tm * BM, M, side, tp);
-      table_round(rcs, 1, tm * BM, M, side + SLOT_U4, tp);
+      const __amdgpu_buffer_rsrc_t rcs = buffer_rsrc(a0.cs, static_cast<uint32_t>(M) * static_cast<uint32_t>(rb));
+      table_round(rcs, rb, 0, tm * BM, M, side, tp);
+      table_round(rcs, rb, 1, tm * BM, M, side + SLOT_U4, tp);
     }
   };
   auto end = [&](int i, const f32x16 (&acc)[4][4], uint4* img, float* side_f) {
@@ -1317,23 +1314,23 @@ __global__ __launch_bounds__(NTHR) void k_norm_kv_p(KvLayers kl, int nl, int64_t
     const KvLane L(a, n0, ch);
     // 1: K columns only; 4: V columns only; 5: both
     const int mode = n0 + BN <= kw ? 1 : (n0 >= kw || KMODE != KV_ANY) ? 4 : 5;
-    const bool tab = TAB && mode == 1;
+    const bool tab = mode == 1;
     // the rows' norm scales, through the image area (free until round 0 is staged)
     float* rsx = reinterpret_cast<float*>(img);
-    rsx[t] = my_rs;
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (k < q4 && t % q4 == q4 - 1) rsx[k * (256 / q4) + t / q4] = sc[k];
     __syncthreads();
     float rs[4];
 #pragma unroll
     for (int mt = 0; mt < 4; ++mt) rs[mt] = rsx[wm * 128 + mt * 32 + (lane & 31)];
     __syncthreads();
-    const __amdgpu_buffer_rsrc_t rcs = buffer_rsrc(a0.cs, static_cast<uint32_t>(M) * 256u);
-    float p[32];
+    const __amdgpu_buffer_rsrc_t rcs = buffer_rsrc(a0.cs, static_cast<uint32_t>(M) * static_cast<uint32_t>(rb));
+    float4 pv4[4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       __builtin_amdgcn_sched_barrier(0);
-      RopeEnt re[8];
-      if (!TAB && mode == 1) rope_round(a, L, r, m0, M, re, t);   // in flight while the round is staged
-      if (r == 3 && more) parts_of(i + 1, p);
+      if (r == 3) parts_of(more ? i + 1 : i, pv4, t);   // unconditional (see parts_load)
       float unused;
       switch (r) {
         case 0: stage_round<0, false>(img, acc, [&](int, int, int, float v) { return v * rs[0]; }, unused, t); break;
@@ -1344,8 +1341,7 @@ __global__ __launch_bounds__(NTHR) void k_norm_kv_p(KvLayers kl, int nl, int64_t
       if (tab) __builtin_amdgcn_s_waitcnt(0x0f70);      // vmcnt(0): this round's table rows are in LDS
       __syncthreads();
       if (mode == 1) {
-        if (TAB) k_round_tab<KMODE>(a, L, img, side + (r & 1) * SLOT_U4, r, m0, M, t);
-        else k_round<KV_ANY>(a, L, img, r, m0, M, re, t);
+        k_round_tab<KMODE>(a, L, img, side + (r & 1) * SLOT_U4, rb, r, m0, M, t);
       } else if (mode == 4) {
 #pragma unroll
         for (int it = 0; it < 8; ++it) {
@@ -1362,21 +1358,28 @@ __global__ __launch_bounds__(NTHR) void k_norm_kv_p(KvLayers kl, int nl, int64_t
         }
       }
       __syncthreads();
-      if (tab && r + 2 < 4) table_round(rcs, r + 2, m0, M, side + (r & 1) * SLOT_U4, t);
+      if (tab && r + 2 < 4) table_round(rcs, rb, r + 2, m0, M, side + (r & 1) * SLOT_U4, t);
     }
-    if (more) my_rs = parts_scale(p, a0.h, a0.eps);
+    parts_sum(pv4, q4, a0.h, a0.eps, t, sc);
   };
   stream_tiles(sh.cnt, K / BK, ldx, K, ops, begin, pre, end, lds);
 }
 
 int grid_of(int64_t M, int64_t N) { return static_cast<int>(((M + BM - 1) / BM) * (N / BN)); }
 
+// The persistent K / V kernel takes H a multiple of 1024 up to 4096 (its row statistics: 4 .. 16 partials,
+// 16 bytes a lane) and a power-of-two rot <= 128 (a RoPE table row fills whole 16-byte lanes of a 1 KiB
+// load, and a round's 64 rows fit one 16 KiB slot).
+bool persistent_kv_ok(int64_t H, int rot, int64_t M) {
+  return H % 1024 == 0 && H / SSQ_COLS <= 16 && rot <= 128 && (rot & (rot - 1)) == 0 && M * rot * 2 < (1ll << 32);
+}
+
 // The persistent K / V kernel for nl layers of M rows; the K epilogue's compile-time mode from the
 // configuration in a (d 128 with full rotary: without k_norm, or with Llama-style k_norm; anything else).
 void launch_norm_kv_p(const KvLayers& kl, int nl, int64_t ldx, int64_t M, int64_t N, int64_t K, const KvArgs& a,
                       hipStream_t stream) {
   const dim3 grid(persistent_grid(nl * static_cast<int64_t>(grid_of(M, N)))), block(NTHR);
-  const bool d128 = a.d == 128 && a.rot == 128 && M * 256 < (1ll << 32);   // table offsets fit 32 bits
+  const bool d128 = a.d == 128 && a.rot == 128;
   if (d128 && !a.knorm)
     hipLaunchKernelGGL(k_norm_kv_p<KV_D128>, grid, block, 0, stream, kl, nl, ldx, static_cast<int>(M),
                        static_cast<int>(N), static_cast<int>(K), a);
@@ -1530,7 +1533,7 @@ extern "C" int rf_norm_kv_write(const uint16_t* x, int64_t ldx, const float* ssq
   if (workspace && !aligned16(workspace)) return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write: workspace alignment");
   const Plan pl = plan_with(P, N, H, workspace, ws_bytes);
   const int64_t mf = pl.m_fused, rows = P - mf;
-  if (mf > 0 && H / BK >= 2 && H / SSQ_COLS <= 32) {
+  if (mf > 0 && persistent_kv_ok(H, rot, mf)) {
     KvLayers kl{};
     kl.x[0] = x;
     kl.ssq[0] = ssq;
@@ -1684,9 +1687,8 @@ extern "C" int rf_norm_kv_write_batch(int nl, const uint16_t* const* x, int64_t 
   if (!x || !ssq || !wkv || !cs || !kbuf || !vbuf) return fail(RF_EINVAL_ARG, "rf_norm_kv_write_batch: null pointer");
   if (P < 0 || P > (1ll << 30))
     return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write_batch: P = %lld out of range", (long long)P);
-  if (H <= 0 || H % SSQ_COLS || H < 2 * BK || H / SSQ_COLS > 32)
-    return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write_batch: H = %lld must be a multiple of 256 in [256, 8192]",
-                (long long)H);
+  if (H <= 0 || H % SSQ_COLS)
+    return fail(RF_EINVAL_SHAPE, "rf_norm_kv_write_batch: H = %lld must be a multiple of 256", (long long)H);
   if (d <= 0 || d % 8 || 256 % d || hkv <= 0 || (2ll * hkv * d) % BN)
     return fail(RF_EUNSUPPORTED, "rf_norm_kv_write_batch: head_dim %d / kv heads %d (need 256 %% d == 0, d %% 8 == 0, "
                 "2 hkv d %% 256 == 0)", d, hkv);
@@ -1723,6 +1725,18 @@ extern "C" int rf_norm_kv_write_batch(int nl, const uint16_t* const* x, int64_t 
   KvArgs a{nullptr, static_cast<int>(H / SSQ_COLS), static_cast<float>(H), eps, hkv, d, nullptr, knorm_kind, cs, rot,
            nullptr, nullptr, head_stride, row_stride, slot_begin, nullptr};
   a.knorm = knorm ? knorm[0] : nullptr;            // the K epilogue's mode follows the (shared) configuration
-  launch_norm_kv_p(kl, nl, ldx, P, N, H, a, stream);
+  if (persistent_kv_ok(H, rot, P)) {
+    launch_norm_kv_p(kl, nl, ldx, P, N, H, a, stream);
+  } else {                                          // other widths: the per-tile kernel, one launch per layer
+    for (int l = 0; l < nl; ++l) {
+      KvArgs al = a;
+      al.ssq = kl.ssq[l];
+      al.knorm = kl.knorm[l];
+      al.kbuf = kl.kbuf[l];
+      al.vbuf = kl.vbuf[l];
+      hipLaunchKernelGGL(k_norm_kv, dim3(grid_of(P, N)), dim3(NTHR), 0, stream, kl.x[l], ldx, kl.wkv[l],
+                         static_cast<int>(P), static_cast<int>(N), static_cast<int>(H), al);
+    }
+  }
   return check_launch("rf_norm_kv_write_batch");
 }

@@ -9,7 +9,7 @@ test_gpu_fill.py."""
 import pytest
 import torch
 
-from fill_cases import CASES, case, inputs, rel_err
+from fill_cases import CASES, attn_config, case, inputs, random_tensors, rel_err
 
 pytestmark = pytest.mark.gpu
 
@@ -29,15 +29,35 @@ def _maps(H, layers, seed):
     return W, B
 
 
+# Width-1024 configurations take the persistent K / V kernel (the CASES widths 256 / 512 take the per-tile
+# kernel): its d-128 K epilogue without and with k_norm, and the generic one (d 256 with rot 64, d 64, and
+# rot 8, whose table row is a single 16-byte chunk).
+WIDE = {
+    "w1024_llama_d128": ("llama", 1024, 2, 128, 5e5, {}),
+    "w1024_qwen3_knorm": ("qwen3", 1024, 2, 128, 1e6, dict(eps=1e-6)),
+    "w1024_qwen35_d256_rot64": ("qwen3_5", 1024, 2, 256, 1e7, dict(eps=1e-6, rot_frac=0.25)),
+    "w1024_llama_d64": ("llama", 1024, 4, 64, 1e4, {}),
+    "w1024_qwen35_d64_rot8": ("qwen3_5", 1024, 4, 64, 1e7, dict(eps=1e-6, rot_frac=0.125)),
+}
+
+
+def _case(name, layers):
+    if name in CASES:
+        return case(name, layers=layers)
+    arch, h, hkv, d, theta, kw = WIDE[name]
+    cfg = attn_config(arch, h, hkv, d, theta, layers=layers, **kw)
+    return cfg, random_tensors(cfg, 0)
+
+
 # P: 700 rows give fewer tiles than CUs for most cases (one tile per block); 20000 rows run every block
 # over several tiles, with a ragged last tile row
 @pytest.mark.parametrize("P", [700, 20000])
-@pytest.mark.parametrize("name", sorted(CASES))
+@pytest.mark.parametrize("name", sorted(CASES) + sorted(WIDE))
 def test_batch_equals_per_layer(dev, name, P):
     from rfill import ops
     from rfill.model import FillModel
     nl = 3
-    cfg, t = case(name, layers=nl)
+    cfg, t = _case(name, nl)
     H, hkv, d = cfg["hidden_size"], cfg["num_key_value_heads"], cfg["head_dim"]
     layers = list(range(nl))
     m = FillModel(cfg, t, dev)
@@ -73,6 +93,16 @@ def test_batch_equals_per_layer(dev, name, P):
         assert torch.equal(vbs[i], ref_c[i][1]), f"layer {i}: V differs"
         assert bool((kbs[i][:, :slot0] == sentinel).all()) and bool((kbs[i][:, slot0 + P:] == sentinel).all())
         assert bool((vbs[i][:, :slot0] == sentinel).all()) and bool((vbs[i][:, slot0 + P:] == sentinel).all())
+    # layer 0's K / V against the oracle's fill of the same inputs (sampled rows at P = 20000)
+    from oracle import model as OM
+    sel = torch.arange(P) if P <= 1000 else torch.randperm(P, generator=torch.Generator().manual_seed(28))[:512].sort().values
+    om = OM.OracleModel(cfg, t, dtype=torch.bfloat16)
+    oc = om.new_cache()
+    om.fill(0, ref_x[0][sel.to(dev)].cpu(), sel, oc)
+    ek = rel_err(kbs[0][:, (slot0 + sel).to(dev)], oc[0]["k"])
+    ev = rel_err(vbs[0][:, (slot0 + sel).to(dev)], oc[0]["v"])
+    print(f"{name} P {P}: K rel err {ek:.2e}, V rel err {ev:.2e} vs the oracle")
+    assert ek < 1e-2 and ev < 1e-2
 
 
 def test_batch_c2_shape(dev):
