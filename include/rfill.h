@@ -122,6 +122,15 @@ int rf_norm_kv_write_batch(int nl, const uint16_t* const* x, int64_t ldx, const 
                            uint16_t* const* kbuf, uint16_t* const* vbuf, int64_t head_stride, int64_t row_stride,
                            int64_t slot_begin, int64_t cap, hipStream_t stream);
 
+/* rf_norm_linear for nl (1 .. 32) layers in one launch over the same P rows (the in-projections of a group of
+ * Gated DeltaNet layers, code/kva/model.py:448-450 per layer): out[l] = bf16(rms-normed x[l] w[l]^T), each
+ * layer bit-identical to rf_norm_linear of it alone without a workspace. x, ssq, w, out: host arrays of nl
+ * device pointers; one input row stride ldx and one output row stride ldo. H a multiple of 1024 up to 4096
+ * runs every layer's tiles on one persistent grid; other widths launch per layer. */
+int rf_norm_linear_batch(int nl, const uint16_t* const* x, int64_t ldx, const float* const* ssq, int64_t P, int64_t H,
+                         float eps, const uint16_t* const* w, int64_t N, uint16_t* const* out, int64_t ldo,
+                         hipStream_t stream);
+
 /* RoPE on given pre-RoPE K and the K / V cache write of m rows.
  * Replaces Model.fill_kv (code/kva/model.py:161-165): ops.apply_rope (ops.py:66-77) + _append_kv.
  * k / v: [m, hkv, d] with token strides ld_k / ld_v (a head's d values contiguous, heads d apart);

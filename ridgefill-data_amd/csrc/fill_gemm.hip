@@ -1365,11 +1365,104 @@ __global__ __launch_bounds__(NTHR) void k_norm_kv_p(KvLayers kl, int nl, int64_t
   stream_tiles(sh.cnt, K / BK, ldx, K, ops, begin, pre, end, lds);
 }
 
+// Per-layer operands of a batched norm + linear launch.
+struct LinLayers {
+  const uint16_t* x[MAXL];
+  const float* ssq[MAXL];
+  const uint16_t* w[MAXL];
+  uint16_t* out[MAXL];
+};
+
+// rf_norm_linear on persistent tiles for nl layers at once: out_l = bf16(r_row * (x_l W_l^T)), r_row from the
+// rows' statistics (parts_load / parts_sum; K a multiple of 1024 up to 4096); one output row stride ldo.
+__global__ __launch_bounds__(NTHR) void k_norm_linear_p(LinLayers ll, int nl, int64_t ldx, int64_t ldo, int M, int N,
+                                                        int K, float eps) {
+  __shared__ uint4 lds[LDS_U4];
+  const int tiles_n = N / BN, tiles_m = (M + BM - 1) / BM, per = tiles_m * tiles_n;
+  const Share sh = block_share(nl * per);
+  if (sh.cnt == 0) return;
+  const int t = threadIdx.x, q4 = K / (4 * SSQ_COLS);
+  const float width = static_cast<float>(K);
+  auto coords = [&](int i, int& l, int& tm, int& tn) {
+    const int u = sh.first + i * sh.stride;
+    l = u / per;
+    tile_coords(u - l * per, tiles_m, tiles_n, tm, tn);
+  };
+  auto ops = [&](int i) {
+    int l, tm, tn;
+    coords(i, l, tm, tn);
+    const int m0 = tm * BM;
+    return TileOps{buffer_rsrc(ll.x[l] + static_cast<int64_t>(m0) * ldx, static_cast<uint32_t>(min(M - m0, BM) * ldx * 2)),
+                   buffer_rsrc(ll.w[l] + static_cast<int64_t>(tn) * BN * K, static_cast<uint32_t>(BN * K * 2))};
+  };
+  auto parts_of = [&](int i, float4 (&v)[4], int tt) {
+    int l, tm, tn;
+    coords(i, l, tm, tn);
+    parts_load(ll.ssq[l], q4, M, tm * BM, tt, v);
+  };
+  float sc[4];
+  {
+    float4 v[4];
+    parts_of(0, v, t);
+    parts_sum(v, q4, width, eps, t, sc);
+  }
+  auto begin = [&](int, f32x16 (&acc)[4][4]) {
+#pragma unroll
+    for (int p = 0; p < 4; ++p)
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[p][q][r] = 0.f;
+  };
+  auto end = [&](int i, const f32x16 (&acc)[4][4], uint4* img, float*) {
+    int l, tm, tn;
+    coords(i, l, tm, tn);
+    const int t = pinned_tid(), lane = t & 63, wm = t >> 7;
+    const int m0 = tm * BM, n0 = tn * BN, ch = t & 31;
+    uint16_t* out = ll.out[l];
+    float* rsx = reinterpret_cast<float*>(img);     // the rows' norm scales, through the image area
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (k < q4 && t % q4 == q4 - 1) rsx[k * (256 / q4) + t / q4] = sc[k];
+    __syncthreads();
+    float rs[4];
+#pragma unroll
+    for (int mt = 0; mt < 4; ++mt) rs[mt] = rsx[wm * 128 + mt * 32 + (lane & 31)];
+    __syncthreads();
+    float4 pv4[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (r == 3) parts_of(i + 1 < sh.cnt ? i + 1 : i, pv4, t);   // unconditional (see parts_load)
+      float unused;
+      switch (r) {
+        case 0: stage_round<0, false>(img, acc, [&](int, int, int, float v) { return v * rs[0]; }, unused, t); break;
+        case 1: stage_round<1, false>(img, acc, [&](int, int, int, float v) { return v * rs[1]; }, unused, t); break;
+        case 2: stage_round<2, false>(img, acc, [&](int, int, int, float v) { return v * rs[2]; }, unused, t); break;
+        default: stage_round<3, false>(img, acc, [&](int, int, int, float v) { return v * rs[3]; }, unused, t); break;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int ir = it * 8 + (t >> 5);
+        const int gm = m0 + round_row(ir, r);
+        if (gm < M) *reinterpret_cast<uint4*>(out + static_cast<int64_t>(gm) * ldo + n0 + ch * 8) = image_chunk(img, ir, ch);
+      }
+      __syncthreads();
+    }
+    parts_sum(pv4, q4, width, eps, t, sc);
+  };
+  stream_tiles(sh.cnt, K / BK, ldx, K, ops, begin, [](int, uint4*) {}, end, lds);
+}
+
 int grid_of(int64_t M, int64_t N) { return static_cast<int>(((M + BM - 1) / BM) * (N / BN)); }
 
 // The persistent K / V kernel takes H a multiple of 1024 up to 4096 (its row statistics: 4 .. 16 partials,
 // 16 bytes a lane) and a power-of-two rot <= 128 (a RoPE table row fills whole 16-byte lanes of a 1 KiB
 // load, and a round's 64 rows fit one 16 KiB slot).
+// The persistent norm + linear kernel: H a multiple of 1024 up to 4096 (as persistent_kv_ok).
+bool persistent_lin_ok(int64_t H) { return H % 1024 == 0 && H / SSQ_COLS <= 16; }
+
 bool persistent_kv_ok(int64_t H, int rot, int64_t M) {
   return H % 1024 == 0 && H / SSQ_COLS <= 16 && rot <= 128 && (rot & (rot - 1)) == 0 && M * rot * 2 < (1ll << 32);
 }
@@ -1636,9 +1729,18 @@ extern "C" int rf_norm_linear(const uint16_t* x, int64_t ldx, const float* ssq, 
   if (P == 0) return RF_OK;
   const Plan pl = plan_with(P, N, H, workspace, ws_bytes);
   const int64_t mf = pl.m_fused, rows = P - mf;
-  if (mf > 0)
+  if (mf > 0 && persistent_lin_ok(H)) {
+    LinLayers ll{};
+    ll.x[0] = x;
+    ll.ssq[0] = ssq;
+    ll.w[0] = w;
+    ll.out[0] = out;
+    hipLaunchKernelGGL(k_norm_linear_p, dim3(persistent_grid(grid_of(mf, N))), dim3(NTHR), 0, stream, ll, 1, ldx, ldo,
+                       static_cast<int>(mf), static_cast<int>(N), static_cast<int>(H), eps);
+  } else if (mf > 0) {
     hipLaunchKernelGGL(k_norm_linear, dim3(grid_of(mf, N)), dim3(NTHR), 0, stream, x, ldx, w, static_cast<int>(mf),
                        static_cast<int>(N), static_cast<int>(H), ssq, eps, out, ldo);
+  }
   if (pl.splits > 1) {
     launch_partials(x, ldx, w, H, P, N, H, pl, workspace, stream);
     hipLaunchKernelGGL(k_norm_linear_reduce, reduce_grid(rows, N), dim3(256), 0, stream,
@@ -1739,4 +1841,39 @@ extern "C" int rf_norm_kv_write_batch(int nl, const uint16_t* const* x, int64_t 
     }
   }
   return check_launch("rf_norm_kv_write_batch");
+}
+
+extern "C" int rf_norm_linear_batch(int nl, const uint16_t* const* x, int64_t ldx, const float* const* ssq, int64_t P,
+                                    int64_t H, float eps, const uint16_t* const* w, int64_t N, uint16_t* const* out,
+                                    int64_t ldo, hipStream_t stream) {
+  if (nl < 1 || nl > MAXL) return fail(RF_EINVAL_ARG, "rf_norm_linear_batch: %d layers (1 .. %d)", nl, MAXL);
+  if (!x || !ssq || !w || !out) return fail(RF_EINVAL_ARG, "rf_norm_linear_batch: null pointer");
+  if (P < 0 || P > (1ll << 30) || H <= 0 || H % SSQ_COLS || N <= 0 || N % BN)
+    return fail(RF_EINVAL_SHAPE, "rf_norm_linear_batch: P %lld, H %lld (multiple of 256), N %lld (multiple of 256)",
+                (long long)P, (long long)H, (long long)N);
+  if (ldx < H || ldx % 8 || ldx > (1 << 21) || ldo < N || ldo % 8)
+    return fail(RF_EINVAL_SHAPE, "rf_norm_linear_batch: strides ldx %lld, ldo %lld", (long long)ldx, (long long)ldo);
+  if (!(eps >= 0.f)) return fail(RF_EINVAL_ARG, "rf_norm_linear_batch: eps");
+  if (static_cast<int64_t>(nl) * grid_of(P, N) > (1ll << 30))
+    return fail(RF_EINVAL_SHAPE, "rf_norm_linear_batch: too many tiles");
+  LinLayers ll{};
+  for (int l = 0; l < nl; ++l) {
+    if (!x[l] || !ssq[l] || !w[l] || !out[l]) return fail(RF_EINVAL_ARG, "rf_norm_linear_batch: null pointer for layer %d", l);
+    if (!aligned16(x[l]) || !aligned16(w[l]) || !aligned16(out[l]))
+      return fail(RF_EINVAL_SHAPE, "rf_norm_linear_batch: layer %d pointers must be 16-byte aligned", l);
+    ll.x[l] = x[l];
+    ll.ssq[l] = ssq[l];
+    ll.w[l] = w[l];
+    ll.out[l] = out[l];
+  }
+  if (P == 0) return RF_OK;
+  if (persistent_lin_ok(H)) {
+    hipLaunchKernelGGL(k_norm_linear_p, dim3(persistent_grid(nl * static_cast<int64_t>(grid_of(P, N)))), dim3(NTHR), 0,
+                       stream, ll, nl, ldx, ldo, static_cast<int>(P), static_cast<int>(N), static_cast<int>(H), eps);
+  } else {                                          // other widths: the per-tile kernel, one launch per layer
+    for (int l = 0; l < nl; ++l)
+      hipLaunchKernelGGL(k_norm_linear, dim3(grid_of(P, N)), dim3(NTHR), 0, stream, ll.x[l], ldx, ll.w[l],
+                         static_cast<int>(P), static_cast<int>(N), static_cast<int>(H), ll.ssq[l], eps, ll.out[l], ldo);
+  }
+  return check_launch("rf_norm_linear_batch");
 }

@@ -42,6 +42,7 @@ SIGNATURES = {
                          _P, _P, _I64, _I64, _I64, _I64, _P, _SZ, _P],
     "rf_rope_kv_write": [_P, _I64, _P, _I64, _I64, _I32, _I32, _P, _I32, _P, _P, _I64, _I64, _I64, _I64, _P],
     "rf_norm_linear": [_P, _I64, _P, _I64, _I64, _F32, _P, _I64, _P, _I64, _P, _SZ, _P],
+    "rf_norm_linear_batch": [_I32, _PP, _I64, _PP, _I64, _I64, _F32, _PP, _I64, _PP, _I64, _P],
     "rf_gdn_fill": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
     "rf_gdn_fill_batch": [_P, _I32, _I64, _I32, _I32, _I32, _I32, _P, _SZ, _P],
     "rf_gdn_workspace_bytes": [_I64, _I32, _I32, _I32, _I32, _PSZ],

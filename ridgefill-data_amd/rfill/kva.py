@@ -480,13 +480,13 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
 
     gbuf = []
 
-    def can_group(i):                                   # attention layers filled by their maps, no computed rows
-        return not computed and model.layer_types[i] == "attn" and fills[i] == "proj"
+    def can_group(i):                                   # layers filled by their maps, no computed rows
+        return not computed and fills[i] == "proj"
 
     def run_group(ids):
-        """The maps of several attention layers in one launch, then their K / V fills in one launch (the GEMMs
-        fill whole waves of the GPU with no tail per layer); each layer's results are bit-identical to its
-        unsplit map apply and fill alone."""
+        """The maps of several late layers in one launch (the GEMM fills whole waves of the GPU, with no tail
+        per layer), then the group's attention layers' K / V fills in one launch and its GDN layers' fills in
+        consecutive pairs; each layer's results are bit-identical to its unsplit map apply and fill alone."""
         while len(gbuf) < len(ids):
             gbuf.append((torch.empty(P, H, dtype=torch.bfloat16, device=dev),
                          torch.empty(P, ops.ssq_parts(H), dtype=torch.float32, device=dev)))
@@ -498,7 +498,18 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
                 if row_inputs is not None:
                     row_inputs[i] = hri
                 ops.row_scatter(x, q, rows, hri)
-        model.fill_attn_batch(ids, xs, pos, cache, ssqs=ss, cs=cs)
+        attn = [k for k, i in enumerate(ids) if model.layer_types[i] == "attn"]
+        if attn:
+            model.fill_attn_batch([ids[k] for k in attn], [xs[k] for k in attn], pos, cache,
+                                  ssqs=[ss[k] for k in attn], cs=cs)
+        k = 0
+        while k < len(ids):
+            if model.layer_types[ids[k]] != "gdn":
+                k += 1
+                continue
+            m = 2 if k + 1 < len(ids) and model.layer_types[ids[k + 1]] == "gdn" else 1
+            model.fill_batch(ids[k:k + m], xs[k:k + m], cache, ssqs=ss[k:k + m])
+            k += m
 
     if overlap:
         two_stream(layers, produce, consume, dev)

@@ -252,10 +252,23 @@ class FillModel:
         ops.norm_linear(x[P - 3:], ssq[P - 3:], self.eps, W[:nq], out=pre[P - 3:, :nq])
         return pre
 
+    def _fill_rows_batch(self, ws, xs, ssqs):
+        """_fill_rows of several GDN layers over the same rows: their k | v | b | a projections in one launch
+        (ops.norm_linear_batch), bit-identical to _fill_rows of each alone."""
+        P = xs[0].shape[0]
+        nq = self.nk * self.dk
+        if nq % 256 or P <= 3 or len(ws) == 1 or any(x.stride(0) != xs[0].stride(0) for x in xs):
+            return [self._fill_rows(w, x, q) for w, x, q in zip(ws, xs, ssqs)]
+        pres = [torch.empty(P, w["w_in"].shape[0], dtype=torch.bfloat16, device=xs[0].device) for w in ws]
+        ops.norm_linear_batch(xs, ssqs, self.eps, [w["w_in"][nq:] for w in ws], [p[:, nq:] for p in pres])
+        for w, x, q, pre in zip(ws, xs, ssqs, pres):
+            ops.norm_linear(x[P - 3:], q[P - 3:], self.eps, w["w_in"][:nq], out=pre[P - 3:, :nq])
+        return pres
+
     def fill_batch(self, ids, xs, cache, ssqs=None):
-        """fill() of up to ops.GDN_BATCH_MAX GDN layers over the same rows at once: their in-projections one after
-        another, then one batched delta-rule fill (rf_gdn_fill_batch), so the layers' sequential chunk scans run
-        side by side. Every layer's conv and recurrent state is bit-identical to fill() of it alone."""
+        """fill() of up to ops.GDN_BATCH_MAX GDN layers over the same rows at once: their in-projections in one launch
+        (_fill_rows_batch), then one batched delta-rule fill (rf_gdn_fill_batch), so the layers' sequential chunk
+        scans run side by side. Every layer's conv and recurrent state is bit-identical to fill() of it alone."""
         ids = list(ids)
         if not 1 <= len(ids) <= ops.GDN_BATCH_MAX or any(self.layer_types[i] != "gdn" for i in ids):
             raise ValueError(f"fill_batch: 1 .. {ops.GDN_BATCH_MAX} GDN layers, got {ids}")
@@ -264,11 +277,11 @@ class FillModel:
             raise ValueError("fill_batch: every layer takes the same rows")
         if P == 0:
             return
-        ssqs = [None] * len(ids) if ssqs is None else ssqs
+        ssqs = [ops.row_ssq(x) if q is None else q for x, q in zip(xs, ssqs or [None] * len(ids))]
+        pres = self._fill_rows_batch([self._layer(i, "gdn") for i in ids], xs, ssqs)
         jobs = []
-        for i, x, ssq in zip(ids, xs, ssqs):
+        for i, x, ssq, pre in zip(ids, xs, ssqs, pres):
             w = self._layer(i, "gdn")
-            pre = self._fill_rows(w, x, ops.row_ssq(x) if ssq is None else ssq)
             c = cache[i]
             rec = c.get("rec")
             rec = (torch.zeros(self.nv, self.dk, self.dv, dtype=torch.float32, device=x.device) if rec is None

@@ -182,3 +182,42 @@ def test_fill_late_groups_equal_per_layer(dev):
         assert cache[i]["n"] == P
         assert torch.equal(cache[i]["k"], kb[:, :P]), f"layer {i}: K differs"
         assert torch.equal(cache[i]["v"], vb[:, :P]), f"layer {i}: V differs"
+
+
+def test_fill_late_hybrid_groups_equal_per_layer(dev):
+    """A hybrid late stack (GDN, GDN, GDN, attention, GDN, GDN) at width 1024 filled by fill_late's grouped
+    schedule (one map launch per group, paired GDN fills with one in-projection launch, batched attention
+    fills) against per-layer unsplit launches: every GDN conv and recurrent state and the attention layer's K
+    / V bitwise equal."""
+    from fill_cases import hybrid_config, hybrid_tensors
+    from rfill import ops
+    from rfill.kva import Arm, Projector, fill_late
+    from rfill.model import FillModel
+    kinds = ["gdn", "gdn", "gdn", "attn", "gdn", "gdn"]
+    cfg = hybrid_config(kinds, hidden=1024)
+    t = hybrid_tensors(cfg, seed=29)
+    H, L, N, tail = cfg["hidden_size"], len(kinds), 2600, 100
+    P = N - tail
+    late = list(range(L))
+    Wl, Bl = _maps(H, late, 30)
+    W, B = dict(zip(late, Wl)), dict(zip(late, Bl))
+    h = inputs(N, H, seed=31).to(dev)
+    m = FillModel(cfg, t, dev)
+    arm = Arm("ridgefill", split=0, tail=tail, fill="proj", projector=Projector(0, W, B))
+    cache, _ = fill_late(m, h, arm)
+    torch.cuda.synchronize()
+    ref = m.new_cache()
+    pos = torch.arange(P, device=dev)
+    for i in late:
+        x, s = ops.map_apply(h[:P], W[i].to(dev), B[i].to(dev))
+        if kinds[i] == "attn":
+            w = m.W[i]
+            kb = torch.zeros(m.n_kv, P + 64, m.head_dim, dtype=torch.bfloat16, device=dev)
+            vb = kb.clone()
+            ops.norm_kv_write(x, s, m.eps, w["wkv"], m.n_kv, m.head_dim, w.get("k_norm"), m.knorm_kind,
+                              m.rope_table(pos), kb, vb, 0)
+            assert torch.equal(cache[i]["k"], kb[:, :P]) and torch.equal(cache[i]["v"], vb[:, :P]), f"layer {i}"
+        else:
+            m.fill(i, x, pos, ref, ssq=s)
+            assert torch.equal(cache[i]["conv"], ref[i]["conv"]), f"layer {i}: conv state differs"
+            assert torch.equal(cache[i]["rec"], ref[i]["rec"]), f"layer {i}: recurrent state differs"
