@@ -223,7 +223,11 @@ int rf_norm_linear(const uint16_t* x, int64_t ldx, const float* ssq, int64_t P, 
  * Qwen35.fill (model.py:510-523). Needs dk = dv = 128, nv % nk == 0, ld % 8 == 0 and 16-byte aligned
  * pre, conv_w, conv_in and workspace. The workspace (caller-owned device memory) holds the per-chunk
  * products between the two kernels; a workspace of rf_gdn_workspace_bytes(P, ...) does the fill in one
- * pass, a smaller one (at least one chunk's worth) in several passes with the same result. */
+ * pass, a smaller one (at least one chunk's worth) in several passes with the same result. A workspace of
+ * two or more chunks is used as two halves: the prep of the next pass runs on a second stream the library
+ * keeps per device (default priority) beside the scan of the current pass on `stream`, ordered by events;
+ * `stream` waits for all of it, so work queued after the call on `stream` sees the finished fill. Results
+ * are bit-identical to the one-stream schedule. */
 int rf_gdn_fill(const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int dk, int dv, const uint16_t* conv_w,
                 const uint16_t* conv_in, uint16_t* conv_out, const float* a_log, const float* dt_bias, float* state,
                 void* workspace, size_t ws_bytes, hipStream_t stream);

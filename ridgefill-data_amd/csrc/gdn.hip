@@ -161,8 +161,10 @@ struct PrepBatch {
   PrepArgs a[BATCH];
 };
 
+// At most 128 VGPRs and no AGPRs (130 allocated as 136): two prep blocks fit on a CU beside one scan block
+// (240 registers per SIMD), so the fill's prep of the next pass runs alongside the scan.
 template <bool OUT>
-__global__ __launch_bounds__(256) void k_gdn_prep(PrepBatch pb) {
+__global__ __launch_bounds__(256) __attribute__((amdgpu_num_vgpr(128))) void k_gdn_prep(PrepBatch pb) {
   const PrepArgs a = blockIdx.z == 0 ? pb.a[0] : pb.a[1];
   __shared__ __align__(16) uint16_t k_s[CH * KST];  // the k tile, then T (fp32)
   __shared__ __align__(16) uint16_t v_s[CH * KST];
@@ -643,6 +645,11 @@ __global__ __launch_bounds__(256) void k_gdn_scan(ScanBatch sbatch) {
     load_part(b0, src(0), part, cb, w, lane);
     load_part(b1, src(1), part, cb, w, lane);
   }
+  // Wait for the two prologue chunks here, once. The compiler may issue the prologue loads in any order
+  // (chunk 0's first operands last), and the wait counts at the loop head merge that entry with the back
+  // edge: without this wait every step would start with a wait for all but the newest few loads, which
+  // leaves the chunk-ahead loads no time in flight.
+  __builtin_amdgcn_s_waitcnt(0x0f70);               // vmcnt(0)
   for (int c = 0; c < a.chunks; c += 3) {
     step(b0, b2, src(c + 2), true, c);
     step(b1, b0, src(c + 3), c + 1 < a.chunks, c + 1);
@@ -813,10 +820,111 @@ struct LayerIO {
   float* state;
 };
 
-// The fill (out null) or the forward (one layer, out given) of n layers over the same P rows: per pass of up to
-// what each layer's share of the workspace holds, one prep and one scan launch cover every layer.
+constexpr int MAX_DEVICES = 64;
+
+// A second stream per device (default priority) for the fill's prep launches, and the events that order
+// them against the scans on the caller's stream; made on first use with that device current and kept.
+struct SideQueue {
+  bool tried = false;
+  hipStream_t stream = nullptr;
+  hipEvent_t start = nullptr;
+  hipEvent_t prepped[2] = {nullptr, nullptr};       // prep of the pass in buffer b written
+  hipEvent_t scanned[2] = {nullptr, nullptr};       // scan of the pass in buffer b done reading
+};
+
+std::mutex g_side_mu;
+SideQueue g_side[MAX_DEVICES];
+
+// The current device's side queue (g_side_mu held), or null when it cannot be made or the caller's stream
+// belongs to another device: the fill then runs both kernels on the caller's stream.
+SideQueue* side_queue(hipStream_t stream) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) {
+    (void)hipGetLastError();
+    return nullptr;
+  }
+  if (stream) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice(stream, &sdev) != hipSuccess || sdev != dev) {
+      (void)hipGetLastError();
+      return nullptr;
+    }
+  }
+  SideQueue& q = g_side[dev];
+  if (!q.tried) {
+    q.tried = true;
+    bool ok = hipStreamCreateWithFlags(&q.stream, hipStreamNonBlocking) == hipSuccess;
+    ok = ok && hipEventCreateWithFlags(&q.start, hipEventDisableTiming) == hipSuccess;
+    for (int b = 0; b < 2; ++b) {
+      ok = ok && hipEventCreateWithFlags(&q.prepped[b], hipEventDisableTiming) == hipSuccess;
+      ok = ok && hipEventCreateWithFlags(&q.scanned[b], hipEventDisableTiming) == hipSuccess;
+    }
+    if (!ok) {
+      (void)hipGetLastError();
+      q.stream = nullptr;                           // handles made before the failure are kept, unused
+    }
+  }
+  return q.stream ? &q : nullptr;
+}
+
+int conv_tails(const char* fn, const LayerIO* io, int n, int64_t P, int C, hipStream_t stream) {
+  for (int l = 0; l < n; ++l) {
+    hipLaunchKernelGGL(k_conv_tail, dim3((3 * C + 255) / 256), dim3(256), 0, stream, io[l].pre, io[l].ld, P, C,
+                       io[l].conv_in, io[l].conv_out);
+    if (const int e = check_launch(fn)) return e;
+  }
+  return RF_OK;
+}
+
+int hip_check(const char* fn, hipError_t e, const char* what) {
+  return e == hipSuccess ? RF_OK : fail(RF_EHIP, "%s: %s: %s", fn, what, hipGetErrorString(e));
+}
+
+// The fill of n layers as one pipeline of passes (every pass of layer 0, then of layer 1, ...) through two
+// workspace buffers: the scan of pass i (the caller's stream) runs while the prep of pass i + 1 (the side
+// stream) writes the other buffer. A scan block (one per CU, one wave per SIMD) leaves room on its CU for
+// two prep blocks; the two kernels slow each other (the scan's chunk steps wait on memory behind the
+// prep's traffic), so the gain over one stream is about a tenth for one layer, and two layers do better
+// with their scans side by side in one launch (gdn_run's batched passes). Pass
+// i's prep waits for the scan of pass i - 2 (its buffer's last reader); the caller's stream waits for every
+// prep through the scans, so work queued after the fill on that stream is ordered after all of it. Every
+// chunk runs the same arithmetic as in the one-stream schedule: the results are bit-identical.
+int fill_overlapped(const char* fn, SideQueue& q, const LayerIO* io, int n, int64_t P, int nk, int nv, int C,
+                    uint8_t* ws, int64_t per_pass, size_t half, uint32_t cbytes, uint32_t sbytes, hipStream_t stream) {
+  const int64_t chunks = (P + CH - 1) / CH;
+  if (const int e = hip_check(fn, hipEventRecord(q.start, stream), "hipEventRecord")) return e;
+  if (const int e = hip_check(fn, hipStreamWaitEvent(q.stream, q.start, 0), "hipStreamWaitEvent")) return e;
+  int64_t item = 0;
+  for (int l = 0; l < n; ++l) {
+    const LayerIO& L = io[l];
+    for (int64_t c0 = 0; c0 < chunks; c0 += per_pass, ++item) {
+      const int nc = static_cast<int>(std::min<int64_t>(per_pass, chunks - c0));
+      const int b = static_cast<int>(item & 1);
+      uint8_t* wb = ws + b * half;
+      if (item >= 2)
+        if (const int e = hip_check(fn, hipStreamWaitEvent(q.stream, q.scanned[b], 0), "hipStreamWaitEvent")) return e;
+      PrepBatch pb{};
+      pb.a[0] = PrepArgs{L.pre, L.ld, P, c0 * CH, nk, nv, C, L.conv_w, L.conv_in, L.a_log, L.dt_bias, wb, cbytes, sbytes};
+      hipLaunchKernelGGL(k_gdn_prep<false>, dim3(nc, nv, 1), dim3(256), 0, q.stream, pb);
+      if (const int e = check_launch(fn)) return e;
+      if (const int e = hip_check(fn, hipEventRecord(q.prepped[b], q.stream), "hipEventRecord")) return e;
+      if (const int e = hip_check(fn, hipStreamWaitEvent(stream, q.prepped[b], 0), "hipStreamWaitEvent")) return e;
+      ScanBatch sb{};
+      sb.a[0] = ScanArgs{wb, cbytes, nc, nk, nv, L.state, wb, sbytes};
+      hipLaunchKernelGGL(k_gdn_scan<false>, dim3(nv * 8), dim3(256), 0, stream, sb);
+      if (const int e = check_launch(fn)) return e;
+      if (const int e = hip_check(fn, hipEventRecord(q.scanned[b], stream), "hipEventRecord")) return e;
+    }
+  }
+  return RF_OK;
+}
+
+// The fill (out null) or the forward (one layer, out given) of n layers over the same P rows. The fill with
+// `overlap` runs fill_overlapped when the workspace holds two chunks (and the side queue exists); otherwise,
+// per pass of up to what each layer's share of the workspace holds, one prep and one scan launch cover every
+// layer on the caller's stream.
 int gdn_run(const char* fn, const LayerIO* io, int n, int64_t P, int nk, int nv, int dk, int dv, uint16_t* out,
-            int64_t ldo, void* workspace, size_t ws_bytes, hipStream_t stream) {
+            int64_t ldo, void* workspace, size_t ws_bytes, hipStream_t stream, bool overlap = false) {
   if (n < 1 || n > BATCH || (out && n != 1)) return fail(RF_EINVAL_ARG, "%s: %d layers (1 .. %d)", fn, n, BATCH);
   if (!workspace) return fail(RF_EINVAL_ARG, "%s: null workspace", fn);
   if (const int e = check_heads(fn, nk, nv, dk, dv)) return e;
@@ -842,14 +950,28 @@ int gdn_run(const char* fn, const LayerIO* io, int n, int64_t P, int nk, int nv,
   const uint64_t cb64 = sbytes + (out ? static_cast<uint64_t>(nv) * OUT_HEAD_BYTES : 0);
   if (cb64 > 0x7fffffffull) return fail(RF_EINVAL_SHAPE, "%s: %d value heads", fn, nv);
   const uint32_t cbytes = static_cast<uint32_t>(cb64);
+  const int64_t chunks = (P + CH - 1) / CH;
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  if (overlap && !out && chunks > 0) {
+    // two buffers, each of up to what half the workspace holds (buffer offsets below 2^31)
+    const size_t half = ws_bytes / 2 / 16 * 16;
+    const int64_t pp = std::min<int64_t>(static_cast<int64_t>(half / cbytes), 0x7fffffffll / cbytes);
+    if (pp >= 1) {
+      std::lock_guard<std::mutex> lock(g_side_mu);
+      if (SideQueue* q = side_queue(stream)) {
+        if (const int e = fill_overlapped(fn, *q, io, n, P, nk, nv, static_cast<int>(C), ws, pp, half, cbytes, sbytes,
+                                          stream))
+          return e;
+        return conv_tails(fn, io, n, P, static_cast<int>(C), stream);
+      }
+    }
+  }
   // each layer's share of the workspace (16-byte aligned); chunks per pass: what a share holds, with buffer
   // offsets below 2^31
   const size_t share = ws_bytes / n / 16 * 16;
   const int64_t per_pass = std::min<int64_t>(static_cast<int64_t>(share / cbytes), 0x7fffffffll / cbytes);
   if (per_pass < 1)
     return fail(RF_EINVAL_ARG, "%s: workspace %zu bytes < %d chunks (%u bytes each)", fn, ws_bytes, n, cbytes);
-  const int64_t chunks = (P + CH - 1) / CH;
-  uint8_t* ws = static_cast<uint8_t*>(workspace);
   for (int64_t c0 = 0; c0 < chunks; c0 += per_pass) {
     const int nc = static_cast<int>(std::min<int64_t>(per_pass, chunks - c0));
     PrepBatch pb{};
@@ -876,12 +998,7 @@ int gdn_run(const char* fn, const LayerIO* io, int n, int64_t P, int nk, int nv,
       if (const int e = check_launch(fn)) return e;
     }
   }
-  for (int l = 0; l < n; ++l) {
-    hipLaunchKernelGGL(k_conv_tail, dim3((3 * C + 255) / 256), dim3(256), 0, stream, io[l].pre, io[l].ld, P,
-                       static_cast<int>(C), io[l].conv_in, io[l].conv_out);
-    if (const int e = check_launch(fn)) return e;
-  }
-  return RF_OK;
+  return conv_tails(fn, io, n, P, static_cast<int>(C), stream);
 }
 
 }  // namespace
@@ -890,7 +1007,7 @@ extern "C" int rf_gdn_fill(const uint16_t* pre, int64_t ld, int64_t P, int nk, i
                            const uint16_t* conv_w, const uint16_t* conv_in, uint16_t* conv_out, const float* a_log,
                            const float* dt_bias, float* state, void* workspace, size_t ws_bytes, hipStream_t stream) {
   const LayerIO io{pre, ld, conv_w, conv_in, conv_out, a_log, dt_bias, state};
-  return gdn_run("rf_gdn_fill", &io, 1, P, nk, nv, dk, dv, nullptr, 0, workspace, ws_bytes, stream);
+  return gdn_run("rf_gdn_fill", &io, 1, P, nk, nv, dk, dv, nullptr, 0, workspace, ws_bytes, stream, true);
 }
 
 extern "C" int rf_gdn_fill_batch(const rf_gdn_layer* layers, int n_layers, int64_t P, int nk, int nv, int dk, int dv,
@@ -903,7 +1020,10 @@ extern "C" int rf_gdn_fill_batch(const rf_gdn_layer* layers, int n_layers, int64
     const rf_gdn_layer& L = layers[l];
     io[l] = LayerIO{L.pre, L.ld, L.conv_w, L.conv_in, L.conv_out, L.a_log, L.dt_bias, L.state};
   }
-  return gdn_run("rf_gdn_fill_batch", io, n_layers, P, nk, nv, dk, dv, nullptr, 0, workspace, ws_bytes, stream);
+  // two layers: their scans side by side in one launch (two blocks per CU) beat one layer's scan beside the
+  // next pass's prep
+  return gdn_run("rf_gdn_fill_batch", io, n_layers, P, nk, nv, dk, dv, nullptr, 0, workspace, ws_bytes, stream,
+                 n_layers == 1);
 }
 
 // ---- allocation-free GDN fill: the per-chunk workspace lives in a file-scope device array
@@ -911,7 +1031,6 @@ extern "C" int rf_gdn_fill_batch(const rf_gdn_layer* layers, int n_layers, int64
 namespace {
 
 constexpr size_t GDN_SCRATCH_BYTES = static_cast<size_t>(RF_GDN_SCRATCH_MAX) << 20;
-constexpr int MAX_DEVICES = 64;
 
 // The workspace of rf_gdn_fill_noalloc: one copy per GPU (at its own address), held until the process ends.
 // Its name is a host-side stand-in: host code uses only the per-device addresses taken below.
