@@ -300,6 +300,169 @@ __global__ __launch_bounds__(NTHR) void k_gemm_partial(const uint16_t* __restric
   store_partial(part + static_cast<int64_t>(sp) * M * N, N, M, tm * BM, tn * BN, acc);
 }
 
+// ---- split partials of products with few rows (M <= ROWS_MAX): the exact rows' projections.
+//
+// A 256 x 256 tile wastes most of its MFMA work and its weight reads on a few hundred rows. Here a block
+// takes every row of its row block (RT row tiles of 32, MT = 32 RT <= 160 rows, row blocks of about equal
+// size) against RN = 256 weight rows, over its split's K range. Wave w computes output columns
+// n0 + 64w .. + 63 for all MT rows (2 x RT accumulators: per 16-deep slice RT + 2 fragment reads feed 2 RT
+// MFMAs). Operands stream through an LDS ring of S stages (one 64-deep K step each: MT activation rows,
+// then the 256 weight rows, 128-byte rows with the slot swizzle) filled straight from memory by
+// buffer_load ... lds, S - 1 steps ahead; one wait and one barrier per step. The products are k_gemm_partial's: the same MFMA, the
+// weight fragment as its first operand, K in the same order, so a split's partial sums are bit-identical
+// to the 256 x 256 path over the same K range (and with one split, to the unsplit kernels' sums).
+constexpr int RN = 256;
+constexpr int64_t ROWS_MAX = 512;
+
+template <int RT>
+struct RowsCfg {
+  static constexpr int MT = 32 * RT;
+  static constexpr int ROWS = MT + RN;              // stage rows
+  static constexpr int STAGE_U4 = ROWS * CPR;
+  static constexpr int S = (LDS_U4 / STAGE_U4) < 6 ? (LDS_U4 / STAGE_U4) : 6;
+  static constexpr int L = ROWS / 32;               // loads per wave per stage (8 rows of 128 bytes each)
+};
+
+// s_waitcnt vmcnt <= n * L (lgkmcnt 0) for a run-time n in [0, 4]
+template <int L>
+__device__ __forceinline__ void wait_steps(int n) {
+  switch (n) {
+    case 0: wait_vm_lgkm0<0>(); break;
+    case 1: wait_vm_lgkm0<L>(); break;
+    case 2: wait_vm_lgkm0<2 * L>(); break;
+    case 3: wait_vm_lgkm0<3 * L>(); break;
+    default: wait_vm_lgkm0<4 * L>(); break;
+  }
+}
+
+template <int RT>
+__device__ __forceinline__ void rows_partial(const uint16_t* __restrict__ X, int64_t ldx, const uint16_t* __restrict__ W,
+                                             int64_t ldw, int M, int N, int K, int kper, int rblocks,
+                                             float* __restrict__ part, uint4* lds) {
+  using C = RowsCfg<RT>;
+  static_assert(C::S >= 3 && (C::S - 2) * C::L < 64, "ring depth");
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  // block -> (row block, column block, split), row blocks fastest over a contiguous run of logical blocks
+  // per XCD: the row blocks of one column block run together on one XCD, so its weight rows are read
+  // from memory once and meet in that XCD's L2
+  const int cblocks = N / RN;
+  const int u = xcd_tile(blockIdx.x, gridDim.x);
+  const int rbk = u % rblocks, rest = u / rblocks;
+  const int cb = rest % cblocks, sp = rest / cblocks;
+  // row blocks of about equal size, each a whole number of row tiles
+  const int per = (M + rblocks - 1) / rblocks;
+  const int m0 = rbk * per, rows_x = max(0, min(M - m0, per));
+  const int n0 = cb * RN;
+  const int kbeg = sp * kper, klen = max(0, min(K - kbeg, kper));
+  const int nk = klen / BK;
+  const __amdgpu_buffer_rsrc_t rx = buffer_rsrc(X + static_cast<int64_t>(m0) * ldx + kbeg,
+                                                static_cast<uint32_t>(rows_x * ldx * 2));
+  const __amdgpu_buffer_rsrc_t rw = buffer_rsrc(W + static_cast<int64_t>(n0) * ldw + kbeg,
+                                                static_cast<uint32_t>(RN * ldw * 2));
+  // load i of this wave: stage rows 8 (4 i + w) .. + 7 (activation rows below MT, then weight rows);
+  // lane L fetches row + L / 8, logical chunk (L % 8) ^ slot_swz(row) into physical chunk L % 8
+  uint32_t voff[C::L];
+#pragma unroll
+  for (int i = 0; i < C::L; ++i) {
+    const int r = 8 * (4 * i + w) + (lane >> 3);
+    const int ch = (lane & 7) ^ slot_swz(r);
+    voff[i] = r < C::MT ? static_cast<uint32_t>((r * ldx + ch * 8) * 2)
+                        : static_cast<uint32_t>(((r - C::MT) * ldw + ch * 8) * 2);
+  }
+  char* base = reinterpret_cast<char*>(lds);
+  auto issue_one = [&](int kt, int st, int i) {
+    const int j = 4 * i + w;                        // wave-uniform
+    lds_ptr dst = (lds_ptr)(base + st * (C::STAGE_U4 * 16) + j * 1024);
+    if (8 * j < C::MT) __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, dst, 16, voff[i], kt * BK * 2, 0, 0);
+    else __builtin_amdgcn_raw_ptr_buffer_load_lds(rw, dst, 16, voff[i], kt * BK * 2, 0, 0);
+  };
+  auto issue = [&](int kt, int st) {
+#pragma unroll
+    for (int i = 0; i < C::L; ++i) issue_one(kt, st, i);
+  };
+
+  f32x16 acc[2][RT];
+#pragma unroll
+  for (int c = 0; c < 2; ++c)
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[c][rt][r] = 0.f;
+
+  const int lr = lane & 31, lk = lane >> 5, swz = slot_swz(lr);
+  bf16x8 fa[2][RT], fb[2][2];
+  // fragment r of slice ks of the step in stage st into buffer b: activation row tile r (r < RT), else
+  // this wave's weight rows 32 (r - RT) .. + 31
+  auto read = [&](int st, int ks, int b, int r) {
+    const int ch = (ks * 2 + lk) ^ swz;
+    const uint4* s = lds + st * C::STAGE_U4;
+    if (r < RT) fa[b][r] = as_frag(s[(r * 32 + lr) * CPR + ch]);
+    else fb[b][r - RT] = as_frag(s[(C::MT + 64 * w + 32 * (r - RT) + lr) * CPR + ch]);
+  };
+
+  for (int kt = 0; kt < C::S - 1; ++kt)
+    if (kt < nk) issue(kt, kt);
+  int st = 0;                                       // stage of step kt
+  for (int kt = 0; kt < nk; ++kt) {
+    wait_steps<C::L>(min(C::S - 2, nk - 1 - kt));   // this step's loads (every wave's, after the barrier)
+    __builtin_amdgcn_s_barrier();                   // and every wave is done with step kt - 1's stage
+    // step kt + S - 1 into the stage step kt - 1 left, one load after every other MFMA below (a burst of
+    // loads fills the texture units' queue, and the wave's in-order issue then stalls its MFMAs)
+    const bool more = kt + C::S - 1 < nk;
+    const int lkt = kt + C::S - 1, lst = st == 0 ? C::S - 1 : st - 1;
+#pragma unroll
+    for (int r = 0; r < RT + 2; ++r) read(st, 0, 0, r);
+    // slice ks: its 2 RT MFMAs, one read of slice ks + 1's fragments after each (the LDS reads run under
+    // the MFMAs instead of ahead of them)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const int b = ks & 1;
+#pragma unroll
+      for (int q = 0; q < 2 * RT; ++q) {
+        acc[q / RT][q % RT] =
+            __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[b][q / RT], fa[b][q % RT], acc[q / RT][q % RT], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ks < 3 && q < RT + 2) read(st, ks + 1, b ^ 1, q);
+        const int g = ks * 2 * RT + q;              // MFMA index in the step
+        if (more && !(g & 1) && (g >> 1) < C::L) issue_one(lkt, lst, g >> 1);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#pragma unroll
+      for (int r = 2 * RT; r < RT + 2; ++r)           // RT = 1: the third fragment
+        if (ks < 3) read(st, ks + 1, b ^ 1, r);
+    }
+    // loads left over when the step has fewer than 2 L MFMAs
+#pragma unroll
+    for (int i = 4 * RT; i < C::L; ++i)
+      if (more) issue_one(lkt, lst, i);
+    st = st + 1 == C::S ? 0 : st + 1;
+  }
+  wait_vm_lgkm0<0>();
+  // lane (lr, lk) holds row 32 rt + lr, columns 64 w + 32 c + 8 g + 4 lk + e (e < 4) of accumulator (c, rt)
+  float* pp = part + static_cast<int64_t>(sp) * M * N;
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) {
+    const int r = rt * 32 + lr;
+    if (r >= rows_x) continue;
+    float* row = pp + static_cast<int64_t>(m0 + r) * N + n0 + 64 * w + 4 * lk;
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4*>(row + 32 * c + 8 * g) =
+            make_float4(acc[c][rt][4 * g], acc[c][rt][4 * g + 1], acc[c][rt][4 * g + 2], acc[c][rt][4 * g + 3]);
+  }
+}
+
+template <int RT>
+__global__ __launch_bounds__(NTHR) void k_rows_partial(const uint16_t* __restrict__ X, int64_t ldx,
+                                                       const uint16_t* __restrict__ W, int64_t ldw, int M, int N,
+                                                       int K, int kper, int rblocks, float* __restrict__ part) {
+  __shared__ uint4 lds[RowsCfg<RT>::S * RowsCfg<RT>::STAGE_U4];
+  rows_partial<RT>(X, ldx, W, ldw, M, N, K, kper, rblocks, part, lds);
+}
+
 // The split sums of 8 consecutive columns col .. col + 7 of row gm: 8 fp32 values, splits added in order.
 __device__ __forceinline__ void split_sums(const float* __restrict__ part, int splits, int64_t plane, int64_t off,
                                            float (&v)[8]) {
@@ -1496,12 +1659,23 @@ int split_count(int64_t M, int64_t N, int64_t K) {
 // `splits` ways (k_gemm_partial + a reduce kernel) when splits > 1. Too few tiles for the GPU: all rows
 // split. Otherwise, when whole tile rows fill the waves (N / 256 divides 256) and the last wave is at
 // most half full, its tile rows are split, so that wave takes a fraction of a tile's time.
+// Products of at most ROWS_MAX rows take k_rows_partial (rt row tiles per row block, rblocks row blocks)
+// for every row, split so that about one block runs per CU, then the reduce epilogue.
 struct Plan {
   int64_t m_fused;
   int splits;
+  int rt = 0;
+  int rblocks = 0;
+  bool split() const { return splits > 1 || rt > 0; }
 };
 
 Plan plan(int64_t M, int64_t N, int64_t K) {
+  if (M <= ROWS_MAX && N % RN == 0) {
+    const int64_t rb = (M + 159) / 160, per = (M + rb - 1) / rb;
+    const int64_t blocks = rb * (N / RN);
+    const int64_t s = std::max<int64_t>(1, std::min<int64_t>(std::min<int64_t>(256 / blocks, K / 512), 16));
+    return Plan{0, static_cast<int>(s), static_cast<int>((per + 31) / 32), static_cast<int>(rb)};
+  }
   const int64_t tiles_n = N / BN, trows = (M + BM - 1) / BM;
   if (trows * tiles_n < 256) {
     const int s = split_count(M, N, K);
@@ -1519,13 +1693,13 @@ Plan plan(int64_t M, int64_t N, int64_t K) {
 
 size_t split_bytes(int64_t M, int64_t N, int64_t K) {
   const Plan p = plan(M, N, K);
-  return p.splits > 1 ? static_cast<size_t>(p.splits) * (M - p.m_fused) * N * 4 : 0;
+  return p.split() ? static_cast<size_t>(p.splits) * (M - p.m_fused) * N * 4 : 0;
 }
 
 // The plan an entry point follows with this workspace: the split part only if the workspace holds it.
 Plan plan_with(int64_t M, int64_t N, int64_t K, const void* ws, size_t ws_bytes) {
   const Plan p = plan(M, N, K);
-  if (p.splits <= 1 || !ws || ws_bytes < split_bytes(M, N, K)) return Plan{M, 1};
+  if (!p.split() || !ws || ws_bytes < split_bytes(M, N, K)) return Plan{M, 1};
   return p;
 }
 
@@ -1534,6 +1708,19 @@ void launch_partials(const uint16_t* X, int64_t ldx, const uint16_t* W, int64_t 
                      const Plan& p, void* ws, hipStream_t stream) {
   const int64_t rows = M - p.m_fused;
   const int kper = static_cast<int>((K / p.splits + BK - 1) / BK * BK);
+  if (p.rt > 0) {
+    const dim3 grid(static_cast<unsigned>(N / RN * p.rblocks * p.splits));
+    const int m = static_cast<int>(rows), n = static_cast<int>(N), k = static_cast<int>(K);
+    float* out = static_cast<float*>(ws);
+    switch (p.rt) {
+      case 1: hipLaunchKernelGGL(k_rows_partial<1>, grid, dim3(NTHR), 0, stream, X, ldx, W, ldw, m, n, k, kper, p.rblocks, out); break;
+      case 2: hipLaunchKernelGGL(k_rows_partial<2>, grid, dim3(NTHR), 0, stream, X, ldx, W, ldw, m, n, k, kper, p.rblocks, out); break;
+      case 3: hipLaunchKernelGGL(k_rows_partial<3>, grid, dim3(NTHR), 0, stream, X, ldx, W, ldw, m, n, k, kper, p.rblocks, out); break;
+      case 4: hipLaunchKernelGGL(k_rows_partial<4>, grid, dim3(NTHR), 0, stream, X, ldx, W, ldw, m, n, k, kper, p.rblocks, out); break;
+      default: hipLaunchKernelGGL(k_rows_partial<5>, grid, dim3(NTHR), 0, stream, X, ldx, W, ldw, m, n, k, kper, p.rblocks, out); break;
+    }
+    return;
+  }
   hipLaunchKernelGGL(k_gemm_partial, dim3(grid_of(rows, N) * p.splits), dim3(NTHR), 0, stream, X + p.m_fused * ldx,
                      ldx, W, ldw, static_cast<int>(rows), static_cast<int>(N), static_cast<int>(K), kper,
                      static_cast<float*>(ws));
@@ -1584,7 +1771,7 @@ extern "C" int rf_map_apply(const uint16_t* b, int64_t ldb, const uint16_t* w, c
     hipLaunchKernelGGL(k_map_apply, dim3(grid_of(mf, h_out)), dim3(NTHR), 0, stream, b, ldb, w, c, x, ldx, ssq,
                        static_cast<int>(mf), static_cast<int>(h_out), static_cast<int>(h_in));
   }
-  if (pl.splits > 1) {
+  if (pl.split()) {
     launch_partials(b, ldb, w, h_in, P, h_out, h_in, pl, workspace, stream);
     hipLaunchKernelGGL(k_map_apply_reduce, reduce_grid(rows, h_out), dim3(256), 0, stream,
                        static_cast<const float*>(workspace), pl.splits, c, x + mf * ldx, ldx,
@@ -1639,7 +1826,7 @@ extern "C" int rf_norm_kv_write(const uint16_t* x, int64_t ldx, const float* ssq
     hipLaunchKernelGGL(k_norm_kv, dim3(grid_of(mf, N)), dim3(NTHR), 0, stream, x, ldx, wkv, static_cast<int>(mf),
                        static_cast<int>(N), static_cast<int>(H), a);
   }
-  if (pl.splits > 1) {
+  if (pl.split()) {
     launch_partials(x, ldx, wkv, H, P, N, H, pl, workspace, stream);
     KvArgs ar = a;                                  // the split rows: statistics, slots and table rows from mf
     ar.ssq += mf * ar.nparts;
@@ -1681,7 +1868,7 @@ extern "C" int rf_norm_q(const uint16_t* x, int64_t ldx, const float* ssq, int64
   if (mf > 0)
     hipLaunchKernelGGL(k_norm_kv, dim3(grid_of(mf, N)), dim3(NTHR), 0, stream, x, ldx, wq, static_cast<int>(mf),
                        static_cast<int>(N), static_cast<int>(H), a);
-  if (pl.splits > 1) {
+  if (pl.split()) {
     launch_partials(x, ldx, wq, H, rows, N, H, pl, workspace, stream);
     KvArgs ar = a;                                  // the split rows: statistics, outputs and positions from mf
     ar.ssq += mf * ar.nparts;
@@ -1741,7 +1928,7 @@ extern "C" int rf_norm_linear(const uint16_t* x, int64_t ldx, const float* ssq, 
     hipLaunchKernelGGL(k_norm_linear, dim3(grid_of(mf, N)), dim3(NTHR), 0, stream, x, ldx, w, static_cast<int>(mf),
                        static_cast<int>(N), static_cast<int>(H), ssq, eps, out, ldo);
   }
-  if (pl.splits > 1) {
+  if (pl.split()) {
     launch_partials(x, ldx, w, H, P, N, H, pl, workspace, stream);
     hipLaunchKernelGGL(k_norm_linear_reduce, reduce_grid(rows, N), dim3(256), 0, stream,
                        static_cast<const float*>(workspace), pl.splits, ssq + mf * (H / SSQ_COLS), static_cast<int>(H),

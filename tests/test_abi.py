@@ -44,18 +44,23 @@ def test_status_codes_match_the_header():
 
 
 def test_gemm_workspace_sizes():
-    """Host-only size rule of the GEMM entry points' split-K workspace: splits x M x N fp32 when the
-    256 x 256 tiles are too few for the GPU (splits = min(256 / tiles, K / 512, 16)), else none."""
+    """Host-only size rule of the GEMM entry points' split-K workspace: splits x M x N fp32. Products of at
+    most 512 rows (the few-rows kernel: row blocks of <= 160 rows x 256 columns)
+    always take it, splits = max(1, min(256 / blocks, K / 512, 16)); otherwise when the 256 x 256 tiles are
+    too few for the GPU (splits = min(256 / tiles, K / 512, 16)), or the last wave's tile rows, else none."""
     from rfill import ops
     assert ops.gemm_workspace_bytes(28672, 4096, 4096) == 0          # the fill: 1792 tiles, unsplit
-    assert ops.gemm_workspace_bytes(287, 4096, 4096) == 8 * 287 * 4096 * 4       # 32 tiles: 8 splits
-    assert ops.gemm_workspace_bytes(287, 24576, 4096) == 0           # 192 tiles
+    assert ops.gemm_workspace_bytes(287, 4096, 4096) == 8 * 287 * 4096 * 4       # 2 x 16 blocks: 8 splits
+    assert ops.gemm_workspace_bytes(287, 24576, 4096) == 287 * 24576 * 4         # 2 x 96 blocks: one split
+    assert ops.gemm_workspace_bytes(123, 4096, 4096) == 8 * 123 * 4096 * 4       # 1 x 16 blocks: K / 512 = 8
+    assert ops.gemm_workspace_bytes(513, 4096, 4096) == 5 * 513 * 4096 * 4       # 3 x 16 tiles of 256 x 256
     assert ops.gemm_workspace_bytes(4096, 2048, 4096) == 2 * 4096 * 2048 * 4     # the tail's K / V: 128 tiles
     # the fill's K / V: 896 tiles = 3 waves + 16 tile rows (128 tiles): those rows split 2 ways
     assert ops.gemm_workspace_bytes(28672, 2048, 4096) == 2 * 4096 * 2048 * 4
     assert ops.gemm_workspace_bytes(28672, 1024, 2048) == 0          # 48 of 64 tile rows in the last wave
     assert ops.gemm_workspace_bytes(40, 512, 2048) == 4 * 40 * 512 * 4           # K / 512 = 4 caps the splits
-    assert ops.gemm_workspace_bytes(287, 4096, 256) == 0             # too little K to split
+    assert ops.gemm_workspace_bytes(287, 4096, 256) == 287 * 4096 * 4            # few rows: one split
+    assert ops.gemm_workspace_bytes(600, 4096, 256) == 0             # too little K to split
     assert ops.gemm_workspace_bytes(0, 4096, 4096) == 0
     with pytest.raises(ValueError):
         ops.gemm_workspace_bytes(10, 100, 4096)                     # N not a multiple of 256

@@ -157,3 +157,32 @@ def test_last_wave_split(dev):
     assert torch.equal(c0[0]["k"][:, :8192], kb[:, :8192])      # the fused rows: the same kernel, the same bits
     assert rel_err(c0[0]["k"], kb[:, :P]) < TOL and rel_err(c0[0]["v"], vb[:, :P]) < TOL
     assert c0[0]["n"] == P
+
+
+@pytest.mark.parametrize("P", [1, 3, 33, 129, 160, 161, 287, 512])
+def test_few_rows_products(dev, P):
+    """Products of at most 512 rows (k_rows_partial: every row of a row block against 128 weight rows). At
+    hidden 512 the K range is one split, and the row-scaled linear is bit-identical to the unsplit kernel
+    (the same MFMA, operands and K order); at hidden 4096 (split 2 .. 8 ways) it agrees with the unsplit
+    kernel and a plain fp32 product, and nothing is written past the rows."""
+    from rfill import ops
+    g = torch.Generator().manual_seed(100 + P)
+    for H, N in ((512, 1024), (4096, 2048)):
+        xc = inputs(P, H, seed=P + H)
+        x = xc.to(dev)
+        ssq = ops.row_ssq(x)
+        w = (torch.randn(N, H, generator=g) / H ** 0.5).to(torch.bfloat16)
+        wd = w.to(dev)
+        nbytes = ops.gemm_workspace_bytes(P, N, H)
+        assert nbytes % (P * N * 4) == 0 and (nbytes == P * N * 4 if H == 512 else nbytes >= 2 * P * N * 4)
+        big = torch.full((P + 3, N), 7.0, dtype=torch.bfloat16, device=dev)
+        a = ops.norm_linear(x, ssq, 1e-6, wd, out=big[:P], workspace="auto")
+        u = ops.norm_linear(x, ssq, 1e-6, wd)
+        torch.cuda.synchronize()
+        xn = xc.float() * torch.rsqrt(xc.float().pow(2).mean(1, keepdim=True) + 1e-6)
+        ref = xn @ w.float().t()
+        print(f"P {P} H {H}: rows-kernel vs unsplit {rel_err(a, u):.2e}, vs fp32 {rel_err(a, ref):.2e}")
+        if H == 512:
+            assert torch.equal(a, u)
+        assert rel_err(a, u) < TOL and rel_err(a, ref) < TOL
+        assert bool((big[P:] == 7.0).all())
