@@ -24,7 +24,10 @@
 // next tile's score MFMAs run in the same instruction block as this tile's exponentials. (Waves of 64
 // query rows, one per SIMD, read half as much LDS per tile but measured 11 % slower: the second wave's
 // overlap matters more here than the LDS reads.) With few query blocks the key range is split over
-// blocks (blockIdx.z) whose partials k_causal_combine merges in a fixed order.
+// blocks (blockIdx.z) whose partials k_causal_combine merges in a fixed order: split sp takes the W tiles
+// [ntiles - (sp + 1) W, ntiles - sp W) counted back from the block's last key tile (the first split of a
+// block may be shorter), and splits past key 0 exit at once. Every live block then has the same work
+// whatever its query block's key range, so blocks fill the CUs evenly.
 // The probabilities enter the second product as bf16 before normalisation (the reference casts after
 // it; the difference is within rounding), scores are fp32 products of the bf16 q and k values as the
 // reference's fp32 matmul, and the output is O / (row sum) rounded to bf16.
@@ -99,6 +102,7 @@ struct CausalArgs {
   uint16_t* out;           // [nq, >= hq * d]
   int64_t ldo;
   float* part;             // splits > 1: per (query block, K / V head, split) O [256][d], max [256], sum [256]
+  int split_tiles;         // W: key tiles per split
 };
 
 __device__ __forceinline__ int64_t query_pos(const CausalArgs& a, int j) { return a.qpos ? a.qpos[j] : a.slot0 + j; }
@@ -278,10 +282,11 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
   const int jlast = min(j0 + qp, a.nq) - 1;
   const int64_t kmax = min(query_pos(a, jlast), a.n_keys - 1);     // the block reads keys 0 .. kmax
   const int ntiles = static_cast<int>(kmax / KT) + 1;
-  // this block's share of the key tiles (split blockIdx.z of gridDim.z)
+  // this block's share of the key tiles: split blockIdx.z, W tiles counted back from the last
   const int ns = gridDim.z, sp = blockIdx.z;
-  const int it0 = static_cast<int>(static_cast<int64_t>(ntiles) * sp / ns);
-  const int it1 = static_cast<int>(static_cast<int64_t>(ntiles) * (sp + 1) / ns);
+  const int it1 = ntiles - sp * a.split_tiles;
+  if (it1 <= 0) return;                                   // past key 0 (block-uniform, before any barrier)
+  const int it0 = max(0, it1 - a.split_tiles);
 
   // the wave's head and queries; lanes past the last query repeat it and write nothing
   const int hg = (32 * w) / qp, po0 = (32 * w) % qp;
@@ -406,11 +411,15 @@ __global__ __launch_bounds__(256) void k_causal_combine(CausalArgs a, int ns) {
   if (jq >= a.nq) return;
   const int64_t stride = QROWS * (AD + 2);
   const float* base = a.part + (static_cast<int64_t>(blockIdx.x) * a.hkv + hk) * ns * stride;
+  // the live splits of this query block (those k_attend_causal ran): ceil(ntiles / W)
+  const int jlast = min(j0 + qp, a.nq) - 1;
+  const int ntiles = static_cast<int>(min(query_pos(a, jlast), a.n_keys - 1) / KT) + 1;
+  const int live = min(ns, (ntiles + a.split_tiles - 1) / a.split_tiles);
   float mx = -INFINITY;
-  for (int sp = 0; sp < ns; ++sp) mx = fmaxf(mx, base[sp * stride + QROWS * AD + r]);
+  for (int sp = 0; sp < live; ++sp) mx = fmaxf(mx, base[sp * stride + QROWS * AD + r]);
   float l = 0.f;
   float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int sp = 0; sp < ns; ++sp) {
+  for (int sp = 0; sp < live; ++sp) {
     const float* pb = base + sp * stride;
     const float ms = pb[QROWS * AD + r];
     const float f = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - mx);
@@ -437,12 +446,38 @@ size_t part_bytes(int64_t nq, int hq, int hkv, int d, int splits) {
   return splits > 1 ? static_cast<size_t>(query_blocks(nq, hq, hkv)) * hkv * splits * QROWS * (d + 2) * 4 : 0;
 }
 
-// Key-range splits: about 512 blocks in all (two per CU), at most 16, at most one per key tile.
-int causal_splits(int64_t nq, int hq, int hkv, int64_t n_keys) {
-  const int64_t blocks = std::max<int64_t>(query_blocks(nq, hq, hkv) * hkv, 1);
-  int64_t s = (512 + blocks - 1) / blocks;
-  s = std::min<int64_t>(std::min<int64_t>(s, 16), key_tiles(n_keys));
-  return static_cast<int>(std::max<int64_t>(s, 1));
+// Key-range splits {ns, W}: W key tiles per split block, ns = ceil(key tiles / W) splits at most. With
+// enough query blocks to fill the CUs (blocks per CU: one at d 128, two at d 64, by LDS), none. Else W
+// minimises (rounds of live blocks) x (W + 2), the live blocks of query block qb being ceil(ntiles_qb / W)
+// per K / V head: ntiles_qb exact for consecutive queries (qpos null), else from query positions spread
+// evenly over the keys (the exact rows). A round is about 0.8 of the CUs' block slots: measured at 287
+// scattered queries over 28672 keys (32 / 8 heads, d 128), 208 live blocks of 56 tiles take 152 us and
+// 240 of 45 tiles 176 us (the blocks slow each other down through the shared K / V reads). Only the time
+// depends on these estimates, not the results.
+struct Splits {
+  int ns, W;
+};
+
+Splits causal_plan(int64_t nq, int hq, int hkv, int d, int64_t n_keys, bool scattered, int64_t slot0) {
+  const int64_t T = key_tiles(n_keys), QB = query_blocks(nq, hq, hkv), qp = QROWS / (hq / hkv);
+  if (QB * hkv >= 256 * (d == 64 ? 2 : 1) || T <= 1) return Splits{1, static_cast<int>(std::max<int64_t>(T, 1))};
+  const int64_t slots = 208 * (d == 64 ? 2 : 1);
+  auto tiles_of = [&](int64_t qb) {
+    if (scattered) return std::max<int64_t>(1, (T * (qb + 1) + QB - 1) / QB);
+    const int64_t last = slot0 + std::min<int64_t>((qb + 1) * qp, nq) - 1;
+    return std::min<int64_t>(T, last / KT + 1);
+  };
+  int64_t best_w = T, best_cost = INT64_MAX;
+  for (int64_t W = std::max<int64_t>(2, (T + 63) / 64); W <= T; ++W) {   // at most 64 splits
+    int64_t live = 0;
+    for (int64_t qb = 0; qb < QB; ++qb) live += (tiles_of(qb) + W - 1) / W;
+    const int64_t cost = ((live * hkv + slots - 1) / slots) * (W + 2);
+    if (cost < best_cost || (cost == best_cost && W > best_w)) {
+      best_cost = cost;
+      best_w = W;
+    }
+  }
+  return Splits{static_cast<int>((T + best_w - 1) / best_w), static_cast<int>(best_w)};
 }
 
 bool causal_shape_ok(int hq, int hkv, int d) {
@@ -460,7 +495,7 @@ extern "C" int rf_attend_causal_workspace_bytes(int64_t nq, int hq, int hkv, int
   if (!causal_shape_ok(hq, hkv, d))
     return fail(RF_EUNSUPPORTED, "rf_attend_causal_workspace_bytes: head_dim %d, %d query heads over %d K / V heads "
                 "(d 64 or 128, a group of 1, 2, 4 or 8)", d, hq, hkv);
-  *bytes = part_bytes(nq, hq, hkv, d, causal_splits(nq, hq, hkv, n_keys));
+  *bytes = part_bytes(nq, hq, hkv, d, causal_plan(nq, hq, hkv, d, n_keys, true, 0).ns);
   return RF_OK;
 }
 
@@ -486,10 +521,16 @@ extern "C" int rf_attend_causal(const uint16_t* q, int64_t ldq, int64_t nq, cons
   if (!(scale > 0.f) || !(scale < 1e30f)) return fail(RF_EINVAL_ARG, "rf_attend_causal: scale %g (must be positive)",
                                                       static_cast<double>(scale));
   if (nq == 0) return RF_OK;
-  int ns = workspace ? causal_splits(nq, hq, hkv, n_keys) : 1;
-  while (ns > 1 && ws_bytes < part_bytes(nq, hq, hkv, d, ns)) --ns;     // what the workspace holds
+  const int64_t T = key_tiles(n_keys);
+  Splits sp = workspace ? causal_plan(nq, hq, hkv, d, n_keys, qpos != nullptr, slot0) : Splits{1, static_cast<int>(T)};
+  while (sp.ns > 1 && ws_bytes < part_bytes(nq, hq, hkv, d, sp.ns)) {     // what the workspace holds
+    --sp.ns;
+    sp.W = static_cast<int>((T + sp.ns - 1) / sp.ns);
+  }
+  if (sp.ns == 1) sp.W = static_cast<int>(T);
+  const int ns = sp.ns;
   CausalArgs a{q, ldq, static_cast<int>(nq), qpos, slot0, kbuf, head_stride, row_stride, n_keys, vbuf, hq, hkv,
-               scale * 1.4426950408889634f, out, ldo, static_cast<float*>(workspace)};
+               scale * 1.4426950408889634f, out, ldo, static_cast<float*>(workspace), sp.W};
   const dim3 grid(static_cast<unsigned>(query_blocks(nq, hq, hkv)), static_cast<unsigned>(hkv),
                   static_cast<unsigned>(ns));
   if (d == 128) hipLaunchKernelGGL(k_attend_causal<128>, grid, dim3(NTHR), 0, stream, a);
