@@ -22,82 +22,96 @@ struct TransposeArgs {
   float* partial_sq;      // [tiles, cols] column sums of squares per 64-row tile, or null
 };
 
-// Block = one 64 x 64 tile, 256 threads. Load: thread t takes tile row t / 4, columns (t % 4) * 16 ..
-// + 15 (two 16-byte loads). Store: thread t writes output row (source column) t / 4, source rows
-// (t % 4) * 16 .. + 15. Rows at or past `rows` give zeros, so padded output columns are zero.
+// Block = 4 waves, wave w one 64 x 64 tile: source rows r0 .. r0 + 63, columns c0 = 256 blockIdx.y + 64 w ..
+// + 63. Lane l = 8 i + j holds the 8 x 8 piece at rows 8 i .., columns 8 j .. in eight 16-byte registers and
+// transposes it in registers (no LDS): its 8 output rows (source columns 8 j + c) get 16 bytes each (source
+// rows 8 i .. + 7). A wave's loads and stores then move whole 128-byte lines: per instruction 8 source
+// rows x 128 bytes, and 8 output rows x 128 bytes (the 8 lanes of one j). Rows at or past `rows` give
+// zeros, so padded output columns are zero.
 // Without a shift the values are copied bit for bit. With one, column c's value d = x - shift[c] (fp32)
 // is written as hi = bf16(d) and, if lo_row[c] >= 0, mid = bf16(d - hi) into row lo_row[c] of dst_lo and
 // lo = bf16(d - hi - mid) into row lo_row[c] + lo_gap: each remainder is exact in fp32 and the last one
 // has at most 8 significant bits, so hi + mid + lo == d exactly and a Gram product over [hi rows; mid and
-// lo rows] gives the products of the centred fp32 values. The sums (and squares) are of d, each 64-row
-// tile's 16 values per thread in order, then the 4 threads of a column pairwise.
+// lo rows] gives the products of the centred fp32 values. The sums (and squares) of d over a 64-row tile:
+// each 16-row group in row order (lane 8 (2g + 1) + j continues the chain lane 8 (2g) + j began), then the
+// four groups pairwise, ((g0 + g1) + (g2 + g3)).
+template <bool SHIFT>
 __global__ __launch_bounds__(256) void k_transpose(TransposeArgs a) {
-  __shared__ uint16_t tile[TT][TT + 2];
-  const int t = threadIdx.x;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, i = lane >> 3, j = lane & 7;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * TT;
-  const int c0 = blockIdx.y * TT;
-  {
-    const int r = t >> 2, c = (t & 3) * 16;
-    uint4 x0 = make_uint4(0u, 0u, 0u, 0u), x1 = x0;
-    if (r0 + r < a.rows) {
-      const uint4* p = reinterpret_cast<const uint4*>(a.src + (r0 + r) * a.ld_src + c0 + c);
-      x0 = p[0];
-      x1 = p[1];
-    }
+  const int c0 = blockIdx.y * 4 * TT + w * TT;
+  if (c0 >= a.cols) return;                       // wave-uniform; no barriers here
+  const int cb = c0 + 8 * j;                      // the lane's first source column
+  uint4 in[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      tile[r][c + e] = lane_of(x0, e);
-      tile[r][c + 8 + e] = lane_of(x1, e);
+  for (int k = 0; k < 8; ++k) {
+    const int64_t r = r0 + 8 * i + k;
+    in[k] = r < a.rows ? *reinterpret_cast<const uint4*>(a.src + r * a.ld_src + cb) : make_uint4(0u, 0u, 0u, 0u);
+  }
+  uint16_t v[8][8], mid[8][8], lo[8][8];          // [column][row]
+  float dv[8][8];                                 // the values the sums take: d, or the copied value
+  int lrow[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const float sh = SHIFT ? a.shift[cb + c] : 0.f;
+    lrow[c] = SHIFT ? a.lo_row[cb + c] : -1;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint16_t x = lane_of(in[k], c);
+      if constexpr (SHIFT) {
+        const float d = (r0 + 8 * i + k < a.rows) ? bf2f(x) - sh : 0.f;
+        v[c][k] = f2bf(d);
+        const float r1 = d - bf2f(v[c][k]);
+        mid[c][k] = f2bf(r1);
+        lo[c][k] = f2bf(r1 - bf2f(mid[c][k]));
+        dv[c][k] = d;
+      } else {
+        v[c][k] = x;
+        dv[c][k] = bf2f(x);
+      }
     }
   }
-  __syncthreads();
-  const int oc = t >> 2, rr = (t & 3) * 16;       // output row = source column c0 + oc
-  uint16_t v[16], mid[16], lo[16];
-  float s = 0.f, q = 0.f;
-  int lrow = -1;
-  if (a.shift) {
-    const float sh = a.shift[c0 + oc];
-    lrow = a.lo_row[c0 + oc];
+  if (a.partial) {
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      const float d = (r0 + rr + e < a.rows) ? bf2f(tile[rr + e][oc]) - sh : 0.f;
-      v[e] = f2bf(d);
-      const float r1 = d - bf2f(v[e]);
-      mid[e] = f2bf(r1);
-      lo[e] = f2bf(r1 - bf2f(mid[e]));
-      s += d;
-      q = fmaf(d, d, q);
-    }
-  } else {
+    for (int c = 0; c < 8; ++c) {
+      // the even row block's 8 values from zero; the odd one continues that chain with its own 8
+      float es = 0.f, eq = 0.f;
 #pragma unroll
-    for (int e = 0; e < 16; ++e) {
-      v[e] = tile[rr + e][oc];
-      const float w = bf2f(v[e]);
-      s += w;
-      q = fmaf(w, w, q);
+      for (int k = 0; k < 8; ++k) {
+        es += dv[c][k];
+        eq = fmaf(dv[c][k], dv[c][k], eq);
+      }
+      float gs = __shfl_xor(es, 8, 64), gq = __shfl_xor(eq, 8, 64);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        gs += dv[c][k];
+        gq = fmaf(dv[c][k], dv[c][k], gq);
+      }
+      // group g's sum now sits in the lanes of row block 2 g + 1: ((g0 + g1) + (g2 + g3))
+      gs += __shfl_xor(gs, 16, 64);
+      gq += __shfl_xor(gq, 16, 64);
+      gs += __shfl_xor(gs, 32, 64);
+      gq += __shfl_xor(gq, 32, 64);
+      if (i == 1) {
+        const int64_t at = static_cast<int64_t>(blockIdx.x) * a.cols + cb + c;
+        a.partial[at] = gs;
+        if (a.partial_sq) a.partial_sq[at] = gq;
+      }
     }
   }
-  uint4* o = reinterpret_cast<uint4*>(a.dst + static_cast<int64_t>(c0 + oc) * a.ld_dst + r0 + rr);
-  o[0] = make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
-  o[1] = make_uint4(pack2(v[8], v[9]), pack2(v[10], v[11]), pack2(v[12], v[13]), pack2(v[14], v[15]));
-  if (lrow >= 0) {
-    uint4* m = reinterpret_cast<uint4*>(a.dst_lo + static_cast<int64_t>(lrow) * a.ld_dst + r0 + rr);
-    m[0] = make_uint4(pack2(mid[0], mid[1]), pack2(mid[2], mid[3]), pack2(mid[4], mid[5]), pack2(mid[6], mid[7]));
-    m[1] = make_uint4(pack2(mid[8], mid[9]), pack2(mid[10], mid[11]), pack2(mid[12], mid[13]),
-                      pack2(mid[14], mid[15]));
-    uint4* l = reinterpret_cast<uint4*>(a.dst_lo + (static_cast<int64_t>(lrow) + a.lo_gap) * a.ld_dst + r0 + rr);
-    l[0] = make_uint4(pack2(lo[0], lo[1]), pack2(lo[2], lo[3]), pack2(lo[4], lo[5]), pack2(lo[6], lo[7]));
-    l[1] = make_uint4(pack2(lo[8], lo[9]), pack2(lo[10], lo[11]), pack2(lo[12], lo[13]), pack2(lo[14], lo[15]));
-  }
-  // the 4 threads of one column are adjacent lanes: fixed-order pairwise sums
-  s += __shfl_xor(s, 1, 64);
-  s += __shfl_xor(s, 2, 64);
-  q += __shfl_xor(q, 1, 64);
-  q += __shfl_xor(q, 2, 64);
-  if ((t & 3) == 0) {
-    const int64_t at = static_cast<int64_t>(blockIdx.x) * a.cols + c0 + oc;
-    if (a.partial) a.partial[at] = s;
-    if (a.partial_sq) a.partial_sq[at] = q;
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    const int64_t orow = cb + c;
+    *reinterpret_cast<uint4*>(a.dst + orow * a.ld_dst + r0 + 8 * i) =
+        make_uint4(pack2(v[c][0], v[c][1]), pack2(v[c][2], v[c][3]), pack2(v[c][4], v[c][5]), pack2(v[c][6], v[c][7]));
+    if (SHIFT && lrow[c] >= 0) {
+      *reinterpret_cast<uint4*>(a.dst_lo + static_cast<int64_t>(lrow[c]) * a.ld_dst + r0 + 8 * i) =
+          make_uint4(pack2(mid[c][0], mid[c][1]), pack2(mid[c][2], mid[c][3]), pack2(mid[c][4], mid[c][5]),
+                     pack2(mid[c][6], mid[c][7]));
+      *reinterpret_cast<uint4*>(a.dst_lo + (static_cast<int64_t>(lrow[c]) + a.lo_gap) * a.ld_dst + r0 + 8 * i) =
+          make_uint4(pack2(lo[c][0], lo[c][1]), pack2(lo[c][2], lo[c][3]), pack2(lo[c][4], lo[c][5]),
+                     pack2(lo[c][6], lo[c][7]));
+    }
   }
 }
 
@@ -226,8 +240,9 @@ static int launch_transpose(const char* fn, const TransposeArgs& a, int64_t rows
   if (!aligned16(a.src) || !aligned16(a.dst) || (a.dst_lo && !aligned16(a.dst_lo)))
     return fail(RF_EINVAL_SHAPE, "%s: 16-byte alignment", fn);
   if (rows == 0) return RF_OK;
-  hipLaunchKernelGGL(k_transpose, dim3(static_cast<unsigned>(rows_out / TT), static_cast<unsigned>(cols / TT)),
-                     dim3(256), 0, stream, a);
+  const dim3 grid(static_cast<unsigned>(rows_out / TT), static_cast<unsigned>((cols + 4 * TT - 1) / (4 * TT)));
+  if (a.shift) hipLaunchKernelGGL(k_transpose<true>, grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL(k_transpose<false>, grid, dim3(256), 0, stream, a);
   return check_launch(fn);
 }
 

@@ -39,8 +39,8 @@ def test_transpose_is_bit_exact_with_column_sums(dev):
 
 @pytest.mark.parametrize("fold_rows", [0, 128, 512])
 def test_gram_accumulate_matches_fp64_products(dev, fold_rows):
-    """fp32 runs of at most fold_rows (staggered by tile: the 6 tiles here start at 6 different offsets) added
-    into fp64, against fp64 products; fold_rows 0 sums the whole K in fp32."""
+    """fp32 runs of at most fold_rows added into fp64 in run order, against fp64 products; fold_rows 0 sums
+    the whole K in fp32. The same bits run to run."""
     from rfill import ridge
     g = torch.Generator().manual_seed(1)
     a = torch.randn(384, 1024, generator=g).to(torch.bfloat16)
