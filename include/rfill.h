@@ -42,14 +42,15 @@ int rf_map_apply(const uint16_t* b, int64_t ldb, const uint16_t* w, const uint16
                  void* workspace, size_t ws_bytes, hipStream_t stream);
 
 /* Bytes of the optional workspace of the GEMM entry points (rf_map_apply, rf_norm_kv_write, rf_norm_q,
- * rf_norm_linear) for an M x N x K product (M rows, N outputs, K inputs): nonzero when the output tiles
- * (256 x 256) are too few to give every CU one, e.g. the exact rows' or the tail's projections, or when
- * the last wave of whole tile rows is at most half full (then only those rows split; the rest run as
- * usual), e.g. the 32K-row K/V product of an 8B model (896 tiles: 768 + 128 split two ways). Given a
- * workspace at least this large (caller-owned device memory, 16-byte aligned), the entry point splits K
- * over more blocks, keeps their fp32 partial sums there and adds them in a fixed order before the
- * epilogue (the same bits every run; the unsplit sum order differs within fp32 rounding). With a
- * smaller or NULL workspace it runs unsplit. Host only. */
+ * rf_norm_linear) for an M x N x K product (M rows, N outputs, K inputs): nonzero for products of at most
+ * 512 rows (the exact rows' projections: a kernel that takes all of a row block's rows against 256 weight
+ * rows, K split up to 16 ways), when the output tiles (256 x 256) are too few to give every CU one, e.g.
+ * the tail's projections, or when the last wave of whole tile rows is at most half full (then only those
+ * rows split; the rest run as usual), e.g. the 32K-row K/V product of an 8B model (896 tiles: 768 + 128
+ * split two ways). Given a workspace at least this large (caller-owned device memory, 16-byte aligned),
+ * the entry point keeps the fp32 partial sums of its K ranges there and adds them in a fixed order before
+ * the epilogue (the same bits every run; with one range, the unsplit kernels' bits; otherwise the sum
+ * order differs within fp32 rounding). With a smaller or NULL workspace it runs unsplit. Host only. */
 int rf_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, size_t* bytes);
 
 /* Row sum-of-squares partials of given layer inputs x [P, H] -> ssq [P, H / 256], the statistics the
@@ -122,14 +123,17 @@ int rf_norm_kv_write_batch(int nl, const uint16_t* const* x, int64_t ldx, const 
                            uint16_t* const* kbuf, uint16_t* const* vbuf, int64_t head_stride, int64_t row_stride,
                            int64_t slot_begin, int64_t cap, hipStream_t stream);
 
-/* rf_norm_linear for nl (1 .. 32) layers in one launch over the same P rows (the in-projections of a group of
- * Gated DeltaNet layers, code/kva/model.py:448-450 per layer): out[l] = bf16(rms-normed x[l] w[l]^T), each
- * layer bit-identical to rf_norm_linear of it alone without a workspace. x, ssq, w, out: host arrays of nl
- * device pointers; one input row stride ldx and one output row stride ldo. H a multiple of 1024 up to 4096
- * runs every layer's tiles on one persistent grid; other widths launch per layer. */
-int rf_norm_linear_batch(int nl, const uint16_t* const* x, int64_t ldx, const float* const* ssq, int64_t P, int64_t H,
-                         float eps, const uint16_t* const* w, int64_t N, uint16_t* const* out, int64_t ldo,
-                         hipStream_t stream);
+/* rf_norm_linear for nl (1 .. 32) entries in one launch (the in-projections of a group of Gated DeltaNet
+ * layers, code/kva/model.py:448-450 per layer): entry l is rows[l] rows of x[l] (statistics ssq[l]) against the
+ * n[l] weight rows of w[l] (a multiple of 256) into out[l], out[l] = bf16(rms-normed x[l] w[l]^T), each
+ * bit-identical to rf_norm_linear of it alone without a workspace. A GDN fill passes two entries per layer:
+ * every row against the k | v | b | a rows, and the last 3 rows (the conv state's) against the q rows. x, ssq,
+ * w, out: host arrays of nl device pointers; rows, n: host arrays of nl counts; one input row stride ldx and
+ * one output row stride ldo (>= every n[l]). H a multiple of 1024 up to 4096 runs every entry's tiles on one
+ * persistent grid; other widths launch per entry. Entries of 0 rows are skipped. */
+int rf_norm_linear_batch(int nl, const uint16_t* const* x, int64_t ldx, const float* const* ssq, const int64_t* rows,
+                         int64_t H, float eps, const uint16_t* const* w, const int64_t* n, uint16_t* const* out,
+                         int64_t ldo, hipStream_t stream);
 
 /* RoPE on given pre-RoPE K and the K / V cache write of m rows.
  * Replaces Model.fill_kv (code/kva/model.py:161-165): ops.apply_rope (ops.py:66-77) + _append_kv.

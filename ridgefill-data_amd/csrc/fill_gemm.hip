@@ -1529,39 +1529,45 @@ __global__ __launch_bounds__(NTHR) void k_norm_kv_p(KvLayers kl, int nl, int64_t
 }
 
 // Per-layer operands of a batched norm + linear launch.
+// Entries of a batched norm + linear: entry l is rows m[l] of x[l] against the n[l] weight rows of w[l]
+// (n[l] a multiple of 256) into out[l]; its tiles are the logical tiles [start[l], start[l + 1]).
 struct LinLayers {
   const uint16_t* x[MAXL];
   const float* ssq[MAXL];
   const uint16_t* w[MAXL];
   uint16_t* out[MAXL];
+  int m[MAXL], n[MAXL];
+  int start[MAXL + 1];
 };
 
-// rf_norm_linear on persistent tiles for nl layers at once: out_l = bf16(r_row * (x_l W_l^T)), r_row from the
-// rows' statistics (parts_load / parts_sum; K a multiple of 1024 up to 4096); one output row stride ldo.
-__global__ __launch_bounds__(NTHR) void k_norm_linear_p(LinLayers ll, int nl, int64_t ldx, int64_t ldo, int M, int N,
-                                                        int K, float eps) {
+// rf_norm_linear on persistent tiles for nl entries at once: out_l = bf16(r_row * (x_l W_l^T)), r_row from the
+// rows' statistics (parts_load / parts_sum; K a multiple of 1024 up to 4096); one input row stride ldx, one
+// output row stride ldo. An entry's tile computes exactly what the per-entry kernel computes for it.
+__global__ __launch_bounds__(NTHR) void k_norm_linear_p(LinLayers ll, int nl, int64_t ldx, int64_t ldo, int K,
+                                                        float eps) {
   __shared__ uint4 lds[LDS_U4];
-  const int tiles_n = N / BN, tiles_m = (M + BM - 1) / BM, per = tiles_m * tiles_n;
-  const Share sh = block_share(nl * per);
+  const Share sh = block_share(ll.start[nl]);
   if (sh.cnt == 0) return;
   const int t = threadIdx.x, q4 = K / (4 * SSQ_COLS);
   const float width = static_cast<float>(K);
   auto coords = [&](int i, int& l, int& tm, int& tn) {
     const int u = sh.first + i * sh.stride;
-    l = u / per;
-    tile_coords(u - l * per, tiles_m, tiles_n, tm, tn);
+    l = 0;
+    while (l + 1 < nl && u >= ll.start[l + 1]) ++l;
+    tile_coords(u - ll.start[l], (ll.m[l] + BM - 1) / BM, ll.n[l] / BN, tm, tn);
   };
   auto ops = [&](int i) {
     int l, tm, tn;
     coords(i, l, tm, tn);
     const int m0 = tm * BM;
-    return TileOps{buffer_rsrc(ll.x[l] + static_cast<int64_t>(m0) * ldx, static_cast<uint32_t>(min(M - m0, BM) * ldx * 2)),
+    return TileOps{buffer_rsrc(ll.x[l] + static_cast<int64_t>(m0) * ldx,
+                               static_cast<uint32_t>(min(ll.m[l] - m0, BM) * ldx * 2)),
                    buffer_rsrc(ll.w[l] + static_cast<int64_t>(tn) * BN * K, static_cast<uint32_t>(BN * K * 2))};
   };
   auto parts_of = [&](int i, float4 (&v)[4], int tt) {
     int l, tm, tn;
     coords(i, l, tm, tn);
-    parts_load(ll.ssq[l], q4, M, tm * BM, tt, v);
+    parts_load(ll.ssq[l], q4, ll.m[l], tm * BM, tt, v);
   };
   float sc[4];
   {
@@ -1581,7 +1587,7 @@ __global__ __launch_bounds__(NTHR) void k_norm_linear_p(LinLayers ll, int nl, in
     int l, tm, tn;
     coords(i, l, tm, tn);
     const int t = pinned_tid(), lane = t & 63, wm = t >> 7;
-    const int m0 = tm * BM, n0 = tn * BN, ch = t & 31;
+    const int m0 = tm * BM, n0 = tn * BN, ch = t & 31, M = ll.m[l];
     uint16_t* out = ll.out[l];
     float* rsx = reinterpret_cast<float*>(img);     // the rows' norm scales, through the image area
 #pragma unroll
@@ -1922,8 +1928,12 @@ extern "C" int rf_norm_linear(const uint16_t* x, int64_t ldx, const float* ssq, 
     ll.ssq[0] = ssq;
     ll.w[0] = w;
     ll.out[0] = out;
+    ll.m[0] = static_cast<int>(mf);
+    ll.n[0] = static_cast<int>(N);
+    ll.start[0] = 0;
+    ll.start[1] = grid_of(mf, N);
     hipLaunchKernelGGL(k_norm_linear_p, dim3(persistent_grid(grid_of(mf, N))), dim3(NTHR), 0, stream, ll, 1, ldx, ldo,
-                       static_cast<int>(mf), static_cast<int>(N), static_cast<int>(H), eps);
+                       static_cast<int>(H), eps);
   } else if (mf > 0) {
     hipLaunchKernelGGL(k_norm_linear, dim3(grid_of(mf, N)), dim3(NTHR), 0, stream, x, ldx, w, static_cast<int>(mf),
                        static_cast<int>(N), static_cast<int>(H), ssq, eps, out, ldo);
@@ -2030,37 +2040,47 @@ extern "C" int rf_norm_kv_write_batch(int nl, const uint16_t* const* x, int64_t 
   return check_launch("rf_norm_kv_write_batch");
 }
 
-extern "C" int rf_norm_linear_batch(int nl, const uint16_t* const* x, int64_t ldx, const float* const* ssq, int64_t P,
-                                    int64_t H, float eps, const uint16_t* const* w, int64_t N, uint16_t* const* out,
-                                    int64_t ldo, hipStream_t stream) {
-  if (nl < 1 || nl > MAXL) return fail(RF_EINVAL_ARG, "rf_norm_linear_batch: %d layers (1 .. %d)", nl, MAXL);
-  if (!x || !ssq || !w || !out) return fail(RF_EINVAL_ARG, "rf_norm_linear_batch: null pointer");
-  if (P < 0 || P > (1ll << 30) || H <= 0 || H % SSQ_COLS || N <= 0 || N % BN)
-    return fail(RF_EINVAL_SHAPE, "rf_norm_linear_batch: P %lld, H %lld (multiple of 256), N %lld (multiple of 256)",
-                (long long)P, (long long)H, (long long)N);
-  if (ldx < H || ldx % 8 || ldx > (1 << 21) || ldo < N || ldo % 8)
-    return fail(RF_EINVAL_SHAPE, "rf_norm_linear_batch: strides ldx %lld, ldo %lld", (long long)ldx, (long long)ldo);
-  if (!(eps >= 0.f)) return fail(RF_EINVAL_ARG, "rf_norm_linear_batch: eps");
-  if (static_cast<int64_t>(nl) * grid_of(P, N) > (1ll << 30))
-    return fail(RF_EINVAL_SHAPE, "rf_norm_linear_batch: too many tiles");
+extern "C" int rf_norm_linear_batch(int nl, const uint16_t* const* x, int64_t ldx, const float* const* ssq,
+                                    const int64_t* rows, int64_t H, float eps, const uint16_t* const* w,
+                                    const int64_t* n, uint16_t* const* out, int64_t ldo, hipStream_t stream) {
+  const char* fn = "rf_norm_linear_batch";
+  if (nl < 1 || nl > MAXL) return fail(RF_EINVAL_ARG, "%s: %d entries (1 .. %d)", fn, nl, MAXL);
+  if (!x || !ssq || !w || !out || !rows || !n) return fail(RF_EINVAL_ARG, "%s: null pointer", fn);
+  if (H <= 0 || H % SSQ_COLS) return fail(RF_EINVAL_SHAPE, "%s: H %lld (multiple of 256)", fn, (long long)H);
+  if (ldx < H || ldx % 8 || ldx > (1 << 21) || ldo % 8)
+    return fail(RF_EINVAL_SHAPE, "%s: strides ldx %lld, ldo %lld", fn, (long long)ldx, (long long)ldo);
+  if (!(eps >= 0.f)) return fail(RF_EINVAL_ARG, "%s: eps", fn);
   LinLayers ll{};
+  int64_t tiles = 0;
+  int live = 0;
   for (int l = 0; l < nl; ++l) {
-    if (!x[l] || !ssq[l] || !w[l] || !out[l]) return fail(RF_EINVAL_ARG, "rf_norm_linear_batch: null pointer for layer %d", l);
+    if (rows[l] < 0 || rows[l] > (1ll << 30) || n[l] <= 0 || n[l] % BN || ldo < n[l])
+      return fail(RF_EINVAL_SHAPE, "%s: entry %d: rows %lld, N %lld (multiple of 256, <= ldo %lld)", fn, l,
+                  (long long)rows[l], (long long)n[l], (long long)ldo);
+    if (!x[l] || !ssq[l] || !w[l] || !out[l]) return fail(RF_EINVAL_ARG, "%s: null pointer in entry %d", fn, l);
     if (!aligned16(x[l]) || !aligned16(w[l]) || !aligned16(out[l]))
-      return fail(RF_EINVAL_SHAPE, "rf_norm_linear_batch: layer %d pointers must be 16-byte aligned", l);
-    ll.x[l] = x[l];
-    ll.ssq[l] = ssq[l];
-    ll.w[l] = w[l];
-    ll.out[l] = out[l];
+      return fail(RF_EINVAL_SHAPE, "%s: entry %d pointers must be 16-byte aligned", fn, l);
+    if (rows[l] == 0) continue;                     // nothing to compute: left out of the launch
+    ll.x[live] = x[l];
+    ll.ssq[live] = ssq[l];
+    ll.w[live] = w[l];
+    ll.out[live] = out[l];
+    ll.m[live] = static_cast<int>(rows[l]);
+    ll.n[live] = static_cast<int>(n[l]);
+    ll.start[live] = static_cast<int>(tiles);
+    tiles += grid_of(rows[l], n[l]);
+    if (tiles > (1ll << 30)) return fail(RF_EINVAL_SHAPE, "%s: too many tiles", fn);
+    ++live;
   }
-  if (P == 0) return RF_OK;
+  ll.start[live] = static_cast<int>(tiles);
+  if (live == 0) return RF_OK;
   if (persistent_lin_ok(H)) {
-    hipLaunchKernelGGL(k_norm_linear_p, dim3(persistent_grid(nl * static_cast<int64_t>(grid_of(P, N)))), dim3(NTHR), 0,
-                       stream, ll, nl, ldx, ldo, static_cast<int>(P), static_cast<int>(N), static_cast<int>(H), eps);
-  } else {                                          // other widths: the per-tile kernel, one launch per layer
-    for (int l = 0; l < nl; ++l)
-      hipLaunchKernelGGL(k_norm_linear, dim3(grid_of(P, N)), dim3(NTHR), 0, stream, ll.x[l], ldx, ll.w[l],
-                         static_cast<int>(P), static_cast<int>(N), static_cast<int>(H), ll.ssq[l], eps, ll.out[l], ldo);
+    hipLaunchKernelGGL(k_norm_linear_p, dim3(persistent_grid(tiles)), dim3(NTHR), 0, stream, ll, live, ldx, ldo,
+                       static_cast<int>(H), eps);
+  } else {                                          // other widths: the per-tile kernel, one launch per entry
+    for (int l = 0; l < live; ++l)
+      hipLaunchKernelGGL(k_norm_linear, dim3(grid_of(ll.m[l], ll.n[l])), dim3(NTHR), 0, stream, ll.x[l], ldx, ll.w[l],
+                         ll.m[l], ll.n[l], static_cast<int>(H), ll.ssq[l], eps, ll.out[l], ldo);
   }
-  return check_launch("rf_norm_linear_batch");
+  return check_launch(fn);
 }

@@ -26,6 +26,7 @@ class HipError(RuntimeError):
 _P, _I64, _I32, _F32, _F64 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float, ctypes.c_double
 _SZ, _PSZ = ctypes.c_size_t, ctypes.POINTER(ctypes.c_size_t)
 _PP = ctypes.POINTER(ctypes.c_void_p)       # a host array of device pointers
+_PI64 = ctypes.POINTER(ctypes.c_int64)      # a host array of counts
 
 # name -> argument types (every function returns int status)
 SIGNATURES = {
@@ -42,7 +43,7 @@ SIGNATURES = {
                          _P, _P, _I64, _I64, _I64, _I64, _P, _SZ, _P],
     "rf_rope_kv_write": [_P, _I64, _P, _I64, _I64, _I32, _I32, _P, _I32, _P, _P, _I64, _I64, _I64, _I64, _P],
     "rf_norm_linear": [_P, _I64, _P, _I64, _I64, _F32, _P, _I64, _P, _I64, _P, _SZ, _P],
-    "rf_norm_linear_batch": [_I32, _PP, _I64, _PP, _I64, _I64, _F32, _PP, _I64, _PP, _I64, _P],
+    "rf_norm_linear_batch": [_I32, _PP, _I64, _PP, _PI64, _I64, _F32, _PP, _PI64, _PP, _I64, _P],
     "rf_gdn_fill": [_P, _I64, _I64, _I32, _I32, _I32, _I32, _P, _P, _P, _P, _P, _P, _P, _SZ, _P],
     "rf_gdn_fill_batch": [_P, _I32, _I64, _I32, _I32, _I32, _I32, _P, _SZ, _P],
     "rf_gdn_workspace_bytes": [_I64, _I32, _I32, _I32, _I32, _PSZ],

@@ -240,29 +240,25 @@ class FillModel:
     def _fill_rows(self, w, x, ssq):
         """The in-projection rows [P, q | k | v | b | a] a GDN fill reads (code/kva/model.py:452-458). The state
         update reads k, v, b and a only, and the conv state the last 3 rows of q | k | v, so q is projected for
-        those 3 rows alone (one unsplit GEMM: the same per-element arithmetic as the full projection, so every
-        value read is the full projection's bits) and the other rows' q columns stay unwritten."""
-        W = w["w_in"]
-        P = x.shape[0]
-        nq = self.nk * self.dk
-        if nq % 256 or P <= 3:
-            return ops.norm_linear(x, ssq, self.eps, W)
-        pre = torch.empty(P, W.shape[0], dtype=torch.bfloat16, device=x.device)
-        ops.norm_linear(x, ssq, self.eps, W[nq:], out=pre[:, nq:])
-        ops.norm_linear(x[P - 3:], ssq[P - 3:], self.eps, W[:nq], out=pre[P - 3:, :nq])
-        return pre
+        those 3 rows alone and the other rows' q columns stay unwritten."""
+        return self._fill_rows_batch([w], [x], [ssq])[0]
 
     def _fill_rows_batch(self, ws, xs, ssqs):
-        """_fill_rows of several GDN layers over the same rows: their k | v | b | a projections in one launch
-        (ops.norm_linear_batch), bit-identical to _fill_rows of each alone."""
+        """_fill_rows of several GDN layers over the same rows in one launch (ops.norm_linear_batch): per layer
+        one entry of every row against the k | v | b | a rows and one of the last 3 rows against the q rows.
+        Each value is the bits of the full projection of its row (the same kernel on the same row and weights)."""
         P = xs[0].shape[0]
         nq = self.nk * self.dk
-        if nq % 256 or P <= 3 or len(ws) == 1 or any(x.stride(0) != xs[0].stride(0) for x in xs):
-            return [self._fill_rows(w, x, q) for w, x, q in zip(ws, xs, ssqs)]
+        if nq % 256 or P <= 3 or any(x.stride(0) != xs[0].stride(0) for x in xs):
+            return [ops.norm_linear(x, q, self.eps, w["w_in"]) for w, x, q in zip(ws, xs, ssqs)]
         pres = [torch.empty(P, w["w_in"].shape[0], dtype=torch.bfloat16, device=xs[0].device) for w in ws]
-        ops.norm_linear_batch(xs, ssqs, self.eps, [w["w_in"][nq:] for w in ws], [p[:, nq:] for p in pres])
+        ex, es, ew, eo = [], [], [], []
         for w, x, q, pre in zip(ws, xs, ssqs, pres):
-            ops.norm_linear(x[P - 3:], q[P - 3:], self.eps, w["w_in"][:nq], out=pre[P - 3:, :nq])
+            ex += [x, x[P - 3:]]
+            es += [q, q[P - 3:]]
+            ew += [w["w_in"][nq:], w["w_in"][:nq]]
+            eo += [pre[:, nq:], pre[P - 3:, :nq]]
+        ops.norm_linear_batch(ex, es, self.eps, ew, eo)
         return pres
 
     def fill_batch(self, ids, xs, cache, ssqs=None):

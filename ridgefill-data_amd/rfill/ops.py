@@ -167,31 +167,36 @@ def norm_kv_write_batch(xs, ssqs, eps, wkvs, hkv, d, knorms, knorm_kind, cs, kbu
 
 
 def norm_linear_batch(xs, ssqs, eps, ws, outs):
-    """norm_linear of several layers in one launch (rf_norm_linear_batch): outs[l] = bf16(rms-normed xs[l] @
-    ws[l]^T), each layer bit-identical to norm_linear of it alone without a workspace. xs[l] [P, H] (one row
-    stride), ssqs[l] [P, H / 256] contiguous, ws[l] [N, H] contiguous, outs[l] [P, N] (one row stride)."""
+    """norm_linear of several entries in one launch (rf_norm_linear_batch): outs[l] = bf16(rms-normed xs[l] @
+    ws[l]^T), each bit-identical to norm_linear of it alone without a workspace. Entry l: xs[l] [M_l, H] (one
+    row stride for all), ssqs[l] [M_l, H / 256] contiguous, ws[l] [N_l, H] contiguous (N_l % 256 == 0),
+    outs[l] [M_l, N_l] (one row stride for all)."""
     nl = len(xs)
     if not 0 < nl <= MAP_BATCH_MAX or not (len(ssqs) == len(ws) == len(outs) == nl):
-        raise ValueError("norm_linear_batch: one input, statistics, weight and output per layer")
-    P, H = xs[0].shape
-    N = ws[0].shape[0]
+        raise ValueError("norm_linear_batch: one input, statistics, weight and output per entry")
+    H = xs[0].shape[1]
+    rows, ns = [], []
     for i in range(nl):
         _need(xs[i], "x", torch.bfloat16, 2)
         _need(ssqs[i], "ssq", torch.float32, 2)
         _need(ws[i], "w", torch.bfloat16, 2)
         _need(outs[i], "out", torch.bfloat16, 2)
-        if tuple(xs[i].shape) != (P, H) or xs[i].stride(0) != xs[0].stride(0):
-            raise ValueError(f"norm_linear_batch: layer {i} input {tuple(xs[i].shape)}, expected ({P}, {H})"
-                             " with layer 0's row stride")
-        if tuple(ssqs[i].shape) != (P, ssq_parts(H)) or not ssqs[i].is_contiguous():
-            raise ValueError(f"norm_linear_batch: layer {i} statistics shape")
-        if tuple(ws[i].shape) != (N, H) or not ws[i].is_contiguous():
-            raise ValueError(f"norm_linear_batch: layer {i} weight {tuple(ws[i].shape)}, expected ({N}, {H})")
-        if tuple(outs[i].shape) != (P, N) or outs[i].stride(0) != outs[0].stride(0) or outs[i].stride(1) != 1:
-            raise ValueError(f"norm_linear_batch: layer {i} output {tuple(outs[i].shape)}, expected ({P}, {N})"
-                             " with layer 0's row stride")
-    _lib.call("rf_norm_linear_batch", nl, _ptr_array(xs), xs[0].stride(0), _ptr_array(ssqs), P, H, float(eps),
-              _ptr_array(ws), N, _ptr_array(outs), outs[0].stride(0), _stream(xs[0]))
+        M, N = xs[i].shape[0], ws[i].shape[0]
+        if xs[i].shape[1] != H or xs[i].stride(0) != xs[0].stride(0):
+            raise ValueError(f"norm_linear_batch: entry {i} input {tuple(xs[i].shape)}: width {H} and entry 0's row"
+                             " stride expected")
+        if tuple(ssqs[i].shape) != (M, ssq_parts(H)) or not ssqs[i].is_contiguous():
+            raise ValueError(f"norm_linear_batch: entry {i} statistics shape")
+        if tuple(ws[i].shape) != (N, H) or not ws[i].is_contiguous() or N % 256:
+            raise ValueError(f"norm_linear_batch: entry {i} weight {tuple(ws[i].shape)}, expected (N % 256 == 0, {H})")
+        if tuple(outs[i].shape) != (M, N) or outs[i].stride(0) != outs[0].stride(0) or outs[i].stride(1) != 1:
+            raise ValueError(f"norm_linear_batch: entry {i} output {tuple(outs[i].shape)}, expected ({M}, {N})"
+                             " with entry 0's row stride")
+        rows.append(M)
+        ns.append(N)
+    _lib.call("rf_norm_linear_batch", nl, _ptr_array(xs), xs[0].stride(0), _ptr_array(ssqs),
+              (ctypes.c_int64 * nl)(*rows), H, float(eps), _ptr_array(ws), (ctypes.c_int64 * nl)(*ns),
+              _ptr_array(outs), outs[0].stride(0), _stream(xs[0]))
 
 
 def row_ssq(x, ssq=None):

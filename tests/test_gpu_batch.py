@@ -221,3 +221,23 @@ def test_fill_late_hybrid_groups_equal_per_layer(dev):
             m.fill(i, x, pos, ref, ssq=s)
             assert torch.equal(cache[i]["conv"], ref[i]["conv"]), f"layer {i}: conv state differs"
             assert torch.equal(cache[i]["rec"], ref[i]["rec"]), f"layer {i}: recurrent state differs"
+
+
+def test_norm_linear_batch_ragged_entries(dev):
+    """rf_norm_linear_batch with entries of different rows and widths in one launch (a GDN fill's two
+    entries per layer: every row against the k | v | b | a rows, the last 3 rows against the q rows): each
+    entry bitwise rf_norm_linear of it alone; the rows and columns outside the entries untouched."""
+    from rfill import ops
+    g = torch.Generator().manual_seed(21)
+    P, H = 1000, 1024
+    x = inputs(P, H, seed=22).to(dev)
+    ssq = ops.row_ssq(x)
+    w = [(torch.randn(n, H, generator=g) / H ** 0.5).to(torch.bfloat16).to(dev) for n in (768, 256, 512)]
+    out = torch.full((P, 1280), 3.0, dtype=torch.bfloat16, device=dev)
+    ops.norm_linear_batch([x, x[P - 3:], x[:130]], [ssq, ssq[P - 3:], ssq[:130]], 1e-6, w,
+                          [out[:, 512:], out[P - 3:, :256], out[:130, :512]])
+    torch.cuda.synchronize()
+    assert torch.equal(out[:, 512:], ops.norm_linear(x, ssq, 1e-6, w[0]))
+    assert torch.equal(out[P - 3:, :256], ops.norm_linear(x[P - 3:], ssq[P - 3:], 1e-6, w[1]))
+    assert torch.equal(out[:130, :512], ops.norm_linear(x[:130], ssq[:130], 1e-6, w[2]))
+    assert bool((out[130:P - 3, :512] == 3.0).all()) and bool((out[P - 3:, 256:512] == 3.0).all())
