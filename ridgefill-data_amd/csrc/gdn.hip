@@ -42,11 +42,16 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 constexpr int DK = 128, DV = 128, CH = 64, TAPS = 4;
 constexpr int KST = DK + 8;                        // bf16 row stride of the k / v tiles in LDS
 constexpr int FST = CH + 4;                        // fp32 row stride of the 64 x 64 tiles in LDS
-// workspace layout per chunk (bytes): every key head's K orders, then every value head's T, V, scalars
+// workspace layout per chunk (bytes): every key head's K orders, then every value head's T (hi / lo, its six
+// nonzero 16 x 32 blocks), V, scalars
 constexpr uint32_t KP_BYTES = 16384, KTP_BYTES = 16384;
-constexpr uint32_t TP_BYTES = 16384, VP_BYTES = 16384, SC_BYTES = 1024;
+constexpr uint32_t TP_BYTES = 12288, VP_BYTES = 16384, SC_BYTES = 1024;
 constexpr uint32_t KH_BYTES = KP_BYTES + KTP_BYTES;
 constexpr uint32_t VH_BYTES = TP_BYTES + VP_BYTES + SC_BYTES;
+
+// T's 16 x 32 blocks (row tile it, k-step s) that can be nonzero (T is lower triangular: row tiles 0 and 1
+// need k-step 0 only), numbered 0 .. 5.
+__device__ __forceinline__ int tp_block(int it, int s) { return it < 2 ? it : 2 * it - 2 + s; }
 // scalar block: beta [64], q = e^gamma r [64], z = r e^{gamma_last - gamma} [64], decay e^{gamma_last}
 constexpr int SC_BETA = 0, SC_Q = 64, SC_Z = 128, SC_DECAY = 192;
 // output region per (chunk, value head), after the chunk's scan operands: the state before the chunk
@@ -408,18 +413,20 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_num_vgpr(128))) void k_g
     float* to = reinterpret_cast<float*>(obase + OS_T);
     for (int idx = t; idx < CH * CH; idx += 256) to[idx] = t_s[(idx >> 6) * FST + (idx & 63)];
   }
-  {  // T split hi / lo in the scan's A-operand order: Tp [it][s][hl][lane][8] = T[16 it + lane % 16][kperm(s, g, e)]
+  {  // T split hi / lo in the scan's A-operand order: Tp [b][hl][lane][8] = T[16 it + lane % 16][kperm(s, g, e)]
+     // for the nonzero blocks b = tp_block(it, s) (the blocks it < 2, s = 1 are zero and not stored)
     uint4* tp = reinterpret_cast<uint4*>(vbase);
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const int idx = t + 256 * k, it = idx >> 7, s = (idx >> 6) & 1, l = idx & 63, g = l >> 4, n = l & 15;
+      if (it < 2 && s == 1) continue;               // wave-uniform
       float x[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) x[e] = t_s[(16 * it + n) * FST + kperm(s, g, e)];
       uint4 hi, lo;
       split8(x, hi, lo);
-      tp[((it * 2 + s) * 2 + 0) * 64 + l] = hi;
-      tp[((it * 2 + s) * 2 + 1) * 64 + l] = lo;
+      tp[(tp_block(it, s) * 2 + 0) * 64 + l] = hi;
+      tp[(tp_block(it, s) * 2 + 1) * 64 + l] = lo;
     }
   }
 }
@@ -464,12 +471,13 @@ __device__ __forceinline__ void load_part(ScanOps& o, const ScanSrc& q, int part
       for (int s = 0; s < 2; ++s)
         o.kt[j][s] = *reinterpret_cast<const uint4*>(q.kb + KP_BYTES + ((2 * w + j) * 2 + s) * 1024);
   } else if (part == 2) {
-    // every wave issues the same loads (uniform wait counts); waves 0 and 1 fetch a k-step 1 frag they skip
+    // every wave issues the same loads (uniform wait counts); waves 0 and 1 load their k-step 0 block twice
+    // (their k-step 1 block is zero and not stored)
 #pragma unroll
     for (int s = 0; s < 2; ++s)
 #pragma unroll
       for (int hl = 0; hl < 2; ++hl)
-        o.tp[s][hl] = *reinterpret_cast<const uint4*>(q.vb + ((w * 2 + s) * 2 + hl) * 1024 + lane * 16);
+        o.tp[s][hl] = *reinterpret_cast<const uint4*>(q.vb + (tp_block(w, w < 2 ? 0 : s) * 2 + hl) * 1024 + lane * 16);
   } else {
     o.v = *reinterpret_cast<const uint2*>(q.vb + TP_BYTES + cb * 2048 + lane * 32 + w * 8);
     const float* sc = reinterpret_cast<const float*>(q.vb + TP_BYTES + VP_BYTES);
