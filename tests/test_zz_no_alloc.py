@@ -1,7 +1,7 @@
 """The allocation-free GDN fill (rf_gdn_fill_noalloc, the library's own device array as the workspace)
 against rf_gdn_fill with a caller workspace, through the C ABI, bit for bit: two calls in a row on the same
 GPU, the second with fewer rows (the array keeps the first call's contents), at the hybrid's widths
-(16 key / 32 value heads: 41 chunks per pass, so the 9000-row call makes 4 passes); and the refusal of heads
+(16 key / 32 value heads: 45 chunks per pass, so the 9000-row call makes 4 passes); and the refusal of heads
 whose one chunk exceeds the array."""
 import pytest
 import torch
