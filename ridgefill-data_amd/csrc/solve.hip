@@ -3,13 +3,14 @@
 // closed form through the inverse of C + lam s I).
 //
 //   k_dgemm       C = alpha A B + beta C, row-major fp64, v_mfma_f64_16x16x4f64. A workgroup of 4 wave64s
-//                 computes a 128 x 128 tile over K in 32-deep blocks; each wave a 64 x 64 quarter as 4 x 4
+//                 computes a 128 x 128 tile over K in 16-deep blocks; each wave a 64 x 64 quarter as 4 x 4
 //                 MFMA tiles (lane l feeds A[l % 16][l / 16] and B[l / 16][l % 16] and holds
 //                 D[l / 16 + 4 i][l % 16] in its register pair i: the fp64 output's rows interleave, unlike the
-//                 fp32 16x16x4 variant's 4 (l / 16) + i). Blocks are double-buffered in LDS, the next block loaded into
-//                 registers while the current one is multiplied. LDS strides: A rows of 34 doubles and B rows
-//                 of 144 doubles, so the 16 rows x 2 k (A) and 16 columns x 2 k (B) of each half-wave's
-//                 fragment reads fall in distinct banks.
+//                 fp32 16x16x4 variant's 4 (l / 16) + i). Blocks are double-buffered in LDS (72 KB, so two
+//                 workgroups share a CU and fill each other's barrier and LDS-latency gaps), the next block
+//                 loaded into registers while the current one is multiplied. LDS strides: A rows of 18 doubles and B rows of 144 doubles, so
+//                 the 16 rows x 2 k (A) and 16 columns x 2 k (B) of each half-wave's fragment reads fall in
+//                 distinct banks. The k order of the sums is that of one pass over K in steps of 4.
 //   k_spd_inv64   the inverse of a 64 x 64 symmetric positive definite block by in-place Gauss-Jordan
 //                 elimination without pivoting (stable for SPD matrices), in LDS, one workgroup.
 //   the inverse   of an n x n SPD matrix (n a multiple of 64) by block recursion on [A11 A12; A21 A22]:
@@ -27,8 +28,9 @@ namespace {
 
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
-constexpr int DBM = 128, DBN = 128, DBK = 32;
+constexpr int DBM = 128, DBN = 128, DBK = 16;
 constexpr int AST = DBK + 2;      // A block row stride in doubles (16-byte aligned rows, conflict-free reads)
+constexpr int DLD = DBM * DBK / 2 / 256;   // double2 loads per thread per block and operand (A; B has the same)
 constexpr int BST = DBN + 16;     // B block row stride in doubles
 
 struct DgemmArgs {
@@ -43,8 +45,9 @@ struct DgemmArgs {
   int64_t sa, sb, sc;     // element strides between the batch's matrices (blockIdx.y)
 };
 
-// Requires K and N even, lda / ldb even, A and B 16-byte aligned (checked by the host callers).
-__global__ __launch_bounds__(256) void k_dgemm(DgemmArgs a) {
+// Requires K and N even, lda / ldb even, A and B 16-byte aligned (checked by the host callers). Loads past
+// M, N or K read a clamped in-bounds address and are replaced by zeros (no divergent branches in the loop).
+__global__ __launch_bounds__(256, 2) void k_dgemm(DgemmArgs a) {
   __shared__ __align__(16) double As[2][DBM * AST];
   __shared__ __align__(16) double Bs[2][DBK * BST];
   const int t = threadIdx.x, lane = t & 63;
@@ -57,26 +60,34 @@ __global__ __launch_bounds__(256) void k_dgemm(DgemmArgs a) {
   const double* __restrict__ Ag = a.A + z * a.sa;
   const double* __restrict__ Bg = a.B + z * a.sb;
   double* __restrict__ Cg = a.C + z * a.sc;
-  // loader mapping: A chunk j = t + 256 i: row j / 16, k pair j % 16; B chunk j: k row j / 64, column pair j % 64
-  double2 ra[8], rb[8];
+  // loader mapping: A chunk j = t + 256 i: row j / 8, k pair j % 8; B chunk j: k row j / 64, column pair j % 64
+  // the zero masks are applied when the block is written to LDS, after the multiply that hides the loads
+  double2 ra[DLD], rb[DLD];
+  unsigned ok = 0;
   auto gload = [&](int k0) {
+    ok = 0;
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < DLD; ++i) {
       const int j = t + 256 * i;
-      const int ar = j >> 4, ak = k0 + 2 * (j & 15);
-      const int64_t gr = static_cast<int64_t>(m0) + ar;
-      ra[i] = (gr < a.M && ak < a.K) ? *reinterpret_cast<const double2*>(Ag + gr * a.lda + ak) : double2{0.0, 0.0};
+      const int ar = j >> 3, ak = k0 + 2 * (j & 7);
+      const int gr = m0 + ar;
+      ok |= (gr < a.M && ak < a.K) ? 1u << i : 0u;
+      ra[i] = *reinterpret_cast<const double2*>(Ag + static_cast<int64_t>(min(gr, a.M - 1)) * a.lda +
+                                                min(ak, a.K - 2));
       const int bk = k0 + (j >> 6), bc = n0 + 2 * (j & 63);
-      rb[i] = (bk < a.K && bc < a.N) ? *reinterpret_cast<const double2*>(Bg + static_cast<int64_t>(bk) * a.ldb + bc)
-                                     : double2{0.0, 0.0};
+      ok |= (bk < a.K && bc < a.N) ? 1u << (DLD + i) : 0u;
+      rb[i] = *reinterpret_cast<const double2*>(Bg + static_cast<int64_t>(min(bk, a.K - 1)) * a.ldb +
+                                                min(bc, a.N - 2));
     }
   };
   auto swrite = [&](int s) {
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
+    for (int i = 0; i < DLD; ++i) {
       const int j = t + 256 * i;
-      *reinterpret_cast<double2*>(&As[s][(j >> 4) * AST + 2 * (j & 15)]) = ra[i];
-      *reinterpret_cast<double2*>(&Bs[s][(j >> 6) * BST + 2 * (j & 63)]) = rb[i];
+      const bool ka = (ok >> i) & 1, kb = (ok >> (DLD + i)) & 1;
+      const double2 va{ka ? ra[i].x : 0.0, ka ? ra[i].y : 0.0}, vb{kb ? rb[i].x : 0.0, kb ? rb[i].y : 0.0};
+      *reinterpret_cast<double2*>(&As[s][(j >> 3) * AST + 2 * (j & 7)]) = va;
+      *reinterpret_cast<double2*>(&Bs[s][(j >> 6) * BST + 2 * (j & 63)]) = vb;
     }
   };
   f64x4 acc[4][4];

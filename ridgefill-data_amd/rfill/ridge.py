@@ -137,8 +137,13 @@ def centred_products(G, ca, A, cb, B):
 
 
 def recentre(D, s1a, s1b, da, db, n):
-    """Sums about shifts moved by da / db: sum (d_a - da)(d_b - db)^T from D = sum d_a d_b^T, s1 = sum d."""
-    return D - torch.outer(da, s1b) - torch.outer(s1a, db) + n * torch.outer(da, db)
+    """Sums about shifts moved by da / db: sum (d_a - da)(d_b - db)^T from D = sum d_a d_b^T, s1 = sum d.
+    Updates D in place (the callers pass a fresh product) by three rank-1 updates: at d 4096 each term would
+    otherwise be a 128 MB fp64 temporary."""
+    D.addr_(da, s1b, alpha=-1.0)
+    D.addr_(s1a, db, alpha=-1.0)
+    D.addr_(da, db, alpha=float(n))
+    return D
 
 
 class RidgeStats:
@@ -335,13 +340,16 @@ class RidgeFit:
         sx = state["sx"].to(dev, torch.float64)
         self.sx = sx
         self.mean_x = state["cx"].to(dev, torch.float64) + sx / n
-        self.cxx = (state["sxx"].to(dev, torch.float64) - torch.outer(sx, sx) / n).contiguous()
+        self.cxx = torch.addr(state["sxx"].to(dev, torch.float64), sx, sx, alpha=-1.0 / n).contiguous()
         self.scale = self.cxx.diagonal().mean().item()
 
-    def cross(self, i):
+    def cross(self, i, out=None):
+        """(cross statistics [d, d_out] of target i about the means, mean_y [d_out]); out: where to write the
+        former (e.g. the target's columns of the side-by-side matrix the solve takes)."""
         st = self.state
         sy = st["sy"][i].to(self.device, torch.float64)
-        cxy = st["sxy"][i].to(self.device, torch.float64) - torch.outer(self.sx, sy) / self.n
+        sxy = st["sxy"][i].to(self.device, torch.float64)
+        cxy = torch.addr(sxy, self.sx, sy, alpha=-1.0 / self.n, out=out)
         return cxy, st["cy"][i].to(self.device, torch.float64) + sy / self.n
 
     def solve(self, cxy, lams, mean_y=None):
@@ -372,17 +380,21 @@ class RidgeFit:
         """{i: {lam: (weight, bias)}} for every layer i in ids: the targets' cross statistics side by side,
         one rf_ridge_solve for every lambda and target."""
         ids, lams = list(ids), list(lams)
-        cross = [self.cross(i) for i in ids]
-        cxy = torch.cat([c for c, _ in cross], 1)
-        mean_y = torch.cat([m for _, m in cross])
-        w_all, b_all = self.solve(cxy, lams, mean_y)
+        widths = [self.state["sxy"][i].shape[1] for i in ids]
+        cols = [0]
+        for k in widths:
+            cols.append(cols[-1] + k)
+        cxy = torch.empty(self.cxx.shape[0], cols[-1], dtype=torch.float64, device=self.device)
+        means = [self.cross(i, out=cxy[:, cols[j]:cols[j + 1]])[1] for j, i in enumerate(ids)]
+        w_all, b_all = self.solve(cxy, lams, torch.cat(means))
+        del cxy
         out = {i: {} for i in ids}
-        for li, lam in enumerate(lams):
-            col = 0
-            for i, (c, _) in zip(ids, cross):
-                k = c.shape[1]
-                out[i][lam] = (w_all[li, :, col:col + k].T.float().contiguous(), b_all[li, col:col + k].float())
-                col += k
+        for j, i in enumerate(ids):             # one transposing fp32 copy per target for all lambdas
+            c0, c1 = cols[j], cols[j + 1]
+            wt = w_all[:, :, c0:c1].transpose(1, 2).to(torch.float32, memory_format=torch.contiguous_format)
+            bt = b_all[:, c0:c1].float()
+            for li, lam in enumerate(lams):
+                out[i][lam] = (wt[li], bt[li])
         return out
 
 
