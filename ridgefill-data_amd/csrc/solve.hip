@@ -12,13 +12,16 @@
 //                 the 16 rows x 2 k (A) and 16 columns x 2 k (B) of each half-wave's fragment reads fall in
 //                 distinct banks. The k order of the sums is that of one pass over K in steps of 4.
 //   k_spd_inv64   the inverse of a 64 x 64 symmetric positive definite block by in-place Gauss-Jordan
-//                 elimination without pivoting (stable for SPD matrices), in LDS, one workgroup.
+//                 elimination without pivoting (stable for SPD matrices), one workgroup, the matrix in
+//                 registers and each step's pivot row and column exchanged through LDS.
 //   the inverse   of an n x n SPD matrix (n a multiple of 64) by block recursion on [A11 A12; A21 A22]:
 //                 X11 = A11^-1, T = A21 X11, S = A22 - T A12 (the Schur complement, SPD), X22 = S^-1,
 //                 X21 = -X22 T, U = X11 A12 (= T^T), X11 -= U X21, X12 = X21^T -- every product a k_dgemm.
+//   k_gemv_rows   out = init + alpha v M, rows summed by 4 waves in order (the bias's vector products).
 //   rf_ridge_solve  per lambda: A = C + lam s I padded to a multiple of 64 with an identity block, X = A^-1,
-//                 W = X[:d, :d] Cxy (k_dgemm, the dominant 2 d^2 R flops), bias = mean_y - mean_x W. Up to 8
-//                 lambdas go together: every launch of the recursion carries all of them in its grid.
+//                 W = X[:d, :d] Cxy (k_dgemm, the dominant 2 d^2 R flops), bias = mean_y - (mean_x X) Cxy
+//                 (= mean_y - mean_x W; one pass over Cxy for every lambda). Up to 8 lambdas go together:
+//                 every launch of the recursion carries all of them in its grid.
 #include <algorithm>
 
 #include "rf_common.h"
@@ -139,37 +142,104 @@ __global__ __launch_bounds__(256, 2) void k_dgemm(DgemmArgs a) {
     }
 }
 
-// X = A^-1 for a 64 x 64 SPD block: in-place Gauss-Jordan, thread t owns row t / 4, columns 16 (t % 4) .. + 15.
-// Step k: p = M[k][k]; row k /= p (M[k][k] = 1 / p); every other row i: M[i][j] -= M[i][k] M[k][j] (j != k),
-// M[i][k] = -M[i][k] / p. The row and column of step k are snapshotted in LDS before the update.
+// X = A^-1 for a 64 x 64 SPD block: Gauss-Jordan elimination in place, thread t keeping row t / 4, columns
+// 16 (t % 4) .. + 15 in registers. Step k: p = M[k][k]; row k /= p (M[k][k] = 1 / p); every other row i:
+// M[i][j] -= M[i][k] M[k][j] (j != k), M[i][k] = -M[i][k] / p. Row k and column k as they were before the
+// step are published in LDS (double-buffered by step parity, one barrier per step); the 64 steps are
+// unrolled so that every register index is a constant.
 __global__ __launch_bounds__(256) void k_spd_inv64(const double* __restrict__ A, int64_t lda, double* __restrict__ X,
                                                    int64_t ldx, int64_t sa, int64_t sx) {
-  __shared__ double m[64][65];
-  __shared__ double prow[64], pcol[64];
-  const int t = threadIdx.x, r = t >> 2, c0 = (t & 3) * 16;
+  __shared__ double prow[2][64], pcol[2][64];
+  const int t = threadIdx.x, r = t >> 2, q = t & 3, c0 = q * 16;
   A += static_cast<int64_t>(blockIdx.x) * sa;           // one block per matrix of the batch
   X += static_cast<int64_t>(blockIdx.x) * sx;
+  double m[16];
 #pragma unroll
-  for (int j = 0; j < 16; ++j) m[r][c0 + j] = A[static_cast<int64_t>(r) * lda + c0 + j];
-  __syncthreads();
+  for (int j = 0; j < 16; ++j) m[j] = A[static_cast<int64_t>(r) * lda + c0 + j];
+#pragma unroll
   for (int k = 0; k < 64; ++k) {
-    const double rinv = 1.0 / m[k][k];
-    if (t < 64) {
-      prow[t] = (t == k) ? rinv : m[k][t] * rinv;
-      pcol[t] = m[t][k];
+    const int b = k & 1;
+    if (r == k) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) prow[b][c0 + j] = m[j];
     }
+    if (q == (k >> 4)) pcol[b][r] = m[k & 15];
     __syncthreads();
-    const double f = pcol[r];
+    const double rinv = 1.0 / prow[b][k];
+    const double f = pcol[b][r];
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
-      const int c = c0 + j;
-      if (r == k) m[r][c] = prow[c];
-      else m[r][c] = (c == k) ? -f * rinv : m[r][c] - f * prow[c];
+      const bool diag = q == (k >> 4) && j == (k & 15);
+      const double p = diag ? rinv : prow[b][c0 + j] * rinv;
+      if (r == k) m[j] = p;
+      else m[j] = diag ? -f * rinv : m[j] - f * p;
     }
-    __syncthreads();
   }
 #pragma unroll
-  for (int j = 0; j < 16; ++j) X[static_cast<int64_t>(r) * ldx + c0 + j] = m[r][c0 + j];
+  for (int j = 0; j < 16; ++j) X[static_cast<int64_t>(r) * ldx + c0 + j] = m[j];
+}
+
+// out_l[c] = init[c] + alpha sum_r v_l[r] M_l[r][c] for the batch's NL vectors v_l (sv apart) and matrices M_l
+// (sm apart; sm 0: one matrix for all, read once), c < cols, r < rows. Block: 128 columns (a double2 per
+// lane), its 4 waves summing row quarters in row order; the quarters are added in order (fixed bits).
+template <int NL>
+__global__ __launch_bounds__(256) void k_gemv_rows(const double* __restrict__ v, int64_t sv,
+                                                   const double* __restrict__ M, int64_t ldm, int64_t sm, int rows,
+                                                   int cols, const double* __restrict__ init, double alpha,
+                                                   double* __restrict__ out, int64_t so) {
+  __shared__ double2 part[4][NL][64];
+  const int t = threadIdx.x, lane = t & 63, w = t >> 6;
+  const int c = blockIdx.x * 128 + 2 * lane;
+  const int l0 = NL == 1 ? blockIdx.y : 0;              // NL > 1: the shared matrix, every vector at once
+  const double* __restrict__ Ml = M + static_cast<int64_t>(l0) * sm;
+  const int per = (rows + 3) / 4, r0 = w * per, r1 = min(rows, r0 + per);
+  double2 acc[NL];
+#pragma unroll
+  for (int l = 0; l < NL; ++l) acc[l] = double2{0.0, 0.0};
+  if (c < cols) {
+    const double* __restrict__ p = Ml + c;
+    int r = r0;
+    for (; r + 8 <= r1; r += 8) {
+      double2 x[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) x[u] = *reinterpret_cast<const double2*>(p + static_cast<int64_t>(r + u) * ldm);
+#pragma unroll
+      for (int u = 0; u < 8; ++u)
+#pragma unroll
+        for (int l = 0; l < NL; ++l) {
+          const double s = v[(l0 + l) * sv + r + u];
+          acc[l].x += s * x[u].x;
+          acc[l].y += s * x[u].y;
+        }
+    }
+    for (; r < r1; ++r) {
+      const double2 x = *reinterpret_cast<const double2*>(p + static_cast<int64_t>(r) * ldm);
+#pragma unroll
+      for (int l = 0; l < NL; ++l) {
+        const double s = v[(l0 + l) * sv + r];
+        acc[l].x += s * x.x;
+        acc[l].y += s * x.y;
+      }
+    }
+  }
+#pragma unroll
+  for (int l = 0; l < NL; ++l) part[w][l][lane] = acc[l];
+  __syncthreads();
+  if (w == 0 && c < cols) {
+#pragma unroll
+    for (int l = 0; l < NL; ++l) {
+      double2 s = part[0][l][lane];
+#pragma unroll
+      for (int i = 1; i < 4; ++i) {
+        s.x += part[i][l][lane].x;
+        s.y += part[i][l][lane].y;
+      }
+      double2 o = init ? *reinterpret_cast<const double2*>(init + c) : double2{0.0, 0.0};
+      o.x += alpha * s.x;
+      o.y += alpha * s.y;
+      *reinterpret_cast<double2*>(out + (l0 + l) * so + c) = o;
+    }
+  }
 }
 
 // dst[j][i] = src[i][j] for an rows x cols block (32 x 32 tiles through LDS).
@@ -302,7 +372,20 @@ constexpr int MAX_LAMBDAS = 8;           // lambdas solved together (one batch o
 size_t solve_workspace(int64_t d, int nlam) {
   const int64_t n = padded(d);
   const int nb = std::max(1, std::min(nlam, MAX_LAMBDAS));
-  return static_cast<size_t>(nb) * (2 * n * n + work_doubles(static_cast<int>(n))) * sizeof(double) + 256;
+  return static_cast<size_t>(nb) * (2 * n * n + work_doubles(static_cast<int>(n)) + n) * sizeof(double) + 256;
+}
+
+// out_l = init + alpha v_l M for l < nb with one matrix M shared by the batch (read once).
+void gemv_shared(int nb, const double* v, int64_t sv, const double* M, int64_t ldm, int rows, int cols,
+                 const double* init, double alpha, double* out, int64_t so, hipStream_t stream) {
+  const dim3 grid((cols + 127) / 128), block(256);
+  switch (nb) {
+#define RF_GEMV(NL) \
+  case NL: hipLaunchKernelGGL(k_gemv_rows<NL>, grid, block, 0, stream, v, sv, M, ldm, 0, rows, cols, init, alpha, out, so); break;
+    RF_GEMV(1) RF_GEMV(2) RF_GEMV(3) RF_GEMV(4) RF_GEMV(5) RF_GEMV(6) RF_GEMV(7) RF_GEMV(8)
+#undef RF_GEMV
+    default: break;
+  }
 }
 
 }  // namespace
@@ -329,8 +412,10 @@ extern "C" int rf_ridge_solve(const double* cxx, int64_t ldc, int64_t d, const d
     return fail(RF_EINVAL_SHAPE, "%s: d %lld, R %lld (even), ldc %lld, ldb %lld, ldw %lld (even, >= R), nlam %d, "
                 "w_stride %lld, bias_stride %lld", fn, (long long)d, (long long)R, (long long)ldc, (long long)ldb,
                 (long long)ldw, nlam, (long long)w_stride, (long long)bias_stride);
-  if (!aligned16(cxy) || !aligned16(w) || !aligned16(workspace) || (mean_x && !aligned16(mean_x)))
-    return fail(RF_EINVAL_SHAPE, "%s: cxy, w, mean_x and the workspace must be 16-byte aligned", fn);
+  if (!aligned16(cxy) || !aligned16(w) || !aligned16(workspace) || (mean_x && !aligned16(mean_x)) ||
+      (bias && (!aligned16(bias) || !aligned16(mean_y) || (nlam > 1 && bias_stride % 2))))
+    return fail(RF_EINVAL_SHAPE, "%s: cxy, w, mean_x, mean_y, bias and the workspace must be 16-byte aligned "
+                "(bias_stride even)", fn);
   if (ws_bytes < solve_workspace(d, nlam))
     return fail(RF_EINVAL_ARG, "%s: workspace %zu bytes, needs %zu (rf_ridge_solve_workspace_bytes)", fn, ws_bytes,
                 solve_workspace(d, nlam));
@@ -354,11 +439,15 @@ extern "C" int rf_ridge_solve(const double* cxx, int64_t ldc, int64_t d, const d
     double* wl = w + l0 * w_stride;
     s.gemm(X, n, nn, cxy, ldb, 0, wl, ldw, w_stride, static_cast<int>(d), static_cast<int>(R), static_cast<int>(d),
            1.0, 0.0);
-    if (bias) {
-      double* bl = bias + l0 * bias_stride;
-      s.copy(mean_y, R, 0, bl, R, bias_stride, 1, static_cast<int>(R));
-      s.gemm(mean_x, d, 0, wl, ldw, w_stride, bl, R, bias_stride, 1, static_cast<int>(R), static_cast<int>(d), -1.0,
-             1.0);                                                                // mean_y - mean_x W
+    if (bias && s.rc == RF_OK) {                       // mean_y - mean_x W = mean_y - (mean_x X) Cxy
+      double* u = work + nb * nw;
+      hipLaunchKernelGGL(k_gemv_rows<1>, dim3(static_cast<unsigned>((d + 127) / 128), nb), dim3(256), 0, stream,
+                         mean_x, 0, X, static_cast<int64_t>(n), nn, static_cast<int>(d), static_cast<int>(d), nullptr,
+                         1.0, u, static_cast<int64_t>(n));
+      if (!s.ok()) return s.rc;
+      gemv_shared(nb, u, n, cxy, ldb, static_cast<int>(d), static_cast<int>(R), mean_y, -1.0,
+                  bias + l0 * bias_stride, bias_stride, stream);
+      if (!s.ok()) return s.rc;
     }
     if (s.rc != RF_OK) return s.rc;
   }
