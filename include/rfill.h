@@ -146,6 +146,19 @@ int rf_rope_kv_write(const uint16_t* k, int64_t ld_k, const uint16_t* v, int64_t
 
 /* ---- the exact rows' full layer (Model.layer_rows, code/kva/model.py:259-276) ---- */
 
+/* K / V of scattered rows into their own cache slots: for j < rows, input row j (x [rows, H], statistics
+ * ssq) at position pos[j] (int64, device) is normed, projected by wkv, k_normed and rotated with table row
+ * pos[j] of cs exactly as rf_norm_kv_write does it, and written to cache slot pos[j]. The exact rows of a
+ * filled layer (code/kva/kva.py:392-454 scatters the rows' inputs into the layer's fill): once the layer
+ * is filled from every prefix row, this overwrites the rows' slots with the K / V of their exact inputs.
+ * Arguments and limits as rf_norm_kv_write; every pos[j] must lie in [0, cap) of the cache and in the
+ * table. The rows run through the few-rows partials (M <= 512 per launch) and the reduce epilogue: a
+ * workspace of rf_gemm_workspace_bytes(min(rows, 512), 2 hkv d, H) bytes is required. */
+int rf_norm_kv_rows(const uint16_t* x, int64_t ldx, const float* ssq, int64_t rows, int64_t H, float eps,
+                    const uint16_t* wkv, int hkv, int d, const uint16_t* knorm, int knorm_kind, const uint16_t* cs,
+                    int rot, const int64_t* pos, uint16_t* kbuf, uint16_t* vbuf, int64_t head_stride,
+                    int64_t row_stride, void* workspace, size_t ws_bytes, hipStream_t stream);
+
 /* out[j] = x[rows[j]] for j < nrows, bit-exact, and out's row sum-of-squares partials ssq [nrows, H / 256]
  * (the rows' input RMSNorm statistics). The gather of h[rows] in layer_rows (code/kva/model.py:270); a row
  * outside [0, P) gives a zero row. rows: int64 on the device. */

@@ -542,6 +542,7 @@ struct KvArgs {
   uint16_t* vbuf;
   int64_t head_stride, row_stride, slot0;
   const int64_t* pos;   // RoPE table row of input row j: pos[j] (null: j)
+  const int64_t* slot = nullptr;   // cache slot of input row j: slot[j] (null: slot0 + j; reduce epilogue only)
 };
 
 // k_norm of one chunk's 8 values given the head's inverse RMS (code/kva/ops.py:14-25 per head), with
@@ -713,14 +714,14 @@ __device__ __forceinline__ float head_ssq(const KvArgs& a, const KvLane& L, cons
 
 // One row's chunk of the K / V epilogue: get(c) returns the row's normed bf16 chunk c (of the tile
 // column); k_norm and RoPE for K chunks (k_chunk, with the row's table entries `re`, rope_fetch), then
-// a streaming store into slot slot0 + gm. All lanes of a 32-lane row group call this, ok or not.
+// a streaming store into slot slot0 + gm (slot[gm] if given). All lanes of a 32-lane row group call this, ok or not.
 template <class Get>
 __device__ __forceinline__ void kv_chunk_row(const KvArgs& a, const KvLane& L, Get get, int ch, int64_t gm, bool ok,
                                              const RopeEnt& re) {
   const uint4 v = get(ch);
   const float ss = head_ssq(a, L, v);
   if (!ok) return;
-  uint16_t* dst = L.dst0 + (a.slot0 + gm) * a.row_stride;
+  uint16_t* dst = L.dst0 + (a.slot ? a.slot[gm] : a.slot0 + gm) * a.row_stride;
   if (!L.is_k || (!L.norm && !L.rope)) {
     st_stream16(dst, v);
     return;
@@ -1842,6 +1843,50 @@ extern "C" int rf_norm_kv_write(const uint16_t* x, int64_t ldx, const float* ssq
                        static_cast<const float*>(workspace), pl.splits, static_cast<int>(rows), static_cast<int>(N), ar);
   }
   return check_launch("rf_norm_kv_write");
+}
+
+extern "C" int rf_norm_kv_rows(const uint16_t* x, int64_t ldx, const float* ssq, int64_t rows, int64_t H,
+                               float eps, const uint16_t* wkv, int hkv, int d, const uint16_t* knorm, int knorm_kind,
+                               const uint16_t* cs, int rot, const int64_t* pos, uint16_t* kbuf, uint16_t* vbuf,
+                               int64_t head_stride, int64_t row_stride, void* workspace, size_t ws_bytes,
+                               hipStream_t stream) {
+  const char* fn = "rf_norm_kv_rows";
+  if (!x || !ssq || !wkv || !cs || !pos || !kbuf || !vbuf || !workspace)
+    return fail(RF_EINVAL_ARG, "%s: null pointer", fn);
+  if (rows < 0 || rows > (1ll << 30)) return fail(RF_EINVAL_SHAPE, "%s: rows = %lld out of range", fn, (long long)rows);
+  if (H <= 0 || H % BK || H % SSQ_COLS)
+    return fail(RF_EINVAL_SHAPE, "%s: H = %lld must be a multiple of 256", fn, (long long)H);
+  if (d <= 0 || d % 8 || 256 % d || hkv <= 0 || (2ll * hkv * d) % BN)
+    return fail(RF_EUNSUPPORTED, "%s: head_dim %d / kv heads %d (need 256 %% d == 0, d %% 8 == 0, 2 hkv d %% 256 == 0)",
+                fn, d, hkv);
+  if (rot <= 0 || rot > d || rot % 2 || ((rot / 2) % 8 && rot / 2 != 4))
+    return fail(RF_EUNSUPPORTED, "%s: rotary dims %d of head_dim %d", fn, rot, d);
+  if (knorm && knorm_kind != 0 && knorm_kind != 1) return fail(RF_EINVAL_ARG, "%s: knorm_kind %d", fn, knorm_kind);
+  if (ldx < H || ldx % 8 || ldx > (1 << 21) || head_stride % 8 || row_stride % 8 || row_stride < d)
+    return fail(RF_EINVAL_SHAPE, "%s: strides (ldx %lld, head %lld, row %lld)", fn, (long long)ldx,
+                (long long)head_stride, (long long)row_stride);
+  if (!aligned16(x) || !aligned16(wkv) || !aligned16(kbuf) || !aligned16(vbuf) || !aligned16(cs) ||
+      !aligned16(workspace) || (knorm && !aligned16(knorm)))
+    return fail(RF_EINVAL_SHAPE, "%s: pointers must be 16-byte aligned", fn);
+  if (!(eps >= 0.f)) return fail(RF_EINVAL_ARG, "%s: eps %g", fn, static_cast<double>(eps));
+  const int64_t N = 2ll * hkv * d;
+  // chunks of at most ROWS_MAX rows, each through the few-rows partials and the reduce epilogue (the only
+  // epilogue that writes to per-row slots)
+  const int64_t chunk = std::min<int64_t>(rows, ROWS_MAX);
+  if (rows > 0 && ws_bytes < split_bytes(chunk, N, H))
+    return fail(RF_EINVAL_ARG, "%s: workspace %zu bytes, needs %zu (rf_gemm_workspace_bytes of min(rows, 512) x %lld x %lld)",
+                fn, ws_bytes, split_bytes(chunk, N, H), (long long)N, (long long)H);
+  for (int64_t r0 = 0; r0 < rows; r0 += ROWS_MAX) {
+    const int64_t m = std::min<int64_t>(ROWS_MAX, rows - r0);
+    const Plan pl = plan(m, N, H);
+    KvArgs a{ssq + r0 * (H / SSQ_COLS), static_cast<int>(H / SSQ_COLS), static_cast<float>(H), eps, hkv, d, knorm,
+             knorm_kind, cs, rot, kbuf, vbuf, head_stride, row_stride, 0, pos + r0};
+    a.slot = pos + r0;
+    launch_partials(x + r0 * ldx, ldx, wkv, H, m, N, H, pl, workspace, stream);
+    hipLaunchKernelGGL(k_norm_kv_reduce, reduce_grid(m, N), dim3(256), 0, stream, static_cast<const float*>(workspace),
+                       pl.splits, static_cast<int>(m), static_cast<int>(N), a);
+  }
+  return check_launch(fn);
 }
 
 extern "C" int rf_norm_q(const uint16_t* x, int64_t ldx, const float* ssq, int64_t rows, int64_t H, float eps,

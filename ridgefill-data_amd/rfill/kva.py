@@ -426,7 +426,13 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
     xbuf = [torch.empty(P, H, dtype=torch.bfloat16, device=dev) for _ in range(2)]
     sbuf = [torch.empty(P, ops.ssq_parts(H), dtype=torch.float32, device=dev) for _ in range(2)]
     base_ssq = (ops.row_ssq(b) if rows is None and "identity" in fills.values() else None)
-    state = {"hr": ops.row_gather(b, rows)[0] if computed else None}
+    # attention-only stacks filled by their maps: the fill of a layer reads the exact rows only at their own
+    # slots, so every layer is filled first (grouped, as without rows) and the rows then overwrite their
+    # K / V layer by layer (FillModel.rows_over_fill); GDN layers carry the rows' inputs into later states
+    decoupled = (computed and not overlap and all(model.layer_types[i] == "attn" and fills[i] == "proj"
+                                                  for i in layers))
+    g0 = ops.row_gather(b, rows) if computed else (None, None)
+    state = {"hr": g0[0], "sr": g0[1]}
     qpos = rows if rows is not None else None
     inputs = {}
 
@@ -462,11 +468,14 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
                 state["hr"] = model.layer(i, state["hr"], qpos, cache)[0]
             return
         x, ssq = inputs[slot]
-        if computed:
+        if computed and not decoupled:
             if row_inputs is not None:
                 row_inputs[i] = state["hr"]
             ops.row_scatter(x, ssq, rows, state["hr"])
-            state["hr"] = model.layer_rows(i, x, pos, rows, cache, ssq=ssq, cs=cs)
+            if i == layers[-1]:                         # the rows' output past the last late layer is unused
+                model.fill(i, x, pos, cache, ssq=ssq, cs=cs)
+            else:
+                state["hr"] = model.layer_rows(i, x, pos, rows, cache, ssq=ssq, cs=cs)
         else:
             model.fill(i, x, pos, cache, ssq=ssq, cs=cs)
 
@@ -480,8 +489,8 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
 
     gbuf = []
 
-    def can_group(i):                                   # layers filled by their maps, no computed rows
-        return not computed and fills[i] == "proj"
+    def can_group(i):                                   # layers filled by their maps, no rows computed between
+        return (not computed or decoupled) and fills[i] == "proj"
 
     def run_group(ids):
         """The maps of several late layers in one launch (the GEMM fills whole waves of the GPU, with no tail
@@ -492,7 +501,7 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
                          torch.empty(P, ops.ssq_parts(H), dtype=torch.float32, device=dev)))
         xs, ss = [g[0] for g in gbuf[:len(ids)]], [g[1] for g in gbuf[:len(ids)]]
         arm.projector.apply_batch(ids, b, xs, ss)
-        if rows is not None:                            # given row inputs
+        if rows is not None and not computed:           # given row inputs
             for i, x, q in zip(ids, xs, ss):
                 hri = (hr[i] if isinstance(hr, dict) else hr).to(dev, torch.bfloat16)
                 if row_inputs is not None:
@@ -515,6 +524,19 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
         two_stream(layers, produce, consume, dev)
     else:
         serial(layers, produce, consume, dev, pair=(can_pair, consume_pair), group=(ATTN_GROUP, can_group, run_group))
+    if decoupled:
+        # every layer is filled from the prefix rows' map outputs; the rows now run their layers in order, each
+        # overwriting its own K / V slots (their inputs replace the fill's at those rows only)
+        hr_i, sr_i = state["hr"], state["sr"]
+        qp = pos[rows]
+        for i in layers:
+            if row_inputs is not None:
+                row_inputs[i] = hr_i
+            out = model.rows_over_fill(i, hr_i, sr_i, pos, rows, cache, cs, full=i != layers[-1], rows_max=P - 1,
+                                       qpos=qp)
+            if out is not None:
+                hr_i, sr_i = out
+        state["hr"] = hr_i
     return cache, P
 
 

@@ -434,6 +434,39 @@ class FillModel:
                                 workspace=self._attn_workspace(R, c["n"], x.device))
         return self._out_mlp(w, xr, self._gate(w, xr, sr, o))[0]
 
+    def rows_over_fill(self, i, h, ssq, pos, rows, cache, cs, full=True, rows_max=None, qpos=None):
+        """The exact rows' layer i over a cache already filled from every prefix row (fill() or
+        fill_attn_batch() of the prefix rows' inputs, the rows' slots holding their fill values): the rows'
+        own K / V, from their exact inputs h [R, H] (row sum-of-squares partials ssq), overwrite their slots
+        (ops.norm_kv_rows), which leaves the cache layer_rows() builds by scattering the inputs in before the
+        fill (code/kva/kva.py:392-454); then, if full, the rows' queries attend over the keys up to their own
+        position, o_proj, the residual and the MLP (code/kva/model.py:259-276). Attention layers only: a GDN
+        layer's fill carries the rows' inputs into every later state. rows: sorted prefix rows (int64 on the
+        device), also their cache slots and table rows of cs (the RoPE table of pos); rows_max: a host bound on
+        them; qpos: pos[rows] if already formed. Returns (output [R, H] bf16, its sum-of-squares partials), or
+        None when not full."""
+        if self.layer_types[i] != "attn":
+            raise ValueError(f"rows_over_fill: layer {i} is {self.layer_types[i]}; attention layers only")
+        c = cache[i]
+        R, H = h.shape
+        wl = self._layer(i)
+        ops.norm_kv_rows(h, ssq, self.eps, wl["wkv"], self.n_kv, self.head_dim, wl.get("k_norm"), self.knorm_kind,
+                         cs, rows, c["kbuf"], c["vbuf"], pos_max=rows_max,
+                         workspace=self.gemm_workspace(min(R, 512), wl["wkv"].shape[0], H, h.device))
+        if not full:
+            return None
+        w = self._pack_rows(i)
+        q = ops.norm_q(h, ssq, self.eps, w["wq"], self.n_heads, self.head_dim, w.get("q_norm"), self.knorm_kind, cs,
+                       rows, workspace=self.gemm_workspace(R, w["wq"].shape[0], H, h.device))
+        qpos = pos[rows] if qpos is None else qpos
+        if self._causal_ok():
+            o = ops.attend_causal(q, 0, c["kbuf"], c["vbuf"], c["n"], self.n_heads, self.scale, qpos=qpos,
+                                  workspace=self._causal_workspace(R, c["n"], h.device))
+        else:
+            o = ops.attend_rows(q, qpos, c["kbuf"], c["vbuf"], c["n"], self.n_heads, self.scale,
+                                workspace=self._attn_workspace(R, c["n"], h.device))
+        return self._out_mlp(w, h, self._gate(w, h, ssq, o))
+
     def _out_mlp(self, w, h, o):
         """The rest of the layer after attention: h + o W_o^T, then the SwiGLU MLP with its residual
         (code/kva/model.py:112-118, :254-257), with the reference's bf16 roundings. Returns the layer

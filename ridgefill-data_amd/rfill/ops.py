@@ -284,6 +284,41 @@ def norm_kv_write(x, ssq, eps, wkv, hkv, d, knorm, knorm_kind, cs, kbuf, vbuf, s
               int(slot_begin), cap, _ptr(ws), nb, _stream(x))
 
 
+def norm_kv_rows(x, ssq, eps, wkv, hkv, d, knorm, knorm_kind, cs, pos, kbuf, vbuf, workspace="auto", pos_max=None):
+    """K / V of scattered rows x [rows, H] at positions pos (int64, device) into cache slots pos: the
+    arithmetic of norm_kv_write, each row written to its own position's slot (the exact rows of a layer
+    already filled from every prefix row). pos_max: a bound on pos known on the host (else read from the
+    device, which waits for it); it must lie below the cache capacity and the table's rows."""
+    _need(x, "x", torch.bfloat16, 2)
+    _need(ssq, "ssq", torch.float32, 2)
+    _need(wkv, "wkv", torch.bfloat16, 2)
+    _need(cs, "cs", torch.bfloat16, 2)
+    _need(pos, "pos", torch.int64, 1)
+    rows, H = x.shape
+    if tuple(ssq.shape) != (rows, ssq_parts(H)) or not ssq.is_contiguous():
+        raise ValueError("norm_kv_rows: ssq shape")
+    if tuple(wkv.shape) != (2 * hkv * d, H) or not wkv.is_contiguous():
+        raise ValueError(f"norm_kv_rows: wkv {tuple(wkv.shape)}, expected ({2 * hkv * d}, {H})")
+    if pos.shape[0] != rows or not pos.is_contiguous() or not cs.is_contiguous():
+        raise ValueError("norm_kv_rows: pos / cs")
+    if knorm is not None:
+        _need(knorm, "knorm", torch.bfloat16, 1)
+        if knorm.shape[0] != d:
+            raise ValueError("norm_kv_rows: knorm width")
+    hs, rs, cap = _cache_args(kbuf, vbuf, hkv, d, 0, rows)
+    if rows == 0:
+        return
+    hi = int(pos.max().item()) if pos_max is None else int(pos_max)
+    if pos_max is None and int(pos.min().item()) < 0:
+        raise ValueError("norm_kv_rows: negative position")
+    if hi >= min(cap, cs.shape[0]):
+        raise ValueError(f"norm_kv_rows: position {hi} beyond the cache ({cap} slots) or the table ({cs.shape[0]} rows)")
+    ws, nb = _ws(workspace, min(rows, 512), 2 * hkv * d, H, x.device)
+    _lib.call("rf_norm_kv_rows", _ptr(x), x.stride(0), _ptr(ssq), rows, H, float(eps), _ptr(wkv), hkv, d,
+              _ptr(knorm), int(knorm_kind), _ptr(cs), cs.shape[1], _ptr(pos), _ptr(kbuf), _ptr(vbuf), hs, rs,
+              _ptr(ws), nb, _stream(x))
+
+
 def rope_kv_write(k, v, cs, kbuf, vbuf, slot_begin):
     """fill_kv: RoPE on pre-RoPE k and the write of k / v [m, hkv, d] into rows [slot_begin, +m)."""
     for name, t in (("k", k), ("v", v)):

@@ -301,3 +301,34 @@ def test_attend_rows_head_dim_256_many_queries(dev):
     err = rel_err(wide, want)
     print(f"head_dim 256, {nq} queries: rel err {err:.2e}")
     assert err < TOL
+
+
+@pytest.mark.parametrize("R,knorm", [(287, True), (700, False)])
+def test_norm_kv_rows_writes_each_row_at_its_slot(dev, R, knorm):
+    """rf_norm_kv_rows: row j's K / V, normed, projected, k_normed and rotated at position rows[j], land in
+    slot rows[j] and nowhere else; bit-identical to rf_norm_kv_write of the same rows at slots 0.. with the
+    gathered RoPE table, chunk by chunk of at most 512 rows (both take the few-rows partials then)."""
+    from rfill import ops
+    H, hkv, d, P = 1024, 2, 128, 3000
+    g = torch.Generator().manual_seed(R)
+    rows = torch.randperm(P, generator=g)[:R].sort().values.to(dev)
+    x = (torch.randn(R, H, generator=g)).to(torch.bfloat16).to(dev)
+    ssq = ops.row_ssq(x)
+    wkv = (torch.randn(2 * hkv * d, H, generator=g) / H ** 0.5).to(torch.bfloat16).to(dev)
+    kn = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(dev) if knorm else None
+    inv = 1.0 / (1e6 ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    cs = ops.rope_table(torch.arange(P, device=dev), inv.to(dev))
+    kb, vb = (torch.zeros(hkv, P, d, dtype=torch.bfloat16, device=dev) for _ in range(2))
+    ops.norm_kv_rows(x, ssq, 1e-6, wkv, hkv, d, kn, 0, cs, rows, kb, vb)
+    want_k, want_v = (torch.zeros(hkv, R, d, dtype=torch.bfloat16, device=dev) for _ in range(2))
+    for r0 in range(0, R, 512):
+        r1 = min(R, r0 + 512)
+        csr = cs[rows[r0:r1]].contiguous()
+        ops.norm_kv_write(x[r0:r1], ssq[r0:r1], 1e-6, wkv, hkv, d, kn, 0, csr, want_k, want_v, r0, workspace="auto")
+    torch.cuda.synchronize()
+    assert torch.equal(kb[:, rows], want_k) and torch.equal(vb[:, rows], want_v)
+    rest = torch.ones(P, dtype=torch.bool, device=dev)
+    rest[rows] = False
+    assert not kb[:, rest].any() and not vb[:, rest].any()
+    with pytest.raises(ValueError, match="beyond the cache"):
+        ops.norm_kv_rows(x, ssq, 1e-6, wkv, hkv, d, kn, 0, cs, rows, kb[:, :100], vb[:, :100])
