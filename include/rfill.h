@@ -159,6 +159,20 @@ int rf_norm_kv_rows(const uint16_t* x, int64_t ldx, const float* ssq, int64_t ro
                     int rot, const int64_t* pos, uint16_t* kbuf, uint16_t* vbuf, int64_t head_stride,
                     int64_t row_stride, void* workspace, size_t ws_bytes, hipStream_t stream);
 
+/* The queries and the K / V of scattered rows in one product: wqkv [hq d + 2 hkv d, H] holds the query
+ * projection's rows then the K and V projections' (each with the input norm gain folded in). Row j of
+ * x [rows, H] (statistics ssq) at position pos[j]: its queries, with qnorm (or none) and RoPE table row
+ * pos[j], to q row j (row stride ldq), as rf_norm_q writes them; its K / V, with knorm, to cache slot pos[j],
+ * as rf_norm_kv_rows writes them (norm_kind is the kind of both norms). One few-rows product per 512 rows,
+ * then the two epilogues over its column ranges. Limits as rf_norm_q and rf_norm_kv_rows; a workspace of
+ * rf_gemm_workspace_bytes(min(rows, 512), hq d + 2 hkv d, H) bytes is required. The exact rows' layer input
+ * side (code/kva/model.py:234-245, :340-352 on the rows of a filled layer). */
+int rf_norm_qkv_rows(const uint16_t* x, int64_t ldx, const float* ssq, int64_t rows, int64_t H, float eps,
+                     const uint16_t* wqkv, int hq, int hkv, int d, const uint16_t* qnorm, const uint16_t* knorm,
+                     int norm_kind, const uint16_t* cs, int rot, const int64_t* pos, uint16_t* q, int64_t ldq,
+                     uint16_t* kbuf, uint16_t* vbuf, int64_t head_stride, int64_t row_stride, void* workspace,
+                     size_t ws_bytes, hipStream_t stream);
+
 /* out[j] = x[rows[j]] for j < nrows, bit-exact, and out's row sum-of-squares partials ssq [nrows, H / 256]
  * (the rows' input RMSNorm statistics). The gather of h[rows] in layer_rows (code/kva/model.py:270); a row
  * outside [0, P) gives a zero row. rows: int64 on the device. */
@@ -216,6 +230,24 @@ int rf_attend_causal_workspace_bytes(int64_t nq, int hq, int hkv, int d, int64_t
  * residual adds of layer_rows (code/kva/model.py:274, Model.mlp :114). out may alias x. */
 int rf_residual_add(const uint16_t* x, int64_t ldx, const uint16_t* y, int64_t ldy, uint16_t* out, int64_t ldo,
                     float* ssq, int64_t rows, int64_t H, hipStream_t stream);
+
+/* out = bf16(res + bf16(x w^T)) for x [M, K] (row stride ldx), w [N, K], res [M, N] (row stride ldr), and
+ * out's row sum-of-squares partials ssq [M, N / 256]: rf_map_apply without a bias followed by
+ * rf_residual_add(res, out), bit-identical to that pair. When every row runs through the split-K sums (a
+ * few rows with the workspace of rf_gemm_workspace_bytes(M, N, K)) the residual is added in the sums'
+ * epilogue, one launch fewer. o_proj and down with their residuals (code/kva/model.py:112-118). */
+int rf_map_apply_residual(const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* res, int64_t ldr,
+                          uint16_t* out, int64_t ldo, float* ssq, int64_t M, int64_t K, int64_t N, void* workspace,
+                          size_t ws_bytes, hipStream_t stream);
+
+/* SwiGLU of a normed [gate; up] product: act [P, I] = rf_silu_mul of rf_norm_linear(x, ssq, eps, w) with
+ * w [2 I, H] (gate rows then up rows, the norm gain folded in), bit-identical to that pair. With a few rows
+ * and the workspace of rf_gemm_workspace_bytes(P, 2 I, H) SwiGLU runs in the split sums' epilogue and gu
+ * is not touched (may be NULL); otherwise gu [P, 2 I] (row stride ldg) receives the product first. Needs
+ * H and I multiples of 256. The MLP's first half (code/kva/model.py:112-118). */
+int rf_norm_linear_swiglu(const uint16_t* x, int64_t ldx, const float* ssq, int64_t P, int64_t H, float eps,
+                          const uint16_t* w, int64_t I, uint16_t* act, int64_t lda, uint16_t* gu, int64_t ldg,
+                          void* workspace, size_t ws_bytes, hipStream_t stream);
 
 /* SwiGLU: act[j, c] = bf16(bf16(silu(gu[j, c])) * gu[j, I + c]) for c < I (gate columns then up columns of
  * one in-projection). Model.mlp's F.silu(gate) * up (code/kva/model.py:112-119). */

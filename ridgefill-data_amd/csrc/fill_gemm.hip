@@ -862,9 +862,12 @@ constexpr int RED_ROWS = 8;
 
 // The unsplit map epilogue on split sums: x = bf16(sum + bias) and the rows' sum-of-squares partial of
 // this 256-column group, formed in the order every producer uses (one wave per row).
+// res (optional): the residual stream, X = bf16(res + bf16(sum + bias)) (rf_residual_add's rounding after
+// the product's), the statistics then being X's.
 __global__ __launch_bounds__(256) void k_map_apply_reduce(const float* __restrict__ part, int splits,
                                                           const uint16_t* __restrict__ bias, uint16_t* __restrict__ X,
-                                                          int64_t ldx, float* __restrict__ ssq, int M, int N) {
+                                                          int64_t ldx, float* __restrict__ ssq, int M, int N,
+                                                          const uint16_t* __restrict__ res = nullptr, int64_t ldr = 0) {
   __shared__ uint4 img[RED_ROWS * 32];
   const int t = threadIdx.x, r = t >> 5, ch = t & 31, tn = blockIdx.y, n0 = tn * BN;
   const int m = blockIdx.x * RED_ROWS + r;
@@ -876,6 +879,11 @@ __global__ __launch_bounds__(256) void k_map_apply_reduce(const float* __restric
       const uint4 b = *reinterpret_cast<const uint4*>(bias + n0 + ch * 8);
 #pragma unroll
       for (int e = 0; e < 8; ++e) v[e] += bf2f(lane_of(b, e));
+    }
+    if (res) {
+      const uint4 h = *reinterpret_cast<const uint4*>(res + static_cast<int64_t>(m) * ldr + n0 + ch * 8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = bf2f(lane_of(h, e)) + bf2f(f2bf(v[e]));
     }
     o = make_uint4(bf16_pair(v[0], v[1]), bf16_pair(v[2], v[3]), bf16_pair(v[4], v[5]), bf16_pair(v[6], v[7]));
     *reinterpret_cast<uint4*>(X + static_cast<int64_t>(m) * ldx + n0 + ch * 8) = o;
@@ -909,6 +917,32 @@ __global__ __launch_bounds__(256) void k_norm_linear_reduce(const float* __restr
   *reinterpret_cast<uint4*>(out + static_cast<int64_t>(m) * ldo + n0 + ch * 8) =
       make_uint4(bf16_pair(v[0] * rs, v[1] * rs), bf16_pair(v[2] * rs, v[3] * rs), bf16_pair(v[4] * rs, v[5] * rs),
                  bf16_pair(v[6] * rs, v[7] * rs));
+}
+
+// SwiGLU on the split sums of a [gate; up] product (gate columns [0, I), up columns [I, 2 I) of the partial
+// planes, row stride N): act = bf16(bf16(silu(g)) * u) with g, u = bf16(sum * r_row), the roundings of the
+// unsplit norm + linear epilogue followed by rf_silu_mul.
+__global__ __launch_bounds__(256) void k_swiglu_reduce(const float* __restrict__ part, int splits,
+                                                       const float* __restrict__ ssq, int K, float eps,
+                                                       uint16_t* __restrict__ act, int64_t lda, int M, int N, int I) {
+  const int t = threadIdx.x, r = t >> 5, ch = t & 31, n0 = blockIdx.y * BN;
+  const int m = blockIdx.x * RED_ROWS + r;
+  if (m >= M) return;
+  const int nparts = K / SSQ_COLS;
+  float s2 = 0.f;
+  for (int i = 0; i < nparts; ++i) s2 += ssq[static_cast<int64_t>(m) * nparts + i];
+  const float rs = 1.0f / sqrtf(s2 / static_cast<float>(K) + eps);
+  float g[8], u[8], o[8];
+  const int64_t plane = static_cast<int64_t>(M) * N, at = static_cast<int64_t>(m) * N + n0 + ch * 8;
+  split_sums(part, splits, plane, at, g);
+  split_sums(part, splits, plane, at + I, u);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float gx = bf2f(f2bf(g[e] * rs)), ux = bf2f(f2bf(u[e] * rs));
+    o[e] = bf2f(f2bf(gx / (1.0f + expf(-gx)))) * ux;
+  }
+  *reinterpret_cast<uint4*>(act + static_cast<int64_t>(m) * lda + n0 + ch * 8) =
+      make_uint4(bf16_pair(o[0], o[1]), bf16_pair(o[2], o[3]), bf16_pair(o[4], o[5]), bf16_pair(o[6], o[7]));
 }
 
 // The unsplit K / V (or query) epilogue on split sums: the normed chunk bf16(sum * r_row), then k_norm,
@@ -1787,6 +1821,63 @@ extern "C" int rf_map_apply(const uint16_t* b, int64_t ldb, const uint16_t* w, c
   return check_launch("rf_map_apply");
 }
 
+extern "C" int rf_map_apply_residual(const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* res,
+                                     int64_t ldr, uint16_t* out, int64_t ldo, float* ssq, int64_t M, int64_t K,
+                                     int64_t N, void* workspace, size_t ws_bytes, hipStream_t stream) {
+  const char* fn = "rf_map_apply_residual";
+  if (!x || !w || !res || !out || !ssq) return fail(RF_EINVAL_ARG, "%s: null pointer", fn);
+  if (M < 0 || M > (1ll << 30)) return fail(RF_EINVAL_SHAPE, "%s: M = %lld out of range", fn, (long long)M);
+  if (K <= 0 || K % BK || N <= 0 || N % BN)
+    return fail(RF_EINVAL_SHAPE, "%s: K %lld must be a multiple of 64 and N %lld of 256", fn, (long long)K, (long long)N);
+  if (ldx < K || ldo < N || ldr < N || ldx % 8 || ldo % 8 || ldr % 8 || ldx > (1 << 21) || K > (1 << 21))
+    return fail(RF_EINVAL_SHAPE, "%s: row strides ldx %lld / ldr %lld / ldo %lld", fn, (long long)ldx, (long long)ldr,
+                (long long)ldo);
+  if (!aligned16(x) || !aligned16(w) || !aligned16(res) || !aligned16(out) || (workspace && !aligned16(workspace)))
+    return fail(RF_EINVAL_SHAPE, "%s: pointers must be 16-byte aligned", fn);
+  if (M == 0) return RF_OK;
+  const Plan pl = plan_with(M, N, K, workspace, ws_bytes);
+  if (pl.split() && pl.m_fused == 0) {             // every row through the split sums: the residual in the reduce
+    launch_partials(x, ldx, w, K, M, N, K, pl, workspace, stream);
+    hipLaunchKernelGGL(k_map_apply_reduce, reduce_grid(M, N), dim3(256), 0, stream,
+                       static_cast<const float*>(workspace), pl.splits, nullptr, out, ldo, ssq, static_cast<int>(M),
+                       static_cast<int>(N), res, ldr);
+    return check_launch(fn);
+  }
+  const int rc = rf_map_apply(x, ldx, w, nullptr, out, ldo, ssq, M, K, N, workspace, ws_bytes, stream);
+  if (rc != RF_OK) return rc;
+  return rf_residual_add(res, ldr, out, ldo, out, ldo, ssq, M, N, stream);
+}
+
+extern "C" int rf_norm_linear_swiglu(const uint16_t* x, int64_t ldx, const float* ssq, int64_t P, int64_t H, float eps,
+                                     const uint16_t* w, int64_t I, uint16_t* act, int64_t lda, uint16_t* gu,
+                                     int64_t ldg, void* workspace, size_t ws_bytes, hipStream_t stream) {
+  const char* fn = "rf_norm_linear_swiglu";
+  if (!x || !ssq || !w || !act) return fail(RF_EINVAL_ARG, "%s: null pointer", fn);
+  if (P < 0 || P > (1ll << 30) || H <= 0 || H % SSQ_COLS || I <= 0 || I % BN)
+    return fail(RF_EINVAL_SHAPE, "%s: P %lld, H %lld (multiple of 256), I %lld (multiple of 256)", fn, (long long)P,
+                (long long)H, (long long)I);
+  if (ldx < H || ldx % 8 || ldx > (1 << 21) || lda < I || lda % 8)
+    return fail(RF_EINVAL_SHAPE, "%s: strides ldx %lld, lda %lld", fn, (long long)ldx, (long long)lda);
+  if (!aligned16(x) || !aligned16(w) || !aligned16(act) || (workspace && !aligned16(workspace)))
+    return fail(RF_EINVAL_SHAPE, "%s: pointers must be 16-byte aligned", fn);
+  if (!(eps >= 0.f)) return fail(RF_EINVAL_ARG, "%s: eps %g", fn, static_cast<double>(eps));
+  if (P == 0) return RF_OK;
+  const int64_t N = 2 * I;
+  const Plan pl = plan_with(P, N, H, workspace, ws_bytes);
+  if (pl.split() && pl.m_fused == 0) {             // every row through the split sums: SwiGLU in the reduce
+    launch_partials(x, ldx, w, H, P, N, H, pl, workspace, stream);
+    hipLaunchKernelGGL(k_swiglu_reduce, reduce_grid(P, I), dim3(256), 0, stream, static_cast<const float*>(workspace),
+                       pl.splits, ssq, static_cast<int>(H), eps, act, lda, static_cast<int>(P), static_cast<int>(N),
+                       static_cast<int>(I));
+    return check_launch(fn);
+  }
+  if (!gu || ldg < N || ldg % 8 || !aligned16(gu))
+    return fail(RF_EINVAL_ARG, "%s: this shape runs unsplit and needs the [P, 2 I] gate / up buffer gu", fn);
+  const int rc = rf_norm_linear(x, ldx, ssq, P, H, eps, w, N, gu, ldg, workspace, ws_bytes, stream);
+  if (rc != RF_OK) return rc;
+  return rf_silu_mul(gu, ldg, P, I, act, lda, stream);
+}
+
 extern "C" int rf_norm_kv_write(const uint16_t* x, int64_t ldx, const float* ssq, int64_t P, int64_t H, float eps,
                                 const uint16_t* wkv, int hkv, int d, const uint16_t* knorm, int knorm_kind,
                                 const uint16_t* cs, int rot, uint16_t* kbuf, uint16_t* vbuf,
@@ -1885,6 +1976,60 @@ extern "C" int rf_norm_kv_rows(const uint16_t* x, int64_t ldx, const float* ssq,
     launch_partials(x + r0 * ldx, ldx, wkv, H, m, N, H, pl, workspace, stream);
     hipLaunchKernelGGL(k_norm_kv_reduce, reduce_grid(m, N), dim3(256), 0, stream, static_cast<const float*>(workspace),
                        pl.splits, static_cast<int>(m), static_cast<int>(N), a);
+  }
+  return check_launch(fn);
+}
+
+extern "C" int rf_norm_qkv_rows(const uint16_t* x, int64_t ldx, const float* ssq, int64_t rows, int64_t H,
+                                float eps, const uint16_t* wqkv, int hq, int hkv, int d, const uint16_t* qnorm,
+                                const uint16_t* knorm, int norm_kind, const uint16_t* cs, int rot, const int64_t* pos,
+                                uint16_t* q, int64_t ldq, uint16_t* kbuf, uint16_t* vbuf, int64_t head_stride,
+                                int64_t row_stride, void* workspace, size_t ws_bytes, hipStream_t stream) {
+  const char* fn = "rf_norm_qkv_rows";
+  if (!x || !ssq || !wqkv || !cs || !pos || !q || !kbuf || !vbuf || !workspace)
+    return fail(RF_EINVAL_ARG, "%s: null pointer", fn);
+  if (rows < 0 || rows > (1ll << 30)) return fail(RF_EINVAL_SHAPE, "%s: rows = %lld out of range", fn, (long long)rows);
+  if (H <= 0 || H % BK || H % SSQ_COLS)
+    return fail(RF_EINVAL_SHAPE, "%s: H = %lld must be a multiple of 256", fn, (long long)H);
+  if (d <= 0 || d % 8 || 256 % d || hq <= 0 || hkv <= 0 || (static_cast<int64_t>(hq) * d) % BN ||
+      (2ll * hkv * d) % BN)
+    return fail(RF_EUNSUPPORTED, "%s: head_dim %d, %d query / %d kv heads (need 256 %% d == 0, d %% 8 == 0, hq d and "
+                "2 hkv d multiples of 256)", fn, d, hq, hkv);
+  if (rot <= 0 || rot > d || rot % 2 || ((rot / 2) % 8 && rot / 2 != 4))
+    return fail(RF_EUNSUPPORTED, "%s: rotary dims %d of head_dim %d", fn, rot, d);
+  if ((qnorm || knorm) && norm_kind != 0 && norm_kind != 1) return fail(RF_EINVAL_ARG, "%s: norm_kind %d", fn, norm_kind);
+  if (ldx < H || ldx % 8 || ldx > (1 << 21) || ldq < static_cast<int64_t>(hq) * d || ldq % 8 || head_stride % 8 ||
+      row_stride % 8 || row_stride < d)
+    return fail(RF_EINVAL_SHAPE, "%s: strides (ldx %lld, ldq %lld, head %lld, row %lld)", fn, (long long)ldx,
+                (long long)ldq, (long long)head_stride, (long long)row_stride);
+  if (!aligned16(x) || !aligned16(wqkv) || !aligned16(q) || !aligned16(kbuf) || !aligned16(vbuf) || !aligned16(cs) ||
+      !aligned16(workspace) || (qnorm && !aligned16(qnorm)) || (knorm && !aligned16(knorm)))
+    return fail(RF_EINVAL_SHAPE, "%s: pointers must be 16-byte aligned", fn);
+  if (!(eps >= 0.f)) return fail(RF_EINVAL_ARG, "%s: eps %g", fn, static_cast<double>(eps));
+  const int64_t NQ = static_cast<int64_t>(hq) * d, NKV = 2ll * hkv * d, N = NQ + NKV;
+  const int64_t chunk = std::min<int64_t>(rows, ROWS_MAX);
+  if (rows > 0 && ws_bytes < split_bytes(chunk, N, H))
+    return fail(RF_EINVAL_ARG, "%s: workspace %zu bytes, needs %zu (rf_gemm_workspace_bytes of min(rows, 512) x %lld x "
+                "%lld)", fn, ws_bytes, split_bytes(chunk, N, H), (long long)N, (long long)H);
+  const float* part = static_cast<const float*>(workspace);
+  for (int64_t r0 = 0; r0 < rows; r0 += ROWS_MAX) {
+    const int64_t m = std::min<int64_t>(ROWS_MAX, rows - r0);
+    const Plan pl = plan(m, N, H);
+    launch_partials(x + r0 * ldx, ldx, wqkv, H, m, N, H, pl, workspace, stream);
+    const int nparts = static_cast<int>(H / SSQ_COLS);
+    const float* s0 = ssq + r0 * nparts;
+    // the query columns [0, NQ): every column a "K" column of hq heads, row j to q row r0 + j
+    const KvArgs aq{s0, nparts, static_cast<float>(H), eps, hq, d, qnorm, norm_kind, cs, rot, q + r0 * ldq,
+                    q + r0 * ldq, static_cast<int64_t>(d), ldq, 0, pos + r0};
+    const dim3 gq = reduce_grid(m, NQ), gkv = reduce_grid(m, NKV);
+    hipLaunchKernelGGL(k_norm_kv_reduce, gq, dim3(256), 0, stream, part, pl.splits, static_cast<int>(m),
+                       static_cast<int>(N), aq);
+    // the K / V columns [NQ, N): the partial planes' rows keep their stride N, the cache slot is the position
+    KvArgs akv{s0, nparts, static_cast<float>(H), eps, hkv, d, knorm, norm_kind, cs, rot, kbuf, vbuf, head_stride,
+               row_stride, 0, pos + r0};
+    akv.slot = pos + r0;
+    hipLaunchKernelGGL(k_norm_kv_reduce, gkv, dim3(256), 0, stream, part + NQ, pl.splits, static_cast<int>(m),
+                       static_cast<int>(N), akv);
   }
   return check_launch(fn);
 }

@@ -341,8 +341,9 @@ class FillModel:
                 qg = wq.view(self.n_heads, 2, self.head_dim, wq.shape[1])
                 w["wq"] = ops.fold_norm(qg[:, 0].reshape(-1, wq.shape[1]).contiguous(), w["ln1"], kind)
                 w["wgate"] = ops.fold_norm(qg[:, 1].reshape(-1, wq.shape[1]).contiguous(), w["ln1"], kind)
-            else:
-                w["wq"] = ops.fold_norm(wq, w["ln1"], kind)
+            else:                                       # [wq; wkv] in one buffer: the exact rows' one product
+                wqkv = torch.cat((ops.fold_norm(wq, w["ln1"], kind), w["wkv"]), 0)
+                w["wqkv"], w["wq"], w["wkv"] = wqkv, wqkv[:wq.shape[0]], wqkv[wq.shape[0]:]
             if self.arch != "llama":
                 w["q_norm"] = dev(a + "q_norm.weight")
             w["wo"] = dev(a + "o_proj.weight")
@@ -449,15 +450,24 @@ class FillModel:
             raise ValueError(f"rows_over_fill: layer {i} is {self.layer_types[i]}; attention layers only")
         c = cache[i]
         R, H = h.shape
-        wl = self._layer(i)
-        ops.norm_kv_rows(h, ssq, self.eps, wl["wkv"], self.n_kv, self.head_dim, wl.get("k_norm"), self.knorm_kind,
-                         cs, rows, c["kbuf"], c["vbuf"], pos_max=rows_max,
-                         workspace=self.gemm_workspace(min(R, 512), wl["wkv"].shape[0], H, h.device))
         if not full:
+            wl = self._layer(i)
+            ops.norm_kv_rows(h, ssq, self.eps, wl["wkv"], self.n_kv, self.head_dim, wl.get("k_norm"),
+                             self.knorm_kind, cs, rows, c["kbuf"], c["vbuf"], pos_max=rows_max,
+                             workspace=self.gemm_workspace(min(R, 512), wl["wkv"].shape[0], H, h.device))
             return None
         w = self._pack_rows(i)
-        q = ops.norm_q(h, ssq, self.eps, w["wq"], self.n_heads, self.head_dim, w.get("q_norm"), self.knorm_kind, cs,
-                       rows, workspace=self.gemm_workspace(R, w["wq"].shape[0], H, h.device))
+        if "wqkv" in w:                                 # queries and the rows' K / V from one product
+            q = ops.norm_qkv_rows(h, ssq, self.eps, w["wqkv"], self.n_heads, self.n_kv, self.head_dim,
+                                  w.get("q_norm"), w.get("k_norm"), self.knorm_kind, cs, rows, c["kbuf"], c["vbuf"],
+                                  pos_max=rows_max,
+                                  workspace=self.gemm_workspace(min(R, 512), w["wqkv"].shape[0], H, h.device))
+        else:
+            ops.norm_kv_rows(h, ssq, self.eps, w["wkv"], self.n_kv, self.head_dim, w.get("k_norm"), self.knorm_kind,
+                             cs, rows, c["kbuf"], c["vbuf"], pos_max=rows_max,
+                             workspace=self.gemm_workspace(min(R, 512), w["wkv"].shape[0], H, h.device))
+            q = ops.norm_q(h, ssq, self.eps, w["wq"], self.n_heads, self.head_dim, w.get("q_norm"), self.knorm_kind,
+                           cs, rows, workspace=self.gemm_workspace(R, w["wq"].shape[0], H, h.device))
         qpos = pos[rows] if qpos is None else qpos
         if self._causal_ok():
             o = ops.attend_causal(q, 0, c["kbuf"], c["vbuf"], c["n"], self.n_heads, self.scale, qpos=qpos,
@@ -473,15 +483,17 @@ class FillModel:
         output [rows, H] bf16 and its row sum-of-squares partials (the next norm's statistics)."""
         R, dev = h.shape[0], h.device
         gws = self.gemm_workspace
-        a, _ = ops.map_apply(o, w["wo"], None, workspace=gws(R, w["wo"].shape[0], w["wo"].shape[1], dev))
-        h1, s1 = ops.residual_add(h, a)
-        gu = ops.norm_linear(h1, s1, self.eps, w["wgu"], workspace=gws(R, w["wgu"].shape[0], w["wgu"].shape[1], dev))
+        h1, s1 = ops.map_apply_residual(o, w["wo"], h, workspace=gws(R, w["wo"].shape[0], w["wo"].shape[1], dev))
         inter = w["inter"]
         act = (torch.zeros if w["wd"].shape[1] != inter else torch.empty)(R, w["wd"].shape[1],
                                                                           dtype=torch.bfloat16, device=dev)
-        ops.silu_mul(gu[:, :2 * inter], act[:, :inter])
-        dn, _ = ops.map_apply(act, w["wd"], None, workspace=gws(R, w["wd"].shape[0], w["wd"].shape[1], dev))
-        return ops.residual_add(h1, dn)
+        wgu = w["wgu"]
+        if wgu.shape[0] == 2 * inter and inter % 256 == 0:
+            ops.norm_linear_swiglu(h1, s1, self.eps, wgu, out=act, workspace=gws(R, wgu.shape[0], wgu.shape[1], dev))
+        else:                                           # [gate; up] padded to a multiple of 256 rows
+            gu = ops.norm_linear(h1, s1, self.eps, wgu, workspace=gws(R, wgu.shape[0], wgu.shape[1], dev))
+            ops.silu_mul(gu[:, :2 * inter], act[:, :inter])
+        return ops.map_apply_residual(act, w["wd"], h1, workspace=gws(R, w["wd"].shape[0], w["wd"].shape[1], dev))
 
     def layer(self, i, h, pos, cache, ssq=None, cs=None):
         """Exact layer i for new rows h [T, H] bf16 at positions pos, appended after the cache's n rows

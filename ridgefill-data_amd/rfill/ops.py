@@ -319,6 +319,46 @@ def norm_kv_rows(x, ssq, eps, wkv, hkv, d, knorm, knorm_kind, cs, pos, kbuf, vbu
               _ptr(ws), nb, _stream(x))
 
 
+def norm_qkv_rows(x, ssq, eps, wqkv, hq, hkv, d, qnorm, knorm, norm_kind, cs, pos, kbuf, vbuf, out=None,
+                  workspace="auto", pos_max=None):
+    """norm_q and norm_kv_rows of the same rows from one product over wqkv = [wq; wkv]: returns the queries
+    [rows, hq d] bf16 and writes the rows' K / V into cache slots pos (see norm_kv_rows for pos_max)."""
+    _need(x, "x", torch.bfloat16, 2)
+    _need(ssq, "ssq", torch.float32, 2)
+    _need(wqkv, "wqkv", torch.bfloat16, 2)
+    _need(cs, "cs", torch.bfloat16, 2)
+    _need(pos, "pos", torch.int64, 1)
+    rows, H = x.shape
+    if tuple(ssq.shape) != (rows, ssq_parts(H)) or not ssq.is_contiguous():
+        raise ValueError("norm_qkv_rows: ssq shape")
+    if tuple(wqkv.shape) != ((hq + 2 * hkv) * d, H) or not wqkv.is_contiguous():
+        raise ValueError(f"norm_qkv_rows: wqkv {tuple(wqkv.shape)}, expected ({(hq + 2 * hkv) * d}, {H})")
+    if pos.shape[0] != rows or not pos.is_contiguous() or not cs.is_contiguous():
+        raise ValueError("norm_qkv_rows: pos / cs")
+    for name, t in (("qnorm", qnorm), ("knorm", knorm)):
+        if t is not None:
+            _need(t, name, torch.bfloat16, 1)
+            if t.shape[0] != d:
+                raise ValueError(f"norm_qkv_rows: {name} width")
+    hs, rs, cap = _cache_args(kbuf, vbuf, hkv, d, 0, rows)
+    out = torch.empty(rows, hq * d, dtype=torch.bfloat16, device=x.device) if out is None else out
+    _need(out, "out", torch.bfloat16, 2)
+    if tuple(out.shape) != (rows, hq * d):
+        raise ValueError("norm_qkv_rows: out shape")
+    if rows == 0:
+        return out
+    hi = int(pos.max().item()) if pos_max is None else int(pos_max)
+    if pos_max is None and int(pos.min().item()) < 0:
+        raise ValueError("norm_qkv_rows: negative position")
+    if hi >= min(cap, cs.shape[0]):
+        raise ValueError(f"norm_qkv_rows: position {hi} beyond the cache ({cap} slots) or the table ({cs.shape[0]} rows)")
+    ws, nb = _ws(workspace, min(rows, 512), (hq + 2 * hkv) * d, H, x.device)
+    _lib.call("rf_norm_qkv_rows", _ptr(x), x.stride(0), _ptr(ssq), rows, H, float(eps), _ptr(wqkv), hq, hkv, d,
+              _ptr(qnorm), _ptr(knorm), int(norm_kind), _ptr(cs), cs.shape[1], _ptr(pos), _ptr(out), out.stride(0),
+              _ptr(kbuf), _ptr(vbuf), hs, rs, _ptr(ws), nb, _stream(x))
+    return out
+
+
 def rope_kv_write(k, v, cs, kbuf, vbuf, slot_begin):
     """fill_kv: RoPE on pre-RoPE k and the write of k / v [m, hkv, d] into rows [slot_begin, +m)."""
     for name, t in (("k", k), ("v", v)):
@@ -486,6 +526,51 @@ def residual_add(x, y, out=None, ssq=None):
     _lib.call("rf_residual_add", _ptr(x), x.stride(0), _ptr(y), y.stride(0), _ptr(out), out.stride(0), _ptr(ssq), rows,
               H, _stream(x))
     return out, ssq
+
+
+def map_apply_residual(x, w, res, out=None, ssq=None, workspace=None):
+    """out = bf16(res + bf16(x w^T)) and its row sum-of-squares partials: map_apply without a bias then
+    residual_add(res, .), bit-identical; with a few rows and a workspace the residual joins the split sums'
+    epilogue."""
+    _need(x, "x", torch.bfloat16, 2)
+    _need(w, "w", torch.bfloat16, 2)
+    _need(res, "res", torch.bfloat16, 2)
+    M, K = x.shape
+    N = w.shape[0]
+    if w.shape[1] != K or not w.is_contiguous() or tuple(res.shape) != (M, N):
+        raise ValueError(f"map_apply_residual: x {tuple(x.shape)}, w {tuple(w.shape)}, res {tuple(res.shape)}")
+    out = torch.empty(M, N, dtype=torch.bfloat16, device=x.device) if out is None else out
+    ssq = torch.empty(M, ssq_parts(N), dtype=torch.float32, device=x.device) if ssq is None else ssq
+    _need(out, "out", torch.bfloat16, 2)
+    _need(ssq, "ssq", torch.float32, 2)
+    if tuple(out.shape) != (M, N) or tuple(ssq.shape) != (M, N // SSQ_COLS) or not ssq.is_contiguous():
+        raise ValueError("map_apply_residual: out / ssq shapes")
+    ws, nb = _ws(workspace, M, N, K, x.device)
+    _lib.call("rf_map_apply_residual", _ptr(x), x.stride(0), _ptr(w), _ptr(res), res.stride(0), _ptr(out),
+              out.stride(0), _ptr(ssq), M, K, N, _ptr(ws), nb, _stream(x))
+    return out, ssq
+
+
+def norm_linear_swiglu(x, ssq, eps, w, out=None, workspace=None):
+    """SwiGLU of the normed [gate; up] product: silu_mul(norm_linear(x, ssq, eps, w)) [rows, I],
+    bit-identical; with a few rows and a workspace SwiGLU joins the split sums' epilogue."""
+    _need(x, "x", torch.bfloat16, 2)
+    _need(ssq, "ssq", torch.float32, 2)
+    _need(w, "w", torch.bfloat16, 2)
+    P, H = x.shape
+    if w.shape[1] != H or w.shape[0] % 2 or not w.is_contiguous() or tuple(ssq.shape) != (P, ssq_parts(H)):
+        raise ValueError(f"norm_linear_swiglu: x {tuple(x.shape)}, w {tuple(w.shape)}, ssq {tuple(ssq.shape)}")
+    I = w.shape[0] // 2
+    out = torch.empty(P, I, dtype=torch.bfloat16, device=x.device) if out is None else out
+    _need(out, "out", torch.bfloat16, 2)
+    if out.shape[0] != P or out.shape[1] < I:
+        raise ValueError(f"norm_linear_swiglu: out {tuple(out.shape)} for {P} rows of {I}")
+    ws, nb = _ws(workspace, P, 2 * I, H, x.device)
+    fused = ws is not None and P <= 512
+    gu = None if fused else torch.empty(P, 2 * I, dtype=torch.bfloat16, device=x.device)
+    _lib.call("rf_norm_linear_swiglu", _ptr(x), x.stride(0), _ptr(ssq), P, H, float(eps), _ptr(w), I, _ptr(out),
+              out.stride(0), _ptr(gu), 0 if gu is None else gu.stride(0), _ptr(ws), nb, _stream(x))
+    return out
 
 
 def silu_mul(gu, out=None):

@@ -332,3 +332,53 @@ def test_norm_kv_rows_writes_each_row_at_its_slot(dev, R, knorm):
     assert not kb[:, rest].any() and not vb[:, rest].any()
     with pytest.raises(ValueError, match="beyond the cache"):
         ops.norm_kv_rows(x, ssq, 1e-6, wkv, hkv, d, kn, 0, cs, rows, kb[:, :100], vb[:, :100])
+
+
+@pytest.mark.parametrize("R,norms", [(287, True), (600, False)])
+def test_norm_qkv_rows_matches_the_separate_products(dev, R, norms):
+    """rf_norm_qkv_rows: queries as rf_norm_q and the rows' K / V at slots pos as rf_norm_kv_rows, from one
+    product over [wq; wkv] (its K split differs, so the bf16 results agree to rounding); slots other than
+    the rows' stay untouched."""
+    from rfill import ops
+    H, hq, hkv, d, P = 1024, 8, 2, 128, 3000
+    g = torch.Generator().manual_seed(R + 1)
+    rows = torch.randperm(P, generator=g)[:R].sort().values.to(dev)
+    x = torch.randn(R, H, generator=g).to(torch.bfloat16).to(dev)
+    ssq = ops.row_ssq(x)
+    wqkv = (torch.randn((hq + 2 * hkv) * d, H, generator=g) / H ** 0.5).to(torch.bfloat16).to(dev)
+    qn = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(dev) if norms else None
+    kn = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(dev) if norms else None
+    inv = 1.0 / (1e6 ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    cs = ops.rope_table(torch.arange(P, device=dev), inv.to(dev))
+    kb, vb, kb2, vb2 = (torch.zeros(hkv, P, d, dtype=torch.bfloat16, device=dev) for _ in range(4))
+    q = ops.norm_qkv_rows(x, ssq, 1e-6, wqkv, hq, hkv, d, qn, kn, 0, cs, rows, kb, vb)
+    q2 = ops.norm_q(x, ssq, 1e-6, wqkv[:hq * d].contiguous(), hq, d, qn, 0, cs, rows, workspace="auto")
+    ops.norm_kv_rows(x, ssq, 1e-6, wqkv[hq * d:].contiguous(), hkv, d, kn, 0, cs, rows, kb2, vb2)
+    torch.cuda.synchronize()
+    for got, want in ((q, q2), (kb[:, rows], kb2[:, rows]), (vb[:, rows], vb2[:, rows])):
+        assert rel_err(got, want) < 5e-3
+    rest = torch.ones(P, dtype=torch.bool, device=dev)
+    rest[rows] = False
+    assert not kb[:, rest].any() and not vb[:, rest].any()
+
+
+@pytest.mark.parametrize("R", [287, 1300])
+def test_fused_residual_and_swiglu_epilogues_are_bit_identical(dev, R):
+    """map_apply_residual == map_apply + residual_add and norm_linear_swiglu == norm_linear + silu_mul, bit
+    for bit, with every row in the split sums' epilogue (287 rows) and through the unsplit kernels (1300)."""
+    from rfill import ops
+    H, I = 1024, 1536
+    g = torch.Generator().manual_seed(R + 7)
+    x = torch.randn(R, H, generator=g).to(torch.bfloat16).to(dev)
+    res = torch.randn(R, H, generator=g).to(torch.bfloat16).to(dev)
+    wo = (torch.randn(H, H, generator=g) / H ** 0.5).to(torch.bfloat16).to(dev)
+    wgu = (torch.randn(2 * I, H, generator=g) / H ** 0.5).to(torch.bfloat16).to(dev)
+    ws = lambda n, k: torch.empty(max(1, ops.gemm_workspace_bytes(R, n, k)), dtype=torch.uint8, device=dev)  # noqa: E731
+    h1, s1 = ops.map_apply_residual(x, wo, res, workspace=ws(H, H))
+    a, _ = ops.map_apply(x, wo, None, workspace=ws(H, H))
+    want_h1, want_s1 = ops.residual_add(res, a)
+    act = ops.norm_linear_swiglu(h1, s1, 1e-5, wgu, workspace=ws(2 * I, H))
+    want_act = ops.silu_mul(ops.norm_linear(want_h1, want_s1, 1e-5, wgu, workspace=ws(2 * I, H)))
+    torch.cuda.synchronize()
+    assert torch.equal(h1, want_h1) and torch.equal(s1, want_s1)
+    assert torch.equal(act, want_act)
