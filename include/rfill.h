@@ -310,12 +310,12 @@ int rf_gdn_workspace_bytes(int64_t rows, int nk, int nv, int dk, int dv, size_t*
 
 /* Size in MiB of the device array rf_gdn_fill_noalloc uses as its workspace (one per GPU, for the life of
  * the process). */
-#define RF_GDN_SCRATCH_MAX 64
+#define RF_GDN_SCRATCH_MAX 56
 
 /* rf_gdn_fill without a workspace argument and without any allocation: the per-chunk products go to a
  * file-scope device array of RF_GDN_SCRATCH_MAX MiB inside the library (its address on each GPU is taken
  * once, on the first call with that GPU current), which holds as many 64-row chunks as fit per pass
- * (45 at 16 key / 32 value heads), so any P runs, in as many passes as it needs; results are
+ * (39 at 16 key / 32 value heads), so any P runs, in as many passes as it needs; results are
  * bit-identical to rf_gdn_fill's. Heads whose one chunk exceeds the array are refused (RF_EINVAL_SHAPE).
  * No counterpart in the reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, serving loops, harnesses that forbid hipMalloc). Every call on one GPU shares its

@@ -6,8 +6,9 @@ largest, 122880 rows (P = 118784, 1188 exact rows).
 
 Checked per late layer, on the CPU oracle's bf16 restatement:
   * cache placement: slots >= P keep a sentinel pattern; every value is finite; the exact rows' slots hold
-    the K / V of their own inputs: the cache equals, bit for bit, the device fill of the projected rows with
-    the rows' inputs copied in by index (the scatter is a bit-exact copy, slot = position);
+    the K / V of their own inputs: the cache equals, bit for bit, the unsplit device fill of the projected
+    rows with each exact row's slot (slot = position) then overwritten by the K / V of its own input
+    (FillModel.rows_over_fill over that fill);
   * K / V values of sampled filled rows and of the exact rows against the oracle's kv() of the same inputs;
   * the exact rows' layer outputs (their next layer's inputs) against the oracle's queries, attention over
     the device's filled cache, o_proj and MLP, and a positive control: the projected rows' K at the exact
@@ -98,10 +99,18 @@ def check_layers(dev, cfg, w, model, proj, cache, ri, out_rows, bitwise_layers=(
         if i > SPLIT:                                   # positive control: the projected rows' K differs
             k_p, _ = om.kv(i, om.in_norm(F.linear(w["h_split"][rows].cpu(), W, B), ln1), rows_c)
             assert rel_err(k_p, k_r) > 10 * TOL and ke < TOL
-        if i in bitwise_layers:                         # placement and scatter: bit-exact against a plain fill
-            x = proj(i, w["h_split"][:P]).index_copy(0, rows, ri[i])
+        if i in bitwise_layers:                         # placement: bit-exact against fill + the rows' overwrite
+            pos = torch.arange(P, device=dev)
+            x = proj(i, w["h_split"][:P])
             ref = model.new_cache()
-            model.fill(i, x, torch.arange(P, device=dev), ref)
+            model.reserve(ref[i], P, model.n_kv, model.head_dim, dev)
+            lw = model.W[i]
+            cs = model.rope_table(pos)
+            ops.norm_kv_write(x, ops.row_ssq(x), model.eps, lw["wkv"], model.n_kv, model.head_dim, lw.get("k_norm"),
+                              model.knorm_kind, cs, ref[i]["kbuf"], ref[i]["vbuf"], 0)
+            model.commit(ref[i], P)
+            model.rows_over_fill(i, ri[i], ops.row_ssq(ri[i]), pos, rows, ref, cs, full=i != w["layers"][-1],
+                                 rows_max=P - 1)
             torch.cuda.synchronize()
             assert torch.equal(ref[i]["k"].view(torch.int16), c["k"].view(torch.int16))
             assert torch.equal(ref[i]["v"].view(torch.int16), c["v"].view(torch.int16))

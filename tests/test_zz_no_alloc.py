@@ -1,7 +1,7 @@
 """The allocation-free GDN fill (rf_gdn_fill_noalloc, the library's own device array as the workspace)
 against rf_gdn_fill with a caller workspace, through the C ABI, bit for bit: two calls in a row on the same
 GPU, the second with fewer rows (the array keeps the first call's contents), at the hybrid's widths
-(16 key / 32 value heads: 45 chunks per pass, so the 9000-row call makes 4 passes); and the refusal of heads
+(16 key / 32 value heads: 39 chunks per pass, so the 9000-row call makes 4 passes); and the refusal of heads
 whose one chunk exceeds the array."""
 import pytest
 import torch
@@ -45,7 +45,7 @@ def test_noalloc_gdn_fill_matches_the_workspace_entry_point(dev):
 
 def test_noalloc_refuses_heads_beyond_the_array(dev):
     from rfill import ops
-    nk = nv = 1024                                      # 66 MB per chunk > 64 MiB
+    nk = nv = 1024                                      # 61 MiB per chunk > 56 MiB
     C = 2 * nk * 128 + nv * 128
     pre = torch.zeros(1, C + 2 * nv, dtype=torch.bfloat16, device=dev)
     conv = torch.zeros(C, 4, dtype=torch.bfloat16, device=dev)
