@@ -403,9 +403,9 @@ def capture_bench(dev, split=SPLIT, n=8192, lams=9):
 def hybrid_bench(dev, reps=3, split=24, n_rows=32768, tail=4096):
     """The Gated-DeltaNet hybrid's late-layer fill (hidden 2048; layers 24..47 = 18 GDN + 6 attention;
     GDN 16 key / 32 value heads of 128, attention 2 KV heads of 256; P = 28672 filled rows from zero
-    state), timed as finish() runs it (fill_late): per layer rf_map_apply, then the GDN fill (rf_norm_linear
-    in-projection + the delta-rule fill, two consecutive GDN layers per rf_gdn_fill_batch) or the attention
-    fill (rf_norm_kv_write). Counted work per filled row (the reference's accounting): GDN layer
+    state), timed as finish() runs it (fill_late: groups of 8 late layers): per layer rf_map_apply, then the
+    GDN fill (rf_norm_linear in-projection + the delta-rule fill, two GDN layers per rf_gdn_fill_batch) or
+    the attention fill (rf_norm_kv_write). Counted work per filled row (the reference's accounting): GDN layer
     2 H (2 nk dk + nv dv + 2 nv) + 2 H^2 + 2 K C + 6 nv dk dv flop, attention layer 2 H^2 + 2 H (2 Hkv d).
     The per-layer means come from a second, layer-by-layer pass (one GDN layer at a time)."""
     from rfill import ops, synth

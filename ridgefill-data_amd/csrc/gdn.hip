@@ -161,7 +161,7 @@ __device__ __forceinline__ float quad_sum(float v) {
 // recomputed by each of the key head's value heads; the first of them writes K's operand orders.
 // Up to BATCH independent layers' fills per launch (the late GDN layers of a fill do not depend on each
 // other): prep blocks take their layer from blockIdx.z, scan blocks from blockIdx.x / (8 nv).
-constexpr int BATCH = 2;
+constexpr int BATCH = RF_GDN_BATCH_MAX;
 struct PrepBatch {
   PrepArgs a[BATCH];
 };
@@ -170,7 +170,7 @@ struct PrepBatch {
 // (240 registers per SIMD), so the fill's prep of the next pass runs alongside the scan.
 template <bool OUT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_num_vgpr(128))) void k_gdn_prep(PrepBatch pb) {
-  const PrepArgs a = blockIdx.z == 0 ? pb.a[0] : pb.a[1];
+  const PrepArgs a = pb.a[blockIdx.z];
   __shared__ __align__(16) uint16_t k_s[CH * KST];  // the k tile, then T (fp32)
   __shared__ __align__(16) uint16_t v_s[CH * KST];
   __shared__ __align__(16) float a_s[CH * FST];     // A
@@ -518,8 +518,8 @@ struct ScanBatch {
 template <bool OUT>
 __global__ __launch_bounds__(256) void k_gdn_scan(ScanBatch sbatch) {
   const int per_layer = sbatch.a[0].nv * 8;
-  const int layer = blockIdx.x >= per_layer ? 1 : 0;
-  const ScanArgs a = layer == 0 ? sbatch.a[0] : sbatch.a[1];
+  const int layer = blockIdx.x / per_layer;
+  const ScanArgs a = sbatch.a[layer];
   __shared__ __align__(16) f32x4 xp[4][4][64];        // X_w partials [wave][row tile][lane]
   __shared__ __align__(16) uint4 yf[2][2][64];        // Y frags [k-step][hi / lo][lane]
   __shared__ __align__(16) uint4 zf[2][2][64];        // Z frags

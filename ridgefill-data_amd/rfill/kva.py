@@ -342,6 +342,9 @@ def two_stream(layers, produce, consume, device):
 
 # Consecutive attention layers filled together by fill_late (one map launch, then one K / V launch per group).
 ATTN_GROUP = 4
+# a hybrid stack's groups (GDN and attention layers): 8 layers, so that the group's GDN fills pair up (the
+# Qwen3.5 pattern of 3 GDN + 1 attention leaves one unpaired GDN layer in every 4)
+HYBRID_GROUP = 8
 
 
 def serial(layers, produce, consume, device, pair=None, group=None):
@@ -495,7 +498,9 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
     def run_group(ids):
         """The maps of several late layers in one launch (the GEMM fills whole waves of the GPU, with no tail
         per layer), then the group's attention layers' K / V fills in one launch and its GDN layers' fills in
-        consecutive pairs; each layer's results are bit-identical to its unsplit map apply and fill alone."""
+        pairs (any two: the layers' fills are independent), each pair's in-projections in one launch right
+        before its delta-rule fill; each layer's results are bit-identical to its unsplit map apply and fill
+        alone."""
         while len(gbuf) < len(ids):
             gbuf.append((torch.empty(P, H, dtype=torch.bfloat16, device=dev),
                          torch.empty(P, ops.ssq_parts(H), dtype=torch.float32, device=dev)))
@@ -511,19 +516,16 @@ def fill_late(model, h_split, arm, exact_rows=None, hr=None, cache=None, overlap
         if attn:
             model.fill_attn_batch([ids[k] for k in attn], [xs[k] for k in attn], pos, cache,
                                   ssqs=[ss[k] for k in attn], cs=cs)
-        k = 0
-        while k < len(ids):
-            if model.layer_types[ids[k]] != "gdn":
-                k += 1
-                continue
-            m = 2 if k + 1 < len(ids) and model.layer_types[ids[k + 1]] == "gdn" else 1
-            model.fill_batch(ids[k:k + m], xs[k:k + m], cache, ssqs=ss[k:k + m])
-            k += m
+        gdn = [k for k, i in enumerate(ids) if model.layer_types[i] == "gdn"]
+        for j in range(0, len(gdn), 2):                 # each pair's in-projections, then its fill: the
+            ks = gdn[j:j + 2]                           # projected rows are read back while still cached
+            model.fill_batch([ids[k] for k in ks], [xs[k] for k in ks], cache, ssqs=[ss[k] for k in ks])
 
     if overlap:
         two_stream(layers, produce, consume, dev)
     else:
-        serial(layers, produce, consume, dev, pair=(can_pair, consume_pair), group=(ATTN_GROUP, can_group, run_group))
+        gsize = HYBRID_GROUP if any(model.layer_types[i] == "gdn" for i in layers) else ATTN_GROUP
+        serial(layers, produce, consume, dev, pair=(can_pair, consume_pair), group=(gsize, can_group, run_group))
     if decoupled:
         # every layer is filled from the prefix rows' map outputs; the rows now run their layers in order, each
         # overwriting its own K / V slots (their inputs replace the fill's at those rows only)
