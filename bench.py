@@ -90,7 +90,9 @@ def fill_step(model, arm, b, pos, cs, xbuf, sbuf, caches, timer=None):
 
 
 def ceilings(dev, P, H):
-    """Library GEMM (hipBLASLt via torch) of the map's shape and a device-to-device copy."""
+    """Library GEMM (hipBLASLt via torch) of the map's shape, a device-to-device copy, and the MFMA throughput
+    the power limit allows (rf_mfma_ceiling: back-to-back bf16 MFMAs on register operands, 2 waves per SIMD)."""
+    from rfill import ops
     a = torch.randn(P, H, device=dev, dtype=torch.bfloat16)
     w = torch.randn(H, H, device=dev, dtype=torch.bfloat16)
     out = torch.empty(P, H, device=dev, dtype=torch.bfloat16)
@@ -100,16 +102,25 @@ def ceilings(dev, P, H):
     t = KernelTimer()
     for _ in range(10):
         t.run("gemm", lambda: torch.matmul(a, w.t(), out=out))
-    src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    src_bytes = 1 << 30
+    src = torch.empty(src_bytes, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
     for _ in range(3):
         dst.copy_(src)
     for _ in range(10):
         t.run("copy", lambda: dst.copy_(src))
+    del src, dst
+    blocks, iters = 512, 20000
+    acc = torch.empty(blocks * 256, dtype=torch.float32, device=dev)
+    for _ in range(2):
+        ops.mfma_ceiling(blocks, iters, acc)
+    for _ in range(5):
+        t.run("mfma", lambda: ops.mfma_ceiling(blocks, iters, acc))
     torch.cuda.synchronize()
     return {"hipblaslt_gemm_tflops": round(2 * P * H * H / t.mean_s("gemm") / 1e12, 1),
-            "copy_gbs": round(2 * src.numel() / t.mean_s("copy") / 1e9, 1),
-            "gemm_shape": [P, H, H]}
+            "copy_gbs": round(2 * src_bytes / t.mean_s("copy") / 1e9, 1),
+            "gemm_shape": [P, H, H],
+            "mfma_power_ceiling_tflops": round(blocks * 4 * 4 * iters * 32768 / t.mean_s("mfma") / 1e12, 1)}
 
 
 def dequant_bench(dev, rows=2560, width=10240, maps=24):
@@ -703,7 +714,12 @@ def main():
         out["kernels"]["rf_dequant_i8_rows"] = dequant_bench(dev)
         out["kernels"]["rf_window_mass"] = window_mass_bench(dev)
         out["kernels"]["rf_dequant_gguf_rows"] = gguf_bench(dev)
-        out["ceilings"] = ceilings(dev, P, H)
+        out["ceilings"] = c = ceilings(dev, P, H)
+        rf = out["roofline"]
+        rf["measured_ceilings_tflops"] = {"mfma_power": c["mfma_power_ceiling_tflops"],
+                                          "hipblaslt_same_shape": c["hipblaslt_gemm_tflops"]}
+        rf["frac_of_mfma_power_ceiling"] = round(rf["achieved"] / c["mfma_power_ceiling_tflops"], 4)
+        rf["frac_of_hipblaslt"] = round(rf["achieved"] / c["hipblaslt_gemm_tflops"], 4)
     del caches, xbuf, sbuf
     torch.cuda.empty_cache()
     if not args.no_finish:

@@ -379,6 +379,13 @@ int rf_transpose_centred(const uint16_t* src, int64_t ld_src, int64_t rows, int6
  * fold; the same bits every run): the sum(0) of a sample block (RidgeStats' sx / sy, code/kva/ridge.py:46, :61). */
 int rf_colsum_fold(const float* partial, int64_t ntiles, int64_t cols, double* sums, hipStream_t stream);
 
+/* A measurement, with no counterpart in the reference: `blocks` workgroups of 256 threads each run 4 x iters
+ * back-to-back v_mfma_f32_32x32x16_bf16 per wave on register operands (pseudo-random bf16), then store one
+ * float per thread to out [blocks * 256]. 32768 flop per MFMA: timed, it gives the MFMA throughput the
+ * GPU's power limit allows with no memory traffic, the ceiling the fill's GEMMs are compared with beside
+ * the nominal peak. */
+int rf_mfma_ceiling(int blocks, int iters, float* out, hipStream_t stream);
+
 /* Gram / cross accumulation C[M, N] += A[M, K] B[N, K]^T: bf16 products summed in fp32 on MFMA over runs
  * of at most fold_rows of K (0: the whole K; else a multiple of 64), each run's sums added into the fp64
  * accumulator C (row stride ldc) as it ends. With A = X^T and B = X^T or Y^T of sample rows and fold_rows

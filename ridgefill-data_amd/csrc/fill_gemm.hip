@@ -1044,6 +1044,44 @@ __global__ __launch_bounds__(NTHR) void k_gram(const uint16_t* __restrict__ A, i
   }
 }
 
+// The MFMA throughput the power budget allows: back-to-back v_mfma_f32_32x32x16_bf16 on register operands,
+// four independent accumulators per wave each with its own pair of operands (pseudo-random bf16: random
+// sign, mantissa and two low exponent bits, magnitudes 2^-7 .. 2^-3), so the operands change from one
+// MFMA to the next as a GEMM's fragments do; no memory traffic but one store per lane at the end. A
+// measurement, not part of the fill.
+__global__ __launch_bounds__(256) void k_mfma_ceiling(int iters, float* __restrict__ out) {
+  const uint32_t id = blockIdx.x * 256u + threadIdx.x;
+  uint32_t h = id * 0x9e3779b9u + 0x7f4a7c15u;
+  auto next = [&]() {
+    h ^= h << 13;
+    h ^= h >> 17;
+    h ^= h << 5;
+    return (h & 0x81ff81ffu) | 0x3c003c00u;
+  };
+  bf16x8 a[4], b[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const uint32_t a0 = next(), a1 = next(), a2 = next(), a3 = next();
+    const uint32_t b0 = next(), b1 = next(), b2 = next(), b3 = next();
+    a[j] = __builtin_bit_cast(bf16x8, make_uint4(a0, a1, a2, a3));
+    b[j] = __builtin_bit_cast(bf16x8, make_uint4(b0, b1, b2, b3));
+  }
+  f32x16 acc[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) acc[j][r] = 0.f;
+  for (int i = 0; i < iters; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[j], b[j], acc[j], 0, 0, 0);
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) sum += acc[j][r];
+  out[id] = sum;
+}
+
 // ---- Persistent tiles: one block per CU runs a sequence of output tiles over one continuous ring of K
 // steps, so the next tile's first operand steps load while this tile finishes (no pipeline fill and no
 // block dispatch per tile), and a launch can hold the tiles of several layers (no tail per layer).
@@ -2074,6 +2112,13 @@ extern "C" int rf_norm_q(const uint16_t* x, int64_t ldx, const float* ssq, int64
                        static_cast<const float*>(workspace), pl.splits, static_cast<int>(rs), static_cast<int>(N), ar);
   }
   return check_launch("rf_norm_q");
+}
+
+extern "C" int rf_mfma_ceiling(int blocks, int iters, float* out, hipStream_t stream) {
+  if (!out || blocks <= 0 || blocks > (1 << 20) || iters <= 0)
+    return fail(RF_EINVAL_ARG, "rf_mfma_ceiling: blocks %d, iters %d", blocks, iters);
+  hipLaunchKernelGGL(k_mfma_ceiling, dim3(blocks), dim3(256), 0, stream, iters, out);
+  return check_launch("rf_mfma_ceiling");
 }
 
 extern "C" int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t M,

@@ -58,6 +58,7 @@ SIGNATURES = {
     "rf_norm_q": [_P, _I64, _P, _I64, _I64, _F32, _P, _I32, _I32, _P, _I32, _P, _I32, _P, _P, _I64, _P, _SZ, _P],
     "rf_norm_kv_rows": [_P, _I64, _P, _I64, _I64, _F32, _P, _I32, _I32, _P, _I32, _P, _I32, _P, _P, _P, _I64, _I64,
                         _P, _SZ, _P],
+    "rf_mfma_ceiling": [_I32, _I32, _P, _P],
     "rf_map_apply_residual": [_P, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _SZ, _P],
     "rf_norm_linear_swiglu": [_P, _I64, _P, _I64, _I64, _F32, _P, _I64, _P, _I64, _P, _I64, _P, _SZ, _P],
     "rf_norm_qkv_rows": [_P, _I64, _P, _I64, _I64, _F32, _P, _I32, _I32, _I32, _P, _P, _I32, _P, _I32, _P, _P, _I64,

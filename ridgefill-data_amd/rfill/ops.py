@@ -573,6 +573,16 @@ def norm_linear_swiglu(x, ssq, eps, w, out=None, workspace=None):
     return out
 
 
+def mfma_ceiling(blocks, iters, out):
+    """rf_mfma_ceiling: blocks x 4 waves x 4 iters back-to-back bf16 MFMAs (32768 flop each) on register
+    operands; out fp32 [blocks * 256] receives one value per thread. Time it to measure the MFMA throughput
+    the power limit allows."""
+    _need(out, "out", torch.float32, 1)
+    if out.numel() < blocks * 256:
+        raise ValueError(f"mfma_ceiling: out holds {out.numel()} values, needs {blocks * 256}")
+    _lib.call("rf_mfma_ceiling", int(blocks), int(iters), _ptr(out), _stream(out))
+
+
 def silu_mul(gu, out=None):
     """SwiGLU of gu = [gate | up] [rows, 2 I]: bf16(bf16(silu(gate)) * up) [rows, I]."""
     _need(gu, "gu", torch.bfloat16, 2)
