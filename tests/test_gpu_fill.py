@@ -234,3 +234,15 @@ def test_bad_inputs_raise_before_launch(dev):
         ops.rope_kv_write(torch.zeros(4, 2, 64, dtype=torch.bfloat16, device=dev),
                           torch.zeros(4, 2, 64, dtype=torch.bfloat16, device=dev),
                           torch.zeros(4, 12, dtype=torch.bfloat16, device=dev), kb, kb.clone(), 0)
+
+
+def test_mfma_ceiling_probe_runs(dev):
+    """rf_mfma_ceiling (bench.py's power-ceiling measurement): every thread stores a finite sum; a short
+    output buffer is refused before any launch."""
+    from rfill import ops
+    out = torch.full((4 * 256,), float("nan"), device=dev)
+    ops.mfma_ceiling(4, 10, out)
+    torch.cuda.synchronize()
+    assert bool(torch.isfinite(out).all()) and bool((out != 0).any())
+    with pytest.raises(ValueError, match="needs"):
+        ops.mfma_ceiling(8, 10, out)
