@@ -24,10 +24,11 @@
 // next tile's score MFMAs run in the same instruction block as this tile's exponentials. (Waves of 64
 // query rows, one per SIMD, read half as much LDS per tile but measured 11 % slower: the second wave's
 // overlap matters more here than the LDS reads.) With few query blocks the key range is split over
-// blocks (blockIdx.z) whose partials k_causal_combine merges in a fixed order: split sp takes the W tiles
-// [ntiles - (sp + 1) W, ntiles - sp W) counted back from the block's last key tile (the first split of a
-// block may be shorter), and splits past key 0 exit at once. Every live block then has the same work
-// whatever its query block's key range, so blocks fill the CUs evenly.
+// blocks whose partials k_causal_combine merges in a fixed order: split sp takes the W key tiles
+// [sp W, (sp + 1) W) (the last split of a query block may be shorter), and splits past the block's last
+// query exit at once. The splits start at key 0 for every query block, so the query blocks of one K / V
+// head and split read the same tiles; they are placed side by side on one XCD, whose L2 then serves the
+// tiles to all of them from one read of memory.
 // The probabilities enter the second product as bf16 before normalisation (the reference casts after
 // it; the difference is within rounding), scores are fp32 products of the bf16 q and k values as the
 // reference's fp32 matmul, and the output is O / (row sum) rounded to bf16.
@@ -277,16 +278,21 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
   __shared__ uint4 lds[NSTAGE * L::STAGE_U4];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, n = lane & 31, hh = lane >> 5;
   const int rep = a.hq / a.hkv, qp = QROWS / rep;          // consecutive queries per block
-  const int hk = blockIdx.y;
-  const int j0 = blockIdx.x * qp;
+  // block -> (query block, split, K / V head), query blocks fastest: each XCD takes a contiguous run, so
+  // the query blocks of one (head, split) run side by side on one XCD and read the same key tiles
+  // through its L2
+  const int qbs = gridDim.x, ns = gridDim.z;
+  const int u = xcd_tile(blockIdx.x + qbs * (blockIdx.y + gridDim.y * blockIdx.z), qbs * gridDim.y * ns);
+  const int qb = u % qbs, sp = (u / qbs) % ns, hk = u / (qbs * ns);
+  const int j0 = qb * qp;
   const int jlast = min(j0 + qp, a.nq) - 1;
   const int64_t kmax = min(query_pos(a, jlast), a.n_keys - 1);     // the block reads keys 0 .. kmax
   const int ntiles = static_cast<int>(kmax / KT) + 1;
-  // this block's share of the key tiles: split blockIdx.z, W tiles counted back from the last
-  const int ns = gridDim.z, sp = blockIdx.z;
-  const int it1 = ntiles - sp * a.split_tiles;
-  if (it1 <= 0) return;                                   // past key 0 (block-uniform, before any barrier)
-  const int it0 = max(0, it1 - a.split_tiles);
+  // this block's share of the key tiles: split sp, tiles [sp W, (sp + 1) W) from key 0, the same key
+  // tiles for every query block
+  const int it0 = sp * a.split_tiles;
+  if (it0 >= ntiles) return;                              // past the last query (block-uniform, before any barrier)
+  const int it1 = min(ntiles, it0 + a.split_tiles);
 
   // the wave's head and queries; lanes past the last query repeat it and write nothing
   const int hg = (32 * w) / qp, po0 = (32 * w) % qp;
@@ -368,7 +374,7 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
   lane_pair(lsum, llo, lhi);
   const float ltot = llo + lhi;
   if (ns > 1) {                                           // unnormalised partials for k_causal_combine
-    float* pb = part_block<AD>(a, blockIdx.x, hk, sp);
+    float* pb = part_block<AD>(a, qb, hk, sp);
     const int r = 32 * w + n;
     float* orow = pb + r * AD + 4 * hh;
 #pragma unroll

@@ -39,13 +39,6 @@ static_assert(LDS_U4 >= IMAGE_U4 + 2048, "the epilogue's image and its 32 KiB of
 
 __device__ __forceinline__ bf16x8 as_frag(const uint4& u) { return __builtin_bit_cast(bf16x8, u); }
 
-// Logical tile of a hardware block. Blocks are dealt round-robin over the 8 XCDs (block b runs on
-// XCD b % 8); this gives every XCD a contiguous run of logical tiles.
-__device__ __forceinline__ int xcd_tile(int bid, int nb) {
-  const int q = nb >> 3, r = nb & 7, x = bid & 7, i = bid >> 3;
-  return (x < r) ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
-}
-
 // Logical tile -> (tile row, tile column). Tiles go in groups of GROUP_M tile rows walked column by
 // column, so the ~32 tiles one XCD runs at a time form a GROUP_M x 8 block: per K step its L2 sees
 // GROUP_M activation slices and 8 weight slices instead of 2 and 16.

@@ -18,6 +18,13 @@ constexpr int SSQ_COLS = 256;
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
+// Logical tile of a hardware block. Blocks are dealt round-robin over the 8 XCDs (block b runs on
+// XCD b % 8); this gives every XCD a contiguous run of logical tiles.
+__device__ __forceinline__ int xcd_tile(int bid, int nb) {
+  const int q = nb >> 3, r = nb & 7, x = bid & 7, i = bid >> 3;
+  return (x < r) ? x * (q + 1) + i : r * (q + 1) + (x - r) * q + i;
+}
+
 __device__ __forceinline__ float bf2f(uint16_t h) { return __uint_as_float(static_cast<uint32_t>(h) << 16); }
 
 // fp32 -> bf16, round to nearest even (the rounding torch's .to(torch.bfloat16) performs).
