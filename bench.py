@@ -739,7 +739,9 @@ def main():
         torch.cuda.empty_cache()
     if not args.no_fit:
         log("closed-form fit leg")
-        out["fit"] = fit_bench(dev)
+        out["fit"] = f = fit_bench(dev)
+        if "ceilings" in out:                     # the Gram against the power-limited MFMA rate of this run
+            f["gram_frac_of_mfma_power_ceiling"] = round(f["gram_tflops"] / out["ceilings"]["mfma_power_ceiling_tflops"], 4)
         torch.cuda.empty_cache()
         log("capture and lambda-selection leg")
         out["capture"] = capture_bench(dev)
