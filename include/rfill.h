@@ -53,6 +53,13 @@ int rf_map_apply(const uint16_t* b, int64_t ldb, const uint16_t* w, const uint16
  * order differs within fp32 rounding). With a smaller or NULL workspace it runs unsplit. Host only. */
 int rf_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, size_t* bytes);
 
+/* Bytes of the workspace rf_norm_kv_rows and rf_norm_qkv_rows require for `rows` scattered rows of an
+ * N-output, K-input product (N = 2 hkv d, or hq d + 2 hkv d; K = H). They run the rows in chunks of 512,
+ * each chunk planned on its own, and a shorter last chunk can take more K splits than a full one: this is
+ * the largest of the chunks' rf_gemm_workspace_bytes. Host only. The few-rows sizing of the exact rows'
+ * cache writes (code/kva/model.py:259-276 runs them as ordinary layer products). */
+int rf_rows_workspace_bytes(int64_t rows, int64_t N, int64_t K, size_t* bytes);
+
 /* Row sum-of-squares partials of given layer inputs x [P, H] -> ssq [P, H / 256], the statistics the
  * fused input RMSNorm of rf_norm_kv_write reads (the mean of x^2 in code/kva/ops.py:14-25).
  * Bitwise the partials rf_map_apply writes for the same x. */
@@ -151,27 +158,30 @@ int rf_rope_kv_write(const uint16_t* k, int64_t ld_k, const uint16_t* v, int64_t
  * pos[j] of cs exactly as rf_norm_kv_write does it, and written to cache slot pos[j]. The exact rows of a
  * filled layer (code/kva/kva.py:392-454 scatters the rows' inputs into the layer's fill): once the layer
  * is filled from every prefix row, this overwrites the rows' slots with the K / V of their exact inputs.
- * Arguments and limits as rf_norm_kv_write; every pos[j] must lie in [0, cap) of the cache and in the
- * table. The rows run through the few-rows partials (M <= 512 per launch) and the reduce epilogue: a
- * workspace of rf_gemm_workspace_bytes(min(rows, 512), 2 hkv d, H) bytes is required. */
+ * Arguments and limits as rf_norm_kv_write. pos_limit (> 0): the smaller of the cache's capacity and the
+ * table's rows; a row whose pos[j] lies outside [0, pos_limit) is skipped on the device (no table read, no
+ * cache write), since the positions live on the device and are not read back. The rows run through the
+ * few-rows partials (M <= 512 per launch) and the reduce epilogue: a workspace of
+ * rf_rows_workspace_bytes(rows, 2 hkv d, H) bytes is required. */
 int rf_norm_kv_rows(const uint16_t* x, int64_t ldx, const float* ssq, int64_t rows, int64_t H, float eps,
                     const uint16_t* wkv, int hkv, int d, const uint16_t* knorm, int knorm_kind, const uint16_t* cs,
-                    int rot, const int64_t* pos, uint16_t* kbuf, uint16_t* vbuf, int64_t head_stride,
-                    int64_t row_stride, void* workspace, size_t ws_bytes, hipStream_t stream);
+                    int rot, const int64_t* pos, int64_t pos_limit, uint16_t* kbuf, uint16_t* vbuf,
+                    int64_t head_stride, int64_t row_stride, void* workspace, size_t ws_bytes, hipStream_t stream);
 
 /* The queries and the K / V of scattered rows in one product: wqkv [hq d + 2 hkv d, H] holds the query
  * projection's rows then the K and V projections' (each with the input norm gain folded in). Row j of
  * x [rows, H] (statistics ssq) at position pos[j]: its queries, with qnorm (or none) and RoPE table row
  * pos[j], to q row j (row stride ldq), as rf_norm_q writes them; its K / V, with knorm, to cache slot pos[j],
  * as rf_norm_kv_rows writes them (norm_kind is the kind of both norms). One few-rows product per 512 rows,
- * then the two epilogues over its column ranges. Limits as rf_norm_q and rf_norm_kv_rows; a workspace of
- * rf_gemm_workspace_bytes(min(rows, 512), hq d + 2 hkv d, H) bytes is required. The exact rows' layer input
- * side (code/kva/model.py:234-245, :340-352 on the rows of a filled layer). */
+ * then the two epilogues over its column ranges. Limits and pos_limit as rf_norm_kv_rows (a row skipped for
+ * its position leaves its q row unwritten too); a workspace of rf_rows_workspace_bytes(rows, hq d + 2 hkv d,
+ * H) bytes is required. The exact rows' layer input side (code/kva/model.py:234-245, :340-352 on the rows of
+ * a filled layer). */
 int rf_norm_qkv_rows(const uint16_t* x, int64_t ldx, const float* ssq, int64_t rows, int64_t H, float eps,
                      const uint16_t* wqkv, int hq, int hkv, int d, const uint16_t* qnorm, const uint16_t* knorm,
-                     int norm_kind, const uint16_t* cs, int rot, const int64_t* pos, uint16_t* q, int64_t ldq,
-                     uint16_t* kbuf, uint16_t* vbuf, int64_t head_stride, int64_t row_stride, void* workspace,
-                     size_t ws_bytes, hipStream_t stream);
+                     int norm_kind, const uint16_t* cs, int rot, const int64_t* pos, int64_t pos_limit, uint16_t* q,
+                     int64_t ldq, uint16_t* kbuf, uint16_t* vbuf, int64_t head_stride, int64_t row_stride,
+                     void* workspace, size_t ws_bytes, hipStream_t stream);
 
 /* out[j] = x[rows[j]] for j < nrows, bit-exact, and out's row sum-of-squares partials ssq [nrows, H / 256]
  * (the rows' input RMSNorm statistics). The gather of h[rows] in layer_rows (code/kva/model.py:270); a row

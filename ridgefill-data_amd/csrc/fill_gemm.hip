@@ -536,6 +536,7 @@ struct KvArgs {
   int64_t head_stride, row_stride, slot0;
   const int64_t* pos;   // RoPE table row of input row j: pos[j] (null: j)
   const int64_t* slot = nullptr;   // cache slot of input row j: slot[j] (null: slot0 + j; reduce epilogue only)
+  int64_t pos_lim = 0;             // > 0: rows with pos[j] outside [0, pos_lim) are skipped (reduce epilogue only)
 };
 
 // k_norm of one chunk's 8 values given the head's inverse RMS (code/kva/ops.py:14-25 per head), with
@@ -958,7 +959,12 @@ __global__ __launch_bounds__(256) void k_norm_kv_reduce(const float* __restrict_
   img[r * 32 + (ch ^ r)] = o;
   __syncthreads();
   const KvLane L(a, n0, ch);
-  kv_chunk_row(a, L, [&](int c) { return image_chunk(img, r, c); }, ch, m, m < M, rope_fetch(a, L, m, m < M));
+  bool ok = m < M;
+  if (ok && a.pos_lim > 0) {                        // positions checked on the device: no table read or write
+    const int64_t p = a.pos[m];                     // outside the table and the cache
+    ok = p >= 0 && p < a.pos_lim;
+  }
+  kv_chunk_row(a, L, [&](int c) { return image_chunk(img, r, c); }, ch, m, ok, rope_fetch(a, L, m, ok));
 }
 
 // Adds a run's fp32 sums (acc) into the fp64 accumulator C for the tile at (m0, n0), rows < M. The sums go
@@ -1768,6 +1774,16 @@ size_t split_bytes(int64_t M, int64_t N, int64_t K) {
   return p.split() ? static_cast<size_t>(p.splits) * (M - p.m_fused) * N * 4 : 0;
 }
 
+// Workspace of a product over `rows` scattered rows run in chunks of ROWS_MAX rows, each chunk planned on
+// its own: the largest of a full chunk's and the last (shorter) chunk's split bytes. A shorter chunk can
+// need more than a full one, since fewer row blocks leave room for more K splits.
+size_t rows_split_bytes(int64_t rows, int64_t N, int64_t K) {
+  size_t b = 0;
+  if (rows >= ROWS_MAX) b = split_bytes(ROWS_MAX, N, K);
+  if (rows % ROWS_MAX) b = std::max(b, split_bytes(rows % ROWS_MAX, N, K));
+  return b;
+}
+
 // The plan an entry point follows with this workspace: the split part only if the workspace holds it.
 Plan plan_with(int64_t M, int64_t N, int64_t K, const void* ws, size_t ws_bytes) {
   const Plan p = plan(M, N, K);
@@ -1812,6 +1828,14 @@ extern "C" int rf_gemm_workspace_bytes(int64_t M, int64_t N, int64_t K, size_t* 
     return fail(RF_EINVAL_ARG, "rf_gemm_workspace_bytes: M %lld, N %lld (multiple of 256), K %lld (multiple of 64)",
                 (long long)M, (long long)N, (long long)K);
   *bytes = M ? split_bytes(M, N, K) : 0;
+  return RF_OK;
+}
+
+extern "C" int rf_rows_workspace_bytes(int64_t rows, int64_t N, int64_t K, size_t* bytes) {
+  if (!bytes || rows < 0 || N <= 0 || N % BN || K <= 0 || K % BK)
+    return fail(RF_EINVAL_ARG, "rf_rows_workspace_bytes: rows %lld, N %lld (multiple of 256), K %lld (multiple of 64)",
+                (long long)rows, (long long)N, (long long)K);
+  *bytes = rows_split_bytes(rows, N, K);
   return RF_OK;
 }
 
@@ -1969,9 +1993,9 @@ extern "C" int rf_norm_kv_write(const uint16_t* x, int64_t ldx, const float* ssq
 
 extern "C" int rf_norm_kv_rows(const uint16_t* x, int64_t ldx, const float* ssq, int64_t rows, int64_t H,
                                float eps, const uint16_t* wkv, int hkv, int d, const uint16_t* knorm, int knorm_kind,
-                               const uint16_t* cs, int rot, const int64_t* pos, uint16_t* kbuf, uint16_t* vbuf,
-                               int64_t head_stride, int64_t row_stride, void* workspace, size_t ws_bytes,
-                               hipStream_t stream) {
+                               const uint16_t* cs, int rot, const int64_t* pos, int64_t pos_limit, uint16_t* kbuf,
+                               uint16_t* vbuf, int64_t head_stride, int64_t row_stride, void* workspace,
+                               size_t ws_bytes, hipStream_t stream) {
   const char* fn = "rf_norm_kv_rows";
   if (!x || !ssq || !wkv || !cs || !pos || !kbuf || !vbuf || !workspace)
     return fail(RF_EINVAL_ARG, "%s: null pointer", fn);
@@ -1994,16 +2018,18 @@ extern "C" int rf_norm_kv_rows(const uint16_t* x, int64_t ldx, const float* ssq,
   const int64_t N = 2ll * hkv * d;
   // chunks of at most ROWS_MAX rows, each through the few-rows partials and the reduce epilogue (the only
   // epilogue that writes to per-row slots)
-  const int64_t chunk = std::min<int64_t>(rows, ROWS_MAX);
-  if (rows > 0 && ws_bytes < split_bytes(chunk, N, H))
-    return fail(RF_EINVAL_ARG, "%s: workspace %zu bytes, needs %zu (rf_gemm_workspace_bytes of min(rows, 512) x %lld x %lld)",
-                fn, ws_bytes, split_bytes(chunk, N, H), (long long)N, (long long)H);
+  if (pos_limit <= 0) return fail(RF_EINVAL_ARG, "%s: pos_limit %lld", fn, (long long)pos_limit);
+  const size_t need = rows_split_bytes(rows, N, H);
+  if (ws_bytes < need)
+    return fail(RF_EINVAL_ARG, "%s: workspace %zu bytes, needs %zu (rf_rows_workspace_bytes of %lld x %lld x %lld)",
+                fn, ws_bytes, need, (long long)rows, (long long)N, (long long)H);
   for (int64_t r0 = 0; r0 < rows; r0 += ROWS_MAX) {
     const int64_t m = std::min<int64_t>(ROWS_MAX, rows - r0);
     const Plan pl = plan(m, N, H);
     KvArgs a{ssq + r0 * (H / SSQ_COLS), static_cast<int>(H / SSQ_COLS), static_cast<float>(H), eps, hkv, d, knorm,
              knorm_kind, cs, rot, kbuf, vbuf, head_stride, row_stride, 0, pos + r0};
     a.slot = pos + r0;
+    a.pos_lim = pos_limit;
     launch_partials(x + r0 * ldx, ldx, wkv, H, m, N, H, pl, workspace, stream);
     hipLaunchKernelGGL(k_norm_kv_reduce, reduce_grid(m, N), dim3(256), 0, stream, static_cast<const float*>(workspace),
                        pl.splits, static_cast<int>(m), static_cast<int>(N), a);
@@ -2014,8 +2040,9 @@ extern "C" int rf_norm_kv_rows(const uint16_t* x, int64_t ldx, const float* ssq,
 extern "C" int rf_norm_qkv_rows(const uint16_t* x, int64_t ldx, const float* ssq, int64_t rows, int64_t H,
                                 float eps, const uint16_t* wqkv, int hq, int hkv, int d, const uint16_t* qnorm,
                                 const uint16_t* knorm, int norm_kind, const uint16_t* cs, int rot, const int64_t* pos,
-                                uint16_t* q, int64_t ldq, uint16_t* kbuf, uint16_t* vbuf, int64_t head_stride,
-                                int64_t row_stride, void* workspace, size_t ws_bytes, hipStream_t stream) {
+                                int64_t pos_limit, uint16_t* q, int64_t ldq, uint16_t* kbuf, uint16_t* vbuf,
+                                int64_t head_stride, int64_t row_stride, void* workspace, size_t ws_bytes,
+                                hipStream_t stream) {
   const char* fn = "rf_norm_qkv_rows";
   if (!x || !ssq || !wqkv || !cs || !pos || !q || !kbuf || !vbuf || !workspace)
     return fail(RF_EINVAL_ARG, "%s: null pointer", fn);
@@ -2038,10 +2065,11 @@ extern "C" int rf_norm_qkv_rows(const uint16_t* x, int64_t ldx, const float* ssq
     return fail(RF_EINVAL_SHAPE, "%s: pointers must be 16-byte aligned", fn);
   if (!(eps >= 0.f)) return fail(RF_EINVAL_ARG, "%s: eps %g", fn, static_cast<double>(eps));
   const int64_t NQ = static_cast<int64_t>(hq) * d, NKV = 2ll * hkv * d, N = NQ + NKV;
-  const int64_t chunk = std::min<int64_t>(rows, ROWS_MAX);
-  if (rows > 0 && ws_bytes < split_bytes(chunk, N, H))
-    return fail(RF_EINVAL_ARG, "%s: workspace %zu bytes, needs %zu (rf_gemm_workspace_bytes of min(rows, 512) x %lld x "
-                "%lld)", fn, ws_bytes, split_bytes(chunk, N, H), (long long)N, (long long)H);
+  if (pos_limit <= 0) return fail(RF_EINVAL_ARG, "%s: pos_limit %lld", fn, (long long)pos_limit);
+  const size_t need = rows_split_bytes(rows, N, H);
+  if (ws_bytes < need)
+    return fail(RF_EINVAL_ARG, "%s: workspace %zu bytes, needs %zu (rf_rows_workspace_bytes of %lld x %lld x %lld)",
+                fn, ws_bytes, need, (long long)rows, (long long)N, (long long)H);
   const float* part = static_cast<const float*>(workspace);
   for (int64_t r0 = 0; r0 < rows; r0 += ROWS_MAX) {
     const int64_t m = std::min<int64_t>(ROWS_MAX, rows - r0);
@@ -2050,8 +2078,9 @@ extern "C" int rf_norm_qkv_rows(const uint16_t* x, int64_t ldx, const float* ssq
     const int nparts = static_cast<int>(H / SSQ_COLS);
     const float* s0 = ssq + r0 * nparts;
     // the query columns [0, NQ): every column a "K" column of hq heads, row j to q row r0 + j
-    const KvArgs aq{s0, nparts, static_cast<float>(H), eps, hq, d, qnorm, norm_kind, cs, rot, q + r0 * ldq,
-                    q + r0 * ldq, static_cast<int64_t>(d), ldq, 0, pos + r0};
+    KvArgs aq{s0, nparts, static_cast<float>(H), eps, hq, d, qnorm, norm_kind, cs, rot, q + r0 * ldq,
+              q + r0 * ldq, static_cast<int64_t>(d), ldq, 0, pos + r0};
+    aq.pos_lim = pos_limit;
     const dim3 gq = reduce_grid(m, NQ), gkv = reduce_grid(m, NKV);
     hipLaunchKernelGGL(k_norm_kv_reduce, gq, dim3(256), 0, stream, part, pl.splits, static_cast<int>(m),
                        static_cast<int>(N), aq);
@@ -2059,6 +2088,7 @@ extern "C" int rf_norm_qkv_rows(const uint16_t* x, int64_t ldx, const float* ssq
     KvArgs akv{s0, nparts, static_cast<float>(H), eps, hkv, d, knorm, norm_kind, cs, rot, kbuf, vbuf, head_stride,
                row_stride, 0, pos + r0};
     akv.slot = pos + r0;
+    akv.pos_lim = pos_limit;
     hipLaunchKernelGGL(k_norm_kv_reduce, gkv, dim3(256), 0, stream, part + NQ, pl.splits, static_cast<int>(m),
                        static_cast<int>(N), akv);
   }

@@ -32,6 +32,7 @@ _PI64 = ctypes.POINTER(ctypes.c_int64)      # a host array of counts
 SIGNATURES = {
     "rf_map_apply": [_P, _I64, _P, _P, _P, _I64, _P, _I64, _I64, _I64, _P, _SZ, _P],
     "rf_gemm_workspace_bytes": [_I64, _I64, _I64, _PSZ],
+    "rf_rows_workspace_bytes": [_I64, _I64, _I64, _PSZ],
     "rf_map_apply_batch": [_I32, _P, _I64, _PP, _PP, _PP, _I64, _PP, _I64, _I64, _I64, _P],
     "rf_norm_kv_write_batch": [_I32, _PP, _I64, _PP, _I64, _I64, _F32, _PP, _I32, _I32, _PP, _I32, _P, _I32,
                                _PP, _PP, _I64, _I64, _I64, _I64, _P],
@@ -56,13 +57,13 @@ SIGNATURES = {
     "rf_ridge_solve_workspace_bytes": [_I64, _I32, _PSZ],
     "rf_row_gather": [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _P],
     "rf_norm_q": [_P, _I64, _P, _I64, _I64, _F32, _P, _I32, _I32, _P, _I32, _P, _I32, _P, _P, _I64, _P, _SZ, _P],
-    "rf_norm_kv_rows": [_P, _I64, _P, _I64, _I64, _F32, _P, _I32, _I32, _P, _I32, _P, _I32, _P, _P, _P, _I64, _I64,
-                        _P, _SZ, _P],
+    "rf_norm_kv_rows": [_P, _I64, _P, _I64, _I64, _F32, _P, _I32, _I32, _P, _I32, _P, _I32, _P, _I64, _P, _P, _I64,
+                        _I64, _P, _SZ, _P],
     "rf_mfma_ceiling": [_I32, _I32, _P, _P],
     "rf_map_apply_residual": [_P, _I64, _P, _P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _SZ, _P],
     "rf_norm_linear_swiglu": [_P, _I64, _P, _I64, _I64, _F32, _P, _I64, _P, _I64, _P, _I64, _P, _SZ, _P],
-    "rf_norm_qkv_rows": [_P, _I64, _P, _I64, _I64, _F32, _P, _I32, _I32, _I32, _P, _P, _I32, _P, _I32, _P, _P, _I64,
-                         _P, _P, _I64, _I64, _P, _SZ, _P],
+    "rf_norm_qkv_rows": [_P, _I64, _P, _I64, _I64, _F32, _P, _I32, _I32, _I32, _P, _P, _I32, _P, _I32, _P, _I64, _P,
+                         _I64, _P, _P, _I64, _I64, _P, _SZ, _P],
     "rf_attend_rows": [_P, _I64, _P, _I64, _I32, _I32, _P, _P, _I32, _I64, _I64, _I64, _F32, _P, _I64, _P, _SZ, _P],
     "rf_attend_rows_workspace_bytes": [_I64, _I32, _I32, _I32, _I64, _PSZ],
     "rf_attend_causal": [_P, _I64, _I64, _P, _I64, _I32, _I32, _P, _P, _I32, _I64, _I64, _I64, _F32, _P, _I64, _P,

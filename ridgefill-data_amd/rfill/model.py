@@ -300,11 +300,12 @@ class FillModel:
             self._attn_ws = ws = torch.empty(need, dtype=torch.uint8, device=device)
         return ws
 
-    def gemm_workspace(self, M, N, K, device, role="consume"):
+    def gemm_workspace(self, M, N, K, device, role="consume", rows=False):
         """The split-K workspace of an M x N x K product (None when it runs unsplit): one buffer per role,
         shared by every GEMM of that role in stream order -- "consume" for the cache fill and the exact
-        rows' and tail's layers, "produce" for the map apply that may run beside them on another stream."""
-        need = ops.gemm_workspace_bytes(M, N, K)
+        rows' and tail's layers, "produce" for the map apply that may run beside them on another stream.
+        rows: size it for norm_kv_rows / norm_qkv_rows over M scattered rows (ops.rows_workspace_bytes)."""
+        need = (ops.rows_workspace_bytes if rows else ops.gemm_workspace_bytes)(M, N, K)
         if need == 0:
             return None
         wss = self.__dict__.setdefault("_gemm_ws", {})
@@ -454,18 +455,18 @@ class FillModel:
             wl = self._layer(i)
             ops.norm_kv_rows(h, ssq, self.eps, wl["wkv"], self.n_kv, self.head_dim, wl.get("k_norm"),
                              self.knorm_kind, cs, rows, c["kbuf"], c["vbuf"], pos_max=rows_max,
-                             workspace=self.gemm_workspace(min(R, 512), wl["wkv"].shape[0], H, h.device))
+                             workspace=self.gemm_workspace(R, wl["wkv"].shape[0], H, h.device, rows=True))
             return None
         w = self._pack_rows(i)
         if "wqkv" in w:                                 # queries and the rows' K / V from one product
             q = ops.norm_qkv_rows(h, ssq, self.eps, w["wqkv"], self.n_heads, self.n_kv, self.head_dim,
                                   w.get("q_norm"), w.get("k_norm"), self.knorm_kind, cs, rows, c["kbuf"], c["vbuf"],
                                   pos_max=rows_max,
-                                  workspace=self.gemm_workspace(min(R, 512), w["wqkv"].shape[0], H, h.device))
+                                  workspace=self.gemm_workspace(R, w["wqkv"].shape[0], H, h.device, rows=True))
         else:
             ops.norm_kv_rows(h, ssq, self.eps, w["wkv"], self.n_kv, self.head_dim, w.get("k_norm"), self.knorm_kind,
                              cs, rows, c["kbuf"], c["vbuf"], pos_max=rows_max,
-                             workspace=self.gemm_workspace(min(R, 512), w["wkv"].shape[0], H, h.device))
+                             workspace=self.gemm_workspace(R, w["wkv"].shape[0], H, h.device, rows=True))
             q = ops.norm_q(h, ssq, self.eps, w["wq"], self.n_heads, self.head_dim, w.get("q_norm"), self.knorm_kind,
                            cs, rows, workspace=self.gemm_workspace(R, w["wq"].shape[0], H, h.device))
         qpos = pos[rows] if qpos is None else qpos

@@ -49,13 +49,22 @@ def gemm_workspace_bytes(M, N, K):
     return b.value
 
 
-def _ws(workspace, M, N, K, device):
+def rows_workspace_bytes(rows, N, K):
+    """Bytes of the workspace norm_kv_rows / norm_qkv_rows require for `rows` scattered rows of an N x K
+    product: they run 512 rows at a time, and a shorter last chunk may split K more ways than a full one."""
+    b = ctypes.c_size_t(0)
+    _lib.call("rf_rows_workspace_bytes", rows, N, K, ctypes.byref(b))
+    return b.value
+
+
+def _ws(workspace, M, N, K, device, need_of=None):
     """(pointer, bytes) of a GEMM's split-K workspace: None -> no split; "auto" -> allocated here when a
-    split pays; a uint8 device tensor -> used if large enough."""
+    split pays; a uint8 device tensor -> used if large enough. need_of: the size function (default
+    gemm_workspace_bytes)."""
     if workspace is None:
         return None, 0
     if isinstance(workspace, str):
-        need = gemm_workspace_bytes(M, N, K)
+        need = (need_of or gemm_workspace_bytes)(M, N, K)
         if not need:
             return None, 0
         workspace = torch.empty(need, dtype=torch.uint8, device=device)
@@ -288,7 +297,9 @@ def norm_kv_rows(x, ssq, eps, wkv, hkv, d, knorm, knorm_kind, cs, pos, kbuf, vbu
     """K / V of scattered rows x [rows, H] at positions pos (int64, device) into cache slots pos: the
     arithmetic of norm_kv_write, each row written to its own position's slot (the exact rows of a layer
     already filled from every prefix row). pos_max: a bound on pos known on the host (else read from the
-    device, which waits for it); it must lie below the cache capacity and the table's rows."""
+    device, which waits for it); it must lie below the cache capacity and the table's rows. With pos_max
+    given, the positions are not read back: the kernel skips any row whose position lies outside the cache
+    or the table. workspace: "auto", or a uint8 tensor of at least rows_workspace_bytes bytes."""
     _need(x, "x", torch.bfloat16, 2)
     _need(ssq, "ssq", torch.float32, 2)
     _need(wkv, "wkv", torch.bfloat16, 2)
@@ -308,14 +319,15 @@ def norm_kv_rows(x, ssq, eps, wkv, hkv, d, knorm, knorm_kind, cs, pos, kbuf, vbu
     hs, rs, cap = _cache_args(kbuf, vbuf, hkv, d, 0, rows)
     if rows == 0:
         return
+    lim = min(cap, cs.shape[0])
     hi = int(pos.max().item()) if pos_max is None else int(pos_max)
     if pos_max is None and int(pos.min().item()) < 0:
         raise ValueError("norm_kv_rows: negative position")
-    if hi >= min(cap, cs.shape[0]):
+    if hi >= lim:
         raise ValueError(f"norm_kv_rows: position {hi} beyond the cache ({cap} slots) or the table ({cs.shape[0]} rows)")
-    ws, nb = _ws(workspace, min(rows, 512), 2 * hkv * d, H, x.device)
+    ws, nb = _ws(workspace, rows, 2 * hkv * d, H, x.device, rows_workspace_bytes)
     _lib.call("rf_norm_kv_rows", _ptr(x), x.stride(0), _ptr(ssq), rows, H, float(eps), _ptr(wkv), hkv, d,
-              _ptr(knorm), int(knorm_kind), _ptr(cs), cs.shape[1], _ptr(pos), _ptr(kbuf), _ptr(vbuf), hs, rs,
+              _ptr(knorm), int(knorm_kind), _ptr(cs), cs.shape[1], _ptr(pos), lim, _ptr(kbuf), _ptr(vbuf), hs, rs,
               _ptr(ws), nb, _stream(x))
 
 
@@ -347,15 +359,16 @@ def norm_qkv_rows(x, ssq, eps, wqkv, hq, hkv, d, qnorm, knorm, norm_kind, cs, po
         raise ValueError("norm_qkv_rows: out shape")
     if rows == 0:
         return out
+    lim = min(cap, cs.shape[0])
     hi = int(pos.max().item()) if pos_max is None else int(pos_max)
     if pos_max is None and int(pos.min().item()) < 0:
         raise ValueError("norm_qkv_rows: negative position")
-    if hi >= min(cap, cs.shape[0]):
+    if hi >= lim:
         raise ValueError(f"norm_qkv_rows: position {hi} beyond the cache ({cap} slots) or the table ({cs.shape[0]} rows)")
-    ws, nb = _ws(workspace, min(rows, 512), (hq + 2 * hkv) * d, H, x.device)
+    ws, nb = _ws(workspace, rows, (hq + 2 * hkv) * d, H, x.device, rows_workspace_bytes)
     _lib.call("rf_norm_qkv_rows", _ptr(x), x.stride(0), _ptr(ssq), rows, H, float(eps), _ptr(wqkv), hq, hkv, d,
-              _ptr(qnorm), _ptr(knorm), int(norm_kind), _ptr(cs), cs.shape[1], _ptr(pos), _ptr(out), out.stride(0),
-              _ptr(kbuf), _ptr(vbuf), hs, rs, _ptr(ws), nb, _stream(x))
+              _ptr(qnorm), _ptr(knorm), int(norm_kind), _ptr(cs), cs.shape[1], _ptr(pos), lim, _ptr(out),
+              out.stride(0), _ptr(kbuf), _ptr(vbuf), hs, rs, _ptr(ws), nb, _stream(x))
     return out
 
 

@@ -296,6 +296,8 @@ class RidgeStats:
             if i not in self.cen_y:                 # no rows of this layer yet: zero sums, no shift (ridge.py:73)
                 sy[i] = self.s1y[i].clone()
                 sxy[i] = torch.zeros(d, o, dtype=torch.float64, device=self.device)
+                if self.base is not None:           # resumed: zero sums about the saved shift, so combine()
+                    cy[i] = self.base["cy"][i]      # carries the saved sums of this layer unchanged
                 continue
             c = self.cen_y[i]
             cy[i] = c.c

@@ -64,3 +64,26 @@ def test_gemm_workspace_sizes():
     assert ops.gemm_workspace_bytes(0, 4096, 4096) == 0
     with pytest.raises(ValueError):
         ops.gemm_workspace_bytes(10, 100, 4096)                     # N not a multiple of 256
+
+
+def test_rows_workspace_sizes():
+    """Host-only size rule of the scattered rows' K / V products (rf_norm_kv_rows, rf_norm_qkv_rows): they
+    run 512 rows at a time, each chunk planned alone, so the workspace is the largest chunk's. At Qwen3-8B
+    widths ([wq; wkv]: N 6144, K 4096) a full chunk takes 4 row blocks x 24 column blocks, K split 2 ways;
+    655 rows leave a last chunk of 143 rows in one row block, split min(256 / 24, K / 512) = 8 ways, which
+    needs more than the full chunk."""
+    from rfill import ops
+    full = 2 * 512 * 6144 * 4
+    assert ops.rows_workspace_bytes(512, 6144, 4096) == full
+    assert ops.rows_workspace_bytes(655, 6144, 4096) == 8 * 143 * 6144 * 4 > full
+    assert ops.rows_workspace_bytes(1024, 6144, 4096) == full
+    assert ops.rows_workspace_bytes(287, 2048, 4096) == 8 * 287 * 2048 * 4      # one chunk: as the GEMM's
+    assert ops.rows_workspace_bytes(0, 2048, 4096) == 0
+    # every chunk of every row count fits, at the widths the exact rows use
+    for n, k in ((6144, 4096), (2048, 4096), (4608, 2048), (1024, 1024)):
+        for rows in range(1, 2100, 7):
+            need = ops.rows_workspace_bytes(rows, n, k)
+            chunks = [512] * (rows // 512) + ([rows % 512] if rows % 512 else [])
+            assert need == max(ops.gemm_workspace_bytes(m, n, k) for m in chunks), (n, k, rows)
+    with pytest.raises(ValueError):
+        ops.rows_workspace_bytes(10, 100, 4096)

@@ -107,6 +107,27 @@ def test_resume_from_a_saved_state():
     _check(mine, ref)
 
 
+def test_resume_adding_a_subset_of_layers():
+    """A resumed state whose new rows add only some layers: state() carries the saved sums of the other layers
+    unchanged (their cy, sy, sxy), and the added layer matches the oracle over all rows."""
+    x, ys = _data(seed=4)
+    ys[9] = (x.float() * 0.5 + 0.25).to(torch.bfloat16)
+    ref = oridge.RidgeStats(3, [7], 16)
+    ref.add(x, {7: ys[7]}, block=1024)
+    ref = ref.state()
+    first = ridge.RidgeStats(3, [7, 9], 16, device="cpu")
+    _emulate(first, x[:1200], {i: ys[i][:1200] for i in (7, 9)}, 1024)
+    saved = first.state()
+    resumed = ridge.RidgeStats.from_state(saved, device="cpu")
+    resumed.layers = [7]                                # the new rows carry layer 7 only
+    _emulate(resumed, x[1200:], {7: ys[7][1200:]}, 1024)
+    resumed.layers = [7, 9]
+    mine = resumed.state()
+    _check(mine, ref)
+    for k in ("cy", "sy", "sxy"):
+        assert torch.equal(mine[k][9], saved[k][9]), k
+
+
 def test_residual_and_combine_agree_with_the_oracle():
     x, ys = _data(seed=2)
     a, b = oridge.RidgeStats(3, [7], 16), oridge.RidgeStats(3, [7], 16)

@@ -362,6 +362,65 @@ def test_norm_qkv_rows_matches_the_separate_products(dev, R, norms):
     assert not kb[:, rest].any() and not vb[:, rest].any()
 
 
+def test_rows_workspace_covers_a_short_last_chunk(dev):
+    """655 rows of a Qwen3-8B-width [wq; wkv] product (H 4096, 32 query / 8 KV heads: N 6144): the last
+    chunk of 143 rows splits K 8 ways (28.1 MB of partials) against 2 ways for the first 512 rows (25.2 MB).
+    With the workspace rf_rows_workspace_bytes gives, a guard region right after it stays untouched and the
+    results match the separate products; a workspace sized for the first chunk only is refused."""
+    from rfill import ops
+    H, hq, hkv, d, P, R = 4096, 32, 8, 128, 4000, 655
+    g = torch.Generator().manual_seed(655)
+    rows = torch.randperm(P, generator=g)[:R].sort().values.to(dev)
+    x = torch.randn(R, H, generator=g).to(torch.bfloat16).to(dev)
+    ssq = ops.row_ssq(x)
+    wqkv = (torch.randn((hq + 2 * hkv) * d, H, generator=g) / H ** 0.5).to(torch.bfloat16).to(dev)
+    kn = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(dev)
+    inv = 1.0 / (1e6 ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    cs = ops.rope_table(torch.arange(P, device=dev), inv.to(dev))
+    need = ops.rows_workspace_bytes(R, (hq + 2 * hkv) * d, H)
+    assert need == 8 * 143 * 6144 * 4
+    guard = 1 << 20
+    buf = torch.full((need + guard,), 0xA5, dtype=torch.uint8, device=dev)
+    kb, vb, kb2, vb2 = (torch.zeros(hkv, P, d, dtype=torch.bfloat16, device=dev) for _ in range(4))
+    q = ops.norm_qkv_rows(x, ssq, 1e-6, wqkv, hq, hkv, d, None, kn, 0, cs, rows, kb, vb, workspace=buf[:need])
+    q2 = ops.norm_q(x, ssq, 1e-6, wqkv[:hq * d].contiguous(), hq, d, None, 0, cs, rows, workspace="auto")
+    ops.norm_kv_rows(x, ssq, 1e-6, wqkv[hq * d:].contiguous(), hkv, d, kn, 0, cs, rows, kb2, vb2)
+    torch.cuda.synchronize()
+    assert bool((buf[need:] == 0xA5).all()), "write past the workspace"
+    for got, want in ((q, q2), (kb[:, rows], kb2[:, rows]), (vb[:, rows], vb2[:, rows])):
+        assert rel_err(got, want) < 5e-3
+    short = ops.gemm_workspace_bytes(512, (hq + 2 * hkv) * d, H)
+    assert short < need
+    with pytest.raises(ValueError, match="workspace"):
+        ops.norm_qkv_rows(x, ssq, 1e-6, wqkv, hq, hkv, d, None, kn, 0, cs, rows, kb, vb, workspace=buf[:short])
+
+
+def test_rows_positions_outside_the_cache_are_skipped(dev):
+    """With pos_max given the positions are not read back; rows whose position lies outside the cache view
+    or the table (here 120 and -3 for a 100-slot view) are skipped on the device. The view sits inside a
+    larger buffer, so a write past either end of it would show; the kept rows are bit-identical to a call
+    over the kept rows alone."""
+    from rfill import ops
+    H, hkv, d = 1024, 2, 128
+    g = torch.Generator().manual_seed(3)
+    pos = torch.tensor([5, 50, 120, -3, 99], dtype=torch.int64, device=dev)
+    keep = torch.tensor([0, 1, 4], device=dev)
+    x = torch.randn(5, H, generator=g).to(torch.bfloat16).to(dev)
+    ssq = ops.row_ssq(x)
+    wkv = (torch.randn(2 * hkv * d, H, generator=g) / H ** 0.5).to(torch.bfloat16).to(dev)
+    inv = 1.0 / (1e6 ** (torch.arange(0, d, 2, dtype=torch.float32) / d))
+    cs_all = ops.rope_table(torch.arange(300, device=dev), inv.to(dev))
+    cs = cs_all[100:200]
+    kb_all, vb_all, kb2, vb2 = (torch.zeros(hkv, 300, d, dtype=torch.bfloat16, device=dev) for _ in range(4))
+    ops.norm_kv_rows(x, ssq, 1e-6, wkv, hkv, d, None, 0, cs, pos, kb_all[:, 100:200], vb_all[:, 100:200], pos_max=99)
+    ops.norm_kv_rows(x[keep].contiguous(), ssq[keep].contiguous(), 1e-6, wkv, hkv, d, None, 0, cs, pos[keep],
+                     kb2[:, 100:200], vb2[:, 100:200], pos_max=99)
+    torch.cuda.synchronize()
+    assert torch.equal(kb_all, kb2) and torch.equal(vb_all, vb2)
+    written = kb_all.abs().sum(dim=(0, 2)).nonzero().flatten().tolist()
+    assert written == [105, 150, 199]
+
+
 @pytest.mark.parametrize("R", [287, 1300])
 def test_fused_residual_and_swiglu_epilogues_are_bit_identical(dev, R):
     """map_apply_residual == map_apply + residual_add and norm_linear_swiglu == norm_linear + silu_mul, bit
