@@ -406,16 +406,20 @@ int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t* b, int64_
                        int64_t K, int64_t fold_rows, double* c, int64_t ldc, hipStream_t stream);
 
 /* Held-out read cosine of one late layer for one document (code/scripts/fit_sweep.py:307-313): pred and
- * truth are [rows, 2 hkv d] bf16 reads, K heads in columns 0 .. hkv d - 1 and V heads after them (the
- * pre-RoPE K / V of code/kva/model.py:282-287, one norm_linear of the [W_k; W_v] projection). Per row
- * and head, cos = a . b / (max(|a|, 1e-8) max(|b|, 1e-8)) in fp32 (F.cosine_similarity over head_dim);
- * K heads are first scaled elementwise by the k_norm gain kgain [d] bf16 (gain_kind 1: 1 + gain; NULL:
- * no k norm), which is the cosine of the k-normed reads (code/kva/model.py:353-359) since the per-head
- * RMS factor cancels. out[0] += weight * (sum of K cosines), out[1] += weight * (sum of V cosines), in
- * fp64 and a fixed order (weight = 1 / (rows hkv) gives the document's means). workspace: at least
- * 8 * ceil(rows / 16) bytes. d = 64, 128 or 256; ld_pred / ld_true multiples of 8. */
+ * truth are [rows, >= (na + nb) d] bf16 reads, each row na vectors of group a then nb vectors of group b,
+ * each d wide. An attention layer's reads are its pre-RoPE K and V (code/kva/model.py:282-287, one
+ * norm_linear of [W_k; W_v]): na = nb = hkv. A GDN layer's reads are its in-projection outputs
+ * (code/kva/model.py:566-571, one norm_linear of [W_qkv; W_b; W_a]): q | k (na = nb = nk, d = dk), v
+ * (na = nv, nb = 0, d = dv) and [b | a] (na = 1, nb = 0, d = 2 nv), one call each on their column range. Per
+ * row and vector, cos = a . b / (max(|a|, 1e-8) max(|b|, 1e-8)) in fp32 (F.cosine_similarity over the
+ * vector); group a's vectors are first scaled elementwise by the k_norm gain kgain [d] bf16 (gain_kind 1:
+ * 1 + gain; NULL: no k norm), which is the cosine of the k-normed reads (code/kva/model.py:353-359) since
+ * the per-head RMS factor cancels. out[0] += weight * (sum of group a's cosines) and, when nb > 0,
+ * out[1] += weight * (sum of group b's), in fp64 and a fixed order (weight = 1 / (rows na) gives a group's
+ * document mean). workspace: at least 8 * ceil(rows / 16) bytes. d a power of two from 8 to 256;
+ * ld_pred / ld_true multiples of 8, pointers 16-byte aligned. */
 int rf_read_cosine(const uint16_t* pred, int64_t ld_pred, const uint16_t* truth, int64_t ld_true, int64_t rows,
-                   int hkv, int d, const uint16_t* kgain, int gain_kind, double weight, double* out,
+                   int na, int nb, int d, const uint16_t* kgain, int gain_kind, double weight, double* out,
                    void* workspace, size_t ws_bytes, hipStream_t stream);
 
 /* The ridge solve of RidgeFit (code/kva/ridge.py:80-105) in fp64: for each of the nlam values lam (host array

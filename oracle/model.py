@@ -162,13 +162,20 @@ class OracleModel:
         return ops.apply_rope(q.transpose(0, 1), cos, sin), None
 
     def reads(self, i, x):
-        """Pre-RoPE K and V per KV head, {'k', 'v'}: [tokens, Hkv, d] of layer i's inputs x, K head-normed
-        for Qwen3 / Qwen3.5 (code/kva/model.py:282-287, :353-359, :558-565 attention layers)."""
-        if self.layer_types[i] != "attn":
-            raise UnsupportedArchitecture("reads of GDN layers")
+        """The reads of layer i's inputs x. Attention layers: pre-RoPE K and V per KV head, {'k', 'v'}:
+        [tokens, Hkv, d], K head-normed for Qwen3 / Qwen3.5 (code/kva/model.py:282-287, :353-359, :558-565).
+        GDN layers: the in-projection outputs that feed the state, {'q', 'k'} [tokens, nk, dk] and 'v'
+        [tokens, nv, dv] before the conv, and 'ba' [tokens, 1, 2 nv] = [b | a], the beta and decay
+        pre-activations (code/kva/model.py:566-571)."""
         w = self.W[i]
         xn = self.in_norm(x, w["ln1"])
         n = x.shape[0]
+        if self.layer_types[i] != "attn":
+            pre, b, a = self.gdn_inputs(i, xn)
+            kd = self.nk * self.dk
+            q, k, v = pre.split([kd, kd, self.nv * self.dv], -1)
+            return dict(q=q.reshape(n, self.nk, self.dk), k=k.reshape(n, self.nk, self.dk),
+                        v=v.reshape(n, self.nv, self.dv), ba=torch.cat((b, a), -1)[:, None, :])
         k = F.linear(xn, w["k"]).view(n, self.n_kv, self.head_dim)
         if self.arch != "llama":
             k = self.head_norm(k, w["k_norm"])

@@ -136,21 +136,22 @@ __global__ __launch_bounds__(256) void k_colsum_fold(const float* __restrict__ p
 }
 
 // Read cosines of one late layer for one held-out document (code/scripts/fit_sweep.py:307-313). A work
-// item is one head vector of one row: items 0 .. hkv - 1 of a row are its K heads, hkv .. 2 hkv - 1 its V
-// heads (the [K | V] column layout of the reads GEMM). d / 8 lanes take one item, one 16-byte chunk each,
-// and reduce dot and norms with xor butterflies (every lane ends with the same sums). A block covers
-// COS_ROWS rows; each lane group walks its items in a fixed order, and the block's per-thread sums are
-// folded by a fixed tree into partial[block] = (sum of K cosines, sum of V cosines).
+// item is one vector of one row: items 0 .. na - 1 of a row are group a's vectors (an attention layer's K
+// heads, scaled by the k_norm gain), na .. na + nb - 1 group b's (its V heads): the [K | V] column layout
+// of the reads GEMM; a GDN layer's q | k, v and [b | a] column ranges are groups too. d / 8 lanes take one
+// item, one 16-byte chunk each, and reduce dot and norms with xor butterflies (every lane ends with the
+// same sums). A block covers COS_ROWS rows; each lane group walks its items in a fixed order, and the
+// block's per-thread sums are folded by a fixed tree into partial[block] = (sum over group a, over group b).
 constexpr int COS_ROWS = 16;
 
 __global__ __launch_bounds__(256) void k_read_cosine(const uint16_t* __restrict__ pred, int64_t ldp,
                                                      const uint16_t* __restrict__ tru, int64_t ldt, int64_t rows,
-                                                     int hkv, int d, const uint16_t* __restrict__ kgain,
+                                                     int na, int nb, int d, const uint16_t* __restrict__ kgain,
                                                      int gain_kind, float2* __restrict__ partial) {
   __shared__ float red[2][256];
   const int t = threadIdx.x;
   const int g = d >> 3, sub = t & (g - 1), grp = t / g, ngrp = 256 / g;
-  const int per_row = 2 * hkv, nitems = COS_ROWS * per_row;
+  const int per_row = na + nb, nitems = COS_ROWS * per_row;
   const int64_t r0 = static_cast<int64_t>(blockIdx.x) * COS_ROWS;
   float gn[8];
 #pragma unroll
@@ -163,7 +164,7 @@ __global__ __launch_bounds__(256) void k_read_cosine(const uint16_t* __restrict_
     const int64_t col = static_cast<int64_t>(hv) * d + sub * 8;
     const uint4 pv = *reinterpret_cast<const uint4*>(pred + r * ldp + col);
     const uint4 tv = *reinterpret_cast<const uint4*>(tru + r * ldt + col);
-    const bool is_k = hv < hkv;
+    const bool is_k = hv < na;
     float dot = 0.0f, n1 = 0.0f, n2 = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
@@ -197,10 +198,10 @@ __global__ __launch_bounds__(256) void k_read_cosine(const uint16_t* __restrict_
   if (t == 0) partial[blockIdx.x] = make_float2(red[0][0], red[1][0]);
 }
 
-// out[0] += weight * sum_j partial[j].x, out[1] += weight * sum_j partial[j].y, in fp64 and a fixed order
-// (thread i sums blocks i, i + 256, ... in order, then a fixed tree over the 256 threads).
+// out[0] += weight * sum_j partial[j].x, and if two, out[1] += weight * sum_j partial[j].y, in fp64 and a
+// fixed order (thread i sums blocks i, i + 256, ... in order, then a fixed tree over the 256 threads).
 __global__ __launch_bounds__(256) void k_cosine_fold(const float2* __restrict__ partial, int64_t nblk, double weight,
-                                                     double* __restrict__ out) {
+                                                     double* __restrict__ out, int two) {
   __shared__ double red[2][256];
   const int t = threadIdx.x;
   double sk = 0.0, sv = 0.0;
@@ -220,7 +221,7 @@ __global__ __launch_bounds__(256) void k_cosine_fold(const float2* __restrict__ 
   }
   if (t == 0) {
     out[0] += weight * red[0][0];
-    out[1] += weight * red[1][0];
+    if (two) out[1] += weight * red[1][0];
   }
 }
 
@@ -276,14 +277,16 @@ extern "C" int rf_colsum_fold(const float* partial, int64_t ntiles, int64_t cols
 }
 
 extern "C" int rf_read_cosine(const uint16_t* pred, int64_t ld_pred, const uint16_t* truth, int64_t ld_true,
-                              int64_t rows, int hkv, int d, const uint16_t* kgain, int gain_kind, double weight,
+                              int64_t rows, int na, int nb, int d, const uint16_t* kgain, int gain_kind, double weight,
                               double* out, void* workspace, size_t ws_bytes, hipStream_t stream) {
   if (!pred || !truth || !out) return fail(RF_EINVAL_ARG, "rf_read_cosine: null pointer");
-  if (rows < 0 || hkv <= 0 || (d != 64 && d != 128 && d != 256) || ld_pred < 2ll * hkv * d ||
-      ld_true < 2ll * hkv * d || ld_pred % 8 || ld_true % 8 || (gain_kind != 0 && gain_kind != 1))
-    return fail(RF_EINVAL_SHAPE, "rf_read_cosine: rows %lld, hkv %d, d %d (64, 128 or 256), ld_pred %lld, "
-                "ld_true %lld (>= 2 hkv d, multiples of 8), gain_kind %d", (long long)rows, hkv, d,
-                (long long)ld_pred, (long long)ld_true, gain_kind);
+  const bool d_ok = d >= 8 && d <= 256 && (d & (d - 1)) == 0;
+  const int64_t width = static_cast<int64_t>(na) * d + static_cast<int64_t>(nb) * d;
+  if (rows < 0 || na <= 0 || nb < 0 || na > 4096 || nb > 4096 || !d_ok || ld_pred < width || ld_true < width ||
+      ld_pred % 8 || ld_true % 8 || (gain_kind != 0 && gain_kind != 1))
+    return fail(RF_EINVAL_SHAPE, "rf_read_cosine: rows %lld, na %d, nb %d, d %d (a power of two, 8 to 256), "
+                "ld_pred %lld, ld_true %lld (>= (na + nb) d, multiples of 8), gain_kind %d", (long long)rows, na, nb,
+                d, (long long)ld_pred, (long long)ld_true, gain_kind);
   if (!aligned16(pred) || !aligned16(truth)) return fail(RF_EINVAL_SHAPE, "rf_read_cosine: 16-byte alignment");
   const int64_t nblk = (rows + COS_ROWS - 1) / COS_ROWS;
   if (nblk > (1ll << 31) - 1) return fail(RF_EINVAL_SHAPE, "rf_read_cosine: rows %lld", (long long)rows);
@@ -293,8 +296,8 @@ extern "C" int rf_read_cosine(const uint16_t* pred, int64_t ld_pred, const uint1
                 (long long)(nblk * static_cast<int64_t>(sizeof(float2))));
   float2* part = static_cast<float2*>(workspace);
   hipLaunchKernelGGL(k_read_cosine, dim3(static_cast<unsigned>(nblk)), dim3(256), 0, stream, pred, ld_pred, truth,
-                     ld_true, rows, hkv, d, kgain, gain_kind, part);
+                     ld_true, rows, na, nb, d, kgain, gain_kind, part);
   if (int rc = check_launch("rf_read_cosine")) return rc;
-  hipLaunchKernelGGL(k_cosine_fold, dim3(1), dim3(256), 0, stream, part, nblk, weight, out);
+  hipLaunchKernelGGL(k_cosine_fold, dim3(1), dim3(256), 0, stream, part, nblk, weight, out, nb > 0 ? 1 : 0);
   return check_launch("rf_read_cosine");
 }

@@ -77,7 +77,7 @@ SIGNATURES = {
     "rf_gated_rms_norm": [_P, _I64, _P, _I64, _P, _I64, _I32, _I32, _F32, _P, _I64, _P],
     "rf_dequant_gguf_rows": [_I32, _P, _I64, _I64, _I64, _P, _I64, _P],
     "rf_dequant_i8_rows": [_P, _I64, _P, _I64, _I64, _I64, _I32, _P, _I64, _P],
-    "rf_read_cosine": [_P, _I64, _P, _I64, _I64, _I32, _I32, _P, _I32, _F64, _P, _P, _SZ, _P],
+    "rf_read_cosine": [_P, _I64, _P, _I64, _I64, _I32, _I32, _I32, _P, _I32, _F64, _P, _P, _SZ, _P],
     "rf_window_mass_workspace_bytes": [_I32, _I32, _I32, _I32, _I64, _PSZ],
     "rf_window_mass": [_P, _I64, _I32, _I64, _I32, _I32, _P, _I32, _I64, _I64, _F32, _P, _P, _SZ, _P],
 }

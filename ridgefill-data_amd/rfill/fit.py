@@ -22,14 +22,17 @@ reference's h.float().mean(0) is), so the state dict has split_state()'s layout 
 into fp64, as the reference's per-document fp32 GEMM is added into fp64.
 
 Selection (fit_sweep.py:298-318). For each held-out document: one exact forward (stopped after the last
-layer's input); per late layer i the true reads norm(h_i) [W_k; W_v]^T (one norm_linear GEMM, the
-pre-RoPE K | V of code/kva/model.py:282-287); per candidate (each lambda's map, then the identity) the
-predicted input x = h_S W^T + b (rf_map_apply) and its reads; rf_read_cosine adds the document's mean
-K and V cosines (k_norm gain applied for Qwen3) into an fp64 score per candidate and layer.
+layer's input); per late layer i the true reads, one norm_linear GEMM: norm(h_i) [W_k; W_v]^T for an
+attention layer (the pre-RoPE K | V of code/kva/model.py:282-287), norm(h_i) [W_qkv; W_b; W_a]^T for a
+GDN layer (its pre-conv q | k | v and [b | a], code/kva/model.py:566-571); per candidate (each lambda's
+map, then the identity) the predicted input x = h_S W^T + b (rf_map_apply) and its reads; rf_read_cosine
+adds the document's mean cosine of each read (K and V, k_norm gain applied for Qwen3 / Qwen3.5; or q, k, v
+and [b | a]) into an fp64 score per candidate and layer, which averages them.
 """
 import torch
 
 from . import ops, ridge
+from ._lib import UnsupportedArchitecture
 from .kva import Projector
 
 LAMBDAS = (1e-4, 3e-4, 1e-3, 3e-3, 0.01, 0.03, 0.1, 0.3, 1.0)      # fit_sweep.py:44
@@ -150,26 +153,48 @@ def _inputs(model, ids, first):
     return got
 
 
+def _read_groups(model, i):
+    """(weights of layer i's reads, [(column, na, nb, d, gain, weight per row), ...]): an attention layer's
+    reads are the pre-RoPE K | V of [W_k; W_v] (code/kva/model.py:282-287, :353-359, :558-565), one group pair
+    with the k_norm gain on K; a GDN layer's are its in-projection outputs before the conv
+    (code/kva/model.py:566-571): q | k per key head, v per value head, and the [b | a] row, from one product
+    over [W_qkv; W_b; W_a]."""
+    if model.layer_types[i] == "attn":
+        w = model._layer(i)
+        hkv, d = model.n_kv, model.head_dim
+        return w["wkv"], [(0, hkv, hkv, d, w.get("k_norm"), 1.0 / hkv)]
+    w = model._layer(i, "gdn")
+    kd, vd, nv = model.nk * model.dk, model.nv * model.dv, model.nv
+    if 2 * nv < 8 or 2 * nv > 256 or (2 * nv) & (2 * nv - 1):
+        raise UnsupportedArchitecture(f"read scores of GDN layers with {nv} value heads (2 nv: a power of two, "
+                                      f"8 to 256)")
+    return w["w_in"], [(0, model.nk, model.nk, model.dk, None, 1.0 / model.nk), (2 * kd, nv, 0, model.dv, None, 1.0 / nv),
+                       (2 * kd + vd, 1, 0, 2 * nv, None, 1.0)]
+
+
 @torch.no_grad()
 def read_scores(model, held, split, maps):
     """{candidate: {layer: mean read cosine}} over the held-out documents (fit_sweep.py:298-314);
-    candidates: the lambdas of maps, then "identity"."""
+    candidates: the lambdas of maps, then "identity". Per document and layer, the mean over the layer's
+    reads (K and V; or q, k, v and [b | a]) of each read's mean cosine over rows and vectors."""
     late = list(range(split, model.n_layers))
     cand = list(maps) + ["identity"]
     dev = model.device
-    score = torch.zeros(len(cand), len(late), 2, dtype=torch.float64, device=dev)
-    H, hkv, d = model.hidden, model.n_kv, model.head_dim
+    score = torch.zeros(len(cand), len(late), 4, dtype=torch.float64, device=dev)
+    nreads = []
+    H = model.hidden
     for ids in held:
         got = _inputs(model, ids, split)
         hs = got[split]
         n = hs.shape[0]
         ws = torch.empty(8 * ((n + 15) // 16) + 8, dtype=torch.uint8, device=dev)
         ssq_s = ops.row_ssq(hs)
+        nreads = []
         for j, i in enumerate(late):
-            w = model._layer(i)
-            wkv = w["wkv"]
-            gws = model.gemm_workspace(n, wkv.shape[0], H, dev)
-            true = ops.norm_linear(got[i], ops.row_ssq(got[i]), model.eps, wkv, workspace=gws)
+            wr, groups = _read_groups(model, i)
+            nreads.append(sum(1 + (nb > 0) for _, _, nb, _, _, _ in groups))
+            gws = model.gemm_workspace(n, wr.shape[0], H, dev)
+            true = ops.norm_linear(got[i], ops.row_ssq(got[i]), model.eps, wr, workspace=gws)
             pred = torch.empty_like(true)
             for c, lam in enumerate(cand):
                 if lam == "identity":
@@ -177,10 +202,15 @@ def read_scores(model, held, split, maps):
                 else:
                     W, b = maps[lam][i]
                     x, sx = ops.map_apply(hs, W, b, workspace=model.gemm_workspace(n, W.shape[0], H, dev))
-                ops.norm_linear(x, sx, model.eps, wkv, out=pred, workspace=gws)
-                ops.read_cosine(pred, true, hkv, d, w.get("k_norm"), model.knorm_kind, 1.0 / (n * hkv),
-                                score[c, j], workspace=ws)
-    s = (score.sum(2) / (2 * len(held))).cpu()
+                ops.norm_linear(x, sx, model.eps, wr, out=pred, workspace=gws)
+                slot = 0
+                for col, na, nb, d, gain, wt in groups:
+                    width = (na + nb) * d
+                    ops.read_cosine(pred[:, col:col + width], true[:, col:col + width], na, nb, d, gain,
+                                    model.knorm_kind, wt / n, score[c, j, slot:slot + 2], workspace=ws)
+                    slot += 1 + (nb > 0)
+    div = torch.tensor(nreads, dtype=torch.float64, device=dev) * len(held)
+    s = (score.sum(2) / div).cpu()
     return {lam: {i: float(s[c, j]) for j, i in enumerate(late)} for c, lam in enumerate(cand)}
 
 

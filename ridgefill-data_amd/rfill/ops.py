@@ -815,25 +815,27 @@ def window_mass(q, pos0, kbuf, hq, scale, mass, workspace=None):
     return mass
 
 
-def read_cosine(pred, truth, hkv, d, kgain, gain_kind, weight, out, workspace=None):
-    """out[0] += weight * sum of the K-head cosines, out[1] += weight * sum of the V-head cosines between
-    the reads pred and truth [rows, >= 2 hkv d] bf16 ([K | V] columns), K heads scaled by the k_norm gain
-    kgain [d] (or None), per row and head (code/scripts/fit_sweep.py:307-313)."""
+def read_cosine(pred, truth, na, nb, d, kgain, gain_kind, weight, out, workspace=None):
+    """Read cosines of one layer and document (code/scripts/fit_sweep.py:307-313): each row of pred and truth
+    [rows, >= (na + nb) d] bf16 holds na vectors of group a, then nb of group b, each d wide (an attention
+    layer's K | V heads: na = nb = hkv; a GDN layer's q | k heads, its v heads or its [b | a] row, one call
+    each on their column range). out[0] += weight * the sum of group a's cosines, group a's vectors scaled by
+    the k_norm gain kgain [d] (or None) first; out[1] += weight * the sum of group b's when nb > 0."""
     _need(pred, "pred", torch.bfloat16, 2)
     _need(truth, "truth", torch.bfloat16, 2)
     _need(out, "out", torch.float64, 1)
     rows = pred.shape[0]
-    if truth.shape[0] != rows or min(pred.shape[1], truth.shape[1]) < 2 * hkv * d or out.numel() < 2:
-        raise ValueError(f"read_cosine: pred {tuple(pred.shape)}, truth {tuple(truth.shape)}, hkv {hkv}, d {d}")
+    if truth.shape[0] != rows or min(pred.shape[1], truth.shape[1]) < (na + nb) * d or out.numel() < (2 if nb else 1):
+        raise ValueError(f"read_cosine: pred {tuple(pred.shape)}, truth {tuple(truth.shape)}, na {na}, nb {nb}, d {d}")
     if kgain is not None:
         _need(kgain, "kgain", torch.bfloat16, 1)
         if kgain.numel() != d:
-            raise ValueError(f"read_cosine: kgain {kgain.numel()} values, head_dim {d}")
+            raise ValueError(f"read_cosine: kgain {kgain.numel()} values, vector width {d}")
     need = 8 * ((rows + 15) // 16)
     if workspace is None:
         workspace = torch.empty(max(need, 8), dtype=torch.uint8, device=pred.device)
-    _lib.call("rf_read_cosine", _ptr(pred), pred.stride(0), _ptr(truth), truth.stride(0), rows, hkv, d, _ptr(kgain),
-              gain_kind, float(weight), _ptr(out), _ptr(workspace), workspace.numel(), _stream(pred))
+    _lib.call("rf_read_cosine", _ptr(pred), pred.stride(0), _ptr(truth), truth.stride(0), rows, na, nb, d,
+              _ptr(kgain), gain_kind, float(weight), _ptr(out), _ptr(workspace), workspace.numel(), _stream(pred))
     return out
 
 

@@ -49,7 +49,7 @@ def test_read_cosine_matches_fp64(dev, rows, hkv, d, gk):
     out = torch.zeros(2, dtype=torch.float64, device=dev)
     w = 1.0 / (rows * hkv)
     for _ in range(2):                            # accumulates
-        ops.read_cosine(p.to(dev), t.to(dev), hkv, d, None if gain is None else gain.to(dev), gk or 0, w, out)
+        ops.read_cosine(p.to(dev), t.to(dev), hkv, hkv, d, None if gain is None else gain.to(dev), gk or 0, w, out)
     torch.cuda.synchronize()
     gw = None if gain is None else gain.double() + (1.0 if gk == 1 else 0.0)
     want = _cos64(p[:, :2 * hkv * d], t[:, :2 * hkv * d], hkv, d, gw)
@@ -59,17 +59,38 @@ def test_read_cosine_matches_fp64(dev, rows, hkv, d, gk):
         assert abs(a - 2 * w * b) < 1e-6
 
 
+@pytest.mark.parametrize("rows,na,nb,d", [(300, 3, 0, 8), (77, 2, 5, 16), (129, 1, 0, 64), (40, 4, 4, 32)])
+def test_read_cosine_groups_match_fp64(dev, rows, na, nb, d):
+    """Unequal groups and narrow vectors (a GDN layer's v heads alone, its [b | a] row of 2 nv values): group
+    a's sum into out[0] with its gain, group b's into out[1]; with nb = 0 out[1] stays untouched."""
+    from rfill import ops
+    g = torch.Generator().manual_seed(rows + na)
+    t = torch.randn(rows, (na + nb) * d + 8, generator=g).to(torch.bfloat16)
+    p = (t.float() + 0.5 * torch.randn(t.shape, generator=g)).to(torch.bfloat16)
+    gain = (1 + 0.2 * torch.randn(d, generator=g)).to(torch.bfloat16)
+    out = torch.full((2,), 7.0, dtype=torch.float64, device=dev)
+    ops.read_cosine(p.to(dev), t.to(dev), na, nb, d, gain.to(dev), 0, 0.5, out)
+    torch.cuda.synchronize()
+    a, b = p[:, :(na + nb) * d].double().view(rows, na + nb, d), t[:, :(na + nb) * d].double().view(rows, na + nb, d)
+    a[:, :na] *= gain.double()
+    b[:, :na] *= gain.double()
+    cos = (a * b).sum(-1) / (a.norm(dim=-1).clamp_min(1e-8) * b.norm(dim=-1).clamp_min(1e-8))
+    want = [7.0 + 0.5 * float(cos[:, :na].sum()), 7.0 + (0.5 * float(cos[:, na:].sum()) if nb else 0.0)]
+    got = out.cpu().tolist()
+    assert abs(got[0] - want[0]) < 1e-5 * max(1.0, abs(want[0])) and abs(got[1] - want[1]) < 1e-5 * max(1.0, abs(want[1]))
+
+
 def test_read_cosine_refuses(dev):
     from rfill import _lib
     x = torch.zeros(16, 2 * 96, dtype=torch.bfloat16, device=dev)
     out = torch.zeros(2, dtype=torch.float64, device=dev)
     ws = torch.empty(64, dtype=torch.uint8, device=dev)
-    with pytest.raises(ValueError, match="64, 128 or 256"):
-        _lib.call("rf_read_cosine", x.data_ptr(), 192, x.data_ptr(), 192, 16, 1, 96, None, 0, 1.0, out.data_ptr(),
+    with pytest.raises(ValueError, match="a power of two"):
+        _lib.call("rf_read_cosine", x.data_ptr(), 192, x.data_ptr(), 192, 16, 1, 1, 96, None, 0, 1.0, out.data_ptr(),
                   ws.data_ptr(), 64, None)
     x = torch.zeros(40, 256, dtype=torch.bfloat16, device=dev)
     with pytest.raises(ValueError, match="workspace"):
-        _lib.call("rf_read_cosine", x.data_ptr(), 256, x.data_ptr(), 256, 40, 1, 128, None, 0, 1.0, out.data_ptr(),
+        _lib.call("rf_read_cosine", x.data_ptr(), 256, x.data_ptr(), 256, 40, 1, 1, 128, None, 0, 1.0, out.data_ptr(),
                   ws.data_ptr(), 16, None)
 
 
@@ -163,6 +184,52 @@ def test_selection_matches_the_oracle(dev):
     x = torch.randn(10, 256, device=dev).to(torch.bfloat16)
     w, b = maps[r["lam"]][3]
     torch.testing.assert_close(r["projector"](3, x).float(), (x.float() @ w.float().T + b.float()), rtol=2e-2, atol=2e-2)
+
+
+def test_hybrid_selection_matches_the_oracle(dev):
+    """lambda selection on a Qwen3.5-style hybrid (3 GDN : 1 attention, the golden workload of
+    tests/golden/q35.py): GDN layers score their pre-conv q / k / v and [b | a] reads, the attention layer its
+    k-normed K and V. Device capture, fit and scores against the oracle's scores of the same maps over its own
+    bf16 forward (2e-4), the same chosen lambda, fit_sweep end to end; and the scores of the golden maps against
+    the ones the reference computed in fp32 (tests/golden/finish_q35.npz, 2e-3: bf16 against fp32 forwards)."""
+    import sys
+    from pathlib import Path
+    import numpy as np
+    sys.path.insert(0, str(Path(__file__).resolve().parent / "golden"))
+    import q35
+    from rfill import fit
+    from rfill.model import FillModel
+    cfg, t = q35.CONFIG, q35.tensors()
+    m = FillModel(cfg, t, dev)
+    S = q35.SPLIT
+    docs, held = _docs([400, 260, 333, 150], 15, q35.VOCAB), _docs([200, 333], 16, q35.VOCAB)
+    lams = (1e-4, 1e-2, 1.0)
+    cap = fit.Capture(m, [S])
+    for ids in docs:
+        cap.add_document(ids)
+    maps = fit.fit_maps(cap.state(S, device=dev), lams, device=dev)
+    mine = fit.read_scores(m, held, S, maps)
+    om = OM.OracleModel(cfg, t, dtype=torch.bfloat16)
+    cpu_maps = {lam: {i: (w.cpu(), b.cpu()) for i, (w, b) in per.items()} for lam, per in maps.items()}
+    want = OF.read_scores(om, held, S, cpu_maps)
+    worst = max(abs(mine[c][i] - want[c][i]) for c in want for i in want[c])
+    print("hybrid scores (device / oracle):", {c: [(round(mine[c][i], 5), round(want[c][i], 5)) for i in mine[c]]
+                                              for c in mine}, f"worst {worst:.1e}")
+    assert worst < SCORE_TOL
+    assert abs(mine["identity"][S] - 1.0) < 1e-6
+    mean = {c: sum(v.values()) / len(v) for c, v in want.items()}
+    top = sorted((mean[lam] for lam in lams), reverse=True)
+    if top[0] - top[1] > 2 * SCORE_TOL:
+        assert fit.best_lambda(mine, lams) == OF.best_lambda(want, lams)
+    res = fit.fit_sweep(m, docs, held, [S], lams)
+    assert res[S]["lam"] == fit.best_lambda(mine, lams) and res[S]["rows"] == 1143
+    gold = np.load(q35.FIXTURE)
+    gm = {"g": {i: (w.to(dev, torch.bfloat16), b.to(dev, torch.bfloat16)) for i, (w, b) in q35.maps().items()}}
+    got = fit.read_scores(m, [q35.held_ids()], S, gm)
+    errs = {(c, i): abs(got[c][i] - float(gold[f"score_{'proj' if c == 'g' else 'identity'}_{i}"]))
+            for c in got for i in got[c]}
+    print("golden scores:", {k: round(v, 6) for k, v in errs.items()})
+    assert max(errs.values()) < 2e-3
 
 
 def test_capture_refuses(dev):
