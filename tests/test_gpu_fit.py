@@ -107,3 +107,60 @@ def test_ridge_stats_and_fit_match_the_oracle(dev):
         print(f"lam {lam:g}: solve-only rel err {e1:.2e}, stats+solve rel err {e2:.2e}")
         assert e1 < MAP_TOL and rel(b1, b_ref) < MAP_TOL
         assert e2 < MAP_TOL
+
+
+def _centred(st, i):
+    """Shift-free statistics of a state: the means of x and y_i, C = sxx - sx sx^T / n, Cxy = sxy - sx sy^T / n."""
+    n = float(st["n"])
+    sx, sy = st["sx"].double().cpu(), st["sy"][i].double().cpu()
+    return dict(mx=st["cx"].double().cpu() + sx / n, my=st["cy"][i].double().cpu() + sy / n,
+                c=st["sxx"].double().cpu() - torch.outer(sx, sx) / n,
+                cxy=st["sxy"][i].double().cpu() - torch.outer(sx, sy) / n)
+
+
+def test_resumed_statistics_continue_the_device_sums(dev):
+    """RidgeStats.from_state on the device (the reference's resumable sufficient statistics,
+    code/scripts/fit_sweep.py:20-25, :271-284): a state saved after the first 7000 rows, moved to the host
+    and back as a saved file would be, then continued with the remaining rows, keeps the saved shifts and
+    gives one pass's means, centred scatter and centred cross products (1e-6); a resume that adds layer 5
+    only carries layer 6's saved sums unchanged; maps fitted from the resumed state agree with one pass's
+    (1e-5)."""
+    from rfill import ridge
+    n, d = 20000, 512
+    x = _student(n, d, 7)
+    g = torch.Generator().manual_seed(8)
+    ys = {}
+    for i in (5, 6):
+        t = torch.eye(d) + 0.05 * torch.randn(d, d, generator=g) / d ** 0.5
+        ys[i] = (x.float() @ t + 0.1 * torch.randn(n, d, generator=g)).to(torch.bfloat16)
+    xd, yd = x.to(dev), {i: y.to(dev) for i, y in ys.items()}
+    one = ridge.RidgeStats(4, [5, 6], d, device=dev)
+    one.add(xd, yd, block=8192)
+    want = one.state()
+    first = ridge.RidgeStats(4, [5, 6], d, device=dev)
+    first.add(xd[:7000], {i: y[:7000] for i, y in yd.items()}, block=8192)
+    saved = first.state(device="cpu")
+    resumed = ridge.RidgeStats.from_state(saved, device=dev)
+    resumed.add(xd[7000:], {i: y[7000:] for i, y in yd.items()}, block=8192)
+    got = resumed.state()
+    assert got["n"] == n and torch.equal(got["cx"].cpu(), saved["cx"].cpu())
+    for i in (5, 6):
+        assert torch.equal(got["cy"][i].cpu(), saved["cy"][i].cpu())
+    # the shifts differ (the first 8192-row block's means against the first 7000 rows'), so compare the
+    # statistics every shift gives alike: means, centred scatter and centred cross products
+    for (k, a), (_, b) in zip(_centred(got, 5).items(), _centred(want, 5).items()):
+        assert rel(a, b) < 1e-6, (k, rel(a, b))
+    for (k, a), (_, b) in zip(_centred(got, 6).items(), _centred(want, 6).items()):
+        assert rel(a, b) < 1e-6, (k, rel(a, b))
+    part = ridge.RidgeStats.from_state(saved, device=dev)
+    part.begin(xd[7000:], block=8192)
+    part.add_layer(5, yd[5][7000:])
+    ps = part.state()
+    assert rel(_centred(ps, 5)["cxy"], _centred(want, 5)["cxy"]) < 1e-6
+    for k in ("cy", "sy", "sxy"):
+        assert torch.equal(ps[k][6].cpu(), saved[k][6].cpu()), k
+    fa, fb = ridge.RidgeFit(got, device=dev), ridge.RidgeFit(want, device=dev)
+    for lam in (1e-3, 1e-2):
+        wa, ba = fa.layer(6, (lam,))[lam]
+        wb, bb = fb.layer(6, (lam,))[lam]
+        assert rel(wa, wb) < 1e-5 and rel(ba, bb) < 1e-5
