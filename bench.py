@@ -16,6 +16,7 @@ reference op sequence in torch on the host cores) timed on a bounded row sample.
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -291,6 +292,83 @@ def cpu_baseline(cfg, w, layer, budget_s=8.0, rows=1024):
                       f"{res['float32'][2]:.1f} s; scaled by 1/16 layers; torch {torch.__version__}"}
 
 
+def cpu_exact_rows_baseline(n=32768, split=18, tail=4096, frac=0.01, reps=2):
+    """The Qwen3-8B-shaped 32K fill with 1 % exact rows on the host, one late layer as the reference runs it
+    (code/kva/kva.py:413-437): x = F.linear(b, W, c), x.index_copy(0, R, h_split[R]), then layer_rows (the
+    fill of all P rows -- norm, K / V, k_norm, RoPE, cache append -- and the rows' full layer: queries,
+    attention over the filled keys, o_proj, the MLP), in bf16, timed `reps` times and scaled to the 18 late
+    layers; the same layer without exact rows (map + fill) for the plain fill's rate. The oracle's op
+    sequence on every core this process may use."""
+    from oracle import model as OM
+    from rfill import synth
+    threads, _, _ = _cpu_info()
+    torch.set_num_threads(threads)
+    cfg = synth.QWEN3_8B
+    L = cfg["num_hidden_layers"] - split
+    P = n - tail
+    t, W, c = synth.layer_weights(cfg, split, "cpu", full=True)
+    b = synth.hidden_states(n, cfg["hidden_size"])[:P]
+    rows = torch.randperm(P, generator=torch.Generator().manual_seed(13))[:int(round(frac * P))].sort().values
+    om = OM.OracleModel(cfg, t, dtype=torch.bfloat16, layers=[split])
+    pos = torch.arange(P)
+    times = {"plain": [], "exact": []}
+    with torch.no_grad():
+        for _ in range(reps):
+            for name in ("plain", "exact"):
+                cache = om.new_cache()
+                t0 = time.perf_counter()
+                x = torch.nn.functional.linear(b, W, c)
+                if name == "exact":
+                    x = x.index_copy(0, rows, b[rows])
+                    om.layer_rows(split, x, pos, rows, cache)
+                else:
+                    om.fill(split, x, pos, cache)
+                times[name].append(time.perf_counter() - t0)
+    te, tp = min(times["exact"]), min(times["plain"])
+    return {"value": round(P / (te * L), 2), "unit": "filled tokens/s", "cores": threads, "kind": "port",
+            "value_without_exact_rows": round(P / (tp * L), 2), "exact_rows": len(rows),
+            "sample": f"oracle layer {split} of the 32K Qwen3-8B-shaped fill ({P} rows, {len(rows)} exact), bf16: "
+                      f"{te:.2f} s with the exact rows' layer_rows, {tp:.2f} s without (best of {reps}); scaled "
+                      f"by {L} late layers"}
+
+
+def cpu_hybrid_baseline(n=32768, split=24, tail=4096, seg=8192):
+    """The Qwen3.5-shaped hybrid's 32K fill on the host, bounded: one 8192-row segment (GDN_ROWS,
+    code/kva/model.py:31) of one GDN layer -- map, in-projections, causal conv, the chunked delta rule's
+    Python chunk loop (code/kva/ops.py:199-262) -- and of one attention layer (map, K / V, RoPE, append),
+    in bf16 with the fp32 recurrence, scaled by P / 8192 segments and the 18 GDN + 6 attention late layers.
+    The oracle's op sequence on every core this process may use."""
+    from oracle import model as OM
+    from rfill import synth
+    threads, _, _ = _cpu_info()
+    torch.set_num_threads(threads)
+    cfg = synth.QWEN35_HYBRID
+    P = n - tail
+    kinds = {i: ("gdn" if cfg["layer_types"][i] == "linear_attention" else "attn")
+             for i in range(split, cfg["num_hidden_layers"])}
+    g = next(i for i in kinds if kinds[i] == "gdn")
+    a = next(i for i in kinds if kinds[i] == "attn")
+    w = synth.hybrid_fill(cfg, split, seg, 0, device="cpu", only=(g, a))
+    n_gdn = sum(k == "gdn" for k in kinds.values())
+    n_attn = len(kinds) - n_gdn
+    t = {k: v for k, v in w["tensors"].items() if f"layers.{g}." in k or f"layers.{a}." in k}
+    om = OM.OracleModel(cfg, t, dtype=torch.bfloat16, layers=[g, a])
+    b = w["h_split"][:seg]
+    pos = torch.arange(seg)
+    took = {}
+    with torch.no_grad():
+        for i in (g, a):
+            cache = om.new_cache()
+            t0 = time.perf_counter()
+            om.fill(i, torch.nn.functional.linear(b, w["maps"][i], w["biases"][i]), pos, cache)
+            took[i] = time.perf_counter() - t0
+    total = P / seg * (n_gdn * took[g] + n_attn * took[a])
+    return {"value": round(P / total, 2), "unit": "filled tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle fill of one {seg}-row segment, bf16: GDN layer {g} {took[g]:.2f} s (map, in-projections, "
+                      f"conv, chunked delta rule), attention layer {a} {took[a]:.2f} s; scaled by {P / seg:.2f} "
+                      f"segments x ({n_gdn} GDN + {n_attn} attention) late layers"}
+
+
 def cpu_fit_baseline(d=4096, targets=16, block=8192, lams=(1e-4, 1e-3, 1e-2)):
     """The reference's fit on the host (code/kva/ridge.py:44-62, 80-105), bounded: one 8192-row block of
     centred fp32 GEMMs into fp64 (X^T X and the 16 X^T Y_l) scaled to the 256 blocks of 2,097,152 rows; the
@@ -418,14 +496,17 @@ def capture_bench(dev, split=SPLIT, n=8192, lams=9):
             "ms_select_per_doc": round(t_sel * 1e3, 1)}
 
 
-def hybrid_bench(dev, reps=3, split=24, n_rows=32768, tail=4096):
+def hybrid_bench(dev, reps=12, split=24, n_rows=32768, tail=4096):
     """The Gated-DeltaNet hybrid's late-layer fill (hidden 2048; layers 24..47 = 18 GDN + 6 attention;
     GDN 16 key / 32 value heads of 128, attention 2 KV heads of 256; P = 28672 filled rows from zero
     state), timed as finish() runs it (fill_late: groups of 8 late layers): per layer rf_map_apply, then the
     GDN fill (rf_norm_linear in-projection + the delta-rule fill, two GDN layers per rf_gdn_fill_batch) or
-    the attention fill (rf_norm_kv_write). Counted work per filled row (the reference's accounting): GDN layer
-    2 H (2 nk dk + nv dv + 2 nv) + 2 H^2 + 2 K C + 6 nv dk dv flop, attention layer 2 H^2 + 2 H (2 Hkv d).
-    The per-layer means come from a second, layer-by-layer pass (one GDN layer at a time)."""
+    the attention fill (rf_norm_kv_write). One cache serves every repetition (its K / V buffers allocated
+    by the warm-up fill, then reset to no rows; GDN states start from zero), each repetition timed with HIP
+    events on the launch stream; the figure is their median, and every repetition's time is reported.
+    Counted work per filled row (the reference's accounting): GDN layer 2 H (2 nk dk + nv dv + 2 nv) + 2 H^2
+    + 2 K C + 6 nv dk dv flop, attention layer 2 H^2 + 2 H (2 Hkv d). The per-layer means come from a
+    second, layer-by-layer pass (one GDN layer at a time)."""
     from rfill import ops, synth
     from rfill.kva import Arm, Projector, fill_late
     from rfill.model import FillModel
@@ -454,13 +535,26 @@ def hybrid_bench(dev, reps=3, split=24, n_rows=32768, tail=4096):
                 f() if timer is None else timer.run(name, f)
         return caches
 
-    fill_late(model, w["h_split"], arm)
+    cache = model.new_cache()
+
+    def reset():                                  # no rows; the attention layers keep their K / V buffers
+        for i in w["layers"]:
+            c = cache[i]
+            cache[i] = dict(kbuf=c["kbuf"], vbuf=c["vbuf"], n=0) if "kbuf" in c else {}
+
+    fill_late(model, w["h_split"], arm, cache=cache)
     torch.cuda.synchronize()
-    t0 = time.perf_counter()
+    rep_ms = []
     for _ in range(reps):
-        fill_late(model, w["h_split"], arm)
-    torch.cuda.synchronize()
-    el = (time.perf_counter() - t0) / reps
+        reset()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        fill_late(model, w["h_split"], arm, cache=cache)
+        e1.record()
+        e1.synchronize()
+        rep_ms.append(e0.elapsed_time(e1))
+    el = statistics.median(rep_ms) / 1e3
+    del cache
     t = KernelTimer()
     step(t)
     # one GDN layer's two kernels apart
@@ -483,6 +577,7 @@ def hybrid_bench(dev, reps=3, split=24, n_rows=32768, tail=4096):
     return {"workload": f"qwen3.5-shaped hybrid fill: hidden {H}, late layers {split}..{cfg['num_hidden_layers'] - 1} "
                         f"({n_gdn} GDN + {n_attn} attention), {P} filled rows",
             "filled_tokens_per_s": round(P / el, 1), "ms_per_fill": round(el * 1e3, 3),
+            "ms_per_fill_reps": [round(x, 3) for x in rep_ms], "timing": f"median of {reps} fills, HIP events",
             "counted_flop": counted, "counted_frac_bf16_peak": round(counted / el / PEAK_BF16, 4),
             "layer_mean_us": {k: round(t.mean_s(k) * 1e6, 1) for k in ("map", "gdn", "attn")},
             "gdn_kernels": {
@@ -756,6 +851,12 @@ def main():
     if not args.no_cpu:
         log("CPU baseline (oracle fill on the host cores)")
         out["cpu_baseline"] = cpu_baseline(cfg, w, SPLIT)
+        if not args.no_exact:
+            log("CPU baseline of the Qwen3-8B 32K fill with 1% exact rows (one layer)")
+            out["cpu_exact_rows_baseline"] = cpu_exact_rows_baseline()
+        if not args.no_hybrid:
+            log("CPU baseline of the hybrid fill (one 8192-row segment per layer kind)")
+            out["cpu_hybrid_baseline"] = cpu_hybrid_baseline()
         if not args.no_fit:
             log("CPU baseline of the fit (bounded sample)")
             out["cpu_fit_baseline"] = cpu_fit_baseline()

@@ -286,7 +286,10 @@ int rf_norm_linear(const uint16_t* x, int64_t ldx, const float* ssq, int64_t P, 
  * two or more chunks is used as two halves: the prep of the next pass runs on a second stream the library
  * keeps per device (default priority) beside the scan of the current pass on `stream`, ordered by events;
  * `stream` waits for all of it, so work queued after the call on `stream` sees the finished fill. Results
- * are bit-identical to the one-stream schedule. */
+ * are bit-identical to the one-stream schedule. That stream and its events are created on the first such
+ * call on a device (under a mutex) and kept until the process ends: the library's one piece of global
+ * state besides the thread-local error text and rf_gdn_fill_noalloc's array. No device memory is
+ * allocated for it. */
 int rf_gdn_fill(const uint16_t* pre, int64_t ld, int64_t P, int nk, int nv, int dk, int dv, const uint16_t* conv_w,
                 const uint16_t* conv_in, uint16_t* conv_out, const float* a_log, const float* dt_bias, float* state,
                 void* workspace, size_t ws_bytes, hipStream_t stream);

@@ -203,11 +203,12 @@ def hybrid_full_weights(cfg, layer, device="cpu"):
     return {k: v.to(torch.bfloat16) for k, v in t.items()}
 
 
-def hybrid_fill(cfg, split, n_rows, tail, device="cpu", map_noise=0.02, full=False):
+def hybrid_fill(cfg, split, n_rows, tail, device="cpu", map_noise=0.02, full=False, only=None):
     """The hybrid late-layer fill workload (dict as dense_fill's, plus layer_types); full: also each late
-    layer's whole weights (hybrid_full_weights) for the exact tail."""
+    layer's whole weights (hybrid_full_weights) for the exact tail; only: build these late layers alone
+    (each layer's draws do not depend on the others)."""
     L, h = cfg["num_hidden_layers"], cfg["hidden_size"]
-    layers = list(range(split, L))
+    layers = list(range(split, L)) if only is None else sorted(only)
     tensors, maps, biases = {}, {}, {}
     for l in layers:
         if cfg["layer_types"][l] == "linear_attention":
