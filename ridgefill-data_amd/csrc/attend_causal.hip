@@ -1,6 +1,9 @@
 // Causal attention of many consecutive queries over one layer's K / V cache: the exact tail's
 // attention in Model.layer (code/kva/ops.py:107-128 attend, queries bottom-right aligned with the keys),
-// head_dim 64 or 128, grouped-query heads with a group of 1, 2, 4 or 8.
+// head_dim 64 or 128 with grouped-query heads in groups of 1, 2, 4 or 8, and head_dim 256 (Qwen3.5's gated
+// attention, code/kva/model.py:436-446) in groups of up to 16. The layout below is the d 64 / 128 one; at
+// d 256 a block has 4 waves (128 query rows: 32 queries of up to four heads of a group, the group's other
+// heads in further blocks), the key tiles are 32 keys, and each wave holds its 32 queries' 256-wide rows.
 //
 // K and V tiles stream from the caches into LDS as full 128-byte lines with direct loads
 // (buffer_load_dwordx4 ... lds), both row-major ([key, d]); the V^T operand of the second product is read
@@ -44,10 +47,17 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-constexpr int KT = 64;                 // keys per tile
-constexpr int NW = 8;                  // waves per block
-constexpr int NTHR = 64 * NW;
-constexpr int QROWS = 32 * NW;         // query rows (query, head) per block: 32 per wave
+// Per head_dim: keys per tile KT and waves per block NW (32 query rows each). d 64 / 128: 64-key tiles,
+// 8 waves (two per SIMD). d 256: a wave's queries (64 registers), its O^T (128) and two tiles' scores
+// leave room for one wave per SIMD, so 4 waves, and 32-key tiles keep four 32 KB stages in LDS.
+template <int AD>
+struct Cfg {
+  static constexpr int KT = AD == 256 ? 32 : 64;
+  static constexpr int NW = AD == 256 ? 4 : 8;
+  static constexpr int NTHR = 64 * NW;
+  static constexpr int QROWS = 32 * NW;  // query rows (query, head) per block: 32 per wave
+  static constexpr int KB = KT / 32;     // 32-key halves of a tile
+};
 constexpr int NSTAGE = 4;              // LDS stages: three tiles in flight, one still read
 
 __device__ __forceinline__ bf16x8 as_frag(const uint4& u) { return __builtin_bit_cast(bf16x8, u); }
@@ -73,6 +83,7 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
 // rows onto four different 64-byte bank ranges.
 template <int AD>
 struct Layout {
+  static constexpr int KT = Cfg<AD>::KT, NW = Cfg<AD>::NW;
   static constexpr int KCPR = AD / 8;
   static constexpr int K_U4 = KT * KCPR;
   static constexpr int V_U4 = KT * KCPR;
@@ -81,10 +92,11 @@ struct Layout {
   static constexpr int VLOADS = V_U4 / 64 / NW;
   static constexpr int LOADS = KLOADS + VLOADS;
   static_assert(KLOADS * 64 * NW == K_U4 && VLOADS * 64 * NW == V_U4, "tile loads must split evenly");
+  static_assert(NSTAGE * STAGE_U4 * 16 <= 160 * 1024, "stages fit the LDS");
   __device__ static int kslot(int row, int c) { return row * KCPR + (c ^ (row & (KCPR - 1))); }
-  // d 128: a row is 256 bytes, rows r .. r + 3 shift by 0, 64, 128, 192 bytes; d 64: rows are 128 bytes,
-  // row parity already picks the half of a 256-byte bank line, and rows r, r + 2 shift by 0 and 64
-  __device__ static int vsw(int row) { return AD == 128 ? (row & 3) : ((row >> 1) & 1); }
+  // d 128 / 256: a row is 256 / 512 bytes, rows r .. r + 3 shift by 0, 64, 128, 192 bytes; d 64: rows are
+  // 128 bytes, row parity already picks the half of a 256-byte bank line, and rows r, r + 2 shift by 0 and 64
+  __device__ static int vsw(int row) { return AD >= 128 ? (row & 3) : ((row >> 1) & 1); }
   __device__ static int vslot(int row, int c) { return K_U4 + row * KCPR + (c ^ (4 * vsw(row))); }
 };
 
@@ -102,15 +114,18 @@ struct CausalArgs {
   float scale_log2;        // scale * log2(e)
   uint16_t* out;           // [nq, >= hq * d]
   int64_t ldo;
-  float* part;             // splits > 1: per (query block, K / V head, split) O [256][d], max [256], sum [256]
+  float* part;             // splits > 1: per (query block, head block, split) O [QROWS][d], max, sum [QROWS]
   int split_tiles;         // W: key tiles per split
+  int hpb;                 // query heads per block (all rep of a K / V head, or a run of NW of them)
 };
 
 __device__ __forceinline__ int64_t query_pos(const CausalArgs& a, int j) { return a.qpos ? a.qpos[j] : a.slot0 + j; }
 
+// partials of (query block qb, head block hb, split sp); head blocks are gridDim.y = hkv (rep / hpb)
 template <int AD>
-__device__ __forceinline__ float* part_block(const CausalArgs& a, int qb, int hk, int sp) {
-  return a.part + ((static_cast<int64_t>(qb) * a.hkv + hk) * gridDim.z + sp) * (QROWS * (AD + 2));
+__device__ __forceinline__ float* part_block(const CausalArgs& a, int qb, int hb, int sp) {
+  constexpr int QROWS = Cfg<AD>::QROWS;
+  return a.part + ((static_cast<int64_t>(qb) * gridDim.y + hb) * gridDim.z + sp) * (QROWS * (AD + 2));
 }
 
 // The direct loads of one tile into stage st: instruction i of wave w fills 64 consecutive 16-byte slots
@@ -173,17 +188,17 @@ __device__ __forceinline__ void lane_pair(float v, float& lo, float& hi) {
   hi = __uint_as_float(r[1]);
 }
 
-// S^T = K Q^T for one 64-key tile and the wave's 32 queries: sc[kb][j] = the raw score of key
-// 32 kb + 8 (j / 4) + 4 hh + j % 4 of the tile for query n. (The stage pointers are __restrict__: the
-// LDS reads then carry alias information, and the compiler does not make them wait for the direct loads
-// in flight into the other stages; the kernel's own waits order them.)
+// S^T = K Q^T for one key tile (KB halves of 32 keys) and the wave's 32 queries: sc[kb][j] = the raw
+// score of key 32 kb + 8 (j / 4) + 4 hh + j % 4 of the tile for query n. (The stage pointers are
+// __restrict__: the LDS reads then carry alias information, and the compiler does not make them wait for
+// the direct loads in flight into the other stages; the kernel's own waits order them.)
 template <int AD>
-__device__ __forceinline__ void tile_scores(const char* __restrict__ st, const bf16x8 (&qf)[AD / 16], f32x16 (&sc)[2],
-                                            const FragOffsets<AD>& fo) {
+__device__ __forceinline__ void tile_scores(const char* __restrict__ st, const bf16x8 (&qf)[AD / 16],
+                                            f32x16 (&sc)[Cfg<AD>::KB], const FragOffsets<AD>& fo) {
   using L = Layout<AD>;
-  constexpr int NS = AD / 16;
+  constexpr int NS = AD / 16, KB = Cfg<AD>::KB;
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
+  for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) sc[kb][r] = 0.f;
 #pragma unroll
@@ -200,23 +215,25 @@ __device__ __forceinline__ void tile_scores(const char* __restrict__ st, const b
 // tile's scores sn (from stage sn_st), and O^T += V^T P^T from this tile's stage st.
 template <int AD>
 __device__ __forceinline__ void tile_step(const char* __restrict__ st, const char* __restrict__ sn_st,
-                                          const bf16x8 (&qf)[AD / 16], f32x16 (&sc)[2], f32x16 (&sn)[2],
-                                          f32x16 (&o)[AD / 32], float& mref, float& lsum, int64_t k0, bool edge,
-                                          int64_t mypos, int hh, float c, const FragOffsets<AD>& fo) {
+                                          const bf16x8 (&qf)[AD / 16], f32x16 (&sc)[Cfg<AD>::KB],
+                                          f32x16 (&sn)[Cfg<AD>::KB], f32x16 (&o)[AD / 32], float& mref, float& lsum,
+                                          int64_t k0, bool edge, int64_t mypos, int hh, float c,
+                                          const FragOffsets<AD>& fo) {
   using L = Layout<AD>;
-  constexpr int NB = AD / 32, NS = AD / 16;
+  constexpr int NB = AD / 32, NS = AD / 16, KB = Cfg<AD>::KB, KT = Cfg<AD>::KT;
+  constexpr int NP = 8 * KB;                            // probability pairs per lane
   if (edge) {
     // key 32 kb + 8 (j / 4) + 4 hh + j % 4 of the tile is past the query when its offset exceeds rel
     const int rel = static_cast<int>(min<int64_t>(max<int64_t>(mypos - k0, -1), KT)) - 4 * hh;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
       for (int j = 0; j < 16; ++j)
         if (32 * kb + 8 * (j >> 2) + (j & 3) > rel) sc[kb][j] = -INFINITY;
   }
   float tmax = -INFINITY;
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb)
+  for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
     for (int j = 0; j < 16; ++j) tmax = fmaxf(tmax, sc[kb][j]);
   float lo, hi;
@@ -232,21 +249,21 @@ __device__ __forceinline__ void tile_step(const char* __restrict__ st, const cha
     lsum *= alpha;
   }
   const float mc = mref == -INFINITY ? 0.f : mref * c;  // every key so far masked (a split past the query)
-  // the next tile's 16 score MFMAs, two probabilities after each
+  // the next tile's KB NS score MFMAs, the NP probability pairs spread between them
   float psum = 0.f;
-  uint32_t pk[16];
+  uint32_t pk[NP];
 #pragma unroll
-  for (int kb = 0; kb < 2; ++kb) {
+  for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) sn[kb][r] = 0.f;
   }
 #pragma unroll
-  for (int q = 0; q < 2 * NS; ++q) {
+  for (int q = 0; q < KB * NS; ++q) {
     const int kb = q / NS, s = q % NS;
     sn[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
         as_frag(*reinterpret_cast<const uint4*>(sn_st + fo.ko[s] + kb * 32 * L::KCPR * 16)), qf[s], sn[kb], 0, 0, 0);
 #pragma unroll
-    for (int e = q * 16 / (2 * NS); e < (q + 1) * 16 / (2 * NS); ++e) {
+    for (int e = q * NP / (KB * NS); e < (q + 1) * NP / (KB * NS); ++e) {
       const int pkb = e / 8, pj = 2 * (e % 8);
       const float p0 = __builtin_amdgcn_exp2f(fmaf(sc[pkb][pj], c, -mc));
       const float p1 = __builtin_amdgcn_exp2f(fmaf(sc[pkb][pj + 1], c, -mc));
@@ -255,10 +272,10 @@ __device__ __forceinline__ void tile_step(const char* __restrict__ st, const cha
     }
   }
   lsum += psum;
-  // O^T[d, query] += V^T[d, keys] P^T[keys, query] over the four 16-key steps (keys 16 stp ..: chunks
+  // O^T[d, query] += V^T[d, keys] P^T[keys, query] over the tile's 16-key steps (keys 16 stp ..: chunks
   // 2 stp and 2 stp + 1; P^T step stp = the lane's probabilities 8 stp .. 8 stp + 7)
 #pragma unroll
-  for (int stp = 0; stp < 4; ++stp) {
+  for (int stp = 0; stp < KT / 16; ++stp) {
     const bf16x8 pf = __builtin_bit_cast(bf16x8, make_uint4(pk[4 * stp], pk[4 * stp + 1], pk[4 * stp + 2],
                                                              pk[4 * stp + 3]));
 #pragma unroll
@@ -271,19 +288,21 @@ __device__ __forceinline__ void tile_step(const char* __restrict__ st, const cha
 }
 
 template <int AD>
-__global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
+__global__ __launch_bounds__(Cfg<AD>::NTHR, 1) void k_attend_causal(CausalArgs a) {
   using L = Layout<AD>;
   constexpr int NS = AD / 16;      // 16-deep d steps of S^T
   constexpr int NB = AD / 32;      // 32-row d blocks of O^T
+  constexpr int KT = Cfg<AD>::KT, QROWS = Cfg<AD>::QROWS, KB = Cfg<AD>::KB;
   __shared__ uint4 lds[NSTAGE * L::STAGE_U4];
   const int t = threadIdx.x, lane = t & 63, w = t >> 6, n = lane & 31, hh = lane >> 5;
-  const int rep = a.hq / a.hkv, qp = QROWS / rep;          // consecutive queries per block
-  // block -> (query block, split, K / V head), query blocks fastest: each XCD takes a contiguous run, so
-  // the query blocks of one (head, split) run side by side on one XCD and read the same key tiles
-  // through its L2
+  const int rep = a.hq / a.hkv, qp = QROWS / a.hpb;        // consecutive queries per block
+  // block -> (query block, split, head block), query blocks fastest: each XCD takes a contiguous run, so
+  // the query blocks of one (head block, split) run side by side on one XCD and read the same key tiles
+  // through its L2. Head block hb: K / V head hb / (rep / hpb), its query heads from (hb % (rep / hpb)) hpb.
   const int qbs = gridDim.x, ns = gridDim.z;
   const int u = xcd_tile(blockIdx.x + qbs * (blockIdx.y + gridDim.y * blockIdx.z), qbs * gridDim.y * ns);
-  const int qb = u % qbs, sp = (u / qbs) % ns, hk = u / (qbs * ns);
+  const int qb = u % qbs, sp = (u / qbs) % ns, hb = u / (qbs * ns);
+  const int hk = hb / (rep / a.hpb), hoff = (hb % (rep / a.hpb)) * a.hpb;
   const int j0 = qb * qp;
   const int jlast = min(j0 + qp, a.nq) - 1;
   const int64_t kmax = min(query_pos(a, jlast), a.n_keys - 1);     // the block reads keys 0 .. kmax
@@ -301,7 +320,7 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
   const bool live = jw0 + n <= jlast;
   const int64_t mypos = query_pos(a, jq);
   const int64_t wave_first = query_pos(a, min(jw0, jlast)), wave_last = query_pos(a, min(jw0 + 31, jlast));
-  const int head = hk * rep + hg;
+  const int head = hk * rep + hoff + hg;
   bf16x8 qf[NS];
   {
     const uint16_t* qrow = a.q + static_cast<int64_t>(jq) * a.ldq + head * AD + 8 * hh;
@@ -347,7 +366,7 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
   // ahead into four stages: tile it + 3 goes into the stage of tile it - 1, whose last reads (its V^T)
   // ended before this iteration's barrier.
   const FragOffsets<AD> fo(lane);
-  f32x16 sc[2], sn[2];
+  f32x16 sc[KB], sn[KB];
   auto stage = [&](int it) { return base + ((it - it0) % NSTAGE) * L::STAGE_U4 * 16; };
   for (int i = 0; i < 3; ++i)
     if (it0 + i < it1) issue(it0 + i);
@@ -365,7 +384,7 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
     if (k0 > wave_last) continue;                         // this and every later tile lie past the wave's queries
     tile_step<AD>(stage(it), stage(it + 1), qf, sc, sn, o, m, lsum, k0, k0 + KT - 1 > wave_first, mypos, hh, c, fo);
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) sc[kb] = sn[kb];
+    for (int kb = 0; kb < KB; ++kb) sc[kb] = sn[kb];
   }
   wait_vm_lgkm0<0>();
 
@@ -374,7 +393,7 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
   lane_pair(lsum, llo, lhi);
   const float ltot = llo + lhi;
   if (ns > 1) {                                           // unnormalised partials for k_causal_combine
-    float* pb = part_block<AD>(a, qb, hk, sp);
+    float* pb = part_block<AD>(a, qb, hb, sp);
     const int r = 32 * w + n;
     float* orow = pb + r * AD + 4 * hh;
 #pragma unroll
@@ -401,22 +420,23 @@ __global__ __launch_bounds__(NTHR, 1) void k_attend_causal(CausalArgs a) {
                      bf16_pair(o[b][4 * g + 2] * inv, o[b][4 * g + 3] * inv));
 }
 
-// Merges the key-range splits of one (query block, K / V head): M = max_s m_s, L = sum_s l_s 2^(m_s - M),
+// Merges the key-range splits of one (query block, head block): M = max_s m_s, L = sum_s l_s 2^(m_s - M),
 // O = sum_s O_s 2^(m_s - M) / L (base-2 maxima), splits in order. A thread takes 4 consecutive d of one query
 // row (AD / 4 threads per row, blockIdx.z picks 256 of the block's QROWS * AD / 4 such pieces), so the
 // partials are read as whole rows and the outputs written as 8-byte runs.
 template <int AD>
 __global__ __launch_bounds__(256) void k_causal_combine(CausalArgs a, int ns) {
-  constexpr int TPR = AD / 4;
+  constexpr int TPR = AD / 4, KT = Cfg<AD>::KT, QROWS = Cfg<AD>::QROWS;
   const int idx = blockIdx.z * 256 + threadIdx.x;
   const int r = idx / TPR, e = 4 * (idx % TPR), w = r / 32, n = r % 32;
-  const int rep = a.hq / a.hkv, qp = QROWS / rep;
-  const int hk = blockIdx.y, j0 = blockIdx.x * qp;
+  const int rep = a.hq / a.hkv, qp = QROWS / a.hpb;
+  const int hb = blockIdx.y, j0 = blockIdx.x * qp;
+  const int hk = hb / (rep / a.hpb), hoff = (hb % (rep / a.hpb)) * a.hpb;
   const int hg = (32 * w) / qp, po0 = (32 * w) % qp;
   const int jq = j0 + po0 + n;
   if (jq >= a.nq) return;
   const int64_t stride = QROWS * (AD + 2);
-  const float* base = a.part + (static_cast<int64_t>(blockIdx.x) * a.hkv + hk) * ns * stride;
+  const float* base = a.part + (static_cast<int64_t>(blockIdx.x) * gridDim.y + hb) * ns * stride;
   // the live splits of this query block (those k_attend_causal ran): ceil(ntiles / W)
   const int jlast = min(j0 + qp, a.nq) - 1;
   const int ntiles = static_cast<int>(min(query_pos(a, jlast), a.n_keys - 1) / KT) + 1;
@@ -437,19 +457,31 @@ __global__ __launch_bounds__(256) void k_causal_combine(CausalArgs a, int ns) {
     acc.w += v.w * f;
   }
   const float inv = 1.0f / l;
-  uint16_t* dst = a.out + static_cast<int64_t>(jq) * a.ldo + (hk * rep + hg) * AD + e;
+  uint16_t* dst = a.out + static_cast<int64_t>(jq) * a.ldo + (hk * rep + hoff + hg) * AD + e;
   *reinterpret_cast<uint2*>(dst) = make_uint2(bf16_pair(acc.x * inv, acc.y * inv), bf16_pair(acc.z * inv, acc.w * inv));
 }
 
-int64_t key_tiles(int64_t n_keys) { return (n_keys + KT - 1) / KT; }
+int kt_of(int d) { return d == 256 ? Cfg<256>::KT : Cfg<128>::KT; }
+int qrows_of(int d) { return d == 256 ? Cfg<256>::QROWS : Cfg<128>::QROWS; }
+// query heads per block: the whole group of a K / V head when its 32-query waves fit the block, else a
+// run of as many heads as the block has waves
+int hpb_of(int hq, int hkv, int d) { return std::min(hq / hkv, qrows_of(d) / 32); }
+// head blocks: hkv K / V heads x (rep / hpb) runs of query heads
+int head_blocks(int hq, int hkv, int d) { return hkv * ((hq / hkv) / hpb_of(hq, hkv, d)); }
 
-int64_t query_blocks(int64_t nq, int hq, int hkv) {
-  const int64_t qp = QROWS / (hq / hkv);
+int64_t key_tiles(int64_t n_keys, int d) { return (n_keys + kt_of(d) - 1) / kt_of(d); }
+
+int64_t queries_per_block(int hq, int hkv, int d) { return qrows_of(d) / hpb_of(hq, hkv, d); }
+
+int64_t query_blocks(int64_t nq, int hq, int hkv, int d) {
+  const int64_t qp = queries_per_block(hq, hkv, d);
   return (nq + qp - 1) / qp;
 }
 
 size_t part_bytes(int64_t nq, int hq, int hkv, int d, int splits) {
-  return splits > 1 ? static_cast<size_t>(query_blocks(nq, hq, hkv)) * hkv * splits * QROWS * (d + 2) * 4 : 0;
+  return splits > 1 ? static_cast<size_t>(query_blocks(nq, hq, hkv, d)) * head_blocks(hq, hkv, d) * splits *
+                          qrows_of(d) * (d + 2) * 4
+                    : 0;
 }
 
 // Key-range splits {ns, W}: W key tiles per split block, ns = ceil(key tiles / W) splits at most. With
@@ -465,8 +497,9 @@ struct Splits {
 };
 
 Splits causal_plan(int64_t nq, int hq, int hkv, int d, int64_t n_keys, bool scattered, int64_t slot0) {
-  const int64_t T = key_tiles(n_keys), QB = query_blocks(nq, hq, hkv), qp = QROWS / (hq / hkv);
-  if (QB * hkv >= 256 * (d == 64 ? 2 : 1) || T <= 1) return Splits{1, static_cast<int>(std::max<int64_t>(T, 1))};
+  const int64_t T = key_tiles(n_keys, d), QB = query_blocks(nq, hq, hkv, d), qp = queries_per_block(hq, hkv, d);
+  const int64_t HB = head_blocks(hq, hkv, d), KT = kt_of(d);
+  if (QB * HB >= 256 * (d == 64 ? 2 : 1) || T <= 1) return Splits{1, static_cast<int>(std::max<int64_t>(T, 1))};
   const int64_t slots = 208 * (d == 64 ? 2 : 1);
   auto tiles_of = [&](int64_t qb) {
     if (scattered) return std::max<int64_t>(1, (T * (qb + 1) + QB - 1) / QB);
@@ -477,7 +510,7 @@ Splits causal_plan(int64_t nq, int hq, int hkv, int d, int64_t n_keys, bool scat
   for (int64_t W = std::max<int64_t>(2, (T + 63) / 64); W <= T; ++W) {   // at most 64 splits
     int64_t live = 0;
     for (int64_t qb = 0; qb < QB; ++qb) live += (tiles_of(qb) + W - 1) / W;
-    const int64_t cost = ((live * hkv + slots - 1) / slots) * (W + 2);
+    const int64_t cost = ((live * HB + slots - 1) / slots) * (W + 2);
     if (cost < best_cost || (cost == best_cost && W > best_w)) {
       best_cost = cost;
       best_w = W;
@@ -486,9 +519,12 @@ Splits causal_plan(int64_t nq, int hq, int hkv, int d, int64_t n_keys, bool scat
   return Splits{static_cast<int>((T + best_w - 1) / best_w), static_cast<int>(best_w)};
 }
 
+// head_dim 64 / 128: groups of 1 .. 8 (a block holds every head of a group); 256: groups of 1 .. 16 (runs of
+// up to four heads per block)
 bool causal_shape_ok(int hq, int hkv, int d) {
-  return (d == 64 || d == 128) && hq > 0 && hkv > 0 && hq % hkv == 0 &&
-         (hq / hkv == 1 || hq / hkv == 2 || hq / hkv == 4 || hq / hkv == 8);
+  if ((d != 64 && d != 128 && d != 256) || hq <= 0 || hkv <= 0 || hq % hkv) return false;
+  const int rep = hq / hkv;
+  return (rep & (rep - 1)) == 0 && rep <= (d == 256 ? 16 : 8);
 }
 
 }  // namespace
@@ -500,7 +536,7 @@ extern "C" int rf_attend_causal_workspace_bytes(int64_t nq, int hq, int hkv, int
   if (!bytes || nq < 0 || n_keys < 0) return fail(RF_EINVAL_ARG, "rf_attend_causal_workspace_bytes: arguments");
   if (!causal_shape_ok(hq, hkv, d))
     return fail(RF_EUNSUPPORTED, "rf_attend_causal_workspace_bytes: head_dim %d, %d query heads over %d K / V heads "
-                "(d 64 or 128, a group of 1, 2, 4 or 8)", d, hq, hkv);
+                "(d 64, 128 or 256; a group of 1, 2, 4 or 8, or up to 16 at d 256)", d, hq, hkv);
   *bytes = part_bytes(nq, hq, hkv, d, causal_plan(nq, hq, hkv, d, n_keys, true, 0).ns);
   return RF_OK;
 }
@@ -510,10 +546,11 @@ extern "C" int rf_attend_causal(const uint16_t* q, int64_t ldq, int64_t nq, cons
                                 int64_t row_stride, int64_t n_keys, float scale, uint16_t* out, int64_t ldo,
                                 void* workspace, size_t ws_bytes, hipStream_t stream) {
   if (!q || !kbuf || !vbuf || !out) return fail(RF_EINVAL_ARG, "rf_attend_causal: null pointer");
-  if (d != 64 && d != 128) return fail(RF_EUNSUPPORTED, "rf_attend_causal: head_dim %d (the kernel takes 64, 128)", d);
+  if (d != 64 && d != 128 && d != 256)
+    return fail(RF_EUNSUPPORTED, "rf_attend_causal: head_dim %d (the kernel takes 64, 128, 256)", d);
   if (!causal_shape_ok(hq, hkv, d))
-    return fail(RF_EUNSUPPORTED, "rf_attend_causal: %d query heads over %d K / V heads (group of 1, 2, 4 or 8)", hq,
-                hkv);
+    return fail(RF_EUNSUPPORTED, "rf_attend_causal: %d query heads over %d K / V heads (group of 1, 2, 4 or 8, or up "
+                "to 16 at head_dim 256)", hq, hkv);
   if (nq < 0 || nq > (1 << 30) || n_keys <= 0 || (!qpos && (slot0 < 0 || slot0 + nq > n_keys)))
     return fail(RF_EINVAL_SHAPE, "rf_attend_causal: queries at slots [%lld, %lld) past the %lld keys", (long long)slot0,
                 (long long)(slot0 + nq), (long long)n_keys);
@@ -527,7 +564,7 @@ extern "C" int rf_attend_causal(const uint16_t* q, int64_t ldq, int64_t nq, cons
   if (!(scale > 0.f) || !(scale < 1e30f)) return fail(RF_EINVAL_ARG, "rf_attend_causal: scale %g (must be positive)",
                                                       static_cast<double>(scale));
   if (nq == 0) return RF_OK;
-  const int64_t T = key_tiles(n_keys);
+  const int64_t T = key_tiles(n_keys, d);
   Splits sp = workspace ? causal_plan(nq, hq, hkv, d, n_keys, qpos != nullptr, slot0) : Splits{1, static_cast<int>(T)};
   while (sp.ns > 1 && ws_bytes < part_bytes(nq, hq, hkv, d, sp.ns)) {     // what the workspace holds
     --sp.ns;
@@ -536,16 +573,18 @@ extern "C" int rf_attend_causal(const uint16_t* q, int64_t ldq, int64_t nq, cons
   if (sp.ns == 1) sp.W = static_cast<int>(T);
   const int ns = sp.ns;
   CausalArgs a{q, ldq, static_cast<int>(nq), qpos, slot0, kbuf, head_stride, row_stride, n_keys, vbuf, hq, hkv,
-               scale * 1.4426950408889634f, out, ldo, static_cast<float*>(workspace), sp.W};
-  const dim3 grid(static_cast<unsigned>(query_blocks(nq, hq, hkv)), static_cast<unsigned>(hkv),
+               scale * 1.4426950408889634f, out, ldo, static_cast<float*>(workspace), sp.W, hpb_of(hq, hkv, d)};
+  const dim3 grid(static_cast<unsigned>(query_blocks(nq, hq, hkv, d)), static_cast<unsigned>(head_blocks(hq, hkv, d)),
                   static_cast<unsigned>(ns));
-  if (d == 128) hipLaunchKernelGGL(k_attend_causal<128>, grid, dim3(NTHR), 0, stream, a);
-  else hipLaunchKernelGGL(k_attend_causal<64>, grid, dim3(NTHR), 0, stream, a);
+  if (d == 256) hipLaunchKernelGGL(k_attend_causal<256>, grid, dim3(Cfg<256>::NTHR), 0, stream, a);
+  else if (d == 128) hipLaunchKernelGGL(k_attend_causal<128>, grid, dim3(Cfg<128>::NTHR), 0, stream, a);
+  else hipLaunchKernelGGL(k_attend_causal<64>, grid, dim3(Cfg<64>::NTHR), 0, stream, a);
   if (ns > 1) {
     const int st = check_launch("rf_attend_causal");
     if (st != RF_OK) return st;
-    const dim3 g2(grid.x, grid.y, static_cast<unsigned>(QROWS * d / 4 / 256));
-    if (d == 128) hipLaunchKernelGGL(k_causal_combine<128>, g2, dim3(256), 0, stream, a, ns);
+    const dim3 g2(grid.x, grid.y, static_cast<unsigned>(qrows_of(d) * d / 4 / 256));
+    if (d == 256) hipLaunchKernelGGL(k_causal_combine<256>, g2, dim3(256), 0, stream, a, ns);
+    else if (d == 128) hipLaunchKernelGGL(k_causal_combine<128>, g2, dim3(256), 0, stream, a, ns);
     else hipLaunchKernelGGL(k_causal_combine<64>, g2, dim3(256), 0, stream, a, ns);
   }
   return check_launch("rf_attend_causal");

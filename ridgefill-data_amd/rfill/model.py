@@ -574,7 +574,9 @@ class FillModel:
         return ws
 
     def _causal_ok(self):
-        return self.n_heads // self.n_kv in ops.CAUSAL_GROUPS and self.head_dim in (64, 128)
+        rep = self.n_heads // self.n_kv
+        return (self.head_dim in (64, 128) and rep in ops.CAUSAL_GROUPS) or (self.head_dim == 256
+                                                                           and rep in ops.CAUSAL_GROUPS_256)
 
     def logits(self, h, ssq=None):
         """F.linear(final_norm(h), lm_head).float() (code/kva/model.py:110-111): [rows, V] fp32 from bf16

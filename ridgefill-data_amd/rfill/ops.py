@@ -481,7 +481,8 @@ def attend_rows(q, qpos, kbuf, vbuf, n, hq, scale, out=None, workspace="auto"):
     return out
 
 
-CAUSAL_GROUPS = (1, 2, 4, 8)
+CAUSAL_GROUPS = (1, 2, 4, 8)            # query heads per K / V head rf_attend_causal takes at head_dim 64 / 128
+CAUSAL_GROUPS_256 = (1, 2, 4, 8, 16)    # and at head_dim 256
 
 
 def attend_causal_workspace_bytes(nq, hq, hkv, d, n):

@@ -169,9 +169,14 @@ def test_fill_late_runs_the_exact_rows_through_every_layer(dev):
                                                  (8, 8, 64, 700, 0, 700),             # group 1, from slot 0
                                                  (16, 2, 128, 333, 517, 1200),        # group 8, keys after
                                                  (4, 2, 64, 1000, 90, 1100),          # group 2, partial block
-                                                 (32, 8, 128, 64, 5, 69)])            # fewer keys than a tile pair
+                                                 (32, 8, 128, 64, 5, 69),             # fewer keys than a tile pair
+                                                 (16, 2, 256, 300, 1000, 1300),       # d 256, group 8: a tail
+                                                 (4, 4, 256, 200, 0, 200),            # d 256, group 1, slot 0
+                                                 (16, 1, 256, 100, 50, 400),          # d 256, group 16
+                                                 (16, 2, 256, 40, 5, 45)])            # d 256, one partial tile
 def test_attend_causal_matches_oracle(dev, hq, hkv, d, nq, slot0, n):
-    """The many-query kernel (rf_attend_causal: V transposed, 256 query rows per block) against the
+    """The many-query kernel (rf_attend_causal: V read transposed out of LDS, 256 query rows per block,
+    128 at head_dim 256) against the
     oracle's attend_at at positions slot0 .. slot0 + nq - 1 (attend itself when they are the last keys),
     and against rf_attend_rows on the same queries."""
     from rfill import ops
@@ -237,7 +242,7 @@ def test_attend_causal_refuses(dev):
 
 
 @pytest.mark.parametrize("hq,hkv,d,nq,n", [(32, 8, 128, 150, 6000), (16, 2, 128, 37, 3000), (4, 2, 64, 300, 2500),
-                                           (8, 8, 64, 5, 900)])
+                                           (8, 8, 64, 5, 900), (16, 2, 256, 150, 3000), (8, 2, 256, 37, 2000)])
 def test_attend_causal_at_positions(dev, hq, hkv, d, nq, n):
     """rf_attend_causal with sorted query positions (the exact rows' attention): with the key range split
     over blocks (full workspace) and unsplit (a workspace holding only V transposed), against the oracle's
