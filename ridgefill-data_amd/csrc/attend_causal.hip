@@ -57,6 +57,9 @@ struct Cfg {
   static constexpr int NTHR = 64 * NW;
   static constexpr int QROWS = 32 * NW;  // query rows (query, head) per block: 32 per wave
   static constexpr int KB = KT / 32;     // 32-key halves of a tile
+  // independent score chains per 32 keys: with one half per tile the d steps alternate between two
+  // accumulators (added at the end), so consecutive score MFMAs never wait on each other
+  static constexpr int CH = KB == 1 ? 2 : 1;
 };
 constexpr int NSTAGE = 4;              // LDS stages: three tiles in flight, one still read
 
@@ -196,15 +199,22 @@ template <int AD>
 __device__ __forceinline__ void tile_scores(const char* __restrict__ st, const bf16x8 (&qf)[AD / 16],
                                             f32x16 (&sc)[Cfg<AD>::KB], const FragOffsets<AD>& fo) {
   using L = Layout<AD>;
-  constexpr int NS = AD / 16, KB = Cfg<AD>::KB;
+  constexpr int NS = AD / 16, KB = Cfg<AD>::KB, CH = Cfg<AD>::CH;
+  f32x16 part[KB][CH];
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sc[kb][r] = 0.f;
+    for (int ch = 0; ch < CH; ++ch)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) part[kb][ch][r] = 0.f;
 #pragma unroll
     for (int s = 0; s < NS; ++s)
-      sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-          as_frag(*reinterpret_cast<const uint4*>(st + fo.ko[s] + kb * 32 * L::KCPR * 16)), qf[s], sc[kb], 0, 0, 0);
+      part[kb][s % CH] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          as_frag(*reinterpret_cast<const uint4*>(st + fo.ko[s] + kb * 32 * L::KCPR * 16)), qf[s], part[kb][s % CH],
+          0, 0, 0);
+    sc[kb] = part[kb][0];
+#pragma unroll
+    for (int ch = 1; ch < CH; ++ch) sc[kb] += part[kb][ch];
   }
 }
 
@@ -249,19 +259,24 @@ __device__ __forceinline__ void tile_step(const char* __restrict__ st, const cha
     lsum *= alpha;
   }
   const float mc = mref == -INFINITY ? 0.f : mref * c;  // every key so far masked (a split past the query)
-  // the next tile's KB NS score MFMAs, the NP probability pairs spread between them
+  // the next tile's KB NS score MFMAs (CH chains per 32 keys), the NP probability pairs spread between them
+  constexpr int CH = Cfg<AD>::CH;
   float psum = 0.f;
   uint32_t pk[NP];
+  f32x16 part[KB][CH];
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sn[kb][r] = 0.f;
+    for (int ch = 0; ch < CH; ++ch)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) part[kb][ch][r] = 0.f;
   }
 #pragma unroll
   for (int q = 0; q < KB * NS; ++q) {
     const int kb = q / NS, s = q % NS;
-    sn[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-        as_frag(*reinterpret_cast<const uint4*>(sn_st + fo.ko[s] + kb * 32 * L::KCPR * 16)), qf[s], sn[kb], 0, 0, 0);
+    part[kb][s % CH] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        as_frag(*reinterpret_cast<const uint4*>(sn_st + fo.ko[s] + kb * 32 * L::KCPR * 16)), qf[s], part[kb][s % CH],
+        0, 0, 0);
 #pragma unroll
     for (int e = q * NP / (KB * NS); e < (q + 1) * NP / (KB * NS); ++e) {
       const int pkb = e / 8, pj = 2 * (e % 8);
@@ -272,6 +287,12 @@ __device__ __forceinline__ void tile_step(const char* __restrict__ st, const cha
     }
   }
   lsum += psum;
+#pragma unroll
+  for (int kb = 0; kb < KB; ++kb) {
+    sn[kb] = part[kb][0];
+#pragma unroll
+    for (int ch = 1; ch < CH; ++ch) sn[kb] += part[kb][ch];
+  }
   // O^T[d, query] += V^T[d, keys] P^T[keys, query] over the tile's 16-key steps (keys 16 stp ..: chunks
   // 2 stp and 2 stp + 1; P^T step stp = the lane's probabilities 8 stp .. 8 stp + 7)
 #pragma unroll
