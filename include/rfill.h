@@ -217,15 +217,16 @@ int rf_attend_rows(const uint16_t* q, int64_t ldq, const int64_t* qpos, int64_t 
 int rf_attend_rows_workspace_bytes(int64_t nq, int hq, int hkv, int d, int64_t cache_rows, size_t* bytes);
 
 /* Causal attention of nq queries q [nq, hq d] over the first n_keys rows of kbuf / vbuf [hkv, cap, d]:
- * query j sees keys 0 .. qpos[j] (qpos: sorted int64 positions on the device), or, with qpos NULL,
+ * query j sees keys 0 .. qpos[j] (qpos: sorted int64 positions on the device; one past n_keys - 1 sees
+ * every key), or, with qpos NULL,
  * consecutive queries at slots slot0 .. slot0 + nq - 1 (slot0 + nq <= n_keys). Scores in fp32 scaled by
  * `scale`, softmax in fp32, probabilities as bf16 into the second product; writes out [nq, hq d] (row
  * stride ldo, 8-byte aligned). With slot0 = n_keys - nq this is the exact tail's attention in
  * Model.layer, ops.attend (code/kva/ops.py:107-128, code/kva/model.py:247-257); with qpos the exact
  * rows' attention in layer_rows, ops.attend_at / attend_rows (code/kva/ops.py:131-170), Qwen3.5's gated
  * attention included (code/kva/model.py:436-446; the gate multiplies the output afterwards). Needs d 64 or
- * 128 with hq / hkv in {1, 2, 4, 8}, or d 256 with hq / hkv in {1, 2, 4, 8, 16}. The workspace (caller-owned device memory, 16-byte aligned; may be NULL)
- * receives, when the query blocks are too few for the GPU, the partial results of a key-range split,
+ * 128 with hq / hkv in {1, 2, 4, 8}, or d 256 with hq / hkv in {1, 2, 4, 8, 16}. The workspace
+ * (caller-owned device memory, 16-byte aligned; may be NULL) receives, when the query blocks are too few for the GPU, the partial results of a key-range split,
  * merged in a fixed order: rf_attend_causal_workspace_bytes gives the size for the full split (a smaller
  * one gives fewer splits, NULL none). */
 int rf_attend_causal(const uint16_t* q, int64_t ldq, int64_t nq, const int64_t* qpos, int64_t slot0, int hq, int d,

@@ -1,9 +1,9 @@
 // Causal attention of many consecutive queries over one layer's K / V cache: the exact tail's
 // attention in Model.layer (code/kva/ops.py:107-128 attend, queries bottom-right aligned with the keys),
 // head_dim 64 or 128 with grouped-query heads in groups of 1, 2, 4 or 8, and head_dim 256 (Qwen3.5's gated
-// attention, code/kva/model.py:436-446) in groups of up to 16. The layout below is the d 64 / 128 one; at
-// d 256 a block has 4 waves (128 query rows: 32 queries of up to four heads of a group, the group's other
-// heads in further blocks), the key tiles are 32 keys, and each wave holds its 32 queries' 256-wide rows.
+// attention, code/kva/model.py:436-446) in groups of up to 16 (runs of eight heads per block, the group's
+// other heads in further blocks). The layout below is the d 64 / 128 one; at d 256 the key tiles are 32
+// keys and each wave holds its 32 queries' 256-wide rows.
 //
 // K and V tiles stream from the caches into LDS as full 128-byte lines with direct loads
 // (buffer_load_dwordx4 ... lds), both row-major ([key, d]); the V^T operand of the second product is read
@@ -47,19 +47,18 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-// Per head_dim: keys per tile KT and waves per block NW (32 query rows each). d 64 / 128: 64-key tiles,
-// 8 waves (two per SIMD). d 256: a wave's queries (64 registers), its O^T (128) and two tiles' scores
-// leave room for one wave per SIMD, so 4 waves, and 32-key tiles keep four 32 KB stages in LDS.
+// Per head_dim: keys per tile KT; 8 waves per block (two per SIMD), 32 query rows each. d 64 / 128:
+// 64-key tiles. d 256: 32-key tiles keep four 32 KB stages in LDS; a wave's queries take 64 registers and
+// its O^T 128 of the 256 two waves per SIMD leave it, so the tile loads' per-lane offsets are recomputed
+// at each issue instead of held, and a few values still spill (outside the key loop but for one query
+// fragment and the edge tiles' lane offset).
 template <int AD>
 struct Cfg {
   static constexpr int KT = AD == 256 ? 32 : 64;
-  static constexpr int NW = AD == 256 ? 4 : 8;
+  static constexpr int NW = 8;
   static constexpr int NTHR = 64 * NW;
   static constexpr int QROWS = 32 * NW;  // query rows (query, head) per block: 32 per wave
   static constexpr int KB = KT / 32;     // 32-key halves of a tile
-  // independent score chains per 32 keys: with one half per tile the d steps alternate between two
-  // accumulators (added at the end), so consecutive score MFMAs never wait on each other
-  static constexpr int CH = KB == 1 ? 2 : 1;
 };
 constexpr int NSTAGE = 4;              // LDS stages: three tiles in flight, one still read
 
@@ -154,25 +153,28 @@ __device__ __forceinline__ void issue_tile(__amdgpu_buffer_rsrc_t rk, __amdgpu_b
 constexpr float RESCALE_LOG2 = 8.0f;
 
 // Per-lane LDS byte offsets of the fragments within a stage, the same for every tile. K fragment (key
-// half kb, d step s): row 32 kb + n, chunk 2 s + hh, at ko[s] + kb * 32 KCPR 16 (row 32 kb + n has the
+// half kb, d step s): row 32 kb + n, chunk 2 s + hh, at k(s) + kb * 32 KCPR 16 (row 32 kb + n has the
 // swizzle of row n). V^T fragment (d block b, 16-key step stp): lane l = 16 g + t takes, in each of two
 // transpose reads, row 16 stp + 8 i + 4 (g / 2) + t / 4 (i = 0, 1) at d 32 b + 16 (g % 2) + 4 (t % 4)
 // (8 bytes), and receives keys 16 stp + 8 i + 4 (g / 2) + 0 .. 3 of d 32 b + 16 (g % 2) + t: the fragment
-// order {0..3, 8..11} + 4 hh. Its byte offset is vo + vb[b] + (16 stp + 8 i) KCPR 16 (rows 16 stp + 8 i + r
-// have the swizzle of row r).
+// order {0..3, 8..11} + 4 hh. Its byte offset is v(b) + (16 stp + 8 i) KCPR 16 (rows 16 stp + 8 i + r have
+// the swizzle of row r).
+// Both are one XOR per read: the K chunk 2 s + hh = 2 s ^ hh, so its swizzled byte offset within row n is
+// 32 s ^ 16 (hh ^ (n % KCPR)), and the row's base n KCPR 16 has no bits in common with it; the V^T block
+// offset 64 (b ^ vsw) = 64 b ^ 64 vsw sits in bits 6 .. 8, which the rest of the V offset leaves clear.
 template <int AD>
 struct FragOffsets {
-  uint32_t ko[AD / 16], vo, vb[AD / 32];
+  uint32_t kz, vz;
   __device__ FragOffsets(int lane) {
     using L = Layout<AD>;
     const int n = lane & 31, hh = lane >> 5, g = lane >> 4, t = lane & 15;
-#pragma unroll
-    for (int s = 0; s < AD / 16; ++s) ko[s] = static_cast<uint32_t>(L::kslot(n, 2 * s + hh) * 16);
+    kz = static_cast<uint32_t>(n * L::KCPR * 16) | static_cast<uint32_t>(16 * (hh ^ (n & (L::KCPR - 1))));
     const int r0 = 4 * (g >> 1) + (t >> 2), cl = 2 * (g & 1) + ((t & 3) >> 1);
-    vo = static_cast<uint32_t>((L::K_U4 + r0 * L::KCPR + cl) * 16 + 8 * (t & 1));
-#pragma unroll
-    for (int b = 0; b < AD / 32; ++b) vb[b] = static_cast<uint32_t>(4 * (b ^ L::vsw(r0)) * 16);
+    vz = static_cast<uint32_t>((L::K_U4 + r0 * L::KCPR + cl) * 16 + 8 * (t & 1)) |
+         static_cast<uint32_t>(64 * L::vsw(r0));
   }
+  __device__ uint32_t k(int s) const { return kz ^ static_cast<uint32_t>(32 * s); }
+  __device__ uint32_t v(int b) const { return vz ^ static_cast<uint32_t>(64 * b); }
 };
 
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -199,22 +201,15 @@ template <int AD>
 __device__ __forceinline__ void tile_scores(const char* __restrict__ st, const bf16x8 (&qf)[AD / 16],
                                             f32x16 (&sc)[Cfg<AD>::KB], const FragOffsets<AD>& fo) {
   using L = Layout<AD>;
-  constexpr int NS = AD / 16, KB = Cfg<AD>::KB, CH = Cfg<AD>::CH;
-  f32x16 part[KB][CH];
+  constexpr int NS = AD / 16, KB = Cfg<AD>::KB;
 #pragma unroll
   for (int kb = 0; kb < KB; ++kb) {
 #pragma unroll
-    for (int ch = 0; ch < CH; ++ch)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) part[kb][ch][r] = 0.f;
+    for (int r = 0; r < 16; ++r) sc[kb][r] = 0.f;
 #pragma unroll
     for (int s = 0; s < NS; ++s)
-      part[kb][s % CH] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-          as_frag(*reinterpret_cast<const uint4*>(st + fo.ko[s] + kb * 32 * L::KCPR * 16)), qf[s], part[kb][s % CH],
-          0, 0, 0);
-    sc[kb] = part[kb][0];
-#pragma unroll
-    for (int ch = 1; ch < CH; ++ch) sc[kb] += part[kb][ch];
+      sc[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+          as_frag(*reinterpret_cast<const uint4*>(st + fo.k(s) + kb * 32 * L::KCPR * 16)), qf[s], sc[kb], 0, 0, 0);
   }
 }
 
@@ -227,14 +222,14 @@ template <int AD>
 __device__ __forceinline__ void tile_step(const char* __restrict__ st, const char* __restrict__ sn_st,
                                           const bf16x8 (&qf)[AD / 16], f32x16 (&sc)[Cfg<AD>::KB],
                                           f32x16 (&sn)[Cfg<AD>::KB], f32x16 (&o)[AD / 32], float& mref, float& lsum,
-                                          int64_t k0, bool edge, int64_t mypos, int hh, float c,
+                                          int k0, bool edge, int mypos, int hh, float c,
                                           const FragOffsets<AD>& fo) {
   using L = Layout<AD>;
   constexpr int NB = AD / 32, NS = AD / 16, KB = Cfg<AD>::KB, KT = Cfg<AD>::KT;
   constexpr int NP = 8 * KB;                            // probability pairs per lane
   if (edge) {
     // key 32 kb + 8 (j / 4) + 4 hh + j % 4 of the tile is past the query when its offset exceeds rel
-    const int rel = static_cast<int>(min<int64_t>(max<int64_t>(mypos - k0, -1), KT)) - 4 * hh;
+    const int rel = min(max(mypos - k0, -1), KT) - 4 * hh;
 #pragma unroll
     for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
@@ -259,24 +254,18 @@ __device__ __forceinline__ void tile_step(const char* __restrict__ st, const cha
     lsum *= alpha;
   }
   const float mc = mref == -INFINITY ? 0.f : mref * c;  // every key so far masked (a split past the query)
-  // the next tile's KB NS score MFMAs (CH chains per 32 keys), the NP probability pairs spread between them
-  constexpr int CH = Cfg<AD>::CH;
+  // the next tile's KB NS score MFMAs, the NP probability pairs spread between them
   float psum = 0.f;
   uint32_t pk[NP];
-  f32x16 part[KB][CH];
 #pragma unroll
-  for (int kb = 0; kb < KB; ++kb) {
+  for (int kb = 0; kb < KB; ++kb)
 #pragma unroll
-    for (int ch = 0; ch < CH; ++ch)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) part[kb][ch][r] = 0.f;
-  }
+    for (int r = 0; r < 16; ++r) sn[kb][r] = 0.f;
 #pragma unroll
   for (int q = 0; q < KB * NS; ++q) {
     const int kb = q / NS, s = q % NS;
-    part[kb][s % CH] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
-        as_frag(*reinterpret_cast<const uint4*>(sn_st + fo.ko[s] + kb * 32 * L::KCPR * 16)), qf[s], part[kb][s % CH],
-        0, 0, 0);
+    sn[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+        as_frag(*reinterpret_cast<const uint4*>(sn_st + fo.k(s) + kb * 32 * L::KCPR * 16)), qf[s], sn[kb], 0, 0, 0);
 #pragma unroll
     for (int e = q * NP / (KB * NS); e < (q + 1) * NP / (KB * NS); ++e) {
       const int pkb = e / 8, pj = 2 * (e % 8);
@@ -287,12 +276,6 @@ __device__ __forceinline__ void tile_step(const char* __restrict__ st, const cha
     }
   }
   lsum += psum;
-#pragma unroll
-  for (int kb = 0; kb < KB; ++kb) {
-    sn[kb] = part[kb][0];
-#pragma unroll
-    for (int ch = 1; ch < CH; ++ch) sn[kb] += part[kb][ch];
-  }
   // O^T[d, query] += V^T[d, keys] P^T[keys, query] over the tile's 16-key steps (keys 16 stp ..: chunks
   // 2 stp and 2 stp + 1; P^T step stp = the lane's probabilities 8 stp .. 8 stp + 7)
 #pragma unroll
@@ -301,7 +284,7 @@ __device__ __forceinline__ void tile_step(const char* __restrict__ st, const cha
                                                              pk[4 * stp + 3]));
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
-      const char* vp = st + fo.vo + fo.vb[b] + 16 * stp * L::KCPR * 16;
+      const char* vp = st + fo.v(b) + 16 * stp * L::KCPR * 16;
       const uint2 vl = read_tr(vp), vh = read_tr(vp + 8 * L::KCPR * 16);
       o[b] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_frag(make_uint4(vl.x, vl.y, vh.x, vh.y)), pf, o[b], 0, 0, 0);
     }
@@ -339,8 +322,11 @@ __global__ __launch_bounds__(Cfg<AD>::NTHR, 1) void k_attend_causal(CausalArgs a
   const int jw0 = j0 + po0;
   const int jq = min(jw0 + n, jlast);
   const bool live = jw0 + n <= jlast;
-  const int64_t mypos = query_pos(a, jq);
-  const int64_t wave_first = query_pos(a, min(jw0, jlast)), wave_last = query_pos(a, min(jw0 + 31, jlast));
+  // positions as int, clamped to -1 .. n_keys - 1 (n_keys < 2^31: the caches' byte range is checked below
+  // 2^32): a query past the last key sees every key, one before key 0 none
+  auto clamp_pos = [&](int64_t p) { return static_cast<int>(min<int64_t>(max<int64_t>(p, -1), a.n_keys - 1)); };
+  const int mypos = clamp_pos(query_pos(a, jq));
+  const int wave_first = clamp_pos(query_pos(a, min(jw0, jlast))), wave_last = clamp_pos(query_pos(a, min(jw0 + 31, jlast)));
   const int head = hk * rep + hoff + hg;
   bf16x8 qf[NS];
   {
@@ -350,28 +336,45 @@ __global__ __launch_bounds__(Cfg<AD>::NTHR, 1) void k_attend_causal(CausalArgs a
   }
   wait_vm_lgkm0<0>();        // the queries are in registers before any tile load is in flight
 
-  // direct loads: instruction i of wave w fills 64 consecutive slots of a tile; lane L's slot
-  // determines the row and logical chunk it fetches
   const uint16_t* kh = a.kc + hk * a.head_stride;
   const __amdgpu_buffer_rsrc_t rk = buffer_rsrc(kh, static_cast<uint32_t>(a.n_keys * a.row_stride * 2));
   const __amdgpu_buffer_rsrc_t rv = buffer_rsrc(a.vc + hk * a.head_stride, static_cast<uint32_t>(a.n_keys * a.row_stride * 2));
-  uint32_t koff[L::KLOADS], voff[L::VLOADS];
-#pragma unroll
-  for (int i = 0; i < L::KLOADS; ++i) {
-    const int s = (w * L::KLOADS + i) * 64 + lane;
-    const int row = s / L::KCPR, pc = s % L::KCPR, c = pc ^ (row & (L::KCPR - 1));
-    koff[i] = static_cast<uint32_t>((row * a.row_stride + c * 8) * 2);
-  }
-#pragma unroll
-  for (int i = 0; i < L::VLOADS; ++i) {
-    const int s = (w * L::VLOADS + i) * 64 + lane;
-    const int row = s / L::KCPR, pc = s % L::KCPR, c = pc ^ (4 * L::vsw(row));
-    voff[i] = static_cast<uint32_t>((row * a.row_stride + c * 8) * 2);
-  }
   char* base = reinterpret_cast<char*>(lds);
+  const uint32_t rs2 = static_cast<uint32_t>(a.row_stride * 2);     // row bytes (the caches span < 2^32 bytes)
+  // lane ln's source offsets for the tile loads (instruction i of wave w fills 64 consecutive slots; the
+  // lane's slot gives the row and logical chunk it fetches)
+  auto offsets = [&](int ln, uint32_t (&koff)[L::KLOADS], uint32_t (&voff)[L::VLOADS]) {
+#pragma unroll
+    for (int i = 0; i < L::KLOADS; ++i) {
+      const int sl = (w * L::KLOADS + i) * 64 + ln;
+      const int row = sl / L::KCPR, pc = sl % L::KCPR, c = pc ^ (row & (L::KCPR - 1));
+      koff[i] = static_cast<uint32_t>(row) * rs2 + static_cast<uint32_t>(c * 16);
+    }
+#pragma unroll
+    for (int i = 0; i < L::VLOADS; ++i) {
+      const int sl = (w * L::VLOADS + i) * 64 + ln;
+      const int row = sl / L::KCPR, pc = sl % L::KCPR, c = pc ^ (4 * L::vsw(row));
+      voff[i] = static_cast<uint32_t>(row) * rs2 + static_cast<uint32_t>(c * 16);
+    }
+  };
+  // d 256 recomputes them at each issue rather than holding them across the loop (registers are the limit
+  // there): the lane index then comes from v_mbcnt in a volatile asm, which the compiler neither hoists
+  // nor keeps in a register
+  constexpr bool RECOMPUTE = AD == 256;
+  uint32_t koff0[L::KLOADS], voff0[L::VLOADS];
+  if constexpr (!RECOMPUTE) offsets(lane, koff0, voff0);
   auto issue = [&](int it) {
-    const uint32_t tb = static_cast<uint32_t>(static_cast<int64_t>(it) * KT * a.row_stride * 2);
-    issue_tile<AD>(rk, rv, koff, voff, base + ((it - it0) % NSTAGE) * L::STAGE_U4 * 16, tb, tb, w);
+    const uint32_t tb = static_cast<uint32_t>(it) * static_cast<uint32_t>(KT) * rs2;
+    char* st = base + ((it - it0) % NSTAGE) * L::STAGE_U4 * 16;
+    if constexpr (RECOMPUTE) {
+      int ln;
+      asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(ln));
+      uint32_t koff[L::KLOADS], voff[L::VLOADS];
+      offsets(ln, koff, voff);
+      issue_tile<AD>(rk, rv, koff, voff, st, tb, tb, w);
+    } else {
+      issue_tile<AD>(rk, rv, koff0, voff0, st, tb, tb, w);
+    }
   };
 
   f32x16 o[NB];
@@ -401,7 +404,7 @@ __global__ __launch_bounds__(Cfg<AD>::NTHR, 1) void k_attend_causal(CausalArgs a
     else wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();                         // every wave's share of it has landed and every
     if (it + 3 < it1) issue(it + 3);                      // wave is done with the stage reloaded here
-    const int64_t k0 = static_cast<int64_t>(it) * KT;
+    const int k0 = it * KT;
     if (k0 > wave_last) continue;                         // this and every later tile lie past the wave's queries
     tile_step<AD>(stage(it), stage(it + 1), qf, sc, sn, o, m, lsum, k0, k0 + KT - 1 > wave_first, mypos, hh, c, fo);
 #pragma unroll
@@ -541,7 +544,7 @@ Splits causal_plan(int64_t nq, int hq, int hkv, int d, int64_t n_keys, bool scat
 }
 
 // head_dim 64 / 128: groups of 1 .. 8 (a block holds every head of a group); 256: groups of 1 .. 16 (runs of
-// up to four heads per block)
+// up to eight heads per block)
 bool causal_shape_ok(int hq, int hkv, int d) {
   if ((d != 64 && d != 128 && d != 256) || hq <= 0 || hkv <= 0 || hq % hkv) return false;
   const int rep = hq / hkv;

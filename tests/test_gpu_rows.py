@@ -175,10 +175,9 @@ def test_fill_late_runs_the_exact_rows_through_every_layer(dev):
                                                  (16, 1, 256, 100, 50, 400),          # d 256, group 16
                                                  (16, 2, 256, 40, 5, 45)])            # d 256, one partial tile
 def test_attend_causal_matches_oracle(dev, hq, hkv, d, nq, slot0, n):
-    """The many-query kernel (rf_attend_causal: V read transposed out of LDS, 256 query rows per block,
-    128 at head_dim 256) against the
-    oracle's attend_at at positions slot0 .. slot0 + nq - 1 (attend itself when they are the last keys),
-    and against rf_attend_rows on the same queries."""
+    """The many-query kernel (rf_attend_causal: V read transposed out of LDS, 256 query rows per block)
+    against the oracle's attend_at at positions slot0 .. slot0 + nq - 1 (attend itself when they are the
+    last keys), and against rf_attend_rows on the same queries."""
     from rfill import ops
     q, k, v = _qkv(nq, hq, hkv, d, n, seed=nq + d)
     cap = n + 64
