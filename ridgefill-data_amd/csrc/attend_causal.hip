@@ -326,7 +326,9 @@ __global__ __launch_bounds__(Cfg<AD>::NTHR, 1) void k_attend_causal(CausalArgs a
   // 2^32): a query past the last key sees every key, one before key 0 none
   auto clamp_pos = [&](int64_t p) { return static_cast<int>(min<int64_t>(max<int64_t>(p, -1), a.n_keys - 1)); };
   const int mypos = clamp_pos(query_pos(a, jq));
-  const int wave_first = clamp_pos(query_pos(a, min(jw0, jlast))), wave_last = clamp_pos(query_pos(a, min(jw0 + 31, jlast)));
+  const int wave_first = clamp_pos(query_pos(a, min(jw0, jlast)));
+  // a wave whose queries all lie past the block's last one (a partial last query block) skips every tile
+  const int wave_last = jw0 <= jlast ? clamp_pos(query_pos(a, min(jw0 + 31, jlast))) : -1;
   const int head = hk * rep + hoff + hg;
   bf16x8 qf[NS];
   {
