@@ -401,16 +401,36 @@ __global__ __launch_bounds__(Cfg<AD>::NTHR, 1) void k_attend_causal(CausalArgs a
   else wait_vm_lgkm0<0>();
   __builtin_amdgcn_s_barrier();
   if (it0 < it1) tile_scores<AD>(stage(it0), qf, sc, fo);
-  for (int it = it0; it < it1; ++it) {
+  // iteration it: the scores of tile it are in cur, those of tile it + 1 go to nxt. At d 64 / 128 the loop
+  // runs two iterations per trip with the buffers' roles swapped, so no scores are copied (8B tail shape:
+  // 2041 -> 1924 us); at d 256 that version spills more and measured slower (2086 -> 2217 us), so there
+  // the next scores are copied back each iteration.
+  auto iteration = [&](int it, f32x16 (&cur)[KB], f32x16 (&nxt)[KB]) {
     if (it + 2 < it1) wait_vm_lgkm0<L::LOADS>();          // tile it + 1 landed, tile it + 2 may fly
     else wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();                         // every wave's share of it has landed and every
     if (it + 3 < it1) issue(it + 3);                      // wave is done with the stage reloaded here
     const int k0 = it * KT;
-    if (k0 > wave_last) continue;                         // this and every later tile lie past the wave's queries
-    tile_step<AD>(stage(it), stage(it + 1), qf, sc, sn, o, m, lsum, k0, k0 + KT - 1 > wave_first, mypos, hh, c, fo);
+    if (k0 > wave_last) return;                           // this and every later tile lie past the wave's queries
+    tile_step<AD>(stage(it), stage(it + 1), qf, cur, nxt, o, m, lsum, k0, k0 + KT - 1 > wave_first, mypos, hh, c, fo);
+  };
+  if constexpr (AD == 256) {
+    for (int it = it0; it < it1; ++it) {
+      if (it + 2 < it1) wait_vm_lgkm0<L::LOADS>();
+      else wait_vm_lgkm0<0>();
+      __builtin_amdgcn_s_barrier();
+      if (it + 3 < it1) issue(it + 3);
+      const int k0 = it * KT;
+      if (k0 > wave_last) continue;
+      tile_step<AD>(stage(it), stage(it + 1), qf, sc, sn, o, m, lsum, k0, k0 + KT - 1 > wave_first, mypos, hh, c, fo);
 #pragma unroll
-    for (int kb = 0; kb < KB; ++kb) sc[kb] = sn[kb];
+      for (int kb = 0; kb < KB; ++kb) sc[kb] = sn[kb];
+    }
+  } else {
+    for (int it = it0; it < it1; it += 2) {
+      iteration(it, sc, sn);
+      if (it + 1 < it1) iteration(it + 1, sn, sc);
+    }
   }
   wait_vm_lgkm0<0>();
 
