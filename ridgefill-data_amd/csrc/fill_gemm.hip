@@ -157,7 +157,8 @@ __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t
                    bf16x8 (&nw)[4], int ld, int lkt, int lo) {
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
-      acc[q >> 2][q & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aw[q >> 2], ax[q & 3], acc[q >> 2][q & 3], 0, 0, 0);
+      const int qi = q >> 2, qj = (qi & 1) ? 3 - (q & 3) : (q & 3);   // snake: one operand changes per MFMA
+      acc[qi][qj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aw[qi], ax[qj], acc[qi][qj], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
       if (q < 8 && rd) read_one(rkt, rks, q, nx, nw);
       if (ld == 2 && !(q & 1)) load(lkt, true, q >> 1);
@@ -1220,7 +1221,8 @@ __device__ __forceinline__ void stream_tiles(int cnt, int nk, int64_t ldx, int64
                    bf16x8 (&nw)[4], int ld, const TileOps& o, int lg, int lk2, int lo) {
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
-      acc[q >> 2][q & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aw[q >> 2], ax[q & 3], acc[q >> 2][q & 3], 0, 0, 0);
+      const int qi = q >> 2, qj = (qi & 1) ? 3 - (q & 3) : (q & 3);   // snake: one operand changes per MFMA
+      acc[qi][qj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aw[qi], ax[qj], acc[qi][qj], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
       if (q < 8 && rd) read_one(rg, rks, q, nx, nw);
       if (ld == 2 && !(q & 1)) load(o, lg, lk2, true, q >> 1);
