@@ -588,11 +588,12 @@ def hybrid_bench(dev, reps=12, split=24, n_rows=32768, tail=4096):
                                 "counted_flop_per_launch": P * (2 * 4 * C + 6 * nv * dk * dv)}}}
 
 
-def hybrid_finish_bench(dev, reps=2, split=24, n_rows=32768, tail=4096):
+def hybrid_finish_bench(dev, reps=5, split=24, n_rows=32768, tail=4096):
     """The hybrid's whole late stack as finish() runs it, without the logits: the fill of layers 24..47
     (P = 28672 rows), then the 4096-row exact tail through every late layer -- GDN layers continue the
     filled conv and recurrent states (in-projection, rf_gdn_forward with outputs, gated norm, out_proj,
-    MLP), attention layers attend over all 32768 keys with the output gate (head_dim 256)."""
+    MLP), attention layers attend over all 32768 keys with the output gate (head_dim 256). The fill and the
+    tail are each the median of `reps` runs after one warm-up run; every run's tail is reported."""
     from rfill import ops, synth
     from rfill.kva import Arm, Projector, fill_late
     from rfill.model import FillModel
@@ -621,15 +622,14 @@ def hybrid_finish_bench(dev, reps=2, split=24, n_rows=32768, tail=4096):
         return t1 - t0, time.perf_counter() - t1
 
     run()
-    tf = tt = 0.0
-    for _ in range(reps):
-        a, b = run()
-        tf += a / reps
-        tt += b / reps
+    runs = [run() for _ in range(reps)]
+    tf = statistics.median(r[0] for r in runs)
+    tt = statistics.median(r[1] for r in runs)
     return {"workload": f"qwen3.5-shaped hybrid late stack: fill of layers {split}..{cfg['num_hidden_layers'] - 1} "
                         f"({P} rows) + {tail}-row exact tail through every late layer (MLP 6144)",
             "prompt_tokens_per_s": round(n_rows / (tf + tt), 1), "ms_fill": round(tf * 1e3, 2),
-            "ms_tail": round(tt * 1e3, 2)}
+            "ms_tail": round(tt * 1e3, 2), "ms_tail_reps": [round(r[1] * 1e3, 2) for r in runs],
+            "timing": f"median of {reps} runs, host clock with a device synchronisation at each end"}
 
 
 def sweep_bench(dev, reps=2, split=18, tail=4096, frac=0.01, lengths=(16384, 32768, 65536, 122880)):
