@@ -1,9 +1,10 @@
 /* librfill -- MI355X (gfx950) kernels for the RidgeFill late-layer fill.
  *
  * A flat C ABI: plain device pointers, element counts and strides, and the HIP stream every call is
- * ordered on. Nothing here allocates device memory or keeps state between calls except the
- * thread-local error text. Every call returns RF_OK or a negative status and leaves a message for
- * rf_last_error(). Tensors are row-major; "bf16" buffers hold IEEE bfloat16 bit patterns (uint16_t).
+ * ordered on. Nothing here allocates device memory, and nothing keeps state between calls except the
+ * thread-local error text, the side stream and events rf_gdn_fill creates once per device, and
+ * rf_gdn_fill_noalloc's static device array. Every call returns RF_OK or a negative status and leaves a
+ * message for rf_last_error(). Tensors are row-major; "bf16" buffers hold IEEE bfloat16 bit patterns (uint16_t).
  *
  * Each entry point names the reference code it replaces (paths in the reference repository,
  * Approximate-Science/ridgefill-data).
