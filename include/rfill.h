@@ -246,9 +246,10 @@ int rf_residual_add(const uint16_t* x, int64_t ldx, const uint16_t* y, int64_t l
 
 /* out = bf16(res + bf16(x w^T)) for x [M, K] (row stride ldx), w [N, K], res [M, N] (row stride ldr), and
  * out's row sum-of-squares partials ssq [M, N / 256]: rf_map_apply without a bias followed by
- * rf_residual_add(res, out), bit-identical to that pair. When every row runs through the split-K sums (a
- * few rows with the workspace of rf_gemm_workspace_bytes(M, N, K)) the residual is added in the sums'
- * epilogue, one launch fewer. o_proj and down with their residuals (code/kva/model.py:112-118). */
+ * rf_residual_add(res, out), bit-identical to that pair, in one pass: the residual is added in the
+ * product's tile epilogue (K >= 128), or in the split sums' epilogue for rows that run through the
+ * split-K sums (a few rows with the workspace of rf_gemm_workspace_bytes(M, N, K)). K = 64 runs the pair.
+ * o_proj and down with their residuals (code/kva/model.py:112-118). */
 int rf_map_apply_residual(const uint16_t* x, int64_t ldx, const uint16_t* w, const uint16_t* res, int64_t ldr,
                           uint16_t* out, int64_t ldo, float* ssq, int64_t M, int64_t K, int64_t N, void* workspace,
                           size_t ws_bytes, hipStream_t stream);

@@ -1293,8 +1293,13 @@ struct MapLayers {
 
 // rf_map_apply on persistent tiles, for nl layers at once: x_l = b W_l^T + c_l, the accumulators starting
 // at the bias, and the rows' sum-of-squares partials; logical tile u is layer u / (tiles of a layer).
+// RES (one layer): x = bf16(res + bf16(b W^T + c)), rf_residual_add's rounding after the product's, the
+// statistics then being x's (a lane loads the residual of its 64 values of a round, the next round's
+// while the current one is written).
+template <bool RES = false>
 __global__ __launch_bounds__(NTHR) void k_map_apply_p(const uint16_t* __restrict__ B, int64_t ldb, MapLayers ml, int nl,
-                                                      int64_t ldx, int M, int N, int K) {
+                                                      int64_t ldx, int M, int N, int K,
+                                                      const uint16_t* __restrict__ res = nullptr, int64_t ldr = 0) {
   __shared__ uint4 lds[LDS_U4];
   const int tiles_n = N / BN, tiles_m = (M + BM - 1) / BM, per = tiles_m * tiles_n;
   const Share sh = block_share(nl * per);
@@ -1348,16 +1353,43 @@ __global__ __launch_bounds__(NTHR) void k_map_apply_p(const uint16_t* __restrict
     uint16_t* X = ml.x[l];
     float* S = ml.ssq[l];
     if (i + 1 < sh.cnt) load_bias(i + 1);
+    // the residual of round r's values of this lane: row wm*128 + r*32 + lr, columns wn*128 + nt*32 + 8g +
+    // 4lk .. + 3 (rows past M read row M - 1; they are not stored)
+    uint2 rq[2][4][4];
+    auto load_res = [&](int r, uint2 (&q)[4][4]) {
+      const int gm = min(m0 + wm * 128 + r * 32 + lr, M - 1);
+      const uint16_t* rr = res + static_cast<int64_t>(gm) * ldr + n0 + wn * 128 + 4 * lk;
+#pragma unroll
+      for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) q[nt][g] = *reinterpret_cast<const uint2*>(rr + nt * 32 + 8 * g);
+    };
+    if constexpr (RES) load_res(0, rq[0]);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       __builtin_amdgcn_sched_barrier(0);
       float ss = 0.f;
-      auto ident = [](int, int, int, float a) { return a; };
-      switch (r) {
-        case 0: stage_round<0, true>(img, acc, ident, ss, t); break;
-        case 1: stage_round<1, true>(img, acc, ident, ss, t); break;
-        case 2: stage_round<2, true>(img, acc, ident, ss, t); break;
-        default: stage_round<3, true>(img, acc, ident, ss, t); break;
+      if constexpr (RES) {
+        auto resv = [&](int nt, int g, int e, float a) {
+          const uint2 q = rq[r & 1][nt][g];
+          const uint32_t u = e < 2 ? q.x : q.y;
+          return ((e & 1) ? bf_hi(u) : bf_lo(u)) + bf2f(f2bf(a));
+        };
+        switch (r) {
+          case 0: stage_round<0, true>(img, acc, resv, ss, t); break;
+          case 1: stage_round<1, true>(img, acc, resv, ss, t); break;
+          case 2: stage_round<2, true>(img, acc, resv, ss, t); break;
+          default: stage_round<3, true>(img, acc, resv, ss, t); break;
+        }
+        if (r < 3) load_res(r + 1, rq[(r + 1) & 1]);
+      } else {
+        auto ident = [](int, int, int, float a) { return a; };
+        switch (r) {
+          case 0: stage_round<0, true>(img, acc, ident, ss, t); break;
+          case 1: stage_round<1, true>(img, acc, ident, ss, t); break;
+          case 2: stage_round<2, true>(img, acc, ident, ss, t); break;
+          default: stage_round<3, true>(img, acc, ident, ss, t); break;
+        }
       }
       const float tot = ss + __shfl_xor(ss, 32, 64);             // the row's 128 columns of this wave
       if (lk == 0) side[wn * 64 + wm * 32 + lr] = tot;
@@ -1374,6 +1406,9 @@ __global__ __launch_bounds__(NTHR) void k_map_apply_p(const uint16_t* __restrict
       }
       __syncthreads();
     }
+    // (RES: nothing of the residual loads stays in flight into the next tile's K loop, whose registers
+    // they share; without this wait the compiler guards that loop's fragment reads with vmcnt waits)
+    if constexpr (RES) wait_vm_lgkm0<0>();
   };
   load_bias(0);
   stream_tiles(sh.cnt, K / BK, ldb, K, ops, begin, [](int, uint4*) {}, end, lds);
@@ -1863,8 +1898,9 @@ extern "C" int rf_map_apply(const uint16_t* b, int64_t ldb, const uint16_t* w, c
     ml.c[0] = c;
     ml.x[0] = x;
     ml.ssq[0] = ssq;
-    hipLaunchKernelGGL(k_map_apply_p, dim3(persistent_grid(grid_of(mf, h_out))), dim3(NTHR), 0, stream, b, ldb, ml, 1,
-                       ldx, static_cast<int>(mf), static_cast<int>(h_out), static_cast<int>(h_in));
+    hipLaunchKernelGGL(k_map_apply_p<false>, dim3(persistent_grid(grid_of(mf, h_out))), dim3(NTHR), 0, stream, b, ldb,
+                       ml, 1, ldx, static_cast<int>(mf), static_cast<int>(h_out), static_cast<int>(h_in),
+                       static_cast<const uint16_t*>(nullptr), static_cast<int64_t>(0));
   } else if (mf > 0) {
     hipLaunchKernelGGL(k_map_apply, dim3(grid_of(mf, h_out)), dim3(NTHR), 0, stream, b, ldb, w, c, x, ldx, ssq,
                        static_cast<int>(mf), static_cast<int>(h_out), static_cast<int>(h_in));
@@ -1900,9 +1936,26 @@ extern "C" int rf_map_apply_residual(const uint16_t* x, int64_t ldx, const uint1
                        static_cast<int>(N), res, ldr);
     return check_launch(fn);
   }
-  const int rc = rf_map_apply(x, ldx, w, nullptr, out, ldo, ssq, M, K, N, workspace, ws_bytes, stream);
-  if (rc != RF_OK) return rc;
-  return rf_residual_add(res, ldr, out, ldo, out, ldo, ssq, M, N, stream);
+  const int64_t mf = pl.m_fused, rows = M - mf;
+  if (mf == 0 || K / BK < 2) {                     // no persistent tiles (K = 64): the product, then the residual
+    const int rc = rf_map_apply(x, ldx, w, nullptr, out, ldo, ssq, M, K, N, workspace, ws_bytes, stream);
+    if (rc != RF_OK) return rc;
+    return rf_residual_add(res, ldr, out, ldo, out, ldo, ssq, M, N, stream);
+  }
+  // the residual in the tiles' epilogue for rows [0, mf), in the split sums' epilogue for the rest
+  MapLayers ml{};
+  ml.w[0] = w;
+  ml.x[0] = out;
+  ml.ssq[0] = ssq;
+  hipLaunchKernelGGL(k_map_apply_p<true>, dim3(persistent_grid(grid_of(mf, N))), dim3(NTHR), 0, stream, x, ldx, ml, 1,
+                     ldo, static_cast<int>(mf), static_cast<int>(N), static_cast<int>(K), res, ldr);
+  if (pl.split()) {
+    launch_partials(x, ldx, w, K, M, N, K, pl, workspace, stream);
+    hipLaunchKernelGGL(k_map_apply_reduce, reduce_grid(rows, N), dim3(256), 0, stream,
+                       static_cast<const float*>(workspace), pl.splits, nullptr, out + mf * ldo, ldo,
+                       ssq + mf * (N / SSQ_COLS), static_cast<int>(rows), static_cast<int>(N), res + mf * ldr, ldr);
+  }
+  return check_launch(fn);
 }
 
 extern "C" int rf_norm_linear_swiglu(const uint16_t* x, int64_t ldx, const float* ssq, int64_t P, int64_t H, float eps,
@@ -2232,8 +2285,9 @@ extern "C" int rf_map_apply_batch(int nl, const uint16_t* b, int64_t ldb, const 
   }
   if (!aligned16(b)) return fail(RF_EINVAL_SHAPE, "rf_map_apply_batch: b must be 16-byte aligned");
   if (P == 0) return RF_OK;
-  hipLaunchKernelGGL(k_map_apply_p, dim3(persistent_grid(nl * static_cast<int64_t>(grid_of(P, h_out)))), dim3(NTHR), 0,
-                     stream, b, ldb, ml, nl, ldx, static_cast<int>(P), static_cast<int>(h_out), static_cast<int>(h_in));
+  hipLaunchKernelGGL(k_map_apply_p<false>, dim3(persistent_grid(nl * static_cast<int64_t>(grid_of(P, h_out)))),
+                     dim3(NTHR), 0, stream, b, ldb, ml, nl, ldx, static_cast<int>(P), static_cast<int>(h_out),
+                     static_cast<int>(h_in), static_cast<const uint16_t*>(nullptr), static_cast<int64_t>(0));
   return check_launch("rf_map_apply_batch");
 }
 
