@@ -76,15 +76,24 @@ __global__ __launch_bounds__(256) void k_mass_stats(MassArgs a) {
   const int kb = blockIdx.x, g = blockIdx.y;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, n = lane & 31, hh = lane >> 5;
   const int rep = a.hq / a.hkv, R = rep * a.w;
+  auto qload = [&](int rb, uint4 (&qv)[NS]) {     // row step rb's query fragments
+    const int r = rb * 32 + n, qh = r / a.w, qi = r - qh * a.w;
+    const uint16_t* qrow = a.q + static_cast<int64_t>(qi) * a.ldq + static_cast<int64_t>(g * rep + qh) * AD + 8 * hh;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qv[s] = *reinterpret_cast<const uint4*>(qrow + 16 * s);
+  };
+  // the first row step's queries load beside the key block, each later one during the step before it
+  uint4 qn[NS];
+  if (wv < R / 32) qload(wv, qn);
   load_keys<AD>(a, g, kb, ks);
   __syncthreads();
   const bool full = static_cast<int64_t>(kb + 1) * MKB - 1 <= a.pos0;   // every key visible to every row
   for (int rb = wv; rb < R / 32; rb += 4) {
-    const int r = rb * 32 + n, qh = r / a.w, qi = r - qh * a.w;
-    const uint16_t* qrow = a.q + static_cast<int64_t>(qi) * a.ldq + static_cast<int64_t>(g * rep + qh) * AD + 8 * hh;
+    const int r = rb * 32 + n, qi = r - (r / a.w) * a.w;
     bf16x8 qf[NS];
 #pragma unroll
-    for (int s = 0; s < NS; ++s) qf[s] = as_frag(*reinterpret_cast<const uint4*>(qrow + 16 * s));
+    for (int s = 0; s < NS; ++s) qf[s] = as_frag(qn[s]);
+    if (rb + 4 < R / 32) qload(rb + 4, qn);
     // the row's last visible key, relative to the block (32-bit): keys 0 .. rel of the block are visible
     const int rel = static_cast<int>(min<int64_t>(a.pos0 + qi - static_cast<int64_t>(kb) * MKB, MKB));
     // online maximum and sum over the 32-key steps: (mx, sum) of the lane's keys so far
@@ -171,6 +180,14 @@ __global__ __launch_bounds__(256) void k_mass_cols(MassArgs a) {
   const int kb = blockIdx.x, g = blockIdx.y;
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, n = lane & 31, hh = lane >> 5;
   const int rep = a.hq / a.hkv, R = rep * a.w;
+  auto qload = [&](int rb, uint4 (&qv)[NS]) {     // row step rb's query fragments
+    const int r = rb * 32 + n, qh = r / a.w, qi = r - qh * a.w;
+    const uint16_t* qrow = a.q + static_cast<int64_t>(qi) * a.ldq + static_cast<int64_t>(g * rep + qh) * AD + 8 * hh;
+#pragma unroll
+    for (int s = 0; s < NS; ++s) qv[s] = *reinterpret_cast<const uint4*>(qrow + 16 * s);
+  };
+  uint4 qn[NS];
+  qload(0, qn);                                   // the first row step's queries load beside the key block
   load_keys<AD>(a, g, kb, ks);
   for (int r = threadIdx.x; r < R; r += 256) {
     st[r] = a.stats[static_cast<int64_t>(g) * R + r];
@@ -191,14 +208,6 @@ __global__ __launch_bounds__(256) void k_mass_cols(MassArgs a) {
   }
   const int64_t key0 = static_cast<int64_t>(kb) * MKB + wv * 64 + n;
   float col[2] = {0.f, 0.f};
-  auto qload = [&](int rb, uint4 (&qv)[NS]) {     // row step rb's query fragments
-    const int r = rb * 32 + n, qh = r / a.w, qi = r - qh * a.w;
-    const uint16_t* qrow = a.q + static_cast<int64_t>(qi) * a.ldq + static_cast<int64_t>(g * rep + qh) * AD + 8 * hh;
-#pragma unroll
-    for (int s = 0; s < NS; ++s) qv[s] = *reinterpret_cast<const uint4*>(qrow + 16 * s);
-  };
-  uint4 qn[NS];
-  qload(0, qn);
   for (int rb = 0; rb < R / 32; ++rb) {          // 32-row steps, in order; the next step's queries in flight
     bf16x8 qf[NS];
 #pragma unroll
