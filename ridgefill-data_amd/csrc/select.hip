@@ -46,6 +46,7 @@ struct MassArgs {
   float2* part;             // [hkv][nkb][R]: (block max in base 2, block sum)
   float2* stats;            // [hkv][R]: (M, 1 / L)
   float* colsum;            // [hkv][nkb * MKB]
+  const uint4* qp;          // the queries in fragment order: [hkv][R / 32][AD / 16][64 lanes] (k_mass_qpack)
 };
 
 // The block's keys [kb * 256, +256) of head g into LDS as [256][AD] bf16, 16-byte chunk c of key row r at
@@ -69,6 +70,23 @@ __device__ __forceinline__ void load_keys(const MassArgs& a, int g, int kb, uint
   }
 }
 
+// The window queries in the order the score products read them: fragment (group g, row step rb, d step s)
+// is 64 lanes x 16 bytes, lane (n, hh) holding row rb * 32 + n's d values 16 s + 8 hh .. + 7, so that each
+// fragment load is one contiguous 1 KB instead of 32 rows' 32-byte pieces.
+template <int AD>
+__global__ __launch_bounds__(256) void k_mass_qpack(MassArgs a, uint4* __restrict__ qp) {
+  constexpr int NS = AD / 16;
+  const int rep = a.hq / a.hkv, R = rep * a.w;
+  const int64_t idx = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (idx >= static_cast<int64_t>(a.hkv) * (R / 32) * NS * 64) return;
+  const int lane = static_cast<int>(idx & 63), n = lane & 31, hh = lane >> 5;
+  const int64_t f = idx >> 6;
+  const int s = static_cast<int>(f % NS), rb = static_cast<int>((f / NS) % (R / 32)), g = static_cast<int>(f / NS / (R / 32));
+  const int r = rb * 32 + n, qh = r / a.w, qi = r - qh * a.w;
+  qp[idx] = *reinterpret_cast<const uint4*>(a.q + static_cast<int64_t>(qi) * a.ldq +
+                                            static_cast<int64_t>(g * rep + qh) * AD + 16 * s + 8 * hh);
+}
+
 template <int AD>
 __global__ __launch_bounds__(256) void k_mass_stats(MassArgs a) {
   constexpr int CPR = AD / 8, NS = AD / 16;
@@ -77,10 +95,9 @@ __global__ __launch_bounds__(256) void k_mass_stats(MassArgs a) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, n = lane & 31, hh = lane >> 5;
   const int rep = a.hq / a.hkv, R = rep * a.w;
   auto qload = [&](int rb, uint4 (&qv)[NS]) {     // row step rb's query fragments
-    const int r = rb * 32 + n, qh = r / a.w, qi = r - qh * a.w;
-    const uint16_t* qrow = a.q + static_cast<int64_t>(qi) * a.ldq + static_cast<int64_t>(g * rep + qh) * AD + 8 * hh;
+    const uint4* f = a.qp + (static_cast<int64_t>(g) * (R / 32) + rb) * NS * 64 + lane;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) qv[s] = *reinterpret_cast<const uint4*>(qrow + 16 * s);
+    for (int s = 0; s < NS; ++s) qv[s] = f[s * 64];
   };
   // the first row step's queries load beside the key block, each later one during the step before it
   uint4 qn[NS];
@@ -181,10 +198,9 @@ __global__ __launch_bounds__(256) void k_mass_cols(MassArgs a) {
   const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, n = lane & 31, hh = lane >> 5;
   const int rep = a.hq / a.hkv, R = rep * a.w;
   auto qload = [&](int rb, uint4 (&qv)[NS]) {     // row step rb's query fragments
-    const int r = rb * 32 + n, qh = r / a.w, qi = r - qh * a.w;
-    const uint16_t* qrow = a.q + static_cast<int64_t>(qi) * a.ldq + static_cast<int64_t>(g * rep + qh) * AD + 8 * hh;
+    const uint4* f = a.qp + (static_cast<int64_t>(g) * (R / 32) + rb) * NS * 64 + lane;
 #pragma unroll
-    for (int s = 0; s < NS; ++s) qv[s] = *reinterpret_cast<const uint4*>(qrow + 16 * s);
+    for (int s = 0; s < NS; ++s) qv[s] = f[s * 64];
   };
   uint4 qn[NS];
   qload(0, qn);                                   // the first row step's queries load beside the key block
@@ -259,11 +275,12 @@ __global__ __launch_bounds__(256) void k_mass_fold(const float* __restrict__ col
 
 int64_t mass_blocks(int64_t n_end) { return (n_end + MKB - 1) / MKB; }
 
-size_t mass_bytes(int w, int hq, int hkv, int64_t n_end) {
+// workspace: the row blocks' statistics, the rows' statistics, the column partials, the packed queries
+size_t mass_bytes(int w, int hq, int hkv, int d, int64_t n_end) {
   const int64_t R = static_cast<int64_t>(hq / hkv) * w, nkb = mass_blocks(n_end);
   const size_t part = static_cast<size_t>(hkv) * R * nkb * 8, stats = static_cast<size_t>(hkv) * R * 8,
-               cols = static_cast<size_t>(hkv) * nkb * MKB * 4;
-  return (part + 255) / 256 * 256 + (stats + 255) / 256 * 256 + cols;
+               cols = static_cast<size_t>(hkv) * nkb * MKB * 4, qp = static_cast<size_t>(hkv) * R * d * 2;
+  return (part + 255) / 256 * 256 + (stats + 255) / 256 * 256 + (cols + 255) / 256 * 256 + qp;
 }
 
 int mass_shape(const char* fn, int w, int hq, int hkv, int d) {
@@ -283,7 +300,7 @@ using namespace rf;
 extern "C" int rf_window_mass_workspace_bytes(int w, int hq, int hkv, int d, int64_t n_end, size_t* bytes) {
   if (!bytes || n_end <= 0) return fail(RF_EINVAL_ARG, "rf_window_mass_workspace_bytes: arguments");
   if (const int e = mass_shape("rf_window_mass_workspace_bytes", w, hq, hkv, d)) return e;
-  *bytes = mass_bytes(w, hq, hkv, n_end);
+  *bytes = mass_bytes(w, hq, hkv, d, n_end);
   return RF_OK;
 }
 
@@ -301,16 +318,25 @@ extern "C" int rf_window_mass(const uint16_t* q, int64_t ldq, int w, int64_t pos
     return fail(RF_EINVAL_SHAPE, "rf_window_mass: alignment");
   if (!(scale > 0.f) || !(scale < 1e30f))
     return fail(RF_EINVAL_ARG, "rf_window_mass: scale %g (must be positive)", static_cast<double>(scale));
-  const size_t need = mass_bytes(w, hq, hkv, n_end);
+  const size_t need = mass_bytes(w, hq, hkv, d, n_end);
   if (ws_bytes < need) return fail(RF_EINVAL_SHAPE, "rf_window_mass: workspace %zu bytes < %zu", ws_bytes, need);
   const int64_t nkb = mass_blocks(n_end), R = static_cast<int64_t>(hq / hkv) * w;
   if (nkb > (1 << 20)) return fail(RF_EINVAL_SHAPE, "rf_window_mass: %lld keys", (long long)n_end);
   char* ws = static_cast<char*>(workspace);
-  const size_t part = static_cast<size_t>(hkv) * R * nkb * 8, stats = static_cast<size_t>(hkv) * R * 8;
+  const size_t part = static_cast<size_t>(hkv) * R * nkb * 8, stats = static_cast<size_t>(hkv) * R * 8,
+               cols = static_cast<size_t>(hkv) * nkb * MKB * 4;
+  const size_t o_stats = (part + 255) / 256 * 256, o_cols = o_stats + (stats + 255) / 256 * 256,
+               o_qp = o_cols + (cols + 255) / 256 * 256;
+  uint4* qp = reinterpret_cast<uint4*>(ws + o_qp);
   MassArgs a{q, ldq, w, pos0, kbuf, head_stride, row_stride, n_end, hq, hkv, static_cast<int>(nkb),
-             scale * 1.4426950408889634f, reinterpret_cast<float2*>(ws),
-             reinterpret_cast<float2*>(ws + (part + 255) / 256 * 256),
-             reinterpret_cast<float*>(ws + (part + 255) / 256 * 256 + (stats + 255) / 256 * 256)};
+             scale * 1.4426950408889634f, reinterpret_cast<float2*>(ws), reinterpret_cast<float2*>(ws + o_stats),
+             reinterpret_cast<float*>(ws + o_cols), qp};
+  const int64_t nq4 = static_cast<int64_t>(hkv) * R * d / 8;       // 16-byte pieces of the packed queries
+  const dim3 qgrid(static_cast<unsigned>((nq4 + 255) / 256));
+  if (d == 256) hipLaunchKernelGGL(k_mass_qpack<256>, qgrid, dim3(256), 0, stream, a, qp);
+  else if (d == 128) hipLaunchKernelGGL(k_mass_qpack<128>, qgrid, dim3(256), 0, stream, a, qp);
+  else hipLaunchKernelGGL(k_mass_qpack<64>, qgrid, dim3(256), 0, stream, a, qp);
+  if (const int e = check_launch("rf_window_mass (queries)")) return e;
   const dim3 grid(static_cast<unsigned>(nkb), static_cast<unsigned>(hkv));
   if (d == 256) hipLaunchKernelGGL(k_mass_stats<256>, grid, dim3(256), 0, stream, a);
   else if (d == 128) hipLaunchKernelGGL(k_mass_stats<128>, grid, dim3(256), 0, stream, a);
