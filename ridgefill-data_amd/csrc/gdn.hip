@@ -30,6 +30,7 @@
 // k_gdn_out (chunk x value head) forms the outputs for all chunks in parallel on fp32 MFMA.
 #include <algorithm>
 #include <mutex>
+#include <type_traits>
 
 #include "rf_common.h"
 
@@ -689,8 +690,12 @@ constexpr int SST = DV + 4;                        // fp32 row stride of S and Y
 // accumulators rotated through v_accvgpr moves at the loop head, the first read 6 wait states after an
 // 8-pass MFMA. The shape used compiles fully unrolled: 768 MFMAs, no v_accvgpr moves or writes, and at
 // least 10 wait states between an MFMA and the first read of its result. The wave index is made
-// wave-uniform (an SGPR), which changes only the address arithmetic. The outputs are checked against
-// the oracle's chunked rule at the hybrid's widths, and any change here must be rechecked on the GPU.
+// wave-uniform (an SGPR), which changes only the address arithmetic. Each product loads all its A values
+// first and reads the next k-step's B values from LDS before the current step's MFMAs (a scheduling
+// barrier keeps that order; left to itself the compiler read each pair of B values just before its two
+// MFMAs and waited on LDS before each pair). The code keeps those properties (768 MFMAs, no v_accvgpr
+// moves, at least 10 wait states). The outputs are checked against the oracle's chunked rule at the
+// hybrid's widths, and any change here must be rechecked on the GPU.
 __global__ __launch_bounds__(256) void k_gdn_out(OutArgs a) {
   __shared__ __align__(16) float s_l[DK * SST];
   __shared__ __align__(16) float y_l[CH * SST];
@@ -714,14 +719,34 @@ __global__ __launch_bounds__(256) void k_gdn_out(OutArgs a) {
   __syncthreads();
   const int r0 = 16 * w;
   f32x4 acc[8];
+  // acc += A B over NKS 4-deep k-steps: A from a_of(ks) (this lane's row r0 + lr, k 4 ks + lk), B from the
+  // LDS rows bl (row 4 ks + lk, column 16 nt + lr), the next k-step's B values read before this step's MFMAs
+  auto product = [&](auto a_of, const float* bl, auto nks_c) {
+    constexpr int NKS = decltype(nks_c)::value;
+    float avs[NKS];                                 // every A value of the product in flight at once
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) avs[ks] = a_of(ks);
+    float bv[2][8];
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) bv[0][nt] = bl[lk * SST + 16 * nt + lr];
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+      const float av = avs[ks];
+      if (ks + 1 < NKS) {
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) bv[(ks + 1) & 1][nt] = bl[(4 * (ks + 1) + lk) * SST + 16 * nt + lr];
+      }
+      __builtin_amdgcn_sched_barrier(0);            // (the reads stay ahead of this step's MFMAs)
+#pragma unroll
+      for (int nt = 0; nt < 8; ++nt)
+        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv[ks & 1][nt], acc[nt], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int ks = 0; ks < DK / 4; ++ks) {             // X = K S
-    const float av = bf2f(K[(r0 + lr) * DK + 4 * ks + lk]);
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt)
-      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, s_l[(4 * ks + lk) * SST + 16 * nt + lr], acc[nt], 0, 0, 0);
-  }
+  product([&](int ks) { return bf2f(K[(r0 + lr) * DK + 4 * ks + lk]); }, s_l,     // X = K S
+          std::integral_constant<int, DK / 4>{});
 #pragma unroll
   for (int r = 0; r < 4; ++r) {                     // Y = beta (V - q X)
     const int i = r0 + 4 * lk + r;
@@ -735,12 +760,8 @@ __global__ __launch_bounds__(256) void k_gdn_out(OutArgs a) {
   __syncthreads();
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int ks = 0; ks < CH / 4; ++ks) {             // v_new = T Y
-    const float av = T[(r0 + lr) * CH + 4 * ks + lk];
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt)
-      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, y_l[(4 * ks + lk) * SST + 16 * nt + lr], acc[nt], 0, 0, 0);
-  }
+  product([&](int ks) { return T[(r0 + lr) * CH + 4 * ks + lk]; }, y_l,            // v_new = T Y
+          std::integral_constant<int, CH / 4>{});
   __syncthreads();                                  // every wave has read Y
 #pragma unroll
   for (int r = 0; r < 4; ++r)
@@ -749,18 +770,10 @@ __global__ __launch_bounds__(256) void k_gdn_out(OutArgs a) {
   __syncthreads();
 #pragma unroll
   for (int nt = 0; nt < 8; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  for (int ks = 0; ks < DK / 4; ++ks) {             // O = Qd S ...
-    const float av = Qd[(r0 + lr) * DK + 4 * ks + lk];
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt)
-      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, s_l[(4 * ks + lk) * SST + 16 * nt + lr], acc[nt], 0, 0, 0);
-  }
-  for (int ks = 0; ks < CH / 4; ++ks) {             // ... + P v_new
-    const float av = Pm[(r0 + lr) * CH + 4 * ks + lk];
-#pragma unroll
-    for (int nt = 0; nt < 8; ++nt)
-      acc[nt] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, y_l[(4 * ks + lk) * SST + 16 * nt + lr], acc[nt], 0, 0, 0);
-  }
+  product([&](int ks) { return Qd[(r0 + lr) * DK + 4 * ks + lk]; }, s_l,           // O = Qd S ...
+          std::integral_constant<int, DK / 4>{});
+  product([&](int ks) { return Pm[(r0 + lr) * CH + 4 * ks + lk]; }, y_l,           // ... + P v_new
+          std::integral_constant<int, CH / 4>{});
   const int64_t p0 = a.p_begin + static_cast<int64_t>(c) * CH;
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
