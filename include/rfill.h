@@ -408,9 +408,19 @@ int rf_mfma_ceiling(int blocks, int iters, float* out, hipStream_t stream);
  * accumulator C (row stride ldc) as it ends. With A = X^T and B = X^T or Y^T of sample rows and fold_rows
  * the block, this is RidgeStats' per-block fp32 GEMM into fp64 (code/kva/ridge.py:47, :62) over many
  * blocks in one launch (runs start at K offsets 0, fold_rows, 2 fold_rows, ...). Needs N % 256 == 0,
- * K % 64 == 0 (pad samples with zero rows), lda / ldb % 8 == 0, ldc even. */
+ * K % 64 == 0 (pad samples with zero rows), lda / ldb % 8 == 0, ldc even.
+ * The 256 x 256 output tiles run one per workgroup. When they are slightly more than one round of the
+ * GPU's 256 CUs (centred channels add a tile row or column to a 4096-wide product), a workspace of
+ * rf_gram_workspace_bytes lets the launch cut the tiles past the first 256 into their runs, which take
+ * one short extra round instead of a second round of whole tiles; their fp32 run sums go to the
+ * workspace and a second kernel adds them into C in run order. The result is bit-identical either way;
+ * workspace NULL or smaller than needed: every tile whole. */
 int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t M, int64_t N,
-                       int64_t K, int64_t fold_rows, double* c, int64_t ldc, hipStream_t stream);
+                       int64_t K, int64_t fold_rows, double* c, int64_t ldc, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes of rf_gram_accumulate's run-split schedule for this shape (0: it uses none). */
+int rf_gram_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t fold_rows, size_t* bytes);
 
 /* Held-out read cosine of one late layer for one document (code/scripts/fit_sweep.py:307-313): pred and
  * truth are [rows, >= (na + nb) d] bf16 reads, each row na vectors of group a then nb vectors of group b,

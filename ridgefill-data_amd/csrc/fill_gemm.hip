@@ -1025,23 +1025,104 @@ __device__ __forceinline__ void fold_tile(const f32x16 (&acc)[4][4], uint4* lds,
   }
 }
 
+// Writes a run's fp32 sums (acc) of one tile as a row-major [256, 256] fp32 plane, through the LDS image of
+// fold_tile (half the tile at a time), so that each wave instruction stores 1 KB of one row. Needs the LDS
+// free on entry; leaves it free.
+__device__ __forceinline__ void store_tile(const f32x16 (&acc)[4][4], uint4* lds, float* __restrict__ out) {
+  const int t = threadIdx.x, lane = t & 63;
+  const int w = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = w >> 1, wn = w & 1, lr = lane & 31, lk = lane >> 5;
+  float4* img = reinterpret_cast<float4*>(lds);
+#pragma unroll
+  for (int h = 0; h < 2; ++h) {
+    if (wm == h) {
+#pragma unroll
+      for (int mt = 0; mt < 4; ++mt)
+#pragma unroll
+        for (int nt = 0; nt < 4; ++nt)
+#pragma unroll
+          for (int g = 0; g < 4; ++g) {
+            const int r = mt * 32 + lr, c = wn * 32 + nt * 8 + 2 * g + lk;
+            img[r * 64 + (c ^ (r & 15))] = make_float4(acc[nt][mt][4 * g], acc[nt][mt][4 * g + 1],
+                                                       acc[nt][mt][4 * g + 2], acc[nt][mt][4 * g + 3]);
+          }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {                // wave w: image rows 32 w .. 32 w + 31
+      const int j = w * 32 + i;
+      *reinterpret_cast<float4*>(out + static_cast<int64_t>(h * 128 + j) * BN + 4 * lane) =
+          img[j * 64 + (lane ^ (j & 15))];
+    }
+    __syncthreads();
+  }
+}
+
+// The schedule of a Gram launch. Logical tiles [0, T - ptiles) run whole, one block each: their runs are
+// added into C as they end (fold_tile). The last ptiles logical tiles are cut into their runs, one block
+// per (tile, run), each writing its run's fp32 sums to part ([ptiles * runs][256][256], run order within a
+// tile); k_gram_fold then adds each tile's runs into C in run order. Same sums, same order: the two
+// schedules give the same bits. The run blocks come first in the grid (pieces of them, a multiple of 8, so
+// the whole tiles keep their XCD placement), which spreads a launch of slightly more tiles than CUs over
+// one round of whole tiles and a short round of runs instead of two rounds of whole tiles.
+struct GramPlan {
+  int pieces;             // grid blocks before the whole tiles (>= ptiles * runs, a multiple of 8)
+  int ptiles, runs;
+  float* part;
+};
+
 // C[m, n] += sum_k A[m, k] B[n, k]: bf16 products summed in fp32 over runs of at most `fold` of K, each run's
-// sums added into the fp64 accumulator C as it ends (fold_tile). Each tile owns its 256 x 256 block of C, so
-// the read-modify-write is race-free and the result does not depend on the schedule.
+// sums added into the fp64 accumulator C as it ends (fold_tile), or stored for k_gram_fold (GramPlan). Each
+// tile owns its 256 x 256 block of C, so the read-modify-write is race-free and the result does not depend
+// on the schedule.
 __global__ __launch_bounds__(NTHR) void k_gram(const uint16_t* __restrict__ A, int64_t lda,
                                                const uint16_t* __restrict__ B, int64_t ldb, int M, int N, int K,
-                                               int fold, double* __restrict__ C, int64_t ldc) {
+                                               int fold, double* __restrict__ C, int64_t ldc, GramPlan pl) {
   __shared__ uint4 lds[LDS_U4];
-  const int tiles_n = N / BN;
+  const int tiles_m = (M + BM - 1) / BM, tiles_n = N / BN;
+  const int whole = static_cast<int>(gridDim.x) - pl.pieces;
   int tm, tn;
-  tile_coords(xcd_tile(blockIdx.x, gridDim.x), (M + BM - 1) / BM, tiles_n, tm, tn);
-  const int m0 = tm * BM, n0 = tn * BN;
   f32x16 acc[4][4];
+  if (static_cast<int>(blockIdx.x) < pl.pieces) {
+    const int p = blockIdx.x, t = p / pl.runs, run = p - t * pl.runs;
+    if (t >= pl.ptiles) return;                     // padding block (block-uniform; no barrier reached)
+    tile_coords(whole + t, tiles_m, tiles_n, tm, tn);
+    const int k0 = run * fold, k1 = min(k0 + fold, K);
+    mainloop(A + k0, lda, B + k0, ldb, M, k1 - k0, tm * BM, tn * BN, lds, acc);
+    store_tile(acc, lds, pl.part + static_cast<int64_t>(p) * BM * BN);
+    return;
+  }
+  tile_coords(xcd_tile(blockIdx.x - pl.pieces, whole), tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
   for (int k0 = 0; k0 < K; k0 += fold) {
     const int k1 = min(k0 + fold, K);
     mainloop(A + k0, lda, B + k0, ldb, M, k1 - k0, m0, n0, lds, acc);
     fold_tile(acc, lds, C, ldc, M, m0, n0);
   }
+}
+
+// C += the stored runs of the last ptiles logical tiles (GramPlan), each tile's runs in run order: block =
+// 4 rows of one tile, thread = 4 consecutive columns (whole 1 KB rows of the planes, 2 KB rows of C).
+__global__ __launch_bounds__(256) void k_gram_fold(const float* __restrict__ part, int ptiles, int runs, int whole,
+                                                   int M, int N, double* __restrict__ C, int64_t ldc) {
+  const int t = blockIdx.x >> 6, row = (blockIdx.x & 63) * 4 + (threadIdx.x >> 6), c4 = threadIdx.x & 63;
+  if (t >= ptiles) return;
+  int tm, tn;
+  tile_coords(whole + t, (M + BM - 1) / BM, N / BN, tm, tn);
+  const int gm = tm * BM + row;
+  if (gm >= M) return;
+  double* p = C + static_cast<int64_t>(gm) * ldc + tn * BN + 4 * c4;
+  double2 v0 = *reinterpret_cast<const double2*>(p), v1 = *reinterpret_cast<const double2*>(p + 2);
+  const float* q = part + (static_cast<int64_t>(t) * runs * BM + row) * BN + 4 * c4;
+  for (int r = 0; r < runs; ++r) {
+    const float4 a = *reinterpret_cast<const float4*>(q + static_cast<int64_t>(r) * BM * BN);
+    v0.x += a.x;
+    v0.y += a.y;
+    v1.x += a.z;
+    v1.y += a.w;
+  }
+  *reinterpret_cast<double2*>(p) = v0;
+  *reinterpret_cast<double2*>(p + 2) = v1;
 }
 
 // The MFMA throughput the power budget allows: back-to-back v_mfma_f32_32x32x16_bf16 on register operands,
@@ -2199,9 +2280,32 @@ extern "C" int rf_mfma_ceiling(int blocks, int iters, float* out, hipStream_t st
   return check_launch("rf_mfma_ceiling");
 }
 
+// The run-split schedule of a Gram launch (GramPlan): used when the tiles take more than one round of CUs but
+// at most two, and their split-off runs fit in two rounds; ptiles = 0 otherwise.
+struct GramShape {
+  int64_t tiles, runs, ptiles;
+};
+static GramShape gram_shape(int64_t M, int64_t N, int64_t K, int64_t fold_rows) {
+  const int64_t fold = (fold_rows == 0 || fold_rows > K) ? K : fold_rows;
+  GramShape g{((M + BM - 1) / BM) * (N / BN), (K + fold - 1) / fold, 0};
+  const int64_t ncu = 256;
+  if (g.tiles > ncu && g.tiles < 2 * ncu && g.runs >= 2 && (g.tiles - ncu) * g.runs <= 2 * ncu)
+    g.ptiles = g.tiles - ncu;
+  return g;
+}
+
+extern "C" int rf_gram_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t fold_rows, size_t* bytes) {
+  if (!bytes || M < 0 || M > (1 << 30) || N <= 0 || N % BN || K <= 0 || K % 64 || fold_rows < 0 || fold_rows % 64)
+    return fail(RF_EINVAL_ARG, "rf_gram_workspace_bytes: M %lld, N %lld (multiple of 256), K %lld, fold_rows %lld",
+                (long long)M, (long long)N, (long long)K, (long long)fold_rows);
+  const GramShape g = gram_shape(M, N, K, fold_rows);
+  *bytes = static_cast<size_t>(g.ptiles * g.runs) * BM * BN * sizeof(float);
+  return RF_OK;
+}
+
 extern "C" int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t M,
-                                  int64_t N, int64_t K, int64_t fold_rows, double* c, int64_t ldc,
-                                  hipStream_t stream) {
+                                  int64_t N, int64_t K, int64_t fold_rows, double* c, int64_t ldc, void* workspace,
+                                  size_t workspace_bytes, hipStream_t stream) {
   if (!a || !b || !c) return fail(RF_EINVAL_ARG, "rf_gram_accumulate: null pointer");
   if (M < 0 || M > (1 << 30) || N <= 0 || N % BN || K <= 0 || K % 64)
     return fail(RF_EINVAL_SHAPE, "rf_gram_accumulate: M %lld, N %lld (multiple of 256), K %lld (multiple of 64)",
@@ -2215,8 +2319,23 @@ extern "C" int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t
     return fail(RF_EINVAL_ARG, "rf_gram_accumulate: fold_rows %lld (0 or a multiple of 64)", (long long)fold_rows);
   if (M == 0) return RF_OK;
   const int64_t fold = (fold_rows == 0 || fold_rows > K) ? K : fold_rows;
-  hipLaunchKernelGGL(k_gram, dim3(grid_of(M, N)), dim3(NTHR), 0, stream, a, lda, b, ldb, static_cast<int>(M),
-                     static_cast<int>(N), static_cast<int>(K), static_cast<int>(fold), c, ldc);
+  const GramShape g = gram_shape(M, N, K, fold_rows);
+  const size_t need = static_cast<size_t>(g.ptiles * g.runs) * BM * BN * sizeof(float);
+  GramPlan pl{0, 0, 1, nullptr};
+  if (g.ptiles > 0 && workspace && workspace_bytes >= need) {     // else every tile whole (same bits)
+    if (!aligned16(workspace)) return fail(RF_EINVAL_ARG, "rf_gram_accumulate: workspace must be 16-byte aligned");
+    pl = GramPlan{static_cast<int>((g.ptiles * g.runs + 7) / 8 * 8), static_cast<int>(g.ptiles),
+                  static_cast<int>(g.runs), static_cast<float*>(workspace)};
+  }
+  const int grid = static_cast<int>(g.tiles - pl.ptiles) + pl.pieces;
+  hipLaunchKernelGGL(k_gram, dim3(grid), dim3(NTHR), 0, stream, a, lda, b, ldb, static_cast<int>(M),
+                     static_cast<int>(N), static_cast<int>(K), static_cast<int>(fold), c, ldc, pl);
+  if (pl.ptiles > 0) {
+    const int rc = check_launch("rf_gram_accumulate");
+    if (rc != RF_OK) return rc;
+    hipLaunchKernelGGL(k_gram_fold, dim3(pl.ptiles * 64), dim3(256), 0, stream, pl.part, pl.ptiles, pl.runs,
+                       static_cast<int>(g.tiles - pl.ptiles), static_cast<int>(M), static_cast<int>(N), c, ldc);
+  }
   return check_launch("rf_gram_accumulate");
 }
 

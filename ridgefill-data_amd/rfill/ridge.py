@@ -23,6 +23,8 @@ recursion on its Schur complements, every product on fp64 MFMA, all lambdas and 
 same closed form the reference's eigendecomposition gives, since C + lam s I is symmetric positive definite
 for lam > 0).
 """
+import ctypes
+
 import torch
 
 from . import _lib
@@ -66,9 +68,18 @@ def _colsum_fold(partial, sums):
     _lib.call("rf_colsum_fold", _ptr(partial), partial.shape[0], partial.shape[1], _ptr(sums), _stream(sums))
 
 
-def gram_accumulate(a, b, c, fold_rows=0):
+def gram_workspace_bytes(M, N, K, fold_rows=0):
+    """Bytes of rf_gram_accumulate's run-split workspace for this shape (0: it uses none)."""
+    nb = ctypes.c_size_t(0)
+    _lib.call("rf_gram_workspace_bytes", M, N, K, int(fold_rows), ctypes.byref(nb))
+    return nb.value
+
+
+def gram_accumulate(a, b, c, fold_rows=0, workspace=None):
     """c += a b^T (a [M, K], b [N, K] bf16 K-contiguous; c [M, N] fp64): fp32 over runs of at most fold_rows
-    of K (0: all of K), each run added in fp64."""
+    of K (0: all of K), each run added in fp64. workspace: a uint8 device buffer for the run-split schedule
+    of shapes just past one round of tiles (gram_workspace_bytes); taken from torch's allocator when None
+    and needed. The result's bits do not depend on it."""
     _need(a, "a", torch.bfloat16, 2)
     _need(b, "b", torch.bfloat16, 2)
     _need(c, "c", torch.float64, 2)
@@ -76,8 +87,12 @@ def gram_accumulate(a, b, c, fold_rows=0):
     N = b.shape[0]
     if b.shape[1] != K or tuple(c.shape) != (M, N):
         raise ValueError(f"gram shapes a {tuple(a.shape)}, b {tuple(b.shape)}, c {tuple(c.shape)}")
+    need = gram_workspace_bytes(M, N, K, fold_rows) if M > 0 and N % 256 == 0 and K % 64 == 0 else 0
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=c.device)
+    nb = workspace.numel() if workspace is not None else 0
     _lib.call("rf_gram_accumulate", _ptr(a), a.stride(0), _ptr(b), b.stride(0), M, N, K, int(fold_rows), _ptr(c),
-              c.stride(0), _stream(a))
+              c.stride(0), _ptr(workspace), nb, _stream(a))
     return c
 
 
@@ -194,6 +209,14 @@ class RidgeStats:
             self._sq = torch.empty_like(self._part)
         return self._xt, self._yt, self._part
 
+    def _gram(self, a, b, c, block):
+        """gram_accumulate with a workspace kept between calls (grown as needed)."""
+        need = gram_workspace_bytes(a.shape[0], b.shape[0], a.shape[1], block)
+        ws = getattr(self, "_gws", None)
+        if need and (ws is None or ws.numel() < need):
+            self._gws = ws = torch.empty(need, dtype=torch.uint8, device=self.device)
+        gram_accumulate(a, b, c, block, ws)
+
     def _x_piece(self, r, sums):
         """Rows r .. r + PIECE of the current boundary rows, centred and transposed into X^T (the column sums
         of their centred values added into s1x when `sums`); returns the row count."""
@@ -239,7 +262,7 @@ class RidgeStats:
             rows = self._x_piece(r, True)
             kp = (rows + 63) // 64 * 64
             xt = self._xt
-            gram_accumulate(xt[:d + 2 * cx.s, :kp], xt[:d + cx.lo_rows, :kp], self.sxx, block)
+            self._gram(xt[:d + 2 * cx.s, :kp], xt[:d + cx.lo_rows, :kp], self.sxx, block)
 
     @torch.no_grad()
     def add_layer(self, i, y):
@@ -272,7 +295,7 @@ class RidgeStats:
             py = tiles_view(part, kp // 64, o)
             transpose_centred(y[r:r + rows], yt[:o, :kp], yt[o:, :kp], cy.shift, cy.lo_row, py, n_centred=cy.s)
             _colsum_fold(py, self.s1y[i])
-            gram_accumulate(xt[:d + 2 * cx.s, :kp], yt[:o + cy.lo_rows, :kp], self.sxy[i], block)
+            self._gram(xt[:d + 2 * cx.s, :kp], yt[:o + cy.lo_rows, :kp], self.sxy[i], block)
 
     def add(self, x, ys, block=8192, w=None):
         """x [n, d] and ys {layer: [n, d_out]}: bf16 rows on the GPU (the same rows, in order)
@@ -321,7 +344,6 @@ def _to(state, device):
 
 
 def ridge_solve_workspace_bytes(d, nlam=1):
-    import ctypes
     n = ctypes.c_size_t(0)
     _lib.call("rf_ridge_solve_workspace_bytes", d, nlam, ctypes.byref(n))
     return n.value
@@ -365,7 +387,6 @@ class RidgeFit:
         w = torch.empty(len(lams), d, R, **f64)
         bias = None if mean_y is None else torch.empty(len(lams), R, **f64)
         ws = torch.empty(ridge_solve_workspace_bytes(d, len(lams)), dtype=torch.uint8, device=self.device)
-        import ctypes
         arr = (ctypes.c_double * len(lams))(*lams)
         mx = self.mean_x.contiguous()
         my = None if mean_y is None else mean_y.to(self.device, torch.float64).contiguous()

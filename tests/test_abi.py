@@ -87,3 +87,22 @@ def test_rows_workspace_sizes():
             assert need == max(ops.gemm_workspace_bytes(m, n, k) for m in chunks), (n, k, rows)
     with pytest.raises(ValueError):
         ops.rows_workspace_bytes(10, 100, 4096)
+
+
+def test_gram_workspace_sizes():
+    """Host-only size rule of rf_gram_accumulate's run-split schedule: when the 256 x 256 tiles are more than
+    256 but fewer than 512 and K holds two or more runs, the tiles past the first 256 are cut into their runs
+    (at most 512 of them), each stored as a 256 x 256 fp32 plane; otherwise no workspace."""
+    from rfill import ridge
+    plane = 256 * 256 * 4
+    assert ridge.gram_workspace_bytes(4096, 4096, 65536, 8192) == 0          # 256 tiles: one round
+    assert ridge.gram_workspace_bytes(4104, 4352, 65536, 8192) == 33 * 8 * plane   # centred X and Y: 289 tiles
+    assert ridge.gram_workspace_bytes(4104, 4096, 65536, 8192) == 16 * 8 * plane   # centred X only: 272 tiles
+    assert ridge.gram_workspace_bytes(4104, 4352, 12288, 8192) == 33 * 2 * plane   # a short last run counts
+    assert ridge.gram_workspace_bytes(4104, 4352, 65536, 0) == 0             # one run: nothing to split
+    assert ridge.gram_workspace_bytes(4104, 4352, 65536, 4096) == 0          # 33 x 16 = 528 runs > 512: whole
+    assert ridge.gram_workspace_bytes(5120, 5120, 65536, 8192) == 0          # 400 tiles, 1152 runs: whole
+    assert ridge.gram_workspace_bytes(8192, 8192, 65536, 8192) == 0          # 1024 tiles: whole rounds
+    assert ridge.gram_workspace_bytes(0, 4096, 65536, 8192) == 0
+    with pytest.raises(ValueError):
+        ridge.gram_workspace_bytes(4096, 100, 65536, 8192)                  # N not a multiple of 256

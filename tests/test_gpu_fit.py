@@ -57,6 +57,33 @@ def test_gram_accumulate_matches_fp64_products(dev, fold_rows):
     assert torch.equal(again, c)
 
 
+@pytest.mark.parametrize("M,N,K,fold_rows", [(4104, 4352, 12288, 8192), (4352, 4096, 16384, 4096)])
+def test_gram_run_split_schedule_is_bit_identical(dev, M, N, K, fold_rows):
+    """Tile counts just past one round of the GPU's 256 CUs (a centred operand's extra rows / columns: 289
+    and 272 tiles): with a workspace the tiles past the first 256 run as single runs whose fp32 sums a second
+    kernel adds into C in run order. The same bits as every tile whole (no workspace), and fp64 products to
+    1e-6; the first shape's last run is shorter than fold_rows (12288 = 8192 + 4096)."""
+    from rfill import _lib, ridge
+    from rfill.ops import _ptr, _stream
+    need = ridge.gram_workspace_bytes(M, N, K, fold_rows)
+    assert need > 0
+    g = torch.Generator(device=dev).manual_seed(3)
+    a = torch.randn(M, K, generator=g, device=dev).to(torch.bfloat16)
+    b = (torch.randn(N, K, generator=g, device=dev) * 2).to(torch.bfloat16)
+    c0 = torch.randn(M, N, generator=g, device=dev, dtype=torch.float64)
+    whole = c0.clone()
+    _lib.call("rf_gram_accumulate", _ptr(a), a.stride(0), _ptr(b), b.stride(0), M, N, K, fold_rows, _ptr(whole),
+              whole.stride(0), None, 0, _stream(a))
+    ws = torch.full((need,), 0xFF, dtype=torch.uint8, device=dev)      # stale contents must not matter
+    split = c0.clone()
+    ridge.gram_accumulate(a, b, split, fold_rows, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(split, whole)
+    err = rel(split - c0, a.double() @ b.double().T)
+    print(f"gram {M} x {N} x {K} (fold {fold_rows}) run-split rel err {err:.2e}")
+    assert err < 1e-6
+
+
 def test_gram_accumulate_refuses_bad_fold(dev):
     from rfill import ridge
     a = torch.zeros(256, 128, dtype=torch.bfloat16, device=dev)
