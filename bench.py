@@ -56,6 +56,10 @@ class KernelTimer:
         pairs = self.ev.get(name, [])
         return sum(s.elapsed_time(e) for s, e in pairs) / max(1, len(pairs)) / 1e3
 
+    def median_s(self, name):
+        ts = sorted(s.elapsed_time(e) for s, e in self.ev.get(name, []))
+        return ts[len(ts) // 2] / 1e3 if ts else 0.0
+
 
 def build_workload(dev):
     from rfill import synth
@@ -97,12 +101,18 @@ def ceilings(dev, P, H):
     a = torch.randn(P, H, device=dev, dtype=torch.bfloat16)
     w = torch.randn(H, H, device=dev, dtype=torch.bfloat16)
     out = torch.empty(P, H, device=dev, dtype=torch.bfloat16)
-    for _ in range(3):
-        torch.matmul(a, w.t(), out=out)
-    torch.cuda.synchronize()
+    # two forms of the same product (torch may route them to different library kernels); the faster median
+    forms = {"matmul_out": lambda: torch.matmul(a, w.t(), out=out),
+             "linear": lambda: torch.nn.functional.linear(a, w)}
     t = KernelTimer()
-    for _ in range(10):
-        t.run("gemm", lambda: torch.matmul(a, w.t(), out=out))
+    for name, f in forms.items():
+        for _ in range(3):
+            f()
+        torch.cuda.synchronize()
+        for _ in range(10):
+            t.run(name, f)
+    torch.cuda.synchronize()
+    gemm_form = min(forms, key=t.median_s)
     src_bytes = 1 << 30
     src = torch.empty(src_bytes, dtype=torch.uint8, device=dev)
     dst = torch.empty_like(src)
@@ -118,7 +128,9 @@ def ceilings(dev, P, H):
     for _ in range(5):
         t.run("mfma", lambda: ops.mfma_ceiling(blocks, iters, acc))
     torch.cuda.synchronize()
-    return {"hipblaslt_gemm_tflops": round(2 * P * H * H / t.mean_s("gemm") / 1e12, 1),
+    return {"hipblaslt_gemm_tflops": round(2 * P * H * H / t.median_s(gemm_form) / 1e12, 1),
+            "gemm_form": gemm_form,
+            "gemm_forms_tflops": {k: round(2 * P * H * H / t.median_s(k) / 1e12, 1) for k in forms},
             "copy_gbs": round(2 * src_bytes / t.mean_s("copy") / 1e9, 1),
             "gemm_shape": [P, H, H],
             "mfma_power_ceiling_tflops": round(blocks * 4 * 4 * iters * 32768 / t.mean_s("mfma") / 1e12, 1)}
