@@ -994,30 +994,37 @@ __device__ __forceinline__ void fold_tile(const f32x16 (&acc)[4][4], uint4* lds,
           }
     }
     __syncthreads();
-#pragma unroll
-    for (int b = 0; b < 4; ++b) {                 // wave w: image rows 32w .. 32w + 31, 8 per batch
-      double2 v[8][2];
+    // wave w: image rows 32w .. 32w + 31 in 4 batches of 8; batch b + 1's rows of C load before batch b's
+    // stores, so two batches' loads are in flight (the compiler keeps loads of C behind earlier stores to
+    // C, so it would not overlap them by itself). Loads are unconditional (rows past M read row M - 1, not
+    // stored): a conditional load would make the stores wait for every load in flight.
+    double2 v[2][8][2];
+    auto load_batch = [&](int b, double2 (&d)[8][2]) {
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        const int gm = m0 + h * 128 + w * 32 + b * 8 + i;
-        if (gm < M) {
-          const double* p = C + static_cast<int64_t>(gm) * ldc + n0 + 4 * lane;
-          v[i][0] = *reinterpret_cast<const double2*>(p);
-          v[i][1] = *reinterpret_cast<const double2*>(p + 2);
-        }
+        const int gm = min(m0 + h * 128 + w * 32 + b * 8 + i, M - 1);
+        const double* p = C + static_cast<int64_t>(gm) * ldc + n0 + 4 * lane;
+        d[i][0] = *reinterpret_cast<const double2*>(p);
+        d[i][1] = *reinterpret_cast<const double2*>(p + 2);
       }
+    };
+    load_batch(0, v[0]);
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      if (b + 1 < 4) load_batch(b + 1, v[(b + 1) & 1]);
+      double2 (&d)[8][2] = v[b & 1];
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
         const int j = w * 32 + b * 8 + i, gm = m0 + h * 128 + j;
         if (gm < M) {
           const float4 a = img[j * 64 + (lane ^ (j & 15))];
-          v[i][0].x += a.x;
-          v[i][0].y += a.y;
-          v[i][1].x += a.z;
-          v[i][1].y += a.w;
+          d[i][0].x += a.x;
+          d[i][0].y += a.y;
+          d[i][1].x += a.z;
+          d[i][1].y += a.w;
           double* p = C + static_cast<int64_t>(gm) * ldc + n0 + 4 * lane;
-          *reinterpret_cast<double2*>(p) = v[i][0];
-          *reinterpret_cast<double2*>(p + 2) = v[i][1];
+          *reinterpret_cast<double2*>(p) = d[i][0];
+          *reinterpret_cast<double2*>(p + 2) = d[i][1];
         }
       }
     }
