@@ -72,19 +72,22 @@ __device__ __forceinline__ void wait_vm_lgkm0() {
   __builtin_amdgcn_s_waitcnt((n & 15) | (7 << 4) | (0 << 8) | ((n >> 4) << 14));
 }
 
-// Slot of quarter q of K step kt: quarters 0, 1 are activation rows 0-127 / 128-255, quarters 2, 3
-// weight rows 0-127 / 128-255.
-__device__ __forceinline__ int slot_of(int kt, int q) { return (4 * kt + q) % NSLOT; }
+// Ring slot of quarter q of K step kt: (4 kt + q) % NSLOT. Quarters 0, 1 are activation rows 0-127 /
+// 128-255, quarters 2, 3 weight rows 0-127 / 128-255. The loops carry the step's ring phase ph = (4 kt) %
+// NSLOT instead of kt, so that a slot is one conditional subtraction, slot_at(ph, q) (q < 12), rather
+// than a division by 10 on the scalar unit before every direct load; next_ph(ph) is the phase of step
+// kt + 1.
+__device__ __forceinline__ int slot_at(int ph, int q) { return ph + q >= NSLOT ? ph + q - NSLOT : ph + q; }
+__device__ __forceinline__ int next_ph(int ph) { return slot_at(ph, 4); }
 
-// Load i (0..3) of this wave for quarter q of step kt, straight from memory into its slot
-// (buffer_load_dwordx4 ... lds): 8 rows x 128 bytes, full cache lines. Lane L writes slot chunk
-// (32w + 8i) * 8 + L, i.e. row 32w + 8i + L / 8, physical chunk L % 8, and so fetches logical chunk
-// (L % 8) ^ slot_swz(row) of that row; `voff` holds the lane's byte offset of that (row, chunk), the
-// step's K offset goes in the scalar offset.
-__device__ __forceinline__ void issue_load(__amdgpu_buffer_rsrc_t rs, uint32_t voff, int kt, int q, int i, char* lds,
-                                           int w) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(
-      rs, (lds_ptr)(lds + slot_of(kt, q) * (SLOT_U4 * 16) + (32 * w + 8 * i) * (CPR * 16)), 16, voff, kt * BK * 2, 0, 0);
+// Load i (0..3) of this wave into ring slot `slot` for K step kt, straight from memory (buffer_load_dwordx4
+// ... lds): 8 rows x 128 bytes, full cache lines. Lane L writes slot chunk (32w + 8i) * 8 + L, i.e. row
+// 32w + 8i + L / 8, physical chunk L % 8, and so fetches logical chunk (L % 8) ^ slot_swz(row) of that row;
+// `voff` holds the lane's byte offset of that (row, chunk), the step's K offset goes in the scalar offset.
+__device__ __forceinline__ void issue_load_at(__amdgpu_buffer_rsrc_t rs, uint32_t voff, int slot, int kt, int i,
+                                              char* lds, int w) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds + slot * (SLOT_U4 * 16) + (32 * w + 8 * i) * (CPR * 16)),
+                                           16, voff, kt * BK * 2, 0, 0);
 }
 
 // acc[nt][mt] += W[n0 + wn*128 + nt*32 .. +32, :] . X[m0 + wm*128 + mt*32 .. +32, :]^T over all of K
@@ -138,61 +141,63 @@ __device__ __forceinline__ void mainloop(const uint16_t* __restrict__ X, int64_t
   const int lr = lane & 31, lk = lane >> 5, swz = slot_swz(lr);
   bf16x8 fx[2][4], fw[2][4];
   // fragment r (0..7) of slice ks of step kt: r < 4 -> weight block r, else activation block r - 4
-  auto read_one = [&](int kt, int ks, int r, bf16x8 (&ax)[4], bf16x8 (&aw)[4]) {
+  // (steps are named by their ring phase ph and, for the loads' K offset, their index kt)
+  auto read_one = [&](int ph, int ks, int r, bf16x8 (&ax)[4], bf16x8 (&aw)[4]) {
     const int ch = (ks * 2 + lk) ^ swz;
-    if (r < 4) aw[r] = as_frag(lds[slot_of(kt, 2 + wn) * SLOT_U4 + (r * 32 + lr) * CPR + ch]);
-    else ax[r - 4] = as_frag(lds[slot_of(kt, wm) * SLOT_U4 + ((r - 4) * 32 + lr) * CPR + ch]);
+    if (r < 4) aw[r] = as_frag(lds[slot_at(ph, 2 + wn) * SLOT_U4 + (r * 32 + lr) * CPR + ch]);
+    else ax[r - 4] = as_frag(lds[slot_at(ph, wm) * SLOT_U4 + ((r - 4) * 32 + lr) * CPR + ch]);
   };
-  // load j (0..7) of step kt's activation (wt = false) or weight (wt = true) quarters
-  auto load = [&](int kt, bool wt, int j) {
+  // load j (0..7) of step kt's (phase ph) activation (wt = false) or weight (wt = true) quarters
+  auto load = [&](int kt, int ph, bool wt, int j) {
     const int h = j >> 2, i = j & 3;
-    if (wt) issue_load(rw, vw[h][i], kt, 2 + h, i, base, w);
-    else issue_load(rx, vx[h][i], kt, h, i, base, w);
+    if (wt) issue_load_at(rw, vw[h][i], slot_at(ph, 2 + h), kt, i, base, w);
+    else issue_load_at(rx, vx[h][i], slot_at(ph, h), kt, i, base, w);
   };
   // one slice: 16 MFMAs on (ax, aw); reads of the next slice's fragments after the first 8 (`rd`);
   // `ld` 0: no loads, 1: activation loads lo .. lo + 3 of step lkt after MFMAs 1, 5, 9, 13,
   // 2: all 8 weight loads of step lkt, one after every even MFMA. Spreading the loads keeps the
   // texture units' queues from filling, which would stall the wave's in-order issue of MFMAs.
-  auto slice = [&](const bf16x8 (&ax)[4], const bf16x8 (&aw)[4], bool rd, int rkt, int rks, bf16x8 (&nx)[4],
-                   bf16x8 (&nw)[4], int ld, int lkt, int lo) {
+  auto slice = [&](const bf16x8 (&ax)[4], const bf16x8 (&aw)[4], bool rd, int rph, int rks, bf16x8 (&nx)[4],
+                   bf16x8 (&nw)[4], int ld, int lkt, int lph, int lo) {
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
       const int qi = q >> 2, qj = (qi & 1) ? 3 - (q & 3) : (q & 3);   // snake: one operand changes per MFMA
       acc[qi][qj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aw[qi], ax[qj], acc[qi][qj], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
-      if (q < 8 && rd) read_one(rkt, rks, q, nx, nw);
-      if (ld == 2 && !(q & 1)) load(lkt, true, q >> 1);
-      if (ld == 1 && (q & 3) == 1) load(lkt, false, lo + (q >> 2));
+      if (q < 8 && rd) read_one(rph, rks, q, nx, nw);
+      if (ld == 2 && !(q & 1)) load(lkt, lph, true, q >> 1);
+      if (ld == 1 && (q & 3) == 1) load(lkt, lph, false, lo + (q >> 2));
       __builtin_amdgcn_sched_barrier(0);
     }
   };
   // `steady` (compile-time): step kt + 2 exists, so its loads are issued and the wait is exact
-  auto step = [&](int kt, auto steady) {
-    slice(fx[0], fw[0], true, kt, 1, fx[1], fw[1], steady ? 1 : 0, kt + 2, 0);
-    slice(fx[1], fw[1], true, kt, 2, fx[0], fw[0], steady ? 1 : 0, kt + 2, 4);
-    slice(fx[0], fw[0], true, kt, 3, fx[1], fw[1], 0, 0, 0);
+  auto step = [&](int kt, int ph, auto steady) {
+    const int ph1 = next_ph(ph), ph2 = next_ph(ph1);
+    slice(fx[0], fw[0], true, ph, 1, fx[1], fw[1], steady ? 1 : 0, kt + 2, ph2, 0);
+    slice(fx[1], fw[1], true, ph, 2, fx[0], fw[0], steady ? 1 : 0, kt + 2, ph2, 4);
+    slice(fx[0], fw[0], true, ph, 3, fx[1], fw[1], 0, 0, 0, 0);
     if (steady) wait_vm_lgkm0<8>();
     else wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
-    slice(fx[1], fw[1], steady || kt + 1 < nk, kt + 1, 0, fx[0], fw[0], steady ? 2 : 0, kt + 2, 0);
+    slice(fx[1], fw[1], steady || kt + 1 < nk, ph1, 0, fx[0], fw[0], steady ? 2 : 0, kt + 2, ph2, 0);
   };
 
   // prologue: steps 0 and 1, then step 0's first fragments
-  for (int j = 0; j < 8; ++j) load(0, false, j);
-  for (int j = 0; j < 8; ++j) load(0, true, j);
+  for (int j = 0; j < 8; ++j) load(0, 0, false, j);
+  for (int j = 0; j < 8; ++j) load(0, 0, true, j);
   if (nk > 1) {
-    for (int j = 0; j < 8; ++j) load(1, false, j);
-    for (int j = 0; j < 8; ++j) load(1, true, j);
+    for (int j = 0; j < 8; ++j) load(1, 4, false, j);
+    for (int j = 0; j < 8; ++j) load(1, 4, true, j);
     wait_vm_lgkm0<16>();
   } else {
     wait_vm_lgkm0<0>();
   }
   __builtin_amdgcn_s_barrier();
   for (int r = 0; r < 8; ++r) read_one(0, 0, r, fx[0], fw[0]);
-  int kt = 0;
-  for (; kt + 2 < nk; ++kt) step(kt, std::true_type{});
-  for (; kt < nk; ++kt) step(kt, std::false_type{});
+  int kt = 0, ph = 0;
+  for (; kt + 2 < nk; ++kt, ph = next_ph(ph)) step(kt, ph, std::true_type{});
+  for (; kt < nk; ++kt, ph = next_ph(ph)) step(kt, ph, std::false_type{});
   wait_vm_lgkm0<0>();
   __syncthreads();
 }
@@ -1188,11 +1193,6 @@ struct TileOps {
   __amdgpu_buffer_rsrc_t rx, rw;
 };
 
-__device__ __forceinline__ void issue_load_at(__amdgpu_buffer_rsrc_t rs, uint32_t voff, int slot, int kstep, int i,
-                                              char* lds, int w) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_ptr)(lds + slot * (SLOT_U4 * 16) + (32 * w + 8 * i) * (CPR * 16)),
-                                           16, voff, kstep * BK * 2, 0, 0);
-}
 
 // This block's tiles of T logical tiles: first + stride * i for i < cnt. With 256 blocks (T >= 256) XCD x
 // (blocks x, x + 8, ...) takes a contiguous eighth of the logical order and its 32 blocks walk it 32 tiles
@@ -1292,78 +1292,84 @@ __device__ __forceinline__ void stream_tiles(int cnt, int nk, int64_t ldx, int64
   TileOps cur = ops(0);
   TileOps nxt = cnt > 1 ? ops(1) : cur;
 
-  // fragment r (0..7) of slice ks of global step g: r < 4 -> weight block r, else activation block r - 4
-  auto read_one = [&](int g, int ks, int r, bf16x8 (&ax)[4], bf16x8 (&aw)[4]) {
+  // (global steps are named by their ring phase, slot_at / next_ph)
+  // fragment r (0..7) of slice ks of the global step of phase ph: r < 4 -> weight block r, else activation
+  // block r - 4
+  auto read_one = [&](int ph, int ks, int r, bf16x8 (&ax)[4], bf16x8 (&aw)[4]) {
     const int ch = (ks * 2 + lk) ^ swz;
-    if (r < 4) aw[r] = as_frag(lds[slot_of(g, 2 + wn) * SLOT_U4 + (r * 32 + lr) * CPR + ch]);
-    else ax[r - 4] = as_frag(lds[slot_of(g, wm) * SLOT_U4 + ((r - 4) * 32 + lr) * CPR + ch]);
+    if (r < 4) aw[r] = as_frag(lds[slot_at(ph, 2 + wn) * SLOT_U4 + (r * 32 + lr) * CPR + ch]);
+    else ax[r - 4] = as_frag(lds[slot_at(ph, wm) * SLOT_U4 + ((r - 4) * 32 + lr) * CPR + ch]);
   };
-  // load j (0..7) of global step g's activation (wt = false) or weight quarters: tile-local step k of o
-  auto load = [&](const TileOps& o, int g, int k, bool wt, int j) {
+  // load j (0..7) of the activation (wt = false) or weight quarters of the global step of phase ph:
+  // tile-local step k of o
+  auto load = [&](const TileOps& o, int ph, int k, bool wt, int j) {
     const int h = j >> 2, i = j & 3;
-    if (wt) issue_load_at(o.rw, vw[h][i], slot_of(g, 2 + h), k, i, base, w);
-    else issue_load_at(o.rx, vx[h][i], slot_of(g, h), k, i, base, w);
+    if (wt) issue_load_at(o.rw, vw[h][i], slot_at(ph, 2 + h), k, i, base, w);
+    else issue_load_at(o.rx, vx[h][i], slot_at(ph, h), k, i, base, w);
   };
-  // as mainloop's slice, with the loads' source o, global step lg and tile-local step lk2
-  auto slice = [&](const bf16x8 (&ax)[4], const bf16x8 (&aw)[4], bool rd, int rg, int rks, bf16x8 (&nx)[4],
-                   bf16x8 (&nw)[4], int ld, const TileOps& o, int lg, int lk2, int lo) {
+  // as mainloop's slice, with the loads' source o, global step phase lph and tile-local step lk2
+  auto slice = [&](const bf16x8 (&ax)[4], const bf16x8 (&aw)[4], bool rd, int rph, int rks, bf16x8 (&nx)[4],
+                   bf16x8 (&nw)[4], int ld, const TileOps& o, int lph, int lk2, int lo) {
 #pragma unroll
     for (int q = 0; q < 16; ++q) {
       const int qi = q >> 2, qj = (qi & 1) ? 3 - (q & 3) : (q & 3);   // snake: one operand changes per MFMA
       acc[qi][qj] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(aw[qi], ax[qj], acc[qi][qj], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
-      if (q < 8 && rd) read_one(rg, rks, q, nx, nw);
-      if (ld == 2 && !(q & 1)) load(o, lg, lk2, true, q >> 1);
-      if (ld == 1 && (q & 3) == 1) load(o, lg, lk2, false, lo + (q >> 2));
+      if (q < 8 && rd) read_one(rph, rks, q, nx, nw);
+      if (ld == 2 && !(q & 1)) load(o, lph, lk2, true, q >> 1);
+      if (ld == 1 && (q & 3) == 1) load(o, lph, lk2, false, lo + (q >> 2));
       __builtin_amdgcn_sched_barrier(0);
     }
   };
   // global step g; the loads of step g + 2 (source o2, tile-local step k2) when `has2`; its weight
   // quarters in slice 3 unless `defer`; `has1`: step g + 1 exists (its first fragments are read)
   // (`defer` marks a tile's last step: its weight slots, free after the barrier, go to pre(i, ...))
-  auto step = [&](int g, const TileOps& o2, int k2, auto has2, auto defer, bool has1, int i) {
-    slice(fx[0], fw[0], true, g, 1, fx[1], fw[1], has2 ? 1 : 0, o2, g + 2, k2, 0);
-    slice(fx[1], fw[1], true, g, 2, fx[0], fw[0], has2 ? 1 : 0, o2, g + 2, k2, 4);
-    slice(fx[0], fw[0], true, g, 3, fx[1], fw[1], 0, o2, 0, 0, 0);
+  auto step = [&](int ph, const TileOps& o2, int k2, auto has2, auto defer, bool has1, int i) {
+    const int ph1 = next_ph(ph), ph2 = next_ph(ph1);
+    slice(fx[0], fw[0], true, ph, 1, fx[1], fw[1], has2 ? 1 : 0, o2, ph2, k2, 0);
+    slice(fx[1], fw[1], true, ph, 2, fx[0], fw[0], has2 ? 1 : 0, o2, ph2, k2, 4);
+    slice(fx[0], fw[0], true, ph, 3, fx[1], fw[1], 0, o2, 0, 0, 0);
     if (has2) wait_vm_lgkm0<8>();
     else wait_vm_lgkm0<0>();
     __builtin_amdgcn_s_barrier();
     __builtin_amdgcn_sched_barrier(0);
     if (defer) {
-      pre(i, lds + slot_of(g, 2) * SLOT_U4);
+      pre(i, lds + slot_at(ph, 2) * SLOT_U4);
       __builtin_amdgcn_sched_barrier(0);
     }
-    slice(fx[1], fw[1], has1, g + 1, 0, fx[0], fw[0], (has2 && !defer) ? 2 : 0, o2, g + 2, k2, 0);
+    slice(fx[1], fw[1], has1, ph1, 0, fx[0], fw[0], (has2 && !defer) ? 2 : 0, o2, ph2, k2, 0);
   };
 
-  // prologue: steps 0 and 1 of tile 0, then the accumulators and step 0's first fragments
+  // prologue: steps 0 and 1 of tile 0 (phases 0 and 4), then the accumulators and step 0's first fragments
   for (int j = 0; j < 8; ++j) load(cur, 0, 0, false, j);
   for (int j = 0; j < 8; ++j) load(cur, 0, 0, true, j);
-  for (int j = 0; j < 8; ++j) load(cur, 1, 1, false, j);
-  for (int j = 0; j < 8; ++j) load(cur, 1, 1, true, j);
+  for (int j = 0; j < 8; ++j) load(cur, 4, 1, false, j);
+  for (int j = 0; j < 8; ++j) load(cur, 4, 1, true, j);
   begin(0, acc);
   wait_vm_lgkm0<16>();
   __builtin_amdgcn_s_barrier();
   for (int r = 0; r < 8; ++r) read_one(0, 0, r, fx[0], fw[0]);
-  int g = 0;
+  int ph = 0;                                     // phase of the global step
   for (int i = 0; i < cnt; ++i) {
     const bool more = i + 1 < cnt;
-    for (int kt = 0; kt + 2 < nk; ++kt, ++g) step(g, cur, kt + 2, std::true_type{}, std::false_type{}, true, i);
+    for (int kt = 0; kt + 2 < nk; ++kt, ph = next_ph(ph))
+      step(ph, cur, kt + 2, std::true_type{}, std::false_type{}, true, i);
     // the tile's last two steps: step g + 2 is the next tile's step 0, then its step 1
-    step(g, nxt, 0, more, std::false_type{}, true, i);
-    ++g;
-    step(g, nxt, 1, more, std::true_type{}, false, i);
-    ++g;
-    // g is the next tile's first step (landed: the last barrier waited for it); step g - 1 left its four
-    // slots free: activation slots (img) and weight slots (side), each pair contiguous. The next tile's first fragments are read after the epilogue, so that they do not hold
+    step(ph, nxt, 0, more, std::false_type{}, true, i);
+    const int ph_last = next_ph(ph);
+    step(ph_last, nxt, 1, more, std::true_type{}, false, i);
+    ph = next_ph(ph_last);
+    // ph is the next tile's first step (landed: the last barrier waited for it); the step before it
+    // (phase ph_last) left its four slots free: activation slots (img) and weight slots (side), each pair
+    // contiguous. The next tile's first fragments are read after the epilogue, so that they do not hold
     // registers through it.
-    end(i, acc, lds + slot_of(g - 1, 0) * SLOT_U4, reinterpret_cast<float*>(lds + slot_of(g - 1, 2) * SLOT_U4));
+    end(i, acc, lds + slot_at(ph_last, 0) * SLOT_U4, reinterpret_cast<float*>(lds + slot_at(ph_last, 2) * SLOT_U4));
     if (more) {
-      for (int j = 0; j < 8; ++j) load(nxt, g + 1, 1, true, j);   // the deferred weight quarters of its step 1
+      for (int j = 0; j < 8; ++j) load(nxt, next_ph(ph), 1, true, j);   // the deferred weight quarters of its step 1
       cur = nxt;
       if (i + 2 < cnt) nxt = ops(i + 2);
       begin(i + 1, acc);
-      for (int r = 0; r < 8; ++r) read_one(g, 0, r, fx[0], fw[0]);
+      for (int r = 0; r < 8; ++r) read_one(ph, 0, r, fx[0], fw[0]);
     }
   }
   wait_vm_lgkm0<0>();
