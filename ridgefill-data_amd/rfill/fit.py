@@ -65,12 +65,12 @@ class Capture:
         self.off = 0
 
     def _room(self, kp):
-        cap = self.T.shape[1] if self.T is not None else 0
+        cap = self.T.shape[1] - ridge.ROW_PAD if self.T is not None else 0
         if kp > cap:
             self.flush()
             cap = max(self.block, kp)
             dev = self.model.device
-            self.T = torch.zeros((self.L - self.S0) * self.R, cap, dtype=torch.bfloat16, device=dev)
+            self.T = torch.zeros((self.L - self.S0) * self.R, cap + ridge.ROW_PAD, dtype=torch.bfloat16, device=dev)
             self.part = torch.empty(cap // 64, self.H, dtype=torch.float32, device=dev)
             self.part_sq = torch.empty_like(self.part)
         elif self.off + kp > cap:

@@ -33,6 +33,8 @@ from .ops import _need, _ptr, _stream
 SHIFT_MAX = 128      # channels per operand centred before the product (each takes a mid and a lo row)
 LO_ROWS = 256        # extra rows per operand when any channel is centred (keeps the Gram width a multiple of 256)
 PIECE = 65536        # rows transposed and multiplied per Gram launch
+ROW_PAD = 64         # elements past the rows of a transposed operand: strides of 65536 or 8192 bf16 (a power of two)
+                     # put all of a transpose block's output rows on the same memory channels (5 % slower)
 
 
 def _transpose(x, dst, partial):
@@ -201,10 +203,10 @@ class RidgeStats:
     def _buffers(self, kp):
         """Transposed-operand buffers for kp rows (grown as needed, kept between calls): X^T and Y^T with their
         extra rows, and the per-64-row column-sum partials."""
-        if self._xt is None or self._xt.shape[1] < kp:
+        if self._xt is None or self._xt.shape[1] - ROW_PAD < kp:
             d, o, lo = self.dim, self.out_dim, LO_ROWS
-            self._xt = torch.zeros(d + lo, kp, dtype=torch.bfloat16, device=self.device)
-            self._yt = torch.zeros(o + lo, kp, dtype=torch.bfloat16, device=self.device)
+            self._xt = torch.zeros(d + lo, kp + ROW_PAD, dtype=torch.bfloat16, device=self.device)
+            self._yt = torch.zeros(o + lo, kp + ROW_PAD, dtype=torch.bfloat16, device=self.device)
             self._part = torch.empty(kp // 64 * max(d, o), dtype=torch.float32, device=self.device)
             self._sq = torch.empty_like(self._part)
         return self._xt, self._yt, self._part
