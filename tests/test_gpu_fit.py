@@ -61,8 +61,9 @@ def test_gram_accumulate_matches_fp64_products(dev, fold_rows):
 def test_gram_run_split_schedule_is_bit_identical(dev, M, N, K, fold_rows):
     """Tile counts just past one round of the GPU's 256 CUs (a centred operand's extra rows / columns: 289
     and 272 tiles): with a workspace the tiles past the first 256 run as single runs whose fp32 sums a second
-    kernel adds into C in run order. The same bits as every tile whole (no workspace), and fp64 products to
-    1e-6; the first shape's last run is shorter than fold_rows (12288 = 8192 + 4096)."""
+    kernel adds into C in run order. The same bits as every tile whole (no workspace, or one a byte short),
+    nothing written past the workspace (a guard region after it), and fp64 products to 1e-6; the first
+    shape's last run is shorter than fold_rows (12288 = 8192 + 4096)."""
     from rfill import _lib, ridge
     from rfill.ops import _ptr, _stream
     need = ridge.gram_workspace_bytes(M, N, K, fold_rows)
@@ -74,11 +75,17 @@ def test_gram_run_split_schedule_is_bit_identical(dev, M, N, K, fold_rows):
     whole = c0.clone()
     _lib.call("rf_gram_accumulate", _ptr(a), a.stride(0), _ptr(b), b.stride(0), M, N, K, fold_rows, _ptr(whole),
               whole.stride(0), None, 0, _stream(a))
-    ws = torch.full((need,), 0xFF, dtype=torch.uint8, device=dev)      # stale contents must not matter
+    guard = 1 << 20
+    buf = torch.full((need + guard,), 0xFF, dtype=torch.uint8, device=dev)     # stale contents must not matter
     split = c0.clone()
-    ridge.gram_accumulate(a, b, split, fold_rows, ws)
+    _lib.call("rf_gram_accumulate", _ptr(a), a.stride(0), _ptr(b), b.stride(0), M, N, K, fold_rows, _ptr(split),
+              split.stride(0), _ptr(buf), need, _stream(a))
+    short = c0.clone()                                                  # one byte short: every tile whole
+    _lib.call("rf_gram_accumulate", _ptr(a), a.stride(0), _ptr(b), b.stride(0), M, N, K, fold_rows, _ptr(short),
+              short.stride(0), _ptr(buf), need - 1, _stream(a))
     torch.cuda.synchronize()
-    assert torch.equal(split, whole)
+    assert torch.equal(split, whole) and torch.equal(short, whole)
+    assert bool((buf[need:] == 0xFF).all()), "the run-split schedule wrote past its workspace"
     err = rel(split - c0, a.double() @ b.double().T)
     print(f"gram {M} x {N} x {K} (fold {fold_rows}) run-split rel err {err:.2e}")
     assert err < 1e-6
