@@ -421,11 +421,12 @@ def fit_bench(dev, chunks=3, rows=65536, d=4096, targets=16, lams=(1e-4, 1e-3, 1
     """The closed-form fit at the 8B-width shape (d 4096, 16 targets, 64K-row chunks of Student-t rows):
     `chunks` of the 32 chunks of 2,097,152 rows are generated (untimed) and accumulated in the reference's
     8192-row blocks (timed: transposes with centring, column sums and the MFMA Gram / cross accumulation
-    into fp64). Chunk 0 also carries the one-time costs (the first block's statistics that pick the shifts
+    into fp64; X^T X on its block-upper tiles only, since it is symmetric). Chunk 0 also carries the one-time costs (the first block's statistics that pick the shifts
     and the centred channels, the accumulators' allocation); the later chunks are the steady state the
     projection uses. Then the fp64 solve of every target for 3 lambdas (timed cold, as a fit runs it, and once
     more with its device memory cached: the difference is the allocation of W and the workspace). Work per chunk:
-    2 rows d^2 (1 + targets) flop."""
+    2 rows d^2 (1 + targets) flop counted (gram_tflops); executed, X^T X takes only its block-upper 256 x 256
+    tiles (gram_executed_tflops)."""
     from rfill import ridge, synth
     maps = synth.fit_maps(d, targets, device=dev)
     stats = ridge.RidgeStats(0, list(range(targets)), d, device=dev)
@@ -442,6 +443,8 @@ def fit_bench(dev, chunks=3, rows=65536, d=4096, targets=16, lams=(1e-4, 1e-3, 1
         del x, ys
     steady = sum(times[1:]) / max(1, len(times) - 1)
     flop = 2.0 * rows * d * d * (1 + targets)
+    tiles = -(-(d + 2 * stats.cen_x.s) // 256)
+    flop_exec = 2.0 * rows * d * d * targets + 2.0 * rows * 256 * 256 * (tiles * tiles - tiles * (tiles - 1) // 2)
     t0 = time.perf_counter()
     fit = ridge.RidgeFit(stats.state(device=dev), device=dev)
     fit.layers(range(targets), lams)
@@ -457,6 +460,8 @@ def fit_bench(dev, chunks=3, rows=65536, d=4096, targets=16, lams=(1e-4, 1e-3, 1
                         f"8192-row blocks",
             "first_chunk_s": round(times[0], 4), "steady_chunk_s": round(steady, 4),
             "gram_tflops": round(flop / steady / 1e12, 1), "gram_frac_bf16_peak": round(flop / steady / PEAK_BF16, 4),
+            "gram_executed_tflops": round(flop_exec / steady / 1e12, 1),
+            "gram_executed_frac_bf16_peak": round(flop_exec / steady / PEAK_BF16, 4),
             "centred_channels_x": stats.cen_x.s, "solve_s": round(t_solve, 3), "solve_warm_s": round(t_warm, 3),
             "projected_full_fit_s": round(times[0] + steady * 31 + t_solve, 2)}
 

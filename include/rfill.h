@@ -422,6 +422,22 @@ int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t* b, int64_
 /* Workspace bytes of rf_gram_accumulate's run-split schedule for this shape (0: it uses none). */
 int rf_gram_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t fold_rows, size_t* bytes);
 
+/* The symmetric X^T X of RidgeStats.begin (code/kva/ridge.py:47, `sxx += xw.T @ xc`): rf_gram_accumulate with
+ * both operands taken from one K-contiguous buffer a [N rows, K] (A = its first M rows, B = all N, M <= N),
+ * on C's block-upper 256 x 256 tiles only (tile column >= tile row): C[i, j] += sum_k a[i, k] a[j, k]. The
+ * block-lower tiles are not written; C's leading M x M part is symmetric, so the caller copies them from
+ * the block-upper ones (C[i, j] = C[j, i]) before reading. Each tile written is bit-identical to
+ * rf_gram_accumulate(a, lda, a, lda, M, N, ...)'s. With a workspace of rf_gram_upper_workspace_bytes (at
+ * most one round of tiles), every tile is split into its fold runs, one workgroup per (tile, run), and
+ * the run sums are added into C in run order by a second kernel, so about half the product's work
+ * spreads over every CU; workspace NULL or smaller: every tile whole, same bits. Limits as
+ * rf_gram_accumulate. */
+int rf_gram_accumulate_upper(const uint16_t* a, int64_t lda, int64_t M, int64_t N, int64_t K, int64_t fold_rows,
+                             double* c, int64_t ldc, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes of rf_gram_accumulate_upper's run-split schedule for this shape (0: it uses none). */
+int rf_gram_upper_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t fold_rows, size_t* bytes);
+
 /* Held-out read cosine of one late layer for one document (code/scripts/fit_sweep.py:307-313): pred and
  * truth are [rows, >= (na + nb) d] bf16 reads, each row na vectors of group a then nb vectors of group b,
  * each d wide. An attention layer's reads are its pre-RoPE K and V (code/kva/model.py:282-287, one

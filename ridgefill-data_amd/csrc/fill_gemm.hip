@@ -1081,7 +1081,24 @@ struct GramPlan {
   int pieces;             // grid blocks before the whole tiles (>= ptiles * runs, a multiple of 8)
   int ptiles, runs;
   float* part;
+  int upper;              // the logical tiles are C's block-upper tiles only (gram_coords)
 };
+
+// Logical tile -> (tile row, tile column) of a Gram launch: tile_coords over every tile, or with `upper` the
+// block-upper tiles (tn >= tm) row by row, for the symmetric X^T X (tiles_m <= tiles_n, tile < the count).
+__device__ __forceinline__ void gram_coords(int tile, int tiles_m, int tiles_n, bool upper, int& tm, int& tn) {
+  if (!upper) {
+    tile_coords(tile, tiles_m, tiles_n, tm, tn);
+    return;
+  }
+  int r = 0;
+  while (r + 1 < tiles_m && tile >= tiles_n - r) {
+    tile -= tiles_n - r;
+    ++r;
+  }
+  tm = r;
+  tn = r + tile;
+}
 
 // C[m, n] += sum_k A[m, k] B[n, k]: bf16 products summed in fp32 over runs of at most `fold` of K, each run's
 // sums added into the fp64 accumulator C as it ends (fold_tile), or stored for k_gram_fold (GramPlan). Each
@@ -1098,13 +1115,13 @@ __global__ __launch_bounds__(NTHR) void k_gram(const uint16_t* __restrict__ A, i
   if (static_cast<int>(blockIdx.x) < pl.pieces) {
     const int p = blockIdx.x, t = p / pl.runs, run = p - t * pl.runs;
     if (t >= pl.ptiles) return;                     // padding block (block-uniform; no barrier reached)
-    tile_coords(whole + t, tiles_m, tiles_n, tm, tn);
+    gram_coords(whole + t, tiles_m, tiles_n, pl.upper, tm, tn);
     const int k0 = run * fold, k1 = min(k0 + fold, K);
     mainloop(A + k0, lda, B + k0, ldb, M, k1 - k0, tm * BM, tn * BN, lds, acc);
     store_tile(acc, lds, pl.part + static_cast<int64_t>(p) * BM * BN);
     return;
   }
-  tile_coords(xcd_tile(blockIdx.x - pl.pieces, whole), tiles_m, tiles_n, tm, tn);
+  gram_coords(xcd_tile(blockIdx.x - pl.pieces, whole), tiles_m, tiles_n, pl.upper, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
   for (int k0 = 0; k0 < K; k0 += fold) {
     const int k1 = min(k0 + fold, K);
@@ -1116,11 +1133,11 @@ __global__ __launch_bounds__(NTHR) void k_gram(const uint16_t* __restrict__ A, i
 // C += the stored runs of the last ptiles logical tiles (GramPlan), each tile's runs in run order: block =
 // 4 rows of one tile, thread = 4 consecutive columns (whole 1 KB rows of the planes, 2 KB rows of C).
 __global__ __launch_bounds__(256) void k_gram_fold(const float* __restrict__ part, int ptiles, int runs, int whole,
-                                                   int M, int N, double* __restrict__ C, int64_t ldc) {
+                                                   int M, int N, double* __restrict__ C, int64_t ldc, int upper) {
   const int t = blockIdx.x >> 6, row = (blockIdx.x & 63) * 4 + (threadIdx.x >> 6), c4 = threadIdx.x & 63;
   if (t >= ptiles) return;
   int tm, tn;
-  tile_coords(whole + t, (M + BM - 1) / BM, N / BN, tm, tn);
+  gram_coords(whole + t, (M + BM - 1) / BM, N / BN, upper, tm, tn);
   const int gm = tm * BM + row;
   if (gm >= M) return;
   double* p = C + static_cast<int64_t>(gm) * ldc + tn * BN + 4 * c4;
@@ -2293,63 +2310,93 @@ extern "C" int rf_mfma_ceiling(int blocks, int iters, float* out, hipStream_t st
   return check_launch("rf_mfma_ceiling");
 }
 
-// The run-split schedule of a Gram launch (GramPlan): used when the tiles take more than one round of CUs but
-// at most two, and their split-off runs fit in two rounds; ptiles = 0 otherwise.
+// The run-split schedule of a Gram launch (GramPlan). Every tile: used when the tiles take more than one
+// round of CUs but at most two, and their split-off runs fit in two rounds; ptiles = 0 otherwise. Block-upper
+// tiles (the symmetric X^T X, at most one round of them): all of them split into their runs, which spreads
+// the half-size product over every CU; past one round, as for every tile.
 struct GramShape {
   int64_t tiles, runs, ptiles;
 };
-static GramShape gram_shape(int64_t M, int64_t N, int64_t K, int64_t fold_rows) {
+static GramShape gram_shape(int64_t M, int64_t N, int64_t K, int64_t fold_rows, bool upper) {
   const int64_t fold = (fold_rows == 0 || fold_rows > K) ? K : fold_rows;
-  GramShape g{((M + BM - 1) / BM) * (N / BN), (K + fold - 1) / fold, 0};
+  const int64_t tm = (M + BM - 1) / BM, tn = N / BN;
+  GramShape g{upper ? tm * tn - tm * (tm - 1) / 2 : tm * tn, (K + fold - 1) / fold, 0};
   const int64_t ncu = 256;
-  if (g.tiles > ncu && g.tiles < 2 * ncu && g.runs >= 2 && (g.tiles - ncu) * g.runs <= 2 * ncu)
+  if (upper && g.tiles <= ncu && g.runs >= 2)
+    g.ptiles = g.tiles;
+  else if (g.tiles > ncu && g.tiles < 2 * ncu && g.runs >= 2 && (g.tiles - ncu) * g.runs <= 2 * ncu)
     g.ptiles = g.tiles - ncu;
   return g;
 }
 
-extern "C" int rf_gram_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t fold_rows, size_t* bytes) {
-  if (!bytes || M < 0 || M > (1 << 30) || N <= 0 || N % BN || K <= 0 || K % 64 || fold_rows < 0 || fold_rows % 64)
-    return fail(RF_EINVAL_ARG, "rf_gram_workspace_bytes: M %lld, N %lld (multiple of 256), K %lld, fold_rows %lld",
-                (long long)M, (long long)N, (long long)K, (long long)fold_rows);
-  const GramShape g = gram_shape(M, N, K, fold_rows);
+static int gram_workspace(const char* who, int64_t M, int64_t N, int64_t K, int64_t fold_rows, bool upper,
+                          size_t* bytes) {
+  if (!bytes || M < 0 || M > (1 << 30) || N <= 0 || N % BN || K <= 0 || K % 64 || fold_rows < 0 || fold_rows % 64 ||
+      (upper && M > N))
+    return fail(RF_EINVAL_ARG, "%s: M %lld, N %lld (multiple of 256%s), K %lld, fold_rows %lld", who, (long long)M,
+                (long long)N, upper ? ", at least M" : "", (long long)K, (long long)fold_rows);
+  const GramShape g = gram_shape(M, N, K, fold_rows, upper);
   *bytes = static_cast<size_t>(g.ptiles * g.runs) * BM * BN * sizeof(float);
   return RF_OK;
 }
 
-extern "C" int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t M,
-                                  int64_t N, int64_t K, int64_t fold_rows, double* c, int64_t ldc, void* workspace,
-                                  size_t workspace_bytes, hipStream_t stream) {
-  if (!a || !b || !c) return fail(RF_EINVAL_ARG, "rf_gram_accumulate: null pointer");
-  if (M < 0 || M > (1 << 30) || N <= 0 || N % BN || K <= 0 || K % 64)
-    return fail(RF_EINVAL_SHAPE, "rf_gram_accumulate: M %lld, N %lld (multiple of 256), K %lld (multiple of 64)",
-                (long long)M, (long long)N, (long long)K);
+static int gram_launch(const char* who, const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t M,
+                       int64_t N, int64_t K, int64_t fold_rows, double* c, int64_t ldc, void* workspace,
+                       size_t workspace_bytes, bool upper, hipStream_t stream) {
+  if (!a || !b || !c) return fail(RF_EINVAL_ARG, "%s: null pointer", who);
+  if (M < 0 || M > (1 << 30) || N <= 0 || N % BN || K <= 0 || K % 64 || (upper && M > N))
+    return fail(RF_EINVAL_SHAPE, "%s: M %lld, N %lld (multiple of 256%s), K %lld (multiple of 64)", who,
+                (long long)M, (long long)N, upper ? ", at least M" : "", (long long)K);
   if (lda < K || ldb < K || lda % 8 || ldb % 8 || lda > (1 << 21) || ldb > (1 << 21) || ldc < N || ldc % 2)
-    return fail(RF_EINVAL_SHAPE, "rf_gram_accumulate: strides lda %lld, ldb %lld, ldc %lld", (long long)lda,
-                (long long)ldb, (long long)ldc);
+    return fail(RF_EINVAL_SHAPE, "%s: strides lda %lld, ldb %lld, ldc %lld", who, (long long)lda, (long long)ldb,
+                (long long)ldc);
   if (!aligned16(a) || !aligned16(b) || !aligned16(c))
-    return fail(RF_EINVAL_SHAPE, "rf_gram_accumulate: pointers must be 16-byte aligned");
+    return fail(RF_EINVAL_SHAPE, "%s: pointers must be 16-byte aligned", who);
   if (fold_rows < 0 || fold_rows % 64)
-    return fail(RF_EINVAL_ARG, "rf_gram_accumulate: fold_rows %lld (0 or a multiple of 64)", (long long)fold_rows);
+    return fail(RF_EINVAL_ARG, "%s: fold_rows %lld (0 or a multiple of 64)", who, (long long)fold_rows);
   if (M == 0) return RF_OK;
   const int64_t fold = (fold_rows == 0 || fold_rows > K) ? K : fold_rows;
-  const GramShape g = gram_shape(M, N, K, fold_rows);
+  const GramShape g = gram_shape(M, N, K, fold_rows, upper);
   const size_t need = static_cast<size_t>(g.ptiles * g.runs) * BM * BN * sizeof(float);
-  GramPlan pl{0, 0, 1, nullptr};
+  GramPlan pl{0, 0, 1, nullptr, upper ? 1 : 0};
   if (g.ptiles > 0 && workspace && workspace_bytes >= need) {     // else every tile whole (same bits)
-    if (!aligned16(workspace)) return fail(RF_EINVAL_ARG, "rf_gram_accumulate: workspace must be 16-byte aligned");
+    if (!aligned16(workspace)) return fail(RF_EINVAL_ARG, "%s: workspace must be 16-byte aligned", who);
     pl = GramPlan{static_cast<int>((g.ptiles * g.runs + 7) / 8 * 8), static_cast<int>(g.ptiles),
-                  static_cast<int>(g.runs), static_cast<float*>(workspace)};
+                  static_cast<int>(g.runs), static_cast<float*>(workspace), upper ? 1 : 0};
   }
   const int grid = static_cast<int>(g.tiles - pl.ptiles) + pl.pieces;
   hipLaunchKernelGGL(k_gram, dim3(grid), dim3(NTHR), 0, stream, a, lda, b, ldb, static_cast<int>(M),
                      static_cast<int>(N), static_cast<int>(K), static_cast<int>(fold), c, ldc, pl);
   if (pl.ptiles > 0) {
-    const int rc = check_launch("rf_gram_accumulate");
+    const int rc = check_launch(who);
     if (rc != RF_OK) return rc;
     hipLaunchKernelGGL(k_gram_fold, dim3(pl.ptiles * 64), dim3(256), 0, stream, pl.part, pl.ptiles, pl.runs,
-                       static_cast<int>(g.tiles - pl.ptiles), static_cast<int>(M), static_cast<int>(N), c, ldc);
+                       static_cast<int>(g.tiles - pl.ptiles), static_cast<int>(M), static_cast<int>(N), c, ldc,
+                       pl.upper);
   }
-  return check_launch("rf_gram_accumulate");
+  return check_launch(who);
+}
+
+extern "C" int rf_gram_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t fold_rows, size_t* bytes) {
+  return gram_workspace("rf_gram_workspace_bytes", M, N, K, fold_rows, false, bytes);
+}
+
+extern "C" int rf_gram_accumulate(const uint16_t* a, int64_t lda, const uint16_t* b, int64_t ldb, int64_t M,
+                                  int64_t N, int64_t K, int64_t fold_rows, double* c, int64_t ldc, void* workspace,
+                                  size_t workspace_bytes, hipStream_t stream) {
+  return gram_launch("rf_gram_accumulate", a, lda, b, ldb, M, N, K, fold_rows, c, ldc, workspace, workspace_bytes,
+                     false, stream);
+}
+
+extern "C" int rf_gram_upper_workspace_bytes(int64_t M, int64_t N, int64_t K, int64_t fold_rows, size_t* bytes) {
+  return gram_workspace("rf_gram_upper_workspace_bytes", M, N, K, fold_rows, true, bytes);
+}
+
+extern "C" int rf_gram_accumulate_upper(const uint16_t* a, int64_t lda, int64_t M, int64_t N, int64_t K,
+                                        int64_t fold_rows, double* c, int64_t ldc, void* workspace,
+                                        size_t workspace_bytes, hipStream_t stream) {
+  return gram_launch("rf_gram_accumulate_upper", a, lda, a, lda, M, N, K, fold_rows, c, ldc, workspace,
+                     workspace_bytes, true, stream);
 }
 
 extern "C" int rf_norm_linear(const uint16_t* x, int64_t ldx, const float* ssq, int64_t P, int64_t H, float eps,

@@ -54,6 +54,8 @@ SIGNATURES = {
     "rf_colsum_fold": [_P, _I64, _I64, _P, _P],
     "rf_gram_accumulate": [_P, _I64, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _SZ, _P],
     "rf_gram_workspace_bytes": [_I64, _I64, _I64, _I64, _PSZ],
+    "rf_gram_accumulate_upper": [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _SZ, _P],
+    "rf_gram_upper_workspace_bytes": [_I64, _I64, _I64, _I64, _PSZ],
     "rf_ridge_solve": [_P, _I64, _I64, _P, _I64, _I64, _P, _P, _P, _I32, _F64, _P, _I64, _I64, _P, _I64, _P, _SZ, _P],
     "rf_ridge_solve_workspace_bytes": [_I64, _I32, _PSZ],
     "rf_row_gather": [_P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _P],

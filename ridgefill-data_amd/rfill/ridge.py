@@ -77,6 +77,44 @@ def gram_workspace_bytes(M, N, K, fold_rows=0):
     return nb.value
 
 
+def gram_upper_workspace_bytes(M, N, K, fold_rows=0):
+    """Bytes of rf_gram_accumulate_upper's run-split workspace for this shape (0: it uses none)."""
+    nb = ctypes.c_size_t(0)
+    _lib.call("rf_gram_upper_workspace_bytes", M, N, K, int(fold_rows), ctypes.byref(nb))
+    return nb.value
+
+
+def gram_accumulate_upper(a, M, c, fold_rows=0, workspace=None):
+    """The symmetric product c += a[:M] a^T (a [N, K] bf16 K-contiguous, M <= N; c [M, N] fp64), fp32 over runs
+    of at most fold_rows of K, each run added in fp64 -- on c's block-upper 256 x 256 tiles only (tile column
+    >= tile row), about half the work of gram_accumulate(a[:M], a, c); the block-lower tiles are left as they
+    are (mirror_block_upper fills them). workspace as gram_accumulate's (gram_upper_workspace_bytes): at most
+    one round of tiles all split into their runs, which keeps every CU busy. The block-upper tiles are
+    bit-identical to gram_accumulate's."""
+    _need(a, "a", torch.bfloat16, 2)
+    _need(c, "c", torch.float64, 2)
+    N, K = a.shape
+    if not 0 <= M <= N or tuple(c.shape) != (M, N):
+        raise ValueError(f"gram_upper shapes a {tuple(a.shape)}, M {M}, c {tuple(c.shape)}")
+    need = gram_upper_workspace_bytes(M, N, K, fold_rows) if M > 0 and N % 256 == 0 and K % 64 == 0 else 0
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=c.device)
+    nb = workspace.numel() if workspace is not None else 0
+    _lib.call("rf_gram_accumulate_upper", _ptr(a), a.stride(0), M, N, K, int(fold_rows), _ptr(c), c.stride(0),
+              _ptr(workspace), nb, _stream(a))
+    return c
+
+
+def mirror_block_upper(c):
+    """c [M, N >= M]: the block-lower 256 x 256 tiles of c's leading M x M part (tile row > tile column) set
+    from the block-upper ones (c[i, j] = c[j, i]), which gram_accumulate_upper accumulates."""
+    M = c.shape[0]
+    for r0 in range(256, M, 256):
+        r1 = min(r0 + 256, M)
+        c[r0:r1, :r0] = c[:r0, r0:r1].transpose(0, 1)
+    return c
+
+
 def gram_accumulate(a, b, c, fold_rows=0, workspace=None):
     """c += a b^T (a [M, K], b [N, K] bf16 K-contiguous; c [M, N] fp64): fp32 over runs of at most fold_rows
     of K (0: all of K), each run added in fp64. workspace: a uint8 device buffer for the run-split schedule
@@ -214,10 +252,19 @@ class RidgeStats:
     def _gram(self, a, b, c, block):
         """gram_accumulate with a workspace kept between calls (grown as needed)."""
         need = gram_workspace_bytes(a.shape[0], b.shape[0], a.shape[1], block)
+        gram_accumulate(a, b, c, block, self._workspace(need))
+
+    def _gram_upper(self, a, M, c, block):
+        """gram_accumulate_upper with the same kept workspace."""
+        need = gram_upper_workspace_bytes(M, a.shape[0], a.shape[1], block)
+        gram_accumulate_upper(a, M, c, block, self._workspace(need))
+
+    def _workspace(self, need):
         ws = getattr(self, "_gws", None)
         if need and (ws is None or ws.numel() < need):
+            self._gws = None                        # the old buffer goes before the larger one is taken
             self._gws = ws = torch.empty(need, dtype=torch.uint8, device=self.device)
-        gram_accumulate(a, b, c, block, ws)
+        return ws
 
     def _x_piece(self, r, sums):
         """Rows r .. r + PIECE of the current boundary rows, centred and transposed into X^T (the column sums
@@ -264,7 +311,8 @@ class RidgeStats:
             rows = self._x_piece(r, True)
             kp = (rows + 63) // 64 * 64
             xt = self._xt
-            self._gram(xt[:d + 2 * cx.s, :kp], xt[:d + cx.lo_rows, :kp], self.sxx, block)
+            self._gram_upper(xt[:d + cx.lo_rows, :kp], d + 2 * cx.s, self.sxx, block)
+            self._sxx_upper = True
 
     @torch.no_grad()
     def add_layer(self, i, y):
@@ -315,6 +363,8 @@ class RidgeStats:
         n = float(self.n)
         d, o, cx = self.dim, self.out_dim, self.cen_x
         dx = cx.delta
+        if getattr(self, "_sxx_upper", False):      # X^T X accumulated on its block-upper tiles only
+            mirror_block_upper(self.sxx)
         sxx = recentre(centred_products(self.sxx, d, cx, d, cx), self.s1x, self.s1x, dx, dx, n)
         cy, sy, sxy = {}, {}, {}
         for i in self.layers:

@@ -106,3 +106,20 @@ def test_gram_workspace_sizes():
     assert ridge.gram_workspace_bytes(0, 4096, 65536, 8192) == 0
     with pytest.raises(ValueError):
         ridge.gram_workspace_bytes(4096, 100, 65536, 8192)                  # N not a multiple of 256
+
+
+def test_gram_upper_workspace_sizes():
+    """Host-only size rule of rf_gram_accumulate_upper: the block-upper tiles (tile column >= tile row), when
+    at most one round of them and K holds two or more runs, all split into their runs; past one round, the
+    rule of rf_gram_accumulate over that tile count."""
+    from rfill import ridge
+    plane = 256 * 256 * 4
+    assert ridge.gram_upper_workspace_bytes(4096, 4096, 65536, 8192) == 136 * 8 * plane   # 16 x 16 tiles
+    assert ridge.gram_upper_workspace_bytes(4104, 4352, 65536, 8192) == 153 * 8 * plane   # centred X: 17 x 17
+    assert ridge.gram_upper_workspace_bytes(5120, 5120, 65536, 8192) == 210 * 8 * plane   # 20 x 20
+    assert ridge.gram_upper_workspace_bytes(4096, 4096, 12288, 8192) == 136 * 2 * plane   # a short last run
+    assert ridge.gram_upper_workspace_bytes(4096, 4096, 65536, 0) == 0      # one run: nothing to split
+    assert ridge.gram_upper_workspace_bytes(8192, 8192, 65536, 8192) == 0   # 528 tiles: whole rounds
+    assert ridge.gram_upper_workspace_bytes(0, 4096, 65536, 8192) == 0
+    with pytest.raises(ValueError):
+        ridge.gram_upper_workspace_bytes(4352, 4096, 65536, 8192)           # M past N

@@ -91,6 +91,54 @@ def test_gram_run_split_schedule_is_bit_identical(dev, M, N, K, fold_rows):
     assert err < 1e-6
 
 
+@pytest.mark.parametrize("M,N,K,fold_rows", [(4104, 4352, 16384, 8192), (1024, 1024, 12288, 8192),
+                                              (768, 1024, 2048, 0)])
+def test_gram_upper_is_the_full_product_on_its_tiles(dev, M, N, K, fold_rows):
+    """The symmetric X^T X on C's block-upper tiles (a centred X's 4104 rows against its 4352-row operand: 153
+    of 289 tiles, each split into its two runs; a short last run; one run, whole tiles): those tiles
+    bit-identical to rf_gram_accumulate of the same operands, the block-lower tiles untouched, the same bits
+    with no workspace, nothing written past the workspace, and after mirror_block_upper the full product
+    (fp64 products to 1e-6; the full launch's own lower tiles differ from the mirrored upper ones by fp32
+    summation order only, about 1e-13 of C here)."""
+    from rfill import _lib, ridge
+    from rfill.ops import _ptr, _stream
+    g = torch.Generator(device=dev).manual_seed(5)
+    a = torch.randn(N, K, generator=g, device=dev).to(torch.bfloat16)
+    a[M:] = 0                                                           # rows past M: a centred operand's padding
+    c0 = torch.randn(M, N, generator=g, device=dev, dtype=torch.float64)
+    c0[:, :M] += c0[:, :M].T.clone()                                    # a symmetric running sum, as RidgeStats'
+    full = c0.clone()
+    ridge.gram_accumulate(a[:M], a, full, fold_rows)
+    need = ridge.gram_upper_workspace_bytes(M, N, K, fold_rows)
+    assert (need > 0) == (fold_rows > 0)
+    guard = 1 << 20
+    buf = torch.full((need + guard,), 0xFF, dtype=torch.uint8, device=dev)
+    up = c0.clone()
+    _lib.call("rf_gram_accumulate_upper", _ptr(a), a.stride(0), M, N, K, fold_rows, _ptr(up), up.stride(0),
+              _ptr(buf), need, _stream(a))
+    whole = c0.clone()
+    ridge.gram_accumulate_upper(a, M, whole, fold_rows, torch.empty(0, dtype=torch.uint8, device=dev))
+    torch.cuda.synchronize()
+    assert bool((buf[need:] == 0xFF).all()), "the upper schedule wrote past its workspace"
+    assert torch.equal(whole, up)
+    ti = torch.arange(M, device=dev)[:, None] // 256
+    tj = torch.arange(N, device=dev)[None, :] // 256
+    upper = tj >= ti
+    assert torch.equal(up[upper], full[upper])
+    assert torch.equal(up[~upper], c0[~upper])
+    ridge.mirror_block_upper(up)
+    sym = full[:, :M] - c0[:, :M]
+    asym = float((sym - sym.T).abs().max())
+    print(f"gram upper {M} x {N} x {K} (fold {fold_rows}): full product symmetric to {asym:.1e}")
+    d = a[:M].double()
+    want = d @ a.double().T
+    assert torch.equal(up[:, M:], c0[:, M:])                           # products with the zero rows
+    low = ~upper[:, :M]
+    assert torch.equal(up[:, :M][low], (up[:, :M].T)[low])
+    err = rel(up[:, :M][low] - c0[:, :M][low], want[:, :M][low])
+    assert err < 1e-6, err
+
+
 def test_gram_accumulate_refuses_bad_fold(dev):
     from rfill import ridge
     a = torch.zeros(256, 128, dtype=torch.bfloat16, device=dev)
